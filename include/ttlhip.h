@@ -1,0 +1,212 @@
+/*
+ * ttlhip.h — C ABI of libttlhip.so, the MI355X (gfx950) execution library
+ * behind the drop-in `ttl` / `ttnn` Python modules.
+ *
+ * The reference (tenstorrent/tt-lang) exposes no C ABI for its kernels: its
+ * host->device boundary is the Python call
+ *     ttnn.generic_op(tensors, ProgramDescriptor)
+ * made by run_kernel_on_device() (python/ttl/kernel_runner.py:188-255), which
+ * launches compiled reader / compute / writer threads on the Tensix grid.
+ * Each entry point below replaces one *class* of such launch: the Python
+ * tracer turns a @ttl.kernel's circular-buffer / copy / store program into one
+ * or a few calls here.  Every reference anchor is cited on the declaration.
+ *
+ * Conventions
+ *  - All tensor pointers are DEVICE pointers (HIP), row-major storage.
+ *    bf16 is stored as uint16_t bit patterns.  Exceptions: the *_host codec
+ *    helpers, which take host pointers.
+ *  - `stream` is a hipStream_t passed as void* (NULL = default stream).
+ *    Every launch is stream-ordered and asynchronous; nothing here
+ *    synchronises, allocates caller-visible memory or frees caller memory.
+ *  - Return value: TTLH_OK (0) on success, a positive TTLH_E* code otherwise;
+ *    ttlh_last_error() then returns a thread-local message (the Python layer
+ *    raises ValueError / RuntimeError with it, mirroring the reference's
+ *    error convention, python/ttl/ttl_api.py:733-737).
+ */
+#ifndef TTLHIP_H
+#define TTLHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TTLH_ABI_VERSION 1
+
+/* status codes */
+#define TTLH_OK 0
+#define TTLH_EINVAL 1       /* bad argument (shape, dtype, null pointer)  */
+#define TTLH_EUNSUPPORTED 2 /* valid request this build does not handle  */
+#define TTLH_EHIP 3         /* HIP runtime error                         */
+
+/* element types (the reference's ttnn.bfloat16 / ttnn.float32,
+ * python/ttl/dtype_utils.py:151-181) */
+#define TTLH_BF16 0
+#define TTLH_F32 1
+
+/* Tile geometry (python/sim/constants.py:42-44: TILE_SHAPE = (32, 32)). */
+#define TTLH_TILE 32
+
+/* ------------------------------------------------------------------------
+ * Fused elementwise / broadcast tile program
+ *
+ * Replaces the compute thread's DST-register tile ops
+ * (include/ttlang/Dialect/TTL/TTLElementwiseOps.def:61-82; simulator:
+ * Block._binary_op python/sim/block.py:870-1010 and broadcast_tensors
+ * python/sim/ttnnsim.py:67-109) together with the reader / writer threads'
+ * tile DMA (noc_async_read_tile / noc_async_write_tile, lowered in
+ * lib/Dialect/TTL/Transforms/ConvertTTLToTTKernel.cpp:563-751).
+ *
+ * A program is a straight-line list of at most TTLH_MAX_INSTR steps of a
+ * small stack machine evaluated per output element in fp32.  The value on
+ * top of the stack is `acc`; at most two more values sit below it.  Step k
+ * owns operand slot k (in[k]); steps that read no operand leave in[k].ptr
+ * NULL.  After each step `acc` is rounded to `rnd` (TTLH_BF16 =
+ * round-to-nearest-even to bfloat16, matching the simulator, which
+ * materialises every intermediate tile in its torch dtype; TTLH_F32 = keep
+ * fp32).  The result is `acc` after the last step.
+ * ---------------------------------------------------------------------- */
+enum ttlh_opcode {
+  TTLH_OP_NONE = 0,
+  TTLH_OP_ADD = 1,      /* binary: x + y                                   */
+  TTLH_OP_SUB = 2,
+  TTLH_OP_MUL = 3,
+  TTLH_OP_DIV = 4,
+  TTLH_OP_MAX = 5,      /* NaN-propagating (torch.maximum)                 */
+  TTLH_OP_MIN = 6,
+  TTLH_OP_POW = 7,      /* x ** y                                          */
+  TTLH_OP_FLOORDIV = 8, /* floor(x / y)  (torch.floor_divide)              */
+  TTLH_OP_MOD = 9,      /* x - floor(x / y) * y  (torch.remainder)         */
+  TTLH_OP_EXP = 16,     /* unary: f(acc)                                   */
+  TTLH_OP_LOG = 17,
+  TTLH_OP_SQRT = 18,
+  TTLH_OP_RSQRT = 19,
+  TTLH_OP_TANH = 20,
+  TTLH_OP_ABS = 21,
+  TTLH_OP_NEG = 22,
+  TTLH_OP_RELU = 23,
+  TTLH_OP_SIGMOID = 24,
+  TTLH_OP_RECIP = 25,
+  TTLH_OP_POWI = 26     /* acc ** imm (integer exponent, Block.__pow__)    */
+};
+
+enum ttlh_form {
+  TTLH_FORM_LOAD = 0,        /* acc = in[k]            (stack was empty)   */
+  TTLH_FORM_PUSH = 1,        /* push acc; acc = in[k]                      */
+  TTLH_FORM_CONST = 2,       /* acc = imm              (stack was empty)   */
+  TTLH_FORM_PUSH_CONST = 3,  /* push acc; acc = imm                        */
+  TTLH_FORM_UNARY = 4,       /* acc = op(acc)                              */
+  TTLH_FORM_BIN = 5,         /* acc = op(acc, in[k])                       */
+  TTLH_FORM_BIN_REV = 6,     /* acc = op(in[k], acc)                       */
+  TTLH_FORM_BIN_IMM = 7,     /* acc = op(acc, imm)                         */
+  TTLH_FORM_BIN_IMM_REV = 8, /* acc = op(imm, acc)                         */
+  TTLH_FORM_BIN_POP = 9      /* acc = op(pop(), acc)                       */
+};
+
+typedef struct ttlh_instr {
+  uint8_t op;   /* ttlh_opcode (ignored by LOAD/PUSH/CONST forms) */
+  uint8_t form; /* ttlh_form                                      */
+  uint8_t rnd;  /* TTLH_BF16 or TTLH_F32                          */
+  uint8_t pad;
+  float imm;    /* CONST value / immediate operand / POWI exponent */
+} ttlh_instr;
+
+#define TTLH_MAX_INSTR 12
+#define TTLH_MAX_STACK 3
+
+/* An input operand, addressed from the output element (y, x):
+ *   iy = (y & row_mask) + row_off ;  ix = (x & col_mask) + col_off
+ *   element = ptr[iy * row_stride + ix * col_stride]
+ * row_mask/col_mask = -1 (identity) or 31 (a fixed tile re-used across the
+ * tile grid, simulator block broadcasting, python/sim/block.py:886-920);
+ * a stride of 0 broadcasts a degenerate (size-1) tensor dimension across the
+ * tile (python/sim/copyhandlers.py:103-131).  The caller guarantees every
+ * addressed element lies inside the allocation.                          */
+typedef struct ttlh_operand {
+  const void* ptr;
+  int32_t dtype;      /* TTLH_BF16 / TTLH_F32 */
+  int32_t pad;
+  int64_t row_stride; /* elements */
+  int64_t col_stride; /* elements: 1 (contiguous) or 0 (broadcast) */
+  int64_t row_mask, col_mask;
+  int64_t row_off, col_off;
+} ttlh_operand;
+
+/* Evaluate `prog` for every element of the out region
+ * [y0, y0+h) x [x0, x0+w) of `out` (row stride out_ld elements) and store
+ * the final `acc` (rounded RNE to out_dtype).  `in` has n_instr entries.
+ * Replaces: the generated reader/compute/writer thread triple of a fused
+ * elementwise kernel launched through ttnn.generic_op
+ * (python/ttl/kernel_runner.py:188-255); simulator call stack
+ * python/sim/program.py:363-647 -> block.py:805-1010. */
+int ttlh_eltwise(const ttlh_instr* prog, const ttlh_operand* in, int n_instr,
+                 void* out, int out_dtype, int64_t out_ld, int64_t y0,
+                 int64_t x0, int64_t h, int64_t w, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Tile matmul:  C[M,N] (=|+=) A[M,K] . B[K,N]
+ *
+ * Replaces Block.__matmul__ + store(acc=True) over the K tiles
+ * (python/sim/block.py:805-868,1012-1013; ttnnsim.py:454-459) and the
+ * Tensix matmul_tiles loop (examples/metal_examples/singlecore_matmul/
+ * metal/kernels/mm_compute.cpp:28-68).  bf16 inputs run on gfx950 bf16
+ * MFMA, f32 inputs on f32 MFMA; accumulation is fp32 over the full K, the
+ * result is rounded once to c_dtype.  accumulate = 1 adds into C.
+ * M, N, K must be multiples of 32 (whole tiles); strides in elements.   */
+int ttlh_matmul(const void* A, int a_dtype, int64_t lda, const void* B,
+                int b_dtype, int64_t ldb, void* C, int c_dtype, int64_t ldc,
+                int64_t M, int64_t N, int64_t K, int accumulate, void* stream);
+
+/* ------------------------------------------------------------------------
+ * bfloat8_b weight tiles.  The reference only fixes the tile size
+ * (32*32 + 64 = 1088 bytes, python/ttl/dtype_utils.py:174-175); the codec
+ * lives in un-vendored tt-metal.  Format implemented here (byte layout of
+ * one 32x32 tile; tiles stored row-major over the tile grid):
+ *   bytes [0, 64):     shared exponents, face-major (faces f0 = rows 0-15 /
+ *                      cols 0-15, f1 = rows 0-15 / cols 16-31, f2 = rows
+ *                      16-31 / cols 0-15, f3 = rows 16-31 / cols 16-31),
+ *                      one byte per 16-element face row;
+ *   bytes [64, 1088):  one byte per element, face-major, row-major inside
+ *                      a face: bit 7 = sign, bits 6..0 = magnitude m.
+ *   value = (-1)^s * m * 2^(e - 133)   (e = shared biased exponent; e = 0 or
+ *   m = 0 gives +-0; a result below the bf16 normal range flushes to +-0).
+ * Pack: e = max biased fp32 exponent of the 16 values (0 if all are zero or
+ * denormal), m = round-half-to-even(|x| * 2^(133 - e)) saturated to 127.  */
+#define TTLH_BFP8_TILE_BYTES 1088
+
+/* host codec (host pointers) */
+int ttlh_bfp8_pack_host(const float* src, void* dst, int64_t rows,
+                        int64_t cols);
+int ttlh_bfp8_unpack_host(const void* src, uint16_t* dst_bf16, int64_t rows,
+                          int64_t cols);
+/* device dequant: tiles -> row-major bf16 (device pointers) */
+int ttlh_bfp8_unpack(const void* src, void* dst_bf16, int64_t rows,
+                     int64_t cols, void* stream);
+
+/* C[M,N] = A[M,K] (bf16, row-major, lda) . dequant(Bq)[K,N], with Bq the
+ * bfloat8_b tile array of a K x N matrix; dequantisation to bf16 happens in
+ * LDS ahead of the bf16 MFMA; fp32 accumulate; bf16 out.                */
+int ttlh_matmul_bfp8w(const void* A, int64_t lda, const void* Bq, void* C,
+                      int64_t ldc, int64_t M, int64_t N, int64_t K,
+                      void* stream);
+
+/* ------------------------------------------------------------------------
+ * Fused scaled-dot-product attention forward (no counterpart in the
+ * reference: composed from spec ops @, exp, recip, reduce_max, reduce_sum,
+ * broadcast, docs/sphinx/specs/TTLangSpecification.md:693-761).
+ * Q, K, V, O: bf16 [B, H, S, D] contiguous; O = softmax(Q K^T * scale) V
+ * with fp32 online softmax; D = 128 (or 64). causal = 1 masks j > i.     */
+int ttlh_sdpa_fwd(const void* Q, const void* K, const void* V, void* O,
+                  int64_t B, int64_t H, int64_t S, int64_t D, float scale,
+                  int causal, void* stream);
+
+/* ------------------------------------------------------------------------ */
+const char* ttlh_last_error(void);
+int ttlh_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TTLHIP_H */

@@ -1,0 +1,208 @@
+"""GPU parity of the fused elementwise / broadcast kernel (ttlh_eltwise).
+
+Each case builds one expression twice: as the product's Expr IR (run on the
+GPU through the C ABI) and as a nested tuple for the CPU oracle
+(oracle.tile_ops.eval_expr, the simulator's per-op torch semantics).
+Bar: bit-exact for + - * / max min neg abs relu and all broadcasts (one fp32
+op, one RNE rounding, same as torch's CPU kernels); transcendental ops within
+1 bf16 ULP (device libm vs torch's CPU libm may differ by one fp32 ulp, which
+flips a bf16 rounding only near a tie) and fp32 results within 4 fp32 ULP-ish
+relative error.
+"""
+
+import pytest
+import torch
+
+from oracle import tile_ops as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _expr(e, env):
+    from ttlhip import expr as X
+    from ttlhip.kernels import OperandMap
+
+    tag = e[0]
+    if tag == "leaf":
+        t, m = env[e[1]]
+        return X.Leaf(m, t.dtype)
+    if tag == "const":
+        return X.Const(e[1])
+    if tag == "powi":
+        x = _expr(e[1], env)
+        return X.Unary("powi", x, x.dtype, imm=float(e[2]))
+    if tag in O.UNARY:
+        x = _expr(e[1], env)
+        return X.Unary(tag, x, x.dtype)
+    a, b = _expr(e[1], env), _expr(e[2], env)
+    if isinstance(a, X.Const):
+        dt = b.dtype
+    elif isinstance(b, X.Const):
+        dt = a.dtype
+    else:
+        dt = X.promote(a.dtype, b.dtype)
+    return X.Binary(tag, a, b, dt)
+
+
+def run_gpu(e, env_cpu, maps, out_shape, out_dtype, region=None):
+    from ttlhip import expr as X
+    from ttlhip import kernels as K
+
+    dev = {k: (v.cuda(), maps.get(k, {})) for k, v in env_cpu.items()}
+    env = {k: (t, K.OperandMap(t, **m)) for k, (t, m) in dev.items()}
+    tree = _expr(e, env)
+    prog = X.compile_expr(tree)
+    ops = [s.leaf.ref if s.leaf is not None else None for s in prog.steps]
+    out = torch.full(out_shape, 7.0, dtype=out_dtype, device="cuda")
+    K.eltwise(prog, ops, out, region=region)
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+def assert_bitexact(got, ref):
+    ref = ref.to(got.dtype)
+    same = (got.view(torch.int16 if got.dtype == torch.bfloat16 else torch.int32)
+            == ref.view(torch.int16 if ref.dtype == torch.bfloat16 else torch.int32))
+    both_nan = torch.isnan(got) & torch.isnan(ref)
+    bad = ~(same | both_nan)
+    assert not bad.any(), f"{int(bad.sum())} mismatches; first at {bad.nonzero()[0].tolist()}"
+
+
+def _u(shape, seed, dtype=torch.bfloat16, lo=-2.0, hi=2.0):
+    return O.seeded(shape, "uniform", seed, dtype, lo=lo, hi=hi)
+
+
+def test_add_bf16_bitexact():
+    a, b = _u((256, 512), 1), _u((256, 512), 2)
+    e = ("add", ("leaf", "a"), ("leaf", "b"))
+    got = run_gpu(e, {"a": a, "b": b}, {}, (256, 512), torch.bfloat16)
+    assert_bitexact(got, O.eval_expr(e, {"a": a, "b": b}))
+
+
+def test_add_f32_bitexact():
+    a, b = _u((128, 256), 3, torch.float32), _u((128, 256), 4, torch.float32)
+    e = ("add", ("leaf", "a"), ("leaf", "b"))
+    got = run_gpu(e, {"a": a, "b": b}, {}, (128, 256), torch.float32)
+    assert_bitexact(got, O.eval_expr(e, {"a": a, "b": b}))
+
+
+def test_fused_exp_rowbcast_mul_bf16():
+    # config 2 shape class: Y = exp(A + b_row) * C, b_row (1, W) broadcast over rows
+    a, c = _u((512, 1024), 5), _u((512, 1024), 6)
+    b = _u((1, 1024), 7)
+    env = {"a": a, "b": b, "c": c}
+    e = ("mul", ("exp", ("add", ("leaf", "a"), ("leaf", "b"))), ("leaf", "c"))
+    got = run_gpu(e, env, {}, (512, 1024), torch.bfloat16)
+    ref = O.eval_expr(e, env)
+    ulp = O.bf16_ulp_diff(got, ref)
+    assert int(ulp.max()) <= 1, f"max ulp {int(ulp.max())}"
+    assert float((ulp > 0).float().mean()) < 1e-3
+
+
+def test_col_broadcast_mul_add():
+    # examples/broadcast.py: a * b + broadcast(c, dims=[1]) with c (N, 1)
+    a, b = _u((256, 256), 8), _u((256, 256), 9)
+    c = _u((256, 1), 10)
+    env = {"a": a, "b": b, "c": c}
+    e = ("add", ("mul", ("leaf", "a"), ("leaf", "b")), ("leaf", "c"))
+    got = run_gpu(e, env, {}, (256, 256), torch.bfloat16)
+    assert_bitexact(got, O.eval_expr(e, env))
+
+
+def test_stack_two_subtrees_and_consts():
+    a, b, c, d = (_u((64, 128), s) for s in (11, 12, 13, 14))
+    env = {"a": a, "b": b, "c": c, "d": d}
+    e = ("sub", ("mul", ("leaf", "a"), ("leaf", "b")),
+         ("div", ("mul", ("leaf", "c"), ("leaf", "d")), ("add", ("leaf", "a"), ("const", 3.0))))
+    got = run_gpu(e, env, {}, (64, 128), torch.bfloat16)
+    assert_bitexact(got, O.eval_expr(e, env))
+
+
+@pytest.mark.parametrize("op", ["add", "sub", "mul", "div", "max", "min", "floordiv", "mod"])
+def test_binary_ops_bitexact(op):
+    a = _u((64, 256), 20, lo=-4, hi=4)
+    b = _u((64, 256), 21, lo=0.25, hi=3)
+    env = {"a": a, "b": b}
+    e = (op, ("leaf", "a"), ("leaf", "b"))
+    got = run_gpu(e, env, {}, (64, 256), torch.bfloat16)
+    assert_bitexact(got, O.eval_expr(e, env))
+
+
+@pytest.mark.parametrize("op", ["exp", "log", "sqrt", "rsqrt", "tanh", "abs", "neg", "relu",
+                                "sigmoid", "recip"])
+def test_unary_ops(op):
+    lo, hi = (0.05, 4.0) if op in ("log", "sqrt", "rsqrt", "recip") else (-4.0, 4.0)
+    a = _u((64, 256), 30, lo=lo, hi=hi)
+    env = {"a": a}
+    e = (op, ("leaf", "a"))
+    got = run_gpu(e, env, {}, (64, 256), torch.bfloat16)
+    ref = O.eval_expr(e, env)
+    ulp = O.bf16_ulp_diff(got, ref)
+    assert int(ulp.max()) <= 1, f"{op}: max ulp {int(ulp.max())}"
+    a32 = a.float()
+    got32 = run_gpu(e, {"a": a32}, {}, (64, 256), torch.float32)
+    ref32 = O.eval_expr(e, {"a": a32})
+    torch.testing.assert_close(got32, ref32, rtol=4e-6, atol=1e-7)
+
+
+def test_pow_and_powi():
+    a = _u((32, 128), 40, lo=0.5, hi=2.0)
+    b = _u((32, 128), 41, lo=-2.0, hi=2.0)
+    env = {"a": a, "b": b}
+    for e in (("pow", ("leaf", "a"), ("leaf", "b")), ("powi", ("leaf", "a"), 3)):
+        got = run_gpu(e, env, {}, (32, 128), torch.bfloat16)
+        assert int(O.bf16_ulp_diff(got, O.eval_expr(e, env)).max()) <= 1
+
+
+def test_mixed_dtype_promotes_to_f32():
+    a = _u((64, 64), 50)
+    b = _u((64, 64), 51, torch.float32)
+    env = {"a": a, "b": b}
+    e = ("mul", ("leaf", "a"), ("leaf", "b"))
+    got = run_gpu(e, env, {}, (64, 64), torch.float32)
+    assert_bitexact(got, O.eval_expr(e, env))
+
+
+def test_tile_reuse_mask_and_region():
+    # one 32x32 tile re-used over the whole grid (block broadcast of a (1,1)
+    # block), written into a sub-region of a larger output
+    a = _u((128, 256), 60)
+    t = _u((32, 32), 61)
+    env = {"a": a, "t": t}
+    maps = {"a": {"row_off": -32, "col_off": -64}, "t": {"row_mask": 31, "col_mask": 31}}
+    e = ("add", ("leaf", "a"), ("leaf", "t"))
+    got = run_gpu(e, env, maps, (192, 320), torch.bfloat16, region=(32, 64, 128, 256))
+    ref = O.eval_expr(e, {"a": a, "t": t.repeat(4, 8)})
+    assert_bitexact(got[32:160, 64:320], ref)
+    assert (got[:32] == 7.0).all() and (got[:, :64] == 7.0).all()
+
+
+def test_scalar_path_unaligned_and_column_output():
+    # width-1 output (column vector) and an odd region force the 1-wide path
+    a = _u((96, 1), 70)
+    c = _u((96, 1), 71)
+    env = {"a": a, "c": c}
+    e = ("mul", ("leaf", "a"), ("leaf", "c"))
+    got = run_gpu(e, env, {}, (96, 1), torch.bfloat16)
+    assert_bitexact(got, O.eval_expr(e, env))
+    b = _u((40, 44), 72)
+    got = run_gpu(("neg", ("leaf", "b")), {"b": b}, {}, (40, 44), torch.bfloat16)
+    assert_bitexact(got, -b)
+
+
+def test_special_values_and_ties():
+    # NaN / inf propagation and exact bf16 rounding ties
+    vals = torch.tensor([float("nan"), float("inf"), -float("inf"), 0.0, -0.0, 1.0,
+                         1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, 65504.0, 3.0e38, 1e-38, -2.5],
+                        dtype=torch.float32)
+    a = vals.repeat(8, 1).reshape(8, 12)[:, :8].contiguous()
+    a = torch.cat([a, a], 1)  # (8, 16)
+    b = torch.full_like(a, 2 ** -9)
+    env = {"a": a, "b": b}
+    e = ("add", ("leaf", "a"), ("leaf", "b"))
+    got = run_gpu(e, env, {}, (8, 16), torch.bfloat16)
+    ref = O.eval_expr(e, env).to(torch.bfloat16)  # f32 add, one RNE rounding at the store
+    assert_bitexact(got, ref)
+    e2 = ("max", ("leaf", "a"), ("leaf", "b"))
+    got = run_gpu(e2, env, {}, (8, 16), torch.float32)
+    assert_bitexact(got, O.eval_expr(e2, env))

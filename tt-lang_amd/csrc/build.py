@@ -1,0 +1,72 @@
+"""Builds libttlhip.so (gfx950) from the HIP sources in this directory.
+
+Every source is compiled with hipcc for gfx950 only, in parallel, then linked
+into tt-lang_amd/ttlhip/libttlhip.so, where the Python runtime loads it.
+Packed-fp32 instruction selection is disabled for all device code.
+"""
+
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+CSRC = Path(__file__).resolve().parent
+PKG = CSRC.parent
+OUT_DIR = PKG / "ttlhip"
+LIB = OUT_DIR / "libttlhip.so"
+OBJ_DIR = CSRC / "_build"
+
+SOURCES = ["runtime.hip", "eltwise.hip", "matmul.hip", "bfp8.hip", "sdpa.hip"]
+
+ARCH = "gfx950"
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (ROCm is required to build libttlhip.so)")
+
+
+COMMON_FLAGS = [
+    "-std=c++17",
+    "-O3",
+    "-fPIC",
+    f"--offload-arch={ARCH}",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
+    "-I", str(PKG.parent / "include"),
+]
+
+
+def _compile(src: str) -> Path:
+    obj = OBJ_DIR / (Path(src).stem + ".o")
+    cmd = [hipcc(), *COMMON_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src}:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    return obj
+
+
+def build(verbose: bool = True) -> Path:
+    OBJ_DIR.mkdir(exist_ok=True)
+    with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES), 8)) as ex:
+        objs = list(ex.map(_compile, SOURCES))
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objs), "-o", str(tmp)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, LIB)
+    if verbose:
+        print(f"built {LIB}")
+    return LIB
+
+
+if __name__ == "__main__":
+    build()
+    sys.exit(0)

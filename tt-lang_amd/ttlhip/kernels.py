@@ -1,0 +1,177 @@
+"""Python wrappers of the libttlhip.so entry points (torch tensors in, launch out).
+
+Each wrapper validates shapes on the host (so that every address a kernel
+forms is inside its allocation), converts torch tensors to raw device
+pointers and calls the C ABI on the current torch stream.  None of them
+synchronises; callers that need reference (synchronous) semantics call
+torch.cuda.synchronize() themselves.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+from typing import List, Optional, Sequence
+
+import torch
+
+from . import _lib as L
+from .expr import StackProgram
+
+
+@dataclass
+class OperandMap:
+    """How an eltwise operand is addressed from output element (y, x):
+    iy = (y & row_mask) + row_off, ix = (x & col_mask) + col_off; a size-1
+    tensor dimension is broadcast (stride 0)."""
+
+    tensor: torch.Tensor
+    row_mask: int = -1
+    col_mask: int = -1
+    row_off: int = 0
+    col_off: int = 0
+
+
+def _check_device(t: torch.Tensor, what: str) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(f"{what} must be a device (HIP) tensor; there is no CPU path")
+    if t.dim() != 2:
+        raise ValueError(f"{what} must be 2-D, got shape {tuple(t.shape)}")
+
+
+def _axis_range(lo: int, n: int, mask: int, off: int):
+    """[min, max] of (c & mask) + off for c in [lo, lo + n)."""
+    if n <= 0:
+        return None
+    if mask == -1:
+        return lo + off, lo + n - 1 + off
+    vals_lo, vals_hi = 31, 0
+    if n >= 32:
+        vals_lo, vals_hi = 0, 31
+    else:
+        for c in range(lo, lo + n):
+            vals_lo, vals_hi = min(vals_lo, c & 31), max(vals_hi, c & 31)
+    return vals_lo + off, vals_hi + off
+
+
+def _operand_struct(m: OperandMap, y0: int, x0: int, h: int, w: int) -> L.Operand:
+    t = m.tensor
+    _check_device(t, "eltwise operand")
+    rows, cols = t.shape
+    rs = t.stride(0) if rows > 1 else 0
+    cs = t.stride(1) if cols > 1 else 0
+    if rows > 1:
+        r = _axis_range(y0, h, m.row_mask, m.row_off)
+        if r and (r[0] < 0 or r[1] >= rows):
+            raise ValueError(f"eltwise operand rows {r} out of range for shape {tuple(t.shape)}")
+    if cols > 1:
+        r = _axis_range(x0, w, m.col_mask, m.col_off)
+        if r and (r[0] < 0 or r[1] >= cols):
+            raise ValueError(f"eltwise operand cols {r} out of range for shape {tuple(t.shape)}")
+    return L.Operand(t.data_ptr(), L.dtype_code(t.dtype), 0, rs, cs, m.row_mask, m.col_mask,
+                     m.row_off, m.col_off)
+
+
+def eltwise(prog: StackProgram, operands: Sequence[Optional[OperandMap]], out: torch.Tensor,
+            region=None, stream=None) -> None:
+    """Runs a compiled stack program over `region` = (y0, x0, h, w) of `out`.
+
+    operands[k] is the operand of step k (None for steps without one).
+    """
+    _check_device(out, "eltwise output")
+    if out.stride(1) != 1:
+        raise ValueError("eltwise output must have unit column stride")
+    n = len(prog.steps)
+    if len(operands) != n:
+        raise ValueError(f"{n} steps but {len(operands)} operand slots")
+    y0, x0, h, w = region if region is not None else (0, 0, out.shape[0], out.shape[1])
+    if y0 < 0 or x0 < 0 or y0 + h > out.shape[0] or x0 + w > out.shape[1]:
+        raise ValueError(f"region {(y0, x0, h, w)} outside output {tuple(out.shape)}")
+    instrs = (L.Instr * n)()
+    ops = (L.Operand * n)()
+    for k, (s, m) in enumerate(zip(prog.steps, operands)):
+        instrs[k] = L.Instr(s.op, s.form, s.rnd, 0, s.imm)
+        if s.form in (L.FORM_LOAD, L.FORM_PUSH, L.FORM_BIN, L.FORM_BIN_REV):
+            if m is None:
+                raise ValueError(f"step {k} needs an operand")
+            ops[k] = _operand_struct(m, y0, x0, h, w)
+    L.call("ttlh_eltwise", instrs, ops, n, out.data_ptr(), L.dtype_code(out.dtype),
+           out.stride(0), y0, x0, h, w, L.stream_ptr(stream))
+
+
+def matmul(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, accumulate: bool = False,
+           stream=None) -> None:
+    """c (=|+=) a @ b on the GPU, fp32 accumulation (bf16 or f32 MFMA)."""
+    for t, nm in ((a, "A"), (b, "B"), (c, "C")):
+        _check_device(t, f"matmul {nm}")
+        if t.stride(1) != 1:
+            raise ValueError(f"matmul {nm} must be row-major with unit column stride")
+    M, K = a.shape
+    K2, N = b.shape
+    if K2 != K or tuple(c.shape) != (M, N):
+        raise ValueError(f"matmul shapes {tuple(a.shape)} @ {tuple(b.shape)} -> {tuple(c.shape)}")
+    L.call("ttlh_matmul", a.data_ptr(), L.dtype_code(a.dtype), a.stride(0), b.data_ptr(),
+           L.dtype_code(b.dtype), b.stride(0), c.data_ptr(), L.dtype_code(c.dtype), c.stride(0),
+           M, N, K, int(bool(accumulate)), L.stream_ptr(stream))
+
+
+def bfp8_tiles_bytes(rows: int, cols: int) -> int:
+    if rows % 32 or cols % 32:
+        raise ValueError(f"bfloat8_b needs whole 32x32 tiles, got {rows}x{cols}")
+    return (rows // 32) * (cols // 32) * L.TTLH_BFP8_TILE_BYTES
+
+
+def bfp8_pack_host(x: torch.Tensor) -> torch.Tensor:
+    """fp32 [rows, cols] (host) -> uint8 bfloat8_b tile bytes (host)."""
+    x = x.detach().to("cpu", torch.float32).contiguous()
+    rows, cols = x.shape
+    out = torch.empty(bfp8_tiles_bytes(rows, cols), dtype=torch.uint8)
+    L.call("ttlh_bfp8_pack_host", x.data_ptr(), out.data_ptr(), rows, cols)
+    return out
+
+
+def bfp8_unpack_host(q: torch.Tensor, rows: int, cols: int) -> torch.Tensor:
+    q = q.detach().to("cpu", torch.uint8).contiguous()
+    if q.numel() != bfp8_tiles_bytes(rows, cols):
+        raise ValueError("bfloat8_b byte count does not match the shape")
+    out = torch.empty((rows, cols), dtype=torch.bfloat16)
+    L.call("ttlh_bfp8_unpack_host", q.data_ptr(), out.data_ptr(), rows, cols)
+    return out
+
+
+def bfp8_unpack(q: torch.Tensor, rows: int, cols: int, stream=None) -> torch.Tensor:
+    if not q.is_cuda:
+        raise RuntimeError("bfp8_unpack takes device tiles")
+    if q.numel() != bfp8_tiles_bytes(rows, cols) or q.dtype != torch.uint8:
+        raise ValueError("bfloat8_b byte count does not match the shape")
+    out = torch.empty((rows, cols), dtype=torch.bfloat16, device=q.device)
+    L.call("ttlh_bfp8_unpack", q.data_ptr(), out.data_ptr(), rows, cols, L.stream_ptr(stream))
+    return out
+
+
+def matmul_bfp8w(a: torch.Tensor, bq: torch.Tensor, c: torch.Tensor, stream=None) -> None:
+    """c[M,N] = a[M,K] (bf16) @ dequant(bq)[K,N]; bf16 out."""
+    _check_device(a, "matmul_bfp8w A")
+    _check_device(c, "matmul_bfp8w C")
+    M, K = a.shape
+    M2, N = c.shape
+    if M2 != M or a.dtype != torch.bfloat16 or c.dtype != torch.bfloat16:
+        raise ValueError("matmul_bfp8w takes bf16 A [M,K] and bf16 C [M,N]")
+    if not bq.is_cuda or bq.dtype != torch.uint8 or bq.numel() != bfp8_tiles_bytes(K, N):
+        raise ValueError("matmul_bfp8w: Bq must be device uint8 tiles of a K x N matrix")
+    if a.stride(1) != 1 or c.stride(1) != 1:
+        raise ValueError("matmul_bfp8w: A and C must be row-major")
+    L.call("ttlh_matmul_bfp8w", a.data_ptr(), a.stride(0), bq.data_ptr(), c.data_ptr(),
+           c.stride(0), M, N, K, L.stream_ptr(stream))
+
+
+def sdpa_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor, scale: float,
+             causal: bool = False, stream=None) -> None:
+    for t, nm in ((q, "Q"), (k, "K"), (v, "V"), (o, "O")):
+        if not t.is_cuda or t.dtype != torch.bfloat16 or t.dim() != 4 or not t.is_contiguous():
+            raise ValueError(f"sdpa {nm} must be a contiguous bf16 device tensor [B,H,S,D]")
+        if tuple(t.shape) != tuple(q.shape):
+            raise ValueError("sdpa Q, K, V, O must share one shape")
+    B, H, S, D = q.shape
+    L.call("ttlh_sdpa_fwd", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), B, H, S, D,
+           float(scale), int(bool(causal)), L.stream_ptr(stream))
