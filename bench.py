@@ -178,9 +178,50 @@ class EltwiseWorkload(Workload):
                           f"(simulator granularity), {dt:.1f} s"}
 
 
+class MatmulWorkload(Workload):
+    """C3: C[M,N] = A[M,K] . B[K,N], bf16 in, fp32 accumulate, bf16 out."""
+
+    bound = "mfma"
+    unit = "TFLOP/s"
+
+    def __init__(self, name, M, N, K, seed=99):
+        self.name, self.M, self.N, self.K, self.seed = name, M, N, K, seed
+
+    def kernel_name(self):
+        return "mm_bf16_kernel"
+
+    def work_per_step(self):
+        return 2.0 * self.M * self.N * self.K
+
+    def setup(self):
+        from oracle.tile_ops import seeded
+        std = 1.0 / math.sqrt(self.K)
+        self.a = seeded((self.M, self.K), "normal", self.seed, std=std).cuda()
+        self.b = seeded((self.K, self.N), "normal", self.seed + 1, std=std).cuda()
+        self.c = torch.empty((self.M, self.N), dtype=torch.bfloat16, device="cuda")
+        from ttlhip import _lib as L
+        self._args = (self.a.data_ptr(), L.TTLH_BF16, self.K, self.b.data_ptr(), L.TTLH_BF16,
+                      self.N, self.c.data_ptr(), L.TTLH_BF16, self.N, self.M, self.N, self.K, 0)
+
+    def launch(self, i):
+        from ttlhip import _lib as L
+        L.call("ttlh_matmul", *self._args, L.stream_ptr())
+
+    def check(self):
+        """64 sampled rows against float64: max error relative to max |C|."""
+        self.launch(0)
+        torch.cuda.synchronize()
+        rows = torch.arange(0, self.M, max(1, self.M // 64))
+        exact = self.a.cpu()[rows].double() @ self.b.cpu().double()
+        got = self.c.cpu()[rows].double()
+        return {"max_abs_err_rel": float((got - exact).abs().max() / exact.abs().max()),
+                "rows_checked": int(rows.numel())}
+
+
 WORKLOADS = {
     "eltwise_add_2048": lambda: EltwiseWorkload("eltwise_add_2048", 2048, 2048, "add"),
     "exp_bcast_mul_4096": lambda: EltwiseWorkload("exp_bcast_mul_4096", 4096, 4096, "pipe"),
+    "matmul_bf16_4096": lambda: MatmulWorkload("matmul_bf16_4096", 4096, 4096, 4096),
 }
 HEADLINE = "exp_bcast_mul_4096"
 

@@ -1,0 +1,95 @@
+"""GPU parity of the tile matmul (ttlh_matmul) against the CPU oracle.
+
+The simulator multiplies 32x32 tiles in the input dtype and accumulates the K
+tile products with store(acc=True) in the output block's dtype
+(oracle.tile_ops.tile_matmul_sim); the MI355X kernel accumulates the full K
+in fp32 and rounds once.  Parity bar (stated by the north star for bf16):
+  - |gpu - exact| <= 1 bf16 ulp of |exact| + 1e-6 * sqrt(K) * max|exact|
+    (one final rounding plus fp32 accumulation error), i.e. max-abs well
+    inside 1e-2 relative to the fp32/fp64 reference, and
+  - the GPU's max error is no worse than the simulator restatement's.
+fp32 inputs: torch.testing.assert_close against float64 with rtol = atol = 1e-5
+(the examples' own assert_pcc uses rtol = atol = 1e-4).
+"""
+
+import math
+
+import pytest
+import torch
+
+from oracle import tile_ops as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _mm(a, b, out_dtype, accumulate=False, c0=None):
+    from ttlhip import kernels as K
+
+    da, db = a.cuda(), b.cuda()
+    c = (c0.cuda().clone() if c0 is not None
+         else torch.zeros((a.shape[0], b.shape[1]), dtype=out_dtype, device="cuda"))
+    K.matmul(da, db, c, accumulate=accumulate)
+    torch.cuda.synchronize()
+    return c.cpu()
+
+
+def _inputs(M, K, N, seed, dtype=torch.bfloat16):
+    a = O.seeded((M, K), "normal", seed, dtype, std=1.0 / math.sqrt(K) ** 0.5)
+    b = O.seeded((K, N), "normal", seed + 1, dtype, std=1.0 / math.sqrt(K) ** 0.5)
+    return a, b
+
+
+@pytest.mark.parametrize("M,K,N", [(128, 128, 128), (256, 384, 192), (96, 160, 224),
+                                   (32, 32, 32), (512, 1024, 256)])
+def test_bf16_matmul_vs_exact_and_sim(M, K, N):
+    a, b = _inputs(M, K, N, 7)
+    got = _mm(a, b, torch.bfloat16).double()
+    exact = O.matmul_fp64(a, b)
+    sim = O.tile_matmul_sim(a, b).double()
+    err_gpu = (got - exact).abs()
+    err_sim = (sim - exact).abs()
+    bound = exact.abs() * 2.0 ** -8 + 1e-6 * math.sqrt(K) * float(exact.abs().max())
+    assert bool((err_gpu <= bound).all()), f"max err {float(err_gpu.max())}"
+    assert float(err_gpu.max()) <= float(err_sim.max()) + 1e-12
+    assert float(err_gpu.max()) <= 1e-2 * float(exact.abs().max())
+
+
+def test_bf16_matmul_accumulate_and_f32_out():
+    a, b = _inputs(128, 256, 160, 11)
+    c0 = O.seeded((128, 160), "normal", 13, torch.float32)
+    got = _mm(a, b, torch.float32, accumulate=True, c0=c0).double()
+    exact = O.matmul_fp64(a, b) + c0.double()
+    torch.testing.assert_close(got, exact, rtol=1e-5, atol=1e-5)
+
+
+def test_bf16_matmul_layout_known_answer():
+    # A = identity-like permutation, B = distinct integers: every output element
+    # is an exact small integer, so any lane-layout mistake shows up exactly.
+    M = K = N = 128
+    perm = torch.randperm(K, generator=torch.Generator().manual_seed(3))
+    a = torch.zeros(M, K)
+    a[torch.arange(M), perm] = 1.0
+    b = (torch.arange(K * N).reshape(K, N) % 251).float()
+    got = _mm(a.bfloat16(), b.bfloat16(), torch.float32)
+    assert torch.equal(got, b[perm])
+
+
+@pytest.mark.parametrize("M,K,N", [(64, 64, 64), (128, 256, 64), (96, 160, 224)])
+def test_f32_matmul(M, K, N):
+    a = O.seeded((M, K), "uniform", 21, torch.float32, lo=0, hi=1)
+    b = O.seeded((K, N), "uniform", 22, torch.float32, lo=0, hi=1)
+    got = _mm(a, b, torch.float32).double()
+    torch.testing.assert_close(got, O.matmul_fp64(a, b), rtol=1e-5, atol=1e-5)
+
+
+def test_bf16_matmul_4096_sampled_rows():
+    # the benchmark shape: check 64 sampled rows against float64
+    M = K = N = 4096
+    a = O.seeded((M, K), "normal", 31, torch.bfloat16, std=1.0 / math.sqrt(K))
+    b = O.seeded((K, N), "normal", 32, torch.bfloat16, std=1.0 / math.sqrt(K))
+    got = _mm(a, b, torch.bfloat16).double()
+    rows = torch.arange(0, M, M // 64)
+    exact = a[rows].double() @ b.double()
+    err = (got[rows] - exact).abs()
+    bound = exact.abs() * 2.0 ** -8 + 1e-6 * math.sqrt(K) * float(exact.abs().max())
+    assert bool((err <= bound).all()), f"max err {float(err.max())}"
