@@ -1,0 +1,355 @@
+"""Eager CPU executor of tt-lang kernels with the simulator's semantics
+(TEST ORACLE ONLY - never imported by the product).
+
+Each core runs its three threads as real Python threads that block on
+circular buffers, one torch op per 32x32 tile, exactly the execution model of
+the reference simulator (python/sim/program.py:100-255 runs cores one after
+another, threads cooperatively; here threads block on condition variables,
+which yields the same dataflow).  Restated rules, with the reference lines
+they follow:
+  - CB: capacity = shape0 * shape1 * buffer_factor tiles; reserve() blocks
+    until a block is free and zero-fills it in the CB dtype; push() publishes;
+    wait() blocks until a block is visible; pop() frees (cb.py:302-408).
+  - copy(tensor[rows, cols] -> block): tile (h, w) of the slice goes to slot
+    h * width + w; size-1 tensor dimensions stay size 1 (copyhandlers.py:
+    103-131, 295-336; tensoraccessor.py:125-159); block -> tensor is the
+    inverse (copyhandlers.py:339-380).
+  - block ops: equal shapes are tile-wise; otherwise tiles are stacked and
+    torch-broadcast over the tile grid (block.py:870-959,
+    ttnnsim.py:67-109); every result is materialised in its torch dtype.
+  - store(acc=True): first store assigns, later ones add in the stored
+    tensors' dtype (block.py:805-868).
+  - grid / core / grid_size (kernel.py:89-291); grid "auto" = (8, 8).
+The oracle takes plain CPU torch tensors and is driven through `make_ttl()`,
+which returns a namespace with the same names as `ttl`.
+"""
+
+from __future__ import annotations
+
+import operator
+import threading
+import types
+from typing import Any, List, Optional, Tuple
+
+import torch
+
+TILE = 32
+TIMEOUT_S = 30.0
+
+
+class OracleTensor:
+    """CPU tensor with tt-lang tile indexing."""
+
+    def __init__(self, t: torch.Tensor):
+        self.t = t
+
+    @property
+    def shape(self):
+        return tuple(self.t.shape)
+
+    @property
+    def dtype(self):
+        return self.t.dtype
+
+    def __getitem__(self, key):
+        rows, cols = key
+        return _Slice(self, rows, cols)
+
+
+class _Slice:
+    def __init__(self, tensor: OracleTensor, rows, cols):
+        def norm(k):
+            if isinstance(k, slice):
+                assert k.start is not None and k.stop is not None and k.step is None
+                return k.start, k.stop
+            return int(k), int(k) + 1
+        self.tensor = tensor
+        self.rows = norm(rows)
+        self.cols = norm(cols)
+
+    def elements(self) -> torch.Tensor:
+        (r0, r1), (c0, c1) = self.rows, self.cols
+        return self.tensor.t[r0 * TILE:r1 * TILE, c0 * TILE:c1 * TILE]
+
+    def tiles_shape(self) -> Tuple[int, int]:
+        e = self.elements()
+        h, w = e.shape
+        return (1 if h == 1 else h // TILE, 1 if w == 1 else w // TILE)
+
+
+class _CB:
+    def __init__(self, element, shape, buffer_factor):
+        self.dtype = element.dtype
+        self.shape = tuple(shape)
+        self.n = shape[0] * shape[1]
+        self.capacity = self.n * buffer_factor
+        self.reset()
+
+    def reset(self):
+        self.cond = threading.Condition()
+        self.slots: List[Optional[torch.Tensor]] = [None] * self.capacity
+        self.head = 0      # first visible tile
+        self.visible = 0
+        self.reserved = 0  # tiles reserved (not yet pushed)
+
+    def _wait_for(self, pred, what):
+        if not self.cond.wait_for(pred, timeout=TIMEOUT_S):
+            raise RuntimeError(f"deadlock: timed out in {what}")
+
+    def reserve(self):
+        with self.cond:
+            self._wait_for(lambda: self.capacity - self.visible - self.reserved >= self.n, "reserve")
+            start = (self.head + self.visible) % self.capacity
+            self.reserved = self.n
+            idx = [(start + i) % self.capacity for i in range(self.n)]
+            for i in idx:  # zero-fill in the CB dtype (cb.py:343-346)
+                self.slots[i] = torch.zeros(TILE, TILE, dtype=self.dtype)
+        return _Block(self, idx, "reserve")
+
+    def push(self):
+        with self.cond:
+            self.visible += self.n
+            self.reserved = 0
+            self.cond.notify_all()
+
+    def wait(self):
+        with self.cond:
+            self._wait_for(lambda: self.visible >= self.n, "wait")
+            idx = [(self.head + i) % self.capacity for i in range(self.n)]
+        return _Block(self, idx, "wait")
+
+    def pop(self):
+        with self.cond:
+            self.head = (self.head + self.n) % self.capacity
+            self.visible -= self.n
+            self.cond.notify_all()
+
+
+class _Tiles:
+    """A block-shaped list of tiles (result of block arithmetic)."""
+
+    def __init__(self, tiles: List[torch.Tensor], shape: Tuple[int, int]):
+        self.tiles = tiles
+        self.shape = shape
+
+    def _bin(self, other, op):
+        other = _tiles_of(other)
+        if self.shape == other.shape:
+            return _Tiles([op(a, b) for a, b in zip(self.tiles, other.tiles)], self.shape)
+        for i, (l, r) in enumerate(zip(self.shape, other.shape)):
+            if l != r and l != 1 and r != 1:
+                raise ValueError(f"Cannot broadcast: incompatible shapes {self.shape} and "
+                                 f"{other.shape}")
+        a = torch.stack(self.tiles).reshape(*self.shape, *self.tiles[0].shape)
+        b = torch.stack(other.tiles).reshape(*other.shape, *other.tiles[0].shape)
+        res = op(a, b)
+        shape = (res.shape[0], res.shape[1])
+        flat = res.reshape(shape[0] * shape[1], *res.shape[2:])
+        return _Tiles([flat[i] for i in range(flat.shape[0])], shape)
+
+    def __add__(self, o): return self._bin(o, operator.add)
+    def __sub__(self, o): return self._bin(o, operator.sub)
+    def __mul__(self, o): return self._bin(o, operator.mul)
+    def __truediv__(self, o): return self._bin(o, operator.truediv)
+    def __floordiv__(self, o): return self._bin(o, operator.floordiv)
+    def __mod__(self, o): return self._bin(o, operator.mod)
+    def __matmul__(self, o): return self._bin(o, operator.matmul)
+
+    def __pow__(self, o):
+        if isinstance(o, int):
+            return _Tiles([t ** o for t in self.tiles], self.shape)
+        return self._bin(o, operator.pow)
+
+    def map(self, fn):
+        return _Tiles([fn(t) for t in self.tiles], self.shape)
+
+
+def _tiles_of(x) -> _Tiles:
+    if isinstance(x, _Tiles):
+        return x
+    if isinstance(x, _Block):
+        return _Tiles([x.cb.slots[i] for i in x.idx], x.cb.shape)
+    raise TypeError(type(x))
+
+
+class _Block(_Tiles):
+    def __init__(self, cb: _CB, idx: List[int], kind: str):
+        self.cb, self.idx, self.kind = cb, idx, kind
+        self.shape = cb.shape
+        self._first_acc = True
+
+    @property
+    def tiles(self):
+        return [self.cb.slots[i] for i in self.idx]
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, et, e, tb):
+        if et is None:
+            (self.cb.push if self.kind == "reserve" else self.cb.pop)()
+
+    def store(self, items, acc: bool = False):
+        src = _tiles_of(items).tiles
+        if len(src) != len(self.idx):
+            raise ValueError("Length mismatch in store()")
+        if acc and not self._first_acc:
+            for k, i in enumerate(self.idx):
+                self.cb.slots[i] = self.cb.slots[i] + src[k]
+        else:
+            for k, i in enumerate(self.idx):
+                self.cb.slots[i] = src[k]
+        if acc:
+            self._first_acc = False
+
+
+def _copy(src, dst):
+    if isinstance(src, _Slice) and isinstance(dst, _Block):
+        if src.tiles_shape() != dst.shape:
+            raise ValueError("copy: tensor slice does not match the block shape")
+        e = src.elements()
+        h, w = dst.shape
+        for k, i in enumerate(dst.idx):
+            r, c = divmod(k, w)
+            dst.cb.slots[i] = e[r * TILE:(r + 1) * TILE, c * TILE:(c + 1) * TILE].clone()
+    elif isinstance(src, _Block) and isinstance(dst, _Slice):
+        if dst.tiles_shape() != src.shape:
+            raise ValueError("copy: tensor slice does not match the block shape")
+        e = dst.elements()
+        h, w = src.shape
+        for k, i in enumerate(src.idx):
+            r, c = divmod(k, w)
+            e[r * TILE:(r + 1) * TILE, c * TILE:(c + 1) * TILE] = src.cb.slots[i]
+    else:
+        raise NotImplementedError("oracle copy supports tensor<->block only")
+
+    class _Tx:
+        def wait(self):
+            return None
+    return _Tx()
+
+
+def make_ttl():
+    """A `ttl`-compatible namespace backed by this eager executor."""
+    state = threading.local()
+    registry: List[Any] = []
+    cbs: List[_CB] = []
+    ns = types.SimpleNamespace()
+    ns.TILE_SHAPE = (TILE, TILE)
+
+    def grid_size(dims=2):
+        g = tuple(state.grid)
+        if dims == len(g):
+            r = g
+        elif dims < len(g):
+            tail = 1
+            for d in g[dims - 1:]:
+                tail *= d
+            r = tuple(g[:dims - 1]) + (tail,)
+        else:
+            r = g + (1,) * (dims - len(g))
+        return r[0] if dims == 1 else r
+
+    def core(dims=2):
+        g = tuple(state.grid)
+        cid = state.core
+        coords = []
+        for s in reversed(g):
+            coords.append(cid % s)
+            cid //= s
+        coords.reverse()
+        if dims < len(coords):
+            flat = coords[0]
+            for i in range(1, len(coords) - dims + 1):
+                flat = flat * g[i] + coords[i]
+            coords = [flat] + coords[len(coords) - dims + 1:]
+        while len(coords) < dims:
+            coords.append(0)
+        return coords[0] if dims == 1 else tuple(coords)
+
+    def compute():
+        def deco(f):
+            registry.append(("compute", f))
+            return f
+        return deco
+
+    def datamovement():
+        def deco(f):
+            registry.append(("dm", f))
+            return f
+        return deco
+
+    def make_cb(element, shape, buffer_factor=2):
+        cb = _CB(element, shape, buffer_factor)
+        cbs.append(cb)
+        return cb
+
+    class _Math:
+        @staticmethod
+        def broadcast(block, _u=None, dims=None):
+            t = _tiles_of(block)
+            for d in dims:
+                if t.shape[d] != 1:
+                    raise ValueError("broadcast dimension must have size 1")
+            return _Tiles(list(t.tiles), t.shape)
+
+    for name, fn in (("exp", torch.exp), ("log", torch.log), ("sqrt", torch.sqrt),
+                     ("rsqrt", torch.rsqrt), ("tanh", torch.tanh), ("abs", torch.abs),
+                     ("neg", torch.neg), ("relu", torch.relu), ("sigmoid", torch.sigmoid),
+                     ("recip", torch.reciprocal)):
+        setattr(_Math, name, staticmethod(lambda x, _f=fn: _tiles_of(x).map(_f)))
+    _Math.max = staticmethod(lambda a, b: _tiles_of(a)._bin(b, torch.maximum))
+    _Math.min = staticmethod(lambda a, b: _tiles_of(a)._bin(b, torch.minimum))
+
+    def kernel(grid="auto"):
+        actual = (8, 8) if grid == "auto" else tuple(grid)
+
+        def deco(func):
+            def run(*args, **kwargs):
+                registry.clear()
+                cbs.clear()
+                g = dict(func.__globals__)
+                g["grid"] = actual
+                body = types.FunctionType(func.__code__, g, func.__name__, func.__defaults__,
+                                          func.__closure__)
+                state.grid = actual
+                body(*args, **kwargs)
+                threads = list(registry)
+                if len(threads) != 3:
+                    raise ValueError("Kernel must define exactly 3 threads (compute, dm0, dm1), "
+                                     f"got {len(threads)}")
+                ncores = 1
+                for d in actual:
+                    ncores *= d
+                for c in range(ncores):
+                    for cb in cbs:
+                        cb.reset()
+                    errors = []
+
+                    def runner(f, c=c):
+                        state.grid = actual
+                        state.core = c
+                        try:
+                            f()
+                        except BaseException as e:  # surfaced after join
+                            errors.append(e)
+
+                    ts = [threading.Thread(target=runner, args=(f,)) for _, f in threads]
+                    for t in ts:
+                        t.start()
+                    for t in ts:
+                        t.join()
+                    if errors:
+                        raise errors[0]
+            return run
+        return deco
+
+    ns.kernel = kernel
+    ns.grid_size = grid_size
+    ns.core = core
+    ns.compute = compute
+    ns.datamovement = datamovement
+    ns.make_circular_buffer_like = make_cb
+    ns.copy = _copy
+    ns.math = _Math()
+    return ns

@@ -1,0 +1,331 @@
+"""tt-lang kernels used by the parity tests.
+
+Each factory takes a `ttl` namespace (this build's drop-in, or the CPU oracle's
+eager executor) and returns the kernel, so one kernel source runs on both.
+They are written in the styles of the reference examples (examples/
+eltwise_add.py, broadcast.py, singlecore_matmul.py, multicore_matmul.py):
+column-split elementwise with (2, 1) blocks, 4x4-tile broadcast blocks on an
+8x8 grid, (1, 1)-tile matmul with store(acc=True) on one core and split over
+a 13x10 grid with split_work_to_cores.
+"""
+
+import math
+
+TILE = 32
+
+
+def make_eltwise_add(ttl, granularity=2, grid="auto"):
+    @ttl.kernel(grid=grid)
+    def eltwise_add(a_in, b_in, out):
+        row_tiles = a_in.shape[0] // ttl.TILE_SHAPE[0]
+        col_tiles = a_in.shape[1] // ttl.TILE_SHAPE[1]
+        gh, gw = ttl.grid_size()
+        cols_per_core = math.ceil(col_tiles / (gh * gw))
+        a_cb = ttl.make_circular_buffer_like(a_in, shape=(granularity, 1), buffer_factor=2)
+        b_cb = ttl.make_circular_buffer_like(b_in, shape=(granularity, 1), buffer_factor=2)
+        o_cb = ttl.make_circular_buffer_like(out, shape=(granularity, 1), buffer_factor=2)
+
+        @ttl.compute()
+        def comp():
+            c = ttl.core(dims=1)
+            start = c * cols_per_core
+            end = min(start + cols_per_core, col_tiles)
+            for ct in range(start, end):
+                for rb in range(row_tiles // granularity):
+                    a = a_cb.wait()
+                    b = b_cb.wait()
+                    o = o_cb.reserve()
+                    o.store(a + b)
+                    o_cb.push()
+                    a_cb.pop()
+                    b_cb.pop()
+
+        @ttl.datamovement()
+        def reader():
+            c = ttl.core(dims=1)
+            start = c * cols_per_core
+            end = min(start + cols_per_core, col_tiles)
+            for ct in range(start, end):
+                for rb in range(row_tiles // granularity):
+                    rows = slice(rb * granularity, (rb + 1) * granularity)
+                    cols = slice(ct, ct + 1)
+                    blk = a_cb.reserve()
+                    ttl.copy(a_in[rows, cols], blk).wait()
+                    a_cb.push()
+                    blk = b_cb.reserve()
+                    ttl.copy(b_in[rows, cols], blk).wait()
+                    b_cb.push()
+
+        @ttl.datamovement()
+        def writer():
+            c = ttl.core(dims=1)
+            start = c * cols_per_core
+            end = min(start + cols_per_core, col_tiles)
+            for ct in range(start, end):
+                for rb in range(row_tiles // granularity):
+                    rows = slice(rb * granularity, (rb + 1) * granularity)
+                    blk = o_cb.wait()
+                    ttl.copy(blk, out[rows, slice(ct, ct + 1)]).wait()
+                    o_cb.pop()
+
+    return eltwise_add
+
+
+def make_bcast_fma(ttl, g=4, grid=(8, 8)):
+    """y = a * b + broadcast(c, dims=[1]) with c a column vector (N, 1)."""
+
+    @ttl.kernel(grid=grid)
+    def bcast_fma(a, b, c, y):
+        gx, gy = ttl.grid_size(dims=2)
+        rows_per_core = a.shape[0] // TILE // gx // g
+        cols_per_core = a.shape[1] // TILE // gy // g
+        a_cb = ttl.make_circular_buffer_like(a, shape=(g, g), buffer_factor=2)
+        b_cb = ttl.make_circular_buffer_like(b, shape=(g, g), buffer_factor=2)
+        c_cb = ttl.make_circular_buffer_like(c, shape=(g, 1), buffer_factor=2)
+        y_cb = ttl.make_circular_buffer_like(y, shape=(g, g), buffer_factor=2)
+
+        @ttl.compute()
+        def comp():
+            for _ in range(rows_per_core):
+                for _ in range(cols_per_core):
+                    with a_cb.wait() as ab, b_cb.wait() as bb, c_cb.wait() as cb, \
+                            y_cb.reserve() as yb:
+                        yb.store(ab * bb + ttl.math.broadcast(cb, dims=[1]))
+
+        @ttl.datamovement()
+        def reader():
+            cx, cy = ttl.core(dims=2)
+            for i in range(rows_per_core):
+                r = (cx * rows_per_core + i) * g
+                for j in range(cols_per_core):
+                    col = (cy * cols_per_core + j) * g
+                    with a_cb.reserve() as ab, b_cb.reserve() as bb, c_cb.reserve() as cb:
+                        ta = ttl.copy(a[r:r + g, col:col + g], ab)
+                        tb = ttl.copy(b[r:r + g, col:col + g], bb)
+                        tc = ttl.copy(c[r:r + g, 0], cb)
+                        ta.wait()
+                        tb.wait()
+                        tc.wait()
+
+        @ttl.datamovement()
+        def writer():
+            cx, cy = ttl.core(dims=2)
+            for i in range(rows_per_core):
+                r = (cx * rows_per_core + i) * g
+                for j in range(cols_per_core):
+                    col = (cy * cols_per_core + j) * g
+                    with y_cb.wait() as yb:
+                        ttl.copy(yb, y[r:r + g, col:col + g]).wait()
+
+    return bcast_fma
+
+
+def make_exp_row_pipe(ttl, g=4, grid=(8, 8)):
+    """y = exp(a + broadcast(b_row, dims=[0])) * c, b_row of shape (1, W)
+    (BASELINE configs[1])."""
+
+    @ttl.kernel(grid=grid)
+    def exp_row_pipe(a, b_row, c, y):
+        gx, gy = ttl.grid_size(dims=2)
+        rows_per_core = a.shape[0] // TILE // gx // g
+        cols_per_core = a.shape[1] // TILE // gy // g
+        a_cb = ttl.make_circular_buffer_like(a, shape=(g, g), buffer_factor=2)
+        b_cb = ttl.make_circular_buffer_like(b_row, shape=(1, g), buffer_factor=2)
+        c_cb = ttl.make_circular_buffer_like(c, shape=(g, g), buffer_factor=2)
+        y_cb = ttl.make_circular_buffer_like(y, shape=(g, g), buffer_factor=2)
+
+        @ttl.compute()
+        def comp():
+            for _ in range(rows_per_core):
+                for _ in range(cols_per_core):
+                    with a_cb.wait() as ab, b_cb.wait() as bb, c_cb.wait() as cb, \
+                            y_cb.reserve() as yb:
+                        yb.store(ttl.math.exp(ab + ttl.math.broadcast(bb, dims=[0])) * cb)
+
+        @ttl.datamovement()
+        def reader():
+            cx, cy = ttl.core(dims=2)
+            for i in range(rows_per_core):
+                r = (cx * rows_per_core + i) * g
+                for j in range(cols_per_core):
+                    col = (cy * cols_per_core + j) * g
+                    with a_cb.reserve() as ab, b_cb.reserve() as bb, c_cb.reserve() as cb:
+                        ttl.copy(a[r:r + g, col:col + g], ab).wait()
+                        ttl.copy(b_row[0, col:col + g], bb).wait()
+                        ttl.copy(c[r:r + g, col:col + g], cb).wait()
+
+        @ttl.datamovement()
+        def writer():
+            cx, cy = ttl.core(dims=2)
+            for i in range(rows_per_core):
+                r = (cx * rows_per_core + i) * g
+                for j in range(cols_per_core):
+                    col = (cy * cols_per_core + j) * g
+                    with y_cb.wait() as yb:
+                        ttl.copy(yb, y[r:r + g, col:col + g]).wait()
+
+    return exp_row_pipe
+
+
+def make_matmul_single(ttl):
+    @ttl.kernel(grid=(1, 1))
+    def mm_single(a, b, out):
+        Mt, Kt, Nt = a.shape[0] // TILE, a.shape[1] // TILE, b.shape[1] // TILE
+        a_cb = ttl.make_circular_buffer_like(a, shape=(1, 1), buffer_factor=2)
+        b_cb = ttl.make_circular_buffer_like(b, shape=(1, 1), buffer_factor=2)
+        o_cb = ttl.make_circular_buffer_like(out, shape=(1, 1), buffer_factor=2)
+
+        @ttl.compute()
+        def comp():
+            for _ in range(Mt):
+                for _ in range(Nt):
+                    with o_cb.reserve() as ob:
+                        for _ in range(Kt):
+                            with a_cb.wait() as ab, b_cb.wait() as bb:
+                                ob.store(ab @ bb, acc=True)
+
+        @ttl.datamovement()
+        def reader():
+            for m in range(Mt):
+                for n in range(Nt):
+                    for k in range(Kt):
+                        with a_cb.reserve() as ab, b_cb.reserve() as bb:
+                            ttl.copy(a[m, k], ab).wait()
+                            ttl.copy(b[k, n], bb).wait()
+
+        @ttl.datamovement()
+        def writer():
+            for m in range(Mt):
+                for n in range(Nt):
+                    with o_cb.wait() as ob:
+                        ttl.copy(ob, out[m, n]).wait()
+
+    return mm_single
+
+
+def make_matmul_multi(ttl, ttnn, grid=(13, 10)):
+    @ttl.kernel(grid=grid)
+    def mm_multi(a, b, out):
+        Kt, Nt = a.shape[1] // TILE, b.shape[1] // TILE
+        total = (a.shape[0] * b.shape[1]) // (TILE * TILE)
+        a_cb = ttl.make_circular_buffer_like(a, shape=(1, 1), buffer_factor=2)
+        b_cb = ttl.make_circular_buffer_like(b, shape=(1, 1), buffer_factor=2)
+        o_cb = ttl.make_circular_buffer_like(out, shape=(1, 1), buffer_factor=2)
+        ys, xs = ttl.grid_size(dims=2)
+        _, _, g1, g2, w1, w2 = ttnn.split_work_to_cores(ttnn.CoreCoord(xs, ys), total,
+                                                         row_wise=True)
+        n1, n2 = g1.num_cores(), g2.num_cores()
+
+        def tiles_of(cid):
+            return w1 if cid < n1 else (w2 if cid < n1 + n2 else 0)
+
+        def first_of(cid):
+            return cid * w1 if cid < n1 else n1 * w1 + (cid - n1) * w2
+
+        @ttl.compute()
+        def comp():
+            cid = ttl.core(dims=1)
+            for _ in range(tiles_of(cid)):
+                with o_cb.reserve() as ob:
+                    for _ in range(Kt):
+                        with a_cb.wait() as ab, b_cb.wait() as bb:
+                            ob.store(ab @ bb, acc=True)
+
+        @ttl.datamovement()
+        def reader():
+            cid = ttl.core(dims=1)
+            for t in range(tiles_of(cid)):
+                tid = first_of(cid) + t
+                r, c = tid // Nt, tid % Nt
+                for k in range(Kt):
+                    with a_cb.reserve() as ab, b_cb.reserve() as bb:
+                        ttl.copy(a[r, k], ab).wait()
+                        ttl.copy(b[k, c], bb).wait()
+
+        @ttl.datamovement()
+        def writer():
+            cid = ttl.core(dims=1)
+            for t in range(tiles_of(cid)):
+                tid = first_of(cid) + t
+                with o_cb.wait() as ob:
+                    ttl.copy(ob, out[tid // Nt, tid % Nt]).wait()
+
+    return mm_multi
+
+
+def make_tile_reuse(ttl):
+    """One (1, 1) block of `t` broadcast over a (2, 2) block of `a` (block
+    broadcasting across the tile grid), minus a scalar-free chain."""
+
+    @ttl.kernel(grid=(2, 2))
+    def tile_reuse(a, t, out):
+        rt, ct = a.shape[0] // TILE, a.shape[1] // TILE
+        gy, gx = ttl.grid_size(dims=2)
+        rpc, cpc = rt // gy // 2, ct // gx // 2
+        a_cb = ttl.make_circular_buffer_like(a, shape=(2, 2), buffer_factor=2)
+        t_cb = ttl.make_circular_buffer_like(t, shape=(1, 1), buffer_factor=2)
+        o_cb = ttl.make_circular_buffer_like(out, shape=(2, 2), buffer_factor=2)
+
+        @ttl.compute()
+        def comp():
+            for _ in range(rpc * cpc):
+                with a_cb.wait() as ab, t_cb.wait() as tb, o_cb.reserve() as ob:
+                    ob.store((ab - tb) * ab)
+
+        @ttl.datamovement()
+        def reader():
+            y, x = ttl.core(dims=2)
+            for i in range(rpc):
+                for j in range(cpc):
+                    r, c = (y * rpc + i) * 2, (x * cpc + j) * 2
+                    with a_cb.reserve() as ab, t_cb.reserve() as tb:
+                        ttl.copy(a[r:r + 2, c:c + 2], ab).wait()
+                        ttl.copy(t[0, 0], tb).wait()
+
+        @ttl.datamovement()
+        def writer():
+            y, x = ttl.core(dims=2)
+            for i in range(rpc):
+                for j in range(cpc):
+                    r, c = (y * rpc + i) * 2, (x * cpc + j) * 2
+                    with o_cb.wait() as ob:
+                        ttl.copy(ob, out[r:r + 2, c:c + 2]).wait()
+
+    return tile_reuse
+
+
+def make_branchy_add(ttl):
+    """Branches on a loop variable, which forces the scalar trace fallback."""
+
+    @ttl.kernel(grid=(1, 2))
+    def branchy(a, b, out):
+        rt, ct = a.shape[0] // TILE, a.shape[1] // TILE
+        a_cb = ttl.make_circular_buffer_like(a, shape=(1, 1), buffer_factor=2)
+        b_cb = ttl.make_circular_buffer_like(b, shape=(1, 1), buffer_factor=2)
+        o_cb = ttl.make_circular_buffer_like(out, shape=(1, 1), buffer_factor=2)
+
+        @ttl.compute()
+        def comp():
+            c = ttl.core(dims=1)
+            for _ in range(rt * ct // 2):
+                with a_cb.wait() as ab, b_cb.wait() as bb, o_cb.reserve() as ob:
+                    ob.store(ab + bb)
+
+        @ttl.datamovement()
+        def reader():
+            c = ttl.core(dims=1)
+            for i in range(rt * ct):
+                if i % 2 == c:  # data-dependent branch on the loop variable
+                    with a_cb.reserve() as ab, b_cb.reserve() as bb:
+                        ttl.copy(a[i // ct, i % ct], ab).wait()
+                        ttl.copy(b[i // ct, i % ct], bb).wait()
+
+        @ttl.datamovement()
+        def writer():
+            c = ttl.core(dims=1)
+            for i in range(rt * ct):
+                if i % 2 == c:
+                    with o_cb.wait() as ob:
+                        ttl.copy(ob, out[i // ct, i % ct]).wait()
+
+    return branchy

@@ -1,0 +1,84 @@
+"""CPU interpreter of a front-end Plan (test infrastructure).
+
+Executes the launches a traced kernel produced with torch on the CPU, using
+the launch's own operand maps (mask / offset / size-1 broadcast) and stack
+program, so the CPU test suite can check the tracer + planner end to end
+against the oracle's eager executor without a GPU.
+"""
+
+import torch
+
+from ttlhip import _lib as L
+from ttlhip.plan import EltwiseLaunch, MatmulLaunch
+
+_TORCH_BIN = {
+    L.OP["add"]: torch.add, L.OP["sub"]: torch.sub, L.OP["mul"]: torch.mul,
+    L.OP["div"]: torch.true_divide, L.OP["max"]: torch.maximum, L.OP["min"]: torch.minimum,
+    L.OP["pow"]: torch.pow, L.OP["floordiv"]: torch.floor_divide, L.OP["mod"]: torch.remainder,
+}
+_TORCH_UN = {
+    L.OP["exp"]: torch.exp, L.OP["log"]: torch.log, L.OP["sqrt"]: torch.sqrt,
+    L.OP["rsqrt"]: torch.rsqrt, L.OP["tanh"]: torch.tanh, L.OP["abs"]: torch.abs,
+    L.OP["neg"]: torch.neg, L.OP["relu"]: torch.relu, L.OP["sigmoid"]: torch.sigmoid,
+    L.OP["recip"]: torch.reciprocal,
+}
+
+
+def _operand(t: torch.Tensor, spec, y0, x0, h, w) -> torch.Tensor:
+    ys = torch.arange(y0, y0 + h)
+    xs = torch.arange(x0, x0 + w)
+    iy = (ys & spec.row_mask) + spec.row_off if spec.row_mask != -1 else ys + spec.row_off
+    ix = (xs & spec.col_mask) + spec.col_off if spec.col_mask != -1 else xs + spec.col_off
+    if t.shape[0] == 1:
+        iy = torch.zeros_like(iy)
+    if t.shape[1] == 1:
+        ix = torch.zeros_like(ix)
+    return t[iy][:, ix].float()
+
+
+def _rnd(x, r):
+    return x.to(torch.bfloat16).float() if r == L.TTLH_BF16 else x
+
+
+def run_eltwise(l: EltwiseLaunch, args):
+    y0, x0, h, w = l.region
+    acc, stack = None, []
+    for s, spec in zip(l.prog.steps, l.operands):
+        v = None
+        if spec is not None:
+            v = _operand(spec.ref.resolve(args).cpu(), spec, y0, x0, h, w)
+        if s.form in (L.FORM_LOAD, L.FORM_PUSH):
+            if s.form == L.FORM_PUSH:
+                stack.append(acc)
+            acc = v
+        elif s.form in (L.FORM_CONST, L.FORM_PUSH_CONST):
+            if s.form == L.FORM_PUSH_CONST:
+                stack.append(acc)
+            acc = torch.full((h, w), s.imm)
+        elif s.form == L.FORM_UNARY:
+            acc = acc ** s.imm if s.op == L.OP["powi"] else _TORCH_UN[s.op](acc)
+        elif s.form == L.FORM_BIN:
+            acc = _TORCH_BIN[s.op](acc, v)
+        elif s.form == L.FORM_BIN_REV:
+            acc = _TORCH_BIN[s.op](v, acc)
+        elif s.form == L.FORM_BIN_IMM:
+            acc = _TORCH_BIN[s.op](acc, torch.tensor(s.imm))
+        elif s.form == L.FORM_BIN_IMM_REV:
+            acc = _TORCH_BIN[s.op](torch.tensor(s.imm), acc)
+        else:
+            acc = _TORCH_BIN[s.op](stack.pop(), acc)
+        acc = _rnd(acc, s.rnd)
+    out = l.out.resolve(args)
+    out[y0:y0 + h, x0:x0 + w] = acc.to(out.dtype).to(out.device)
+
+
+def run_matmul(l: MatmulLaunch, args):
+    a, b, c = l.a.resolve(args), l.b.resolve(args), l.c.resolve(args)
+    r0, r1 = l.rows
+    c0, c1 = l.cols
+    c[r0:r1, c0:c1] = (a[r0:r1].double() @ b[:, c0:c1].double()).to(c.dtype)
+
+
+def run(plan, args):
+    for l in plan.launches:
+        (run_eltwise if isinstance(l, EltwiseLaunch) else run_matmul)(l, args)

@@ -1,0 +1,144 @@
+"""Whole tt-lang kernels on the MI355X through the drop-in `ttl`, checked
+against the CPU oracle's eager tile-by-tile executor (same kernel source).
+
+Bars: elementwise/broadcast kernels bit-exact (exp: <= 1 bf16 ulp); matmul
+kernels within the tolerance the reference's own examples assert
+(assert_pcc rtol = atol = 1e-4 for fp32, singlecore_matmul.py:84-88) and, for
+bf16, within the stated bf16 bound and no worse than the simulator.
+Full-size configs are checked against the vectorised oracle (whole-tensor
+torch ops with the same per-op rounding) and float64 products.
+"""
+
+import math
+
+import pytest
+import torch
+
+import kernel_lib as KL
+import ttl
+import ttnn
+from oracle import sim_exec, tile_ops as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _oracle(factory, tensors, out_index, **kw):
+    ons = sim_exec.make_ttl()
+    k = factory(ons, ttnn, **kw) if "ttnn" in factory.__code__.co_varnames else factory(ons, **kw)
+    oargs = [sim_exec.OracleTensor(t.clone()) for t in tensors]
+    k(*oargs)
+    return oargs[out_index].t
+
+
+def _gpu(factory, tensors, out_index, **kw):
+    k = factory(ttl, ttnn, **kw) if "ttnn" in factory.__code__.co_varnames else factory(ttl, **kw)
+    args = [ttnn.from_torch(t) for t in tensors]
+    k(*args)
+    return ttnn.to_torch(args[out_index]), k
+
+
+def test_eltwise_add_kernel_bitexact():
+    a = O.seeded((256, 256), "uniform", 1, torch.float32, lo=0, hi=1)
+    b = O.seeded((256, 256), "uniform", 2, torch.float32, lo=0, hi=1)
+    out = torch.zeros(256, 256)
+    got, _ = _gpu(KL.make_eltwise_add, [a, b, out], 2)
+    assert torch.equal(got, _oracle(KL.make_eltwise_add, [a, b, out], 2))
+
+
+def test_eltwise_add_bf16_2048_config1():
+    # bf16 2048x2048, U[-1, 1]
+    a = O.seeded((2048, 2048), "uniform", 3, lo=-1, hi=1)
+    b = O.seeded((2048, 2048), "uniform", 4, lo=-1, hi=1)
+    got, k = _gpu(KL.make_eltwise_add, [a, b, torch.zeros(2048, 2048, dtype=torch.bfloat16)], 2)
+    assert len(k.last_plan.launches) == 1
+    assert torch.equal(got, a + b)  # the simulator's per-tile bf16 add, vectorised
+
+
+def test_bcast_fma_kernel_bitexact():
+    n = 512
+    a, b = O.seeded((n, n), "uniform", 5), O.seeded((n, n), "uniform", 6)
+    c = O.seeded((n, 1), "uniform", 7)
+    ts = [a, b, c, torch.zeros(n, n, dtype=torch.bfloat16)]
+    got, _ = _gpu(KL.make_bcast_fma, ts, 3, g=2, grid=(4, 4))
+    assert torch.equal(got, _oracle(KL.make_bcast_fma, ts, 3, g=2, grid=(4, 4)))
+
+
+def test_exp_row_pipe_kernel():
+    n = 256
+    a, c = O.seeded((n, n), "uniform", 8, lo=-2, hi=2), O.seeded((n, n), "uniform", 9, lo=-2, hi=2)
+    b = O.seeded((1, n), "uniform", 10, lo=-2, hi=2)
+    ts = [a, b, c, torch.zeros(n, n, dtype=torch.bfloat16)]
+    got, _ = _gpu(KL.make_exp_row_pipe, ts, 3, g=2, grid=(2, 2))
+    ref = _oracle(KL.make_exp_row_pipe, ts, 3, g=2, grid=(2, 2))
+    assert int(O.bf16_ulp_diff(got, ref).max()) <= 1
+
+
+def test_exp_row_pipe_4096_config2():
+    # BASELINE configs[1] at full size through the unmodified-style kernel
+    n = 4096
+    a, c = O.seeded((n, n), "uniform", 11, lo=-2, hi=2), O.seeded((n, n), "uniform", 12, lo=-2, hi=2)
+    b = O.seeded((1, n), "uniform", 13, lo=-2, hi=2)
+    got, k = _gpu(KL.make_exp_row_pipe, [a, b, c, torch.zeros(n, n, dtype=torch.bfloat16)], 3)
+    ref = torch.exp(a + b) * c
+    ulp = O.bf16_ulp_diff(got, ref)
+    assert int(ulp.max()) <= 1
+    assert float((ulp > 0).float().mean()) < 1e-3
+
+
+def test_tile_reuse_kernel_bitexact():
+    a = O.seeded((256, 256), "uniform", 14)
+    t = O.seeded((32, 32), "uniform", 15)
+    ts = [a, t, torch.zeros(256, 256, dtype=torch.bfloat16)]
+    got, _ = _gpu(KL.make_tile_reuse, ts, 2)
+    assert torch.equal(got, _oracle(KL.make_tile_reuse, ts, 2))
+
+
+def test_branchy_kernel_scalar_fallback():
+    a, b = O.seeded((64, 128), "uniform", 16), O.seeded((64, 128), "uniform", 17)
+    ts = [a, b, torch.zeros(64, 128, dtype=torch.bfloat16)]
+    got, _ = _gpu(KL.make_branchy_add, ts, 2)
+    assert torch.equal(got, _oracle(KL.make_branchy_add, ts, 2))
+
+
+@pytest.mark.parametrize("factory", [KL.make_matmul_single, KL.make_matmul_multi])
+def test_matmul_kernels_fp32_like_examples(factory):
+    # the reference examples' case: fp32 128x256 @ 256x64, assert_pcc rtol=atol=1e-4
+    a = O.seeded((128, 256), "uniform", 18, torch.float32, lo=0, hi=1)
+    b = O.seeded((256, 64), "uniform", 19, torch.float32, lo=0, hi=1)
+    ts = [a, b, torch.zeros(128, 64)]
+    got, _ = _gpu(factory, ts, 2)
+    ref = _oracle(factory, ts, 2)
+    torch.testing.assert_close(got, ref, rtol=1e-4, atol=1e-4)
+
+
+def test_matmul_kernel_bf16_vs_sim_error():
+    M = K = N = 256
+    a = O.seeded((M, K), "normal", 20, std=1 / math.sqrt(K))
+    b = O.seeded((K, N), "normal", 21, std=1 / math.sqrt(K))
+    ts = [a, b, torch.zeros(M, N, dtype=torch.bfloat16)]
+    got, _ = _gpu(KL.make_matmul_single, ts, 2)
+    sim = _oracle(KL.make_matmul_single, ts, 2)
+    exact = O.matmul_fp64(a, b)
+    e_gpu = float((got.double() - exact).abs().max())
+    e_sim = float((sim.double() - exact).abs().max())
+    assert e_gpu <= e_sim
+    assert e_gpu <= 1e-2 * float(exact.abs().max())
+
+
+def test_matmul_multi_4096_config3():
+    n = 4096
+    a = O.seeded((n, n), "normal", 22, std=1 / math.sqrt(n))
+    b = O.seeded((n, n), "normal", 23, std=1 / math.sqrt(n))
+    got, k = _gpu(KL.make_matmul_multi, [a, b, torch.zeros(n, n, dtype=torch.bfloat16)], 2)
+    rows = torch.arange(0, n, 64)
+    exact = a[rows].double() @ b.double()
+    err = (got[rows].double() - exact).abs()
+    assert float(err.max()) <= 1e-2 * float(exact.abs().max())
+    assert bool((err <= exact.abs() * 2 ** -8 + 1e-6 * 64 * float(exact.abs().max())).all())
+
+
+def test_ttnn_multiply_runs_on_device():
+    a = O.seeded((256, 256), "uniform", 24)
+    b = O.seeded((256, 256), "uniform", 25)
+    got = ttnn.to_torch(ttnn.multiply(ttnn.from_torch(a), ttnn.from_torch(b)))
+    assert torch.equal(got, a * b)

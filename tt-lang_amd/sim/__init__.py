@@ -1,0 +1,1 @@
+"""Drop-in for the `sim` helpers tt-lang examples import (sim.testing)."""

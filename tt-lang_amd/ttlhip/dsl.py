@@ -1,0 +1,535 @@
+"""tt-lang DSL objects for the MI355X backend: kernel, CBs, blocks, copy, math.
+
+Semantics follow the reference simulator, which is the only executable
+definition of the language here:
+  kernel / grid / core / grid_size        python/sim/kernel.py:89-291
+  circular buffers (reserve/push/wait/pop)  python/sim/cb.py:158-510
+  copy between tensors and blocks           python/sim/copy.py:160, copyhandlers.py:295-380
+  block expressions and store(acc)          python/sim/block.py:805-1013
+  ttl.math.broadcast                        python/sim/math.py:20-106
+plus the elementwise functions of the TTL op table
+(include/ttlang/Dialect/TTL/TTLElementwiseOps.def:61-82) as ttl.math.<op>.
+
+Nothing here computes on data: inside a kernel every call records what the
+thread does (see trace.py); the recorded program becomes GPU launches
+(plan.py).
+"""
+
+from __future__ import annotations
+
+import inspect
+import itertools
+import os
+import types
+from typing import Any, Callable, Dict, List, Optional, Sequence, Tuple, Union
+
+import numpy as np
+import torch
+
+from . import trace as T
+from .trace import Event, TensorSlice, TraceError, VInt
+
+TILE_SHAPE = (32, 32)
+MAX_CBS = 32  # python/sim/constants.py
+
+_cb_ids = itertools.count()
+
+
+# ---------------------------------------------------------------------------
+# kernel context: grid / core
+
+
+class _KernelState:
+    def __init__(self, grid: Tuple[int, ...]):
+        self.grid = grid
+        self.threads: List["ThreadTemplate"] = []
+        self.cbs: List["CircularBuffer"] = []
+
+
+_kstate: Optional[_KernelState] = None
+
+
+def _grid() -> Tuple[int, ...]:
+    ctx = T.current()
+    if ctx is not None:
+        return ctx.grid
+    if _kstate is not None:
+        return _kstate.grid
+    raise RuntimeError("grid not available - function must be called within a kernel context")
+
+
+def grid_size(dims: int = 2):
+    """Grid shape in `dims` dimensions: trailing dimensions flattened when fewer
+    are asked for, padded with 1s when more are (python/sim/kernel.py:89-152)."""
+    if dims <= 0:
+        raise ValueError(f"dims must be positive, got {dims}")
+    g = tuple(_grid())
+    if dims == len(g):
+        res = g
+    elif dims < len(g):
+        tail = int(np.prod(g[dims - 1:]))
+        res = tuple(g[:dims - 1]) + (tail,)
+    else:
+        res = g + (1,) * (dims - len(g))
+    return res[0] if dims == 1 else res
+
+
+def core(dims: int = 2):
+    """Coordinates of the current core: row-major decomposition of the linear
+    core id over the grid; leading dimensions flattened when fewer are asked
+    for, zeros appended when more are (python/sim/kernel.py:155-199)."""
+    ctx = T.current()
+    if ctx is None:
+        raise RuntimeError("core not available - function must be called within Program context")
+    g = tuple(ctx.grid)
+    cid = ctx.core
+    coords = []
+    for s in reversed(g):
+        coords.append(cid % s)
+        cid //= s
+    coords.reverse()
+    if dims < len(coords):
+        flat = coords[0]
+        for i in range(1, len(coords) - dims + 1):
+            flat = flat * g[i] + coords[i]
+        coords = [flat] + coords[len(coords) - dims + 1:]
+    while len(coords) < dims:
+        coords.append(0)
+    return coords[0] if dims == 1 else tuple(coords)
+
+
+def flatten_core_index(core_coord) -> int:
+    if isinstance(core_coord, (int, np.integer)):
+        return int(core_coord)
+    g = _grid()
+    c = list(core_coord)
+    lin = c[0]
+    for i in range(1, len(c)):
+        lin = lin * g[i] + c[i]
+    return int(lin)
+
+
+# ---------------------------------------------------------------------------
+# threads
+
+
+class ThreadTemplate:
+    def __init__(self, func: types.FunctionType, kind: str):
+        self.func = func
+        self.kind = kind  # "compute" | "dm"
+        self.__name__ = func.__name__
+        self.__wrapped__ = func
+        self._rewritten: Optional[types.FunctionType] = None
+
+    def rewritten(self) -> types.FunctionType:
+        if self._rewritten is None:
+            self._rewritten = T.rewrite_thread(self.func)
+        return self._rewritten
+
+    def __call__(self, *a, **k):
+        raise RuntimeError(f"thread {self.__name__} runs only as part of a ttl.kernel")
+
+
+def _register(t: ThreadTemplate) -> ThreadTemplate:
+    if _kstate is None:
+        raise RuntimeError("ttl.compute / ttl.datamovement must be used inside a ttl.kernel body")
+    _kstate.threads.append(t)
+    return t
+
+
+def compute():
+    def deco(func):
+        return _register(ThreadTemplate(func, "compute"))
+    return deco
+
+
+def datamovement():
+    def deco(func):
+        return _register(ThreadTemplate(func, "dm"))
+    return deco
+
+
+# ---------------------------------------------------------------------------
+# circular buffers and blocks
+
+
+class CircularBuffer:
+    """A CB of `shape` tiles per block and `shape[0]*shape[1]*buffer_factor`
+    tiles of capacity (python/sim/cb.py:158-300).  On the MI355X the ring
+    is not materialised: blocks become tile coordinates of the grid-wide
+    kernels (streaming through VGPRs / LDS)."""
+
+    def __init__(self, element, shape: Tuple[int, int], buffer_factor: int = 2):
+        if len(shape) != 2 or any(int(s) <= 0 for s in shape):
+            raise ValueError(f"CB shape must be two positive tile counts, got {shape}")
+        if buffer_factor < 1:
+            raise ValueError(f"buffer_factor must be >= 1, got {buffer_factor}")
+        self.id = next(_cb_ids)
+        self.shape = (int(shape[0]), int(shape[1]))
+        self.buffer_factor = int(buffer_factor)
+        self.dtype = element.dtype
+        self.capacity_tiles = self.shape[0] * self.shape[1] * self.buffer_factor
+        if _kstate is not None:
+            _kstate.cbs.append(self)
+            if len(_kstate.cbs) > MAX_CBS:
+                raise ValueError(f"a kernel may create at most {MAX_CBS} circular buffers")
+
+    def __repr__(self):
+        return f"CircularBuffer(id={self.id}, shape={self.shape}, bf={self.buffer_factor})"
+
+    def _ctx(self) -> T.TraceContext:
+        ctx = T.current()
+        if ctx is None:
+            raise RuntimeError("CB operations are only valid inside a ttl.kernel thread")
+        return ctx
+
+    def reserve(self) -> "Block":
+        ctx = self._ctx()
+        if self.id in ctx.pending_reserve:
+            raise RuntimeError("Cannot call reserve() again before push(): CircularBuffer already "
+                               "has a pending reserved block. You must call push() before calling "
+                               "reserve() again.")
+        ev = ctx.add(Event("reserve", self, ctx.cur, {"thread": ctx.thread}))
+        blk = Block(self, "reserve", ev)
+        ctx.pending_reserve[self.id] = blk
+        return blk
+
+    def wait(self) -> "Block":
+        ctx = self._ctx()
+        if self.id in ctx.pending_wait:
+            raise RuntimeError("Cannot call wait() again before pop(): CircularBuffer already "
+                               "has a pending waited block. You must call pop() before calling "
+                               "wait() again.")
+        ev = ctx.add(Event("wait", self, ctx.cur, {"thread": ctx.thread}))
+        blk = Block(self, "wait", ev)
+        ctx.pending_wait[self.id] = blk
+        return blk
+
+    def push(self) -> None:
+        ctx = self._ctx()
+        if ctx.pending_reserve.pop(self.id, None) is None:
+            raise RuntimeError("push() without a matching reserve()")
+        ctx.add(Event("push", self, ctx.cur))
+
+    def pop(self) -> None:
+        ctx = self._ctx()
+        if ctx.pending_wait.pop(self.id, None) is None:
+            raise RuntimeError("pop() without a matching wait()")
+        ctx.add(Event("pop", self, ctx.cur))
+
+    def can_wait(self) -> bool:
+        return True
+
+    def can_reserve(self) -> bool:
+        return True
+
+
+def make_circular_buffer_like(element, shape: Tuple[int, int],
+                              buffer_factor: int = 2) -> CircularBuffer:
+    return CircularBuffer(element, shape, buffer_factor)
+
+
+# block expressions ---------------------------------------------------------
+
+
+class BExpr:
+    """A block-shaped expression.  `tree` is one per-tile expression shared by
+    every tile of the block; its leaves are ("leaf", block, rmap, cmap) where
+    rmap[i] / cmap[j] give the leaf block's tile feeding output tile (i, j)
+    (that is how block broadcasting, python/sim/block.py:886-920, is kept)."""
+
+    __slots__ = ("shape", "tree", "dtype")
+
+    def __init__(self, shape: Tuple[int, int], tree, dtype: torch.dtype):
+        self.shape = shape
+        self.tree = tree
+        self.dtype = dtype
+
+    # operators (python/sim/block.py:963-1013)
+    def __add__(self, o): return _binary("add", self, o)
+    def __radd__(self, o): return _binary("add", o, self)
+    def __sub__(self, o): return _binary("sub", self, o)
+    def __rsub__(self, o): return _binary("sub", o, self)
+    def __mul__(self, o): return _binary("mul", self, o)
+    def __rmul__(self, o): return _binary("mul", o, self)
+    def __truediv__(self, o): return _binary("div", self, o)
+    def __rtruediv__(self, o): return _binary("div", o, self)
+    def __floordiv__(self, o): return _binary("floordiv", self, o)
+    def __mod__(self, o): return _binary("mod", self, o)
+    def __matmul__(self, o): return _binary("matmul", self, o)
+    def __neg__(self): return _unary("neg", self)
+
+    def __pow__(self, o):
+        if isinstance(o, int):
+            return BExpr(self.shape, ("powi", self.tree, o), self.dtype)
+        return _binary("pow", self, o)
+
+    def __len__(self):
+        return self.shape[0] * self.shape[1]
+
+
+def _as_bexpr(x) -> BExpr:
+    if isinstance(x, BExpr):
+        return x
+    if isinstance(x, Block):
+        return x.expr()
+    raise TypeError(f"expected a block or block expression, got {type(x).__name__}")
+
+
+def _remap(tree, axis: int, new_len: int):
+    """Broadcast a size-1 axis of every leaf map in `tree` to `new_len`."""
+    tag = tree[0]
+    if tag == "leaf":
+        _, blk, rmap, cmap = tree
+        if axis == 0:
+            rmap = np.repeat(rmap[:1], new_len)
+        else:
+            cmap = np.repeat(cmap[:1], new_len)
+        return ("leaf", blk, rmap, cmap)
+    if tag == "const":
+        return tree
+    if tag == "powi":
+        return ("powi", _remap(tree[1], axis, new_len), tree[2])
+    return (tag,) + tuple(_remap(t, axis, new_len) for t in tree[1:])
+
+
+def _binary(op: str, a, b) -> BExpr:
+    if isinstance(a, (int, float)) and not isinstance(a, bool):
+        bb = _as_bexpr(b)
+        return BExpr(bb.shape, (op, ("const", float(a)), bb.tree), bb.dtype)
+    if isinstance(b, (int, float)) and not isinstance(b, bool):
+        aa = _as_bexpr(a)
+        return BExpr(aa.shape, (op, aa.tree, ("const", float(b))), aa.dtype)
+    aa, bb = _as_bexpr(a), _as_bexpr(b)
+    sa, sb = aa.shape, bb.shape
+    if len(sa) != len(sb):
+        raise ValueError(f"Cannot broadcast: dimension mismatch between shapes {sa} and {sb}. "
+                         "Shapes must have the same number of dimensions.")
+    out = []
+    ta, tb = aa.tree, bb.tree
+    for i, (la, lb) in enumerate(zip(sa, sb)):
+        if la != lb and la != 1 and lb != 1:
+            raise ValueError(f"Cannot broadcast: incompatible shapes {sa} and {sb}. Dimension {i} "
+                             f"has sizes {la} and {lb} which are incompatible (must be equal or one "
+                             "must be 1).")
+        n = max(la, lb)
+        if la != n:
+            ta = _remap(ta, i, n)
+        if lb != n:
+            tb = _remap(tb, i, n)
+        out.append(n)
+    return BExpr(tuple(out), (op, ta, tb), torch.promote_types(aa.dtype, bb.dtype))
+
+
+def _unary(op: str, a, imm: Optional[float] = None) -> BExpr:
+    aa = _as_bexpr(a)
+    return BExpr(aa.shape, (op, aa.tree), aa.dtype)
+
+
+class Block:
+    """A block of a CB obtained from wait() (readable) or reserve() (writable).
+    Used as a context manager it pops / pushes on exit (python/sim/cb.py:40-157)."""
+
+    def __init__(self, cb: CircularBuffer, kind: str, event: Event):
+        self.cb = cb
+        self.kind = kind
+        self.event = event
+        self.shape = cb.shape
+        self._stores = 0
+
+    def __enter__(self) -> "Block":
+        return self
+
+    def __exit__(self, exc_type, exc, tb) -> None:
+        if exc_type is not None:
+            return
+        if self.kind == "reserve":
+            self.cb.push()
+        else:
+            self.cb.pop()
+
+    def block(self) -> "Block":
+        return self
+
+    def __len__(self) -> int:
+        return self.shape[0] * self.shape[1]
+
+    def __getitem__(self, idx):
+        raise RuntimeError("Block indexing (block[index]) is not allowed. Blocks must be used as "
+                           "whole units in operations like store() or arithmetic. Use block "
+                           "directly without indexing.")
+
+    def __setitem__(self, idx, value):
+        raise RuntimeError("Direct assignment to Block is not allowed. Use block.store() or "
+                           "copy() instead.")
+
+    def expr(self) -> BExpr:
+        if self.kind != "wait":
+            raise NotImplementedError("reading a reserved (output) block back is not supported by "
+                                      "the MI355X backend; read blocks obtained from wait()")
+        r, c = self.shape
+        return BExpr(self.shape, ("leaf", self, np.arange(r), np.arange(c)), self.cb.dtype)
+
+    # arithmetic delegates to BExpr
+    def __add__(self, o): return _binary("add", self, o)
+    def __radd__(self, o): return _binary("add", o, self)
+    def __sub__(self, o): return _binary("sub", self, o)
+    def __rsub__(self, o): return _binary("sub", o, self)
+    def __mul__(self, o): return _binary("mul", self, o)
+    def __rmul__(self, o): return _binary("mul", o, self)
+    def __truediv__(self, o): return _binary("div", self, o)
+    def __rtruediv__(self, o): return _binary("div", o, self)
+    def __floordiv__(self, o): return _binary("floordiv", self, o)
+    def __mod__(self, o): return _binary("mod", self, o)
+    def __matmul__(self, o): return _binary("matmul", self, o)
+    def __neg__(self): return _unary("neg", self)
+
+    def __pow__(self, o):
+        return self.expr() ** o
+
+    def store(self, items, acc: bool = False) -> None:
+        """Store a block expression into this reserved block.  acc=True: the first
+        store assigns, later ones add (python/sim/block.py:805-868)."""
+        if self.kind != "reserve":
+            raise RuntimeError("store() needs a block obtained from reserve()")
+        ctx = T.current()
+        if ctx is None:
+            raise RuntimeError("store() is only valid inside a ttl.kernel thread")
+        e = _as_bexpr(items)
+        if len(e) != len(self):
+            raise ValueError("Length mismatch in store()")
+        ctx.add(Event("store", self.cb, ctx.cur,
+                      {"target": self, "expr": e, "acc": bool(acc), "thread": ctx.thread}))
+        self._stores += 1
+
+
+# ---------------------------------------------------------------------------
+# copy
+
+
+class CopyTransaction:
+    def wait(self) -> None:
+        return None
+
+    def is_done(self) -> bool:
+        return True
+
+
+def copy(src, dst) -> CopyTransaction:
+    """Tensor slice -> reserved block, or waited block -> tensor slice.  Tiles
+    go into block slots row-major over the block's tile grid
+    (python/sim/copyhandlers.py:295-380)."""
+    ctx = T.current()
+    if ctx is None:
+        raise RuntimeError("ttl.copy is only valid inside a ttl.kernel thread")
+    if isinstance(src, TensorSlice) and isinstance(dst, Block):
+        if dst.kind != "reserve":
+            raise TraceError("copy into a block needs a block obtained from reserve()")
+        _check_slice_shape(src, dst)
+        for x, nm in ((src.r0, "row index"), (src.c0, "col index")):
+            ctx.check_loops(x, nm)
+        ctx.add(Event("copy_in", dst.cb, ctx.cur, {"block": dst, "slice": src}))
+        return CopyTransaction()
+    if isinstance(src, Block) and isinstance(dst, TensorSlice):
+        if src.kind != "wait":
+            raise TraceError("copy out of a block needs a block obtained from wait()")
+        _check_slice_shape(dst, src)
+        for x, nm in ((dst.r0, "row index"), (dst.c0, "col index")):
+            ctx.check_loops(x, nm)
+        ctx.add(Event("copy_out", src.cb, ctx.cur, {"block": src, "slice": dst}))
+        return CopyTransaction()
+    raise NotImplementedError(
+        f"ttl.copy({type(src).__name__} -> {type(dst).__name__}) is not supported by the MI355X "
+        "backend (tensor<->block copies only; pipes are not implemented)")
+
+
+def _check_slice_shape(s: TensorSlice, blk: Block) -> None:
+    if len(s.tensor.shape) != 2:
+        raise ValueError(f"Tensor must be 2-dimensional, got shape {s.tensor.shape}")
+    tiles = s.shape_in_tiles()
+    if tiles != tuple(blk.shape):
+        raise ValueError(f"Tensor shape {tuple(s.tensor.shape)} slice (={tiles} tiles) does not "
+                         f"match Block shape {tuple(blk.shape)} tiles")
+    s.check_bounds()
+
+
+# ---------------------------------------------------------------------------
+# ttl.math
+
+
+class _Math:
+    """ttl.math: broadcast plus the elementwise tile ops."""
+
+    @staticmethod
+    def broadcast(block, _unused=None, dims: Optional[Sequence[int]] = None) -> BExpr:
+        """Validates that `block` has size 1 along `dims`; the broadcast itself
+        happens in the enclosing binary op (python/sim/math.py:20-106)."""
+        if dims is None:
+            raise ValueError("dims parameter is required for broadcast()")
+        e = _as_bexpr(block)
+        for d in dims:
+            if d >= len(e.shape):
+                raise ValueError(f"Cannot broadcast along dimension {d}: block has shape {e.shape} "
+                                 f"with only {len(e.shape)} dimensions")
+            if e.shape[d] != 1:
+                raise ValueError(f"Cannot broadcast along dimension {d}: dimension must have size "
+                                 f"1, but has size {e.shape[d]}")
+        return e
+
+    @staticmethod
+    def exp(x): return _unary("exp", x)
+    @staticmethod
+    def log(x): return _unary("log", x)
+    @staticmethod
+    def sqrt(x): return _unary("sqrt", x)
+    @staticmethod
+    def rsqrt(x): return _unary("rsqrt", x)
+    @staticmethod
+    def tanh(x): return _unary("tanh", x)
+    @staticmethod
+    def abs(x): return _unary("abs", x)
+    @staticmethod
+    def neg(x): return _unary("neg", x)
+    @staticmethod
+    def relu(x): return _unary("relu", x)
+    @staticmethod
+    def sigmoid(x): return _unary("sigmoid", x)
+    @staticmethod
+    def recip(x): return _unary("recip", x)
+    @staticmethod
+    def max(a, b): return _binary("max", a, b)
+    @staticmethod
+    def min(a, b): return _binary("min", a, b)
+    maximum = max
+    minimum = min
+
+
+math = _Math()
+
+
+def signpost(*_a, **_k) -> None:
+    """Profiling marker (python/ttl/ttl.py:23-26); timing on the MI355X comes
+    from rocprofv3 kernel traces."""
+    return None
+
+
+# ---------------------------------------------------------------------------
+# kernel
+
+
+def kernel(grid: Union[str, Tuple[int, ...]] = "auto", **options) -> Callable:
+    """@ttl.kernel(grid=...): runs the kernel body to collect its CBs and its
+    three threads, traces every core, and executes the resulting tile program
+    on the GPU.  grid="auto" is the simulator's (8, 8) (python/sim/kernel.py:226).
+    The output tensors are written in place; the call returns None after the
+    device work has finished (the reference's synchronous semantics)."""
+    actual_grid = (8, 8) if grid == "auto" else tuple(int(g) for g in grid)
+    if any(g <= 0 for g in actual_grid):
+        raise ValueError(f"grid dimensions must be positive, got {grid}")
+
+    def decorator(func):
+        from . import runner
+
+        return runner.KernelRunner(func, actual_grid, grid, options)
+
+    return decorator

@@ -1,0 +1,435 @@
+"""From traced thread events to MI355X kernel launches.
+
+A circular buffer is a FIFO between exactly one producer and one consumer
+thread (python/sim/cb.py:302-408, one pending block per side), so the n-th
+block a producer reserves is the n-th block its consumer waits on.  With the
+block indices the tracer assigns, every stored tile resolves to
+
+    output tensor tile  <-  store(expr, acc)  <-  leaf blocks  <-  input tensor tiles
+
+as numpy arrays over all cores and loop iterations at once.  Each store site
+becomes one launch:
+  * every output tile written once by an elementwise expression -> one
+    ttlh_eltwise over the covered rectangle, operands addressed as identity
+    (+offset), fixed-tile reuse or size-1 broadcast (what the simulator's
+    block broadcasting and degenerate tiles produce);
+  * A(m,k) @ B(k,n) accumulated with store(acc=True) over all k into every
+    output tile of a rectangle -> one ttlh_matmul.
+Anything else raises NotImplementedError naming the unsupported pattern.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Any, Dict, List, Optional, Tuple
+
+import numpy as np
+import torch
+
+from . import expr as X
+from . import trace as T
+
+TILE = 32
+
+
+class PlanError(NotImplementedError):
+    """The traced tile program uses a pattern the MI355X backend does not run."""
+
+
+# ---------------------------------------------------------------------------
+# launches
+
+
+@dataclass
+class TensorRef:
+    """A tensor the plan reads or writes: kernel argument `arg` (by position or
+    name) or, for tensors captured from an enclosing scope, the object."""
+
+    arg: Any = None
+    obj: Any = None
+
+    def resolve(self, args: Dict[Any, Any]):
+        t = args[self.arg] if self.arg is not None else self.obj
+        return t._tensor if hasattr(t, "_tensor") else t
+
+
+@dataclass
+class OperandSpec:
+    ref: TensorRef
+    row_mask: int
+    col_mask: int
+    row_off: int
+    col_off: int
+
+
+@dataclass
+class EltwiseLaunch:
+    prog: X.StackProgram
+    operands: List[Optional[OperandSpec]]  # per step
+    out: TensorRef
+    region: Tuple[int, int, int, int]      # y0, x0, h, w (elements)
+    tiles: int = 0
+
+    def describe(self) -> str:
+        return (f"eltwise {len(self.prog.steps)} steps over {self.region[2]}x{self.region[3]} "
+                f"elements at ({self.region[0]}, {self.region[1]})")
+
+
+@dataclass
+class MatmulLaunch:
+    a: TensorRef
+    b: TensorRef
+    c: TensorRef
+    rows: Tuple[int, int]   # output element rows [r0, r1)
+    cols: Tuple[int, int]   # output element cols [c0, c1)
+    k: int
+
+    def describe(self) -> str:
+        return (f"matmul C[{self.rows[0]}:{self.rows[1]}, {self.cols[0]}:{self.cols[1]}] = "
+                f"A . B over K={self.k}")
+
+
+@dataclass
+class Plan:
+    launches: List[Any] = field(default_factory=list)
+
+    def describe(self) -> str:
+        return "\n".join(l.describe() for l in self.launches)
+
+
+# ---------------------------------------------------------------------------
+# resolution
+
+
+@dataclass
+class _CopyTable:
+    """Per (core, CB): tensor tile origin of every block index."""
+
+    tensor: Any
+    r0: np.ndarray
+    c0: np.ndarray
+
+
+def _thread_events(root) -> List[T.Event]:
+    return list(T.iter_events(root))
+
+
+def _copy_table(events: List[T.Event], cb, n: int, kind: str) -> _CopyTable:
+    r0 = np.full(n, -1, dtype=np.int64)
+    c0 = np.full(n, -1, dtype=np.int64)
+    tensor = None
+    for ev in events:
+        if ev.kind != kind or ev.cb is not cb:
+            continue
+        blk, sl = ev.data["block"], ev.data["slice"]
+        if tensor is None:
+            tensor = sl.tensor
+        elif sl.tensor is not tensor:
+            raise PlanError("one circular buffer is filled from / drained to more than one "
+                            "tensor on a core; use one CB per tensor")
+        shape = ev.domain_shape()
+        idx = T.broadcast_to_domain(blk.event.index, shape).ravel()
+        if np.any(r0[idx] >= 0):
+            raise PlanError("a block is copied more than once")
+        r0[idx] = T.broadcast_to_domain(sl.r0, shape).ravel()
+        c0[idx] = T.broadcast_to_domain(sl.c0, shape).ravel()
+    if n and (tensor is None or np.any(r0 < 0)):
+        what = "filled by ttl.copy" if kind == "copy_in" else "copied out"
+        raise PlanError(f"every block of CB {cb.id} must be {what} exactly once "
+                        "(blocks pushed without a copy are not supported)")
+    return _CopyTable(tensor, r0, c0)
+
+
+@dataclass
+class _Group:
+    """All instances of one store site (same expression, tensors, acc)."""
+
+    tree: Any
+    leaf_blocks: List[Any]        # first-core leaf descriptors (for dtypes)
+    leaf_tensors: List[Any]
+    out_tensor: Any
+    acc: bool
+    dtype: torch.dtype
+    out_rc: List[np.ndarray] = field(default_factory=list)     # [(N,2)]
+    leaf_rc: List[List[np.ndarray]] = field(default_factory=list)
+    order: List[np.ndarray] = field(default_factory=list)
+
+
+def _tree_leaves(tree, out: List):
+    tag = tree[0]
+    if tag == "leaf":
+        out.append(tree)
+    elif tag == "const":
+        pass
+    elif tag == "powi":
+        _tree_leaves(tree[1], out)
+    else:
+        for t in tree[1:]:
+            _tree_leaves(t, out)
+    return out
+
+
+def _tree_key(tree, leaf_ids: Dict[int, int]):
+    tag = tree[0]
+    if tag == "leaf":
+        return ("leaf", leaf_ids.setdefault(id(tree), len(leaf_ids)), str(tree[1].cb.dtype))
+    if tag == "const":
+        return ("const", tree[1])
+    if tag == "powi":
+        return ("powi", _tree_key(tree[1], leaf_ids), tree[2])
+    return (tag,) + tuple(_tree_key(t, leaf_ids) for t in tree[1:])
+
+
+def resolve(core_traces: List[Dict[str, Any]]) -> List[_Group]:
+    """core_traces[c] = {"threads": [(template, root_node), ...]} for core c."""
+    groups: Dict[Tuple, _Group] = {}
+    for ct in core_traces:
+        threads = ct["threads"]
+        events = {id(tmpl): _thread_events(root) for tmpl, root in threads}
+        totals = {id(tmpl): T.assign_indices(root) for tmpl, root in threads}
+        # producer / consumer of every CB on this core
+        producers: Dict[int, Any] = {}
+        consumers: Dict[int, Any] = {}
+        cbs: Dict[int, Any] = {}
+        for tmpl, root in threads:
+            for ev in events[id(tmpl)]:
+                if ev.kind == "reserve":
+                    if producers.setdefault(ev.cb.id, tmpl) is not tmpl:
+                        raise PlanError(f"CB {ev.cb.id} is reserved by two threads")
+                    cbs[ev.cb.id] = ev.cb
+                elif ev.kind == "wait":
+                    if consumers.setdefault(ev.cb.id, tmpl) is not tmpl:
+                        raise PlanError(f"CB {ev.cb.id} is waited on by two threads")
+                    cbs[ev.cb.id] = ev.cb
+        count = {}
+        for cid, cb in cbs.items():
+            np_ = totals[id(producers[cid])].get((cid, "reserve"), 0) if cid in producers else 0
+            nc_ = totals[id(consumers[cid])].get((cid, "wait"), 0) if cid in consumers else 0
+            if np_ != nc_:
+                raise RuntimeError(f"Deadlock: CB {cid} has {np_} blocks pushed but {nc_} blocks "
+                                   f"waited on core {ct['core']} (producer and consumer disagree)")
+            count[cid] = np_
+        # copy tables
+        fill: Dict[int, _CopyTable] = {}
+        drain: Dict[int, _CopyTable] = {}
+        for cid, cb in cbs.items():
+            if cid in producers and producers[cid].kind == "dm":
+                fill[cid] = _copy_table(events[id(producers[cid])], cb, count[cid], "copy_in")
+            if cid in consumers and consumers[cid].kind == "dm":
+                drain[cid] = _copy_table(events[id(consumers[cid])], cb, count[cid], "copy_out")
+        # stores
+        for tmpl, root in threads:
+            for ev in events[id(tmpl)]:
+                if ev.kind != "store":
+                    continue
+                target = ev.data["target"]
+                e = ev.data["expr"]
+                cid = target.cb.id
+                if cid not in drain:
+                    raise PlanError("stored blocks must be copied to a tensor by a data-movement "
+                                    "thread (CB-to-CB chains are not supported)")
+                shape = ev.domain_shape()
+                rout = T.broadcast_to_domain(target.event.index, shape).ravel()
+                dt = drain[cid]
+                R, C = target.shape
+                er, ec = e.shape
+                nslot = R * C
+                # output tile of every (instance, slot)
+                slot = np.arange(nslot)
+                oi, oj = slot // C, slot % C
+                out_r = (dt.r0[rout][:, None] + oi[None, :]).ravel()
+                out_c = (dt.c0[rout][:, None] + oj[None, :]).ravel()
+                leaves = _tree_leaves(e.tree, [])
+                leaf_rc = []
+                leaf_tensors = []
+                ei, ej = slot // ec, slot % ec  # expression slot of each target slot
+                for lf in leaves:
+                    _, blk, rmap, cmap = lf
+                    lcid = blk.cb.id
+                    if lcid not in fill:
+                        raise PlanError("expression operands must come from blocks filled by "
+                                        "ttl.copy from a tensor")
+                    ft = fill[lcid]
+                    w = T.broadcast_to_domain(blk.event.index, shape).ravel()
+                    lr = (ft.r0[w][:, None] + np.asarray(rmap)[ei][None, :]).ravel()
+                    lc = (ft.c0[w][:, None] + np.asarray(cmap)[ej][None, :]).ravel()
+                    leaf_rc.append(np.stack([lr, lc], 1))
+                    leaf_tensors.append(ft.tensor)
+                order = np.repeat(np.arange(rout.size), nslot)
+                key = (_tree_key(e.tree, {}), tuple(id(t) for t in leaf_tensors), id(dt.tensor),
+                       ev.data["acc"])
+                g = groups.get(key)
+                if g is None:
+                    g = _Group(e.tree, leaves, leaf_tensors, dt.tensor, ev.data["acc"], e.dtype)
+                    groups[key] = g
+                g.out_rc.append(np.stack([out_r, out_c], 1))
+                g.leaf_rc.append(leaf_rc)
+                g.order.append(order)
+    return list(groups.values())
+
+
+# ---------------------------------------------------------------------------
+# classification
+
+
+def _rect(rc: np.ndarray) -> Tuple[int, int, int, int]:
+    r0, c0 = rc.min(0)
+    r1, c1 = rc.max(0) + 1
+    return int(r0), int(r1), int(c0), int(c1)
+
+
+def _unique_tiles(rc: np.ndarray) -> int:
+    key = rc[:, 0] * (int(rc[:, 1].max()) + 1) + rc[:, 1]
+    return int(np.unique(key).size)
+
+
+def _axis_map(out_t: np.ndarray, in_t: np.ndarray, dim: int) -> Tuple[int, int]:
+    """(mask, element offset) reproducing in_tile = f(out_tile) on one axis."""
+    if dim == 1:  # degenerate tensor dimension: stride 0, only tile 0 exists
+        return 31, 0
+    d = in_t - out_t
+    if np.all(d == d[0]):
+        return -1, int(d[0]) * TILE
+    if np.all(in_t == in_t[0]):
+        return 31, int(in_t[0]) * TILE
+    raise PlanError("an operand's tiles are not an affine image of the output tiles "
+                    "(only identity, offset, fixed-tile reuse and size-1 broadcast map onto the "
+                    "grid-wide kernel)")
+
+
+_BIN = {"add", "sub", "mul", "div", "max", "min", "pow", "floordiv", "mod"}
+_UN = {"exp", "log", "sqrt", "rsqrt", "tanh", "abs", "neg", "relu", "sigmoid", "recip"}
+
+
+def _to_expr(tree, leaf_nodes: Dict[int, X.Leaf]) -> X.Expr:
+    tag = tree[0]
+    if tag == "leaf":
+        return leaf_nodes[id(tree)]
+    if tag == "const":
+        return X.Const(tree[1])
+    if tag == "powi":
+        x = _to_expr(tree[1], leaf_nodes)
+        return X.Unary("powi", x, x.dtype, imm=float(tree[2]))
+    if tag in _UN:
+        x = _to_expr(tree[1], leaf_nodes)
+        return X.Unary(tag, x, x.dtype)
+    if tag in _BIN:
+        a, b = _to_expr(tree[1], leaf_nodes), _to_expr(tree[2], leaf_nodes)
+        if isinstance(a, X.Const):
+            dt = b.dtype
+        elif isinstance(b, X.Const):
+            dt = a.dtype
+        else:
+            dt = X.promote(a.dtype, b.dtype)
+        return X.Binary(tag, a, b, dt)
+    if tag == "matmul":
+        raise PlanError("a tile matmul combined with other ops in one store() is not supported; "
+                        "store the product on its own (acc=True accumulates over K)")
+    raise PlanError(f"unsupported tile op {tag!r}")
+
+
+def _has(tree, tag) -> bool:
+    if tree[0] == tag:
+        return True
+    if tree[0] in ("leaf", "const"):
+        return False
+    return any(_has(t, tag) for t in tree[1:] if isinstance(t, tuple))
+
+
+def build_plan(groups: List[_Group], tensor_ref) -> Plan:
+    plan = Plan()
+    for g in groups:
+        out_rc = np.concatenate(g.out_rc, 0)
+        leaf_rc = [np.concatenate([li[k] for li in g.leaf_rc], 0) for k in range(len(g.leaf_blocks))]
+        if g.tree[0] == "matmul" and g.tree[1][0] == "leaf" and g.tree[2][0] == "leaf":
+            plan.launches.append(_plan_matmul(g, out_rc, leaf_rc, tensor_ref))
+        elif _has(g.tree, "matmul"):
+            raise PlanError("a tile matmul combined with other ops in one store() is not "
+                            "supported; store the product on its own")
+        else:
+            plan.launches.append(_plan_eltwise(g, out_rc, leaf_rc, tensor_ref))
+    return plan
+
+
+def _plan_eltwise(g: _Group, out_rc, leaf_rc, tensor_ref) -> EltwiseLaunch:
+    n = out_rc.shape[0]
+    if _unique_tiles(out_rc) != n:
+        if g.acc:
+            raise PlanError("store(acc=True) of an elementwise expression into the same output "
+                            "tile more than once is not supported (only tile matmul accumulates)")
+        raise PlanError("an output tile is written more than once")
+    r0, r1, c0, c1 = _rect(out_rc)
+    if (r1 - r0) * (c1 - c0) != n:
+        raise PlanError("the stored output tiles do not form a rectangle of the output tensor")
+    out_t = g.out_tensor
+    H, W = out_t.shape
+    leaf_nodes: Dict[int, X.Leaf] = {}
+    specs: Dict[int, OperandSpec] = {}
+    for k, lf in enumerate(g.leaf_blocks):
+        tens = g.leaf_tensors[k]
+        h, w = tens.shape
+        rm, ro = _axis_map(out_rc[:, 0], leaf_rc[k][:, 0], h)
+        cm, co = _axis_map(out_rc[:, 1], leaf_rc[k][:, 1], w)
+        leaf = X.Leaf(k, lf[1].cb.dtype)
+        leaf_nodes[id(lf)] = leaf
+        specs[k] = OperandSpec(tensor_ref(tens), rm, cm, ro, co)
+    e = _to_expr(g.tree, leaf_nodes)
+    prog = X.compile_expr(e)
+    operands = [specs[s.leaf.ref] if s.leaf is not None else None for s in prog.steps]
+    y0, x0 = r0 * TILE, c0 * TILE
+    h = min(r1 * TILE, H) - y0
+    w = min(c1 * TILE, W) - x0
+    return EltwiseLaunch(prog, operands, tensor_ref(out_t), (y0, x0, h, w), n)
+
+
+def _plan_matmul(g: _Group, out_rc, leaf_rc, tensor_ref) -> MatmulLaunch:
+    a_t, b_t = g.leaf_tensors
+    (ar, ac), (br, bc) = leaf_rc[0].T, leaf_rc[1].T
+    orow, ocol = out_rc[:, 0], out_rc[:, 1]
+    if not (np.array_equal(ar, orow) and np.array_equal(bc, ocol) and np.array_equal(ac, br)):
+        raise PlanError("tile matmul operands are not A(m, k) @ B(k, n) for output tile (m, n)")
+    if len(a_t.shape) != 2 or len(b_t.shape) != 2 or a_t.shape[1] != b_t.shape[0]:
+        raise PlanError("tile matmul operand shapes do not chain")
+    K = a_t.shape[1]
+    kt = K // TILE
+    n_out = _unique_tiles(out_rc)
+    triples = np.stack([orow, ocol, ac], 1)
+    key = (orow * (int(ocol.max()) + 1) + ocol) * (kt + 1) + ac
+    if np.unique(key).size != key.size:
+        raise PlanError("a (output tile, k) product is accumulated twice")
+    if key.size != n_out * kt or (not g.acc and kt != 1):
+        raise PlanError("every output tile must accumulate A(m,k) @ B(k,n) over all k "
+                        "(store(acc=True) inside the K loop)")
+    r0, r1, c0, c1 = _rect(out_rc)
+    if (r1 - r0) * (c1 - c0) != n_out:
+        raise PlanError("the matmul output tiles do not form a rectangle")
+    return MatmulLaunch(tensor_ref(a_t), tensor_ref(b_t), tensor_ref(g.out_tensor),
+                        (r0 * TILE, r1 * TILE), (c0 * TILE, c1 * TILE), K)
+
+
+# ---------------------------------------------------------------------------
+# execution
+
+
+def execute(plan: Plan, args: Dict[Any, Any], stream=None) -> None:
+    from . import kernels as Kn
+    from ._lib import require_device
+
+    require_device()
+    for l in plan.launches:
+        if isinstance(l, EltwiseLaunch):
+            ops = []
+            for spec in l.operands:
+                if spec is None:
+                    ops.append(None)
+                    continue
+                ops.append(Kn.OperandMap(spec.ref.resolve(args), spec.row_mask, spec.col_mask,
+                                         spec.row_off, spec.col_off))
+            Kn.eltwise(l.prog, ops, l.out.resolve(args), region=l.region, stream=stream)
+        else:
+            a, b, c = l.a.resolve(args), l.b.resolve(args), l.c.resolve(args)
+            if c.data_ptr() in (a.data_ptr(), b.data_ptr()):
+                raise ValueError("matmul output aliases an input")
+            r0, r1 = l.rows
+            c0, c1 = l.cols
+            Kn.matmul(a[r0:r1], b[:, c0:c1], c[r0:r1, c0:c1], accumulate=False, stream=stream)

@@ -1,0 +1,381 @@
+"""Drop-in `ttnn` for tt-lang kernels running on one MI355X.
+
+Mirrors the subset of ttnn that tt-lang programs use (the surface of the
+reference simulator's ttnn stand-in, python/sim/ttnnsim.py): device
+open/close, a Tensor wrapper with tile indexing, tensor creation and
+conversion, dtypes / layouts / memory configs, core-grid helpers and
+split_work_to_cores, plus elementwise ttnn ops.
+
+Storage: a Tensor wraps a torch tensor that lives in HBM on the GPU (torch
+for allocation and interop only).  Layout is row-major; "TILE_LAYOUT" is a
+logical 32x32 tiling (the kernels address tiles in place).  Without a GPU
+(CPU-only hosts) tensors stay in host memory so kernels can still be traced
+and planned; running a kernel then raises.
+"""
+
+from __future__ import annotations
+
+import operator as _op
+from typing import Any, List, Optional, Sequence, Tuple, Union
+
+import torch
+
+TILE_SIZE = 32
+TILE_SHAPE = (32, 32)
+
+
+class _Layout:
+    def __init__(self, name: str):
+        self.name = name
+
+    def __repr__(self) -> str:
+        return f"Layout.{self.name}"
+
+
+TILE_LAYOUT = _Layout("TILE")
+ROW_MAJOR_LAYOUT = _Layout("ROW_MAJOR")
+DRAM_MEMORY_CONFIG = None
+L1_MEMORY_CONFIG = None
+
+bfloat16 = torch.bfloat16
+float32 = torch.float32
+
+TTNN_AVAILABLE = True
+
+
+def _device() -> torch.device:
+    return torch.device("cuda") if torch.cuda.is_available() else torch.device("cpu")
+
+
+class Tensor:
+    """ttnn tensor: a torch tensor in device memory with tt-lang tile indexing.
+
+    `t[r, c]`, `t[r0:r1, c0:c1]` (tile coordinates, explicit start/stop, no
+    step; python/sim/tensoraccessor.py:85-159) return a TensorSlice that
+    ttl.copy moves between the tensor and a circular-buffer block.
+    """
+
+    def __init__(self, tensor: torch.Tensor) -> None:
+        if not isinstance(tensor, torch.Tensor):
+            raise TypeError(f"ttnn.Tensor wraps a torch.Tensor, got {type(tensor)}")
+        self._tensor = tensor
+
+    # -- metadata -----------------------------------------------------------
+    @property
+    def shape(self) -> Tuple[int, ...]:
+        return tuple(self._tensor.shape)
+
+    @property
+    def dtype(self) -> torch.dtype:
+        return self._tensor.dtype
+
+    @property
+    def layout(self):
+        return TILE_LAYOUT
+
+    def to_torch(self) -> torch.Tensor:
+        return self._tensor.detach().cpu()
+
+    def __repr__(self) -> str:
+        return f"ttnn.Tensor(shape={self.shape}, dtype={self.dtype}, device={self._tensor.device})"
+
+    # -- tile indexing ------------------------------------------------------
+    def _tile_indexable(self) -> bool:
+        if len(self.shape) != 2:
+            return False
+        return all(d == 1 or d % t == 0 for d, t in zip(self.shape, TILE_SHAPE))
+
+    def __getitem__(self, key: Any):
+        if isinstance(key, tuple) and len(key) == 2 and self._tile_indexable():
+            from ttlhip.trace import TensorSlice, is_index
+
+            if all(is_index(k) for k in key):
+                return TensorSlice.from_key(self, key)
+        return Tensor(self._tensor[key])
+
+    def __setitem__(self, key: Any, value: Any) -> None:
+        if isinstance(value, Tensor):
+            value = value._tensor
+        self._tensor[key] = value
+
+    # -- host-side arithmetic (user code around kernels, e.g. goldens) -------
+    def _binop(self, other: Any, fn, reverse: bool = False) -> "Tensor":
+        o = other._tensor if isinstance(other, Tensor) else other
+        if isinstance(o, torch.Tensor) and o.device != self._tensor.device:
+            o = o.to(self._tensor.device)
+        return Tensor(fn(o, self._tensor) if reverse else fn(self._tensor, o))
+
+    def __add__(self, o): return self._binop(o, _op.add)
+    def __sub__(self, o): return self._binop(o, _op.sub)
+    def __mul__(self, o): return self._binop(o, _op.mul)
+    def __truediv__(self, o): return self._binop(o, _op.truediv)
+    def __floordiv__(self, o): return self._binop(o, _op.floordiv)
+    def __mod__(self, o): return self._binop(o, _op.mod)
+    def __pow__(self, o): return self._binop(o, _op.pow)
+    def __matmul__(self, o): return self._binop(o, _op.matmul)
+    def __radd__(self, o): return self._binop(o, _op.add, True)
+    def __rsub__(self, o): return self._binop(o, _op.sub, True)
+    def __rmul__(self, o): return self._binop(o, _op.mul, True)
+    def __rtruediv__(self, o): return self._binop(o, _op.truediv, True)
+    def __neg__(self): return Tensor(-self._tensor)
+
+
+# ---------------------------------------------------------------------------
+# device
+
+
+class Device:
+    def __init__(self, device_id: int = 0) -> None:
+        self.device_id = device_id
+
+    def __repr__(self) -> str:
+        return f"Device(id={self.device_id}, MI355X)"
+
+    def compute_with_storage_grid_size(self) -> "CoreCoord":
+        """The logical core grid tt-lang programs see: (8, 8), the simulator's
+        "auto" grid (python/sim/ttnnsim.py:215-226).  The MI355X executes the
+        whole tile program grid-wide regardless."""
+        return CoreCoord(8, 8)
+
+
+def open_device(device_id: int = 0, **_: Any) -> Device:
+    return Device(device_id)
+
+
+def close_device(device: Device) -> None:
+    return None
+
+
+def synchronize_device(device: Optional[Device] = None) -> None:
+    if torch.cuda.is_available():
+        torch.cuda.synchronize()
+
+
+# ---------------------------------------------------------------------------
+# creation / conversion
+
+
+def _shape(shape: Union[Sequence[int], int]) -> Tuple[int, ...]:
+    return (shape,) if isinstance(shape, int) else tuple(shape)
+
+
+def rand(shape, dtype: torch.dtype = bfloat16, **_: Any) -> Tensor:
+    """U[0, 1) drawn in fp32 from torch's global generator, then cast - the
+    same stream and rounding as python/sim/ttnnsim.py:521-531."""
+    t = torch.rand(_shape(shape), dtype=torch.float32).to(dtype)
+    return Tensor(t.to(_device()))
+
+
+def empty(shape, dtype: torch.dtype = bfloat16, **_: Any) -> Tensor:
+    return Tensor(torch.empty(_shape(shape), dtype=dtype, device=_device()))
+
+
+def zeros(shape, dtype: torch.dtype = bfloat16, **_: Any) -> Tensor:
+    return Tensor(torch.zeros(_shape(shape), dtype=dtype, device=_device()))
+
+
+def ones(shape, dtype: torch.dtype = bfloat16, **_: Any) -> Tensor:
+    return Tensor(torch.ones(_shape(shape), dtype=dtype, device=_device()))
+
+
+def full(shape, fill_value: float, dtype: torch.dtype = bfloat16, **_: Any) -> Tensor:
+    return Tensor(torch.full(_shape(shape), fill_value, dtype=dtype, device=_device()))
+
+
+def zeros_like(t: Tensor, dtype=None, **_: Any) -> Tensor:
+    return Tensor(torch.zeros_like(t._tensor, dtype=dtype))
+
+
+def empty_like(t: Tensor, dtype=None, **_: Any) -> Tensor:
+    return Tensor(torch.empty_like(t._tensor, dtype=dtype))
+
+
+def from_torch(tensor: torch.Tensor, dtype: Optional[torch.dtype] = None, layout: Any = None,
+               device: Any = None, memory_config: Any = None, **_: Any) -> Tensor:
+    t = tensor.detach()
+    if dtype is not None:
+        t = t.to(dtype)
+    return Tensor(t.to(_device()).contiguous())
+
+
+def to_torch(t: Union[Tensor, torch.Tensor], **_: Any) -> torch.Tensor:
+    if isinstance(t, Tensor):
+        return t.to_torch()
+    return t
+
+
+def to_layout(t: Tensor, layout: Any, **_: Any) -> Tensor:
+    return t
+
+
+def to_device(t: Tensor, device: Any = None, **_: Any) -> Tensor:
+    return t
+
+
+def from_device(t: Tensor, **_: Any) -> Tensor:
+    return t
+
+
+def isclose(a: Tensor, b: Tensor, rtol: float = 1e-05, atol: float = 1e-08,
+            equal_nan: bool = False) -> Tensor:
+    ta = a._tensor if isinstance(a, Tensor) else a
+    tb = b._tensor if isinstance(b, Tensor) else b
+    if isinstance(tb, torch.Tensor) and isinstance(ta, torch.Tensor) and tb.device != ta.device:
+        tb = tb.to(ta.device)
+    return Tensor(torch.isclose(ta, tb, rtol=rtol, atol=atol, equal_nan=equal_nan))
+
+
+# ---------------------------------------------------------------------------
+# elementwise ttnn ops, executed by the MI355X eltwise kernel
+
+
+def _eltwise(op: str, a: Tensor, b: Optional[Tensor]) -> Tensor:
+    from ttlhip import _lib, expr as X
+    from ttlhip.kernels import OperandMap, eltwise
+
+    _lib.require_device()
+    ta = a._tensor.contiguous()
+    leaves = [X.Leaf(OperandMap(ta), ta.dtype)]
+    shape = list(ta.shape)
+    if b is not None:
+        tb = b._tensor.contiguous()
+        if ta.dim() != 2 or tb.dim() != 2:
+            raise ValueError("ttnn elementwise ops take 2-D tensors")
+        for i in range(2):
+            if ta.shape[i] != tb.shape[i] and 1 not in (ta.shape[i], tb.shape[i]):
+                raise ValueError(f"shapes {tuple(ta.shape)} and {tuple(tb.shape)} do not broadcast")
+            shape[i] = max(ta.shape[i], tb.shape[i])
+        leaves.append(X.Leaf(OperandMap(tb), tb.dtype))
+        e = X.Binary(op, leaves[0], leaves[1], X.promote(ta.dtype, tb.dtype))
+    else:
+        e = X.Unary(op, leaves[0], ta.dtype)
+    out = torch.empty(shape, dtype=e.dtype, device=ta.device)
+    prog = X.compile_expr(e)
+    eltwise(prog, [s.leaf.ref if s.leaf is not None else None for s in prog.steps], out)
+    return Tensor(out)
+
+
+def add(a: Tensor, b: Tensor, **_: Any) -> Tensor: return _eltwise("add", a, b)
+def subtract(a: Tensor, b: Tensor, **_: Any) -> Tensor: return _eltwise("sub", a, b)
+def multiply(a: Tensor, b: Tensor, **_: Any) -> Tensor: return _eltwise("mul", a, b)
+def divide(a: Tensor, b: Tensor, **_: Any) -> Tensor: return _eltwise("div", a, b)
+def maximum(a: Tensor, b: Tensor, **_: Any) -> Tensor: return _eltwise("max", a, b)
+def minimum(a: Tensor, b: Tensor, **_: Any) -> Tensor: return _eltwise("min", a, b)
+def exp(a: Tensor, **_: Any) -> Tensor: return _eltwise("exp", a, None)
+def log(a: Tensor, **_: Any) -> Tensor: return _eltwise("log", a, None)
+def sqrt(a: Tensor, **_: Any) -> Tensor: return _eltwise("sqrt", a, None)
+def rsqrt(a: Tensor, **_: Any) -> Tensor: return _eltwise("rsqrt", a, None)
+def tanh(a: Tensor, **_: Any) -> Tensor: return _eltwise("tanh", a, None)
+def abs(a: Tensor, **_: Any) -> Tensor: return _eltwise("abs", a, None)  # noqa: A001
+def neg(a: Tensor, **_: Any) -> Tensor: return _eltwise("neg", a, None)
+def relu(a: Tensor, **_: Any) -> Tensor: return _eltwise("relu", a, None)
+def sigmoid(a: Tensor, **_: Any) -> Tensor: return _eltwise("sigmoid", a, None)
+def reciprocal(a: Tensor, **_: Any) -> Tensor: return _eltwise("recip", a, None)
+
+
+def matmul(a: Tensor, b: Tensor, **_: Any) -> Tensor:
+    """C = A @ B on the MI355X tile-matmul kernel (fp32 accumulation)."""
+    from ttlhip import _lib
+    from ttlhip.kernels import matmul as mm
+
+    _lib.require_device()
+    ta, tb = a._tensor.contiguous(), b._tensor.contiguous()
+    out = torch.empty((ta.shape[0], tb.shape[1]), dtype=torch.promote_types(ta.dtype, tb.dtype),
+                      device=ta.device)
+    mm(ta, tb, out)
+    return Tensor(out)
+
+
+# ---------------------------------------------------------------------------
+# core grid helpers (python/sim/ttnnsim.py:111-189)
+
+
+class CoreCoord:
+    def __init__(self, x: int, y: int):
+        self.x = x
+        self.y = y
+
+    def __repr__(self) -> str:
+        return f"CoreCoord(x={self.x}, y={self.y})"
+
+    def __eq__(self, other: object) -> bool:
+        return isinstance(other, CoreCoord) and self.x == other.x and self.y == other.y
+
+    def __hash__(self) -> int:
+        return hash((self.x, self.y))
+
+
+class CoreRange:
+    def __init__(self, start: CoreCoord, end: CoreCoord):
+        self.start = start
+        self.end = end
+
+    def __repr__(self) -> str:
+        return f"CoreRange(start={self.start}, end={self.end})"
+
+    def num_cores(self) -> int:
+        return (self.end.x - self.start.x + 1) * (self.end.y - self.start.y + 1)
+
+
+class CoreRangeSet:
+    def __init__(self, ranges: List[CoreRange]):
+        self._ranges = list(ranges)
+
+    def ranges(self) -> List[CoreRange]:
+        return self._ranges
+
+    def num_cores(self) -> int:
+        return sum(r.num_cores() for r in self._ranges)
+
+    def __repr__(self) -> str:
+        return f"CoreRangeSet(ranges={self._ranges})"
+
+
+def _ordered_cores(core_grid: Union[CoreCoord, CoreRangeSet], row_wise: bool) -> List[CoreCoord]:
+    if isinstance(core_grid, CoreCoord):
+        if row_wise:
+            return [CoreCoord(x, y) for y in range(core_grid.y) for x in range(core_grid.x)]
+        return [CoreCoord(x, y) for x in range(core_grid.x) for y in range(core_grid.y)]
+    out = []
+    for r in core_grid.ranges():
+        for y in range(r.start.y, r.end.y + 1):
+            for x in range(r.start.x, r.end.x + 1):
+                out.append(CoreCoord(x, y))
+    return out
+
+
+def split_work_to_cores(core_grid: Union[CoreCoord, CoreRangeSet], units_to_divide: int,
+                        row_wise: bool = False):
+    """Divides `units_to_divide` work units over the cores of `core_grid`.
+
+    Same assignment as the reference (python/sim/ttnnsim.py:583-752): min(cores,
+    units) cores are used; with a remainder, the first `remainder` cores
+    (group 1) get one unit more than the rest (group 2); cores are taken y-outer
+    / x-inner when row_wise (x-outer otherwise) for a CoreCoord grid and range
+    by range for a CoreRangeSet.  Each group lists single-core ranges.
+    Returns (num_cores, all_cores, group_1, group_2, units_1, units_2).
+    """
+    if isinstance(core_grid, CoreCoord):
+        n_cores = core_grid.x * core_grid.y
+        all_cores = CoreRangeSet([CoreRange(CoreCoord(0, 0),
+                                            CoreCoord(core_grid.x - 1, core_grid.y - 1))])
+    else:
+        n_cores = core_grid.num_cores()
+        all_cores = core_grid
+    used = min(n_cores, units_to_divide)
+    if used == 0:
+        e = CoreRangeSet([])
+        return 0, e, e, e, 0, 0
+    base, rem = divmod(units_to_divide, used)
+    if rem:
+        u1, u2, n1 = base + 1, base, rem
+    else:
+        u1, u2, n1 = base, 0, used
+    cores = _ordered_cores(core_grid, row_wise)[:used]
+    g1 = CoreRangeSet([CoreRange(c, c) for c in cores[:n1]])
+    g2 = CoreRangeSet([CoreRange(c, c) for c in cores[n1:used]])
+    return used, all_cores, g1, g2, u1, u2
+
+
+def num_cores_to_corerangeset(n: int, grid: CoreCoord, row_wise: bool = False) -> CoreRangeSet:
+    return CoreRangeSet([CoreRange(c, c) for c in _ordered_cores(grid, row_wise)[:n]])
