@@ -218,10 +218,45 @@ class MatmulWorkload(Workload):
                 "rows_checked": int(rows.numel())}
 
 
+class Bfp8MatmulWorkload(MatmulWorkload):
+    """C4: C = A (bf16 [M,K], N(0,1)) . dequant(Bq) with Bq the bfloat8_b
+    tiles of a N(0, 0.02) fp32 [K,N] matrix; dequantised in LDS."""
+
+    def kernel_name(self):
+        return "mm_bf16_kernel<bfp8>"
+
+    def setup(self):
+        from oracle.tile_ops import seeded
+        from ttlhip import kernels as K
+        self.a = seeded((self.M, self.K), "normal", self.seed).cuda()
+        w = seeded((self.K, self.N), "normal", self.seed + 1, torch.float32, std=0.02)
+        self.bq = K.bfp8_pack_host(w).cuda()
+        self.c = torch.empty((self.M, self.N), dtype=torch.bfloat16, device="cuda")
+        self._args = (self.a.data_ptr(), self.K, self.bq.data_ptr(), self.c.data_ptr(), self.N,
+                      self.M, self.N, self.K)
+
+    def launch(self, i):
+        from ttlhip import _lib as L
+        L.call("ttlh_matmul_bfp8w", *self._args, L.stream_ptr())
+
+    def check(self):
+        from oracle import bfp8 as OB
+        self.launch(0)
+        torch.cuda.synchronize()
+        rows = torch.arange(0, self.M, max(1, self.M // 32))
+        wd = OB.unpack_c(self.bq.cpu(), self.K, self.N).double()
+        exact = self.a.cpu()[rows].double() @ wd
+        got = self.c.cpu()[rows].double()
+        return {"max_abs_err_rel": float((got - exact).abs().max() / exact.abs().max()),
+                "rows_checked": int(rows.numel())}
+
+
 WORKLOADS = {
     "eltwise_add_2048": lambda: EltwiseWorkload("eltwise_add_2048", 2048, 2048, "add"),
     "exp_bcast_mul_4096": lambda: EltwiseWorkload("exp_bcast_mul_4096", 4096, 4096, "pipe"),
     "matmul_bf16_4096": lambda: MatmulWorkload("matmul_bf16_4096", 4096, 4096, 4096),
+    "matmul_bfp8w_4096x11008": lambda: Bfp8MatmulWorkload("matmul_bfp8w_4096x11008", 4096, 11008,
+                                                          4096),
 }
 HEADLINE = "exp_bcast_mul_4096"
 

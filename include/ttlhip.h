@@ -167,13 +167,15 @@ int ttlh_matmul(const void* A, int a_dtype, int64_t lda, const void* B,
  *   bytes [0, 64):     shared exponents, face-major (faces f0 = rows 0-15 /
  *                      cols 0-15, f1 = rows 0-15 / cols 16-31, f2 = rows
  *                      16-31 / cols 0-15, f3 = rows 16-31 / cols 16-31),
- *                      one byte per 16-element face row;
- *   bytes [64, 1088):  one byte per element, face-major, row-major inside
- *                      a face: bit 7 = sign, bits 6..0 = magnitude m.
- *   value = (-1)^s * m * 2^(e - 133)   (e = shared biased exponent; e = 0 or
- *   m = 0 gives +-0; a result below the bf16 normal range flushes to +-0).
- * Pack: e = max biased fp32 exponent of the 16 values (0 if all are zero or
- * denormal), m = round-half-to-even(|x| * 2^(133 - e)) saturated to 127.  */
+ *                      byte 16*f + r for face row r;
+ *   bytes [64, 1088):  one byte per element, byte 64 + 256*f + 16*r + c:
+ *                      bit 7 = sign, bits 6..0 = magnitude m.
+ *   value = (-1)^s * m * 2^(e - 133), exactly (m has at most 7 significant
+ *   bits, so every value is a bfloat16, normal or subnormal; only e = 255,
+ *   which packing finite data never produces, can overflow to +-inf).
+ * Pack: e = largest biased fp32 exponent of the 16 values of a face row (0
+ * when all are zero / subnormal), m = round-half-even(|x| * 2^(133 - e))
+ * saturated to 127.  Inputs must be finite.  */
 #define TTLH_BFP8_TILE_BYTES 1088
 
 /* host codec (host pointers) */

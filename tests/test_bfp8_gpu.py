@@ -1,0 +1,75 @@
+"""bfloat8_b on the MI355X: device dequantisation (bit-exact against the
+oracle for every (exponent, byte) pair) and the bf16 x bfp8-weight matmul
+(dequantised in LDS ahead of the MFMA), checked against float64 products of
+the oracle-dequantised weights."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import bfp8 as OB
+from oracle import tile_ops as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _all_pairs_tiles():
+    q = np.zeros((64, 1088), dtype=np.uint8)
+    for t in range(64):
+        for r in range(32):
+            for c in range(32):
+                f = (r // 16) * 2 + c // 16
+                q[t, 16 * f + r % 16] = (t * 4 + f) % 256
+                q[t, 64 + 256 * f + 16 * (r % 16) + c % 16] = ((r % 16) * 16 + c % 16) % 256
+    return torch.from_numpy(q.ravel().copy())
+
+
+def test_device_dequant_all_pairs_bitexact():
+    from ttlhip import kernels as K
+    q = _all_pairs_tiles()
+    got = K.bfp8_unpack(q.cuda(), 32, 2048).cpu()
+    ref = OB.unpack_c(q, 32, 2048)
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+
+
+def test_device_dequant_random_weights():
+    from ttlhip import kernels as K
+    w = O.seeded((256, 512), "normal", 3, torch.float32, std=0.02)
+    q = OB.pack_c(w)
+    got = K.bfp8_unpack(q.cuda(), 256, 512).cpu()
+    assert torch.equal(got.view(torch.int16), OB.unpack_c(q, 256, 512).view(torch.int16))
+
+
+@pytest.mark.parametrize("M,K,N", [(128, 256, 128), (96, 160, 224), (256, 512, 352)])
+def test_matmul_bfp8w_small(M, K, N):
+    from ttlhip import kernels as Kn
+    a = O.seeded((M, K), "normal", 5)
+    w = O.seeded((K, N), "normal", 6, torch.float32, std=0.02)
+    q = OB.pack_c(w)
+    c = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    Kn.matmul_bfp8w(a.cuda(), q.cuda(), c)
+    torch.cuda.synchronize()
+    wd = OB.unpack_c(q, K, N)
+    exact = a.double() @ wd.double()
+    err = (c.cpu().double() - exact).abs()
+    bound = exact.abs() * 2.0 ** -8 + 1e-6 * math.sqrt(K) * float(exact.abs().max())
+    assert bool((err <= bound).all()), float(err.max())
+
+
+def test_matmul_bfp8w_config4_sampled():
+    from ttlhip import kernels as Kn
+    M, K, N = 4096, 4096, 11008
+    a = O.seeded((M, K), "normal", 7)
+    w = O.seeded((K, N), "normal", 8, torch.float32, std=0.02)
+    q = OB.pack_c(w)
+    c = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    Kn.matmul_bfp8w(a.cuda(), q.cuda(), c)
+    torch.cuda.synchronize()
+    rows = torch.arange(0, M, 128)
+    wd = OB.unpack_c(q, K, N).double()
+    exact = a[rows].double() @ wd
+    err = (c.cpu()[rows].double() - exact).abs()
+    bound = exact.abs() * 2.0 ** -8 + 1e-6 * 64 * float(exact.abs().max())
+    assert bool((err <= bound).all()), float(err.max())

@@ -1,5 +1,168 @@
+// bfloat8_b tiles: host codec and device dequantisation.
+//
+// The reference fixes only the tile size, 32*32 + 64 = 1088 bytes
+// (python/ttl/dtype_utils.py:174-175); the packing lives in un-vendored
+// tt-metal.  This build's format (also documented in include/ttlhip.h):
+//   one 32x32 tile = 64 exponent bytes, then 1024 element bytes;
+//   faces f0..f3 = (rows 0-15, cols 0-15), (0-15, 16-31), (16-31, 0-15),
+//   (16-31, 16-31); exponent byte 16*f + r is shared by the 16 elements of
+//   face f, row r; element byte 64 + 256*f + 16*r + c holds sign (bit 7) and
+//   magnitude m (bits 6..0) of face f, row r, col c;
+//   value = (-1)^sign * m * 2^(e - 133), exactly (every such value is a
+//   bfloat16, normal or subnormal, because m has at most 7 significant bits).
+// Pack: e = largest biased fp32 exponent among the 16 values (0 when they are
+// all zero / subnormal), m = round-half-even(|x| * 2^(133 - e)) saturated at
+// 127.  Tiles are stored row-major over the tile grid of the matrix.
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
 #include "ttlh_common.h"
-extern "C" int ttlh_bfp8_pack_host(const float*, void*, int64_t, int64_t) { ttlh::set_error("not built"); return TTLH_EUNSUPPORTED; }
-extern "C" int ttlh_bfp8_unpack_host(const void*, uint16_t*, int64_t, int64_t) { ttlh::set_error("not built"); return TTLH_EUNSUPPORTED; }
-extern "C" int ttlh_bfp8_unpack(const void*, void*, int64_t, int64_t, void*) { ttlh::set_error("not built"); return TTLH_EUNSUPPORTED; }
-extern "C" int ttlh_matmul_bfp8w(const void*, int64_t, const void*, void*, int64_t, int64_t, int64_t, int64_t, void*) { ttlh::set_error("not built"); return TTLH_EUNSUPPORTED; }
+
+namespace ttlh {
+
+// byte offset of element (r, c) inside a tile and of its exponent
+__host__ __device__ inline int bfp8_elem_off(int r, int c) {
+  const int f = ((r >> 4) << 1) | (c >> 4);
+  return 64 + 256 * f + 16 * (r & 15) + (c & 15);
+}
+__host__ __device__ inline int bfp8_exp_off(int r, int c) {
+  const int f = ((r >> 4) << 1) | (c >> 4);
+  return 16 * f + (r & 15);
+}
+
+// exact bf16 bits of (-1)^s * m * 2^(e - 133)
+inline uint16_t bfp8_decode_host(uint8_t e, uint8_t b) {
+  const int m = b & 0x7f;
+  const double v = std::ldexp(static_cast<double>(m), static_cast<int>(e) - 133);
+  const float f = static_cast<float>(v);  // exact: m has <= 7 significant bits
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  return static_cast<uint16_t>((u >> 16) | ((b & 0x80u) << 8));
+}
+
+}  // namespace ttlh
+
+using namespace ttlh;
+
+namespace {
+
+bool finite_all(const float* p, int64_t n) {
+  for (int64_t i = 0; i < n; ++i)
+    if (!std::isfinite(p[i])) return false;
+  return true;
+}
+
+// round-half-to-even of a non-negative double
+double rne(double x) {
+  const double f = std::floor(x);
+  const double d = x - f;
+  if (d > 0.5) return f + 1.0;
+  if (d < 0.5) return f;
+  return std::fmod(f, 2.0) == 0.0 ? f : f + 1.0;
+}
+
+}  // namespace
+
+extern "C" int ttlh_bfp8_pack_host(const float* src, void* dst, int64_t rows, int64_t cols) {
+  clear_error();
+  TTLH_REQUIRE(src && dst, TTLH_EINVAL, "ttlh_bfp8_pack_host: null pointer");
+  TTLH_REQUIRE(rows > 0 && cols > 0 && rows % 32 == 0 && cols % 32 == 0, TTLH_EINVAL,
+               "ttlh_bfp8_pack_host: rows and cols must be positive multiples of 32");
+  TTLH_REQUIRE(finite_all(src, rows * cols), TTLH_EINVAL,
+               "ttlh_bfp8_pack_host: input holds inf or NaN (not representable in bfloat8_b)");
+  uint8_t* out = static_cast<uint8_t*>(dst);
+  const int64_t nt_c = cols / 32;
+  for (int64_t tr = 0; tr < rows / 32; ++tr)
+    for (int64_t tc = 0; tc < nt_c; ++tc) {
+      uint8_t* tile = out + (tr * nt_c + tc) * TTLH_BFP8_TILE_BYTES;
+      for (int r = 0; r < 32; ++r)
+        for (int half = 0; half < 2; ++half) {
+          const float* row = src + (tr * 32 + r) * cols + tc * 32 + half * 16;
+          int e = 0;
+          for (int c = 0; c < 16; ++c) {
+            uint32_t u;
+            std::memcpy(&u, &row[c], 4);
+            e = std::max(e, static_cast<int>((u >> 23) & 0xff));
+          }
+          tile[bfp8_exp_off(r, half * 16)] = static_cast<uint8_t>(e);
+          const double scale = std::ldexp(1.0, 133 - e);
+          for (int c = 0; c < 16; ++c) {
+            const double a = std::fabs(static_cast<double>(row[c])) * scale;
+            const int m = static_cast<int>(std::min(127.0, rne(a)));
+            const uint8_t sign = std::signbit(row[c]) ? 0x80 : 0x00;
+            tile[bfp8_elem_off(r, half * 16 + c)] = static_cast<uint8_t>(sign | m);
+          }
+        }
+    }
+  return TTLH_OK;
+}
+
+extern "C" int ttlh_bfp8_unpack_host(const void* src, uint16_t* dst, int64_t rows, int64_t cols) {
+  clear_error();
+  TTLH_REQUIRE(src && dst, TTLH_EINVAL, "ttlh_bfp8_unpack_host: null pointer");
+  TTLH_REQUIRE(rows > 0 && cols > 0 && rows % 32 == 0 && cols % 32 == 0, TTLH_EINVAL,
+               "ttlh_bfp8_unpack_host: rows and cols must be positive multiples of 32");
+  const uint8_t* in = static_cast<const uint8_t*>(src);
+  const int64_t nt_c = cols / 32;
+  for (int64_t tr = 0; tr < rows / 32; ++tr)
+    for (int64_t tc = 0; tc < nt_c; ++tc) {
+      const uint8_t* tile = in + (tr * nt_c + tc) * TTLH_BFP8_TILE_BYTES;
+      for (int r = 0; r < 32; ++r)
+        for (int c = 0; c < 32; ++c)
+          dst[(tr * 32 + r) * cols + tc * 32 + c] =
+              bfp8_decode_host(tile[bfp8_exp_off(r, c)], tile[bfp8_elem_off(r, c)]);
+    }
+  return TTLH_OK;
+}
+
+// ---------------------------------------------------------------------------
+// device dequantisation (the same decode the bfp8-weight matmul runs in LDS
+// staging, see bfp8_decode8 in ttlh_bfp8.h)
+
+#include "ttlh_bfp8.h"
+
+namespace {
+
+// one thread per (tile, row, half-row of 16): 8 bytes -> 8 bf16 twice
+__global__ __launch_bounds__(256) void bfp8_unpack_kernel(const uint8_t* __restrict__ q,
+                                                          uint16_t* __restrict__ out,
+                                                          int64_t cols, int64_t ntiles,
+                                                          int64_t nt_c) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t tile = gid >> 6;  // 64 half-rows per tile
+  if (tile >= ntiles) return;
+  const int hr = static_cast<int>(gid & 63);
+  const int r = hr >> 1, half = hr & 1;
+  const uint8_t* t = q + tile * TTLH_BFP8_TILE_BYTES;
+  const uint8_t e = t[bfp8_exp_off(r, half * 16)];
+  const uint64_t* mp = reinterpret_cast<const uint64_t*>(t + bfp8_elem_off(r, half * 16));
+  const int64_t tr = tile / nt_c, tc = tile - tr * nt_c;
+  uint16_t* o = out + (tr * 32 + r) * cols + tc * 32 + half * 16;
+  const u32x4 lo = bfp8_decode8(mp[0], e);
+  const u32x4 hi = bfp8_decode8(mp[1], e);
+  *reinterpret_cast<u32x4*>(o) = lo;
+  *reinterpret_cast<u32x4*>(o + 8) = hi;
+}
+
+}  // namespace
+
+extern "C" int ttlh_bfp8_unpack(const void* src, void* dst_bf16, int64_t rows, int64_t cols,
+                                void* stream) {
+  clear_error();
+  TTLH_REQUIRE(src && dst_bf16, TTLH_EINVAL, "ttlh_bfp8_unpack: null pointer");
+  TTLH_REQUIRE(rows > 0 && cols > 0 && rows % 32 == 0 && cols % 32 == 0, TTLH_EINVAL,
+               "ttlh_bfp8_unpack: rows and cols must be positive multiples of 32");
+  TTLH_REQUIRE((reinterpret_cast<uintptr_t>(src) & 7) == 0 &&
+                   (reinterpret_cast<uintptr_t>(dst_bf16) & 15) == 0,
+               TTLH_EINVAL, "ttlh_bfp8_unpack: src must be 8-byte and dst 16-byte aligned");
+  const int64_t ntiles = (rows / 32) * (cols / 32);
+  const int64_t threads = ntiles * 64;
+  const int64_t blocks = (threads + 255) / 256;
+  TTLH_REQUIRE(blocks < (int64_t(1) << 31), TTLH_EUNSUPPORTED, "ttlh_bfp8_unpack: too large");
+  hipLaunchKernelGGL(bfp8_unpack_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint8_t*>(src),
+                     static_cast<uint16_t*>(dst_bf16), cols, ntiles, cols / 32);
+  return check_launch("bfp8_unpack_kernel");
+}

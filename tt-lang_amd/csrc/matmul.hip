@@ -26,6 +26,7 @@
 //  - the epilogue rounds once to the output dtype (RNE).
 // fp32 inputs take a simpler v_mfma_f32_32x32x2f32 kernel (64x64 blocks).
 
+#include "ttlh_bfp8.h"
 #include "ttlh_common.h"
 
 namespace ttlh {
@@ -42,6 +43,8 @@ constexpr int kThreads = 256;
 struct MmArgs {
   const uint16_t* A;
   const uint16_t* B;
+  const uint8_t* Bq;       // bfloat8_b tiles of B (weight-quantised variant)
+  int32_t bq_tiles_n;      // tiles per tile-row of Bq (N / 32)
   void* C;
   int64_t lda, ldb, ldc;
   int32_t M, N, K;
@@ -75,10 +78,13 @@ __device__ __forceinline__ void block_coords(const MmArgs& a, int& bm, int& bn) 
 struct Stage {
   u32x4 a[4];
   u32x4 b[4];
+  uint64_t bq[4];  // bfloat8_b: 8 element bytes per k row (decoded in store_stage)
+  uint32_t be[4];  // and their shared exponents
 };
 
 __device__ __forceinline__ u32x4 zero4() { return u32x4{0u, 0u, 0u, 0u}; }
 
+template <bool BQ>
 __device__ __forceinline__ void load_stage(const MmArgs& p, int bm, int bn, int k0, Stage& s) {
   const int t = threadIdx.x;
 #pragma unroll
@@ -97,9 +103,21 @@ __device__ __forceinline__ void load_stage(const MmArgs& p, int bm, int bn, int 
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int gk = k0 + kq + i;
-    s.b[i] = (gk < p.K && gn < p.N)
-                 ? *reinterpret_cast<gu32x4*>(reinterpret_cast<uintptr_t>(p.B + static_cast<int64_t>(gk) * p.ldb + gn))
-                 : zero4();
+    const bool ok = gk < p.K && gn < p.N;
+    if constexpr (BQ) {
+      // 8 consecutive columns of one k row sit in one half face row
+      const int64_t tile = static_cast<int64_t>(gk >> 5) * p.bq_tiles_n + (gn >> 5);
+      const uint8_t* t8 = p.Bq + tile * TTLH_BFP8_TILE_BYTES;
+      const int r = gk & 31, c = gn & 31;
+      const int f = ((r >> 4) << 1) | (c >> 4);
+      s.bq[i] = ok ? *reinterpret_cast<const uint64_t*>(t8 + 64 + 256 * f + 16 * (r & 15) + (c & 15))
+                   : 0ull;
+      s.be[i] = ok ? t8[16 * f + (r & 15)] : 0u;
+    } else {
+      s.b[i] = ok ? *reinterpret_cast<gu32x4*>(reinterpret_cast<uintptr_t>(
+                        p.B + static_cast<int64_t>(gk) * p.ldb + gn))
+                  : zero4();
+    }
   }
 }
 
@@ -108,8 +126,13 @@ __device__ __forceinline__ uint32_t hi16(uint32_t w) { return w >> 16; }
 
 // Register -> LDS.  A chunks go straight in; the 4x8 B block is transposed to
 // 8 rows of Bt (n-major) with 4 consecutive k each (one 8-byte store per n).
-__device__ __forceinline__ void store_stage(const Stage& s, uint16_t* As, uint16_t* Bts) {
+template <bool BQ>
+__device__ __forceinline__ void store_stage(Stage& s, uint16_t* As, uint16_t* Bts) {
   const int t = threadIdx.x;
+  if constexpr (BQ) {  // dequantise the bfloat8_b rows to bf16 on their way into LDS
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s.b[i] = bfp8_decode8(s.bq[i], static_cast<uint8_t>(s.be[i]));
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int c = t + i * kThreads;
@@ -131,6 +154,7 @@ __device__ __forceinline__ void store_stage(const Stage& s, uint16_t* As, uint16
   }
 }
 
+template <bool BQ>
 __global__ __launch_bounds__(kThreads, 2) void mm_bf16_kernel(const MmArgs p) {
   __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][BM * LDP];  // [buf][A/Bt]
   int bm, bn;
@@ -152,13 +176,13 @@ __global__ __launch_bounds__(kThreads, 2) void mm_bf16_kernel(const MmArgs p) {
 
   const int nk = (p.K + BK - 1) / BK;
   Stage st;
-  load_stage(p, bm, bn, 0, st);
-  store_stage(st, lds[0][0], lds[0][1]);
+  load_stage<BQ>(p, bm, bn, 0, st);
+  store_stage<BQ>(st, lds[0][0], lds[0][1]);
   __syncthreads();
 
   for (int ks = 0; ks < nk; ++ks) {
     const int cur = ks & 1;
-    if (ks + 1 < nk) load_stage(p, bm, bn, (ks + 1) * BK, st);
+    if (ks + 1 < nk) load_stage<BQ>(p, bm, bn, (ks + 1) * BK, st);
     const uint16_t* As = lds[cur][0];
     const uint16_t* Bts = lds[cur][1];
 #pragma unroll
@@ -176,7 +200,7 @@ __global__ __launch_bounds__(kThreads, 2) void mm_bf16_kernel(const MmArgs p) {
         for (int j = 0; j < 2; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
     }
-    if (ks + 1 < nk) store_stage(st, lds[cur ^ 1][0], lds[cur ^ 1][1]);
+    if (ks + 1 < nk) store_stage<BQ>(st, lds[cur ^ 1][0], lds[cur ^ 1][1]);
     __syncthreads();
   }
 
@@ -298,7 +322,7 @@ extern "C" int ttlh_matmul(const void* A, int a_dtype, int64_t lda, const void* 
     TTLH_REQUIRE((reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
                      (reinterpret_cast<uintptr_t>(B) & 15) == 0 && lda % 8 == 0 && ldb % 8 == 0,
                  TTLH_EUNSUPPORTED, "ttlh_matmul: bf16 operands need 16-byte aligned rows");
-    MmArgs a;
+    MmArgs a = {};
     a.A = static_cast<const uint16_t*>(A);
     a.B = static_cast<const uint16_t*>(B);
     a.C = C;
@@ -312,7 +336,7 @@ extern "C" int ttlh_matmul(const void* A, int a_dtype, int64_t lda, const void* 
     a.accumulate = accumulate ? 1 : 0;
     a.grid_m = static_cast<int32_t>((M + BM - 1) / BM);
     a.grid_n = static_cast<int32_t>((N + BN - 1) / BN);
-    hipLaunchKernelGGL(mm_bf16_kernel, dim3(a.grid_m * a.grid_n), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL(mm_bf16_kernel<false>, dim3(a.grid_m * a.grid_n), dim3(kThreads), 0, s, a);
     return check_launch("mm_bf16_kernel");
   }
   MmArgsF a;
@@ -330,4 +354,36 @@ extern "C" int ttlh_matmul(const void* A, int a_dtype, int64_t lda, const void* 
   dim3 grid(static_cast<unsigned>((N + FBN - 1) / FBN), static_cast<unsigned>((M + FBM - 1) / FBM));
   hipLaunchKernelGGL(mm_f32_kernel, grid, dim3(256), 0, s, a);
   return check_launch("mm_f32_kernel");
+}
+
+extern "C" int ttlh_matmul_bfp8w(const void* A, int64_t lda, const void* Bq, void* C, int64_t ldc,
+                                 int64_t M, int64_t N, int64_t K, void* stream) {
+  clear_error();
+  TTLH_REQUIRE(A && Bq && C, TTLH_EINVAL, "ttlh_matmul_bfp8w: null pointer");
+  TTLH_REQUIRE(M > 0 && N > 0 && K > 0 && M % 32 == 0 && N % 32 == 0 && K % 32 == 0, TTLH_EINVAL,
+               "ttlh_matmul_bfp8w: M, N, K must be positive multiples of 32");
+  TTLH_REQUIRE(M < (1 << 30) && N < (1 << 30) && K < (1 << 30), TTLH_EUNSUPPORTED,
+               "ttlh_matmul_bfp8w: dimension too large");
+  TTLH_REQUIRE(lda >= K && ldc >= N && lda % 8 == 0, TTLH_EINVAL,
+               "ttlh_matmul_bfp8w: bad leading dims");
+  TTLH_REQUIRE((reinterpret_cast<uintptr_t>(A) & 15) == 0 && (reinterpret_cast<uintptr_t>(Bq) & 7) == 0,
+               TTLH_EINVAL, "ttlh_matmul_bfp8w: A must be 16-byte and Bq 8-byte aligned");
+  MmArgs a = {};
+  a.A = static_cast<const uint16_t*>(A);
+  a.Bq = static_cast<const uint8_t*>(Bq);
+  a.bq_tiles_n = static_cast<int32_t>(N / 32);
+  a.C = C;
+  a.lda = lda;
+  a.ldb = N;
+  a.ldc = ldc;
+  a.M = static_cast<int32_t>(M);
+  a.N = static_cast<int32_t>(N);
+  a.K = static_cast<int32_t>(K);
+  a.c_dtype = TTLH_BF16;
+  a.accumulate = 0;
+  a.grid_m = static_cast<int32_t>((M + BM - 1) / BM);
+  a.grid_n = static_cast<int32_t>((N + BN - 1) / BN);
+  hipLaunchKernelGGL(mm_bf16_kernel<true>, dim3(a.grid_m * a.grid_n), dim3(kThreads), 0,
+                     static_cast<hipStream_t>(stream), a);
+  return check_launch("mm_bf16_kernel<bfp8>");
 }
