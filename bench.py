@@ -251,12 +251,51 @@ class Bfp8MatmulWorkload(MatmulWorkload):
                 "rows_checked": int(rows.numel())}
 
 
+class SdpaWorkload(Workload):
+    """C5: softmax(Q K^T / sqrt(128)) V, bf16 [4, 32, 4096, 128], non-causal."""
+
+    bound = "mfma"
+    unit = "TFLOP/s"
+
+    def __init__(self, name, B, H, S, D, seed=7):
+        self.name, self.B, self.H, self.S, self.D, self.seed = name, B, H, S, D, seed
+
+    def kernel_name(self):
+        return "sdpa_fwd_kernel"
+
+    def work_per_step(self):
+        return 4.0 * self.B * self.H * self.S * self.S * self.D
+
+    def setup(self):
+        from oracle.tile_ops import seeded
+        shape = (self.B, self.H, self.S, self.D)
+        self.q, self.k, self.v = (seeded(shape, "normal", self.seed + i).cuda() for i in range(3))
+        self.o = torch.empty_like(self.q)
+        self.scale = 1.0 / math.sqrt(self.D)
+        self._args = (self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.o.data_ptr(),
+                      self.B, self.H, self.S, self.D, self.scale, 0)
+
+    def launch(self, i):
+        from ttlhip import _lib as L
+        L.call("ttlh_sdpa_fwd", *self._args, L.stream_ptr())
+
+    def check(self):
+        from oracle.tile_ops import sdpa_ref
+        self.launch(0)
+        torch.cuda.synchronize()
+        ref = sdpa_ref(self.q[:1, :1].cpu(), self.k[:1, :1].cpu(), self.v[:1, :1].cpu(), self.scale)
+        got = self.o[:1, :1].cpu().double()
+        return {"max_abs_err_rel": float((got - ref).abs().max() / ref.abs().max()),
+                "heads_checked": 1}
+
+
 WORKLOADS = {
     "eltwise_add_2048": lambda: EltwiseWorkload("eltwise_add_2048", 2048, 2048, "add"),
     "exp_bcast_mul_4096": lambda: EltwiseWorkload("exp_bcast_mul_4096", 4096, 4096, "pipe"),
     "matmul_bf16_4096": lambda: MatmulWorkload("matmul_bf16_4096", 4096, 4096, 4096),
     "matmul_bfp8w_4096x11008": lambda: Bfp8MatmulWorkload("matmul_bfp8w_4096x11008", 4096, 11008,
                                                           4096),
+    "sdpa_4x32x4096x128": lambda: SdpaWorkload("sdpa_4x32x4096x128", 4, 32, 4096, 128),
 }
 HEADLINE = "exp_bcast_mul_4096"
 

@@ -1,0 +1,80 @@
+"""Fused attention forward (ttlh_sdpa_fwd) against the float64 CPU reference
+softmax(Q K^T s) V (oracle.tile_ops.sdpa_ref).
+
+Bar (north star: bf16 out within a stated tolerance of an fp32 reference):
+max |O - ref| <= 1e-2 * max |ref| and mean |O - ref| <= 4e-3 * mean |ref|
+(bf16 rounding of P and of O contribute about 1e-3 each),
+plus invariants that catch layout / indexing slips exactly: V = 1 gives
+O = 1 (rows of P sum to one), a one-hot V column selects that column of P.
+"""
+
+import math
+
+import pytest
+import torch
+
+from oracle import tile_ops as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(q, k, v, scale, causal=False):
+    from ttlhip import kernels as K
+    out = torch.empty_like(q, device="cuda")
+    K.sdpa_fwd(q.cuda(), k.cuda(), v.cuda(), out, scale, causal)
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+def _qkv(B, H, S, D, seed):
+    return [O.seeded((B, H, S, D), "normal", seed + i) for i in range(3)]
+
+
+def _check(out, ref):
+    err = (out.double() - ref).abs()
+    assert float(err.max()) <= 1e-2 * float(ref.abs().max()), float(err.max())
+    assert float(err.mean()) <= 4e-3 * float(ref.abs().mean()), float(err.mean())
+
+
+@pytest.mark.parametrize("B,H,S,D", [(1, 1, 128, 128), (2, 3, 256, 128), (1, 2, 384, 64)])
+def test_sdpa_matches_reference(B, H, S, D):
+    q, k, v = _qkv(B, H, S, D, 1)
+    scale = 1.0 / math.sqrt(D)
+    _check(_run(q, k, v, scale), O.sdpa_ref(q, k, v, scale))
+
+
+@pytest.mark.parametrize("S", [128, 512])
+def test_sdpa_causal(S):
+    q, k, v = _qkv(1, 2, S, 128, 5)
+    scale = 1.0 / math.sqrt(128)
+    _check(_run(q, k, v, scale, causal=True), O.sdpa_ref(q, k, v, scale, causal=True))
+
+
+def test_sdpa_rows_of_p_sum_to_one():
+    q, k, _ = _qkv(1, 1, 256, 128, 9)
+    v = torch.ones(1, 1, 256, 128, dtype=torch.bfloat16)
+    out = _run(q, k, v, 1.0 / math.sqrt(128))
+    assert float((out.float() - 1.0).abs().max()) <= 2 ** -7
+
+
+def test_sdpa_one_hot_value_selects_probabilities():
+    S = 256
+    q, k, _ = _qkv(1, 1, S, 128, 11)
+    v = torch.zeros(1, 1, S, 128, dtype=torch.bfloat16)
+    v[0, 0, torch.arange(128), torch.arange(128)] = 1.0  # O[:, j] = P[:, j] for j < 128
+    scale = 1.0 / math.sqrt(128)
+    out = _run(q, k, v, scale)
+    s = (q[0, 0].double() @ k[0, 0].double().T) * scale
+    p = torch.softmax(s, -1)
+    err = (out[0, 0].double() - p[:, :128]).abs()
+    assert float(err.max()) <= 1e-2 * float(p.max())
+
+
+def test_sdpa_config5_sampled_heads():
+    B, H, S, D = 4, 32, 4096, 128
+    q, k, v = _qkv(B, H, S, D, 21)
+    scale = 1.0 / math.sqrt(D)
+    out = _run(q, k, v, scale)
+    for b, h in ((0, 0), (3, 31), (2, 17)):
+        ref = O.sdpa_ref(q[b:b + 1, h:h + 1], k[b:b + 1, h:h + 1], v[b:b + 1, h:h + 1], scale)
+        _check(out[b:b + 1, h:h + 1], ref)
