@@ -3,16 +3,22 @@
 
 `python bench.py [--gpus 1] [--steps K] [--warmup W] [--only NAMES]` prints ONE
 JSON line.  The headline workload is BASELINE.json configs[1], the fused
-elementwise + broadcast pipe Y = exp(A + b_row) * C on bf16 4096x4096 tiles;
-`value` is its whole-job HBM throughput in GB/s.  The other configs are
-measured in the same run and reported under "workloads".
+elementwise + broadcast pipe Y = exp(A + b_row) * C on bf16 4096x4096 tiles,
+written as a tt-lang kernel (tests/kernel_lib.py: make_exp_row_pipe) and run
+through the drop-in `ttl`; `value` is its HBM throughput in GB/s.  The other
+configs are measured in the same run and listed under "workloads" with their
+own roofline figures:
+  C1 eltwise add 2048^2       tt-lang kernel (eltwise_add style)   HBM GB/s
+  C3 bf16 matmul 4096^3       tt-lang kernel (multicore style)     TFLOP/s
+  C4 bf16 x bfp8 4096x4096x11008   ttlh_matmul_bfp8w               TFLOP/s
+  C5 SDPA [4,32,4096,128]     ttlh_sdpa_fwd                        TFLOP/s
 
 A "step" is one pass of the hot path over one batch of synthetic input: one
-kernel launch over one resident buffer set.  Inputs live in HBM before the
-timed region starts; eltwise configs rotate buffer sets totalling > 256 MB so
-the 256 MB Infinity Cache cannot serve them.  The K timed launches are
-captured once into a HIP graph and replayed, so host launch overhead does not
-pad the small kernels; HIP events on the launch stream bracket the replay.
+execution of the kernel's launch plan over one resident buffer set.  Inputs
+are in HBM before the timed region; elementwise configs rotate buffer sets
+totalling > 256 MB so the Infinity Cache cannot serve them.  The K timed
+steps are captured once into a HIP graph and replayed, so host overhead does
+not pad short kernels; HIP events on the launch stream bracket the replay.
 """
 
 from __future__ import annotations
@@ -25,13 +31,15 @@ import sys
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
-sys.path.insert(0, os.path.join(ROOT, "tt-lang_amd"))
-sys.path.insert(0, ROOT)
+for _p in (os.path.join(ROOT, "tests"), os.path.join(ROOT, "tt-lang_amd"), ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
 
 import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
 
 def log(msg: str) -> None:
@@ -40,152 +48,146 @@ def log(msg: str) -> None:
 
 # --------------------------------------------------------------------------
 # workloads
-# --------------------------------------------------------------------------
+
 
 class Workload:
     name = ""
     bound = "hbm"
     unit = "GB/s"
+    config = ""
 
-    def setup(self):  # allocate resident inputs
+    def setup(self):
         raise NotImplementedError
 
-    def launch(self, i: int):  # enqueue step i on the current stream
+    def launch(self, i: int):
         raise NotImplementedError
 
-    def work_per_step(self) -> float:  # algorithmic bytes or flops of one launch
+    def work_per_step(self) -> float:
         raise NotImplementedError
 
     def kernel_name(self) -> str:
         raise NotImplementedError
 
+    def check(self) -> dict:
+        raise NotImplementedError
 
-class EltwiseWorkload(Workload):
-    """C1 (eltwise add 2048^2) and C2 (exp(A + b_row) * C, 4096^2)."""
 
-    def __init__(self, name, rows, cols, expr_kind, seed=1234):
-        self.name = name
-        self.rows, self.cols = rows, cols
-        self.kind = expr_kind
-        self.seed = seed
+class PlanWorkload(Workload):
+    """A tt-lang kernel traced once by the drop-in `ttl`; each step executes
+    its launch plan on one of the resident buffer sets."""
 
-    def kernel_name(self):
-        return "eltwise_kernel"
-
-    def work_per_step(self):
-        n = self.rows * self.cols * 2
-        return 3 * n if self.kind == "add" else 3 * n + self.cols * 2
-
-    def build_expr(self, t):
-        from ttlhip import expr as X
-        from ttlhip.kernels import OperandMap
-
-        bf = torch.bfloat16
-        if self.kind == "add":
-            a, b = X.Leaf(OperandMap(t["a"]), bf), X.Leaf(OperandMap(t["b"]), bf)
-            return X.Binary("add", a, b, bf)
-        a = X.Leaf(OperandMap(t["a"]), bf)
-        b = X.Leaf(OperandMap(t["b"]), bf)
-        c = X.Leaf(OperandMap(t["c"]), bf)
-        return X.Binary("mul", X.Unary("exp", X.Binary("add", a, b, bf), bf), c, bf)
-
-    def cpu_inputs(self, seed):
-        from oracle.tile_ops import seeded
-        r, c = self.rows, self.cols
-        if self.kind == "add":
-            return {"a": seeded((r, c), "uniform", seed, lo=-1, hi=1),
-                    "b": seeded((r, c), "uniform", seed + 1, lo=-1, hi=1)}
-        return {"a": seeded((r, c), "uniform", seed, lo=-2, hi=2),
-                "b": seeded((1, c), "uniform", seed + 1, lo=-2, hi=2),
-                "c": seeded((r, c), "uniform", seed + 2, lo=-2, hi=2)}
+    def make_sets(self):  # -> list of arg lists (ttnn tensors)
+        raise NotImplementedError
 
     def setup(self):
-        from ttlhip import expr as X
+        from ttlhip import plan as P
 
-        per_set = self.work_per_step()
-        self.nsets = max(3, math.ceil(300e6 / per_set))
-        self.sets = []
-        base = {k: v.cuda() for k, v in self.cpu_inputs(self.seed).items()}
-        for s in range(self.nsets):
-            t = base if s == 0 else {k: v.clone() for k, v in base.items()}
-            out = torch.empty((self.rows, self.cols), dtype=torch.bfloat16, device="cuda")
-            e = self.build_expr(t)
-            prog = X.compile_expr(e)
-            self.sets.append((t, out, prog))
-        self._prepared = [self._prepare(t, out, prog) for (t, out, prog) in self.sets]
-
-    def _prepare(self, t, out, prog):
-        from ttlhip import _lib as L
-        from ttlhip.kernels import _operand_struct
-
-        n = len(prog.steps)
-        instrs = (L.Instr * n)()
-        ops = (L.Operand * n)()
-        for k, s in enumerate(prog.steps):
-            instrs[k] = L.Instr(s.op, s.form, s.rnd, 0, s.imm)
-            if s.leaf is not None:
-                ops[k] = _operand_struct(s.leaf.ref, 0, 0, self.rows, self.cols)
-        return (instrs, ops, n, out.data_ptr(), L.TTLH_BF16, out.stride(0), 0, 0, self.rows,
-                self.cols)
+        self.sets = self.make_sets()
+        self.plan = self.kernel.trace(*self.sets[0])
+        assert len(self.plan.launches) == 1, self.plan.describe()
+        self.amaps = [dict(enumerate(s)) for s in self.sets]
+        self._execute = P.execute
 
     def launch(self, i):
-        from ttlhip import _lib as L
-        args = self._prepared[i % self.nsets]
-        L.call("ttlh_eltwise", *args, L.stream_ptr())
+        self._execute(self.plan, self.amaps[i % len(self.amaps)])
+
+
+class EltwiseWorkload(PlanWorkload):
+    def __init__(self, name, n, kind, seed=1234):
+        self.name, self.n, self.kind, self.seed = name, n, kind, seed
+        self.config = ("eltwise add C = A + B, bf16 %dx%d, U[-1,1] (BASELINE configs[0])" % (n, n)
+                       if kind == "add" else
+                       "fused eltwise pipe + broadcast Y = exp(A + b_row) * C, bf16 %dx%d, "
+                       "b_row 1x%d, U[-2,2] (BASELINE configs[1])" % (n, n, n))
+
+    def kernel_name(self):
+        return "chain_kernel"
+
+    def work_per_step(self):
+        e = self.n * self.n * 2
+        return 3 * e if self.kind == "add" else 3 * e + self.n * 2
+
+    def expr(self):
+        if self.kind == "add":
+            return ("add", ("leaf", "a"), ("leaf", "b"))
+        return ("mul", ("exp", ("add", ("leaf", "a"), ("leaf", "b"))), ("leaf", "c"))
+
+    def cpu_inputs(self):
+        from oracle.tile_ops import seeded
+        n, s = self.n, self.seed
+        if self.kind == "add":
+            return [seeded((n, n), "uniform", s, lo=-1, hi=1),
+                    seeded((n, n), "uniform", s + 1, lo=-1, hi=1)]
+        return [seeded((n, n), "uniform", s, lo=-2, hi=2),
+                seeded((1, n), "uniform", s + 1, lo=-2, hi=2),
+                seeded((n, n), "uniform", s + 2, lo=-2, hi=2)]
+
+    def make_kernel(self, ttl_ns):
+        import kernel_lib as KL
+        return KL.make_eltwise_add(ttl_ns) if self.kind == "add" else KL.make_exp_row_pipe(ttl_ns)
+
+    def make_sets(self):
+        import ttl
+        import ttnn
+
+        self.kernel = self.make_kernel(ttl)
+        base = [ttnn.from_torch(t) for t in self.cpu_inputs()]
+        nsets = max(3, math.ceil(300e6 / self.work_per_step()))
+        sets = []
+        for i in range(nsets):
+            ins = base if i == 0 else [ttnn.Tensor(t._tensor.clone()) for t in base]
+            sets.append(ins + [ttnn.empty((self.n, self.n), dtype=torch.bfloat16)])
+        return sets
 
     def check(self):
-        """Parity of set 0 against the oracle (bit-exact except exp: <= 1 ulp)."""
         from oracle import tile_ops as O
-        t, out, _ = self.sets[0]
         self.launch(0)
         torch.cuda.synchronize()
-        env = {k: v.cpu() for k, v in t.items()}
-        if self.kind == "add":
-            ref = O.eval_expr(("add", ("leaf", "a"), ("leaf", "b")), env)
-        else:
-            ref = O.eval_expr(("mul", ("exp", ("add", ("leaf", "a"), ("leaf", "b"))),
-                               ("leaf", "c")), env)
-        ulp = O.bf16_ulp_diff(out.cpu(), ref)
-        return {"max_ulp": int(ulp.max()), "mismatch_frac": float((ulp > 0).float().mean())}
+        ref = O.eval_expr(self.expr(), dict(zip("abc", self.cpu_inputs())))
+        ulp = O.bf16_ulp_diff(self.sets[0][-1].to_torch(), ref)
+        return {"max_ulp": int(ulp.max()), "mismatch_frac": float((ulp > 0).float().mean()),
+                "oracle": "vectorised simulator semantics (per-op bf16 rounding)"}
 
-    def cpu_baseline(self, budget_s=8.0):
-        """Oracle timed tile-by-tile, one torch op per 32x32 tile on one
-        thread (the simulator's execution granularity), on a sample of tiles."""
-        from oracle import tile_ops as O
-        env = self.cpu_inputs(self.seed)
-        nthreads = torch.get_num_threads()
+    def cpu_baseline(self):
+        """The oracle's eager executor (one torch op per 32x32 tile, CB ring
+        bookkeeping, three threads per core under the GIL: the simulator's
+        execution model) on the same tt-lang kernel and the full-size input."""
+        from oracle import sim_exec, tile_ops as O
+        k = self.make_kernel(sim_exec.make_ttl())
+        ins = [sim_exec.OracleTensor(t) for t in self.cpu_inputs()]
+        out = sim_exec.OracleTensor(torch.zeros(self.n, self.n, dtype=torch.bfloat16))
+        nthr = torch.get_num_threads()
         torch.set_num_threads(1)
         try:
-            rt, ct = self.rows // 32, self.cols // 32
-            done, t0 = 0, time.perf_counter()
-            while time.perf_counter() - t0 < budget_s and done < rt * ct:
-                r, c = divmod(done, ct)
-                a = env["a"][r * 32:(r + 1) * 32, c * 32:(c + 1) * 32]
-                b = env["b"][0:1, c * 32:(c + 1) * 32] if self.kind != "add" else \
-                    env["b"][r * 32:(r + 1) * 32, c * 32:(c + 1) * 32]
-                if self.kind == "add":
-                    y = a + b
-                else:
-                    y = torch.exp(a + b) * env["c"][r * 32:(r + 1) * 32, c * 32:(c + 1) * 32]
-                done += 1
+            t0 = time.perf_counter()
+            k(*ins, out)
             dt = time.perf_counter() - t0
         finally:
-            torch.set_num_threads(nthreads)
-        bytes_per_tile = self.work_per_step() / (rt * ct)
-        return {"value": done * bytes_per_tile / dt / 1e9, "unit": "GB/s", "cores": 1,
+            torch.set_num_threads(nthr)
+        env = dict(zip("abc", self.cpu_inputs()))
+        t0 = time.perf_counter()
+        O.eval_expr(self.expr(), env)
+        dtv = time.perf_counter() - t0
+        return {"value": round(self.work_per_step() / dt / 1e9, 4), "unit": "GB/s", "cores": 1,
                 "kind": "port",
-                "sample": f"{done} of {rt * ct} output tiles, tile-by-tile torch CPU ops "
-                          f"(simulator granularity), {dt:.1f} s"}
+                "sample": f"the full {self.n}x{self.n} workload through the eager tile-by-tile "
+                          f"oracle executor (simulator execution model, 1 thread): {dt:.2f} s",
+                "host_cpu_count": os.cpu_count(),
+                "vectorised_torch_cpu": {"value": round(self.work_per_step() / dtv / 1e9, 3),
+                                         "unit": "GB/s", "cores": nthr}}
 
 
-class MatmulWorkload(Workload):
-    """C3: C[M,N] = A[M,K] . B[K,N], bf16 in, fp32 accumulate, bf16 out."""
+class MatmulWorkload(PlanWorkload):
+    """C3 through the multicore-style tt-lang kernel (13x10 grid, (1,1) CBs,
+    store(acc=True) over K) -> one MFMA GEMM launch."""
 
     bound = "mfma"
     unit = "TFLOP/s"
 
     def __init__(self, name, M, N, K, seed=99):
         self.name, self.M, self.N, self.K, self.seed = name, M, N, K, seed
+        self.config = (f"tiled matmul C = A.B bf16 {M}x{K}x{N}, N(0,1)/sqrt(K), fp32 accumulate, "
+                       "bf16 out, 4x4-tile output blocks (BASELINE configs[2])")
 
     def kernel_name(self):
         return "mm_bf16_kernel"
@@ -193,37 +195,46 @@ class MatmulWorkload(Workload):
     def work_per_step(self):
         return 2.0 * self.M * self.N * self.K
 
-    def setup(self):
+    def make_sets(self):
+        import kernel_lib as KL
+        import ttl
+        import ttnn
         from oracle.tile_ops import seeded
+        self.kernel = KL.make_matmul_multi(ttl, ttnn)
         std = 1.0 / math.sqrt(self.K)
-        self.a = seeded((self.M, self.K), "normal", self.seed, std=std).cuda()
-        self.b = seeded((self.K, self.N), "normal", self.seed + 1, std=std).cuda()
-        self.c = torch.empty((self.M, self.N), dtype=torch.bfloat16, device="cuda")
-        from ttlhip import _lib as L
-        self._args = (self.a.data_ptr(), L.TTLH_BF16, self.K, self.b.data_ptr(), L.TTLH_BF16,
-                      self.N, self.c.data_ptr(), L.TTLH_BF16, self.N, self.M, self.N, self.K, 0)
-
-    def launch(self, i):
-        from ttlhip import _lib as L
-        L.call("ttlh_matmul", *self._args, L.stream_ptr())
+        a = ttnn.from_torch(seeded((self.M, self.K), "normal", self.seed, std=std))
+        b = ttnn.from_torch(seeded((self.K, self.N), "normal", self.seed + 1, std=std))
+        c = ttnn.empty((self.M, self.N), dtype=torch.bfloat16)
+        return [[a, b, c]]
 
     def check(self):
-        """64 sampled rows against float64: max error relative to max |C|."""
         self.launch(0)
         torch.cuda.synchronize()
+        a, b, c = (t.to_torch() for t in self.sets[0])
         rows = torch.arange(0, self.M, max(1, self.M // 64))
-        exact = self.a.cpu()[rows].double() @ self.b.cpu().double()
-        got = self.c.cpu()[rows].double()
+        exact = a[rows].double() @ b.double()
+        got = c[rows].double()
         return {"max_abs_err_rel": float((got - exact).abs().max() / exact.abs().max()),
-                "rows_checked": int(rows.numel())}
+                "rows_checked": int(rows.numel()), "oracle": "float64 product"}
 
 
-class Bfp8MatmulWorkload(MatmulWorkload):
-    """C4: C = A (bf16 [M,K], N(0,1)) . dequant(Bq) with Bq the bfloat8_b
-    tiles of a N(0, 0.02) fp32 [K,N] matrix; dequantised in LDS."""
+class Bfp8MatmulWorkload(Workload):
+    """C4: C = A (bf16 [M,K], N(0,1)) . dequant(Bq), Bq the bfloat8_b tiles of
+    an N(0, 0.02) fp32 [K,N] matrix, dequantised in LDS (C ABI)."""
+
+    bound = "mfma"
+    unit = "TFLOP/s"
+
+    def __init__(self, name, M, N, K, seed=77):
+        self.name, self.M, self.N, self.K, self.seed = name, M, N, K, seed
+        self.config = (f"weight-quantised matmul bf16 [{M},{K}] x bfloat8_b [{K},{N}], fp32 "
+                       "accumulate, bf16 out (BASELINE configs[3])")
 
     def kernel_name(self):
         return "mm_bf16_kernel<bfp8>"
+
+    def work_per_step(self):
+        return 2.0 * self.M * self.N * self.K
 
     def setup(self):
         from oracle.tile_ops import seeded
@@ -248,17 +259,20 @@ class Bfp8MatmulWorkload(MatmulWorkload):
         exact = self.a.cpu()[rows].double() @ wd
         got = self.c.cpu()[rows].double()
         return {"max_abs_err_rel": float((got - exact).abs().max() / exact.abs().max()),
-                "rows_checked": int(rows.numel())}
+                "rows_checked": int(rows.numel()),
+                "oracle": "float64 product of the C oracle's dequantisation"}
 
 
 class SdpaWorkload(Workload):
-    """C5: softmax(Q K^T / sqrt(128)) V, bf16 [4, 32, 4096, 128], non-causal."""
+    """C5: softmax(Q K^T / sqrt(D)) V, bf16 [B, H, S, D], non-causal (C ABI)."""
 
     bound = "mfma"
     unit = "TFLOP/s"
 
     def __init__(self, name, B, H, S, D, seed=7):
         self.name, self.B, self.H, self.S, self.D, self.seed = name, B, H, S, D, seed
+        self.config = (f"fused SDPA fwd Q,K,V bf16 [{B},{H},{S},{D}], N(0,1), scale 1/sqrt({D}), "
+                       "non-causal, fp32 online softmax (BASELINE configs[4])")
 
     def kernel_name(self):
         return "sdpa_fwd_kernel"
@@ -286,21 +300,21 @@ class SdpaWorkload(Workload):
         ref = sdpa_ref(self.q[:1, :1].cpu(), self.k[:1, :1].cpu(), self.v[:1, :1].cpu(), self.scale)
         got = self.o[:1, :1].cpu().double()
         return {"max_abs_err_rel": float((got - ref).abs().max() / ref.abs().max()),
-                "heads_checked": 1}
+                "heads_checked": 1, "oracle": "float64 softmax(QK^T s)V"}
 
 
 WORKLOADS = {
-    "eltwise_add_2048": lambda: EltwiseWorkload("eltwise_add_2048", 2048, 2048, "add"),
-    "exp_bcast_mul_4096": lambda: EltwiseWorkload("exp_bcast_mul_4096", 4096, 4096, "pipe"),
+    "exp_bcast_mul_4096": lambda: EltwiseWorkload("exp_bcast_mul_4096", 4096, "pipe"),
+    "eltwise_add_2048": lambda: EltwiseWorkload("eltwise_add_2048", 2048, "add"),
     "matmul_bf16_4096": lambda: MatmulWorkload("matmul_bf16_4096", 4096, 4096, 4096),
-    "matmul_bfp8w_4096x11008": lambda: Bfp8MatmulWorkload("matmul_bfp8w_4096x11008", 4096, 11008,
-                                                          4096),
+    "matmul_bfp8w_4096x11008": lambda: Bfp8MatmulWorkload("matmul_bfp8w_4096x11008", 4096,
+                                                          11008, 4096),
     "sdpa_4x32x4096x128": lambda: SdpaWorkload("sdpa_4x32x4096x128", 4, 32, 4096, 128),
 }
 HEADLINE = "exp_bcast_mul_4096"
 
 
-def measure(w: Workload, steps: int, warmup: int, use_graph: bool = True):
+def measure(w: Workload, steps: int, warmup: int, use_graph: bool = True) -> dict:
     w.setup()
     for i in range(warmup):
         w.launch(i)
@@ -332,46 +346,65 @@ def measure(w: Workload, steps: int, warmup: int, use_graph: bool = True):
     ms = e0.elapsed_time(e1)
     per = ms / steps
     work = w.work_per_step()
-    achieved = work / (per * 1e-3) / (1e9 if w.unit == "GB/s" else 1e12)
+    scale = 1e9 if w.unit == "GB/s" else 1e12
+    achieved = work / (per * 1e-3) / scale
     peak = HBM_PEAK_GBS if w.unit == "GB/s" else BF16_PEAK_TFLOPS
-    return {"name": w.name, "ms_total": ms, "ms_per_step": per, "achieved": achieved,
-            "unit": w.unit, "peak": peak, "frac": achieved / peak, "work_per_step": work,
-            "kernel": w.kernel_name(), "bound": w.bound}
+    return {"name": w.name, "config": w.config, "kernel": w.kernel_name(), "bound": w.bound,
+            "steps": steps, "ms_total": ms, "ms_per_step": per, "achieved": achieved,
+            "unit": w.unit, "peak": peak, "frac": achieved / peak, "work_per_step": work}
+
+
+def traffic_for(name: str):
+    """HBM bytes per launch measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+    (scaled by a copy kernel's readings), from the committed profile summary."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f).get(name)
+        return None if t is None else t.get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
 
 
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", default="", help="comma-separated workload names")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run one 256 MiB device copy (PMC byte-counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
-              f"--gpus {args.gpus}); the per-GPU work shards without communication, "
-              f"see DESIGN.md.", file=sys.stderr)
+              f"--gpus {args.gpus}). Every config shards without communication; see DESIGN.md "
+              "'More than one GPU'.", file=sys.stderr)
         return 2
     if not torch.cuda.is_available():
         print("bench.py needs an MI355X (no HIP device visible)", file=sys.stderr)
         return 1
+    if args.copy_calibration:
+        src = torch.ones(128 * 1024 * 1024, dtype=torch.int16, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     names = [n for n in (args.only.split(",") if args.only else WORKLOADS) if n]
     if HEADLINE not in names:
         names.insert(0, HEADLINE)
     results = {}
-    checks = {}
     for n in names:
         w = WORKLOADS[n]()
-        log(f"[bench] {n}: steps={args.steps} warmup={args.warmup}")
-        results[n] = measure(w, args.steps, args.warmup, use_graph=not args.no_graph)
-        checks[n] = w.check()
-        results[n]["parity"] = checks[n]
-        log(f"[bench] {n}: {results[n]['ms_per_step']*1e3:.2f} us/step "
-            f"{results[n]['achieved']:.1f} {results[n]['unit']} ({results[n]['frac']*100:.1f}%) "
-            f"parity={checks[n]}")
-        if n == HEADLINE:
-            headline_w = w
+        steps = args.steps if w.unit == "GB/s" else max(1, min(args.steps, 20))
+        warm = args.warmup if w.unit == "GB/s" else max(1, min(args.warmup, 3))
+        log(f"[bench] {n}: steps={steps} warmup={warm}")
+        r = measure(w, steps, warm, use_graph=not args.no_graph)
+        r["parity"] = w.check()
+        r["traffic"] = traffic_for(n)
+        results[n] = r
+        log(f"[bench] {n}: {r['ms_per_step'] * 1e3:.2f} us/step {r['achieved']:.1f} {r['unit']} "
+            f"({r['frac'] * 100:.1f}%) parity={r['parity']}")
         del w
         torch.cuda.empty_cache()
     h = results[HEADLINE]
@@ -379,6 +412,7 @@ def main() -> int:
     if not args.no_cpu:
         log("[bench] cpu baseline ...")
         cpu = WORKLOADS[HEADLINE]().cpu_baseline()
+        log(f"[bench] cpu baseline {cpu['value']} GB/s")
     line = {
         "metric": "eltwise GB/s (% HBM peak); matmul/SDPA bf16 TFLOP/s (% MFMA peak) @1 GPU",
         "value": round(h["achieved"], 2),
@@ -391,13 +425,12 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded U[-2,2] bf16; resident in HBM; buffer sets rotated)",
-        "config": {"workload": "fused eltwise pipe + broadcast: Y = exp(A + b_row) * C, "
-                               "A,C bf16 4096x4096, b_row 1x4096 (BASELINE configs[1])",
-                   "tiles": "32x32", "grid": "whole tensor, one launch"},
-        "roofline": {"bound": h["bound"], "achieved": round(h["achieved"], 2),
-                     "peak": h["peak"], "unit": h["unit"], "frac": round(h["frac"], 4),
-                     "traffic": None},
+        "data": "synthetic (seeded; resident in HBM; eltwise buffer sets rotated over > 256 MB)",
+        "config": {"workload": h["config"], "kernel": "tt-lang kernel via drop-in ttl -> "
+                   "ttlh_eltwise chain_kernel", "tiles": "32x32", "cb_block": "4x4 tiles",
+                   "grid": "(8, 8) tt-lang cores -> one grid-wide launch"},
+        "roofline": {"bound": h["bound"], "achieved": round(h["achieved"], 2), "peak": h["peak"],
+                     "unit": h["unit"], "frac": round(h["frac"], 4), "traffic": h["traffic"]},
         "cpu_baseline": cpu,
         "workloads": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
                       for r in results.values()],
