@@ -101,7 +101,7 @@ class EltwiseWorkload(PlanWorkload):
                        "b_row 1x%d, U[-2,2] (BASELINE configs[1])" % (n, n, n))
 
     def kernel_name(self):
-        return "chain_kernel"
+        return "stream_kernel"
 
     def work_per_step(self):
         e = self.n * self.n * 2
@@ -360,7 +360,7 @@ def traffic_for(name: str):
     try:
         with open(TRAFFIC_FILE) as f:
             t = json.load(f).get(name)
-        return None if t is None else t.get("hbm_bytes_per_launch")
+        return None if t is None else t.get("hbm_bytes_per_launch")  # measured for t["kernel"]
     except (OSError, ValueError):
         return None
 
@@ -427,7 +427,7 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic (seeded; resident in HBM; eltwise buffer sets rotated over > 256 MB)",
         "config": {"workload": h["config"], "kernel": "tt-lang kernel via drop-in ttl -> "
-                   "ttlh_eltwise chain_kernel", "tiles": "32x32", "cb_block": "4x4 tiles",
+                   "ttlh_eltwise stream_kernel", "tiles": "32x32", "cb_block": "4x4 tiles",
                    "grid": "(8, 8) tt-lang cores -> one grid-wide launch"},
         "roofline": {"bound": h["bound"], "achieved": round(h["achieved"], 2), "peak": h["peak"],
                      "unit": h["unit"], "frac": round(h["frac"], 4), "traffic": h["traffic"]},

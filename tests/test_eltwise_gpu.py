@@ -206,3 +206,37 @@ def test_special_values_and_ties():
     e2 = ("max", ("leaf", "a"), ("leaf", "b"))
     got = run_gpu(e2, env, {}, (8, 16), torch.float32)
     assert_bitexact(got, O.eval_expr(e2, env))
+
+
+@pytest.mark.parametrize("h,w", [(37, 296), (3, 4104), (1, 8), (5, 2048), (130, 520)])
+def test_chain_fast_path_shapes(h, w):
+    # bf16 linear chains take the 2-D stream kernel: rows narrower than 256
+    # chunks share a workgroup, non-power-of-two chunk counts leave dead lanes,
+    # rows wider than 2048 elements span several workgroups
+    a, c = _u((h, w), 80), _u((h, w), 81)
+    b = _u((1, w), 82)
+    env = {"a": a, "b": b, "c": c}
+    e = ("mul", ("exp", ("add", ("leaf", "a"), ("leaf", "b"))), ("leaf", "c"))
+    got = run_gpu(e, env, {}, (h, w), torch.bfloat16)
+    ulp = O.bf16_ulp_diff(got, O.eval_expr(e, env))
+    assert int(ulp.max()) <= 1
+    e2 = ("sub", ("mul", ("add", ("leaf", "a"), ("const", 3.0)), ("leaf", "c")), ("leaf", "b"))
+    got = run_gpu(e2, env, {}, (h, w), torch.bfloat16)
+    assert_bitexact(got, O.eval_expr(e2, env))
+    got = run_gpu(("add", ("leaf", "a"), ("leaf", "c")), env, {}, (h, w), torch.float32)
+    assert_bitexact(got, O.eval_expr(("add", ("leaf", "a"), ("leaf", "c")), env).float())
+
+
+def test_chain_exp_special_values():
+    # a wave whose arguments include inf / NaN / overflow / subnormal results
+    # leaves the straight-line exp path; every element still matches torch
+    vals = torch.tensor([float("nan"), float("inf"), -float("inf"), 0.0, -0.0, 1.0, 88.0,
+                         89.0, -87.0, -100.0, -104.0, 1e-30], dtype=torch.float32)
+    a = vals.repeat(64).reshape(24, 32).bfloat16()
+    env = {"a": a}
+    e = ("exp", ("leaf", "a"))
+    got = run_gpu(e, env, {}, (24, 32), torch.bfloat16)
+    ref = O.eval_expr(e, env)
+    both_nan = torch.isnan(got) & torch.isnan(ref)
+    ulp = O.bf16_ulp_diff(got, ref)
+    assert bool(((ulp <= 1) | both_nan).all()), got[~((ulp <= 1) | both_nan)]

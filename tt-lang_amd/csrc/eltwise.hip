@@ -133,10 +133,11 @@ __device__ __forceinline__ uint32_t pick_dword(const u32x4 q, uint32_t byte) {
   return (w & 2) ? hi : lo;
 }
 
-template <int VEC, bool BF16>
+// ALLVEC: the caller guarantees op.vec (8 distinct consecutive elements).
+template <int VEC, bool BF16, bool ALLVEC = false>
 __device__ __forceinline__ f32x8 to_f32(const EltOperand& op, const Raw& r) {
   if (BF16 || op.dtype == TTLH_BF16) {
-    if (VEC == 8 && op.vec) {
+    if (VEC == 8 && (ALLVEC || op.vec)) {
       const u32x4 q = r.q;
       return f32x8{__uint_as_float(q.x << 16), __uint_as_float(q.x & 0xffff0000u),
                    __uint_as_float(q.y << 16), __uint_as_float(q.y & 0xffff0000u),
@@ -146,7 +147,7 @@ __device__ __forceinline__ f32x8 to_f32(const EltOperand& op, const Raw& r) {
     const uint32_t d = pick_dword(r.q, r.sel);
     return splat(__uint_as_float((r.sel & 2) ? (d & 0xffff0000u) : (d << 16)));
   }
-  if (VEC == 8 && op.vec)
+  if (VEC == 8 && (ALLVEC || op.vec))
     return f32x8{__uint_as_float(r.q.x), __uint_as_float(r.q.y), __uint_as_float(r.q.z),
                  __uint_as_float(r.q.w), __uint_as_float(r.q1.x), __uint_as_float(r.q1.y),
                  __uint_as_float(r.q1.z), __uint_as_float(r.q1.w)};
@@ -169,15 +170,40 @@ __device__ __forceinline__ float exp1(float x) {
   const float t = x * kL2E;
   float lo = __builtin_fmaf(x, kL2E, -t);
   lo = __builtin_fmaf(x, kL2ELo, lo);
-  lo = __builtin_fabsf(t) < 128.0f ? lo : 0.0f;  // false for inf / NaN
+  const bool fin = __builtin_fabsf(t) < 128.0f;  // false for inf / NaN / overflow
   const bool tiny = t < -125.0f;
   const float p = __builtin_amdgcn_exp2f(tiny ? t + 64.0f : t);
-  const float r = __builtin_fmaf(p, lo * kLn2, p);
+  // (no correction where p may be inf: inf * 0 would make a NaN)
+  const float r = fin ? __builtin_fmaf(p, lo * kLn2, p) : p;
   return tiny ? r * 5.42101086e-20f : r;  // 2^-64
 }
 
 __device__ __forceinline__ f32x8 vexp(f32x8 x) {
   return map8(x, [](float v) { return exp1(v); });
+}
+
+// The same function with the range handling hoisted out: when every lane's
+// 8 arguments satisfy |x log2 e| < 125 (no overflow, no subnormal result, no
+// inf / NaN) the wave takes the straight-line FMA-split path, which computes
+// exactly what exp1 computes for such arguments; otherwise it runs exp1.
+__device__ __forceinline__ f32x8 vexp_uniform(f32x8 x) {
+  constexpr float kL2E = 1.44269502e+00f;
+  constexpr float kL2ELo = 1.92596299e-08f;
+  constexpr float kLn2 = 6.93147182e-01f;
+  const f32x8 t = x * kL2E;
+  bool ok = true;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ok &= __builtin_fabsf(t[e]) < 125.0f;
+  if (!__all(ok)) return vexp(x);
+  f32x8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float lo = __builtin_fmaf(x[e], kL2E, -t[e]);
+    lo = __builtin_fmaf(x[e], kL2ELo, lo);
+    const float p = __builtin_amdgcn_exp2f(t[e]);
+    r[e] = __builtin_fmaf(p, lo * kLn2, p);
+  }
+  return r;
 }
 
 template <typename F>
@@ -390,6 +416,7 @@ void eltwise_kernel(const EltArgs args) {
     q1 = load_raw<VEC, BF16>(args.ops[1], p1);
     q2 = load_raw<VEC, BF16>(args.ops[2], p2);
     q3 = load_raw<VEC, BF16>(args.ops[3], p3);
+    asm volatile("" ::: "memory");  // all loads stay above the arithmetic
   }
   const f32x8 acc =
       run_program<VEC, PRELOAD, BF16, STACK, OFF32, FULL>(args, q0, q1, q2, q3, y, x);
@@ -434,7 +461,7 @@ __device__ __forceinline__ f32x8 chain_op(uint8_t code, f32x8 acc, f32x8 v) {
     case C_SUB: return acc - v;
     case C_RSUB: return v - acc;
     case C_MUL: return acc * v;
-    case C_EXP: return vexp(acc);
+    case C_EXP: return vexp_uniform(acc);
     case C_NEG: return -acc;
     case C_ABS: return map8(acc, [](float t) { return fabsf(t); });
     case C_RELU: return map8(acc, [](float t) { return t != t ? t : fmaxf(t, 0.0f); });
@@ -442,38 +469,66 @@ __device__ __forceinline__ f32x8 chain_op(uint8_t code, f32x8 acc, f32x8 v) {
   }
 }
 
-template <int N, bool BF16>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BF16 ? 8 : 6, BF16 ? 8 : 6)))
+// Each lane runs U chunks, 256 chunks apart (a wave's loads stay 1 KiB
+// contiguous per operand); every load of every chunk is issued before the
+// first arithmetic.  Lanes past the end clamp their chunk index for the loads
+// (an in-bounds re-read) and skip the store.
+#ifndef TTLH_CHAIN_U
+#define TTLH_CHAIN_U 1
+#endif
+constexpr int kChainU = TTLH_CHAIN_U;
+
+#ifndef TTLH_CHAIN_WAVES
+#define TTLH_CHAIN_WAVES 8
+#endif
+template <int N, bool BF16, bool ALLVEC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BF16 ? TTLH_CHAIN_WAVES : 6, BF16 ? TTLH_CHAIN_WAVES : 6)))
 void chain_kernel(const ChainArgs args) {
-  const uint32_t chunk = blockIdx.x * 256u + threadIdx.x;
-  if (chunk >= args.total) return;
-  const uint32_t yr = divide(chunk, args.magic, args.shift);
-  const uint32_t xr = chunk - yr * args.cpr;
-  const int64_t y = args.y0 + yr;
-  const int64_t x = args.x0 + static_cast<int64_t>(xr) * 8;
-  uintptr_t p[N];
+  constexpr int U = kChainU;
+  const uint32_t base = blockIdx.x * (256u * U) + threadIdx.x;
+  int64_t y[U], x[U];
+  Raw q[U][N];
 #pragma unroll
-  for (int k = 0; k < N; ++k) p[k] = operand_addr<true>(args.ops[k], y, x);
-  Raw q[N];
+  for (int j = 0; j < U; ++j) {
+    const uint32_t chunk = min(base + 256u * j, args.total - 1u);
+    const uint32_t yr = divide(chunk, args.magic, args.shift);
+    const uint32_t xr = chunk - yr * args.cpr;
+    y[j] = args.y0 + yr;
+    x[j] = args.x0 + static_cast<int64_t>(xr) * 8;
 #pragma unroll
-  for (int k = 0; k < N; ++k)
-    if (k == 0 || args.imm_src[k] == 0) q[k] = load_raw<8, BF16>(args.ops[k], p[k]);
-  f32x8 acc = to_f32<8, BF16>(args.ops[0], q[0]);
-#pragma unroll
-  for (int k = 1; k < N; ++k) {
-    f32x8 v = acc;
-    if (args.imm_src[k] == 0) v = to_f32<8, BF16>(args.ops[k], q[k]);
-    else if (args.imm_src[k] == 1) v = splat(args.imm[k]);
-    acc = chain_op(args.code[k], acc, v);
-    if (args.rnd[k] == TTLH_BF16) acc = round_bf16x8(acc);
+    for (int k = 0; k < N; ++k)
+      if (k == 0 || args.imm_src[k] == 0)
+        q[j][k] = load_raw<8, BF16>(args.ops[k], operand_addr<true>(args.ops[k], y[j], x[j]));
   }
-  store_chunk<8>(args, y, x, acc);
+  asm volatile("" ::: "memory");  // all loads stay above the arithmetic
+#pragma unroll
+  for (int j = 0; j < U; ++j) {
+    f32x8 acc = to_f32<8, BF16, ALLVEC>(args.ops[0], q[j][0]);
+#pragma unroll
+    for (int k = 1; k < N; ++k) {
+      f32x8 v = acc;
+      if (args.imm_src[k] == 0) v = to_f32<8, BF16, ALLVEC>(args.ops[k], q[j][k]);
+      else if (args.imm_src[k] == 1) v = splat(args.imm[k]);
+      acc = chain_op(args.code[k], acc, v);
+      // a bf16 rounding right before a bf16 store is the store's own RNE
+      const bool last_into_bf16 = k == N - 1 && args.out_dtype == TTLH_BF16;
+      if (args.rnd[k] == TTLH_BF16 && !last_into_bf16) acc = round_bf16x8(acc);
+    }
+    if (base + 256u * j < args.total) store_chunk<8>(args, y[j], x[j], acc);
+  }
 }
 
 template <int N, bool BF16>
 int launch_chain(const ChainArgs& a, hipStream_t s) {
-  const uint32_t blocks = (a.total + 255u) / 256u;
-  hipLaunchKernelGGL((chain_kernel<N, BF16>), dim3(blocks), dim3(256), 0, s, a);
+  const uint32_t per_block = 256u * kChainU;
+  const uint32_t blocks = (a.total + per_block - 1u) / per_block;
+  bool allvec = true;
+  for (int k = 0; k < N; ++k)
+    if (k == 0 || a.imm_src[k] == 0) allvec &= a.ops[k].vec != 0;
+  if (allvec)
+    hipLaunchKernelGGL((chain_kernel<N, BF16, true>), dim3(blocks), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((chain_kernel<N, BF16, false>), dim3(blocks), dim3(256), 0, s, a);
   return check_launch("chain_kernel");
 }
 
@@ -542,6 +597,138 @@ int dispatch_chain(const ChainArgs& c, int n, hipStream_t s) {
     case 5: return launch_chain<5, BF16>(c, s);
     default: return launch_chain<6, BF16>(c, s);
   }
+}
+
+// ---------------------------------------------------------------------------
+// Stream kernel: the chain kernel specialised for the common case — every
+// operand bf16 and 8-wide (unit column stride, 16-byte aligned rows), at most
+// 4 steps, 32-bit offsets, row indices and row strides below 2^24.  Which
+// steps read an operand is a compile-time mask, so the loads form one
+// straight block issued back to back; the grid is 2-D (lanes of a workgroup
+// cover 1 << lsh chunks of a row, 256 >> lsh rows), so no division; the
+// element offset of an operand is one 24-bit multiply-add.
+struct StreamOp {
+  const uint16_t* ptr;
+  uint32_t rs, rmask, roff, cmask, coff, pad;
+};
+struct StreamArgs {
+  StreamOp ops[4];
+  uint8_t code[4];
+  uint8_t rnd[4];
+  float imm[4];
+  void* out;
+  uint32_t out_ld, y0, x0, h, cpr, lsh;
+  int32_t out_dtype;
+};
+
+__device__ __forceinline__ f32x8 unpack_bf16x8(const u32x4 q) {
+  return f32x8{__uint_as_float(q.x << 16), __uint_as_float(q.x & 0xffff0000u),
+               __uint_as_float(q.y << 16), __uint_as_float(q.y & 0xffff0000u),
+               __uint_as_float(q.z << 16), __uint_as_float(q.z & 0xffff0000u),
+               __uint_as_float(q.w << 16), __uint_as_float(q.w & 0xffff0000u)};
+}
+
+template <int N, unsigned MASK>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8)))
+void stream_kernel(const StreamArgs a) {
+  const uint32_t t = threadIdx.x;
+  uint32_t yr = blockIdx.y * (256u >> a.lsh) + (t >> a.lsh);
+  uint32_t cr = (blockIdx.x << a.lsh) + (t & ((1u << a.lsh) - 1u));
+  const bool live = yr < a.h && cr < a.cpr;
+  yr = min(yr, a.h - 1u);  // dead lanes re-read an in-bounds chunk and store nothing
+  cr = min(cr, a.cpr - 1u);
+  const uint32_t y = a.y0 + yr;
+  const uint32_t x = a.x0 + cr * 8u;
+  u32x4 q[N];
+#pragma unroll
+  for (int k = 0; k < N; ++k)
+    if ((MASK >> k) & 1u) {
+      const StreamOp& o = a.ops[k];
+      const uint32_t e = __umul24((y & o.rmask) + o.roff, o.rs) + (x & o.cmask) + o.coff;
+      q[k] = *reinterpret_cast<gu32x4*>(reinterpret_cast<uintptr_t>(o.ptr + e));
+    }
+  // keep every load above this point: without it the compiler sinks a load
+  // to its first use, past the arithmetic of the earlier steps, and the wave
+  // then waits for memory twice
+  asm volatile("" ::: "memory");
+  f32x8 acc = unpack_bf16x8(q[0]);
+#pragma unroll
+  for (int k = 1; k < N; ++k) {
+    const f32x8 v = ((MASK >> k) & 1u) ? unpack_bf16x8(q[k]) : splat(a.imm[k]);
+    acc = chain_op(a.code[k], acc, v);
+    const bool last_into_bf16 = k == N - 1 && a.out_dtype == TTLH_BF16;
+    if (a.rnd[k] == TTLH_BF16 && !last_into_bf16) acc = round_bf16x8(acc);
+  }
+  if (!live) return;
+  const uint32_t off = y * a.out_ld + x;
+  if (a.out_dtype == TTLH_BF16) {
+    u32x4 r;
+    r.x = cvt_pk_bf16(acc[0], acc[1]);
+    r.y = cvt_pk_bf16(acc[2], acc[3]);
+    r.z = cvt_pk_bf16(acc[4], acc[5]);
+    r.w = cvt_pk_bf16(acc[6], acc[7]);
+    __builtin_nontemporal_store(r, reinterpret_cast<u32x4*>(static_cast<uint16_t*>(a.out) + off));
+  } else {
+    float* p = static_cast<float*>(a.out) + off;
+    __builtin_nontemporal_store(f32x4{acc[0], acc[1], acc[2], acc[3]}, reinterpret_cast<f32x4*>(p));
+    __builtin_nontemporal_store(f32x4{acc[4], acc[5], acc[6], acc[7]},
+                                reinterpret_cast<f32x4*>(p + 4));
+  }
+}
+
+// Launches the stream kernel when `c` qualifies (see above); returns false
+// to let the caller fall back to the chain kernel.
+bool try_stream(const ChainArgs& c, int n, hipStream_t s, int* status) {
+  if (n > 4 || c.out_ld >= (int64_t(1) << 31)) return false;
+  StreamArgs a{};
+  unsigned mask = 0;
+  for (int k = 0; k < n; ++k) {
+    const bool reads = k == 0 || c.imm_src[k] == 0;
+    if (reads) {
+      const EltOperand& o = c.ops[k];
+      if (o.dtype != TTLH_BF16 || !o.vec || o.rs >= (int64_t(1) << 24)) return false;
+      const int64_t ymax = o.rmask == -1 ? c.y0 + int64_t(c.total / c.cpr) - 1 + o.roff : 31 + o.roff;
+      if (ymax >= (int64_t(1) << 24)) return false;
+      mask |= 1u << k;
+      a.ops[k] = StreamOp{static_cast<const uint16_t*>(o.ptr), static_cast<uint32_t>(o.rs),
+                          static_cast<uint32_t>(o.rmask), static_cast<uint32_t>(o.roff),
+                          static_cast<uint32_t>(o.cmask), static_cast<uint32_t>(o.coff), 0};
+    }
+    a.code[k] = c.code[k];
+    a.rnd[k] = c.rnd[k];
+    a.imm[k] = c.imm[k];
+  }
+  const uint32_t h = c.total / c.cpr;
+  uint32_t lsh = 0;
+  while (lsh < 8 && (1u << lsh) < c.cpr) ++lsh;
+  const uint32_t gx = (c.cpr + (1u << lsh) - 1u) >> lsh;
+  const uint32_t rpb = 256u >> lsh;
+  const uint32_t gy = (h + rpb - 1u) / rpb;
+  if (gy > 65535u) return false;
+  a.out = c.out;
+  a.out_ld = static_cast<uint32_t>(c.out_ld);
+  a.y0 = static_cast<uint32_t>(c.y0);
+  a.x0 = static_cast<uint32_t>(c.x0);
+  a.h = h;
+  a.cpr = c.cpr;
+  a.lsh = lsh;
+  a.out_dtype = c.out_dtype;
+  const dim3 grid(gx, gy), block(256);
+#define TTLH_STREAM_CASE(NN, MM)                                                   \
+  case (NN << 4) | MM:                                                              \
+    hipLaunchKernelGGL((stream_kernel<NN, MM>), grid, block, 0, s, a);             \
+    break;
+  switch ((n << 4) | mask) {
+    TTLH_STREAM_CASE(1, 1)
+    TTLH_STREAM_CASE(2, 1) TTLH_STREAM_CASE(2, 3)
+    TTLH_STREAM_CASE(3, 1) TTLH_STREAM_CASE(3, 3) TTLH_STREAM_CASE(3, 5) TTLH_STREAM_CASE(3, 7)
+    TTLH_STREAM_CASE(4, 1) TTLH_STREAM_CASE(4, 3) TTLH_STREAM_CASE(4, 5) TTLH_STREAM_CASE(4, 7)
+    TTLH_STREAM_CASE(4, 9) TTLH_STREAM_CASE(4, 11) TTLH_STREAM_CASE(4, 13) TTLH_STREAM_CASE(4, 15)
+    default: return false;
+  }
+#undef TTLH_STREAM_CASE
+  *status = check_launch("stream_kernel");
+  return true;
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -695,8 +882,11 @@ extern "C" int ttlh_eltwise(const ttlh_instr* prog, const ttlh_operand* in, int 
                          : launch<1, false, false, true, false, true>(a, s);
   if (!vec) return launch<1, false, false, true, true, true>(a, s);
   ChainArgs chain;
-  if (make_chain(prog, n_instr, a, &chain))
+  if (make_chain(prog, n_instr, a, &chain)) {
+    int status = TTLH_OK;
+    if (all_bf16 && try_stream(chain, n_instr, s, &status)) return status;
     return all_bf16 ? dispatch_chain<true>(chain, n_instr, s) : dispatch_chain<false>(chain, n_instr, s);
+  }
   if (!preload) return launch<8, false, false, true, true, true>(a, s);
   if (full) return launch<8, true, false, true, true, true>(a, s);
   // common ops, 8-wide, preloaded
