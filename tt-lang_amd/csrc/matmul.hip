@@ -97,8 +97,10 @@ __device__ __forceinline__ void load_stage(const MmArgs& p, int bm, int bn, int 
                  ? *reinterpret_cast<gu32x4*>(reinterpret_cast<uintptr_t>(p.A + static_cast<int64_t>(gr) * p.lda + gk))
                  : zero4();
   }
-  const int kq = (t >> 4) * 4;  // 0..60
-  const int n8 = (t & 15) * 8;  // 0..120
+  // lanes 16 apart share an n column group; the 16 lanes of a group take the
+  // 16 k quads, so their 8-byte transposed LDS stores cover all 32 banks
+  const int kq = (t & 15) * 4;  // 0..60
+  const int n8 = (t >> 4) * 8;  // 0..120
   const int gn = bn * BN + n8;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -139,8 +141,8 @@ __device__ __forceinline__ void store_stage(Stage& s, uint16_t* As, uint16_t* Bt
     const int r = c >> 3, kc = (c & 7) * 8;
     *reinterpret_cast<u32x4*>(As + r * LDP + kc) = s.a[i];
   }
-  const int kq = (t >> 4) * 4;
-  const int n8 = (t & 15) * 8;
+  const int kq = (t & 15) * 4;
+  const int n8 = (t >> 4) * 8;
   // b[i] = row k = kq + i, 8 values n8..n8+7 (2 per dword)
 #pragma unroll
   for (int j = 0; j < 8; ++j) {

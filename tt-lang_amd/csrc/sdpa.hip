@@ -73,10 +73,13 @@ __device__ __forceinline__ void load_kv(const SdpaArgs& p, int64_t base, int kv0
     st.k[i] = *reinterpret_cast<gu32x4*>(
         reinterpret_cast<uintptr_t>(p.K + base + static_cast<int64_t>(kv0 + r) * D + dc));
   }
-  // V: thread -> (kv quad, d octet); D/8 octets per row, 16 quads per 64 rows
+  // V: thread -> (kv group, d octet).  Consecutive lanes take consecutive kv
+  // groups of one octet, so the transposed LDS stores of 16 lanes are one
+  // contiguous 128-byte run (all 32 banks).
   constexpr int kOct = D / 8;
-  const int oct = t % kOct, quad = t / kOct;  // quad < 256 / kOct
   constexpr int kRowsPerThread = BKV * kOct / kThreads;  // 4 for D = 128, 2 for D = 64
+  constexpr int kGroups = BKV / kRowsPerThread;           // 16 for D = 128, 32 for D = 64
+  const int quad = t % kGroups, oct = t / kGroups;
 #pragma unroll
   for (int i = 0; i < kRowsPerThread; ++i) {
     const int r = quad * kRowsPerThread + i;
@@ -87,7 +90,7 @@ __device__ __forceinline__ void load_kv(const SdpaArgs& p, int64_t base, int kv0
 
 template <int D>
 __device__ __forceinline__ void store_kv(const KvStage<D>& st, uint16_t* Ks, uint16_t* Vts) {
-  constexpr int KP = D + 8, VP = BKV + 8;
+  constexpr int KP = D + 8, VP = BKV + 4;
   const int t = threadIdx.x;
   constexpr int kChunksPerRow = D / 8;
 #pragma unroll
@@ -97,8 +100,9 @@ __device__ __forceinline__ void store_kv(const KvStage<D>& st, uint16_t* Ks, uin
     *reinterpret_cast<u32x4*>(Ks + r * KP + dc) = st.k[i];
   }
   constexpr int kOct = D / 8;
-  const int oct = t % kOct, quad = t / kOct;
   constexpr int kRowsPerThread = BKV * kOct / kThreads;
+  constexpr int kGroups = BKV / kRowsPerThread;
+  const int quad = t % kGroups, oct = t / kGroups;
   // transpose: rows kv = quad*R + i, cols d = oct*8 + j  ->  Vt[d][kv]
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
@@ -131,7 +135,7 @@ __device__ __forceinline__ void block_coords(const SdpaArgs& p, int& bh, int& qb
 
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(const SdpaArgs p) {
-  constexpr int KP = D + 8, VP = BKV + 8;
+  constexpr int KP = D + 8, VP = BKV + 4;
   constexpr int ND = D / 32;   // d tiles of O^T
   constexpr int NDC = D / 16;  // 16-wide d chunks of the S^T contraction
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BKV * KP];
