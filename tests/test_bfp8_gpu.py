@@ -73,3 +73,22 @@ def test_matmul_bfp8w_config4_sampled():
     err = (c.cpu()[rows].double() - exact).abs()
     bound = exact.abs() * 2.0 ** -8 + 1e-6 * 64 * float(exact.abs().max())
     assert bool((err <= bound).all()), float(err.max())
+
+
+def test_matmul_bfp8w_large_block_ragged():
+    # >= 192 output blocks of 256x256 -> the large-block kernel; M, N ragged
+    # against 256 and K against its 64-deep staging step
+    from ttlhip import kernels as Kn
+    M, K, N = 2080, 544, 5408
+    a = O.seeded((M, K), "normal", 9)
+    w = O.seeded((K, N), "normal", 10, torch.float32, std=0.02)
+    q = OB.pack_c(w)
+    c = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    Kn.matmul_bfp8w(a.cuda(), q.cuda(), c)
+    torch.cuda.synchronize()
+    rows = torch.cat([torch.arange(0, M, 41), torch.arange(M - 32, M)])
+    wd = OB.unpack_c(q, K, N).double()
+    exact = a[rows].double() @ wd
+    err = (c.cpu()[rows].double() - exact).abs()
+    bound = exact.abs() * 2.0 ** -8 + 1e-6 * math.sqrt(K) * float(exact.abs().max())
+    assert bool((err <= bound).all()), float(err.max())

@@ -93,3 +93,41 @@ def test_bf16_matmul_4096_sampled_rows():
     err = (got[rows] - exact).abs()
     bound = exact.abs() * 2.0 ** -8 + 1e-6 * math.sqrt(K) * float(exact.abs().max())
     assert bool((err <= bound).all()), f"max err {float(err.max())}"
+
+
+# Problems with >= 192 output blocks of 256x256 take the large-block kernel
+# (mm256_kernel); the shapes below are ragged on purpose: M and N not
+# multiples of 256, K not a multiple of its 64-deep staging step.
+
+def test_bf16_large_block_kernel_ragged_sampled():
+    M, K, N = 4000, 1056, 3104  # 16 x 13 = 208 blocks
+    a, b = _inputs(M, K, N, 41)
+    got = _mm(a, b, torch.bfloat16).double()
+    rows = torch.cat([torch.arange(0, M, 37), torch.arange(M - 40, M)])
+    exact = a[rows].double() @ b.double()
+    err = (got[rows] - exact).abs()
+    bound = exact.abs() * 2.0 ** -8 + 1e-6 * math.sqrt(K) * float(exact.abs().max())
+    assert bool((err <= bound).all()), f"max err {float(err.max())}"
+    sim_rows = O.tile_matmul_sim(a[-32:], b).double()  # last tile row through the simulator rule
+    assert float((got[-32:] - exact[-32:]).abs().max()) <= float((sim_rows - exact[-32:]).abs().max()) + 1e-12
+
+
+def test_bf16_large_block_kernel_layout_known_answer():
+    # permutation rows x small integers: every output is exact, so any
+    # fragment / accumulator layout mistake in the 256x256 kernel is visible
+    M = K = N = 3584  # 14 x 14 = 196 blocks
+    perm = torch.randperm(K, generator=torch.Generator().manual_seed(5))
+    a = torch.zeros(M, K, dtype=torch.bfloat16)
+    a[torch.arange(M), perm] = 1.0
+    b = (torch.arange(K * N).reshape(K, N) % 251).to(torch.bfloat16)
+    got = _mm(a, b, torch.float32)
+    assert torch.equal(got, b[perm].float())
+
+
+def test_bf16_large_block_kernel_accumulate_f32():
+    M, K, N = 3584, 96, 3616  # 14 x 15 = 210 blocks, K shorter than one 64-step pair
+    a, b = _inputs(M, K, N, 43)
+    c0 = O.seeded((M, N), "normal", 44, torch.float32)
+    got = _mm(a, b, torch.float32, accumulate=True, c0=c0).double()
+    exact = O.matmul_fp64(a, b) + c0.double()
+    torch.testing.assert_close(got, exact, rtol=1e-5, atol=1e-5)

@@ -26,6 +26,9 @@
 //  - the epilogue rounds once to the output dtype (RNE).
 // fp32 inputs take a simpler v_mfma_f32_32x32x2f32 kernel (64x64 blocks).
 
+#include <atomic>
+#include <type_traits>
+
 #include "ttlh_bfp8.h"
 #include "ttlh_common.h"
 
@@ -234,6 +237,531 @@ __global__ __launch_bounds__(kThreads, 2) void mm_bf16_kernel(const MmArgs p) {
 }
 
 // ---------------------------------------------------------------------------
+// Large-problem kernel: 256x256 output block per workgroup, four waves each
+// owning a 128x128 quadrant (4x4 MFMA tiles, 256 fp32 accumulators per lane,
+// which the compiler places in the accumulation registers; one wave per
+// SIMD).  A wave re-uses every A fragment 4 times and every B fragment 4
+// times, which halves the LDS read traffic per MFMA of the 128x128 kernel:
+// per 64-k step a CU reads 128 KB and writes 64 KB of LDS for 256 MFMAs.
+// Staging per 64-k step: A = 256 rows x 64 k (8 chunks of 8 per thread,
+// stored as loaded); B = 64 k x 256 n, each thread an 8 (k) x 8 (n) block
+// transposed in registers (v_perm_b32) to 8 Bt rows of 8 k (one 16-byte LDS
+// store each).  With one wave per SIMD nothing else hides a stall, so the
+// steady-state 64-k step is a single basic block in which every LDS store,
+// global load and transpose is interleaved between MFMAs, and the fragments
+// of the next 16-k substep are read while the current substep's MFMAs run.
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (N > 0) {
+    static_for<N - 1>(f);
+    f(std::integral_constant<int, N - 1>());
+  }
+}
+
+// Writes one 32x32 accumulator tile at (r0, c0): the lane holds column
+// c0 + lane % 32, rows r0 + 8 (r / 4) + 4 (lane / 32) + r % 4.
+__device__ __forceinline__ void store_acc_tile(const MmArgs& p, const f32x16& t, int r0, int c0,
+                                               int lane) {
+  const int gc = c0 + (lane & 31);
+  if (gc >= p.N) return;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int gr = r0 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+    if (gr >= p.M) continue;
+    const int64_t off = static_cast<int64_t>(gr) * p.ldc + gc;
+    float v = t[r];
+    if (p.c_dtype == TTLH_BF16) {
+      uint16_t* c = static_cast<uint16_t*>(p.C) + off;
+      if (p.accumulate) v += bf16_to_f32(*c);
+      *c = f32_to_bf16(v);
+    } else {
+      float* c = static_cast<float*>(p.C) + off;
+      if (p.accumulate) v += *c;
+      *c = v;
+    }
+  }
+}
+
+// Writes one 32x32 accumulator tile lying wholly inside C, two columns per
+// store.  Lanes 2c and 2c + 1 hold columns 2c and 2c + 1 of the same 16
+// rows; DPP swaps of each row pair give the even lane rows 8 (r / 4) +
+// 4 (lane / 32) + r % 4 for even r and the odd lane those for odd r, both as
+// (column 2c, column 2c + 1) pairs: 8 packed stores per lane instead of 16
+// 2-byte ones.  Offsets are 32-bit (the launcher checks M * ldc < 2^31).
+template <bool BF16OUT, bool ACC>
+__device__ __forceinline__ void store_acc_tile_pairs(const MmArgs& p, const f32x16& t, int r0,
+                                                     int c0, int lane) {
+  const bool odd = lane & 1;
+  const int col = c0 + ((lane & 31) & ~1);
+  const int rbase = r0 + 4 * (lane >> 5) + (odd ? 1 : 0);
+  static_for<8>([&](auto mm) {
+    constexpr int m = decltype(mm)::value;
+    // quad_perm [1, 0, 3, 2]: the neighbouring lane's value (selecting on
+    // the DPP results, not on t's index, keeps t's elements in registers)
+    const float e0 = t[2 * m], e1 = t[2 * m + 1];
+    const float n0 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(e0), 0xB1, 0xF, 0xF, false));
+    const float n1 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(e1), 0xB1, 0xF, 0xF, false));
+    const float lo = odd ? n1 : e0;  // column 2c
+    const float hi = odd ? e1 : n0;  // column 2c + 1
+    const int row = rbase + 8 * (m >> 1) + 2 * (m & 1);
+    const uint32_t off = static_cast<uint32_t>(row) * static_cast<uint32_t>(p.ldc) +
+                         static_cast<uint32_t>(col);
+    if constexpr (BF16OUT) {
+      uint32_t* c = reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p.C) + off);
+      float a = lo, b = hi;
+      if constexpr (ACC) {
+        const uint32_t old = *c;
+        a += __uint_as_float(old << 16);
+        b += __uint_as_float(old & 0xffff0000u);
+      }
+      *c = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(a))) |
+           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(b))) << 16);
+    } else {
+      typedef float f32x2 __attribute__((ext_vector_type(2)));
+      f32x2* c = reinterpret_cast<f32x2*>(static_cast<float*>(p.C) + off);
+      f32x2 v = {lo, hi};
+      if constexpr (ACC) v += *c;
+      *c = v;
+    }
+  });
+}
+
+constexpr int LM = 256, LN = 256, LK = 64, LP = LK + 8;
+
+// Per-thread staging geometry of the 256x256 kernel.  A: chunks of 8 k at
+// rows ar0 + 32 i (i < 8), k offset akc.  B: an 8 (k) x 8 (n) block at k rows
+// kb + i, columns n8..n8+7.  Rows past M and columns past N are clamped to the
+// last valid one: they only feed output rows / columns that are never stored.
+struct Stage2 {
+  u32x4 a[8];
+  u32x4 b[8];
+  uint64_t bq[8];  // bfloat8_b: 8 element bytes of each of the 8 k rows
+  uint64_t be;     // and the 8 rows' shared exponents (consecutive bytes)
+};
+
+struct Geo2 {
+  const uint16_t* a_row[8];  // A + row * lda + akc, per chunk
+  int akc, kb, gn;           // gn: first staged column (clamped)
+  int64_t b_col;             // bf16 B: element offset of (k = kb, column gn)
+};
+
+template <bool BQ>
+__device__ __forceinline__ Geo2 make_geo2(const MmArgs& p, int bm, int bn) {
+  const int t = threadIdx.x;
+  Geo2 g;
+  g.akc = (t & 7) * 8;
+  g.kb = (t & 7) * 8;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int row = min(bm * LM + (t >> 3) + 32 * i, p.M - 1);
+    g.a_row[i] = p.A + static_cast<int64_t>(row) * p.lda + g.akc;
+  }
+  g.gn = min(bn * LN + (t >> 3) * 8, p.N - 8);
+  g.b_col = static_cast<int64_t>(g.kb) * p.ldb + g.gn;
+  return g;
+}
+
+// FULL: the whole 64-k step lies inside K (no k bounds checks, no branches);
+// otherwise k rows at or past K read as zero (K % 64 == 32 tail step).
+template <bool BQ, bool FULL>
+__device__ __forceinline__ void load_a2(const MmArgs& p, const Geo2& g, int k0, Stage2& s) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    if (FULL || k0 + g.akc < p.K)
+      s.a[i] = *reinterpret_cast<gu32x4*>(reinterpret_cast<uintptr_t>(g.a_row[i] + k0));
+    else
+      s.a[i] = zero4();
+  }
+}
+
+template <bool BQ, bool FULL>
+__device__ __forceinline__ void load_b2(const MmArgs& p, const Geo2& g, int k0, Stage2& s) {
+  if constexpr (BQ) {
+    // the 8 k rows kb..kb+7 share a face (kb is a multiple of 8): their
+    // exponents are 8 consecutive bytes and their element bytes 16 apart
+    const int gk = k0 + g.kb;
+    const int64_t tile = static_cast<int64_t>(gk >> 5) * p.bq_tiles_n + (g.gn >> 5);
+    const uint8_t* t8 = p.Bq + tile * TTLH_BFP8_TILE_BYTES;
+    const int r = gk & 31, c = g.gn & 31;
+    const int f = ((r >> 4) << 1) | (c >> 4);
+    const uint8_t* el = t8 + 64 + 256 * f + 16 * (r & 15) + (c & 15);
+    if (FULL || gk < p.K) {
+      s.be = *reinterpret_cast<const uint64_t*>(t8 + 16 * f + (r & 15));
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s.bq[i] = *reinterpret_cast<const uint64_t*>(el + 16 * i);
+    } else {
+      s.be = 0ull;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s.bq[i] = 0ull;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (FULL || k0 + g.kb + i < p.K)
+        s.b[i] = *reinterpret_cast<gu32x4*>(reinterpret_cast<uintptr_t>(
+            p.B + g.b_col + static_cast<int64_t>(k0 + i) * p.ldb));
+      else
+        s.b[i] = zero4();
+    }
+  }
+}
+
+// lo16(x) | lo16(y) << 16 and hi16(x) | hi16(y) << 16
+__device__ __forceinline__ uint32_t pack_lo(uint32_t x, uint32_t y) {
+  return __builtin_amdgcn_perm(y, x, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t pack_hi(uint32_t x, uint32_t y) {
+  return __builtin_amdgcn_perm(y, x, 0x07060302u);
+}
+
+__device__ __forceinline__ void store_a2(const Stage2& s, uint16_t* As) {
+  const int t = threadIdx.x;
+  uint16_t* d = As + (t >> 3) * LP + (t & 7) * 8;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4*>(d + i * 32 * LP) = s.a[i];
+}
+
+// b[i] = k row kb + i, columns n8..n8+7 (dword d = columns 2d, 2d + 1);
+// Bt row n8 + j receives the 8 k values of column j
+template <bool BQ>
+__device__ __forceinline__ void store_b2(Stage2& s, uint16_t* Bts) {
+  const int t = threadIdx.x;
+  if constexpr (BQ) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s.b[i] = bfp8_decode8(s.bq[i], static_cast<uint8_t>(s.be >> (8 * i)));
+  }
+  uint16_t* d = Bts + ((t >> 3) * 8) * LP + (t & 7) * 8;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int w = j >> 1;
+    u32x4 v;
+    if (j & 1) {
+      v.x = pack_hi(s.b[0][w], s.b[1][w]);
+      v.y = pack_hi(s.b[2][w], s.b[3][w]);
+      v.z = pack_hi(s.b[4][w], s.b[5][w]);
+      v.w = pack_hi(s.b[6][w], s.b[7][w]);
+    } else {
+      v.x = pack_lo(s.b[0][w], s.b[1][w]);
+      v.y = pack_lo(s.b[2][w], s.b[3][w]);
+      v.z = pack_lo(s.b[4][w], s.b[5][w]);
+      v.w = pack_lo(s.b[6][w], s.b[7][w]);
+    }
+    *reinterpret_cast<u32x4*>(d + j * LP) = v;
+  }
+}
+
+__device__ __forceinline__ void block_coords2(const MmArgs& a, int& bm, int& bn) {
+  const int nblk = a.grid_m * a.grid_n;
+  int id = blockIdx.x;
+  constexpr int kXcd = 8;
+  if (nblk % kXcd == 0) {
+    const int per = nblk / kXcd;
+    id = (id % kXcd) * per + id / kXcd;
+  }
+  constexpr int kBand = 4;
+  const int band_size = kBand * a.grid_n;
+  const int band = id / band_size;
+  const int in_band = id - band * band_size;
+  const int rows = min(kBand, a.grid_m - band * kBand);
+  bm = band * kBand + in_band % rows;
+  bn = in_band / rows;
+}
+
+struct Frags {
+  bf16x8 a[4], b[4];
+};
+
+__device__ __forceinline__ void read_frags(const uint16_t* As, const uint16_t* Bts, int fa_off,
+                                           int fb_off, int kk, Frags& f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f.a[i] = *reinterpret_cast<const bf16x8*>(As + fa_off + i * 32 * LP + kk);
+    f.b[i] = *reinterpret_cast<const bf16x8*>(Bts + fb_off + i * 32 * LP + kk);
+  }
+}
+
+__device__ __forceinline__ void mfma16(const Frags& f, f32x16 (&acc)[4][4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+}
+
+// scheduling-group masks (LLVM AMDGPU): MFMA, VALU, VMEM read, DS read, DS write
+constexpr int kSgMfma = 0x008, kSgValu = 0x002, kSgVmemRd = 0x020, kSgDsRd = 0x100,
+              kSgDsWr = 0x200;
+#define TTLH_SG(mask, n) __builtin_amdgcn_sched_group_barrier((mask), (n), 0)
+
+// Single-instruction pieces of a 64-k step, so a substep can be written as
+// an explicit sequence: MFMA, then the memory / transpose work that issues
+// while it executes.
+__device__ __forceinline__ void mfma_one(const Frags& f, f32x16 (&acc)[4][4], int q) {
+  acc[q >> 2][q & 3] =
+      __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[q >> 2], f.b[q & 3], acc[q >> 2][q & 3], 0, 0, 0);
+}
+__device__ __forceinline__ void read_one(const uint16_t* As, const uint16_t* Bts, int fa_off,
+                                         int fb_off, int kk, Frags& f, int q) {
+  if (q < 4) f.a[q] = *reinterpret_cast<const bf16x8*>(As + fa_off + q * 32 * LP + kk);
+  else f.b[q - 4] = *reinterpret_cast<const bf16x8*>(Bts + fb_off + (q - 4) * 32 * LP + kk);
+}
+__device__ __forceinline__ void store_a_one(const Stage2& s, uint16_t* As, int i) {
+  const int t = threadIdx.x;
+  *reinterpret_cast<u32x4*>(As + (t >> 3) * LP + (t & 7) * 8 + i * 32 * LP) = s.a[i];
+}
+// Bt row n8 + j <- the 8 k values of staged column j (b[i] = k row kb + i)
+__device__ __forceinline__ void store_b_one(const Stage2& s, uint16_t* Bts, int j) {
+  const int t = threadIdx.x;
+  const int w = j >> 1;
+  u32x4 v;
+  if (j & 1) {
+    v.x = pack_hi(s.b[0][w], s.b[1][w]);
+    v.y = pack_hi(s.b[2][w], s.b[3][w]);
+    v.z = pack_hi(s.b[4][w], s.b[5][w]);
+    v.w = pack_hi(s.b[6][w], s.b[7][w]);
+  } else {
+    v.x = pack_lo(s.b[0][w], s.b[1][w]);
+    v.y = pack_lo(s.b[2][w], s.b[3][w]);
+    v.z = pack_lo(s.b[4][w], s.b[5][w]);
+    v.w = pack_lo(s.b[6][w], s.b[7][w]);
+  }
+  *reinterpret_cast<u32x4*>(Bts + ((t >> 3) * 8 + j) * LP + (t & 7) * 8) = v;
+}
+__device__ __forceinline__ void load_a_one(const Geo2& g, int k0, Stage2& s, int i) {
+  s.a[i] = *reinterpret_cast<gu32x4*>(reinterpret_cast<uintptr_t>(g.a_row[i] + k0));
+}
+template <bool BQ>
+__device__ __forceinline__ void load_b_one(const MmArgs& p, const Geo2& g, int k0, Stage2& s,
+                                           int i) {
+  if constexpr (BQ) {
+    const int gk = k0 + g.kb;
+    const int64_t tile = static_cast<int64_t>(gk >> 5) * p.bq_tiles_n + (g.gn >> 5);
+    const uint8_t* t8 = p.Bq + tile * TTLH_BFP8_TILE_BYTES;
+    const int r = gk & 31, c = g.gn & 31;
+    const int f = ((r >> 4) << 1) | (c >> 4);
+    if (i == 0) s.be = *reinterpret_cast<const uint64_t*>(t8 + 16 * f + (r & 15));
+    s.bq[i] = *reinterpret_cast<const uint64_t*>(t8 + 64 + 256 * f + 16 * (r & 15) + (c & 15) + 16 * i);
+  } else {
+    s.b[i] = *reinterpret_cast<gu32x4*>(reinterpret_cast<uintptr_t>(
+        p.B + g.b_col + static_cast<int64_t>(k0 + i) * p.ldb));
+  }
+}
+
+#define TTLH_FENCE() __builtin_amdgcn_sched_barrier(0)
+
+// One 64-k step in four 16-k substeps.  Buffer X (= ks & 1) holds step ks,
+// whose substep-0 fragments are already in f0; Y (the other) receives step
+// ks + 1 from the staging registers, which then fetch step ks + 2.
+//   s0: MFMAs(f0) | read X s1 fragments, store A -> Y, transpose + store B -> Y
+//       (bfloat8_b: dequantise B first)
+//   s1: MFMAs(f1) | read X s2 fragments, load A and B of step ks + 2
+//   barrier (Y complete)
+//   s2: MFMAs(f0) | read X s3 fragments
+//   s3: MFMAs(f1) | read Y s0 fragments of step ks + 1
+//   barrier (X no longer read: step ks + 1 may overwrite it)
+// With one wave per SIMD nothing else hides a stall, so the STEADY form
+// (steps ks + 1 and ks + 2 exist and are full: one basic block) is written as
+// an explicit instruction sequence, fenced against reordering, with the
+// memory and transpose work after each MFMA, where it issues while the MFMA
+// executes.  Edge steps run the same work without the interleave.
+template <bool BQ, bool STEADY>
+__device__ __forceinline__ void k_step(const MmArgs& p, const Geo2& g, uint16_t* lds, int ks,
+                                       int nk, int nfull, int fa_off, int fb_off, Frags& f0,
+                                       f32x16 (&acc)[4][4], Stage2& st) {
+  constexpr int kBuf = 2 * LM * LP;
+  const uint16_t* As = lds + (ks & 1) * kBuf;
+  const uint16_t* Bts = As + LM * LP;
+  uint16_t* nA = lds + ((ks + 1) & 1) * kBuf;
+  uint16_t* nB = nA + LM * LP;
+  const int k2 = (ks + 2) * LK;
+  Frags f1;
+  if constexpr (STEADY) {
+    // s0
+    if constexpr (BQ) {
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        mfma_one(f0, acc, q);
+        if (q < 8) {
+          read_one(As, Bts, fa_off, fb_off, 16, f1, q);
+          st.b[q] = bfp8_decode8(st.bq[q], static_cast<uint8_t>(st.be >> (8 * q)));
+        } else {
+          store_a_one(st, nA, q - 8);
+          store_b_one(st, nB, q - 8);
+        }
+        TTLH_FENCE();
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        mfma_one(f0, acc, q);
+        if (q < 8) {
+          read_one(As, Bts, fa_off, fb_off, 16, f1, q);
+          store_a_one(st, nA, q);
+        } else {
+          store_b_one(st, nB, q - 8);
+        }
+        TTLH_FENCE();
+      }
+    }
+    // s1 (bf16: A loads first, in the order s0 stores them, so each store
+    // waits only for its own load; bfloat8_b: B first, dequantised first)
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      mfma_one(f1, acc, q);
+      if (q < 8) {
+        read_one(As, Bts, fa_off, fb_off, 32, f0, q);
+        if (BQ) load_b_one<BQ>(p, g, k2, st, q);
+        else load_a_one(g, k2, st, q);
+      } else {
+        if (BQ) load_a_one(g, k2, st, q - 8);
+        else load_b_one<BQ>(p, g, k2, st, q - 8);
+      }
+      TTLH_FENCE();
+    }
+    __syncthreads();
+    // s2
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      mfma_one(f0, acc, q);
+      if (q < 8) read_one(As, Bts, fa_off, fb_off, 48, f1, q);
+      TTLH_FENCE();
+    }
+    // s3
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      mfma_one(f1, acc, q);
+      if (q < 8) read_one(nA, nB, fa_off, fb_off, 0, f0, q);
+      TTLH_FENCE();
+    }
+    __syncthreads();
+  } else {
+    const bool has1 = ks + 1 < nk;
+    const bool has2 = ks + 2 < nk;
+    read_frags(As, Bts, fa_off, fb_off, 16, f1);
+    if (has1) {
+      store_a2(st, nA);
+      store_b2<BQ>(st, nB);
+    }
+    mfma16(f0, acc);
+    read_frags(As, Bts, fa_off, fb_off, 32, f0);
+    if (has2) {
+      load_a2<BQ, false>(p, g, k2, st);
+      load_b2<BQ, false>(p, g, k2, st);
+    }
+    mfma16(f1, acc);
+    __syncthreads();
+    read_frags(As, Bts, fa_off, fb_off, 48, f1);
+    mfma16(f0, acc);
+    if (has1) read_frags(nA, nB, fa_off, fb_off, 0, f0);
+    mfma16(f1, acc);
+    __syncthreads();
+  }
+}
+
+template <bool BQ, bool OUT_BF16, bool ACC>
+__global__ __launch_bounds__(kThreads, 1) void mm256_kernel(const MmArgs p) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t lds2[];  // [2][A | Bt][256 * LP]
+  int bm, bn;
+  block_coords2(p, bm, bn);
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = (wave >> 1) * 128;
+  const int wn = (wave & 1) * 128;
+  const int fa_off = (wm + (lane & 31)) * LP + (lane >> 5) * 8;
+  const int fb_off = (wn + (lane & 31)) * LP + (lane >> 5) * 8;
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const Geo2 g = make_geo2<BQ>(p, bm, bn);
+  const int nfull = p.K / LK;
+  const int nk = (p.K + LK - 1) / LK;
+  Stage2 st;
+  if (nfull > 0) {
+    load_a2<BQ, true>(p, g, 0, st);
+    load_b2<BQ, true>(p, g, 0, st);
+  } else {
+    load_a2<BQ, false>(p, g, 0, st);
+    load_b2<BQ, false>(p, g, 0, st);
+  }
+  store_a2(st, lds2);
+  store_b2<BQ>(st, lds2 + LM * LP);
+  if (nk > 1) {
+    if (nfull > 1) {
+      load_a2<BQ, true>(p, g, LK, st);
+      load_b2<BQ, true>(p, g, LK, st);
+    } else {
+      load_a2<BQ, false>(p, g, LK, st);
+      load_b2<BQ, false>(p, g, LK, st);
+    }
+  }
+  __syncthreads();
+  Frags f0;
+  read_frags(lds2, lds2 + LM * LP, fa_off, fb_off, 0, f0);
+
+  int ks = 0;
+  for (; ks + 2 < nfull; ++ks) k_step<BQ, true>(p, g, lds2, ks, nk, nfull, fa_off, fb_off, f0, acc, st);
+  for (; ks < nk; ++ks) k_step<BQ, false>(p, g, lds2, ks, nk, nfull, fa_off, fb_off, f0, acc, st);
+
+  // (a compile-time loop: with a runtime (i, j) index the accumulators
+  // would be kept in scratch memory)
+  // M and N are multiples of 32, so every 32x32 tile is wholly inside C or
+  // wholly outside it
+  const int r0 = bm * LM + wm, c0 = bn * LN + wn;
+  static_for<16>([&](auto ij) {
+    constexpr int i = decltype(ij)::value / 4, j = decltype(ij)::value % 4;
+    if (r0 + i * 32 < p.M && c0 + j * 32 < p.N)
+      store_acc_tile_pairs<OUT_BF16, ACC>(p, acc[i][j], r0 + i * 32, c0 + j * 32, lane);
+  });
+}
+
+constexpr size_t kLds256 = 2ull * 2 * LM * LP * sizeof(uint16_t);  // 147,456 bytes
+
+template <bool BQ, bool OUT_BF16, bool ACC>
+bool launch_mm256_as(const MmArgs& a, hipStream_t s, int* status) {
+  // raise the kernel's dynamic LDS limit once per device
+  static std::atomic<uint64_t> attr_set{0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev >= 64) return false;
+  if (!(attr_set.load() & (uint64_t(1) << dev))) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&mm256_kernel<BQ, OUT_BF16, ACC>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                            static_cast<int>(kLds256)) != hipSuccess)
+      return false;
+    attr_set.fetch_or(uint64_t(1) << dev);
+  }
+  hipLaunchKernelGGL((mm256_kernel<BQ, OUT_BF16, ACC>), dim3(a.grid_m * a.grid_n), dim3(kThreads),
+                     kLds256, s, a);
+  *status = check_launch(BQ ? "mm256_kernel<bfp8>" : "mm256_kernel");
+  return true;
+}
+
+// Launches the 256x256 kernel when the problem has enough 256x256 blocks to
+// fill the chip; returns false otherwise.
+template <bool BQ>
+bool launch_mm256(MmArgs a, hipStream_t s, int* status) {
+  const int gm = (a.M + LM - 1) / LM, gn = (a.N + LN - 1) / LN;
+  if (static_cast<int64_t>(gm) * gn < 192) return false;
+  if (static_cast<int64_t>(a.M) * a.ldc >= (int64_t(1) << 31)) return false;  // 32-bit C offsets
+  a.grid_m = gm;
+  a.grid_n = gn;
+  if constexpr (BQ) {
+    return launch_mm256_as<true, true, false>(a, s, status);
+  } else {
+    if (a.c_dtype == TTLH_BF16)
+      return a.accumulate ? launch_mm256_as<false, true, true>(a, s, status)
+                          : launch_mm256_as<false, true, false>(a, s, status);
+    return a.accumulate ? launch_mm256_as<false, false, true>(a, s, status)
+                        : launch_mm256_as<false, false, false>(a, s, status);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // fp32: 64x64 blocks, 4 waves (2x2) of 32x32 v_mfma_f32_32x32x2f32 tiles,
 // BK = 32 through LDS (A row-major, B row-major; the f32 MFMA operands are
 // single elements, read with ds_read_b32).
@@ -336,6 +864,8 @@ extern "C" int ttlh_matmul(const void* A, int a_dtype, int64_t lda, const void* 
     a.K = static_cast<int32_t>(K);
     a.c_dtype = c_dtype;
     a.accumulate = accumulate ? 1 : 0;
+    int status = TTLH_OK;
+    if (launch_mm256<false>(a, s, &status)) return status;
     a.grid_m = static_cast<int32_t>((M + BM - 1) / BM);
     a.grid_n = static_cast<int32_t>((N + BN - 1) / BN);
     hipLaunchKernelGGL(mm_bf16_kernel<false>, dim3(a.grid_m * a.grid_n), dim3(kThreads), 0, s, a);
@@ -383,6 +913,8 @@ extern "C" int ttlh_matmul_bfp8w(const void* A, int64_t lda, const void* Bq, voi
   a.K = static_cast<int32_t>(K);
   a.c_dtype = TTLH_BF16;
   a.accumulate = 0;
+  int status = TTLH_OK;
+  if (launch_mm256<true>(a, static_cast<hipStream_t>(stream), &status)) return status;
   a.grid_m = static_cast<int32_t>((M + BM - 1) / BM);
   a.grid_n = static_cast<int32_t>((N + BN - 1) / BN);
   hipLaunchKernelGGL(mm_bf16_kernel<true>, dim3(a.grid_m * a.grid_n), dim3(kThreads), 0,
