@@ -78,3 +78,28 @@ def test_sdpa_config5_sampled_heads():
     for b, h in ((0, 0), (3, 31), (2, 17)):
         ref = O.sdpa_ref(q[b:b + 1, h:h + 1], k[b:b + 1, h:h + 1], v[b:b + 1, h:h + 1], scale)
         _check(out[b:b + 1, h:h + 1], ref)
+
+
+@pytest.mark.parametrize("scale", [-0.09, 0.0])
+@pytest.mark.parametrize("causal", [False, True])
+def test_sdpa_negative_and_zero_scale(scale, causal):
+    # a negative scale flips which raw score is the row maximum; scale 0 is
+    # uniform attention (plain / prefix mean of V)
+    q, k, v = _qkv(1, 2, 256, 64, 31)
+    out = _run(q, k, v, scale, causal=causal)
+    _check(out, O.sdpa_ref(q, k, v, scale, causal=causal))
+    if scale == 0.0:
+        vd = v.double()
+        mean = (vd.cumsum(2) / torch.arange(1, 257, dtype=torch.float64).view(1, 1, -1, 1)
+                if causal else vd.mean(2, keepdim=True).expand_as(vd))
+        assert float((out.double() - mean).abs().max()) <= 1e-2 * float(mean.abs().max())
+
+
+def test_sdpa_causal_d64_and_value_layout():
+    # D = 64 path, causal; V = column index pattern makes O's d layout exact:
+    # every row of P sums to one, so O[:, :, :, d] == d (to bf16 rounding)
+    q, k, _ = _qkv(1, 1, 384, 64, 41)
+    v = torch.arange(64, dtype=torch.float32).repeat(1, 1, 384, 1).bfloat16()
+    out = _run(q, k, v, 0.125, causal=True)
+    expect = torch.arange(64, dtype=torch.float64).expand(1, 1, 384, 64)
+    assert float((out.double() - expect).abs().max()) <= 63 * 2 ** -7

@@ -287,13 +287,17 @@ __device__ __forceinline__ f32x8 unary(int op, f32x8 a, float imm) {
 }
 
 __device__ __forceinline__ f32x8 round_bf16x8(f32x8 a) {
-  return map8(a, [](float v) { return static_cast<float>(static_cast<__bf16>(v)); });
+  f32x8 r;
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    const uint32_t u = cvt_pk_bf16x2(a[e], a[e + 1]);
+    r[e] = __uint_as_float(u << 16);
+    r[e + 1] = __uint_as_float(u & 0xffff0000u);
+  }
+  return r;
 }
 
-__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
-  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(lo))) |
-         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(hi))) << 16);
-}
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) { return cvt_pk_bf16x2(lo, hi); }
 
 template <int VEC, bool BF16>
 __device__ __forceinline__ f32x8 operand_value(const EltArgs& args, int idx, const Raw& q0,

@@ -314,8 +314,7 @@ __device__ __forceinline__ void store_acc_tile_pairs(const MmArgs& p, const f32x
         a += __uint_as_float(old << 16);
         b += __uint_as_float(old & 0xffff0000u);
       }
-      *c = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(a))) |
-           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(b))) << 16);
+      *c = cvt_pk_bf16x2(a, b);
     } else {
       typedef float f32x2 __attribute__((ext_vector_type(2)));
       f32x2* c = reinterpret_cast<f32x2*>(static_cast<float*>(p.C) + off);

@@ -7,9 +7,7 @@
 // docs/sphinx/specs/TTLangSpecification.md:693-761) into one flash-style pass.
 //
 // MI355X design.  One workgroup = one (batch, head) and 128 query rows; four
-// waves own 32 query rows each.  K/V stream through a double-buffered LDS
-// stage 64 rows at a time (K row-major, V transposed on its way in).  Per KV
-// block each wave computes
+// waves own 32 query rows each.  Per KV block (64 rows) each wave computes
 //     S^T = K Q^T   (16 x v_mfma_f32_32x32x16_bf16, Q^T operands kept in VGPRs)
 //     O^T += V^T P^T (16 more MFMAs)
 // Computing the transposes puts one query row in each lane's accumulator
@@ -17,12 +15,24 @@
 // l) and the O rescale are per-lane scalars; the two lane halves that share a
 // query combine with one xor-32 swizzle.  P goes from the S accumulators to
 // the second MFMA without touching LDS: the accumulator layout hands each
-// lane kv rows {16c + 4h + 8u + i}, so the V^T operand reads the same kv
-// order (two 8-byte LDS reads), the contraction being invariant under a
-// common permutation of kv.  exp is v_exp_f32 on pre-scaled log2-domain
-// scores; P is rounded to bf16 for the MFMA; O is divided by l at the end.
-// Workgroup ids are regrouped so the query blocks of one (batch, head) land
-// on the same XCD and share K/V in its L2.
+// lane kv rows {16c + 4h + 8u + i}, so the V^T operand is read in the same kv
+// order (the contraction is invariant under a common permutation of kv), with
+// two ds_read_b64_tr_b16 transpose loads from row-major V: within a group of
+// 16 lanes, output lane i, element k is element i % 4 of the 8 bytes that
+// lane 4k + i / 4 addresses, so lanes addressing 4 kv rows x 16 d columns
+// receive 4 consecutive kv of one d column each.
+//
+// K and V stream through a double-buffered LDS stage as loaded (row-major,
+// 16-byte stores); row pitches of D + 8 (K) and D + 16 (V) elements keep the
+// K fragment reads (8 rows, one 16-byte chunk) and the V transpose reads (4
+// rows, two chunks) free of bank conflicts.  The next block's K and V are
+// fetched into registers while the current block computes.
+// Softmax runs in the log2 domain: exp2(fma(s, scale log2 e, -m)), with the
+// block max taken on the raw scores; the O rescale is skipped when no lane's
+// running max moved (wave-uniform); the causal mask touches only the blocks
+// that straddle the diagonal.  P is rounded to bf16 for the MFMA; O is
+// divided by l at the end.  Workgroup ids are regrouped so the query blocks
+// of one (batch, head) land on the same XCD and share K/V in its L2.
 
 #include <cmath>
 
@@ -35,9 +45,12 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef const __attribute__((address_space(1))) u32x4 gu32x4;
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 constexpr int BQ = 128;   // query rows per workgroup
-constexpr int BKV = 64;   // kv rows per stage
+constexpr int BKV = 64;   // kv rows per block
 constexpr int kThreads = 256;
 
 struct SdpaArgs {
@@ -51,73 +64,45 @@ struct SdpaArgs {
   float scale_log2;   // scale * log2(e)
 };
 
-__device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
-  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(lo))) |
-         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(hi))) << 16);
-}
+__device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) { return cvt_pk_bf16x2(lo, hi); }
 
 template <int D>
-struct KvStage {
-  u32x4 k[D / 32];  // K: 64 x D, D/32 chunks of 8 per thread
-  u32x4 v[D / 32];  // V: 4 (kv) x 8 (d) block per thread for D = 128 (2 x 8 for D = 64)
-};
-
+constexpr int kKPitch = D + 8;   // K rows in LDS (elements)
 template <int D>
-__device__ __forceinline__ void load_kv(const SdpaArgs& p, int64_t base, int kv0, KvStage<D>& st) {
+constexpr int kVPitch = D + 16;  // V rows in LDS (elements)
+
+// K or V rows kv0 .. kv0 + 63 as 16-byte chunks, D / 32 per thread
+template <int D>
+__device__ __forceinline__ void load_rows(const uint16_t* X, int64_t base, int kv0, u32x4 (&r)[D / 32]) {
   const int t = threadIdx.x;
   constexpr int kChunksPerRow = D / 8;
 #pragma unroll
   for (int i = 0; i < D / 32; ++i) {
     const int c = t + i * kThreads;
-    const int r = c / kChunksPerRow, dc = (c % kChunksPerRow) * 8;
-    st.k[i] = *reinterpret_cast<gu32x4*>(
-        reinterpret_cast<uintptr_t>(p.K + base + static_cast<int64_t>(kv0 + r) * D + dc));
-  }
-  // V: thread -> (kv group, d octet).  Consecutive lanes take consecutive kv
-  // groups of one octet, so the transposed LDS stores of 16 lanes are one
-  // contiguous 128-byte run (all 32 banks).
-  constexpr int kOct = D / 8;
-  constexpr int kRowsPerThread = BKV * kOct / kThreads;  // 4 for D = 128, 2 for D = 64
-  constexpr int kGroups = BKV / kRowsPerThread;           // 16 for D = 128, 32 for D = 64
-  const int quad = t % kGroups, oct = t / kGroups;
-#pragma unroll
-  for (int i = 0; i < kRowsPerThread; ++i) {
-    const int r = quad * kRowsPerThread + i;
-    st.v[i] = *reinterpret_cast<gu32x4*>(
-        reinterpret_cast<uintptr_t>(p.V + base + static_cast<int64_t>(kv0 + r) * D + oct * 8));
+    const int row = c / kChunksPerRow, dc = (c % kChunksPerRow) * 8;
+    r[i] = *reinterpret_cast<gu32x4*>(
+        reinterpret_cast<uintptr_t>(X + base + static_cast<int64_t>(kv0 + row) * D + dc));
   }
 }
 
-template <int D>
-__device__ __forceinline__ void store_kv(const KvStage<D>& st, uint16_t* Ks, uint16_t* Vts) {
-  constexpr int KP = D + 8, VP = BKV + 4;
+template <int D, int PITCH>
+__device__ __forceinline__ void store_rows(const u32x4 (&r)[D / 32], uint16_t* dst) {
   const int t = threadIdx.x;
   constexpr int kChunksPerRow = D / 8;
 #pragma unroll
   for (int i = 0; i < D / 32; ++i) {
     const int c = t + i * kThreads;
-    const int r = c / kChunksPerRow, dc = (c % kChunksPerRow) * 8;
-    *reinterpret_cast<u32x4*>(Ks + r * KP + dc) = st.k[i];
+    const int row = c / kChunksPerRow, dc = (c % kChunksPerRow) * 8;
+    *reinterpret_cast<u32x4*>(dst + row * PITCH + dc) = r[i];
   }
-  constexpr int kOct = D / 8;
-  constexpr int kRowsPerThread = BKV * kOct / kThreads;
-  constexpr int kGroups = BKV / kRowsPerThread;
-  const int quad = t % kGroups, oct = t / kGroups;
-  // transpose: rows kv = quad*R + i, cols d = oct*8 + j  ->  Vt[d][kv]
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int w = j >> 1;
-    uint32_t e[kRowsPerThread];
-#pragma unroll
-    for (int i = 0; i < kRowsPerThread; ++i)
-      e[i] = (j & 1) ? (st.v[i][w] >> 16) : (st.v[i][w] & 0xffffu);
-    uint16_t* dst = Vts + (oct * 8 + j) * VP + quad * kRowsPerThread;
-    if constexpr (kRowsPerThread == 4) {
-      *reinterpret_cast<u32x2*>(dst) = u32x2{e[0] | (e[1] << 16), e[2] | (e[3] << 16)};
-    } else {
-      *reinterpret_cast<uint32_t*>(dst) = e[0] | (e[1] << 16);
-    }
-  }
+}
+
+// 4 consecutive kv rows (from kv0) of column d0 + (lane & 15) of V, as 4
+// bf16 (see the transpose-load rule above)
+template <int D>
+__device__ __forceinline__ i16x4 read_v4(const uint16_t* Vs, int kv0, int d0, int lane) {
+  const uint16_t* a = Vs + (kv0 + ((lane & 15) >> 2)) * kVPitch<D> + d0 + 4 * (lane & 3);
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)a);
 }
 
 // the block's queries: q blocks of one (b, h) are kept on one XCD
@@ -134,89 +119,113 @@ __device__ __forceinline__ void block_coords(const SdpaArgs& p, int& bh, int& qb
 }
 
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(const SdpaArgs p) {
-  constexpr int KP = D + 8, VP = BKV + 4;
-  constexpr int ND = D / 32;   // d tiles of O^T
-  constexpr int NDC = D / 16;  // 16-wide d chunks of the S^T contraction
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BKV * KP];
-  __shared__ __attribute__((aligned(16))) uint16_t Vts[2][D * VP];
+struct Sdpa {
+  static constexpr int ND = D / 32;   // d tiles of O^T
+  static constexpr int NDC = D / 16;  // 16-wide d chunks of the S^T contraction
 
-  int bh, qb;
-  block_coords(p, bh, qb);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int l32 = lane & 31, h = lane >> 5;
-  const int64_t base = static_cast<int64_t>(bh) * p.S * D;
-  const int q = qb * BQ + wave * 32 + l32;  // this lane's query row
-
-  // Q^T operands (B of S^T = K Q^T): col = query, k = d
+  const SdpaArgs& p;
+  uint16_t (*Ks)[BKV * kKPitch<D>];
+  uint16_t (*Vs)[BKV * kVPitch<D>];
+  int64_t base;
+  int qb, wave, lane, l32, h, q, nkv;
+  float sc;
   bf16x8 qop[NDC];
-#pragma unroll
-  for (int dc = 0; dc < NDC; ++dc)
-    qop[dc] = *reinterpret_cast<const bf16x8*>(p.Q + base + static_cast<int64_t>(q) * D +
-                                               dc * 16 + 8 * h);
-
   f32x16 o[ND];
-#pragma unroll
-  for (int j = 0; j < ND; ++j)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[j][r] = 0.0f;
-  float m = -INFINITY, l = 0.0f;
+  float m, l;
+  u32x4 stk[D / 32], stv[D / 32];  // K and V rows of the next block
 
-  const int nkv = CAUSAL ? (qb * BQ + BQ) / BKV : p.S / BKV;
-  KvStage<D> st;
-  load_kv<D>(p, base, 0, st);
-  store_kv<D>(st, Ks[0], Vts[0]);
-  __syncthreads();
-
-  for (int kb = 0; kb < nkv; ++kb) {
-    const int cur = kb & 1;
-    if (kb + 1 < nkv) load_kv<D>(p, base, (kb + 1) * BKV, st);
-    const uint16_t* K_ = Ks[cur];
-    const uint16_t* Vt = Vts[cur];
-
-    // S^T tiles: kv rows 32t.., query cols
-    f32x16 s[2];
+  // S^T = K Q^T for the K block at K_ (raw scores)
+  __device__ __forceinline__ void scores(const uint16_t* K_, f32x16 (&sv)[2]) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[t][r] = 0.0f;
+      for (int r = 0; r < 16; ++r) sv[t][r] = 0.0f;
 #pragma unroll
       for (int dc = 0; dc < NDC; ++dc) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(K_ + (32 * t + l32) * KP + dc * 16 + 8 * h);
-        s[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qop[dc], s[t], 0, 0, 0);
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(K_ + (32 * t + l32) * kKPitch<D> +
+                                                          dc * 16 + 8 * h);
+        sv[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qop[dc], sv[t], 0, 0, 0);
       }
     }
-    // scale into the log2 domain, causal mask, block row max
-    float mx = -INFINITY;
+  }
+
+  __device__ __forceinline__ float expo(float v) const {
+    return __builtin_amdgcn_exp2f(__builtin_fmaf(v, sc, -m));
+  }
+
+  // One KV block kb: the next block's K and V are fetched into registers
+  // while this one computes S, the softmax and O += V(kb)^T P^T from LDS
+  // buffer kb & 1, then stored into the other buffer (last read before the
+  // previous barrier).
+  __device__ __forceinline__ void step(int kb) {
+    const uint16_t* Kc = Ks[kb & 1];
+    const uint16_t* Vc = Vs[kb & 1];
+    if (kb + 1 < nkv) {
+      load_rows<D>(p.K, base, (kb + 1) * BKV, stk);
+      load_rows<D>(p.V, base, (kb + 1) * BKV, stv);
+    }
+    f32x16 cur[2];
+    scores(Kc, cur);
+
+    // causal: only blocks that reach past this wave's first query need a
+    // mask (masked scores drop out of the block extreme and get exp 0)
+    const bool diag = CAUSAL && kb * BKV + BKV - 1 > qb * BQ + wave * 32;
+    if (diag) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float v = s[t][r] * p.scale_log2;
-        if constexpr (CAUSAL) {
+        for (int r = 0; r < 16; ++r) {
           const int kv = kb * BKV + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
-          if (kv > q) v = -INFINITY;
+          if (kv > q) cur[t][r] = sc >= 0.0f ? -INFINITY : INFINITY;
         }
-        s[t][r] = v;
-        mx = fmaxf(mx, v);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m, mx);
-    const float alpha = __builtin_amdgcn_exp2f(m - m_new);  // 0 on the first block
+    }
+    // block extreme of the raw scores: max if the scale is positive, else min
+    float ex = cur[0][0];
+    if (sc >= 0.0f) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ex = fmaxf(ex, cur[t][r]);
+      ex = fmaxf(ex, __shfl_xor(ex, 32));
+    } else {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ex = fminf(ex, cur[t][r]);
+      ex = fminf(ex, __shfl_xor(ex, 32));
+    }
+    const float m_new = fmaxf(m, ex * sc);
+    // rescale O only when some lane's running max moved
+    if (__any(m_new != m)) {
+      const float alpha = __builtin_amdgcn_exp2f(m - m_new);  // 0 on the first block
+      l *= alpha;
+#pragma unroll
+      for (int j = 0; j < ND; ++j) o[j] *= alpha;
+      m = m_new;
+    }
     float rs = 0.0f;
+    if (diag) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float e = __builtin_amdgcn_exp2f(s[t][r] - m_new);
-        s[t][r] = e;
-        rs += e;
-      }
+        for (int r = 0; r < 16; ++r) {
+          const int kv = kb * BKV + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
+          const float e = kv > q ? 0.0f : expo(cur[t][r]);
+          cur[t][r] = e;
+          rs += e;
+        }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float e = expo(cur[t][r]);
+          cur[t][r] = e;
+          rs += e;
+        }
+    }
     rs += __shfl_xor(rs, 32);
-    l = l * alpha + rs;
-    m = m_new;
-#pragma unroll
-    for (int j = 0; j < ND; ++j) o[j] *= alpha;
+    l += rs;
 
     // P^T operands: chunk c (16 kv) = tile c/2, accumulators 8(c%2) .. +8
     bf16x8 pb[4];
@@ -224,40 +233,80 @@ __global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(const SdpaArgs p)
     for (int c = 0; c < 4; ++c) {
       const int t = c >> 1, r0 = 8 * (c & 1);
       u32x4 w;
-      w.x = pk_bf16(s[t][r0 + 0], s[t][r0 + 1]);
-      w.y = pk_bf16(s[t][r0 + 2], s[t][r0 + 3]);
-      w.z = pk_bf16(s[t][r0 + 4], s[t][r0 + 5]);
-      w.w = pk_bf16(s[t][r0 + 6], s[t][r0 + 7]);
+      w.x = pk_bf16(cur[t][r0 + 0], cur[t][r0 + 1]);
+      w.y = pk_bf16(cur[t][r0 + 2], cur[t][r0 + 3]);
+      w.z = pk_bf16(cur[t][r0 + 4], cur[t][r0 + 5]);
+      w.w = pk_bf16(cur[t][r0 + 6], cur[t][r0 + 7]);
       pb[c] = __builtin_bit_cast(bf16x8, w);
     }
-    // O^T += V^T P^T; V^T operand rows d, kv order {16c + 4h + 8u + i}
+    // O^T += V^T P^T; the V^T operand of lane (d = 32j + l32, h) holds kv
+    // {16c + 4h + i, 16c + 4h + 8 + i}
 #pragma unroll
     for (int j = 0; j < ND; ++j) {
-      const uint16_t* vrow = Vt + (32 * j + l32) * VP;
+      const int d0 = 32 * j + 16 * ((lane >> 4) & 1);
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow + 16 * c + 4 * h);
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 16 * c + 4 * h + 8);
-        const u32x4 w = {lo.x, lo.y, hi.x, hi.y};
+        const i16x4 lo = read_v4<D>(Vc, 16 * c + 4 * h, d0, lane);
+        const i16x4 hi = read_v4<D>(Vc, 16 * c + 4 * h + 8, d0, lane);
+        const i16x8 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         o[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), pb[c], o[j],
                                                        0, 0, 0);
       }
     }
-    if (kb + 1 < nkv) store_kv<D>(st, Ks[cur ^ 1], Vts[cur ^ 1]);
+    if (kb + 1 < nkv) {
+      store_rows<D, kKPitch<D>>(stk, Ks[(kb + 1) & 1]);
+      store_rows<D, kVPitch<D>>(stv, Vs[(kb + 1) & 1]);
+    }
     __syncthreads();
   }
+};
+
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(const SdpaArgs p) {
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BKV * kKPitch<D>];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][BKV * kVPitch<D>];
+  Sdpa<D, CAUSAL> w{p, Ks, Vs};
+  int bh;
+  block_coords(p, bh, w.qb);
+  w.lane = threadIdx.x & 63;
+  w.wave = threadIdx.x >> 6;
+  w.l32 = w.lane & 31;
+  w.h = w.lane >> 5;
+  w.base = static_cast<int64_t>(bh) * p.S * D;
+  w.q = w.qb * BQ + w.wave * 32 + w.l32;  // this lane's query row
+  w.sc = p.scale_log2;
+  w.m = -INFINITY;  // running max of s * scale * log2 e
+  w.l = 0.0f;
+  w.nkv = CAUSAL ? (w.qb * BQ + BQ) / BKV : p.S / BKV;
+
+  // prologue: K(0), V(0) into LDS; Q^T into VGPRs
+  load_rows<D>(p.K, w.base, 0, w.stk);
+  load_rows<D>(p.V, w.base, 0, w.stv);
+#pragma unroll
+  for (int dc = 0; dc < D / 16; ++dc)
+    w.qop[dc] = *reinterpret_cast<const bf16x8*>(p.Q + w.base + static_cast<int64_t>(w.q) * D +
+                                                 dc * 16 + 8 * w.h);
+#pragma unroll
+  for (int j = 0; j < D / 32; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) w.o[j][r] = 0.0f;
+  store_rows<D, kKPitch<D>>(w.stk, Ks[0]);
+  store_rows<D, kVPitch<D>>(w.stv, Vs[0]);
+  __syncthreads();
+
+  for (int kb = 0; kb < w.nkv; ++kb) w.step(kb);
 
   // O[q][d], d = 32j + 8u + 4h + i: four contiguous bf16 per (j, u)
-  const float inv = 1.0f / l;
-  uint16_t* orow = p.O + base + static_cast<int64_t>(q) * D;
+  const float inv = 1.0f / w.l;
+  uint16_t* orow = p.O + w.base + static_cast<int64_t>(w.q) * D;
 #pragma unroll
-  for (int j = 0; j < ND; ++j)
+  for (int j = 0; j < D / 32; ++j)
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int d = 32 * j + 8 * u + 4 * h;
-      const u32x2 w = {pk_bf16(o[j][4 * u] * inv, o[j][4 * u + 1] * inv),
-                       pk_bf16(o[j][4 * u + 2] * inv, o[j][4 * u + 3] * inv)};
-      *reinterpret_cast<u32x2*>(orow + d) = w;
+      const int d = 32 * j + 8 * u + 4 * w.h;
+      const u32x2 v = {pk_bf16(w.o[j][4 * u] * inv, w.o[j][4 * u + 1] * inv),
+                       pk_bf16(w.o[j][4 * u + 2] * inv, w.o[j][4 * u + 3] * inv)};
+      *reinterpret_cast<u32x2*>(orow + d) = v;
     }
 }
 

@@ -81,6 +81,15 @@ __device__ inline uint32_t pack_bf16x2(float a, float b) {
   return static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
 }
 
+// (lo, hi) -> two bf16 in one dword (lo in the low half), round to nearest
+// even, NaN -> quiet NaN: one v_cvt_pk_bf16_f32 (a vector conversion; two
+// scalar conversions would cost a conversion each plus a shift and an or).
+__device__ __forceinline__ uint32_t cvt_pk_bf16x2(float lo, float hi) {
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
+}
+
 inline int num_cus() {
   static int n = [] {
     int dev = 0, cus = 256;
