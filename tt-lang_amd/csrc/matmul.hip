@@ -551,9 +551,10 @@ __device__ __forceinline__ void load_b_one(const MmArgs& p, const Geo2& g, int k
 // One 64-k step in four 16-k substeps.  Buffer X (= ks & 1) holds step ks,
 // whose substep-0 fragments are already in f0; Y (the other) receives step
 // ks + 1 from the staging registers, which then fetch step ks + 2.
-//   s0: MFMAs(f0) | read X s1 fragments, store A -> Y, transpose + store B -> Y
-//       (bfloat8_b: dequantise B first)
-//   s1: MFMAs(f1) | read X s2 fragments, load A and B of step ks + 2
+//   s0: MFMAs(f0) | read X s1 fragments, store A -> Y, load A of step ks + 2
+//       (bfloat8_b: dequantise B)
+//   s1: MFMAs(f1) | read X s2 fragments, transpose + store B -> Y, load B of
+//       step ks + 2
 //   barrier (Y complete)
 //   s2: MFMAs(f0) | read X s3 fragments
 //   s3: MFMAs(f1) | read Y s0 fragments of step ks + 1
@@ -575,45 +576,30 @@ __device__ __forceinline__ void k_step(const MmArgs& p, const Geo2& g, uint16_t*
   const int k2 = (ks + 2) * LK;
   Frags f1;
   if constexpr (STEADY) {
-    // s0
-    if constexpr (BQ) {
+    // s0: A stores, each followed by the A load of step ks + 2 into the
+    // same registers (a full step for that load to land); bfloat8_b: the B
+    // dequantisation as well
 #pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        mfma_one(f0, acc, q);
-        if (q < 8) {
-          read_one(As, Bts, fa_off, fb_off, 16, f1, q);
-          st.b[q] = bfp8_decode8(st.bq[q], static_cast<uint8_t>(st.be >> (8 * q)));
-        } else {
-          store_a_one(st, nA, q - 8);
-          store_b_one(st, nB, q - 8);
-        }
-        TTLH_FENCE();
+    for (int q = 0; q < 16; ++q) {
+      mfma_one(f0, acc, q);
+      if (q < 8) {
+        read_one(As, Bts, fa_off, fb_off, 16, f1, q);
+        store_a_one(st, nA, q);
+        load_a_one(g, k2, st, q);
+      } else if (BQ) {
+        st.b[q - 8] = bfp8_decode8(st.bq[q - 8], static_cast<uint8_t>(st.be >> (8 * (q - 8))));
       }
-    } else {
-#pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        mfma_one(f0, acc, q);
-        if (q < 8) {
-          read_one(As, Bts, fa_off, fb_off, 16, f1, q);
-          store_a_one(st, nA, q);
-        } else {
-          store_b_one(st, nB, q - 8);
-        }
-        TTLH_FENCE();
-      }
+      TTLH_FENCE();
     }
-    // s1 (bf16: A loads first, in the order s0 stores them, so each store
-    // waits only for its own load; bfloat8_b: B first, dequantised first)
+    // s1: B transposes and stores, then the B loads of step ks + 2
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
       mfma_one(f1, acc, q);
       if (q < 8) {
         read_one(As, Bts, fa_off, fb_off, 32, f0, q);
-        if (BQ) load_b_one<BQ>(p, g, k2, st, q);
-        else load_a_one(g, k2, st, q);
+        store_b_one(st, nB, q);
       } else {
-        if (BQ) load_a_one(g, k2, st, q - 8);
-        else load_b_one<BQ>(p, g, k2, st, q - 8);
+        load_b_one<BQ>(p, g, k2, st, q - 8);
       }
       TTLH_FENCE();
     }
@@ -704,6 +690,12 @@ __global__ __launch_bounds__(kThreads, 1) void mm256_kernel(const MmArgs p) {
   read_frags(lds2, lds2 + LM * LP, fa_off, fb_off, 0, f0);
 
   int ks = 0;
+  // (two steps per iteration: the second step's waits for its staged data
+  // are then counted exactly instead of conservatively across the back edge)
+  for (; ks + 3 < nfull; ks += 2) {
+    k_step<BQ, true>(p, g, lds2, ks, nk, nfull, fa_off, fb_off, f0, acc, st);
+    k_step<BQ, true>(p, g, lds2, ks + 1, nk, nfull, fa_off, fb_off, f0, acc, st);
+  }
   for (; ks + 2 < nfull; ++ks) k_step<BQ, true>(p, g, lds2, ks, nk, nfull, fa_off, fb_off, f0, acc, st);
   for (; ks < nk; ++ks) k_step<BQ, false>(p, g, lds2, ks, nk, nfull, fa_off, fb_off, f0, acc, st);
 
