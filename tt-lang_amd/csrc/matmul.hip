@@ -732,6 +732,262 @@ bool launch_mm256_as(const MmArgs& a, hipStream_t s, int* status) {
   return true;
 }
 
+// ---------------------------------------------------------------------------
+// bf16 x bf16 large-problem kernel with a four-stage direct-to-LDS pipeline.
+// Same 256x256 block / 128x128-per-wave MFMA tiling as mm256_kernel, but:
+//  - operands reach LDS through global_load_lds_dwordx4 (lane l's 16 bytes
+//    land at the wave's LDS base + 16 l): no staging registers, no LDS store
+//    instructions;
+//  - B stays row-major (k rows, n contiguous) in LDS and its MFMA operand
+//    (8 consecutive k of one column) is read with ds_read_b64_tr_b16 (within
+//    16 lanes, output lane i, element k = element i % 4 of the 8 bytes lane
+//    4k + i / 4 addresses), so no register transposes;
+//  - 32-k stages in four LDS buffers (4 x 32 KB): a stage's loads are issued
+//    two and a half stages before its data is needed;
+//  - rows are unpadded; 16-byte chunk c of A row r sits at chunk c ^ ((r >> 1) & 3)
+//    and of B row r at c ^ (2 (r & 3)), which makes the A fragment reads (8
+//    rows, one chunk) and the B transpose reads (4 rows, two chunks) free of
+//    bank conflicts;
+//  - one barrier per stage, between its two 16-k substeps: before it each
+//    wave waits for its own loads of the next stage, after it the next
+//    stage's first fragments are read and the stage four ahead is fetched
+//    into the buffer just released.
+// Every buffer is a separate LDS variable so the compiler can tell a load
+// into one buffer from reads of another.
+constexpr int DK = 32;  // k per stage
+
+struct DmaGeo {
+  const uint16_t* a_src[4];  // per A load: row (clamped to M - 1) and chunk, at k = 0
+  const uint16_t* b_src[4];  // per B load: k row and chunk (column clamped), at k = 0
+  int fa_off;                // A fragment byte offset of this lane (row, substep 0)
+  int fa_off1;               // ... substep 1
+  int fb_even, fb_odd;       // B transpose-read byte offsets for even / odd n tiles
+};
+
+__device__ __forceinline__ DmaGeo make_dma_geo(const MmArgs& p, int bm, int bn, int wm, int wn,
+                                               int lane) {
+  DmaGeo g;
+  const int t = threadIdx.x;
+  const int wbase = (t & ~63);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int pos = i * kThreads + wbase + (t & 63);  // 16-byte position in the stage buffer
+    // A: 4 chunks per 64-byte row
+    const int ar = pos >> 2;
+    const int alc = (pos & 3) ^ ((ar >> 1) & 3);
+    const int grow = min(bm * LM + ar, p.M - 1);
+    g.a_src[i] = p.A + static_cast<int64_t>(grow) * p.lda + alc * 8;
+    // B: 32 chunks per 512-byte k row
+    const int br = pos >> 5;
+    const int blc = (pos & 31) ^ ((br & 3) << 1);
+    const int gcol = min(bn * LN + blc * 8, p.N - 8);
+    g.b_src[i] = p.B + static_cast<int64_t>(br) * p.ldb + gcol;
+  }
+  const int l32 = lane & 31, h = lane >> 5;
+  const int xa = (l32 >> 1) & 3;
+  const int arow = wm + l32;
+  g.fa_off = arow * 64 + ((0 + h) ^ xa) * 16;
+  g.fa_off1 = arow * 64 + ((2 + h) ^ xa) * 16;
+  // B operand of n tile j, k rows kb.. (kb multiple of 4): lane addresses
+  // row kb + (lane & 15) / 4, column wn + 32 j + 16 ((lane >> 4) & 1) + 4 (lane & 3)
+  const int brow = (lane & 15) >> 2;
+  const int xb = (brow & 3) << 1;
+  const int e = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);  // chunk within the 32-column group
+  const int cw = wn / 8;                                   // first chunk of the wave's columns
+  // chunk of tile j = cw + 4 j + e; XOR with xb flips bit 2 (j's bit 0) when xb >= 4
+  const int lo = (e ^ (xb & 3));
+  const int jflip = xb >> 2;  // 0 or 1
+  g.fb_even = brow * 512 + ((cw + 4 * jflip + lo) * 16) + 8 * (lane & 1);
+  g.fb_odd = brow * 512 + ((cw + 4 * (1 - jflip) + lo) * 16) + 8 * (lane & 1) - 64;
+  return g;
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef short i16x4m __attribute__((ext_vector_type(4)));
+typedef short i16x8m __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) i16x4m lds_i16x4m;
+
+// DMA of stage k0 into (A, B) buffers
+__device__ __forceinline__ void dma_stage(const MmArgs& p, const DmaGeo& g, int k0, uint16_t* Ab,
+                                          uint16_t* Bb) {
+  const int wbase = threadIdx.x & ~63;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    __builtin_amdgcn_global_load_lds(g.a_src[i] + k0, (lds_void*)(Ab + (i * kThreads + wbase) * 8), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(g.b_src[i] + static_cast<int64_t>(k0) * p.ldb,
+                                     (lds_void*)(Bb + (i * kThreads + wbase) * 8), 16, 0, 0);
+  }
+}
+
+struct DFrags {
+  bf16x8 a[4], b[4];
+};
+
+// fragments of substep `sub` (0 or 1) of the stage in (Ab, Bb)
+__device__ __forceinline__ void dma_read_frags(const uint16_t* Ab, const uint16_t* Bb,
+                                               const DmaGeo& g, int sub, int lane, DFrags& f) {
+  const char* ab = reinterpret_cast<const char*>(Ab);
+  const char* bb = reinterpret_cast<const char*>(Bb);
+  const int aoff = sub ? g.fa_off1 : g.fa_off;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    f.a[i] = *reinterpret_cast<const bf16x8*>(ab + aoff + i * 32 * 64);
+  const int kb = 16 * sub + 8 * (lane >> 5);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int off = ((j & 1) ? g.fb_odd : g.fb_even) + 64 * j;
+    const i16x4m lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4m*)(bb + off + kb * 512));
+    const i16x4m hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4m*)(bb + off + (kb + 4) * 512));
+    const i16x8m w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    f.b[j] = __builtin_bit_cast(bf16x8, w);
+  }
+}
+
+__device__ __forceinline__ void dma_mfma16(const DFrags& f, f32x16 (&acc)[4][4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+}
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4,
+// lgkmcnt 11:8): wait until at most n global loads are outstanding
+constexpr int vmcnt_imm(int n) { return 0x0F70 | (n & 0xF) | ((n >> 4) << 14); }
+
+// at most `stages` stages (8 loads per thread each) still in flight
+__device__ __forceinline__ void wait_stages(int stages) {
+  if (stages >= 3) __builtin_amdgcn_s_waitcnt(vmcnt_imm(24));
+  else if (stages == 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(16));
+  else if (stages == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(8));
+  else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+}
+
+// the four stage buffers, each its own LDS variable (see above)
+__shared__ __attribute__((aligned(16))) uint16_t dmaA0[LM * DK], dmaA1[LM * DK], dmaA2[LM * DK],
+    dmaA3[LM * DK];
+__shared__ __attribute__((aligned(16))) uint16_t dmaB0[DK * LN], dmaB1[DK * LN], dmaB2[DK * LN],
+    dmaB3[DK * LN];
+
+template <int Q>
+__device__ __forceinline__ uint16_t* dma_abuf() {
+  if constexpr (Q == 0) return dmaA0;
+  else if constexpr (Q == 1) return dmaA1;
+  else if constexpr (Q == 2) return dmaA2;
+  else return dmaA3;
+}
+template <int Q>
+__device__ __forceinline__ uint16_t* dma_bbuf() {
+  if constexpr (Q == 0) return dmaB0;
+  else if constexpr (Q == 1) return dmaB1;
+  else if constexpr (Q == 2) return dmaB2;
+  else return dmaB3;
+}
+
+// Barrier without a memory fence: the waits it needs are explicit (LDS reads
+// done, this thread's loads of the next stage landed), so the loads of later
+// stages stay in flight across it.
+__device__ __forceinline__ void stage_barrier() { __builtin_amdgcn_s_barrier(); }
+
+template <bool OUT_BF16, bool ACC>
+__global__ __launch_bounds__(kThreads, 1) void mm_dma_kernel(const MmArgs p) {
+  int bm, bn;
+  block_coords2(p, bm, bn);
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = (wave >> 1) * 128;
+  const int wn = (wave & 1) * 128;
+  const DmaGeo g = make_dma_geo(p, bm, bn, wm, wn, lane);
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int nk = p.K / DK;
+  // prologue: stages 0..3 in flight, stage 0 visible, its substep-0 fragments
+  dma_stage(p, g, 0, dma_abuf<0>(), dma_bbuf<0>());
+  if (1 < nk) dma_stage(p, g, DK, dma_abuf<1>(), dma_bbuf<1>());
+  if (2 < nk) dma_stage(p, g, 2 * DK, dma_abuf<2>(), dma_bbuf<2>());
+  if (3 < nk) dma_stage(p, g, 3 * DK, dma_abuf<3>(), dma_bbuf<3>());
+  wait_stages(min(nk - 1, 3));  // stage 0 landed; stages 1..3 may be in flight
+  stage_barrier();
+  DFrags f0, f1;
+  dma_read_frags(dma_abuf<0>(), dma_bbuf<0>(), g, 0, lane, f0);
+
+  // STEADY: stages s + 1 .. s + 4 exist (fixed waits, no branches)
+  auto stage = [&](auto qq, auto steady, int s) {
+    constexpr int q = decltype(qq)::value;  // buffer of stage s
+    constexpr bool STEADY = decltype(steady)::value;
+    uint16_t* Ab = dma_abuf<q>();
+    uint16_t* Bb = dma_bbuf<q>();
+    uint16_t* An = dma_abuf<(q + 1) & 3>();
+    uint16_t* Bn = dma_bbuf<(q + 1) & 3>();
+    // substep 0: MFMAs on f0, read this stage's substep-1 fragments
+    dma_read_frags(Ab, Bb, g, 1, lane, f1);
+    dma_mfma16(f0, acc);
+#pragma unroll
+    for (int x = 0; x < 12; ++x) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    // this wave's LDS reads are done (the buffer may be refilled after the
+    // barrier) and its loads of stage s + 1 landed (later stages may still
+    // be in flight)
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    if (STEADY) __builtin_amdgcn_s_waitcnt(vmcnt_imm(16));
+    else if (s + 1 < nk) wait_stages(min(nk - 2 - s, 2));
+    stage_barrier();
+    // substep 1: MFMAs on f1, read the next stage's substep-0 fragments and
+    // fetch stage s + 4 into the buffer this stage no longer reads
+    if (STEADY || s + 1 < nk) dma_read_frags(An, Bn, g, 0, lane, f0);
+    if (STEADY || s + 4 < nk) dma_stage(p, g, (s + 4) * DK, Ab, Bb);
+    dma_mfma16(f1, acc);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  int s = 0;
+  for (; s + 8 <= nk; s += 4) {
+    stage(I0(), std::true_type(), s);
+    stage(I1(), std::true_type(), s + 1);
+    stage(I2(), std::true_type(), s + 2);
+    stage(I3(), std::true_type(), s + 3);
+  }
+  for (; s + 4 <= nk; s += 4) {
+    stage(I0(), std::false_type(), s);
+    stage(I1(), std::false_type(), s + 1);
+    stage(I2(), std::false_type(), s + 2);
+    stage(I3(), std::false_type(), s + 3);
+  }
+  if (s < nk) stage(I0(), std::false_type(), s);
+  if (s + 1 < nk) stage(I1(), std::false_type(), s + 1);
+  if (s + 2 < nk) stage(I2(), std::false_type(), s + 2);
+
+  const int r0 = bm * LM + wm, c0 = bn * LN + wn;
+  static_for<16>([&](auto ij) {
+    constexpr int i = decltype(ij)::value / 4, j = decltype(ij)::value % 4;
+    if (r0 + i * 32 < p.M && c0 + j * 32 < p.N)
+      store_acc_tile_pairs<OUT_BF16, ACC>(p, acc[i][j], r0 + i * 32, c0 + j * 32, lane);
+  });
+}
+
+template <bool OUT_BF16, bool ACC>
+bool launch_mm_dma_as(const MmArgs& a, hipStream_t s, int* status) {
+  hipLaunchKernelGGL((mm_dma_kernel<OUT_BF16, ACC>), dim3(a.grid_m * a.grid_n), dim3(kThreads), 0,
+                     s, a);
+  *status = check_launch("mm_dma_kernel");
+  return true;
+}
+
 // Launches the 256x256 kernel when the problem has enough 256x256 blocks to
 // fill the chip; returns false otherwise.
 template <bool BQ>
@@ -744,6 +1000,13 @@ bool launch_mm256(MmArgs a, hipStream_t s, int* status) {
   if constexpr (BQ) {
     return launch_mm256_as<true, true, false>(a, s, status);
   } else {
+#ifndef TTLH_MM_NO_DMA
+    if (a.c_dtype == TTLH_BF16)
+      return a.accumulate ? launch_mm_dma_as<true, true>(a, s, status)
+                          : launch_mm_dma_as<true, false>(a, s, status);
+    return a.accumulate ? launch_mm_dma_as<false, true>(a, s, status)
+                        : launch_mm_dma_as<false, false>(a, s, status);
+#endif
     if (a.c_dtype == TTLH_BF16)
       return a.accumulate ? launch_mm256_as<false, true, true>(a, s, status)
                           : launch_mm256_as<false, true, false>(a, s, status);
