@@ -851,6 +851,56 @@ __device__ __forceinline__ void dma_mfma16(const DFrags& f, f32x16 (&acc)[4][4])
       acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
 }
 
+// Single-instruction pieces, for explicitly sequenced substeps.
+// Fragment piece q of substep `sub`: q < 4 -> A fragment q (ds_read_b128);
+// q >= 4 -> half (q & 1) of B fragment (q - 4) / 2 (a transpose read).
+struct DFragParts {
+  bf16x8 a[4];
+  i16x4m b[8];
+  __device__ __forceinline__ void to_frags(DFrags& f) const {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const i16x8m w = {b[2 * j][0], b[2 * j][1], b[2 * j][2], b[2 * j][3],
+                        b[2 * j + 1][0], b[2 * j + 1][1], b[2 * j + 1][2], b[2 * j + 1][3]};
+      f.b[j] = __builtin_bit_cast(bf16x8, w);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f.a[i] = a[i];
+  }
+};
+
+__device__ __forceinline__ void dma_read_piece(const uint16_t* Ab, const uint16_t* Bb,
+                                               const DmaGeo& g, int sub, int lane, DFragParts& f,
+                                               int q) {
+  const char* ab = reinterpret_cast<const char*>(Ab);
+  const char* bb = reinterpret_cast<const char*>(Bb);
+  if (q < 4) {
+    f.a[q] = *reinterpret_cast<const bf16x8*>(ab + (sub ? g.fa_off1 : g.fa_off) + q * 32 * 64);
+  } else {
+    const int j = (q - 4) >> 1, half = q & 1;
+    const int kb = 16 * sub + 8 * (lane >> 5) + 4 * half;
+    const int off = ((j & 1) ? g.fb_odd : g.fb_even) + 64 * j;
+    f.b[q - 4] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4m*)(bb + off + kb * 512));
+  }
+}
+
+// load i of the 8 (4 A, 4 B) that fetch stage k0 into (Ab, Bb)
+__device__ __forceinline__ void dma_piece(const MmArgs& p, const DmaGeo& g, int k0, uint16_t* Ab,
+                                          uint16_t* Bb, int i) {
+  const int wbase = threadIdx.x & ~63;
+  if (i < 4)
+    __builtin_amdgcn_global_load_lds(g.a_src[i] + k0, (lds_void*)(Ab + (i * kThreads + wbase) * 8),
+                                     16, 0, 0);
+  else
+    __builtin_amdgcn_global_load_lds(g.b_src[i - 4] + static_cast<int64_t>(k0) * p.ldb,
+                                     (lds_void*)(Bb + ((i - 4) * kThreads + wbase) * 8), 16, 0, 0);
+}
+
+__device__ __forceinline__ void dma_mfma_one(const DFrags& f, f32x16 (&acc)[4][4], int q) {
+  acc[q >> 2][q & 3] =
+      __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[q >> 2], f.b[q & 3], acc[q >> 2][q & 3], 0, 0, 0);
+}
+
 // s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4,
 // lgkmcnt 11:8): wait until at most n global loads are outstanding
 constexpr int vmcnt_imm(int n) { return 0x0F70 | (n & 0xF) | ((n >> 4) << 14); }
@@ -926,29 +976,49 @@ __global__ __launch_bounds__(kThreads, 1) void mm_dma_kernel(const MmArgs p) {
     uint16_t* Bb = dma_bbuf<q>();
     uint16_t* An = dma_abuf<(q + 1) & 3>();
     uint16_t* Bn = dma_bbuf<(q + 1) & 3>();
-    // substep 0: MFMAs on f0, read this stage's substep-1 fragments
-    dma_read_frags(Ab, Bb, g, 1, lane, f1);
-    dma_mfma16(f0, acc);
+    if constexpr (STEADY) {
+      // substep 0: one MFMA on f0, then one piece of this stage's substep-1
+      // fragments, fenced so the order holds
+      DFragParts parts;
 #pragma unroll
-    for (int x = 0; x < 12; ++x) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      for (int x = 0; x < 16; ++x) {
+        dma_mfma_one(f0, acc, x);
+        if (x < 12) dma_read_piece(Ab, Bb, g, 1, lane, parts, x);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      parts.to_frags(f1);
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's reads of the buffer done
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(16));  // own loads of stage s + 1 landed
+      stage_barrier();
+      // substep 1: one MFMA on f1, then a piece of the next stage's substep-0
+      // fragments and one load of stage s + 4 into the buffer just released
+      DFragParts nparts;
+#pragma unroll
+      for (int x = 0; x < 16; ++x) {
+        dma_mfma_one(f1, acc, x);
+        if (x < 12) dma_read_piece(An, Bn, g, 0, lane, nparts, x);
+        if (x >= 4 && x < 12) dma_piece(p, g, (s + 4) * DK, Ab, Bb, x - 4);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      nparts.to_frags(f0);
+    } else {
+      // substep 0: MFMAs on f0, read this stage's substep-1 fragments
+      dma_read_frags(Ab, Bb, g, 1, lane, f1);
+      dma_mfma16(f0, acc);
+      __builtin_amdgcn_sched_barrier(0);
+      // this wave's LDS reads are done (the buffer may be refilled after the
+      // barrier) and its loads of stage s + 1 landed (later stages may still
+      // be in flight)
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+      if (s + 1 < nk) wait_stages(min(nk - 2 - s, 2));
+      stage_barrier();
+      // substep 1: MFMAs on f1, read the next stage's substep-0 fragments and
+      // fetch stage s + 4 into the buffer this stage no longer reads
+      if (s + 1 < nk) dma_read_frags(An, Bn, g, 0, lane, f0);
+      if (s + 4 < nk) dma_stage(p, g, (s + 4) * DK, Ab, Bb);
+      dma_mfma16(f1, acc);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    // this wave's LDS reads are done (the buffer may be refilled after the
-    // barrier) and its loads of stage s + 1 landed (later stages may still
-    // be in flight)
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-    if (STEADY) __builtin_amdgcn_s_waitcnt(vmcnt_imm(16));
-    else if (s + 1 < nk) wait_stages(min(nk - 2 - s, 2));
-    stage_barrier();
-    // substep 1: MFMAs on f1, read the next stage's substep-0 fragments and
-    // fetch stage s + 4 into the buffer this stage no longer reads
-    if (STEADY || s + 1 < nk) dma_read_frags(An, Bn, g, 0, lane, f0);
-    if (STEADY || s + 4 < nk) dma_stage(p, g, (s + 4) * DK, Ab, Bb);
-    dma_mfma16(f1, acc);
-    __builtin_amdgcn_sched_barrier(0);
   };
 
   using I0 = std::integral_constant<int, 0>;
