@@ -744,10 +744,12 @@ bool launch_mm256_as(const MmArgs& a, hipStream_t s, int* status) {
 //    4k + i / 4 addresses), so no register transposes;
 //  - 32-k stages in four LDS buffers (4 x 32 KB): a stage's loads are issued
 //    two and a half stages before its data is needed;
-//  - rows are unpadded; 16-byte chunk c of A row r sits at chunk c ^ ((r >> 1) & 3)
-//    and of B row r at c ^ (2 (r & 3)), which makes the A fragment reads (8
-//    rows, one chunk) and the B transpose reads (4 rows, two chunks) free of
-//    bank conflicts;
+//  - rows are unpadded; 16-byte chunk c of A row r sits at chunk c ^ ((r >> 2) & 3)
+//    and of B row r at c ^ (4 (r & 3)).  gfx950's LDS serves 256 bytes (64
+//    banks) per cycle: a ds_read_b128 is conflict-free when each 16 lanes hit
+//    16 distinct 16-byte bank groups, a ds_read_b64 when each 32 lanes do.
+//    The A fragment reads (16 rows, one chunk) and the B transpose reads (4
+//    rows x 4 chunks per 32 lanes) both meet that;
 //  - one barrier per stage, between its two 16-k substeps: before it each
 //    wave waits for its own loads of the next stage, after it the next
 //    stage's first fragments are read and the stage four ahead is fetched
@@ -761,7 +763,7 @@ struct DmaGeo {
   const uint16_t* b_src[4];  // per B load: k row and chunk (column clamped), at k = 0
   int fa_off;                // A fragment byte offset of this lane (row, substep 0)
   int fa_off1;               // ... substep 1
-  int fb_even, fb_odd;       // B transpose-read byte offsets for even / odd n tiles
+  int fb[4];                 // B transpose-read byte offsets of the 4 n tiles
 };
 
 __device__ __forceinline__ DmaGeo make_dma_geo(const MmArgs& p, int bm, int bn, int wm, int wn,
@@ -774,31 +776,28 @@ __device__ __forceinline__ DmaGeo make_dma_geo(const MmArgs& p, int bm, int bn, 
     const int pos = i * kThreads + wbase + (t & 63);  // 16-byte position in the stage buffer
     // A: 4 chunks per 64-byte row
     const int ar = pos >> 2;
-    const int alc = (pos & 3) ^ ((ar >> 1) & 3);
+    const int alc = (pos & 3) ^ ((ar >> 2) & 3);
     const int grow = min(bm * LM + ar, p.M - 1);
     g.a_src[i] = p.A + static_cast<int64_t>(grow) * p.lda + alc * 8;
     // B: 32 chunks per 512-byte k row
     const int br = pos >> 5;
-    const int blc = (pos & 31) ^ ((br & 3) << 1);
+    const int blc = (pos & 31) ^ ((br & 3) << 2);
     const int gcol = min(bn * LN + blc * 8, p.N - 8);
     g.b_src[i] = p.B + static_cast<int64_t>(br) * p.ldb + gcol;
   }
   const int l32 = lane & 31, h = lane >> 5;
-  const int xa = (l32 >> 1) & 3;
+  const int xa = (l32 >> 2) & 3;
   const int arow = wm + l32;
   g.fa_off = arow * 64 + ((0 + h) ^ xa) * 16;
   g.fa_off1 = arow * 64 + ((2 + h) ^ xa) * 16;
   // B operand of n tile j, k rows kb.. (kb multiple of 4): lane addresses
-  // row kb + (lane & 15) / 4, column wn + 32 j + 16 ((lane >> 4) & 1) + 4 (lane & 3)
+  // row kb + (lane & 15) / 4, column wn + 32 j + 16 ((lane >> 4) & 1) + 4 (lane & 3),
+  // i.e. chunk wn / 8 + 4 j + e stored at chunk wn / 8 + 4 (j ^ brow) + e
   const int brow = (lane & 15) >> 2;
-  const int xb = (brow & 3) << 1;
-  const int e = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);  // chunk within the 32-column group
-  const int cw = wn / 8;                                   // first chunk of the wave's columns
-  // chunk of tile j = cw + 4 j + e; XOR with xb flips bit 2 (j's bit 0) when xb >= 4
-  const int lo = (e ^ (xb & 3));
-  const int jflip = xb >> 2;  // 0 or 1
-  g.fb_even = brow * 512 + ((cw + 4 * jflip + lo) * 16) + 8 * (lane & 1);
-  g.fb_odd = brow * 512 + ((cw + 4 * (1 - jflip) + lo) * 16) + 8 * (lane & 1) - 64;
+  const int e = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+  const int base = brow * 512 + (wn / 8 + e) * 16 + 8 * (lane & 1);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) g.fb[j] = base + 64 * (j ^ brow);
   return g;
 }
 
@@ -835,7 +834,7 @@ __device__ __forceinline__ void dma_read_frags(const uint16_t* Ab, const uint16_
   const int kb = 16 * sub + 8 * (lane >> 5);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int off = ((j & 1) ? g.fb_odd : g.fb_even) + 64 * j;
+    const int off = g.fb[j];
     const i16x4m lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4m*)(bb + off + kb * 512));
     const i16x4m hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4m*)(bb + off + (kb + 4) * 512));
     const i16x8m w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
@@ -879,7 +878,7 @@ __device__ __forceinline__ void dma_read_piece(const uint16_t* Ab, const uint16_
   } else {
     const int j = (q - 4) >> 1, half = q & 1;
     const int kb = 16 * sub + 8 * (lane >> 5) + 4 * half;
-    const int off = ((j & 1) ? g.fb_odd : g.fb_even) + 64 * j;
+    const int off = g.fb[j];
     f.b[q - 4] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4m*)(bb + off + kb * 512));
   }
 }

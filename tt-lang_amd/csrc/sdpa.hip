@@ -23,9 +23,11 @@
 // receive 4 consecutive kv of one d column each.
 //
 // K and V stream through a double-buffered LDS stage as loaded (row-major,
-// 16-byte stores); row pitches of D + 8 (K) and D + 16 (V) elements keep the
-// K fragment reads (8 rows, one 16-byte chunk) and the V transpose reads (4
-// rows, two chunks) free of bank conflicts.  The next block's K and V are
+// 16-byte stores).  gfx950's LDS serves 256 bytes (64 banks) per cycle: a
+// ds_read_b128 is conflict-free when each 16 lanes hit 16 distinct 16-byte
+// bank groups, a ds_read_b64 when each 32 lanes do.  Row pitches of D + 8 (K:
+// 16 rows, one chunk each) and D + 32 elements (V: 4 rows x 4 chunks per 32
+// lanes of a transpose read) meet that.  The next block's K and V are
 // fetched into registers while the current block computes.
 // Softmax runs in the log2 domain: exp2(fma(s, scale log2 e, -m)), with the
 // block max taken on the raw scores; the O rescale is skipped when no lane's
@@ -69,7 +71,7 @@ __device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) { return cvt_pk_
 template <int D>
 constexpr int kKPitch = D + 8;   // K rows in LDS (elements)
 template <int D>
-constexpr int kVPitch = D + 16;  // V rows in LDS (elements)
+constexpr int kVPitch = D + 32;  // V rows in LDS (elements)
 
 // K or V rows kv0 .. kv0 + 63 as 16-byte chunks, D / 32 per thread
 template <int D>
