@@ -294,6 +294,10 @@ __global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(const SdpaArgs p)
     for (int r = 0; r < 16; ++r) w.o[j][r] = 0.0f;
   store_rows<D, kKPitch<D>>(w.stk, Ks[0]);
   store_rows<D, kVPitch<D>>(w.stv, Vs[0]);
+  // Q^T must have landed before the loop: otherwise the compiler, merging
+  // the first iteration's state (Q loads in flight) with later ones, makes
+  // every S MFMA of every block wait on the next block's K/V prefetch
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   __syncthreads();
 
   for (int kb = 0; kb < w.nkv; ++kb) w.step(kb);
