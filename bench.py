@@ -190,7 +190,7 @@ class MatmulWorkload(PlanWorkload):
                        "bf16 out, 4x4-tile output blocks (BASELINE configs[2])")
 
     def kernel_name(self):
-        return "mm_bf16_kernel"
+        return "mm_dma_kernel"
 
     def work_per_step(self):
         return 2.0 * self.M * self.N * self.K
@@ -231,7 +231,7 @@ class Bfp8MatmulWorkload(Workload):
                        "accumulate, bf16 out (BASELINE configs[3])")
 
     def kernel_name(self):
-        return "mm_bf16_kernel<bfp8>"
+        return "mm256_kernel<bfp8>"
 
     def work_per_step(self):
         return 2.0 * self.M * self.N * self.K
