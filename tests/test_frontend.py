@@ -323,3 +323,68 @@ def test_reference_example_matmuls_plan_one_gemm(name, fn):
     plan = g[fn].trace(a, b, o)
     (l,) = plan.launches
     assert isinstance(l, P.MatmulLaunch) and l.k == 256
+
+
+# The tutorials and general_broadcast.py: kernel definitions read from the
+# reference tree (source cut before the driver code, which is re-stated here
+# with smaller shapes), traced by the drop-in and executed by the CPU plan
+# interpreter; results bit-exact against the oracle's per-op-rounded formula.
+
+def _load_defs(path):
+    src = open(os.path.join(REF, path)).read().split("torch.manual_seed(42)")[0]
+    g = {"__name__": "example", "device": None}
+    exec(compile(src, os.path.join(REF, path), "exec"), g)
+    return g
+
+
+@pytest.fixture
+def cpu_exec(monkeypatch):
+    """Kernel calls trace and run on the CPU plan interpreter (tests only)."""
+    from ttlhip import runner
+
+    def call(self, *args):
+        plan = self.trace(*args)
+        plan_interp.run(plan, {i: a for i, a in enumerate(args)})
+        call.plans.append(plan)
+    call.plans = []
+    monkeypatch.setattr(runner.KernelRunner, "__call__", call)
+    return call
+
+
+def _bf(shape, seed):
+    return O.seeded(shape, "uniform", seed, torch.bfloat16, lo=0, hi=1)
+
+
+@needs_ref
+@pytest.mark.parametrize("name,n,bcast", [
+    ("tutorial/single_core_single_tile_block.py", 128, False),
+    ("tutorial/single_core_multitile_block.py", 256, False),
+    ("tutorial/single_core_broadcast_single_tile_block.py", 128, True),
+    ("tutorial/single_core_broadcast_multitile_blocks.py", 256, True),
+    ("tutorial/multicore.py", 512, False),
+    ("tutorial/multicore_grid_auto.py", 1024, False),
+])
+def test_reference_tutorials(cpu_exec, name, n, bcast):
+    g = _load_defs(name)
+    if bcast:
+        a, b, c = _bf((n, 1), 1), _bf((1, n), 2), _bf((1, 1), 3)
+    else:
+        a, b, c = _bf((n, n), 1), _bf((n, n), 2), _bf((n, n), 3)
+    y = g["demo_kernel"](ttnn.from_torch(a), ttnn.from_torch(b), ttnn.from_torch(c))
+    expect = O.eval_expr(("add", ("mul", ("leaf", "a"), ("leaf", "b")), ("leaf", "c")),
+                         {"a": a, "b": b, "c": c})
+    assert torch.equal(ttnn.to_torch(y), expect.expand(n, n))
+    assert len(cpu_exec.plans[-1].launches) == 1
+
+
+@needs_ref
+@pytest.mark.parametrize("bshape,cshape", [((1024, 1024), (1024, 1024)), ((1024, 1), (1, 1024)),
+                                           ((1, 1024), (1, 1)), ((1, 1), (1024, 1))])
+def test_reference_general_broadcast(cpu_exec, bshape, cshape):
+    g = _load_defs("general_broadcast.py")
+    a, b, c = _bf((1024, 1024), 4), _bf(bshape, 5), _bf(cshape, 6)
+    y = ttnn.from_torch(torch.zeros(1024, 1024, dtype=torch.bfloat16))
+    g["__demo_kernel"](ttnn.from_torch(a), ttnn.from_torch(b), ttnn.from_torch(c), y)
+    expect = O.eval_expr(("add", ("mul", ("leaf", "a"), ("leaf", "b")), ("leaf", "c")),
+                         {"a": a, "b": b, "c": c})
+    assert torch.equal(ttnn.to_torch(y), expect)
