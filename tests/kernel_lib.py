@@ -329,3 +329,118 @@ def make_branchy_add(ttl):
                         ttl.copy(ob, out[i // ct, i % ct]).wait()
 
     return branchy
+
+
+def make_outer_fma(ttl, g=2, grid=(4, 4)):
+    """y = a_col * b_row + c with a (H, 1), b (1, W), c (1, 1): every operand
+    broadcast against the output block (three-argument broadcast), the scalar
+    block held by compute for the whole kernel, g x g-tile output blocks split
+    over a 2-D grid (the broadcast tutorials' pattern, multicore)."""
+
+    @ttl.kernel(grid=grid)
+    def outer_fma(a, b, c, y):
+        gx, gy = ttl.grid_size(dims=2)
+        rpc = y.shape[0] // TILE // g // gx
+        cpc = y.shape[1] // TILE // g // gy
+        a_cb = ttl.make_circular_buffer_like(a, shape=(g, 1), buffer_factor=2)
+        b_cb = ttl.make_circular_buffer_like(b, shape=(1, g), buffer_factor=2)
+        c_cb = ttl.make_circular_buffer_like(c, shape=(1, 1), buffer_factor=1)
+        y_cb = ttl.make_circular_buffer_like(y, shape=(g, g), buffer_factor=2)
+
+        @ttl.compute()
+        def comp():
+            with c_cb.wait() as cs:
+                for _ in range(rpc):
+                    for _ in range(cpc):
+                        with a_cb.wait() as ab, b_cb.wait() as bb, y_cb.reserve() as yb:
+                            yb.store(ttl.math.broadcast(ab, yb, dims=[1])
+                                     * ttl.math.broadcast(bb, yb, dims=[0])
+                                     + ttl.math.broadcast(cs, yb, dims=[0, 1]))
+
+        @ttl.datamovement()
+        def reader():
+            cx, cy = ttl.core(dims=2)
+            with c_cb.reserve() as cs:
+                ttl.copy(c[0, 0], cs).wait()
+            for i in range(rpc):
+                r = (cx * rpc + i) * g
+                for j in range(cpc):
+                    col = (cy * cpc + j) * g
+                    with a_cb.reserve() as ab, b_cb.reserve() as bb:
+                        ta = ttl.copy(a[r:r + g, 0], ab)
+                        tb = ttl.copy(b[0, col:col + g], bb)
+                        ta.wait()
+                        tb.wait()
+
+        @ttl.datamovement()
+        def writer():
+            cx, cy = ttl.core(dims=2)
+            for i in range(rpc):
+                r = (cx * rpc + i) * g
+                for j in range(cpc):
+                    col = (cy * cpc + j) * g
+                    with y_cb.wait() as yb:
+                        ttl.copy(yb, y[r:r + g, col:col + g]).wait()
+
+    return outer_fma
+
+
+def make_shape_dispatch_fma(ttl, g=2):
+    """y = a * b + c where b and c may each be full (H, W), a column (H, 1), a
+    row (1, W) or a scalar (1, 1): CB shapes, copy slices and broadcast dims
+    are chosen from the operand shapes in Python at trace time
+    (general_broadcast.py's pattern, auto grid)."""
+
+    def cb_shape(t):
+        return (g if t.shape[0] > TILE else 1, g if t.shape[1] > TILE else 1)
+
+    def src(t, r, col):
+        rs = slice(r, r + g) if t.shape[0] > TILE else 0
+        cs = slice(col, col + g) if t.shape[1] > TILE else 0
+        return t[rs, cs]
+
+    def bcast(x, like, shape):
+        dims = [d for d in (0, 1) if shape[d] == 1]
+        return ttl.math.broadcast(x, like, dims=dims) if dims else x
+
+    @ttl.kernel(grid="auto")
+    def shape_dispatch(a, b, c, y):
+        gx, gy = ttl.grid_size(dims=2)
+        rpc = y.shape[0] // TILE // g // gx
+        cpc = y.shape[1] // TILE // g // gy
+        a_cb = ttl.make_circular_buffer_like(a, shape=(g, g), buffer_factor=2)
+        b_cb = ttl.make_circular_buffer_like(b, shape=cb_shape(b), buffer_factor=2)
+        c_cb = ttl.make_circular_buffer_like(c, shape=cb_shape(c), buffer_factor=2)
+        y_cb = ttl.make_circular_buffer_like(y, shape=(g, g), buffer_factor=2)
+
+        @ttl.compute()
+        def comp():
+            for _ in range(rpc * cpc):
+                with a_cb.wait() as ab, b_cb.wait() as bb, c_cb.wait() as cb, \
+                        y_cb.reserve() as yb:
+                    yb.store(ab * bcast(bb, yb, cb_shape(b)) + bcast(cb, yb, cb_shape(c)))
+
+        @ttl.datamovement()
+        def reader():
+            cx, cy = ttl.core(dims=2)
+            for i in range(rpc):
+                r = (cx * rpc + i) * g
+                for j in range(cpc):
+                    col = (cy * cpc + j) * g
+                    with a_cb.reserve() as ab, b_cb.reserve() as bb, c_cb.reserve() as cb:
+                        xs = [ttl.copy(a[r:r + g, col:col + g], ab), ttl.copy(src(b, r, col), bb),
+                              ttl.copy(src(c, r, col), cb)]
+                        for x in xs:
+                            x.wait()
+
+        @ttl.datamovement()
+        def writer():
+            cx, cy = ttl.core(dims=2)
+            for i in range(rpc):
+                r = (cx * rpc + i) * g
+                for j in range(cpc):
+                    col = (cy * cpc + j) * g
+                    with y_cb.wait() as yb:
+                        ttl.copy(yb, y[r:r + g, col:col + g]).wait()
+
+    return shape_dispatch

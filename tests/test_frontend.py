@@ -66,6 +66,26 @@ def test_bcast_fma_column_vector():
     assert torch.equal(ref, a * b + c)  # per-op bf16 rounding == torch bf16 ops
 
 
+def test_outer_fma_three_arg_broadcast():
+    n = 256
+    a, b, c = O.seeded((n, 1), "uniform", 6), O.seeded((1, n), "uniform", 7), O.seeded((1, 1), "uniform", 8)
+    got, ref, plan = _run_both(KL.make_outer_fma, [a, b, c, torch.zeros(n, n, dtype=torch.bfloat16)],
+                               3, grid=(2, 2))
+    assert len(plan.launches) == 1
+    assert torch.equal(got, ref)
+    assert torch.equal(ref, a * b + c)
+
+
+@pytest.mark.parametrize("bshape,cshape", [((512, 512), (512, 1)), ((1, 512), (1, 1))])
+def test_shape_dispatch_fma(bshape, cshape):
+    n = 512
+    a, b, c = O.seeded((n, n), "uniform", 9), O.seeded(bshape, "uniform", 10), O.seeded(cshape, "uniform", 11)
+    got, ref, plan = _run_both(KL.make_shape_dispatch_fma,
+                               [a, b, c, torch.zeros(n, n, dtype=torch.bfloat16)], 3)
+    assert len(plan.launches) == 1
+    assert torch.equal(got, ref)
+
+
 def test_exp_row_pipe_config2_semantics():
     n = 256
     a, c = O.seeded((n, n), "uniform", 6, lo=-2, hi=2), O.seeded((n, n), "uniform", 7, lo=-2, hi=2)

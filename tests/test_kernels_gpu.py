@@ -142,3 +142,29 @@ def test_ttnn_multiply_runs_on_device():
     b = O.seeded((256, 256), "uniform", 25)
     got = ttnn.to_torch(ttnn.multiply(ttnn.from_torch(a), ttnn.from_torch(b)))
     assert torch.equal(got, a * b)
+
+
+def test_outer_fma_three_arg_broadcast_bitexact():
+    # the broadcast tutorials' pattern: (H,1) x (1,W) + (1,1), scalar block held
+    # by compute for the whole kernel, multicore
+    n = 512
+    a, b, c = O.seeded((n, 1), "uniform", 21), O.seeded((1, n), "uniform", 22), O.seeded((1, 1), "uniform", 23)
+    ts = [a, b, c, torch.zeros(n, n, dtype=torch.bfloat16)]
+    got, k = _gpu(KL.make_outer_fma, ts, 3)
+    assert len(k.last_plan.launches) == 1
+    assert torch.equal(got, _oracle(KL.make_outer_fma, ts, 3))
+
+
+@pytest.mark.parametrize("bshape,cshape", [((1024, 1024), (1024, 1024)), ((1024, 1), (1, 1024)),
+                                           ((1, 1024), (1, 1)), ((1, 1), (1024, 1))])
+def test_shape_dispatch_fma_bitexact(bshape, cshape):
+    # general_broadcast.py's pattern: CB shapes / slices / broadcast dims picked
+    # from the operand shapes, auto grid
+    n = 1024
+    a, b, c = O.seeded((n, n), "uniform", 24), O.seeded(bshape, "uniform", 25), O.seeded(cshape, "uniform", 26)
+    ts = [a, b, c, torch.zeros(n, n, dtype=torch.bfloat16)]
+    got, k = _gpu(KL.make_shape_dispatch_fma, ts, 3)
+    assert len(k.last_plan.launches) == 1
+    expect = O.eval_expr(("add", ("mul", ("leaf", "a"), ("leaf", "b")), ("leaf", "c")),
+                         {"a": a, "b": b, "c": c})
+    assert torch.equal(got, expect)
