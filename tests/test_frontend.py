@@ -9,6 +9,7 @@ classification end to end.
 """
 
 import math
+import traceback
 import os
 
 import numpy as np
@@ -218,6 +219,64 @@ def test_copy_shape_mismatch_is_rejected():
 
     with pytest.raises(ValueError, match="does not match Block shape"):
         k.trace(ttnn.Tensor(torch.zeros(64, 32)), ttnn.Tensor(torch.zeros(64, 32)))
+
+
+def _copy_lock_kernel(mistake):
+    @ttl.kernel(grid=(1, 1))
+    def k(a, out):
+        a_cb = ttl.make_circular_buffer_like(a, shape=(1, 1))
+        o_cb = ttl.make_circular_buffer_like(out, shape=(1, 1))
+
+        @ttl.compute()
+        def c():
+            with a_cb.wait() as ab, o_cb.reserve() as ob:
+                ob.store(ab)
+
+        @ttl.datamovement()
+        def r():
+            blk = a_cb.reserve()
+            tx = ttl.copy(a[0, 0], blk)
+            if mistake == "store":
+                blk.store(blk)  # written before tx.wait() (examples/copy_lock_error.py:86-88)
+            elif mistake == "push":
+                a_cb.push()  # pushed before tx.wait()
+            elif mistake == "copy":
+                ttl.copy(a[0, 0], blk)  # second copy into a locked block
+            tx.wait()
+            a_cb.push()
+
+        @ttl.datamovement()
+        def w():
+            with o_cb.wait() as ob:
+                tx = ttl.copy(ob, out[0, 0])
+                if mistake == "pop":
+                    o_cb.pop()  # popped while still the source of a copy
+                tx.wait()
+    return k
+
+
+@pytest.mark.parametrize("mistake,msg", [
+    ("store", r"locked as copy destination until tx.wait\(\) completes \(copy lock error\)"),
+    ("push", r"Cannot perform push\(\): Expected one of \[TX_WAIT\]"),
+    ("copy", r"Cannot perform copy \(as destination\): Expected one of \[TX_WAIT\]"),
+    ("pop", r"Cannot perform pop\(\): Expected one of \[TX_WAIT\]"),
+])
+def test_copy_lock_errors(mistake, msg):
+    # simulator block state machine: a block is locked from copy() to tx.wait()
+    # (python/sim/block.py:263-343, 656-694; test/sim/test_examples.py:160-190)
+    a = ttnn.Tensor(torch.zeros(32, 32))
+    with pytest.raises(RuntimeError, match=msg) as ei:
+        _copy_lock_kernel(mistake).trace(a, ttnn.Tensor(torch.zeros(32, 32)))
+    # the traceback names the offending line of the kernel source
+    here = [f for f in traceback.extract_tb(ei.tb) if f.filename == __file__]
+    assert here and {"store": "blk.store", "push": "a_cb.push()", "copy": "ttl.copy(a[0, 0], blk)",
+                     "pop": "o_cb.pop()"}[mistake] in here[-1].line
+
+
+def test_copy_lock_released_by_wait():
+    a = ttnn.Tensor(torch.zeros(32, 32))
+    plan = _copy_lock_kernel(None).trace(a, ttnn.Tensor(torch.zeros(32, 32)))
+    assert len(plan.launches) == 1
 
 
 def test_unbalanced_cb_is_reported_as_deadlock():

@@ -207,14 +207,20 @@ class CircularBuffer:
 
     def push(self) -> None:
         ctx = self._ctx()
-        if ctx.pending_reserve.pop(self.id, None) is None:
+        blk = ctx.pending_reserve.get(self.id)
+        if blk is None:
             raise RuntimeError("push() without a matching reserve()")
+        blk._check_no_pending_copy("push()")
+        del ctx.pending_reserve[self.id]
         ctx.add(Event("push", self, ctx.cur))
 
     def pop(self) -> None:
         ctx = self._ctx()
-        if ctx.pending_wait.pop(self.id, None) is None:
+        blk = ctx.pending_wait.get(self.id)
+        if blk is None:
             raise RuntimeError("pop() without a matching wait()")
+        blk._check_no_pending_copy("pop()")
+        del ctx.pending_wait[self.id]
         ctx.add(Event("pop", self, ctx.cur))
 
     def can_wait(self) -> bool:
@@ -336,6 +342,16 @@ class Block:
         self.event = event
         self.shape = cb.shape
         self._stores = 0
+        # a copy into ("dst") or out of ("src") this block whose wait() has not
+        # run yet: the block is locked until then (python/sim/block.py:263-343,656-694)
+        self._pending_copy: Optional[str] = None
+
+    def _check_no_pending_copy(self, operation: str) -> None:
+        if self._pending_copy is not None:
+            state = "NAW" if self._pending_copy == "dst" else "NAR"
+            raise RuntimeError(f"Cannot perform {operation}: Expected one of [TX_WAIT], but got "
+                               f"{operation}. Current state: Acquisition={self.kind.upper()}, "
+                               f"Thread=DM, Access={state}")
 
     def __enter__(self) -> "Block":
         return self
@@ -364,6 +380,9 @@ class Block:
                            "copy() instead.")
 
     def expr(self) -> BExpr:
+        if self._pending_copy == "dst":
+            raise RuntimeError("Cannot read from Block: Block has no access (NAW state). Current "
+                               "state: NAW, Expected operations: [TX_WAIT]")
         if self.kind != "wait":
             raise NotImplementedError("reading a reserved (output) block back is not supported by "
                                       "the MI355X backend; read blocks obtained from wait()")
@@ -390,6 +409,14 @@ class Block:
     def store(self, items, acc: bool = False) -> None:
         """Store a block expression into this reserved block.  acc=True: the first
         store assigns, later ones add (python/sim/block.py:805-868)."""
+        if self._pending_copy == "dst":
+            raise RuntimeError("Cannot write to Block: Block is locked as copy destination until "
+                               "tx.wait() completes (copy lock error). Current state: NAW, "
+                               "Expected operations: [TX_WAIT]")
+        if self._pending_copy == "src":
+            raise RuntimeError("Cannot write to Block: Block is locked as copy source until "
+                               "tx.wait() completes. Current state: NAR, Expected operations: "
+                               "[TX_WAIT]")
         if self.kind != "reserve":
             raise RuntimeError("store() needs a block obtained from reserve()")
         ctx = T.current()
@@ -408,8 +435,21 @@ class Block:
 
 
 class CopyTransaction:
+    """Handle of one tensor<->block copy; wait() releases the block's copy
+    lock (python/sim/copy.py:37-195).  The transfer itself is part of the
+    planned kernel, so the handle carries no data."""
+
+    def __init__(self, block: "Block", role: str):
+        if block._pending_copy is not None:
+            op = "copy (as destination)" if role == "dst" else "copy (as source)"
+            block._check_no_pending_copy(op)
+        self._block: Optional[Block] = block
+        block._pending_copy = role
+
     def wait(self) -> None:
-        return None
+        if self._block is not None:
+            self._block._pending_copy = None
+            self._block = None
 
     def is_done(self) -> bool:
         return True
@@ -428,16 +468,18 @@ def copy(src, dst) -> CopyTransaction:
         _check_slice_shape(src, dst)
         for x, nm in ((src.r0, "row index"), (src.c0, "col index")):
             ctx.check_loops(x, nm)
+        tx = CopyTransaction(dst, "dst")
         ctx.add(Event("copy_in", dst.cb, ctx.cur, {"block": dst, "slice": src}))
-        return CopyTransaction()
+        return tx
     if isinstance(src, Block) and isinstance(dst, TensorSlice):
         if src.kind != "wait":
             raise TraceError("copy out of a block needs a block obtained from wait()")
         _check_slice_shape(dst, src)
         for x, nm in ((dst.r0, "row index"), (dst.c0, "col index")):
             ctx.check_loops(x, nm)
+        tx = CopyTransaction(src, "src")
         ctx.add(Event("copy_out", src.cb, ctx.cur, {"block": src, "slice": dst}))
-        return CopyTransaction()
+        return tx
     raise NotImplementedError(
         f"ttl.copy({type(src).__name__} -> {type(dst).__name__}) is not supported by the MI355X "
         "backend (tensor<->block copies only; pipes are not implemented)")
