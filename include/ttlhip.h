@@ -194,6 +194,20 @@ int ttlh_matmul_bfp8w(const void* A, int64_t lda, const void* Bq, void* C,
                       int64_t ldc, int64_t M, int64_t N, int64_t K,
                       void* stream);
 
+/* The same product in two passes, for large M: Bq is dequantised once into
+ * `workspace` (row-major bf16 [K, N], at least ttlh_matmul_bfp8w_workspace_bytes
+ * bytes, 16-byte aligned, caller-owned) by ttlh_bfp8_unpack, then multiplied
+ * by the bf16 GEMM of ttlh_matmul.  The fused entry point above decodes each
+ * weight tile once per 256-row block of A, so it is the better choice when M
+ * is small (one or two blocks); this one decodes each tile once.  Results are
+ * identical to the fused path's within fp32 summation order.  Reference
+ * counterpart: as ttlh_matmul_bfp8w (tile size dtype_utils.py:174-175).   */
+int64_t ttlh_matmul_bfp8w_workspace_bytes(int64_t M, int64_t N, int64_t K);
+int ttlh_matmul_bfp8w_ws(const void* A, int64_t lda, const void* Bq, void* C,
+                         int64_t ldc, int64_t M, int64_t N, int64_t K,
+                         void* workspace, int64_t workspace_bytes,
+                         void* stream);
+
 /* ------------------------------------------------------------------------
  * Fused scaled-dot-product attention forward (no counterpart in the
  * reference: composed from spec ops @, exp, recip, reduce_max, reduce_sum,

@@ -17,7 +17,8 @@ def declared_symbols():
 
 def test_header_declares_the_expected_entry_points():
     syms = declared_symbols()
-    for s in ("ttlh_eltwise", "ttlh_matmul", "ttlh_matmul_bfp8w", "ttlh_bfp8_pack_host",
+    for s in ("ttlh_eltwise", "ttlh_matmul", "ttlh_matmul_bfp8w", "ttlh_matmul_bfp8w_ws",
+              "ttlh_matmul_bfp8w_workspace_bytes", "ttlh_bfp8_pack_host",
               "ttlh_bfp8_unpack_host", "ttlh_bfp8_unpack", "ttlh_sdpa_fwd", "ttlh_last_error",
               "ttlh_version"):
         assert s in syms, s
@@ -41,3 +42,15 @@ def test_validation_errors_need_no_gpu():
     assert b"multiples of 32" in lib.ttlh_last_error()
     st = lib.ttlh_sdpa_fwd(16, 16, 16, 16, 1, 1, 100, 128, 0.1, 0, None)
     assert st == _lib.TTLH_EUNSUPPORTED
+
+
+def test_bfp8_two_pass_workspace_is_checked_before_any_device_call():
+    from ttlhip import _lib
+    lib = _lib.load()
+    need = lib.ttlh_matmul_bfp8w_workspace_bytes(4096, 11008, 4096)
+    assert need == 4096 * 11008 * 2
+    st = lib.ttlh_matmul_bfp8w_ws(16, 4096, 16, 16, 11008, 4096, 11008, 4096, 16, need - 1, None)
+    assert st == _lib.TTLH_EINVAL
+    assert b"workspace" in lib.ttlh_last_error()
+    st = lib.ttlh_matmul_bfp8w_ws(16, 4096, 16, 16, 11008, 4096, 11008, 4096, None, need, None)
+    assert st == _lib.TTLH_EINVAL

@@ -1,7 +1,8 @@
 """bfloat8_b on the MI355X: device dequantisation (bit-exact against the
-oracle for every (exponent, byte) pair) and the bf16 x bfp8-weight matmul
-(dequantised in LDS ahead of the MFMA), checked against float64 products of
-the oracle-dequantised weights."""
+oracle for every (exponent, byte) pair) and the bf16 x bfp8-weight matmul on
+both paths (fused: dequantised in LDS ahead of the MFMA; two-pass: dequantised
+once into a bf16 workspace, then the bf16 GEMM), checked against float64
+products of the oracle-dequantised weights."""
 
 import math
 
@@ -42,14 +43,25 @@ def test_device_dequant_random_weights():
     assert torch.equal(got.view(torch.int16), OB.unpack_c(q, 256, 512).view(torch.int16))
 
 
+@pytest.mark.parametrize("rows,cols", [(96, 1440), (32, 32), (64, 2080)])
+def test_device_dequant_ragged_tile_runs(rows, cols):
+    # ragged tile grids (odd tile counts per row, a single tile, partial last workgroup)
+    from ttlhip import kernels as K
+    w = O.seeded((rows, cols), "normal", 4, torch.float32, std=0.5)
+    q = OB.pack_c(w)
+    got = K.bfp8_unpack(q.cuda(), rows, cols).cpu()
+    assert torch.equal(got.view(torch.int16), OB.unpack_c(q, rows, cols).view(torch.int16))
+
+
+@pytest.mark.parametrize("two_pass", [False, True])
 @pytest.mark.parametrize("M,K,N", [(128, 256, 128), (96, 160, 224), (256, 512, 352)])
-def test_matmul_bfp8w_small(M, K, N):
+def test_matmul_bfp8w_small(M, K, N, two_pass):
     from ttlhip import kernels as Kn
     a = O.seeded((M, K), "normal", 5)
     w = O.seeded((K, N), "normal", 6, torch.float32, std=0.02)
     q = OB.pack_c(w)
     c = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
-    Kn.matmul_bfp8w(a.cuda(), q.cuda(), c)
+    Kn.matmul_bfp8w(a.cuda(), q.cuda(), c, two_pass=two_pass)
     torch.cuda.synchronize()
     wd = OB.unpack_c(q, K, N)
     exact = a.double() @ wd.double()
@@ -58,14 +70,15 @@ def test_matmul_bfp8w_small(M, K, N):
     assert bool((err <= bound).all()), float(err.max())
 
 
-def test_matmul_bfp8w_config4_sampled():
+@pytest.mark.parametrize("two_pass", [False, True])
+def test_matmul_bfp8w_config4_sampled(two_pass):
     from ttlhip import kernels as Kn
     M, K, N = 4096, 4096, 11008
     a = O.seeded((M, K), "normal", 7)
     w = O.seeded((K, N), "normal", 8, torch.float32, std=0.02)
     q = OB.pack_c(w)
     c = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
-    Kn.matmul_bfp8w(a.cuda(), q.cuda(), c)
+    Kn.matmul_bfp8w(a.cuda(), q.cuda(), c, two_pass=two_pass)
     torch.cuda.synchronize()
     rows = torch.arange(0, M, 128)
     wd = OB.unpack_c(q, K, N).double()
@@ -75,7 +88,8 @@ def test_matmul_bfp8w_config4_sampled():
     assert bool((err <= bound).all()), float(err.max())
 
 
-def test_matmul_bfp8w_large_block_ragged():
+@pytest.mark.parametrize("two_pass", [False, True])
+def test_matmul_bfp8w_large_block_ragged(two_pass):
     # >= 192 output blocks of 256x256 -> the large-block kernel; M, N ragged
     # against 256 and K against its 64-deep staging step
     from ttlhip import kernels as Kn
@@ -84,7 +98,7 @@ def test_matmul_bfp8w_large_block_ragged():
     w = O.seeded((K, N), "normal", 10, torch.float32, std=0.02)
     q = OB.pack_c(w)
     c = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
-    Kn.matmul_bfp8w(a.cuda(), q.cuda(), c)
+    Kn.matmul_bfp8w(a.cuda(), q.cuda(), c, two_pass=two_pass)
     torch.cuda.synchronize()
     rows = torch.cat([torch.arange(0, M, 41), torch.arange(M - 32, M)])
     wd = OB.unpack_c(q, K, N).double()
@@ -92,3 +106,18 @@ def test_matmul_bfp8w_large_block_ragged():
     err = (c.cpu()[rows].double() - exact).abs()
     bound = exact.abs() * 2.0 ** -8 + 1e-6 * math.sqrt(K) * float(exact.abs().max())
     assert bool((err <= bound).all()), float(err.max())
+
+
+def test_two_pass_matches_fused_path():
+    # both paths multiply the same bf16 values with fp32 accumulation in
+    # ascending k: results agree to within one bf16 rounding of the sum
+    from ttlhip import kernels as Kn
+    M, K, N = 1024, 1024, 2048
+    a = O.seeded((M, K), "normal", 11).cuda()
+    q = OB.pack_c(O.seeded((K, N), "normal", 12, torch.float32, std=0.02)).cuda()
+    c1 = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    c2 = torch.empty_like(c1)
+    Kn.matmul_bfp8w(a, q, c1, two_pass=False)
+    Kn.matmul_bfp8w(a, q, c2, two_pass=True)
+    torch.cuda.synchronize()
+    assert int(O.bf16_ulp_diff(c1.cpu(), c2.cpu()).max()) <= 1

@@ -1244,3 +1244,29 @@ extern "C" int ttlh_matmul_bfp8w(const void* A, int64_t lda, const void* Bq, voi
                      static_cast<hipStream_t>(stream), a);
   return check_launch("mm_bf16_kernel<bfp8>");
 }
+
+extern "C" int64_t ttlh_matmul_bfp8w_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  (void)M;
+  return K > 0 && N > 0 ? K * N * 2 : 0;
+}
+
+extern "C" int ttlh_matmul_bfp8w_ws(const void* A, int64_t lda, const void* Bq, void* C,
+                                    int64_t ldc, int64_t M, int64_t N, int64_t K,
+                                    void* workspace, int64_t workspace_bytes, void* stream) {
+  clear_error();
+  TTLH_REQUIRE(workspace, TTLH_EINVAL, "ttlh_matmul_bfp8w_ws: null workspace");
+  TTLH_REQUIRE(K > 0 && N > 0 && workspace_bytes >= K * N * 2, TTLH_EINVAL,
+               "ttlh_matmul_bfp8w_ws: workspace of %lld bytes is smaller than K*N*2 = %lld",
+               (long long)workspace_bytes, (long long)(K > 0 && N > 0 ? K * N * 2 : 0));
+  TTLH_REQUIRE(A && Bq && C, TTLH_EINVAL, "ttlh_matmul_bfp8w_ws: null pointer");
+  TTLH_REQUIRE(M > 0 && M % 32 == 0 && N % 32 == 0 && K % 32 == 0, TTLH_EINVAL,
+               "ttlh_matmul_bfp8w_ws: M, N, K must be positive multiples of 32");
+  TTLH_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15) == 0, TTLH_EINVAL,
+               "ttlh_matmul_bfp8w_ws: workspace must be 16-byte aligned");
+  // pass 1: Bq tiles -> row-major bf16 [K, N] in the workspace (HBM bound);
+  // pass 2: the bf16 GEMM.  The error text of a failing pass names it.
+  int st = ttlh_bfp8_unpack(Bq, workspace, K, N, stream);
+  if (st != TTLH_OK) return st;
+  return ttlh_matmul(A, TTLH_BF16, lda, workspace, TTLH_BF16, N, C, TTLH_BF16, ldc, M, N, K, 0,
+                     stream);
+}

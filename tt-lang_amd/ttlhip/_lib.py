@@ -72,6 +72,8 @@ SIGNATURES = {
     "ttlh_bfp8_unpack_host": (_int, [_vp, _vp, _i64, _i64]),
     "ttlh_bfp8_unpack": (_int, [_vp, _vp, _i64, _i64, _vp]),
     "ttlh_matmul_bfp8w": (_int, [_vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
+    "ttlh_matmul_bfp8w_workspace_bytes": (_i64, [_i64, _i64, _i64]),
+    "ttlh_matmul_bfp8w_ws": (_int, [_vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp]),
     "ttlh_sdpa_fwd": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, C.c_float, _int, _vp]),
     "ttlh_last_error": (C.c_char_p, []),
     "ttlh_version": (_int, []),

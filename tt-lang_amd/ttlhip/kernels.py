@@ -149,8 +149,18 @@ def bfp8_unpack(q: torch.Tensor, rows: int, cols: int, stream=None) -> torch.Ten
     return out
 
 
-def matmul_bfp8w(a: torch.Tensor, bq: torch.Tensor, c: torch.Tensor, stream=None) -> None:
-    """c[M,N] = a[M,K] (bf16) @ dequant(bq)[K,N]; bf16 out."""
+# At and above this many rows of A the weight tiles are dequantised once into a
+# bf16 workspace and multiplied by the bf16 GEMM (ttlh_matmul_bfp8w_ws); below
+# it the fused kernel, which decodes each tile once per 256-row block of A, is
+# used (ttlh_matmul_bfp8w).
+BFP8_TWO_PASS_MIN_M = 512
+
+
+def matmul_bfp8w(a: torch.Tensor, bq: torch.Tensor, c: torch.Tensor, stream=None,
+                 two_pass: Optional[bool] = None) -> None:
+    """c[M,N] = a[M,K] (bf16) @ dequant(bq)[K,N]; bf16 out.  `two_pass`
+    forces the path (None: by M, see BFP8_TWO_PASS_MIN_M); the two-pass
+    workspace comes from torch's caching allocator on c's device."""
     _check_device(a, "matmul_bfp8w A")
     _check_device(c, "matmul_bfp8w C")
     M, K = a.shape
@@ -161,8 +171,18 @@ def matmul_bfp8w(a: torch.Tensor, bq: torch.Tensor, c: torch.Tensor, stream=None
         raise ValueError("matmul_bfp8w: Bq must be device uint8 tiles of a K x N matrix")
     if a.stride(1) != 1 or c.stride(1) != 1:
         raise ValueError("matmul_bfp8w: A and C must be row-major")
-    L.call("ttlh_matmul_bfp8w", a.data_ptr(), a.stride(0), bq.data_ptr(), c.data_ptr(),
-           c.stride(0), M, N, K, L.stream_ptr(stream))
+    if two_pass is None:
+        two_pass = M >= BFP8_TWO_PASS_MIN_M
+    if not two_pass:
+        L.call("ttlh_matmul_bfp8w", a.data_ptr(), a.stride(0), bq.data_ptr(), c.data_ptr(),
+               c.stride(0), M, N, K, L.stream_ptr(stream))
+        return
+    nbytes = int(L.load().ttlh_matmul_bfp8w_workspace_bytes(M, N, K))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=c.device)
+    L.call("ttlh_matmul_bfp8w_ws", a.data_ptr(), a.stride(0), bq.data_ptr(), c.data_ptr(),
+           c.stride(0), M, N, K, ws.data_ptr(), nbytes, L.stream_ptr(stream))
+    if stream is not None:
+        ws.record_stream(stream)
 
 
 def sdpa_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor, scale: float,
