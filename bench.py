@@ -289,7 +289,7 @@ class SdpaWorkload(Workload):
                        "non-causal, fp32 online softmax (BASELINE configs[4])")
 
     def kernel_name(self):
-        return "sdpa_fwd_kernel"
+        return "sdpa_pp_kernel"
 
     def work_per_step(self):
         return 4.0 * self.B * self.H * self.S * self.S * self.D

@@ -103,3 +103,24 @@ def test_sdpa_causal_d64_and_value_layout():
     out = _run(q, k, v, 0.125, causal=True)
     expect = torch.arange(64, dtype=torch.float64).expand(1, 1, 384, 64)
     assert float((out.double() - expect).abs().max()) <= 63 * 2 ** -7
+
+
+@pytest.mark.parametrize("jump", [False, True])
+def test_sdpa_running_max_growth(jump):
+    # scores that grow along kv (several rescales of O and l by the running
+    # max) and, with jump, one late key whose score dwarfs every earlier one
+    # (the rescale factor underflows to zero): the float64 softmax decides
+    S, D = 512, 128
+    q = torch.zeros(1, 2, S, D)
+    q[..., 0] = 1.0
+    q[..., 1] = torch.linspace(-1, 1, S)
+    k = torch.zeros(1, 2, S, D)
+    k[..., 0] = torch.linspace(0, 30, S)
+    k[..., 1] = 0.5
+    if jump:
+        k[0, :, S - 70, 0] = 1000.0
+    v = O.seeded((1, 2, S, D), "normal", 51)
+    q, k = q.bfloat16(), k.bfloat16()
+    for causal in (False, True):
+        out = _run(q, k, v, 1.0, causal=causal)
+        _check(out, O.sdpa_ref(q, k, v, 1.0, causal=causal))

@@ -6,37 +6,44 @@
 // (@, exp, reduce_max, reduce_sum, recip, broadcast:
 // docs/sphinx/specs/TTLangSpecification.md:693-761) into one flash-style pass.
 //
-// MI355X design.  One workgroup = one (batch, head) and 128 query rows; four
-// waves own 32 query rows each.  Per KV block (64 rows) each wave computes
+// Per wave, 32 query rows and per KV block (64 rows):
 //     S^T = K Q^T   (16 x v_mfma_f32_32x32x16_bf16, Q^T operands kept in VGPRs)
 //     O^T += V^T P^T (16 more MFMAs)
 // Computing the transposes puts one query row in each lane's accumulator
 // column for both products, so the softmax statistics (running max m and sum
 // l) and the O rescale are per-lane scalars; the two lane halves that share a
-// query combine with one xor-32 swizzle.  P goes from the S accumulators to
-// the second MFMA without touching LDS: the accumulator layout hands each
-// lane kv rows {16c + 4h + 8u + i}, so the V^T operand is read in the same kv
-// order (the contraction is invariant under a common permutation of kv), with
-// two ds_read_b64_tr_b16 transpose loads from row-major V: within a group of
-// 16 lanes, output lane i, element k is element i % 4 of the 8 bytes that
-// lane 4k + i / 4 addresses, so lanes addressing 4 kv rows x 16 d columns
-// receive 4 consecutive kv of one d column each.
+// query combine with one exchange.  P goes from the S accumulators to the
+// second MFMA without touching LDS: the accumulator layout hands each lane kv
+// rows {16c + 4h + 8u + i}, so the V^T operand is read in the same kv order
+// (the contraction is invariant under a common permutation of kv), with two
+// ds_read_b64_tr_b16 transpose loads from row-major V: within a group of 16
+// lanes, output lane i, element k is element i % 4 of the 8 bytes that lane
+// 4k + i / 4 addresses, so lanes addressing 4 kv rows x 16 d columns receive
+// 4 consecutive kv of one d column each.
 //
-// K and V stream through a double-buffered LDS stage as loaded (row-major,
-// 16-byte stores).  gfx950's LDS serves 256 bytes (64 banks) per cycle: a
-// ds_read_b128 is conflict-free when each 16 lanes hit 16 distinct 16-byte
-// bank groups, a ds_read_b64 when each 32 lanes do.  Row pitches of D + 8 (K:
-// 16 rows, one chunk each) and D + 32 elements (V: 4 rows x 4 chunks per 32
-// lanes of a transpose read) meet that.  The next block's K and V are
-// fetched into registers while the current block computes.
+// Two kernels share that per-wave math:
+//  * sdpa_pp_kernel (S a multiple of 256): 8 waves, 256 queries per
+//    workgroup, the two groups of four waves in ping-pong, one issuing the
+//    MFMAs of a block while the other runs the softmax of the previous one
+//    (details at its definition);
+//  * sdpa_fwd_kernel (S a multiple of 128): 4 waves, 128 queries, each wave
+//    running both parts in turn, two workgroups per CU.
+//
+// K and V are staged in LDS as loaded (row-major, 16-byte stores).  gfx950's
+// LDS serves 256 bytes (64 banks) per cycle: a ds_read_b128 is conflict-free
+// when each 16 lanes hit 16 distinct 16-byte bank groups, a ds_read_b64 when
+// each 32 lanes do.  Row pitches of D + 8 (K: 16 rows, one chunk each) and
+// D + 32 elements (V: 4 rows x 4 chunks per 32 lanes of a transpose read)
+// meet that.  The next block's K and V are fetched into registers while the
+// current block computes.
 // Softmax runs in the log2 domain: exp2(fma(s, scale log2 e, -m)), with the
-// block max taken on the raw scores; the O rescale is skipped when no lane's
-// running max moved (wave-uniform); the causal mask touches only the blocks
+// block max taken on the raw scores; the causal mask touches only the blocks
 // that straddle the diagonal.  P is rounded to bf16 for the MFMA; O is
 // divided by l at the end.  Workgroup ids are regrouped so the query blocks
 // of one (batch, head) land on the same XCD and share K/V in its L2.
 
 #include <cmath>
+#include <type_traits>
 
 #include "ttlh_common.h"
 
@@ -67,6 +74,29 @@ struct SdpaArgs {
 };
 
 __device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) { return cvt_pk_bf16x2(lo, hi); }
+
+// x combined with the value of lane l ^ 32, without LDS: v_permlane32_swap
+// exchanges the upper half of its first operand with the lower half of its
+// second, so with both operands = x the two results hold, per lane, x and
+// x of lane l ^ 32 (in some order)
+__device__ __forceinline__ float xor32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_min(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fminf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_add(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// s_waitcnt immediate (gfx9 encoding): at most n global loads outstanding
+constexpr int vmcnt_imm_sdpa(int n) { return 0x0F70 | (n & 0xF) | ((n >> 4) << 14); }
 
 template <int D>
 constexpr int kKPitch = D + 8;   // K rows in LDS (elements)
@@ -316,8 +346,386 @@ __global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(const SdpaArgs p)
     }
 }
 
+// ---------------------------------------------------------------------------
+// Ping-pong variant: 512 threads = two groups of four waves, 256 queries per
+// workgroup (wave w owns rows 32 w .. 32 w + 31; group g = w / 4).  Each wave
+// alternates two phases per KV block i:
+//   X(i): O^T += V(i-1)^T P(i-1)^T and S^T = K(i) Q^T  (32 MFMAs, no softmax)
+//   Y(i): softmax of S(i) -> P(i), running max / sum, O rescale (VALU only)
+// and group 1 runs one phase behind group 0, so on every SIMD (which holds one
+// wave of each group) one wave issues MFMAs while the other does the softmax:
+// the matrix core and the VALU overlap across waves.  A workgroup barrier
+// separates the phases.  LDS holds two stages; stage i = {K(i), V(i-1)} (the
+// operands of X(i)) in buffer i & 1.  Every wave loads its share of stage
+// i + 1 into registers one phase before writing it to LDS, right after the
+// last reader of that buffer has passed a barrier.
+constexpr int PP_BQ = 256;
+constexpr int PP_THREADS = 512;
+
+template <int N, typename F>
+__device__ __forceinline__ void sd_static_for(F&& f) {
+  if constexpr (N > 0) {
+    sd_static_for<N - 1>(f);
+    f(std::integral_constant<int, N - 1>());
+  }
+}
+
+#ifdef TTLH_SDPA_TRACE
+__device__ unsigned long long g_pp_trace[16][8][320];
+#define PP_MARK(w)                                                                  \
+  do {                                                                              \
+    if ((w).lane == 0 && blockIdx.x < 16 && (w).ev < 320)                           \
+      g_pp_trace[blockIdx.x][(w).wave][(w).ev] = __builtin_amdgcn_s_memtime();      \
+    ++(w).ev;                                                                       \
+  } while (0)
+#else
+#define PP_MARK(w) \
+  do {             \
+  } while (0)
+#endif
+
+template <int D>
+__device__ __forceinline__ void pp_load(const uint16_t* X, int64_t base, int kv0,
+                                        u32x4 (&r)[D / 64]) {
+  const int t = threadIdx.x;
+  constexpr int kChunksPerRow = D / 8;
+#pragma unroll
+  for (int i = 0; i < D / 64; ++i) {
+    const int c = t + i * PP_THREADS;
+    const int row = c / kChunksPerRow, dc = (c % kChunksPerRow) * 8;
+    r[i] = *reinterpret_cast<gu32x4*>(
+        reinterpret_cast<uintptr_t>(X + base + static_cast<int64_t>(kv0 + row) * D + dc));
+  }
+}
+
+template <int D, int PITCH>
+__device__ __forceinline__ void pp_store(const u32x4 (&r)[D / 64], uint16_t* dst) {
+  const int t = threadIdx.x;
+  constexpr int kChunksPerRow = D / 8;
+#pragma unroll
+  for (int i = 0; i < D / 64; ++i) {
+    const int c = t + i * PP_THREADS;
+    const int row = c / kChunksPerRow, dc = (c % kChunksPerRow) * 8;
+    *reinterpret_cast<u32x4*>(dst + row * PITCH + dc) = r[i];
+  }
+}
+
+// phase boundary: this wave's LDS accesses are complete, then a workgroup
+// barrier with no memory fence (global loads stay in flight); the empty asm
+// statements keep the compiler from moving memory accesses across it and the
+// scheduling barriers keep MFMAs and VALU work in their phase
+__device__ __forceinline__ void pp_boundary() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int D, bool CAUSAL>
+struct SdpaPP {
+  static constexpr int ND = D / 32;
+  static constexpr int NDC = D / 16;
+
+  const SdpaArgs& p;
+  uint16_t (*Ks)[BKV * kKPitch<D>];
+  uint16_t (*Vs)[BKV * kVPitch<D>];
+  int64_t base;
+  int qb, wave, lane, l32, h, q, n;
+  float sc;
+  bf16x8 qop[NDC];
+  f32x16 o[ND];
+  f32x16 cur[2];
+  bf16x8 pb[4];
+  float m, l;
+  u32x4 stk[D / 64], stv[D / 64];
+  int ev = 0;
+
+  // stage j = {K(j) if j < n, V(j - 1) if j >= 1} into registers / into LDS
+  __device__ __forceinline__ void load_stage(int j) {
+    if (j < n) pp_load<D>(p.K, base, j * BKV, stk);
+    if (j >= 1 && j <= n) pp_load<D>(p.V, base, (j - 1) * BKV, stv);
+  }
+  __device__ __forceinline__ void write_stage(int j) {
+    if (j < n) pp_store<D, kKPitch<D>>(stk, Ks[j & 1]);
+    if (j >= 1 && j <= n) pp_store<D, kVPitch<D>>(stv, Vs[j & 1]);
+  }
+
+  // X(i): DO_O adds V(i-1)^T P(i-1)^T, DO_S computes S(i); operands from
+  // LDS buffer i & 1.  The MFMAs (S and O alternating when both run) form a
+  // software pipeline: the LDS fragments of MFMA m + kPipe are requested
+  // right after MFMA m issues, so LDS latency hides behind kPipe MFMAs; the
+  // scheduling barriers keep that order.
+  static constexpr int kPipe = 6;
+
+  template <bool DO_O, bool DO_S, int M>
+  __device__ __forceinline__ void x_frag(const uint16_t* Kc, const uint16_t* Vc, bf16x8& f) {
+    constexpr bool kIsO = DO_O && DO_S ? (M & 1) != 0 : DO_O;
+    constexpr int k = DO_O && DO_S ? (M >> 1) : M;
+    if constexpr (kIsO) {
+      constexpr int j = k >> 2, c = k & 3;
+      const int d0 = 32 * j + 16 * ((lane >> 4) & 1);
+      const i16x4 lo = read_v4<D>(Vc, 16 * c + 4 * h, d0, lane);
+      const i16x4 hi = read_v4<D>(Vc, 16 * c + 4 * h + 8, d0, lane);
+      const i16x8 w = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      f = __builtin_bit_cast(bf16x8, w);
+    } else {
+      constexpr int t = k / NDC, dc = k % NDC;
+      f = *reinterpret_cast<const bf16x8*>(Kc + (32 * t + l32) * kKPitch<D> + dc * 16 + 8 * h);
+    }
+  }
+
+  template <bool DO_O, bool DO_S, int M>
+  __device__ __forceinline__ void x_mfma(const bf16x8& f) {
+    constexpr bool kIsO = DO_O && DO_S ? (M & 1) != 0 : DO_O;
+    constexpr int k = DO_O && DO_S ? (M >> 1) : M;
+    if constexpr (kIsO) {
+      constexpr int j = k >> 2, c = k & 3;
+      o[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f, pb[c], o[j], 0, 0, 0);
+    } else {
+      constexpr int t = k / NDC, dc = k % NDC;
+      cur[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f, qop[dc], cur[t], 0, 0, 0);
+    }
+  }
+
+  template <bool DO_O, bool DO_S>
+  __device__ __forceinline__ void x_phase(int i) {
+    const uint16_t* Kc = Ks[i & 1];
+    const uint16_t* Vc = Vs[i & 1];
+    constexpr int T = (DO_S ? 2 * NDC : 0) + (DO_O ? 4 * ND : 0);
+    if constexpr (DO_S) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) cur[t][r] = 0.0f;
+    }
+    bf16x8 fr[T];
+    sd_static_for<(kPipe < T ? kPipe : T)>([&](auto mc) {
+      x_frag<DO_O, DO_S, decltype(mc)::value>(Kc, Vc, fr[decltype(mc)::value]);
+    });
+    __builtin_amdgcn_sched_barrier(0);
+    sd_static_for<T>([&](auto mc) {
+      constexpr int m = decltype(mc)::value;
+      x_mfma<DO_O, DO_S, m>(fr[m]);
+      if constexpr (m + kPipe < T) x_frag<DO_O, DO_S, m + kPipe>(Kc, Vc, fr[m + kPipe]);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  }
+
+  __device__ __forceinline__ float expo(float v) const {
+    return __builtin_amdgcn_exp2f(__builtin_fmaf(v, sc, -m));
+  }
+
+  // Y(i): online softmax of S(i) into P(i) (masking and extreme rules as in
+  // Sdpa::step).  The running max m moves lazily: only when a lane's block
+  // maximum exceeds it by more than kLazy (log2 units), so O and l are rarely
+  // rescaled; until then P = exp2(s - m) <= 2^kLazy, which fp32 O / l and the
+  // bf16 P operands hold without loss (the final O / l is unchanged by the
+  // choice of m).
+  static constexpr float kLazy = 8.0f;
+
+  __device__ __forceinline__ void y_phase(int kb) {
+    const bool diag = CAUSAL && kb * BKV + BKV - 1 > qb * PP_BQ + wave * 32;
+    // element (t, r) holds kv = kb*BKV + 4h + (32t + 8(r/4) + r%4): masked
+    // when that offset exceeds lim (compared against literal constants)
+    const int lim = q - kb * BKV - 4 * h;
+    if (diag) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (32 * t + 8 * (r >> 2) + (r & 3) > lim) cur[t][r] = sc >= 0.0f ? -INFINITY : INFINITY;
+    }
+    // block extreme as a 4-way tree (short dependency chains)
+    float ex;
+    if (sc >= 0.0f) {
+      float p4[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int t = u >> 1, r0 = 8 * (u & 1);
+        p4[u] = fmaxf(fmaxf(fmaxf(cur[t][r0], cur[t][r0 + 1]), fmaxf(cur[t][r0 + 2], cur[t][r0 + 3])),
+                      fmaxf(fmaxf(cur[t][r0 + 4], cur[t][r0 + 5]), fmaxf(cur[t][r0 + 6], cur[t][r0 + 7])));
+      }
+      ex = xor32_max(fmaxf(fmaxf(p4[0], p4[1]), fmaxf(p4[2], p4[3])));
+    } else {
+      float p4[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int t = u >> 1, r0 = 8 * (u & 1);
+        p4[u] = fminf(fminf(fminf(cur[t][r0], cur[t][r0 + 1]), fminf(cur[t][r0 + 2], cur[t][r0 + 3])),
+                      fminf(fminf(cur[t][r0 + 4], cur[t][r0 + 5]), fminf(cur[t][r0 + 6], cur[t][r0 + 7])));
+      }
+      ex = xor32_min(fminf(fminf(p4[0], p4[1]), fminf(p4[2], p4[3])));
+    }
+    const float m_blk = ex * sc;
+#ifdef TTLH_SDPA_NO_LAZY
+    const bool grow = m_blk > m;
+#else
+    const bool grow = m_blk > m + kLazy;
+#endif
+    if (__any(grow)) {
+      const float m_new = grow ? m_blk : m;
+      const float alpha = __builtin_amdgcn_exp2f(m - m_new);  // 1 where m stays, 0 at first
+      l *= alpha;
+#pragma unroll
+      for (int j = 0; j < ND; ++j) o[j] *= alpha;
+      m = m_new;
+    }
+    if (diag) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          cur[t][r] = 32 * t + 8 * (r >> 2) + (r & 3) > lim ? 0.0f : expo(cur[t][r]);
+    } else {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) cur[t][r] = expo(cur[t][r]);
+    }
+    // row sum as four independent partial sums (short dependency chains)
+    float rs4[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int t = c >> 1, r0 = 8 * (c & 1);
+      u32x4 w;
+      w.x = pk_bf16(cur[t][r0 + 0], cur[t][r0 + 1]);
+      w.y = pk_bf16(cur[t][r0 + 2], cur[t][r0 + 3]);
+      w.z = pk_bf16(cur[t][r0 + 4], cur[t][r0 + 5]);
+      w.w = pk_bf16(cur[t][r0 + 6], cur[t][r0 + 7]);
+      pb[c] = __builtin_bit_cast(bf16x8, w);
+      rs4[c] = ((cur[t][r0] + cur[t][r0 + 1]) + (cur[t][r0 + 2] + cur[t][r0 + 3])) +
+               ((cur[t][r0 + 4] + cur[t][r0 + 5]) + (cur[t][r0 + 6] + cur[t][r0 + 7]));
+    }
+    l += xor32_add((rs4[0] + rs4[1]) + (rs4[2] + rs4[3]));
+  }
+
+  // group 0: X(i), write stage i+1 | load stage i+2, Y(i).  The first and
+  // last X phases (S only, O only) are peeled so the steady loop has one body.
+  __device__ __forceinline__ void run_group0() {
+    PP_MARK(*this);
+    x_phase<false, true>(0);
+    write_stage(1);
+    PP_MARK(*this);
+    pp_boundary();
+    PP_MARK(*this);
+    load_stage(2);
+    y_phase(0);
+    PP_MARK(*this);
+    pp_boundary();
+    for (int i = 1; i < n; ++i) {
+      PP_MARK(*this);
+      x_phase<true, true>(i);
+      write_stage(i + 1);
+      PP_MARK(*this);
+      pp_boundary();
+      PP_MARK(*this);
+      load_stage(i + 2);
+      y_phase(i);
+      PP_MARK(*this);
+      pp_boundary();
+    }
+    x_phase<true, false>(n);
+    pp_boundary();
+  }
+  // group 1, one phase behind: Y(i-1), write stage i+1 | load stage i+2, X(i)
+  __device__ __forceinline__ void run_group1() {
+    PP_MARK(*this);
+    write_stage(1);
+    PP_MARK(*this);
+    pp_boundary();
+    PP_MARK(*this);
+    load_stage(2);
+    x_phase<false, true>(0);
+    PP_MARK(*this);
+    pp_boundary();
+    for (int i = 1; i < n; ++i) {
+      PP_MARK(*this);
+      y_phase(i - 1);
+      write_stage(i + 1);
+      PP_MARK(*this);
+      pp_boundary();
+      PP_MARK(*this);
+      load_stage(i + 2);
+      x_phase<true, true>(i);
+      PP_MARK(*this);
+      pp_boundary();
+    }
+    y_phase(n - 1);
+    pp_boundary();
+    x_phase<true, false>(n);
+  }
+};
+
+// the workgroup's queries: query blocks of one (b, h) kept on one XCD
+__device__ __forceinline__ void pp_block_coords(const SdpaArgs& p, int& bh, int& qb) {
+  block_coords(p, bh, qb);
+}
+
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(PP_THREADS, 1) void sdpa_pp_kernel(const SdpaArgs p) {
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BKV * kKPitch<D>];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][BKV * kVPitch<D>];
+  SdpaPP<D, CAUSAL> w{p, Ks, Vs};
+  int bh;
+  pp_block_coords(p, bh, w.qb);
+  w.lane = threadIdx.x & 63;
+  w.wave = threadIdx.x >> 6;
+  w.l32 = w.lane & 31;
+  w.h = w.lane >> 5;
+  w.base = static_cast<int64_t>(bh) * p.S * D;
+  w.q = w.qb * PP_BQ + w.wave * 32 + w.l32;
+  w.sc = p.scale_log2;
+  w.m = -INFINITY;
+  w.l = 0.0f;
+  w.n = CAUSAL ? (w.qb * PP_BQ + PP_BQ) / BKV : p.S / BKV;
+
+  // prologue: Q^T into VGPRs, stage 0 (K(0)) into LDS, stage 1 into registers
+#pragma unroll
+  for (int dc = 0; dc < D / 16; ++dc)
+    w.qop[dc] = *reinterpret_cast<const bf16x8*>(p.Q + w.base + static_cast<int64_t>(w.q) * D +
+                                                 dc * 16 + 8 * w.h);
+  w.load_stage(0);
+  // Q^T and K(0) must have landed before any later load is issued: the
+  // stage loads are conditional, so a partial wait after them would leave Q
+  // "possibly in flight" on some path, and the compiler would then make every
+  // S MFMA wait for the stage prefetch in flight at that point
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm_sdpa(0));
+  w.write_stage(0);
+  w.load_stage(1);
+#pragma unroll
+  for (int j = 0; j < D / 32; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) w.o[j][r] = 0.0f;
+  pp_boundary();
+
+  if (w.wave < 4) w.run_group0();
+  else w.run_group1();
+
+  const float inv = 1.0f / w.l;
+  uint16_t* orow = p.O + w.base + static_cast<int64_t>(w.q) * D;
+#pragma unroll
+  for (int j = 0; j < D / 32; ++j)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int d = 32 * j + 8 * u + 4 * w.h;
+      const u32x2 v = {pk_bf16(w.o[j][4 * u] * inv, w.o[j][4 * u + 1] * inv),
+                       pk_bf16(w.o[j][4 * u + 2] * inv, w.o[j][4 * u + 3] * inv)};
+      *reinterpret_cast<u32x2*>(orow + d) = v;
+    }
+}
+
 template <int D, bool CAUSAL>
 int launch(const SdpaArgs& a, hipStream_t s) {
+#ifndef TTLH_SDPA_NO_PP
+  if (a.S % PP_BQ == 0) {
+    SdpaArgs b = a;
+    b.nqb = a.S / PP_BQ;
+    hipLaunchKernelGGL((sdpa_pp_kernel<D, CAUSAL>), dim3(b.nbh * b.nqb), dim3(PP_THREADS), 0, s, b);
+    return check_launch("sdpa_pp_kernel");
+  }
+#endif
   hipLaunchKernelGGL((sdpa_fwd_kernel<D, CAUSAL>), dim3(a.nbh * a.nqb), dim3(kThreads), 0, s, a);
   return check_launch("sdpa_fwd_kernel");
 }
