@@ -444,3 +444,61 @@ def make_shape_dispatch_fma(ttl, g=2):
                         ttl.copy(yb, y[r:r + g, col:col + g]).wait()
 
     return shape_dispatch
+
+
+def make_matmul_split_rows(ttl, grid=(13, 10)):
+    """C = A @ B with one (1, 1) output tile per step and the output tiles
+    divided over the grid by utils.block_allocation.split_work_to_cores
+    (group boxes counted as full rectangles, as the metal examples' tt-lang
+    versions do); store(acc=True) over K."""
+    from utils.block_allocation import split_work_to_cores
+
+    @ttl.kernel(grid=grid)
+    def mm_split(a, b, out):
+        mt, kt, nt = a.shape[0] // TILE, a.shape[1] // TILE, b.shape[1] // TILE
+        a_cb = ttl.make_circular_buffer_like(a, shape=(1, 1), buffer_factor=2)
+        b_cb = ttl.make_circular_buffer_like(b, shape=(1, 1), buffer_factor=2)
+        o_cb = ttl.make_circular_buffer_like(out, shape=(1, 1), buffer_factor=2)
+        _, g1, g2, u1, u2 = split_work_to_cores(ttl.grid_size(dims=2), mt * nt, row_wise=True)
+
+        def box(g):
+            return (g[1][0] - g[0][0] + 1) * (g[1][1] - g[0][1] + 1) if g else 0
+
+        n1, n2 = box(g1), box(g2)
+
+        def count(c):
+            return u1 if c < n1 else (u2 if c < n1 + n2 else 0)
+
+        def first(c):
+            return c * u1 if c < n1 else n1 * u1 + (c - n1) * u2
+
+        @ttl.compute()
+        def comp():
+            c = ttl.core(dims=1)
+            for _ in range(count(c)):
+                with o_cb.reserve() as ob:
+                    for _ in range(kt):
+                        with a_cb.wait() as ab, b_cb.wait() as bb:
+                            ob.store(ab @ bb, acc=True)
+
+        @ttl.datamovement()
+        def reader():
+            c = ttl.core(dims=1)
+            for i in range(count(c)):
+                t = first(c) + i
+                for k in range(kt):
+                    with a_cb.reserve() as ab, b_cb.reserve() as bb:
+                        ta = ttl.copy(a[t // nt, k], ab)
+                        tb = ttl.copy(b[k, t % nt], bb)
+                        ta.wait()
+                        tb.wait()
+
+        @ttl.datamovement()
+        def writer():
+            c = ttl.core(dims=1)
+            for i in range(count(c)):
+                t = first(c) + i
+                with o_cb.wait() as ob:
+                    ttl.copy(ob, out[t // nt, t % nt]).wait()
+
+    return mm_split

@@ -168,3 +168,18 @@ def test_shape_dispatch_fma_bitexact(bshape, cshape):
     expect = O.eval_expr(("add", ("mul", ("leaf", "a"), ("leaf", "b")), ("leaf", "c")),
                          {"a": a, "b": b, "c": c})
     assert torch.equal(got, expect)
+
+
+def test_matmul_split_rows_meets_metal_examples_ulp_bar():
+    # the metal examples' tt-lang versions check 10 bf16 ULP against torch's
+    # bf16 matmul (examples/metal_examples/*/ttlang/*.py, utils/correctness.py)
+    from utils.correctness import assert_with_ulp
+    n = 640
+    a = ttnn.rand((n, n), dtype=ttnn.bfloat16, layout=ttnn.TILE_LAYOUT)
+    b = ttnn.rand((n, n), dtype=ttnn.bfloat16, layout=ttnn.TILE_LAYOUT)
+    c = ttnn.empty((n, n), dtype=ttnn.bfloat16, layout=ttnn.TILE_LAYOUT)
+    k = KL.make_matmul_split_rows(ttl)
+    k(a, b, c)
+    assert len(k.last_plan.launches) == 1
+    golden = torch.matmul(ttnn.to_torch(a).to(torch.bfloat16), ttnn.to_torch(b).to(torch.bfloat16))
+    assert_with_ulp(golden, ttnn.to_torch(c).to(torch.bfloat16))

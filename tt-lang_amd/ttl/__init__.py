@@ -9,6 +9,7 @@ unchanged; their tile programs execute as HIP kernels (tt-lang_amd/csrc).
 
 from ttlhip.dsl import (  # noqa: F401
     MAX_CBS,
+    Program,
     TILE_SHAPE,
     Block,
     CircularBuffer,

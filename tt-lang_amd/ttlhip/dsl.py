@@ -44,6 +44,8 @@ class _KernelState:
         self.grid = grid
         self.threads: List["ThreadTemplate"] = []
         self.cbs: List["CircularBuffer"] = []
+        # thread order given by an explicit Program(compute, dm0, dm1)()
+        self.program_order: Optional[List["ThreadTemplate"]] = None
 
 
 _kstate: Optional[_KernelState] = None
@@ -135,6 +137,31 @@ def _register(t: ThreadTemplate) -> ThreadTemplate:
         raise RuntimeError("ttl.compute / ttl.datamovement must be used inside a ttl.kernel body")
     _kstate.threads.append(t)
     return t
+
+
+class _ProgramCall:
+    def __init__(self, funcs: Tuple[Any, ...]):
+        self.funcs = funcs
+
+    def __call__(self, *args: Any, **kwargs: Any) -> None:
+        if _kstate is None:
+            raise RuntimeError("Program(...)() is only valid inside a ttl.kernel body")
+        if len(self.funcs) != 3:
+            raise ValueError(f"Kernel must define exactly 3 threads (compute, dm0, dm1), got "
+                             f"{len(self.funcs)}")
+        for f in self.funcs:
+            if not isinstance(f, ThreadTemplate) or f not in _kstate.threads:
+                raise ValueError("Program() takes the ttl.compute / ttl.datamovement functions "
+                                 "defined in this kernel body")
+        _kstate.program_order = list(self.funcs)
+
+
+def Program(*funcs: Any, grid: Any = None) -> _ProgramCall:
+    """Explicit thread list of a kernel body, `return Program(compute, dm0,
+    dm1, grid=grid)()` (python/sim/program.py:100-255): fixes which data
+    movement thread is dm0 / dm1; the kernel still runs when the body
+    returns (on the grid the ttl.kernel decorator resolved)."""
+    return _ProgramCall(funcs)
 
 
 def compute():

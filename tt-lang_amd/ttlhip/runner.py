@@ -74,6 +74,7 @@ class KernelRunner:
         try:
             body(*args, **kwargs)
             threads = list(dsl._kstate.threads)
+            explicit = dsl._kstate.program_order
         finally:
             dsl._kstate = prev
         if len(threads) != 3:
@@ -86,6 +87,11 @@ class KernelRunner:
         if len(dms) != 2:
             raise ValueError(f"Kernel must define exactly 2 datamovement threads, got {len(dms)}")
         ordered = [comp[0], dms[0], dms[1]]
+        if explicit is not None:
+            if [t.kind for t in explicit] != ["compute", "dm", "dm"]:
+                raise ValueError("Program() expects (compute, dm0, dm1): one ttl.compute function "
+                                 "followed by two ttl.datamovement functions")
+            ordered = explicit
         ncores = int(np.prod(self.grid))
         core_traces = []
         for c in range(ncores):
