@@ -76,6 +76,9 @@ def run_matmul(l: MatmulLaunch, args):
     a, b, c = l.a.resolve(args), l.b.resolve(args), l.c.resolve(args)
     r0, r1 = l.rows
     c0, c1 = l.cols
+    if l.b_block:  # packed bfloat8_b tiles: the oracle's integer decoder
+        from oracle import bfp8 as OB
+        b = OB.unpack_c(b.cpu(), a.shape[1], c.shape[1])
     c[r0:r1, c0:c1] = (a[r0:r1].double() @ b[:, c0:c1].double()).to(c.dtype)
 
 

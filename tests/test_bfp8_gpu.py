@@ -121,3 +121,42 @@ def test_two_pass_matches_fused_path():
     Kn.matmul_bfp8w(a, q, c2, two_pass=True)
     torch.cuda.synchronize()
     assert int(O.bf16_ulp_diff(c1.cpu(), c2.cpu()).max()) <= 1
+
+
+def _bound_check(got, exact, K):
+    err = (got.double() - exact).abs()
+    bound = exact.abs() * 2.0 ** -8 + 1e-6 * math.sqrt(K) * float(exact.abs().max())
+    assert bool((err <= bound).all()), float(err.max())
+
+
+@pytest.mark.parametrize("M,K,N", [(96, 256, 160), (512, 384, 640)])
+def test_ttnn_matmul_with_bfloat8_b_weights(M, K, N):
+    # ttnn-level use of the format: from_torch(dtype=bfloat8_b) packs, matmul
+    # runs the fused (small M) or two-pass (M >= 512) bf16 x bfloat8_b GEMM
+    import ttnn
+    a = O.seeded((M, K), "normal", 61)
+    w = O.seeded((K, N), "normal", 62, torch.float32, std=0.02)
+    wq = ttnn.from_torch(w, dtype=ttnn.bfloat8_b, layout=ttnn.TILE_LAYOUT)
+    back = ttnn.to_torch(wq)  # device dequantisation
+    assert torch.equal(back, OB.unpack_c(OB.pack_c(w), K, N).float())
+    c = ttnn.to_torch(ttnn.matmul(ttnn.from_torch(a), wq))
+    _bound_check(c, a.double() @ back.double(), K)
+
+
+@pytest.mark.parametrize("M,K,N", [(256, 256, 320), (1024, 512, 1024)])
+def test_ttl_kernel_with_bfloat8_b_weights(M, K, N):
+    # a tt-lang multicore matmul kernel whose B tensor is bfloat8_b: the plan
+    # is one bf16 x bfloat8_b GEMM launch
+    import kernel_lib as KL
+    import ttl
+    import ttnn
+    a = O.seeded((M, K), "normal", 63)
+    w = O.seeded((K, N), "normal", 64, torch.float32, std=0.02)
+    wq = ttnn.from_torch(w, dtype=ttnn.bfloat8_b)
+    c = ttnn.empty((M, N), dtype=ttnn.bfloat16)
+    k = KL.make_matmul_multi(ttl, ttnn)
+    k(ttnn.from_torch(a), wq, c)
+    (l,) = k.last_plan.launches
+    assert l.b_block
+    exact = a.double() @ OB.unpack_c(OB.pack_c(w), K, N).double()
+    _bound_check(ttnn.to_torch(c), exact, K)

@@ -180,6 +180,12 @@ def datamovement():
 # circular buffers and blocks
 
 
+def compute_dtype(dtype):
+    """The torch dtype block arithmetic uses for a CB element type: itself,
+    or bfloat16 for a block-float format (ttnn.bfloat8_b)."""
+    return getattr(dtype, "compute_dtype", dtype)
+
+
 class CircularBuffer:
     """A CB of `shape` tiles per block and `shape[0]*shape[1]*buffer_factor`
     tiles of capacity (python/sim/cb.py:158-300).  On the MI355X the ring
@@ -414,7 +420,8 @@ class Block:
             raise NotImplementedError("reading a reserved (output) block back is not supported by "
                                       "the MI355X backend; read blocks obtained from wait()")
         r, c = self.shape
-        return BExpr(self.shape, ("leaf", self, np.arange(r), np.arange(c)), self.cb.dtype)
+        return BExpr(self.shape, ("leaf", self, np.arange(r), np.arange(c)),
+                     compute_dtype(self.cb.dtype))
 
     # arithmetic delegates to BExpr
     def __add__(self, o): return _binary("add", self, o)

@@ -83,6 +83,7 @@ class MatmulLaunch:
     rows: Tuple[int, int]   # output element rows [r0, r1)
     cols: Tuple[int, int]   # output element cols [c0, c1)
     k: int
+    b_block: bool = False   # B is a block-float (bfloat8_b) tensor of packed tiles
 
     def describe(self) -> str:
         return (f"matmul C[{self.rows[0]}:{self.rows[1]}, {self.cols[0]}:{self.cols[1]}] = "
@@ -365,8 +366,14 @@ def _plan_eltwise(g: _Group, out_rc, leaf_rc, tensor_ref) -> EltwiseLaunch:
     H, W = out_t.shape
     leaf_nodes: Dict[int, X.Leaf] = {}
     specs: Dict[int, OperandSpec] = {}
+    if getattr(out_t, "is_block_float", False):
+        raise PlanError(f"storing into a {out_t.dtype.name} tensor is not supported (block-float "
+                        "tensors are read-only tile-matmul weights here)")
     for k, lf in enumerate(g.leaf_blocks):
         tens = g.leaf_tensors[k]
+        if getattr(tens, "is_block_float", False):
+            raise PlanError(f"a {tens.dtype.name} tensor as an elementwise operand is not "
+                            "supported; it can be the B operand of a tile matmul")
         h, w = tens.shape
         rm, ro = _axis_map(out_rc[:, 0], leaf_rc[k][:, 0], h)
         cm, co = _axis_map(out_rc[:, 1], leaf_rc[k][:, 1], w)
@@ -403,8 +410,16 @@ def _plan_matmul(g: _Group, out_rc, leaf_rc, tensor_ref) -> MatmulLaunch:
     r0, r1, c0, c1 = _rect(out_rc)
     if (r1 - r0) * (c1 - c0) != n_out:
         raise PlanError("the matmul output tiles do not form a rectangle")
+    if getattr(a_t, "is_block_float", False) or getattr(g.out_tensor, "is_block_float", False):
+        raise PlanError("block-float tensors are supported as the B operand of a tile matmul only")
+    b_block = getattr(b_t, "is_block_float", False)
+    if b_block:
+        if (c0, c1) != (0, b_t.shape[1] // TILE):
+            raise PlanError(f"a {b_t.dtype.name} B operand must be used over all of its columns")
+        if a_t.dtype != torch.bfloat16 or g.out_tensor.dtype != torch.bfloat16:
+            raise PlanError(f"the {b_t.dtype.name} matmul takes bfloat16 A and output tensors")
     return MatmulLaunch(tensor_ref(a_t), tensor_ref(b_t), tensor_ref(g.out_tensor),
-                        (r0 * TILE, r1 * TILE), (c0 * TILE, c1 * TILE), K)
+                        (r0 * TILE, r1 * TILE), (c0 * TILE, c1 * TILE), K, b_block)
 
 
 # ---------------------------------------------------------------------------
@@ -432,4 +447,7 @@ def execute(plan: Plan, args: Dict[Any, Any], stream=None) -> None:
                 raise ValueError("matmul output aliases an input")
             r0, r1 = l.rows
             c0, c1 = l.cols
-            Kn.matmul(a[r0:r1], b[:, c0:c1], c[r0:r1, c0:c1], accumulate=False, stream=stream)
+            if l.b_block:
+                Kn.matmul_bfp8w(a[r0:r1], b, c[r0:r1], stream=stream)
+            else:
+                Kn.matmul(a[r0:r1], b[:, c0:c1], c[r0:r1, c0:c1], accumulate=False, stream=stream)

@@ -40,6 +40,25 @@ L1_MEMORY_CONFIG = None
 bfloat16 = torch.bfloat16
 float32 = torch.float32
 
+
+class BlockFloatType:
+    """A block-floating-point tile format (ttnn.bfloat8_b): tensors of this
+    dtype hold packed 32x32 tiles, `tile_bytes` each (the reference fixes the
+    size, python/ttl/dtype_utils.py:151-181).  Arithmetic on them happens in
+    bfloat16 (`compute_dtype`)."""
+
+    compute_dtype = torch.bfloat16
+
+    def __init__(self, name: str, tile_bytes: int):
+        self.name = name
+        self.tile_bytes = tile_bytes
+
+    def __repr__(self) -> str:
+        return f"DataType.{self.name.upper()}"
+
+
+bfloat8_b = BlockFloatType("bfloat8_b", 1088)
+
 TTNN_AVAILABLE = True
 
 
@@ -55,25 +74,44 @@ class Tensor:
     ttl.copy moves between the tensor and a circular-buffer block.
     """
 
-    def __init__(self, tensor: torch.Tensor) -> None:
+    def __init__(self, tensor: torch.Tensor, *, block: Optional[BlockFloatType] = None,
+                 logical_shape: Optional[Tuple[int, ...]] = None) -> None:
         if not isinstance(tensor, torch.Tensor):
             raise TypeError(f"ttnn.Tensor wraps a torch.Tensor, got {type(tensor)}")
         self._tensor = tensor
+        # block-float tensors: _tensor holds the packed tile bytes (uint8)
+        self._block = block
+        self._logical_shape = tuple(logical_shape) if logical_shape is not None else None
 
     # -- metadata -----------------------------------------------------------
     @property
     def shape(self) -> Tuple[int, ...]:
+        if self._block is not None:
+            return self._logical_shape
         return tuple(self._tensor.shape)
 
     @property
-    def dtype(self) -> torch.dtype:
-        return self._tensor.dtype
+    def dtype(self):
+        return self._block if self._block is not None else self._tensor.dtype
+
+    @property
+    def is_block_float(self) -> bool:
+        return self._block is not None
 
     @property
     def layout(self):
         return TILE_LAYOUT
 
     def to_torch(self) -> torch.Tensor:
+        """Host copy; block-float tensors come back as float32 values (the
+        conversion ttnn.to_torch applies to bfloat8_b)."""
+        if self._block is not None:
+            from ttlhip import kernels as K
+
+            rows, cols = self._logical_shape
+            if self._tensor.is_cuda:
+                return K.bfp8_unpack(self._tensor, rows, cols).float().cpu()
+            return K.bfp8_unpack_host(self._tensor, rows, cols).float()
         return self._tensor.detach().cpu()
 
     def __repr__(self) -> str:
@@ -91,6 +129,8 @@ class Tensor:
 
             if all(is_index(k) for k in key):
                 return TensorSlice.from_key(self, key)
+        if self._block is not None:
+            raise TypeError(f"a {self._block.name} tensor is indexed by tiles only")
         return Tensor(self._tensor[key])
 
     def __setitem__(self, key: Any, value: Any) -> None:
@@ -159,26 +199,46 @@ def _shape(shape: Union[Sequence[int], int]) -> Tuple[int, ...]:
     return (shape,) if isinstance(shape, int) else tuple(shape)
 
 
-def rand(shape, dtype: torch.dtype = bfloat16, **_: Any) -> Tensor:
+def _block_from_fp32(t: torch.Tensor, block: BlockFloatType) -> Tensor:
+    """fp32 [rows, cols] -> packed tiles in device memory (host codec)."""
+    from ttlhip import kernels as K
+
+    if t.dim() != 2:
+        raise ValueError(f"{block.name} tensors are 2-D, got shape {tuple(t.shape)}")
+    packed = K.bfp8_pack_host(t.to(torch.float32))
+    return Tensor(packed.to(_device()), block=block, logical_shape=tuple(t.shape))
+
+
+def rand(shape, dtype=bfloat16, **_: Any) -> Tensor:
     """U[0, 1) drawn in fp32 from torch's global generator, then cast - the
     same stream and rounding as python/sim/ttnnsim.py:521-531."""
-    t = torch.rand(_shape(shape), dtype=torch.float32).to(dtype)
-    return Tensor(t.to(_device()))
+    t = torch.rand(_shape(shape), dtype=torch.float32)
+    if isinstance(dtype, BlockFloatType):
+        return _block_from_fp32(t, dtype)
+    return Tensor(t.to(dtype).to(_device()))
 
 
-def empty(shape, dtype: torch.dtype = bfloat16, **_: Any) -> Tensor:
+def empty(shape, dtype=bfloat16, **_: Any) -> Tensor:
+    if isinstance(dtype, BlockFloatType):
+        return _block_from_fp32(torch.zeros(_shape(shape)), dtype)
     return Tensor(torch.empty(_shape(shape), dtype=dtype, device=_device()))
 
 
-def zeros(shape, dtype: torch.dtype = bfloat16, **_: Any) -> Tensor:
+def zeros(shape, dtype=bfloat16, **_: Any) -> Tensor:
+    if isinstance(dtype, BlockFloatType):
+        return _block_from_fp32(torch.zeros(_shape(shape)), dtype)
     return Tensor(torch.zeros(_shape(shape), dtype=dtype, device=_device()))
 
 
-def ones(shape, dtype: torch.dtype = bfloat16, **_: Any) -> Tensor:
+def ones(shape, dtype=bfloat16, **_: Any) -> Tensor:
+    if isinstance(dtype, BlockFloatType):
+        return _block_from_fp32(torch.ones(_shape(shape)), dtype)
     return Tensor(torch.ones(_shape(shape), dtype=dtype, device=_device()))
 
 
-def full(shape, fill_value: float, dtype: torch.dtype = bfloat16, **_: Any) -> Tensor:
+def full(shape, fill_value: float, dtype=bfloat16, **_: Any) -> Tensor:
+    if isinstance(dtype, BlockFloatType):
+        return _block_from_fp32(torch.full(_shape(shape), float(fill_value)), dtype)
     return Tensor(torch.full(_shape(shape), fill_value, dtype=dtype, device=_device()))
 
 
@@ -190,9 +250,13 @@ def empty_like(t: Tensor, dtype=None, **_: Any) -> Tensor:
     return Tensor(torch.empty_like(t._tensor, dtype=dtype))
 
 
-def from_torch(tensor: torch.Tensor, dtype: Optional[torch.dtype] = None, layout: Any = None,
+def from_torch(tensor: torch.Tensor, dtype=None, layout: Any = None,
                device: Any = None, memory_config: Any = None, **_: Any) -> Tensor:
+    """Device copy of `tensor`; dtype=ttnn.bfloat8_b quantises it into packed
+    tiles (shared exponent per 16-element face row, round half to even)."""
     t = tensor.detach()
+    if isinstance(dtype, BlockFloatType):
+        return _block_from_fp32(t.cpu(), dtype)
     if dtype is not None:
         t = t.to(dtype)
     return Tensor(t.to(_device()).contiguous())
@@ -206,6 +270,43 @@ def to_torch(t: Union[Tensor, torch.Tensor], **_: Any) -> torch.Tensor:
 
 def to_layout(t: Tensor, layout: Any, **_: Any) -> Tensor:
     return t
+
+
+def typecast(t: Tensor, dtype, **_: Any) -> Tensor:
+    """Converts between bfloat16 / float32 and the block-float formats."""
+    if isinstance(dtype, BlockFloatType):
+        return _block_from_fp32(t.to_torch().float(), dtype)
+    if t.is_block_float:
+        return Tensor(t.to_torch().to(dtype).to(_device()))
+    return Tensor(t._tensor.to(dtype))
+
+
+def matmul(a: Tensor, b: Tensor, **_: Any) -> Tensor:
+    """a @ b on the MI355X (bf16 / f32 MFMA, fp32 accumulation; a bfloat8_b
+    `b` goes through the bf16 x bfloat8_b GEMM).  The result is bfloat16 for
+    bfloat16 / block-float inputs, float32 for float32 ones."""
+    from ttlhip import _lib
+    from ttlhip import kernels as K
+
+    _lib.require_device()
+    if a.is_block_float:
+        raise NotImplementedError("ttnn.matmul takes a block-float tensor as the second operand only")
+    ta = a._tensor.contiguous()
+    M, Ka = ta.shape
+    Kb, N = b.shape
+    if Ka != Kb:
+        raise ValueError(f"matmul shapes {tuple(ta.shape)} @ {tuple(b.shape)} do not chain")
+    if b.is_block_float:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=ta.device)
+        K.matmul_bfp8w(ta.to(torch.bfloat16), b._tensor, out)
+        return Tensor(out)
+    tb = b._tensor.contiguous()
+    out_dtype = torch.float32 if torch.float32 in (ta.dtype, tb.dtype) else torch.bfloat16
+    if ta.dtype != tb.dtype:
+        ta, tb = ta.to(out_dtype), tb.to(out_dtype)
+    out = torch.empty((M, N), dtype=out_dtype, device=ta.device)
+    K.matmul(ta, tb, out)
+    return Tensor(out)
 
 
 def to_device(t: Tensor, device: Any = None, **_: Any) -> Tensor:
@@ -271,19 +372,6 @@ def neg(a: Tensor, **_: Any) -> Tensor: return _eltwise("neg", a, None)
 def relu(a: Tensor, **_: Any) -> Tensor: return _eltwise("relu", a, None)
 def sigmoid(a: Tensor, **_: Any) -> Tensor: return _eltwise("sigmoid", a, None)
 def reciprocal(a: Tensor, **_: Any) -> Tensor: return _eltwise("recip", a, None)
-
-
-def matmul(a: Tensor, b: Tensor, **_: Any) -> Tensor:
-    """C = A @ B on the MI355X tile-matmul kernel (fp32 accumulation)."""
-    from ttlhip import _lib
-    from ttlhip.kernels import matmul as mm
-
-    _lib.require_device()
-    ta, tb = a._tensor.contiguous(), b._tensor.contiguous()
-    out = torch.empty((ta.shape[0], tb.shape[1]), dtype=torch.promote_types(ta.dtype, tb.dtype),
-                      device=ta.device)
-    mm(ta, tb, out)
-    return Tensor(out)
 
 
 # ---------------------------------------------------------------------------
