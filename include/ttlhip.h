@@ -209,6 +209,37 @@ int ttlh_matmul_bfp8w_ws(const void* A, int64_t lda, const void* Bq, void* C,
                          void* stream);
 
 /* ------------------------------------------------------------------------
+ * bfloat4_b tiles.  The reference fixes only the tile size, 64 + 512 = 576
+ * bytes (python/ttl/dtype_utils.py:176-177); this build's format:
+ *   bytes [0, 64):    exponent byte 16*f + r shared by face f, row r (faces
+ *                     as for bfloat8_b);
+ *   bytes [64, 576):  one nibble per element, byte 64 + 128*f + 8*r + c/2
+ *                     (low nibble: even c, high nibble: odd c), bit 3 = sign,
+ *                     bits 2..0 = magnitude m.
+ *   value = (-1)^s * m * 2^(e - 129), exactly (at most 3 significant bits,
+ *   always a bfloat16).
+ * Pack: e = largest biased fp32 exponent of the face row's 16 values (0 when
+ * all are zero / subnormal), m = round-half-even(|x| * 2^(129 - e)) capped at
+ * 7.  Inputs must be finite.                                               */
+#define TTLH_BFP4_TILE_BYTES 576
+
+int ttlh_bfp4_pack_host(const float* src, void* dst, int64_t rows,
+                        int64_t cols);
+int ttlh_bfp4_unpack_host(const void* src, uint16_t* dst_bf16, int64_t rows,
+                          int64_t cols);
+/* device dequant: tiles -> row-major bf16 (device pointers) */
+int ttlh_bfp4_unpack(const void* src, void* dst_bf16, int64_t rows,
+                     int64_t cols, void* stream);
+/* C[M,N] = A[M,K] (bf16, row-major) . dequant(Bq4)[K,N] in two passes: the
+ * bfloat4_b weights are dequantised into `workspace` (row-major bf16 [K, N],
+ * K*N*2 bytes, 16-byte aligned) and multiplied by the bf16 GEMM; bf16 out.
+ * Reference counterpart: the bfloat4_b dtype (tile size as above).        */
+int ttlh_matmul_bfp4w_ws(const void* A, int64_t lda, const void* Bq4, void* C,
+                         int64_t ldc, int64_t M, int64_t N, int64_t K,
+                         void* workspace, int64_t workspace_bytes,
+                         void* stream);
+
+/* ------------------------------------------------------------------------
  * Fused scaled-dot-product attention forward (no counterpart in the
  * reference: composed from spec ops @, exp, recip, reduce_max, reduce_sum,
  * broadcast, docs/sphinx/specs/TTLangSpecification.md:693-761).

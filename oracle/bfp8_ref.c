@@ -84,3 +84,81 @@ void oracle_bfp8_unpack(const uint8_t* src, uint16_t* dst, int64_t rows, int64_t
         }
     }
 }
+
+/* ---------------------------------------------------------------------------
+ * bfloat4_b (576-byte tiles, python/ttl/dtype_utils.py:176-177) - TEST ORACLE.
+ * Same faces and shared exponents; element nibble = sign (bit 3) | magnitude m
+ * (bits 2..0), byte 64 + 128*f + 8*r + c/2 (low nibble: even c);
+ * value = (-1)^s m 2^(e-129); pack m = round-half-even(|x| 2^(129-e)) <= 7.
+ */
+
+/* |x| * 2^(129 - e) rounded half-to-even, capped at 7 (integer arithmetic) */
+static uint32_t quantise4(uint32_t bits, int e) {
+  uint32_t ex = (bits >> 23) & 0xff, frac = bits & 0x7fffff;
+  uint64_t sig;
+  int shift;
+  if (ex == 0) { sig = frac; shift = -149; }
+  else { sig = frac | 0x800000u; shift = (int)ex - 150; }
+  int s = shift + 129 - e;
+  if (sig == 0) return 0;
+  if (s >= 0) { uint64_t m = sig << (s > 40 ? 40 : s); return m > 7 ? 7 : (uint32_t)m; }
+  int r = -s;
+  if (r > 63) return 0;
+  uint64_t q = sig >> r, rem = sig & ((1ull << r) - 1), half = 1ull << (r - 1);
+  if (rem > half || (rem == half && (q & 1))) q += 1;
+  return q > 7 ? 7 : (uint32_t)q;
+}
+
+void oracle_bfp4_pack(const float* src, uint8_t* dst, int64_t rows, int64_t cols) {
+  int64_t ntc = cols / 32;
+  memset(dst, 0, (size_t)((rows / 32) * ntc * 576));
+  for (int64_t tr = 0; tr < rows / 32; ++tr)
+    for (int64_t tc = 0; tc < ntc; ++tc) {
+      uint8_t* t = dst + (tr * ntc + tc) * 576;
+      for (int r = 0; r < 32; ++r)
+        for (int h = 0; h < 2; ++h) {
+          uint32_t bits[16];
+          int e = 0;
+          for (int c = 0; c < 16; ++c) {
+            memcpy(&bits[c], &src[(tr * 32 + r) * cols + tc * 32 + h * 16 + c], 4);
+            int ex = (bits[c] >> 23) & 0xff;
+            if (ex > e) e = ex;
+          }
+          int f = face_of(r, h * 16);
+          t[16 * f + (r & 15)] = (uint8_t)e;
+          for (int c = 0; c < 16; ++c) {
+            uint32_t nib = ((bits[c] >> 31) << 3) | quantise4(bits[c] & 0x7fffffffu, e);
+            t[64 + 128 * f + 8 * (r & 15) + (c >> 1)] |= (uint8_t)(nib << (4 * (c & 1)));
+          }
+        }
+    }
+}
+
+/* exact bf16 of (-1)^s m 2^(e-129), built from integer fields */
+uint16_t oracle_bfp4_decode(uint8_t e, uint8_t nib) {
+  uint32_t s = (nib >> 3) & 1, m = nib & 7;
+  if (m == 0) return (uint16_t)(s << 15);
+  int p = 2;
+  while (!(m & (1u << p))) --p;          /* leading one */
+  int E = p + (int)e - 2;                /* biased bf16 exponent of m 2^(e-129) */
+  uint32_t out;
+  if (E >= 255) out = 0x7f80;            /* e >= 253 with m >= 4: overflow -> inf */
+  else if (E >= 1) out = ((uint32_t)E << 7) | ((m << (7 - p)) & 0x7f);
+  else out = m << (e + 4);               /* subnormal: field = value / 2^-133 */
+  return (uint16_t)((s << 15) | out);
+}
+
+void oracle_bfp4_unpack(const uint8_t* src, uint16_t* dst, int64_t rows, int64_t cols) {
+  int64_t ntc = cols / 32;
+  for (int64_t tr = 0; tr < rows / 32; ++tr)
+    for (int64_t tc = 0; tc < ntc; ++tc) {
+      const uint8_t* t = src + (tr * ntc + tc) * 576;
+      for (int r = 0; r < 32; ++r)
+        for (int c = 0; c < 32; ++c) {
+          int f = face_of(r, c);
+          uint8_t byte = t[64 + 128 * f + 8 * (r & 15) + ((c & 15) >> 1)];
+          dst[(tr * 32 + r) * cols + tc * 32 + c] =
+              oracle_bfp4_decode(t[16 * f + (r & 15)], (uint8_t)((byte >> (4 * (c & 1))) & 0xf));
+        }
+    }
+}

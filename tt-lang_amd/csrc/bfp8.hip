@@ -169,3 +169,139 @@ extern "C" int ttlh_bfp8_unpack(const void* src, void* dst_bf16, int64_t rows, i
                      static_cast<uint16_t*>(dst_bf16), cols, ntiles, nt_c);
   return check_launch("bfp8_unpack_kernel");
 }
+
+// ---------------------------------------------------------------------------
+// bfloat4_b (format in include/ttlhip.h): the same face / shared-exponent
+// structure with 4-bit sign-magnitude elements, two per byte.
+
+namespace {
+
+int bfp4_elem_byte(int r, int c) {
+  const int f = ((r >> 4) << 1) | (c >> 4);
+  return 64 + 128 * f + 8 * (r & 15) + ((c & 15) >> 1);
+}
+
+uint16_t bfp4_decode_host(uint8_t e, uint32_t n) {
+  const double v = std::ldexp(static_cast<double>(n & 7u), static_cast<int>(e) - 129);
+  const float f = static_cast<float>(v);  // exact: at most 3 significant bits
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  return static_cast<uint16_t>((u >> 16) | ((n & 8u) << 12));
+}
+
+// One wave per tile, lane l = (face l / 16, face row l % 16): one exponent
+// byte and 8 element bytes per lane (contiguous across the wave), 32 bytes of
+// one bf16 output row written per lane.
+__global__ __launch_bounds__(256) void bfp4_unpack_kernel(const uint8_t* __restrict__ q,
+                                                          uint16_t* __restrict__ out,
+                                                          int64_t cols, int64_t ntiles,
+                                                          int64_t nt_c) {
+  const int64_t tile = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) >> 6;
+  if (tile >= ntiles) return;
+  const int lane = threadIdx.x & 63;
+  const int f = lane >> 4, r = lane & 15;
+  const uint8_t* t = q + tile * TTLH_BFP4_TILE_BYTES;
+  const uint8_t e = t[lane];
+  const uint64_t nib = *reinterpret_cast<const uint64_t*>(t + 64 + 8 * lane);
+  u32x4 lo, hi;
+  bfp4_decode16(nib, e, lo, hi);
+  const int64_t tr = tile / nt_c, tc = tile - tr * nt_c;
+  uint16_t* o = out + (tr * 32 + (f >> 1) * 16 + r) * cols + tc * 32 + (f & 1) * 16;
+  *reinterpret_cast<u32x4*>(o) = lo;
+  *reinterpret_cast<u32x4*>(o + 8) = hi;
+}
+
+}  // namespace
+
+extern "C" int ttlh_bfp4_pack_host(const float* src, void* dst, int64_t rows, int64_t cols) {
+  clear_error();
+  TTLH_REQUIRE(src && dst, TTLH_EINVAL, "ttlh_bfp4_pack_host: null pointer");
+  TTLH_REQUIRE(rows > 0 && cols > 0 && rows % 32 == 0 && cols % 32 == 0, TTLH_EINVAL,
+               "ttlh_bfp4_pack_host: rows and cols must be positive multiples of 32");
+  TTLH_REQUIRE(finite_all(src, rows * cols), TTLH_EINVAL,
+               "ttlh_bfp4_pack_host: input holds inf or NaN (not representable in bfloat4_b)");
+  uint8_t* out = static_cast<uint8_t*>(dst);
+  const int64_t nt_c = cols / 32;
+  std::memset(out, 0, static_cast<size_t>((rows / 32) * nt_c * TTLH_BFP4_TILE_BYTES));
+  for (int64_t tr = 0; tr < rows / 32; ++tr)
+    for (int64_t tc = 0; tc < nt_c; ++tc) {
+      uint8_t* tile = out + (tr * nt_c + tc) * TTLH_BFP4_TILE_BYTES;
+      for (int r = 0; r < 32; ++r)
+        for (int half = 0; half < 2; ++half) {
+          const float* row = src + (tr * 32 + r) * cols + tc * 32 + half * 16;
+          int e = 0;
+          for (int c = 0; c < 16; ++c) {
+            uint32_t u;
+            std::memcpy(&u, &row[c], 4);
+            e = std::max(e, static_cast<int>((u >> 23) & 0xff));
+          }
+          tile[bfp8_exp_off(r, half * 16)] = static_cast<uint8_t>(e);
+          const double scale = std::ldexp(1.0, 129 - e);
+          for (int c = 0; c < 16; ++c) {
+            const double a = std::fabs(static_cast<double>(row[c])) * scale;
+            const uint32_t m = static_cast<uint32_t>(std::min(7.0, rne(a)));
+            const uint32_t nib = (std::signbit(row[c]) ? 8u : 0u) | m;
+            const int cc = half * 16 + c;
+            tile[bfp4_elem_byte(r, cc)] |= static_cast<uint8_t>(nib << (4 * (cc & 1)));
+          }
+        }
+    }
+  return TTLH_OK;
+}
+
+extern "C" int ttlh_bfp4_unpack_host(const void* src, uint16_t* dst, int64_t rows, int64_t cols) {
+  clear_error();
+  TTLH_REQUIRE(src && dst, TTLH_EINVAL, "ttlh_bfp4_unpack_host: null pointer");
+  TTLH_REQUIRE(rows > 0 && cols > 0 && rows % 32 == 0 && cols % 32 == 0, TTLH_EINVAL,
+               "ttlh_bfp4_unpack_host: rows and cols must be positive multiples of 32");
+  const uint8_t* in = static_cast<const uint8_t*>(src);
+  const int64_t nt_c = cols / 32;
+  for (int64_t tr = 0; tr < rows / 32; ++tr)
+    for (int64_t tc = 0; tc < nt_c; ++tc) {
+      const uint8_t* tile = in + (tr * nt_c + tc) * TTLH_BFP4_TILE_BYTES;
+      for (int r = 0; r < 32; ++r)
+        for (int c = 0; c < 32; ++c) {
+          const uint32_t nib = (tile[bfp4_elem_byte(r, c)] >> (4 * (c & 1))) & 0xfu;
+          dst[(tr * 32 + r) * cols + tc * 32 + c] = bfp4_decode_host(tile[bfp8_exp_off(r, c)], nib);
+        }
+    }
+  return TTLH_OK;
+}
+
+extern "C" int ttlh_bfp4_unpack(const void* src, void* dst_bf16, int64_t rows, int64_t cols,
+                                void* stream) {
+  clear_error();
+  TTLH_REQUIRE(src && dst_bf16, TTLH_EINVAL, "ttlh_bfp4_unpack: null pointer");
+  TTLH_REQUIRE(rows > 0 && cols > 0 && rows % 32 == 0 && cols % 32 == 0, TTLH_EINVAL,
+               "ttlh_bfp4_unpack: rows and cols must be positive multiples of 32");
+  TTLH_REQUIRE((reinterpret_cast<uintptr_t>(src) & 7) == 0 &&
+                   (reinterpret_cast<uintptr_t>(dst_bf16) & 15) == 0,
+               TTLH_EINVAL, "ttlh_bfp4_unpack: src must be 8-byte and dst 16-byte aligned");
+  const int64_t nt_c = cols / 32;
+  const int64_t ntiles = (rows / 32) * nt_c;
+  const int64_t blocks = (ntiles + 3) / 4;
+  TTLH_REQUIRE(blocks < (int64_t(1) << 31), TTLH_EUNSUPPORTED, "ttlh_bfp4_unpack: too large");
+  hipLaunchKernelGGL(bfp4_unpack_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint8_t*>(src),
+                     static_cast<uint16_t*>(dst_bf16), cols, ntiles, nt_c);
+  return check_launch("bfp4_unpack_kernel");
+}
+
+extern "C" int ttlh_matmul_bfp4w_ws(const void* A, int64_t lda, const void* Bq4, void* C,
+                                    int64_t ldc, int64_t M, int64_t N, int64_t K,
+                                    void* workspace, int64_t workspace_bytes, void* stream) {
+  clear_error();
+  TTLH_REQUIRE(workspace, TTLH_EINVAL, "ttlh_matmul_bfp4w_ws: null workspace");
+  TTLH_REQUIRE(K > 0 && N > 0 && workspace_bytes >= K * N * 2, TTLH_EINVAL,
+               "ttlh_matmul_bfp4w_ws: workspace of %lld bytes is smaller than K*N*2 = %lld",
+               (long long)workspace_bytes, (long long)(K > 0 && N > 0 ? K * N * 2 : 0));
+  TTLH_REQUIRE(A && Bq4 && C, TTLH_EINVAL, "ttlh_matmul_bfp4w_ws: null pointer");
+  TTLH_REQUIRE(M > 0 && M % 32 == 0 && N % 32 == 0 && K % 32 == 0, TTLH_EINVAL,
+               "ttlh_matmul_bfp4w_ws: M, N, K must be positive multiples of 32");
+  TTLH_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15) == 0, TTLH_EINVAL,
+               "ttlh_matmul_bfp4w_ws: workspace must be 16-byte aligned");
+  int st = ttlh_bfp4_unpack(Bq4, workspace, K, N, stream);
+  if (st != TTLH_OK) return st;
+  return ttlh_matmul(A, TTLH_BF16, lda, workspace, TTLH_BF16, N, C, TTLH_BF16, ldc, M, N, K, 0,
+                     stream);
+}

@@ -29,6 +29,7 @@ TTLH_F32 = 1
 TTLH_MAX_INSTR = 12
 TTLH_MAX_STACK = 3
 TTLH_BFP8_TILE_BYTES = 1088
+TTLH_BFP4_TILE_BYTES = 576
 
 # opcodes (enum ttlh_opcode)
 OP = {
@@ -73,6 +74,10 @@ SIGNATURES = {
     "ttlh_bfp8_unpack": (_int, [_vp, _vp, _i64, _i64, _vp]),
     "ttlh_matmul_bfp8w": (_int, [_vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
     "ttlh_matmul_bfp8w_workspace_bytes": (_i64, [_i64, _i64, _i64]),
+    "ttlh_bfp4_pack_host": (_int, [_vp, _vp, _i64, _i64]),
+    "ttlh_bfp4_unpack_host": (_int, [_vp, _vp, _i64, _i64]),
+    "ttlh_bfp4_unpack": (_int, [_vp, _vp, _i64, _i64, _vp]),
+    "ttlh_matmul_bfp4w_ws": (_int, [_vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp]),
     "ttlh_matmul_bfp8w_ws": (_int, [_vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp]),
     "ttlh_sdpa_fwd": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, C.c_float, _int, _vp]),
     "ttlh_last_error": (C.c_char_p, []),

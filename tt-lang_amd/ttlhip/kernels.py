@@ -185,6 +185,60 @@ def matmul_bfp8w(a: torch.Tensor, bq: torch.Tensor, c: torch.Tensor, stream=None
         ws.record_stream(stream)
 
 
+def bfp4_tiles_bytes(rows: int, cols: int) -> int:
+    if rows % 32 or cols % 32:
+        raise ValueError(f"bfloat4_b needs whole 32x32 tiles, got {rows}x{cols}")
+    return (rows // 32) * (cols // 32) * L.TTLH_BFP4_TILE_BYTES
+
+
+def bfp4_pack_host(x: torch.Tensor) -> torch.Tensor:
+    """fp32 [rows, cols] (host) -> uint8 bfloat4_b tile bytes (host)."""
+    x = x.detach().to("cpu", torch.float32).contiguous()
+    rows, cols = x.shape
+    out = torch.empty(bfp4_tiles_bytes(rows, cols), dtype=torch.uint8)
+    L.call("ttlh_bfp4_pack_host", x.data_ptr(), out.data_ptr(), rows, cols)
+    return out
+
+
+def bfp4_unpack_host(q: torch.Tensor, rows: int, cols: int) -> torch.Tensor:
+    q = q.detach().to("cpu", torch.uint8).contiguous()
+    if q.numel() != bfp4_tiles_bytes(rows, cols):
+        raise ValueError("bfloat4_b byte count does not match the shape")
+    out = torch.empty((rows, cols), dtype=torch.bfloat16)
+    L.call("ttlh_bfp4_unpack_host", q.data_ptr(), out.data_ptr(), rows, cols)
+    return out
+
+
+def bfp4_unpack(q: torch.Tensor, rows: int, cols: int, stream=None) -> torch.Tensor:
+    if not q.is_cuda:
+        raise RuntimeError("bfp4_unpack takes device tiles")
+    if q.numel() != bfp4_tiles_bytes(rows, cols) or q.dtype != torch.uint8:
+        raise ValueError("bfloat4_b byte count does not match the shape")
+    out = torch.empty((rows, cols), dtype=torch.bfloat16, device=q.device)
+    L.call("ttlh_bfp4_unpack", q.data_ptr(), out.data_ptr(), rows, cols, L.stream_ptr(stream))
+    return out
+
+
+def matmul_bfp4w(a: torch.Tensor, bq: torch.Tensor, c: torch.Tensor, stream=None) -> None:
+    """c[M,N] = a[M,K] (bf16) @ dequant(bq)[K,N] with bfloat4_b weights; the
+    dequantised weights go through a bf16 workspace from torch's allocator."""
+    _check_device(a, "matmul_bfp4w A")
+    _check_device(c, "matmul_bfp4w C")
+    M, K = a.shape
+    M2, N = c.shape
+    if M2 != M or a.dtype != torch.bfloat16 or c.dtype != torch.bfloat16:
+        raise ValueError("matmul_bfp4w takes bf16 A [M,K] and bf16 C [M,N]")
+    if not bq.is_cuda or bq.dtype != torch.uint8 or bq.numel() != bfp4_tiles_bytes(K, N):
+        raise ValueError("matmul_bfp4w: Bq must be device uint8 tiles of a K x N matrix")
+    if a.stride(1) != 1 or c.stride(1) != 1:
+        raise ValueError("matmul_bfp4w: A and C must be row-major")
+    ws = torch.empty(K * N * 2, dtype=torch.uint8, device=c.device)
+    L.call("ttlh_matmul_bfp4w_ws", a.data_ptr(), a.stride(0), bq.data_ptr(), c.data_ptr(),
+           c.stride(0), M, N, K, ws.data_ptr(), K * N * 2, L.stream_ptr(stream))
+    if stream is not None:
+        ws.record_stream(stream)
+
+
 def sdpa_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor, scale: float,
              causal: bool = False, stream=None) -> None:
     for t, nm in ((q, "Q"), (k, "K"), (v, "V"), (o, "O")):

@@ -49,8 +49,11 @@ class TensorRef:
     obj: Any = None
 
     def resolve(self, args: Dict[Any, Any]):
-        t = args[self.arg] if self.arg is not None else self.obj
+        t = self.resolve_obj(args)
         return t._tensor if hasattr(t, "_tensor") else t
+
+    def resolve_obj(self, args: Dict[Any, Any]):
+        return args[self.arg] if self.arg is not None else self.obj
 
 
 @dataclass
@@ -83,7 +86,7 @@ class MatmulLaunch:
     rows: Tuple[int, int]   # output element rows [r0, r1)
     cols: Tuple[int, int]   # output element cols [c0, c1)
     k: int
-    b_block: bool = False   # B is a block-float (bfloat8_b) tensor of packed tiles
+    b_block: bool = False   # B is a block-float (bfloat8_b / bfloat4_b) tensor
 
     def describe(self) -> str:
         return (f"matmul C[{self.rows[0]}:{self.rows[1]}, {self.cols[0]}:{self.cols[1]}] = "
@@ -448,6 +451,6 @@ def execute(plan: Plan, args: Dict[Any, Any], stream=None) -> None:
             r0, r1 = l.rows
             c0, c1 = l.cols
             if l.b_block:
-                Kn.matmul_bfp8w(a[r0:r1], b, c[r0:r1], stream=stream)
+                l.b.resolve_obj(args).dtype.matmul(a[r0:r1], b, c[r0:r1], stream=stream)
             else:
                 Kn.matmul(a[r0:r1], b[:, c0:c1], c[r0:r1, c0:c1], accumulate=False, stream=stream)

@@ -49,15 +49,38 @@ class BlockFloatType:
 
     compute_dtype = torch.bfloat16
 
-    def __init__(self, name: str, tile_bytes: int):
+    def __init__(self, name: str, tile_bytes: int, codec: str):
         self.name = name
         self.tile_bytes = tile_bytes
+        self.codec = codec  # "bfp8" | "bfp4": the ttlhip.kernels function prefix
 
     def __repr__(self) -> str:
         return f"DataType.{self.name.upper()}"
 
+    def _fn(self, what: str):
+        from ttlhip import kernels as K
 
-bfloat8_b = BlockFloatType("bfloat8_b", 1088)
+        return getattr(K, f"{self.codec}_{what}")
+
+    def pack(self, t: torch.Tensor) -> torch.Tensor:
+        """fp32 [rows, cols] (host) -> packed tile bytes (host)."""
+        return self._fn("pack_host")(t)
+
+    def unpack(self, q: torch.Tensor, rows: int, cols: int) -> torch.Tensor:
+        """Packed tiles -> bf16 [rows, cols] on q's device."""
+        if q.is_cuda:
+            return self._fn("unpack")(q, rows, cols)
+        return self._fn("unpack_host")(q, rows, cols)
+
+    def matmul(self, a: torch.Tensor, q: torch.Tensor, c: torch.Tensor, stream=None) -> None:
+        """c = a @ dequant(q) on the GPU (bf16 a and c)."""
+        from ttlhip import kernels as K
+
+        (K.matmul_bfp8w if self.codec == "bfp8" else K.matmul_bfp4w)(a, q, c, stream=stream)
+
+
+bfloat8_b = BlockFloatType("bfloat8_b", 1088, "bfp8")
+bfloat4_b = BlockFloatType("bfloat4_b", 576, "bfp4")
 
 TTNN_AVAILABLE = True
 
@@ -106,12 +129,8 @@ class Tensor:
         """Host copy; block-float tensors come back as float32 values (the
         conversion ttnn.to_torch applies to bfloat8_b)."""
         if self._block is not None:
-            from ttlhip import kernels as K
-
             rows, cols = self._logical_shape
-            if self._tensor.is_cuda:
-                return K.bfp8_unpack(self._tensor, rows, cols).float().cpu()
-            return K.bfp8_unpack_host(self._tensor, rows, cols).float()
+            return self._block.unpack(self._tensor, rows, cols).float().cpu()
         return self._tensor.detach().cpu()
 
     def __repr__(self) -> str:
@@ -201,11 +220,9 @@ def _shape(shape: Union[Sequence[int], int]) -> Tuple[int, ...]:
 
 def _block_from_fp32(t: torch.Tensor, block: BlockFloatType) -> Tensor:
     """fp32 [rows, cols] -> packed tiles in device memory (host codec)."""
-    from ttlhip import kernels as K
-
     if t.dim() != 2:
         raise ValueError(f"{block.name} tensors are 2-D, got shape {tuple(t.shape)}")
-    packed = K.bfp8_pack_host(t.to(torch.float32))
+    packed = block.pack(t.to(torch.float32))
     return Tensor(packed.to(_device()), block=block, logical_shape=tuple(t.shape))
 
 
@@ -252,8 +269,9 @@ def empty_like(t: Tensor, dtype=None, **_: Any) -> Tensor:
 
 def from_torch(tensor: torch.Tensor, dtype=None, layout: Any = None,
                device: Any = None, memory_config: Any = None, **_: Any) -> Tensor:
-    """Device copy of `tensor`; dtype=ttnn.bfloat8_b quantises it into packed
-    tiles (shared exponent per 16-element face row, round half to even)."""
+    """Device copy of `tensor`; dtype=ttnn.bfloat8_b / bfloat4_b quantises it
+    into packed tiles (shared exponent per 16-element face row, round half to
+    even)."""
     t = tensor.detach()
     if isinstance(dtype, BlockFloatType):
         return _block_from_fp32(t.cpu(), dtype)
@@ -282,8 +300,9 @@ def typecast(t: Tensor, dtype, **_: Any) -> Tensor:
 
 
 def matmul(a: Tensor, b: Tensor, **_: Any) -> Tensor:
-    """a @ b on the MI355X (bf16 / f32 MFMA, fp32 accumulation; a bfloat8_b
-    `b` goes through the bf16 x bfloat8_b GEMM).  The result is bfloat16 for
+    """a @ b on the MI355X (bf16 / f32 MFMA, fp32 accumulation; a block-float
+    `b` goes through the bf16 x bfloat8_b GEMM or, for bfloat4_b, a
+    dequantisation pass and the bf16 GEMM).  The result is bfloat16 for
     bfloat16 / block-float inputs, float32 for float32 ones."""
     from ttlhip import _lib
     from ttlhip import kernels as K
@@ -298,7 +317,7 @@ def matmul(a: Tensor, b: Tensor, **_: Any) -> Tensor:
         raise ValueError(f"matmul shapes {tuple(ta.shape)} @ {tuple(b.shape)} do not chain")
     if b.is_block_float:
         out = torch.empty((M, N), dtype=torch.bfloat16, device=ta.device)
-        K.matmul_bfp8w(ta.to(torch.bfloat16), b._tensor, out)
+        b.dtype.matmul(ta.to(torch.bfloat16), b._tensor, out)
         return Tensor(out)
     tb = b._tensor.contiguous()
     out_dtype = torch.float32 if torch.float32 in (ta.dtype, tb.dtype) else torch.bfloat16
