@@ -502,3 +502,100 @@ def make_matmul_split_rows(ttl, grid=(13, 10)):
                     ttl.copy(ob, out[t // nt, t % nt]).wait()
 
     return mm_split
+
+
+def make_row_bias_multicast(ttl, g=2, grid=(2, 4)):
+    """y = a + broadcast(bias_row): on every grid row, core (r, 0) reads the
+    (1, g)-tile bias block for each column block once per output column block and
+    multicasts it over a pipe to the other cores of its row, which use it for
+    their own row blocks (the eltwise_pipe.py pattern, one pipe per grid row)."""
+
+    @ttl.kernel(grid=grid)
+    def row_bias(a, bias, y):
+        gy, gx = ttl.grid_size(dims=2)
+        rt, ct = a.shape[0] // TILE, a.shape[1] // TILE
+        rows_per_core = rt // g // (gy * gx)
+        a_cb = ttl.make_circular_buffer_like(a, shape=(g, g), buffer_factor=2)
+        b_cb = ttl.make_circular_buffer_like(bias, shape=(1, g), buffer_factor=2)
+        y_cb = ttl.make_circular_buffer_like(y, shape=(g, g), buffer_factor=2)
+        pipes = [ttl.Pipe((r, 0), (r, slice(1, gx))) for r in range(gy)]
+        net = ttl.PipeNet(pipes)
+
+        @ttl.compute()
+        def comp():
+            for _ in range(ct // g):
+                with b_cb.wait() as bb:
+                    for _ in range(rows_per_core):
+                        with a_cb.wait() as ab, y_cb.reserve() as yb:
+                            yb.store(ab + ttl.math.broadcast(bb, dims=[0]))
+
+        @ttl.datamovement()
+        def reader():
+            c = ttl.core(dims=1)
+            for j in range(ct // g):
+                with b_cb.reserve() as bb:
+                    def send(p):
+                        ttl.copy(bias[0, j * g:(j + 1) * g], bb).wait()
+                        ttl.copy(bb, p).wait()
+
+                    def recv(p):
+                        ttl.copy(p, bb).wait()
+
+                    net.if_src(send)
+                    net.if_dst(recv)
+                for i in range(rows_per_core):
+                    r = (c * rows_per_core + i) * g
+                    with a_cb.reserve() as ab:
+                        ttl.copy(a[r:r + g, j * g:(j + 1) * g], ab).wait()
+
+        @ttl.datamovement()
+        def writer():
+            c = ttl.core(dims=1)
+            for j in range(ct // g):
+                for i in range(rows_per_core):
+                    r = (c * rows_per_core + i) * g
+                    with y_cb.wait() as yb:
+                        ttl.copy(yb, y[r:r + g, j * g:(j + 1) * g]).wait()
+
+    return row_bias
+
+
+def make_scalar_expand_add(ttl, ttnn):
+    """y = a + c with c a (1, 1) tensor expanded in the kernel body to one
+    32 x 32 tile (ttnn.repeat / squeeze, as eltwise_pipe.py does): the plan
+    refers to a tensor the body creates."""
+
+    @ttl.kernel(grid=(1, 2))
+    def scalar_add(a, c, y):
+        c_tile = ttnn.squeeze(ttnn.repeat(c, (1, 1, *ttl.TILE_SHAPE)))
+        rt, ct = a.shape[0] // TILE, a.shape[1] // TILE
+        a_cb = ttl.make_circular_buffer_like(a, shape=(1, 1), buffer_factor=2)
+        c_cb = ttl.make_circular_buffer_like(c_tile, shape=(1, 1), buffer_factor=1)
+        y_cb = ttl.make_circular_buffer_like(y, shape=(1, 1), buffer_factor=2)
+
+        @ttl.compute()
+        def comp():
+            with c_cb.wait() as cb:
+                for _ in range(rt * ct // 2):
+                    with a_cb.wait() as ab, y_cb.reserve() as yb:
+                        yb.store(ab + cb)
+
+        @ttl.datamovement()
+        def reader():
+            k = ttl.core(dims=1)
+            with c_cb.reserve() as cb:
+                ttl.copy(c_tile[0, 0], cb).wait()
+            for t in range(rt * ct // 2):
+                i = k * (rt * ct // 2) + t
+                with a_cb.reserve() as ab:
+                    ttl.copy(a[i // ct, i % ct], ab).wait()
+
+        @ttl.datamovement()
+        def writer():
+            k = ttl.core(dims=1)
+            for t in range(rt * ct // 2):
+                i = k * (rt * ct // 2) + t
+                with y_cb.wait() as yb:
+                    ttl.copy(yb, y[i // ct, i % ct]).wait()
+
+    return scalar_add

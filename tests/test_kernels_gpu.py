@@ -183,3 +183,25 @@ def test_matmul_split_rows_meets_metal_examples_ulp_bar():
     assert len(k.last_plan.launches) == 1
     golden = torch.matmul(ttnn.to_torch(a).to(torch.bfloat16), ttnn.to_torch(b).to(torch.bfloat16))
     assert_with_ulp(golden, ttnn.to_torch(c).to(torch.bfloat16))
+
+
+def test_row_bias_multicast_pipe_kernel_bitexact():
+    # blocks multicast over pipes become direct tile reads of the sent block's
+    # origin; per-op bf16 rounding = torch's bf16 add (pinned in test_oracle)
+    a = O.seeded((512, 256), "uniform", 31)
+    bias = O.seeded((1, 256), "uniform", 32)
+    got, k = _gpu(KL.make_row_bias_multicast, [a, bias, torch.zeros(512, 256, dtype=torch.bfloat16)], 2)
+    assert len(k.last_plan.launches) == 1
+    assert torch.equal(got, a + bias)
+
+
+def test_body_created_tensor_rebound_across_calls():
+    # the kernel body expands c to a tile with ttnn ops; a second call with a
+    # new c reuses the cached plan but must read the new expansion
+    k = KL.make_scalar_expand_add(ttl, ttnn)
+    a = O.seeded((64, 128), "uniform", 33)
+    y = ttnn.from_torch(torch.zeros(64, 128, dtype=torch.bfloat16))
+    for cval in (1.5, -2.0, 0.25):
+        k(ttnn.from_torch(a), ttnn.from_torch(torch.full((1, 1), cval, dtype=torch.bfloat16)), y)
+        assert torch.equal(ttnn.to_torch(y), a + torch.tensor(cval, dtype=torch.bfloat16))
+    assert len(k._cache) == 1

@@ -1,1 +1,2 @@
-"""Drop-in for the `sim` helpers tt-lang examples import (sim.testing)."""
+"""Drop-in for the `sim` helpers tt-lang examples import (sim.testing,
+sim.typedefs)."""

@@ -514,9 +514,144 @@ def copy(src, dst) -> CopyTransaction:
         tx = CopyTransaction(src, "src")
         ctx.add(Event("copy_out", src.cb, ctx.cur, {"block": src, "slice": dst}))
         return tx
+    if isinstance(src, Block) and isinstance(dst, SrcPipeIdentity):
+        tx = CopyTransaction(src, "src")
+        ctx.add(Event("pipe_send", src.cb, ctx.cur, {"block": src, "pipe": dst.pipe}))
+        return tx
+    if isinstance(src, DstPipeIdentity) and isinstance(dst, Block):
+        if dst.kind != "reserve":
+            raise TraceError("a pipe delivers into a block obtained from reserve()")
+        tx = CopyTransaction(dst, "dst")
+        ctx.add(Event("pipe_recv", dst.cb, ctx.cur, {"block": dst, "pipe": src.pipe}))
+        return tx
     raise NotImplementedError(
-        f"ttl.copy({type(src).__name__} -> {type(dst).__name__}) is not supported by the MI355X "
-        "backend (tensor<->block copies only; pipes are not implemented)")
+        f"ttl.copy({type(src).__name__} -> {type(dst).__name__}) is not supported (tensor <-> "
+        "block and block <-> pipe copies are)")
+
+
+# ---------------------------------------------------------------------------
+# pipes: core-to-core block transfers (python/sim/pipe.py:1-270,
+# python/sim/typedefs.py:41-90).  The tracer records sends and receives; the
+# planner gives a received block the tensor-tile origin of the matching sent
+# block (k-th send <-> k-th receive of a pipe), so on the GPU every receiving
+# workgroup reads that tile itself (through L2) instead of a core forwarding it.
+
+
+def _linear_core(coord) -> int:
+    if isinstance(coord, (int, np.integer)):
+        return int(coord)
+    g = _grid()
+    c = tuple(int(x) for x in coord)
+    if len(c) != len(g):
+        gs = grid_size(dims=len(c))
+        lin = 0
+        for x, s in zip(c, gs):
+            lin = lin * s + x
+        return lin
+    return flatten_core_index(c)
+
+
+def _expand_range(spec) -> List[int]:
+    """Linear ids of a destination: a core (int or coordinate tuple), a tuple
+    with slices (python/sim/pipe.py expand_core_range), or a (first, last)
+    pair of coordinate tuples (inclusive rectangle)."""
+    if isinstance(spec, (int, np.integer)):
+        return [int(spec)]
+    spec = tuple(spec)
+    if len(spec) == 2 and all(isinstance(x, tuple) for x in spec):
+        a, b = spec
+        ranges = [range(min(x, y), max(x, y) + 1) for x, y in zip(a, b)]
+    else:
+        gs = grid_size(dims=len(spec))
+        if not isinstance(gs, tuple):
+            gs = (gs,)
+        ranges = []
+        for i, item in enumerate(spec):
+            if isinstance(item, slice):
+                start = 0 if item.start is None else item.start
+                stop = gs[i] if item.stop is None else item.stop
+                ranges.append(range(start, stop, 1 if item.step is None else item.step))
+            else:
+                ranges.append(range(int(item), int(item) + 1))
+    out: List[int] = []
+
+    def walk(i, acc):
+        if i == len(ranges):
+            out.append(_linear_core(tuple(acc)))
+            return
+        for v in ranges[i]:
+            walk(i + 1, acc + [v])
+    walk(0, [])
+    return out
+
+
+_pipe_ids = itertools.count()
+
+
+class Pipe:
+    """A block transfer from `src_core` to the core(s) of `dst_core_range`
+    (unicast: one coordinate; multicast: a tuple with slices)."""
+
+    def __init__(self, src_core, dst_core_range):
+        self.id = next(_pipe_ids)
+        self.src_core = src_core
+        self.dst_core_range = dst_core_range
+
+    def _src(self) -> int:
+        return _linear_core(self.src_core)
+
+    def _dsts(self) -> List[int]:
+        return _expand_range(self.dst_core_range)
+
+    def has_current_core(self) -> bool:
+        """Whether the current core sends or receives on this pipe."""
+        c = core(dims=1)
+        return c == self._src() or c in self._dsts()
+
+    def __repr__(self) -> str:
+        return f"Pipe({self.src_core} -> {self.dst_core_range})"
+
+
+class SrcPipeIdentity:
+    """A pipe as seen by its source core (`dst` tells where blocks go)."""
+
+    def __init__(self, pipe: Pipe):
+        self.pipe = pipe
+
+    @property
+    def dst(self):
+        return self.pipe.dst_core_range
+
+
+class DstPipeIdentity:
+    """A pipe as seen by a destination core (`src` tells where blocks come from)."""
+
+    def __init__(self, pipe: Pipe):
+        self.pipe = pipe
+
+    @property
+    def src(self):
+        return self.pipe.src_core
+
+
+class PipeNet:
+    """Pipes grouped so a thread can run one callback per pipe it sends on
+    (`if_src`) and one per pipe it receives on (`if_dst`)."""
+
+    def __init__(self, pipes: Sequence[Pipe]):
+        self._pipes = list(pipes)
+
+    def if_src(self, fn: Callable[[SrcPipeIdentity], Any]) -> None:
+        c = core(dims=1)
+        for p in self._pipes:
+            if p._src() == c:
+                fn(SrcPipeIdentity(p))
+
+    def if_dst(self, fn: Callable[[DstPipeIdentity], Any]) -> None:
+        c = core(dims=1)
+        for p in self._pipes:
+            if c in p._dsts():
+                fn(DstPipeIdentity(p))
 
 
 def _check_slice_shape(s: TensorSlice, blk: Block) -> None:

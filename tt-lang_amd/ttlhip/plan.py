@@ -43,7 +43,9 @@ class PlanError(NotImplementedError):
 @dataclass
 class TensorRef:
     """A tensor the plan reads or writes: kernel argument `arg` (by position or
-    name) or, for tensors captured from an enclosing scope, the object."""
+    name), a tensor the kernel body created (arg = ("created", i), i-th in
+    creation order; obj = the trace-time one) or, for tensors captured from
+    an enclosing scope, the object."""
 
     arg: Any = None
     obj: Any = None
@@ -53,7 +55,11 @@ class TensorRef:
         return t._tensor if hasattr(t, "_tensor") else t
 
     def resolve_obj(self, args: Dict[Any, Any]):
-        return args[self.arg] if self.arg is not None else self.obj
+        if self.arg is None:
+            return self.obj
+        if isinstance(self.arg, tuple) and self.arg not in args:
+            return self.obj  # a body-created tensor: the one from the trace
+        return args[self.arg]
 
 
 @dataclass
@@ -96,6 +102,10 @@ class MatmulLaunch:
 @dataclass
 class Plan:
     launches: List[Any] = field(default_factory=list)
+    # tensors the kernel body created at trace time (bound by creation order
+    # on later calls) and whether any launch refers to one
+    created: List[Any] = field(default_factory=list)
+    uses_created: bool = False
 
     def describe(self) -> str:
         return "\n".join(l.describe() for l in self.launches)
@@ -118,25 +128,38 @@ def _thread_events(root) -> List[T.Event]:
     return list(T.iter_events(root))
 
 
-def _copy_table(events: List[T.Event], cb, n: int, kind: str) -> _CopyTable:
+def _copy_table(events: List[T.Event], cb, n: int, kind: str, received=None) -> _CopyTable:
+    """Tile origin of every block of `cb` from its copy events; with kind
+    "copy_in", blocks delivered by a pipe take their origin from `received`
+    (event -> (tensor, r0, c0) arrays over the event's instances)."""
     r0 = np.full(n, -1, dtype=np.int64)
     c0 = np.full(n, -1, dtype=np.int64)
     tensor = None
     for ev in events:
-        if ev.kind != kind or ev.cb is not cb:
+        if ev.cb is not cb:
             continue
-        blk, sl = ev.data["block"], ev.data["slice"]
+        if ev.kind == kind:
+            blk, sl = ev.data["block"], ev.data["slice"]
+            src_t = sl.tensor
+            shape = ev.domain_shape()
+            vr = T.broadcast_to_domain(sl.r0, shape).ravel()
+            vc = T.broadcast_to_domain(sl.c0, shape).ravel()
+        elif kind == "copy_in" and ev.kind == "pipe_recv":
+            blk = ev.data["block"]
+            shape = ev.domain_shape()
+            src_t, vr, vc = received(ev)
+        else:
+            continue
         if tensor is None:
-            tensor = sl.tensor
-        elif sl.tensor is not tensor:
+            tensor = src_t
+        elif src_t is not tensor:
             raise PlanError("one circular buffer is filled from / drained to more than one "
                             "tensor on a core; use one CB per tensor")
-        shape = ev.domain_shape()
         idx = T.broadcast_to_domain(blk.event.index, shape).ravel()
         if np.any(r0[idx] >= 0):
             raise PlanError("a block is copied more than once")
-        r0[idx] = T.broadcast_to_domain(sl.r0, shape).ravel()
-        c0[idx] = T.broadcast_to_domain(sl.c0, shape).ravel()
+        r0[idx] = vr
+        c0[idx] = vc
     if n and (tensor is None or np.any(r0 < 0)):
         what = "filled by ttl.copy" if kind == "copy_in" else "copied out"
         raise PlanError(f"every block of CB {cb.id} must be {what} exactly once "
@@ -184,13 +207,80 @@ def _tree_key(tree, leaf_ids: Dict[int, int]):
     return (tag,) + tuple(_tree_key(t, leaf_ids) for t in tree[1:])
 
 
+def _no_forwarding(ev: T.Event):
+    raise PlanError("a block received from one pipe and sent on another is not supported")
+
+
+def _pipe_instances(ev: T.Event) -> int:
+    return int(np.prod(ev.domain_shape())) if ev.domain_shape() else 1
+
+
+def _pipe_sends(core_traces, per_core) -> Dict[int, List[Tuple[Any, np.ndarray, np.ndarray]]]:
+    """pipe id -> origins of the blocks its source core sends, in send order:
+    one (tensor, r0, c0) per send event (arrays over the event's instances).
+    A sent block must have been filled from a tensor on the source core."""
+    sends: Dict[int, List] = {}
+    src_of: Dict[int, int] = {}
+    for ct, (events, fill_direct) in zip(core_traces, per_core):
+        for tmpl, _ in ct["threads"]:
+            for ev in events[id(tmpl)]:
+                if ev.kind != "pipe_send":
+                    continue
+                pipe = ev.data["pipe"]
+                if src_of.setdefault(pipe.id, ct["core"]) != ct["core"]:
+                    raise PlanError(f"{pipe} is sent on from two cores")
+                blk = ev.data["block"]
+                ft = fill_direct.get(blk.cb.id)
+                if ft is None:
+                    raise PlanError("a block sent on a pipe must be filled by ttl.copy from a "
+                                    "tensor on the sending core")
+                shape = ev.domain_shape()
+                idx = T.broadcast_to_domain(blk.event.index, shape).ravel()
+                sends.setdefault(pipe.id, []).append((ft.tensor, ft.r0[idx], ft.c0[idx]))
+    return sends
+
+
 def resolve(core_traces: List[Dict[str, Any]]) -> List[_Group]:
     """core_traces[c] = {"threads": [(template, root_node), ...]} for core c."""
     groups: Dict[Tuple, _Group] = {}
+    # pass 1: events and tensor-filled copy tables of every core, for pipe sends
+    pre = []
     for ct in core_traces:
         threads = ct["threads"]
         events = {id(tmpl): _thread_events(root) for tmpl, root in threads}
         totals = {id(tmpl): T.assign_indices(root) for tmpl, root in threads}
+        direct: Dict[int, _CopyTable] = {}
+        for tmpl, _ in threads:
+            if tmpl.kind != "dm":
+                continue
+            evs = events[id(tmpl)]
+            if not any(e.kind == "pipe_send" for e in evs):
+                continue
+            for cb in {id(e.cb): e.cb for e in evs if e.kind == "copy_in"}.values():
+                n = totals[id(tmpl)].get((cb.id, "reserve"), 0)
+                direct[cb.id] = _copy_table(evs, cb, n, "copy_in", received=_no_forwarding)
+        pre.append((events, direct, totals))
+    sends = _pipe_sends(core_traces, [(e, d) for e, d, _ in pre])
+
+    for ct, (events, _, totals) in zip(core_traces, pre):
+        threads = ct["threads"]
+        # k-th receive of a pipe on this core <-> k-th send of that pipe
+        recv_pos: Dict[int, int] = {}
+
+        def received(ev, _pos=recv_pos, _core=ct["core"]):
+            pipe = ev.data["pipe"]
+            k = _pos.get(pipe.id, 0)
+            _pos[pipe.id] = k + 1
+            lst = sends.get(pipe.id, [])
+            if k >= len(lst):
+                raise RuntimeError(f"Deadlock: core {_core} receives more blocks on {pipe} than its "
+                                   "source core sends")
+            tens, r0, c0 = lst[k]
+            n = _pipe_instances(ev)
+            if r0.size != n:
+                raise PlanError(f"{pipe}: a receive and the matching send run a different number "
+                                "of times")
+            return tens, r0, c0
         # producer / consumer of every CB on this core
         producers: Dict[int, Any] = {}
         consumers: Dict[int, Any] = {}
@@ -218,7 +308,8 @@ def resolve(core_traces: List[Dict[str, Any]]) -> List[_Group]:
         drain: Dict[int, _CopyTable] = {}
         for cid, cb in cbs.items():
             if cid in producers and producers[cid].kind == "dm":
-                fill[cid] = _copy_table(events[id(producers[cid])], cb, count[cid], "copy_in")
+                fill[cid] = _copy_table(events[id(producers[cid])], cb, count[cid], "copy_in",
+                                        received)
             if cid in consumers and consumers[cid].kind == "dm":
                 drain[cid] = _copy_table(events[id(consumers[cid])], cb, count[cid], "copy_out")
         # stores

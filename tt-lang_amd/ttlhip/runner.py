@@ -19,6 +19,8 @@ from typing import Any, Dict, List, Optional, Tuple
 import numpy as np
 import torch
 
+import ttnn
+
 from . import dsl
 from . import plan as P
 from . import trace as T
@@ -29,6 +31,17 @@ def _trace_print(*args, **kwargs):
     their prints are shown only with TTLH_TRACE_PRINT=1."""
     if os.environ.get("TTLH_TRACE_PRINT") == "1":
         print(*args, **kwargs)
+
+
+def _refs(plan: P.Plan):
+    for l in plan.launches:
+        if isinstance(l, P.EltwiseLaunch):
+            yield l.out
+            for spec in l.operands:
+                if spec is not None:
+                    yield spec.ref
+        else:
+            yield from (l.a, l.b, l.c)
 
 
 class KernelRunner:
@@ -71,12 +84,15 @@ class KernelRunner:
                                   self.func.__defaults__, self.func.__closure__)
         prev = dsl._kstate
         dsl._kstate = dsl._KernelState(self.grid)
+        prev_created, ttnn._created = ttnn._created, []
         try:
             body(*args, **kwargs)
             threads = list(dsl._kstate.threads)
             explicit = dsl._kstate.program_order
+            created = ttnn._created
         finally:
             dsl._kstate = prev
+            ttnn._created = prev_created
         if len(threads) != 3:
             raise ValueError(f"Kernel must define exactly 3 threads (compute, dm0, dm1), got "
                              f"{len(threads)}")
@@ -108,12 +124,36 @@ class KernelRunner:
         for k, a in kwargs.items():
             pos.setdefault(id(a), k)
 
+        made = {id(t): i for i, t in enumerate(created)}
+
         def tensor_ref(t):
             if id(t) in pos:
                 return P.TensorRef(arg=pos[id(t)])
+            if id(t) in made:
+                return P.TensorRef(arg=("created", made[id(t)]), obj=t)
             return P.TensorRef(obj=t)
 
-        return P.build_plan(groups, tensor_ref)
+        plan = P.build_plan(groups, tensor_ref)
+        plan.created = list(created)
+        plan.uses_created = any(isinstance(r.arg, tuple) for r in _refs(plan))
+        return plan
+
+    def _created_tensors(self, *args, **kwargs) -> List[Any]:
+        """Runs the kernel body again (no thread tracing) and returns the
+        tensors it creates, in creation order."""
+        g = dict(self.func.__globals__)
+        g["grid"] = self.grid
+        body = types.FunctionType(self.func.__code__, g, self.func.__name__,
+                                  self.func.__defaults__, self.func.__closure__)
+        prev = dsl._kstate
+        dsl._kstate = dsl._KernelState(self.grid)
+        prev_created, ttnn._created = ttnn._created, []
+        try:
+            body(*args, **kwargs)
+            return ttnn._created
+        finally:
+            dsl._kstate = prev
+            ttnn._created = prev_created
 
     def _trace_thread(self, t: dsl.ThreadTemplate, core: int):
         fn = t.rewritten()
@@ -140,12 +180,21 @@ class KernelRunner:
     def __call__(self, *args, **kwargs):
         key = self._cache_key(args, kwargs)
         plan = self._cache.get(key)
+        created = None
         if plan is None:
             plan = self.trace(*args, **kwargs)
             self._cache[key] = plan
+            created = plan.created
+        elif plan.uses_created:
+            created = self._created_tensors(*args, **kwargs)
+            if len(created) != len(plan.created):
+                raise RuntimeError("the kernel body created a different number of tensors than "
+                                   "when it was traced; cannot reuse the cached plan")
         self.last_plan = plan
         amap: Dict[Any, Any] = dict(enumerate(args))
         amap.update(kwargs)
+        if created is not None:
+            amap.update({("created", i): t for i, t in enumerate(created)})
         P.execute(plan, amap)
         if self.sync:
             torch.cuda.synchronize()

@@ -84,6 +84,11 @@ bfloat4_b = BlockFloatType("bfloat4_b", 576, "bfp4")
 
 TTNN_AVAILABLE = True
 
+# While a ttl.kernel body runs, the tensors it creates are appended here, so a
+# cached kernel plan can be bound to the same tensors of a later call (the
+# body is run again; tensors are matched by creation order).
+_created: Optional[List["Tensor"]] = None
+
 
 def _device() -> torch.device:
     return torch.device("cuda") if torch.cuda.is_available() else torch.device("cpu")
@@ -102,6 +107,8 @@ class Tensor:
         if not isinstance(tensor, torch.Tensor):
             raise TypeError(f"ttnn.Tensor wraps a torch.Tensor, got {type(tensor)}")
         self._tensor = tensor
+        if _created is not None:  # created while a kernel body runs
+            _created.append(self)
         # block-float tensors: _tensor holds the packed tile bytes (uint8)
         self._block = block
         self._logical_shape = tuple(logical_shape) if logical_shape is not None else None
@@ -288,6 +295,25 @@ def to_torch(t: Union[Tensor, torch.Tensor], **_: Any) -> torch.Tensor:
 
 def to_layout(t: Tensor, layout: Any, **_: Any) -> Tensor:
     return t
+
+
+def repeat(t: Tensor, repeats: Sequence[int], **_: Any) -> Tensor:
+    """torch.Tensor.repeat semantics (leading dimensions added as needed)."""
+    if t.is_block_float:
+        raise NotImplementedError("ttnn.repeat of a block-float tensor")
+    return Tensor(t._tensor.repeat(*[int(r) for r in repeats]))
+
+
+def squeeze(t: Tensor, dim: Optional[int] = None, **_: Any) -> Tensor:
+    if t.is_block_float:
+        raise NotImplementedError("ttnn.squeeze of a block-float tensor")
+    return Tensor(t._tensor.squeeze() if dim is None else t._tensor.squeeze(dim))
+
+
+def reshape(t: Tensor, shape: Sequence[int], **_: Any) -> Tensor:
+    if t.is_block_float:
+        raise NotImplementedError("ttnn.reshape of a block-float tensor")
+    return Tensor(t._tensor.reshape(tuple(shape)))
 
 
 def typecast(t: Tensor, dtype, **_: Any) -> Tensor:
