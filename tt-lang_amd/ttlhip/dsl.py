@@ -20,6 +20,7 @@ from __future__ import annotations
 import inspect
 import itertools
 import os
+import sys
 import types
 from typing import Any, Callable, Dict, List, Optional, Sequence, Tuple, Union
 
@@ -460,12 +461,25 @@ class Block:
         if len(e) != len(self):
             raise ValueError("Length mismatch in store()")
         ctx.add(Event("store", self.cb, ctx.cur,
-                      {"target": self, "expr": e, "acc": bool(acc), "thread": ctx.thread}))
+                      {"target": self, "expr": e, "acc": bool(acc), "thread": ctx.thread,
+                       "loc": _user_location()}))
         self._stores += 1
 
 
 # ---------------------------------------------------------------------------
 # copy
+
+
+_PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+
+
+def _user_location() -> Tuple[str, int]:
+    """(file, line) of the innermost caller outside this package: the kernel
+    source line a traced operation came from."""
+    f = sys._getframe(1)
+    while f is not None and os.path.dirname(os.path.abspath(f.f_code.co_filename)) == _PKG_DIR:
+        f = f.f_back
+    return (f.f_code.co_filename, f.f_lineno) if f is not None else ("?", 0)
 
 
 class CopyTransaction:

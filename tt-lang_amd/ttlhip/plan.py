@@ -78,6 +78,7 @@ class EltwiseLaunch:
     out: TensorRef
     region: Tuple[int, int, int, int]      # y0, x0, h, w (elements)
     tiles: int = 0
+    loc: Optional[Tuple[str, int]] = None  # kernel source line of the store()
 
     def describe(self) -> str:
         return (f"eltwise {len(self.prog.steps)} steps over {self.region[2]}x{self.region[3]} "
@@ -93,6 +94,7 @@ class MatmulLaunch:
     cols: Tuple[int, int]   # output element cols [c0, c1)
     k: int
     b_block: bool = False   # B is a block-float (bfloat8_b / bfloat4_b) tensor
+    loc: Optional[Tuple[str, int]] = None  # kernel source line of the store()
 
     def describe(self) -> str:
         return (f"matmul C[{self.rows[0]}:{self.rows[1]}, {self.cols[0]}:{self.cols[1]}] = "
@@ -177,6 +179,7 @@ class _Group:
     out_tensor: Any
     acc: bool
     dtype: torch.dtype
+    loc: Optional[Tuple[str, int]] = None
     out_rc: List[np.ndarray] = field(default_factory=list)     # [(N,2)]
     leaf_rc: List[List[np.ndarray]] = field(default_factory=list)
     order: List[np.ndarray] = field(default_factory=list)
@@ -355,7 +358,8 @@ def resolve(core_traces: List[Dict[str, Any]]) -> List[_Group]:
                        ev.data["acc"])
                 g = groups.get(key)
                 if g is None:
-                    g = _Group(e.tree, leaves, leaf_tensors, dt.tensor, ev.data["acc"], e.dtype)
+                    g = _Group(e.tree, leaves, leaf_tensors, dt.tensor, ev.data["acc"], e.dtype,
+                               ev.data.get("loc"))
                     groups[key] = g
                 g.out_rc.append(np.stack([out_r, out_c], 1))
                 g.leaf_rc.append(leaf_rc)
@@ -437,12 +441,14 @@ def build_plan(groups: List[_Group], tensor_ref) -> Plan:
         out_rc = np.concatenate(g.out_rc, 0)
         leaf_rc = [np.concatenate([li[k] for li in g.leaf_rc], 0) for k in range(len(g.leaf_blocks))]
         if g.tree[0] == "matmul" and g.tree[1][0] == "leaf" and g.tree[2][0] == "leaf":
-            plan.launches.append(_plan_matmul(g, out_rc, leaf_rc, tensor_ref))
+            launch = _plan_matmul(g, out_rc, leaf_rc, tensor_ref)
         elif _has(g.tree, "matmul"):
             raise PlanError("a tile matmul combined with other ops in one store() is not "
                             "supported; store the product on its own")
         else:
-            plan.launches.append(_plan_eltwise(g, out_rc, leaf_rc, tensor_ref))
+            launch = _plan_eltwise(g, out_rc, leaf_rc, tensor_ref)
+        launch.loc = g.loc
+        plan.launches.append(launch)
     return plan
 
 
@@ -520,28 +526,46 @@ def _plan_matmul(g: _Group, out_rc, leaf_rc, tensor_ref) -> MatmulLaunch:
 # execution
 
 
-def execute(plan: Plan, args: Dict[Any, Any], stream=None) -> None:
+def execute(plan: Plan, args: Dict[Any, Any], stream=None, events=None) -> None:
+    """Runs the plan's launches on the current (or given) stream.  With an
+    `events` list, a pair of timing events is recorded around every launch."""
     from . import kernels as Kn
     from ._lib import require_device
 
     require_device()
     for l in plan.launches:
-        if isinstance(l, EltwiseLaunch):
-            ops = []
-            for spec in l.operands:
-                if spec is None:
-                    ops.append(None)
-                    continue
-                ops.append(Kn.OperandMap(spec.ref.resolve(args), spec.row_mask, spec.col_mask,
-                                         spec.row_off, spec.col_off))
-            Kn.eltwise(l.prog, ops, l.out.resolve(args), region=l.region, stream=stream)
+        if events is not None:
+            # a short device spin ahead of the start event keeps the GPU busy
+            # while the host enqueues the launch, so the events bracket device
+            # time only (not the host's launch latency)
+            with torch.cuda.stream(stream if stream is not None else torch.cuda.current_stream()):
+                torch.cuda._sleep(200_000)
+            e0 = torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+        _execute_one(l, args, stream, Kn)
+        if events is not None:
+            e1 = torch.cuda.Event(enable_timing=True)
+            e1.record(stream)
+            events.append((e0, e1))
+
+
+def _execute_one(l, args, stream, Kn) -> None:
+    if isinstance(l, EltwiseLaunch):
+        ops = []
+        for spec in l.operands:
+            if spec is None:
+                ops.append(None)
+                continue
+            ops.append(Kn.OperandMap(spec.ref.resolve(args), spec.row_mask, spec.col_mask,
+                                     spec.row_off, spec.col_off))
+        Kn.eltwise(l.prog, ops, l.out.resolve(args), region=l.region, stream=stream)
+    else:
+        a, b, c = l.a.resolve(args), l.b.resolve(args), l.c.resolve(args)
+        if c.data_ptr() in (a.data_ptr(), b.data_ptr()):
+            raise ValueError("matmul output aliases an input")
+        r0, r1 = l.rows
+        c0, c1 = l.cols
+        if l.b_block:
+            l.b.resolve_obj(args).dtype.matmul(a[r0:r1], b, c[r0:r1], stream=stream)
         else:
-            a, b, c = l.a.resolve(args), l.b.resolve(args), l.c.resolve(args)
-            if c.data_ptr() in (a.data_ptr(), b.data_ptr()):
-                raise ValueError("matmul output aliases an input")
-            r0, r1 = l.rows
-            c0, c1 = l.cols
-            if l.b_block:
-                l.b.resolve_obj(args).dtype.matmul(a[r0:r1], b, c[r0:r1], stream=stream)
-            else:
-                Kn.matmul(a[r0:r1], b[:, c0:c1], c[r0:r1, c0:c1], accumulate=False, stream=stream)
+            Kn.matmul(a[r0:r1], b[:, c0:c1], c[r0:r1, c0:c1], accumulate=False, stream=stream)

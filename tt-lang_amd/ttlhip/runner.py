@@ -22,6 +22,7 @@ import torch
 import ttnn
 
 from . import dsl
+from . import profile
 from . import plan as P
 from . import trace as T
 
@@ -195,6 +196,13 @@ class KernelRunner:
         amap.update(kwargs)
         if created is not None:
             amap.update({("created", i): t for i, t in enumerate(created)})
+        if profile.enabled():
+            events: List[Any] = []
+            P.execute(plan, amap, events=events)
+            torch.cuda.synchronize()
+            times = [a.elapsed_time(b) * 1e3 for a, b in events]
+            print(profile.report(self.func.__name__, self.grid, plan, amap, times), flush=True)
+            return None
         P.execute(plan, amap)
         if self.sync:
             torch.cuda.synchronize()
