@@ -80,12 +80,13 @@ def test_sdpa_config5_sampled_heads():
         _check(out[b:b + 1, h:h + 1], ref)
 
 
+@pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("scale", [-0.09, 0.0])
 @pytest.mark.parametrize("causal", [False, True])
-def test_sdpa_negative_and_zero_scale(scale, causal):
+def test_sdpa_negative_and_zero_scale(scale, causal, D):
     # a negative scale flips which raw score is the row maximum; scale 0 is
     # uniform attention (plain / prefix mean of V)
-    q, k, v = _qkv(1, 2, 256, 64, 31)
+    q, k, v = _qkv(1, 2, 256, D, 31)
     out = _run(q, k, v, scale, causal=causal)
     _check(out, O.sdpa_ref(q, k, v, scale, causal=causal))
     if scale == 0.0:
@@ -93,6 +94,20 @@ def test_sdpa_negative_and_zero_scale(scale, causal):
         mean = (vd.cumsum(2) / torch.arange(1, 257, dtype=torch.float64).view(1, 1, -1, 1)
                 if causal else vd.mean(2, keepdim=True).expand_as(vd))
         assert float((out.double() - mean).abs().max()) <= 1e-2 * float(mean.abs().max())
+
+
+@pytest.mark.parametrize("B,H,S", [(1, 3, 1024), (3, 1, 512)])
+def test_sdpa_several_query_blocks(B, H, S):
+    # several 256-query workgroups per head and several KV double-buffer
+    # cycles; V = 1 in the second head (or batch) pins the row sums exactly
+    q, k, v = _qkv(B, H, S, 128, 61)
+    v[-1, -1] = 1.0
+    scale = 1.0 / math.sqrt(128)
+    out = _run(q, k, v, scale)
+    ref = O.sdpa_ref(q, k, v, scale)
+    rest = (slice(0, B - 1),) if B > 1 else (slice(None), slice(0, H - 1))
+    _check(out[rest], ref[rest])
+    assert float((out[-1, -1].float() - 1.0).abs().max()) <= 2 ** -7
 
 
 def test_sdpa_causal_d64_and_value_layout():
