@@ -19,6 +19,9 @@ are in HBM before the timed region; elementwise configs rotate buffer sets
 totalling > 256 MB so the Infinity Cache cannot serve them.  The K timed
 steps are captured once into a HIP graph and replayed, so host overhead does
 not pad short kernels; HIP events on the launch stream bracket the replay.
+MFMA workloads time at least MFMA_MIN_MS of work (their step count is raised
+from a short probe): the engine clock ramps up after the idle gap before a
+replay, and 20 steps of a 0.1 ms GEMM would mostly measure that ramp.
 """
 
 from __future__ import annotations
@@ -38,6 +41,7 @@ for _p in (os.path.join(ROOT, "tests"), os.path.join(ROOT, "tt-lang_amd"), ROOT)
 import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+MFMA_MIN_MS = 30.0             # timed work per MFMA workload (ms), at least
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
@@ -332,12 +336,25 @@ WORKLOADS = {
 HEADLINE = "exp_bcast_mul_4096"
 
 
-def measure(w: Workload, steps: int, warmup: int, use_graph: bool = True) -> dict:
+def measure(w: Workload, steps: int, warmup: int, use_graph: bool = True,
+            min_ms: float = 0.0) -> dict:
+    """Times `steps` steps (at least `min_ms` of work when min_ms > 0: the step
+    count is raised from a probe of a few eager steps, capped at 1000)."""
     w.setup()
     for i in range(warmup):
         w.launch(i)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
+    if min_ms > 0.0:
+        p0 = torch.cuda.Event(enable_timing=True)
+        p1 = torch.cuda.Event(enable_timing=True)
+        p0.record(stream)
+        for i in range(3):
+            w.launch(i)
+        p1.record(stream)
+        torch.cuda.synchronize()
+        est = max(p0.elapsed_time(p1) / 3, 1e-3)
+        steps = max(steps, min(1000, math.ceil(min_ms / est)))
     g = None
     if use_graph:
         s = torch.cuda.Stream()
@@ -386,8 +403,8 @@ def traffic_for(name: str):
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--only", default="", help="comma-separated workload names")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
@@ -414,14 +431,18 @@ def main() -> int:
     results = {}
     for n in names:
         w = WORKLOADS[n]()
+        # MFMA workloads: the timed graph covers >= MFMA_MIN_MS of steady work
+        # (the clock ramps after the idle gap before a replay; a 20-step
+        # replay of a 0.1 ms GEMM is mostly ramp)
         steps = args.steps if w.unit == "GB/s" else max(1, min(args.steps, 20))
         warm = args.warmup if w.unit == "GB/s" else max(1, min(args.warmup, 3))
-        log(f"[bench] {n}: steps={steps} warmup={warm}")
-        r = measure(w, steps, warm, use_graph=not args.no_graph)
+        min_ms = 0.0 if w.unit == "GB/s" else MFMA_MIN_MS
+        log(f"[bench] {n}: steps={steps}{'+' if min_ms else ''} warmup={warm}")
+        r = measure(w, steps, warm, use_graph=not args.no_graph, min_ms=min_ms)
         r["parity"] = w.check()
         r["traffic"] = traffic_for(n)
         results[n] = r
-        log(f"[bench] {n}: {r['ms_per_step'] * 1e3:.2f} us/step {r['achieved']:.1f} {r['unit']} "
+        log(f"[bench] {n}: {r['steps']} steps, {r['ms_per_step'] * 1e3:.2f} us/step {r['achieved']:.1f} {r['unit']} "
             f"({r['frac'] * 100:.1f}%) parity={r['parity']}")
         del w
         torch.cuda.empty_cache()
