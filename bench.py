@@ -12,6 +12,7 @@ own roofline figures:
   C3 bf16 matmul 4096^3       tt-lang kernel (multicore style)     TFLOP/s
   C4 bf16 x bfp8 4096x4096x11008   ttlh_matmul_bfp8w_ws (two-pass)  TFLOP/s
   C5 SDPA [4,32,4096,128]     ttlh_sdpa_fwd                        TFLOP/s
+  row sums 4096^2 (spec reduce_sum)  tt-lang kernel (reduce_rows)  HBM GB/s
 
 A "step" is one pass of the hot path over one batch of synthetic input: one
 execution of the kernel's launch plan over one resident buffer set.  Inputs
@@ -181,6 +182,48 @@ class EltwiseWorkload(PlanWorkload):
                                          "unit": "GB/s", "cores": nthr}}
 
 
+class ReduceWorkload(PlanWorkload):
+    """Row sums of a bf16 matrix through a tt-lang kernel
+    (ttl.math.reduce_sum(x, s, dims=[1]) over (2, 16)-tile blocks accumulated
+    with store(acc=True), 8x8 grid) -> one ttlh_reduce launch; HBM-bound."""
+
+    def __init__(self, name, n, seed=4321):
+        self.name, self.n, self.seed = name, n, seed
+        self.config = (f"row sums out[r] = sum_c x[r, c] * s, x bf16 {n}x{n} U[-2,2], s = 1, "
+                       f"bf16 out {n}x1 (spec reduce_sum, dims=[1])")
+
+    def kernel_name(self):
+        return "reduce_rows_kernel"
+
+    def work_per_step(self):
+        return self.n * self.n * 2 + self.n * 2
+
+    def make_sets(self):
+        import kernel_lib as KL
+        import ttl
+        import ttnn
+        from oracle.tile_ops import seeded
+        self.kernel = KL.make_reduce_rows(ttl, kind="sum", gr=2, gc=16, grid=(8, 8))
+        self.x = seeded((self.n, self.n), "uniform", self.seed, lo=-2, hi=2)
+        x = ttnn.from_torch(self.x)
+        sc = ttnn.from_torch(torch.ones(32, 32, dtype=torch.bfloat16))
+        nsets = max(3, math.ceil(300e6 / self.work_per_step()))
+        sets = []
+        for i in range(nsets):
+            xi = x if i == 0 else ttnn.Tensor(x._tensor.clone())
+            sets.append([xi, sc, ttnn.empty((self.n, 1), dtype=torch.bfloat16)])
+        return sets
+
+    def check(self):
+        from oracle import tile_ops as O
+        self.launch(0)
+        torch.cuda.synchronize()
+        exact = self.x.double().sum(1, keepdim=True).float().bfloat16()
+        ulp = O.bf16_ulp_diff(self.sets[0][-1].to_torch(), exact)
+        return {"max_ulp": int(ulp.max()), "mismatch_frac": float((ulp > 0).float().mean()),
+                "oracle": "float64 row sums rounded once to bf16"}
+
+
 class MatmulWorkload(PlanWorkload):
     """C3 through the multicore-style tt-lang kernel (13x10 grid, (1,1) CBs,
     store(acc=True) over K) -> one MFMA GEMM launch."""
@@ -332,6 +375,7 @@ WORKLOADS = {
     "matmul_bfp8w_4096x11008": lambda: Bfp8MatmulWorkload("matmul_bfp8w_4096x11008", 4096,
                                                           11008, 4096),
     "sdpa_4x32x4096x128": lambda: SdpaWorkload("sdpa_4x32x4096x128", 4, 32, 4096, 128),
+    "reduce_sum_rows_4096": lambda: ReduceWorkload("reduce_sum_rows_4096", 4096),
 }
 HEADLINE = "exp_bcast_mul_4096"
 

@@ -146,6 +146,43 @@ int ttlh_eltwise(const ttlh_instr* prog, const ttlh_operand* in, int n_instr,
                  int64_t x0, int64_t h, int64_t w, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Scaled reductions of a tile program
+ *
+ * The spec's ttl.math.reduce_sum / reduce_max (docs/sphinx/specs/
+ * TTLangSpecification.md:754-755: "scaled sum / maximum reduction over the
+ * specified dimensions"); the reference has no implementation (neither the
+ * compiler's op table nor the simulator), so the semantics are fixed here:
+ *   v(y, x) = the value `prog` computes for iteration element (y, x) of the
+ *             region [y0, y0+h) x [x0, x0+w), operands addressed exactly as
+ *             in ttlh_eltwise (per-step rounding included);
+ *   s       = scale_imm * (*scaler) (scaler NULL: s = scale_imm);
+ *   result  = sum or NaN-propagating max of v * s over the reduced
+ *             dimension(s), products and accumulation in fp32, rounded once
+ *             (RNE) to out_dtype.
+ * dims: TTLH_REDUCE_DIM0 reduces over rows (one value per column, written
+ * at out[x - x0]), TTLH_REDUCE_DIM1 over columns (one value per row, at
+ * out[(y - y0) * out_ld]), both bits: one value at out[0].  out_pad = 1
+ * writes whole 32-wide result tiles instead, the reduced position(s) of
+ * every tile being 0 (column reduce: rows 1..31 under each value zeroed;
+ * row reduce: columns 1..31 after each value; both: the 32x32 tile).
+ * Summation order is fixed by the launch shape, so results repeat exactly
+ * for equal arguments.  Row reductions need no workspace; the others take
+ * ttlh_reduce_workspace_bytes(dims, h, w) bytes of caller-owned device
+ * memory (fp32 partial results).                                          */
+#define TTLH_REDUCE_SUM 0
+#define TTLH_REDUCE_MAX 1
+#define TTLH_REDUCE_DIM0 1
+#define TTLH_REDUCE_DIM1 2
+
+int64_t ttlh_reduce_workspace_bytes(int dims, int64_t h, int64_t w);
+
+int ttlh_reduce(const ttlh_instr* prog, const ttlh_operand* in, int n_instr,
+                int kind, int dims, const void* scaler, int scaler_dtype,
+                float scale_imm, void* out, int out_dtype, int64_t out_ld,
+                int out_pad, int64_t y0, int64_t x0, int64_t h, int64_t w,
+                void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
  * Tile matmul:  C[M,N] (=|+=) A[M,K] . B[K,N]
  *
  * Replaces Block.__matmul__ + store(acc=True) over the K tiles

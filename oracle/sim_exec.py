@@ -20,6 +20,14 @@ they follow:
   - store(acc=True): first store assigns, later ones add in the stored
     tensors' dtype (block.py:805-868).
   - grid / core / grid_size (kernel.py:89-291); grid "auto" = (8, 8).
+  - ttl.math.reduce_sum / reduce_max (spec TTLangSpecification.md:754-755;
+    no reference implementation exists, the semantics are the ones the
+    backend defines): every element times the scaler (first element of its
+    tile, or a number), summed / maximised (NaN-propagating) in float64 over
+    the block's element rows ([0]), columns ([1]) or both, rounded to the
+    block dtype (via fp32); result tiles are 32x32 with the values in row /
+    column 0 ([0, 0] for both) and zeros elsewhere.  Copying such a tile to a
+    size-1 tensor dimension keeps its first row / column.
 The oracle takes plain CPU torch tensors and is driven through `make_ttl()`,
 which returns a namespace with the same names as `ttl`.
 """
@@ -203,6 +211,41 @@ class _Block(_Tiles):
             self._first_acc = False
 
 
+def _reduce(kind: str, x, scaler, dims) -> _Tiles:
+    t = _tiles_of(x)
+    dims = sorted(int(d) for d in dims)
+    if isinstance(scaler, (int, float)):
+        sv = float(scaler)
+    else:
+        sv = float(_tiles_of(scaler).tiles[0].reshape(-1)[0])
+    R, C = t.shape
+    th, tw = t.tiles[0].shape
+    m = torch.stack(t.tiles).double().reshape(R, C, th, tw).permute(0, 2, 1, 3)
+    m = m.reshape(R * th, C * tw) * sv
+    fn = (lambda v, d: v.sum(d)) if kind == "sum" else (lambda v, d: v.amax(d))
+    dtype = t.tiles[0].dtype
+    def fin(v):
+        return v.to(torch.float32).to(dtype)
+    out = []
+    if dims == [0, 1]:
+        tile = torch.zeros(TILE, TILE, dtype=dtype)
+        tile[0, 0] = fin(fn(m.reshape(-1), 0))
+        return _Tiles([tile], (1, 1))
+    if dims == [1]:  # one value per element row, tiles (R, 1)
+        v = fin(fn(m, 1))
+        for i in range(R):
+            tile = torch.zeros(TILE, TILE, dtype=dtype)
+            tile[:th, 0] = v[i * th:(i + 1) * th]
+            out.append(tile)
+        return _Tiles(out, (R, 1))
+    v = fin(fn(m, 0))  # dims [0]: one value per element column, tiles (1, C)
+    for j in range(C):
+        tile = torch.zeros(TILE, TILE, dtype=dtype)
+        tile[0, :tw] = v[j * tw:(j + 1) * tw]
+        out.append(tile)
+    return _Tiles(out, (1, C))
+
+
 def _copy(src, dst):
     if isinstance(src, _Slice) and isinstance(dst, _Block):
         if src.tiles_shape() != dst.shape:
@@ -219,7 +262,11 @@ def _copy(src, dst):
         h, w = src.shape
         for k, i in enumerate(src.idx):
             r, c = divmod(k, w)
-            e[r * TILE:(r + 1) * TILE, c * TILE:(c + 1) * TILE] = src.cb.slots[i]
+            view = e[r * TILE:(r + 1) * TILE, c * TILE:(c + 1) * TILE]
+            tile = src.cb.slots[i]
+            if tuple(tile.shape) != tuple(view.shape):  # a result tile into a size-1 dimension
+                tile = tile[:view.shape[0], :view.shape[1]]
+            view.copy_(tile)
     else:
         raise NotImplementedError("oracle copy supports tensor<->block only")
 
@@ -300,6 +347,8 @@ def make_ttl():
         setattr(_Math, name, staticmethod(lambda x, _f=fn: _tiles_of(x).map(_f)))
     _Math.max = staticmethod(lambda a, b: _tiles_of(a)._bin(b, torch.maximum))
     _Math.min = staticmethod(lambda a, b: _tiles_of(a)._bin(b, torch.minimum))
+    _Math.reduce_sum = staticmethod(lambda x, scaler, dims=None: _reduce("sum", x, scaler, dims))
+    _Math.reduce_max = staticmethod(lambda x, scaler, dims=None: _reduce("max", x, scaler, dims))
 
     def kernel(grid="auto"):
         actual = (8, 8) if grid == "auto" else tuple(grid)

@@ -599,3 +599,174 @@ def make_scalar_expand_add(ttl, ttnn):
                     ttl.copy(yb, y[i // ct, i % ct]).wait()
 
     return scalar_add
+
+
+def make_reduce_rows(ttl, kind="sum", gr=2, gc=4, grid=(2, 2), scaler_const=None):
+    """out[r] = reduce_<kind> over the columns of x[r, :] * s (ttl.math.reduce_*,
+    dims=[1], spec TTLangSpecification.md:754-755): (gr, gc)-tile blocks, the
+    column blocks of a row accumulated with store(acc=True) when there are
+    several.  The scaler is the (1, 1) tile s[0, 0], or a number."""
+
+    @ttl.kernel(grid=grid)
+    def reduce_rows(x, s, out):
+        gx, gy = ttl.grid_size(dims=2)
+        rows_per_core = x.shape[0] // TILE // gr // (gx * gy)
+        nk = x.shape[1] // TILE // gc
+        x_cb = ttl.make_circular_buffer_like(x, shape=(gr, gc), buffer_factor=2)
+        s_cb = ttl.make_circular_buffer_like(s, shape=(1, 1), buffer_factor=1)
+        o_cb = ttl.make_circular_buffer_like(out, shape=(gr, 1), buffer_factor=2)
+        red = ttl.math.reduce_sum if kind == "sum" else ttl.math.reduce_max
+
+        @ttl.compute()
+        def comp():
+            with s_cb.wait() as sb:
+                scaler = sb if scaler_const is None else scaler_const
+                for _ in range(rows_per_core):
+                    with o_cb.reserve() as ob:
+                        for _ in range(nk):
+                            with x_cb.wait() as xb:
+                                ob.store(red(xb, scaler, dims=[1]), acc=nk > 1)
+
+        @ttl.datamovement()
+        def reader():
+            c = ttl.core(dims=1)
+            with s_cb.reserve() as sb:
+                ttl.copy(s[0, 0], sb).wait()
+            for i in range(rows_per_core):
+                r = (c * rows_per_core + i) * gr
+                for k in range(nk):
+                    with x_cb.reserve() as xb:
+                        ttl.copy(x[r:r + gr, k * gc:(k + 1) * gc], xb).wait()
+
+        @ttl.datamovement()
+        def writer():
+            c = ttl.core(dims=1)
+            for i in range(rows_per_core):
+                r = (c * rows_per_core + i) * gr
+                with o_cb.wait() as ob:
+                    ttl.copy(ob, out[r:r + gr, 0]).wait()
+
+    return reduce_rows
+
+
+def make_reduce_cols(ttl, kind="sum", gr=4, gc=2, grid=(2, 2)):
+    """out[:, c] = reduce_<kind> over the rows of x[:, c] * s (dims=[0]):
+    (gr, gc)-tile blocks, the row blocks of a column range accumulated with
+    store(acc=True) when there are several."""
+
+    @ttl.kernel(grid=grid)
+    def reduce_cols(x, s, out):
+        gx, gy = ttl.grid_size(dims=2)
+        cols_per_core = x.shape[1] // TILE // gc // (gx * gy)
+        nk = x.shape[0] // TILE // gr
+        x_cb = ttl.make_circular_buffer_like(x, shape=(gr, gc), buffer_factor=2)
+        s_cb = ttl.make_circular_buffer_like(s, shape=(1, 1), buffer_factor=1)
+        o_cb = ttl.make_circular_buffer_like(out, shape=(1, gc), buffer_factor=2)
+        red = ttl.math.reduce_sum if kind == "sum" else ttl.math.reduce_max
+
+        @ttl.compute()
+        def comp():
+            with s_cb.wait() as sb:
+                for _ in range(cols_per_core):
+                    with o_cb.reserve() as ob:
+                        for _ in range(nk):
+                            with x_cb.wait() as xb:
+                                ob.store(red(xb, sb, dims=[0]), acc=nk > 1)
+
+        @ttl.datamovement()
+        def reader():
+            c = ttl.core(dims=1)
+            with s_cb.reserve() as sb:
+                ttl.copy(s[0, 0], sb).wait()
+            for j in range(cols_per_core):
+                col = (c * cols_per_core + j) * gc
+                for k in range(nk):
+                    with x_cb.reserve() as xb:
+                        ttl.copy(x[k * gr:(k + 1) * gr, col:col + gc], xb).wait()
+
+        @ttl.datamovement()
+        def writer():
+            c = ttl.core(dims=1)
+            for j in range(cols_per_core):
+                col = (c * cols_per_core + j) * gc
+                with o_cb.wait() as ob:
+                    ttl.copy(ob, out[0, col:col + gc]).wait()
+
+    return reduce_cols
+
+
+def make_reduce_all(ttl, kind="max"):
+    """out = reduce_<kind> of exp(x) * y over a whole (R, C)-tile block on one
+    core (dims=[0, 1]), scaler s[0, 0]."""
+
+    @ttl.kernel(grid=(1, 1))
+    def reduce_all(x, y, s, out):
+        R, C = x.shape[0] // TILE, x.shape[1] // TILE
+        x_cb = ttl.make_circular_buffer_like(x, shape=(R, C), buffer_factor=1)
+        y_cb = ttl.make_circular_buffer_like(y, shape=(R, C), buffer_factor=1)
+        s_cb = ttl.make_circular_buffer_like(s, shape=(1, 1), buffer_factor=1)
+        o_cb = ttl.make_circular_buffer_like(out, shape=(1, 1), buffer_factor=1)
+        red = ttl.math.reduce_sum if kind == "sum" else ttl.math.reduce_max
+
+        @ttl.compute()
+        def comp():
+            with x_cb.wait() as xb, y_cb.wait() as yb, s_cb.wait() as sb, \
+                    o_cb.reserve() as ob:
+                ob.store(red(ttl.math.exp(xb) * yb, sb, dims=[0, 1]))
+
+        @ttl.datamovement()
+        def reader():
+            with x_cb.reserve() as xb, y_cb.reserve() as yb, s_cb.reserve() as sb:
+                tx = ttl.copy(x[0:R, 0:C], xb)
+                ty = ttl.copy(y[0:R, 0:C], yb)
+                ts = ttl.copy(s[0, 0], sb)
+                tx.wait()
+                ty.wait()
+                ts.wait()
+
+        @ttl.datamovement()
+        def writer():
+            with o_cb.wait() as ob:
+                ttl.copy(ob, out[0, 0]).wait()
+
+    return reduce_all
+
+
+def make_row_dot(ttl, gr=2, gc=4, grid=(2, 2)):
+    """out[r] = sum over c of a[r, c] * b[r, c] (reduce_sum of a product, a
+    constant scaler of 1), one block per row run of tiles."""
+
+    @ttl.kernel(grid=grid)
+    def row_dot(a, b, out):
+        gx, gy = ttl.grid_size(dims=2)
+        rows_per_core = a.shape[0] // TILE // gr // (gx * gy)
+        a_cb = ttl.make_circular_buffer_like(a, shape=(gr, gc), buffer_factor=2)
+        b_cb = ttl.make_circular_buffer_like(b, shape=(gr, gc), buffer_factor=2)
+        o_cb = ttl.make_circular_buffer_like(out, shape=(gr, 1), buffer_factor=2)
+
+        @ttl.compute()
+        def comp():
+            for _ in range(rows_per_core):
+                with a_cb.wait() as ab, b_cb.wait() as bb, o_cb.reserve() as ob:
+                    ob.store(ttl.math.reduce_sum(ab * bb, 1.0, dims=[1]))
+
+        @ttl.datamovement()
+        def reader():
+            c = ttl.core(dims=1)
+            for i in range(rows_per_core):
+                r = (c * rows_per_core + i) * gr
+                with a_cb.reserve() as ab, b_cb.reserve() as bb:
+                    ta = ttl.copy(a[r:r + gr, 0:gc], ab)
+                    tb = ttl.copy(b[r:r + gr, 0:gc], bb)
+                    ta.wait()
+                    tb.wait()
+
+        @ttl.datamovement()
+        def writer():
+            c = ttl.core(dims=1)
+            for i in range(rows_per_core):
+                r = (c * rows_per_core + i) * gr
+                with o_cb.wait() as ob:
+                    ttl.copy(ob, out[r:r + gr, 0]).wait()
+
+    return row_dot

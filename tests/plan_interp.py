@@ -9,7 +9,7 @@ against the oracle's eager executor without a GPU.
 import torch
 
 from ttlhip import _lib as L
-from ttlhip.plan import EltwiseLaunch, MatmulLaunch
+from ttlhip.plan import EltwiseLaunch, MatmulLaunch, ReduceLaunch
 
 _TORCH_BIN = {
     L.OP["add"]: torch.add, L.OP["sub"]: torch.sub, L.OP["mul"]: torch.mul,
@@ -40,7 +40,8 @@ def _rnd(x, r):
     return x.to(torch.bfloat16).float() if r == L.TTLH_BF16 else x
 
 
-def run_eltwise(l: EltwiseLaunch, args):
+def _values(l, args):
+    """The launch's stack program over its region, with per-step rounding."""
     y0, x0, h, w = l.region
     acc, stack = None, []
     for s, spec in zip(l.prog.steps, l.operands):
@@ -68,8 +69,40 @@ def run_eltwise(l: EltwiseLaunch, args):
         else:
             acc = _TORCH_BIN[s.op](stack.pop(), acc)
         acc = _rnd(acc, s.rnd)
+    return acc
+
+
+def run_eltwise(l: EltwiseLaunch, args):
+    y0, x0, h, w = l.region
+    acc = _values(l, args)
     out = l.out.resolve(args)
     out[y0:y0 + h, x0:x0 + w] = acc.to(out.dtype).to(out.device)
+
+
+def run_reduce(l: ReduceLaunch, args):
+    v = _values(l, args).double()
+    s = l.scale
+    if l.scaler is not None:
+        r, c = l.scaler_at
+        s *= float(l.scaler.resolve(args)[r, c])
+    v = v * s
+    dims = tuple(l.dims)
+    fn = (lambda t, d: t.sum(d)) if l.kind == "sum" else (lambda t, d: t.amax(d))
+    out = l.out.resolve(args)
+    oy, ox = l.out_origin
+    if dims == (0, 1):
+        res = fn(v.reshape(-1), 0).reshape(1, 1)
+    elif dims == (1,):
+        res = fn(v, 1).reshape(-1, 1)
+    else:
+        res = fn(v, 0).reshape(1, -1)
+    res = res.to(torch.float32).to(out.dtype)
+    rh, rw = res.shape
+    if l.out_pad:  # whole 32-wide result tiles, zeros beside the values
+        ph = 32 if 0 in dims else rh
+        pw = 32 if 1 in dims else rw
+        out[oy:oy + ph, ox:ox + pw] = 0
+    out[oy:oy + rh, ox:ox + rw] = res.to(out.device)
 
 
 def run_matmul(l: MatmulLaunch, args):
@@ -85,4 +118,9 @@ def run_matmul(l: MatmulLaunch, args):
 
 def run(plan, args):
     for l in plan.launches:
-        (run_eltwise if isinstance(l, EltwiseLaunch) else run_matmul)(l, args)
+        if isinstance(l, ReduceLaunch):
+            run_reduce(l, args)
+        elif isinstance(l, EltwiseLaunch):
+            run_eltwise(l, args)
+        else:
+            run_matmul(l, args)

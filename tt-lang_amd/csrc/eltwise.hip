@@ -35,6 +35,8 @@
 //    separate "full" kernel variants so the common-op variants fit 8 waves
 //    per SIMD (<= 64 VGPRs) without spilling.
 
+#include <utility>
+
 #include "ttlh_common.h"
 
 namespace ttlh {
@@ -735,6 +737,293 @@ bool try_stream(const ChainArgs& c, int n, hipStream_t s, int* status) {
   return true;
 }
 
+// ---------------------------------------------------------------------------
+// Scaled reductions (ttlh_reduce).  The tile program runs through the generic
+// interpreter (all ops, mixed dtypes, 64-bit addressing); each element is
+// multiplied by the scale and combined in fp32.
+//  * rows (reduce over columns): one wave per iteration row, lane l takes the
+//    8-element chunks l, l + 64, ... of the row, then an xor-shuffle tree;
+//  * columns (reduce over rows): lane l of every wave takes the same 8
+//    columns, wave w rows w, w + 4, ... of the block's row split; the four
+//    waves combine through LDS; with several splits the fp32 partials go to
+//    the workspace and a second pass combines them in split order;
+//  * both: the row kernel writes one fp32 value per row to the workspace and
+//    one workgroup combines them.
+struct RedArgs {
+  EltArgs e;             // program and operands; e.y0 / e.x0 = iteration origin
+  int64_t h, w;          // iteration region
+  const void* scaler;
+  int32_t scaler_dtype;
+  float scale_imm;
+  void* out;
+  int64_t out_ld;
+  int32_t out_dtype, out_pad;
+  float* ws;
+  int64_t rows_per_split;
+  int32_t kind, splits;
+};
+
+__device__ __forceinline__ float red_identity(int kind) {
+  return kind == TTLH_REDUCE_MAX ? -__builtin_inff() : 0.0f;
+}
+
+__device__ __forceinline__ float red_combine(int kind, float a, float b) {
+  if (kind == TTLH_REDUCE_MAX) return (a != a || b != b) ? __builtin_nanf("") : fmaxf(a, b);
+  return a + b;
+}
+
+__device__ __forceinline__ float red_scale(const RedArgs& a) {
+  float s = a.scale_imm;
+  if (a.scaler)
+    s *= a.scaler_dtype == TTLH_BF16 ? bf16_to_f32(*static_cast<const uint16_t*>(a.scaler))
+                                     : *static_cast<const float*>(a.scaler);
+  return s;
+}
+
+__device__ __forceinline__ void red_store(const RedArgs& a, int64_t off, float v) {
+  if (a.out_dtype == TTLH_BF16)
+    static_cast<uint16_t*>(a.out)[off] = f32_to_bf16(v);
+  else
+    static_cast<float*>(a.out)[off] = v;
+}
+
+// result `idx` of a row reduce (DIM1) / column reduce (DIM0), with the zero
+// padding of the result tile when out_pad is set
+template <int DIMS>
+__device__ __forceinline__ void red_write(const RedArgs& a, int64_t idx, float v) {
+  if constexpr (DIMS == TTLH_REDUCE_DIM1) {
+    const int64_t off = idx * a.out_ld;
+    red_store(a, off, v);
+    if (a.out_pad)
+      for (int c = 1; c < 32; ++c) red_store(a, off + c, 0.0f);
+  } else {
+    red_store(a, idx, v);
+    if (a.out_pad)
+      for (int r = 1; r < 32; ++r) red_store(a, idx + r * a.out_ld, 0.0f);
+  }
+}
+
+__device__ __forceinline__ float red_wave(int kind, float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = red_combine(kind, v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// Kernel variants of the reductions (MODE):
+//   0: the generic loop, loads inside the program (any operand count and
+//      alignment, VEC 8 or 1, every op);
+//   1: plain (the program is one LOAD step: the operand itself);
+//   2: up to four operands, common ops (add sub mul exp neg abs relu recip).
+// Modes 1 and 2 read 8-wide chunks in a four-deep software pipeline (chunk
+// k + 4 is fetched as soon as chunk k is consumed, so four loads per lane
+// stay in flight; past the end the fetch re-reads the lane's first chunk).
+// Programs with other ops take mode 0: four inlined copies of the every-op
+// interpreter (pow, fmod, log, ...) would overflow the instruction cache.
+struct RedChunk {
+  Raw q0, q1, q2, q3;
+};
+
+template <int MODE>
+__device__ __forceinline__ RedChunk red_fetch(const EltArgs& e, int64_t y, int64_t x) {
+  RedChunk c;
+  const uintptr_t p0 = operand_addr<false>(e.ops[0], y, x);
+  c.q0 = load_raw<8, false>(e.ops[0], p0);
+  if constexpr (MODE >= 2) {  // unused slots re-read operand 0 (a cache hit)
+    const int n = e.n_ops;
+    const uintptr_t p1 = n > 1 ? operand_addr<false>(e.ops[1], y, x) : p0;
+    const uintptr_t p2 = n > 2 ? operand_addr<false>(e.ops[2], y, x) : p0;
+    const uintptr_t p3 = n > 3 ? operand_addr<false>(e.ops[3], y, x) : p0;
+    c.q1 = load_raw<8, false>(e.ops[1], p1);
+    c.q2 = load_raw<8, false>(e.ops[2], p2);
+    c.q3 = load_raw<8, false>(e.ops[3], p3);
+  }
+  return c;
+}
+
+template <int MODE>
+__device__ __forceinline__ f32x8 red_eval(const EltArgs& e, const RedChunk& c, int64_t y,
+                                          int64_t x) {
+  if constexpr (MODE == 1) {
+    const f32x8 v = to_f32<8, false>(e.ops[0], c.q0);
+    return e.prog[0].rnd == TTLH_BF16 ? round_bf16x8(v) : v;
+  } else {
+    return run_program<8, true, false, true, false, false>(e, c.q0, c.q1, c.q2, c.q3, y, x);
+  }
+}
+
+// pipeline depth: the plain mode keeps all eight chunks of a 4096-wide row
+// in flight per lane, the interpreting mode four (register budget)
+template <int MODE>
+constexpr int red_depth() {
+  return MODE == 1 ? 8 : 4;
+}
+
+// f(integral_constant<int, i>) for i = 0 .. N-1, unrolled at compile time
+// (constant indices keep the chunk arrays in registers)
+template <typename F, int... I>
+__device__ __forceinline__ void red_unroll(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>()), ...);
+}
+
+template <int VEC, bool TO_WS, int MODE>
+__global__ __launch_bounds__(256) void reduce_rows_kernel(const RedArgs a) {
+  const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= a.h) return;  // wave-uniform
+  const float s = red_scale(a);
+  const int64_t y = a.e.y0 + row;
+  float r = red_identity(a.kind);
+  if constexpr (MODE == 0) {
+    const Raw q{};
+    for (int64_t xo = int64_t(lane) * VEC; xo < a.w; xo += 64 * VEC) {
+      const f32x8 v =
+          run_program<VEC, false, false, true, false, true>(a.e, q, q, q, q, y, a.e.x0 + xo);
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) r = red_combine(a.kind, r, v[k] * s);
+    }
+  } else {
+    constexpr int D = red_depth<MODE>();
+    constexpr int64_t S = 64 * 8;
+    const int64_t xf = int64_t(lane) * 8;
+    if (xf < a.w) {
+      auto at = [&](int64_t xo) { return a.e.x0 + (xo < a.w ? xo : xf); };
+      RedChunk c[D];
+      red_unroll([&](auto i) { c[i] = red_fetch<MODE>(a.e, y, at(xf + i * S)); },
+                 std::make_integer_sequence<int, D>());
+      for (int64_t xb = xf; xb < a.w; xb += D * S) {
+        red_unroll([&](auto i) {
+          const int64_t xo = xb + i * S;
+          if (xo < a.w) {
+            const f32x8 v = red_eval<MODE>(a.e, c[i], y, a.e.x0 + xo);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) r = red_combine(a.kind, r, v[k] * s);
+          }
+          c[i] = red_fetch<MODE>(a.e, y, at(xo + D * S));
+        }, std::make_integer_sequence<int, D>());
+      }
+    }
+  }
+  r = red_wave(a.kind, r);
+  if (lane == 0) {
+    if constexpr (TO_WS) a.ws[row] = r;
+    else red_write<TTLH_REDUCE_DIM1>(a, row, r);
+  }
+}
+
+// Column reduce; MODE as for the row reduce (the pipeline runs over the
+// wave's rows: rows r, r + 4, ... in flight).
+template <int VEC, int MODE>
+__global__ __launch_bounds__(256) void reduce_cols_kernel(const RedArgs a) {
+  __shared__ float part[3][64 * VEC];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t xo = (int64_t(blockIdx.x) * 64 + lane) * VEC;  // this lane's first column
+  const int64_t rb = int64_t(blockIdx.y) * a.rows_per_split;
+  const int64_t re = rb + a.rows_per_split < a.h ? rb + a.rows_per_split : a.h;
+  const float s = red_scale(a);
+  const bool active = xo < a.w;  // VEC = 8 needs w % 8 == 0: all 8 columns valid
+  float acc[VEC];
+#pragma unroll
+  for (int k = 0; k < VEC; ++k) acc[k] = red_identity(a.kind);
+  if (active) {
+    if constexpr (MODE == 0) {
+      const Raw q{};
+      for (int64_t row = rb + wave; row < re; row += 4) {
+        const f32x8 v = run_program<VEC, false, false, true, false, true>(
+            a.e, q, q, q, q, a.e.y0 + row, a.e.x0 + xo);
+#pragma unroll
+        for (int k = 0; k < VEC; ++k) acc[k] = red_combine(a.kind, acc[k], v[k] * s);
+      }
+    } else {
+      constexpr int D = red_depth<MODE>();
+      const int64_t rf = rb + wave;
+      if (rf < re) {
+        const int64_t x = a.e.x0 + xo;
+        auto at = [&](int64_t row) { return a.e.y0 + (row < re ? row : rf); };
+        RedChunk c[D];
+        red_unroll([&](auto i) { c[i] = red_fetch<MODE>(a.e, at(rf + 4 * i), x); },
+                   std::make_integer_sequence<int, D>());
+        for (int64_t rr = rf; rr < re; rr += 4 * D) {
+          red_unroll([&](auto i) {
+            const int64_t row = rr + 4 * i;
+            if (row < re) {
+              const f32x8 v = red_eval<MODE>(a.e, c[i], a.e.y0 + row, x);
+#pragma unroll
+              for (int k = 0; k < VEC; ++k) acc[k] = red_combine(a.kind, acc[k], v[k] * s);
+            }
+            c[i] = red_fetch<MODE>(a.e, at(row + 4 * D), x);
+          }, std::make_integer_sequence<int, D>());
+        }
+      }
+    }
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) part[wave - 1][lane * VEC + k] = acc[k];
+  }
+  __syncthreads();
+  if (wave != 0 || !active) return;
+#pragma unroll
+  for (int k = 0; k < VEC; ++k) {
+#pragma unroll
+    for (int w = 0; w < 3; ++w) acc[k] = red_combine(a.kind, acc[k], part[w][lane * VEC + k]);
+    if (a.splits == 1) red_write<TTLH_REDUCE_DIM0>(a, xo + k, acc[k]);
+    else a.ws[int64_t(blockIdx.y) * a.w + xo + k] = acc[k];
+  }
+}
+
+// p[0], p[stride], ..., p[(n - 1) stride] combined in that order, eight
+// loads in flight
+__device__ __forceinline__ float red_strided(int kind, const float* p, int64_t n, int64_t stride) {
+  float r = red_identity(kind);
+  int64_t i = 0;
+  for (; i + 8 <= n; i += 8) {
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) v[k] = p[(i + k) * stride];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) r = red_combine(kind, r, v[k]);
+  }
+  for (; i < n; ++i) r = red_combine(kind, r, p[i * stride]);
+  return r;
+}
+
+// Column reduce, several splits: a workgroup takes 32 columns; its eight
+// thread groups combine the splits g, g + 8, ... of their column, then group
+// 0 combines the eight results (fixed order throughout).
+__global__ __launch_bounds__(256) void reduce_cols_finish_kernel(const RedArgs a) {
+  __shared__ float part[8][32];
+  const int t = threadIdx.x, c = t & 31, g = t >> 5;
+  const int64_t col = int64_t(blockIdx.x) * 32 + c;
+  float r = red_identity(a.kind);
+  if (col < a.w && g < a.splits)
+    r = red_strided(a.kind, a.ws + int64_t(g) * a.w + col, (a.splits - g + 7) / 8, 8 * a.w);
+  part[g][c] = r;
+  __syncthreads();
+  if (g != 0 || col >= a.w) return;
+#pragma unroll
+  for (int k = 1; k < 8; ++k) r = red_combine(a.kind, r, part[k][c]);
+  red_write<TTLH_REDUCE_DIM0>(a, col, r);
+}
+
+// full reduce: one workgroup combines the h row values (thread t: rows t,
+// t + 256, ... in order, then a fixed tree) and writes the result tile
+__global__ __launch_bounds__(256) void reduce_all_finish_kernel(const RedArgs a) {
+  __shared__ float part[256];
+  const int t = threadIdx.x;
+  part[t] = t < a.h ? red_strided(a.kind, a.ws + t, (a.h - t + 255) / 256, 256)
+                    : red_identity(a.kind);
+  __syncthreads();
+  for (int n = 128; n >= 1; n >>= 1) {
+    if (t < n) part[t] = red_combine(a.kind, part[t], part[t + n]);
+    __syncthreads();
+  }
+  if (t == 0) red_store(a, 0, part[0]);
+  if (a.out_pad) {
+    for (int i = t; i < 32 * 32; i += 256)
+      if (i != 0) red_store(a, int64_t(i >> 5) * a.out_ld + (i & 31), 0.0f);
+  }
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 bool is_binary(int op) { return op >= TTLH_OP_ADD && op <= TTLH_OP_MOD; }
@@ -768,54 +1057,57 @@ int64_t max_offset(const ttlh_operand& o, int64_t y0, int64_t x0, int64_t h, int
 
 using namespace ttlh;
 
-extern "C" int ttlh_eltwise(const ttlh_instr* prog, const ttlh_operand* in, int n_instr, void* out,
-                            int out_dtype, int64_t out_ld, int64_t y0, int64_t x0, int64_t h,
-                            int64_t w, void* stream) {
-  clear_error();
-  TTLH_REQUIRE(prog && in && n_instr > 0 && n_instr <= TTLH_MAX_INSTR, TTLH_EINVAL,
-               "ttlh_eltwise: program must have 1..%d steps (got %d)", TTLH_MAX_INSTR, n_instr);
-  TTLH_REQUIRE(out && (out_dtype == TTLH_BF16 || out_dtype == TTLH_F32), TTLH_EINVAL,
-               "ttlh_eltwise: bad output pointer or dtype");
-  TTLH_REQUIRE(h >= 0 && w >= 0 && y0 >= 0 && x0 >= 0 && out_ld >= x0 + w, TTLH_EINVAL,
-               "ttlh_eltwise: bad output region");
+namespace ttlh {
+namespace {
 
-  EltArgs a = {};
-  int depth = 0;  // values on the stack including acc
-  int max_depth = 0;
-  bool all_bf16 = true;
+// What decode_program learned about a program and its operands.
+struct ProgInfo {
   int n_ops = 0;
-  bool full = false;  // program uses an op outside the common set
-  bool off32 = (y0 + h) * out_ld < (int64_t(1) << 31);
-  bool vec = (w % 8 == 0) && (x0 % 8 == 0) && (out_ld % 8 == 0) && aligned16(out);
+  int max_depth = 0;
+  bool all_bf16 = true;  // every operand is bf16
+  bool full = false;     // some step uses an op outside the common set
+  bool vec = true;       // every contiguous operand allows 16-byte chunks at x0
+  bool off32 = true;     // every operand offset over the region fits 31 bits
+};
+
+// Validates the ABI program `prog` / operands `in` over the iteration region
+// (y0, x0, h, w) and decodes it into a.prog / a.ops / a.n_instr / a.n_ops.
+// `who` prefixes the error messages.
+int decode_program(const char* who, const ttlh_instr* prog, const ttlh_operand* in, int n_instr,
+                   int64_t y0, int64_t x0, int64_t h, int64_t w, EltArgs& a, ProgInfo& pi) {
+  TTLH_REQUIRE(prog && in && n_instr > 0 && n_instr <= TTLH_MAX_INSTR, TTLH_EINVAL,
+               "%s: program must have 1..%d steps (got %d)", who, TTLH_MAX_INSTR, n_instr);
+  int depth = 0;  // values on the stack including acc
+  pi.vec = (w % 8 == 0) && (x0 % 8 == 0);
   for (int k = 0; k < n_instr; ++k) {
     const ttlh_instr& p = prog[k];
     const int f = p.form;
     const bool uses_operand = f == TTLH_FORM_LOAD || f == TTLH_FORM_PUSH || f == TTLH_FORM_BIN ||
                               f == TTLH_FORM_BIN_REV;
     TTLH_REQUIRE(f >= TTLH_FORM_LOAD && f <= TTLH_FORM_BIN_POP, TTLH_EINVAL,
-                 "ttlh_eltwise: bad form %d at step %d", f, k);
+                 "%s: bad form %d at step %d", who, f, k);
     TTLH_REQUIRE(p.rnd == TTLH_BF16 || p.rnd == TTLH_F32, TTLH_EINVAL,
-                 "ttlh_eltwise: bad rounding mode at step %d", k);
+                 "%s: bad rounding mode at step %d", who, k);
     if (f == TTLH_FORM_UNARY)
-      TTLH_REQUIRE(is_unary(p.op), TTLH_EINVAL, "ttlh_eltwise: step %d needs a unary opcode", k);
+      TTLH_REQUIRE(is_unary(p.op), TTLH_EINVAL, "%s: step %d needs a unary opcode", who, k);
     if (f >= TTLH_FORM_BIN)
-      TTLH_REQUIRE(is_binary(p.op), TTLH_EINVAL, "ttlh_eltwise: step %d needs a binary opcode", k);
+      TTLH_REQUIRE(is_binary(p.op), TTLH_EINVAL, "%s: step %d needs a binary opcode", who, k);
     // stack discipline
     if (f == TTLH_FORM_LOAD || f == TTLH_FORM_CONST) {
-      TTLH_REQUIRE(depth == 0, TTLH_EINVAL, "ttlh_eltwise: LOAD/CONST at step %d on a live stack", k);
+      TTLH_REQUIRE(depth == 0, TTLH_EINVAL, "%s: LOAD/CONST at step %d on a live stack", who, k);
       depth = 1;
     } else if (f == TTLH_FORM_PUSH || f == TTLH_FORM_PUSH_CONST) {
       TTLH_REQUIRE(depth >= 1 && depth < TTLH_MAX_STACK, TTLH_EINVAL,
-                   "ttlh_eltwise: stack overflow at step %d", k);
+                   "%s: stack overflow at step %d", who, k);
       ++depth;
     } else if (f == TTLH_FORM_BIN_POP) {
-      TTLH_REQUIRE(depth >= 2, TTLH_EINVAL, "ttlh_eltwise: stack underflow at step %d", k);
+      TTLH_REQUIRE(depth >= 2, TTLH_EINVAL, "%s: stack underflow at step %d", who, k);
       --depth;
     } else {
-      TTLH_REQUIRE(depth >= 1, TTLH_EINVAL, "ttlh_eltwise: step %d reads an empty stack", k);
+      TTLH_REQUIRE(depth >= 1, TTLH_EINVAL, "%s: step %d reads an empty stack", who, k);
     }
-    max_depth = depth > max_depth ? depth : max_depth;
-    if ((f == TTLH_FORM_UNARY || f >= TTLH_FORM_BIN) && !is_common(p.op)) full = true;
+    pi.max_depth = depth > pi.max_depth ? depth : pi.max_depth;
+    if ((f == TTLH_FORM_UNARY || f >= TTLH_FORM_BIN) && !is_common(p.op)) pi.full = true;
     Ins& q = a.prog[k];
     q.op = p.op;
     q.rnd = p.rnd;
@@ -833,17 +1125,17 @@ extern "C" int ttlh_eltwise(const ttlh_instr* prog, const ttlh_operand* in, int 
       default: q.kind = K_BIN_REV; q.src = SRC_POP; break;  // BIN_POP: op(pop, acc)
     }
     if (!uses_operand) continue;
-    q.arg = static_cast<uint8_t>(n_ops);
+    q.arg = static_cast<uint8_t>(pi.n_ops);
     const ttlh_operand& o = in[k];
     TTLH_REQUIRE(o.ptr && (o.dtype == TTLH_BF16 || o.dtype == TTLH_F32), TTLH_EINVAL,
-                 "ttlh_eltwise: operand %d has a null pointer or bad dtype", k);
+                 "%s: operand %d has a null pointer or bad dtype", who, k);
     TTLH_REQUIRE(o.row_mask == -1 || o.row_mask == 31, TTLH_EINVAL,
-                 "ttlh_eltwise: operand %d row_mask must be -1 or 31", k);
+                 "%s: operand %d row_mask must be -1 or 31", who, k);
     TTLH_REQUIRE(o.col_mask == -1 || o.col_mask == 31, TTLH_EINVAL,
-                 "ttlh_eltwise: operand %d col_mask must be -1 or 31", k);
+                 "%s: operand %d col_mask must be -1 or 31", who, k);
     TTLH_REQUIRE(o.row_stride >= 0 && o.col_stride >= 0, TTLH_EINVAL,
-                 "ttlh_eltwise: operand %d has a negative stride", k);
-    EltOperand& e = a.ops[n_ops++];
+                 "%s: operand %d has a negative stride", who, k);
+    EltOperand& e = a.ops[pi.n_ops++];
     e.ptr = o.ptr;
     e.rs = o.row_stride;
     e.cs = o.col_stride;
@@ -852,24 +1144,44 @@ extern "C" int ttlh_eltwise(const ttlh_instr* prog, const ttlh_operand* in, int 
     e.roff = o.row_off;
     e.coff = o.col_off;
     e.dtype = o.dtype;
-    all_bf16 = all_bf16 && o.dtype == TTLH_BF16;
+    pi.all_bf16 = pi.all_bf16 && o.dtype == TTLH_BF16;
     const int esz = o.dtype == TTLH_BF16 ? 2 : 4;
     e.vec = o.col_stride == 1 && aligned16(o.ptr) && ((o.row_stride * esz) % 16 == 0) &&
             ((o.col_off * esz) % 16 == 0) && ((x0 * esz) % 16 == 0);
     // stride-0 (broadcast) operands keep the 8-wide path; others need alignment
-    if (o.col_stride != 0 && !e.vec) vec = false;
+    if (o.col_stride != 0 && !e.vec) pi.vec = false;
     const int64_t mo = max_offset(o, y0, x0, h, w);
-    if (mo >= (int64_t(1) << 31) || o.row_off < 0 || o.col_off < 0) off32 = false;
+    if (mo >= (int64_t(1) << 31) || o.row_off < 0 || o.col_off < 0) pi.off32 = false;
   }
-  TTLH_REQUIRE(depth == 1, TTLH_EINVAL, "ttlh_eltwise: program leaves %d values on the stack",
-               depth);
+  TTLH_REQUIRE(depth == 1, TTLH_EINVAL, "%s: program leaves %d values on the stack", who, depth);
+  a.n_instr = n_instr;
+  a.n_ops = pi.n_ops;
+  a.y0 = y0;
+  a.x0 = x0;
+  return TTLH_OK;
+}
+
+}  // namespace
+}  // namespace ttlh
+
+extern "C" int ttlh_eltwise(const ttlh_instr* prog, const ttlh_operand* in, int n_instr, void* out,
+                            int out_dtype, int64_t out_ld, int64_t y0, int64_t x0, int64_t h,
+                            int64_t w, void* stream) {
+  clear_error();
+  TTLH_REQUIRE(out && (out_dtype == TTLH_BF16 || out_dtype == TTLH_F32), TTLH_EINVAL,
+               "ttlh_eltwise: bad output pointer or dtype");
+  TTLH_REQUIRE(h >= 0 && w >= 0 && y0 >= 0 && x0 >= 0 && out_ld >= x0 + w, TTLH_EINVAL,
+               "ttlh_eltwise: bad output region");
+
+  EltArgs a = {};
+  ProgInfo pi;
+  const int st = decode_program("ttlh_eltwise", prog, in, n_instr, y0, x0, h, w, a, pi);
+  if (st != TTLH_OK) return st;
+  const bool off32 = pi.off32 && (y0 + h) * out_ld < (int64_t(1) << 31);
+  const bool vec = pi.vec && (out_ld % 8 == 0) && aligned16(out);
   if (h == 0 || w == 0) return TTLH_OK;
   a.out = out;
   a.out_ld = out_ld;
-  a.y0 = y0;
-  a.x0 = x0;
-  a.n_instr = n_instr;
-  a.n_ops = n_ops;
   a.out_dtype = out_dtype;
   const int64_t vw = vec ? 8 : 1;
   const int64_t cpr = w / vw;
@@ -880,6 +1192,7 @@ extern "C" int ttlh_eltwise(const ttlh_instr* prog, const ttlh_operand* in, int 
   a.total = static_cast<uint32_t>(total);
   division_magic(a.cpr, &a.magic, &a.shift);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const int n_ops = pi.n_ops;
   const bool preload = n_ops >= 1 && n_ops <= 4;  // preload reads operand 0 unconditionally
   // rare shapes: one generic variant each
   if (!off32) return vec ? launch<8, false, false, true, false, true>(a, s)
@@ -888,13 +1201,130 @@ extern "C" int ttlh_eltwise(const ttlh_instr* prog, const ttlh_operand* in, int 
   ChainArgs chain;
   if (make_chain(prog, n_instr, a, &chain)) {
     int status = TTLH_OK;
-    if (all_bf16 && try_stream(chain, n_instr, s, &status)) return status;
-    return all_bf16 ? dispatch_chain<true>(chain, n_instr, s) : dispatch_chain<false>(chain, n_instr, s);
+    if (pi.all_bf16 && try_stream(chain, n_instr, s, &status)) return status;
+    return pi.all_bf16 ? dispatch_chain<true>(chain, n_instr, s)
+                       : dispatch_chain<false>(chain, n_instr, s);
   }
   if (!preload) return launch<8, false, false, true, true, true>(a, s);
-  if (full) return launch<8, true, false, true, true, true>(a, s);
+  if (pi.full) return launch<8, true, false, true, true, true>(a, s);
   // common ops, 8-wide, preloaded
-  if (!all_bf16) return launch<8, true, false, true, true, false>(a, s);
-  return max_depth > 1 ? launch<8, true, true, true, true, false>(a, s)
-                       : launch<8, true, true, false, true, false>(a, s);
+  if (!pi.all_bf16) return launch<8, true, false, true, true, false>(a, s);
+  return pi.max_depth > 1 ? launch<8, true, true, true, true, false>(a, s)
+                          : launch<8, true, true, false, true, false>(a, s);
+}
+
+namespace ttlh {
+namespace {
+
+// row splits of a column reduce: about 1024 workgroups, at least 32 rows
+// each (8 per wave)
+int64_t red_rows_per_split(int64_t h, int64_t w) {
+  const int64_t bx = (w + 511) / 512;
+  int64_t sp = (1024 + bx - 1) / bx;
+  const int64_t max_sp = h / 32 > 1 ? h / 32 : 1;
+  if (sp > max_sp) sp = max_sp;
+  if (sp > 65535) sp = 65535;
+  if (sp < 1) sp = 1;
+  return (h + sp - 1) / sp;
+}
+
+}  // namespace
+}  // namespace ttlh
+
+extern "C" int64_t ttlh_reduce_workspace_bytes(int dims, int64_t h, int64_t w) {
+  if (h <= 0 || w <= 0 || dims == TTLH_REDUCE_DIM1) return 0;
+  if (dims == TTLH_REDUCE_DIM0) {
+    const int64_t rps = red_rows_per_split(h, w);
+    const int64_t splits = (h + rps - 1) / rps;
+    return splits > 1 ? splits * w * int64_t(sizeof(float)) : 0;
+  }
+  return h * int64_t(sizeof(float));
+}
+
+extern "C" int ttlh_reduce(const ttlh_instr* prog, const ttlh_operand* in, int n_instr, int kind,
+                           int dims, const void* scaler, int scaler_dtype, float scale_imm,
+                           void* out, int out_dtype, int64_t out_ld, int out_pad, int64_t y0,
+                           int64_t x0, int64_t h, int64_t w, void* workspace,
+                           int64_t workspace_bytes, void* stream) {
+  clear_error();
+  TTLH_REQUIRE(kind == TTLH_REDUCE_SUM || kind == TTLH_REDUCE_MAX, TTLH_EINVAL,
+               "ttlh_reduce: kind must be TTLH_REDUCE_SUM or TTLH_REDUCE_MAX");
+  TTLH_REQUIRE(dims >= 1 && dims <= 3, TTLH_EINVAL,
+               "ttlh_reduce: dims must be TTLH_REDUCE_DIM0, TTLH_REDUCE_DIM1 or both");
+  TTLH_REQUIRE(out && (out_dtype == TTLH_BF16 || out_dtype == TTLH_F32), TTLH_EINVAL,
+               "ttlh_reduce: bad output pointer or dtype");
+  TTLH_REQUIRE(!scaler || scaler_dtype == TTLH_BF16 || scaler_dtype == TTLH_F32, TTLH_EINVAL,
+               "ttlh_reduce: bad scaler dtype");
+  TTLH_REQUIRE(out_pad == 0 || out_pad == 1, TTLH_EINVAL, "ttlh_reduce: out_pad must be 0 or 1");
+  TTLH_REQUIRE(h >= 1 && w >= 1 && y0 >= 0 && x0 >= 0, TTLH_EINVAL,
+               "ttlh_reduce: empty or negative region");
+  TTLH_REQUIRE(out_ld >= (out_pad ? 32 : 1), TTLH_EINVAL, "ttlh_reduce: out_ld too small");
+  RedArgs a = {};
+  ProgInfo pi;
+  const int st = decode_program("ttlh_reduce", prog, in, n_instr, y0, x0, h, w, a.e, pi);
+  if (st != TTLH_OK) return st;
+  const int64_t need = ttlh_reduce_workspace_bytes(dims, h, w);
+  TTLH_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), TTLH_EINVAL,
+               "ttlh_reduce: needs a workspace of %lld bytes (got %lld)", (long long)need,
+               (long long)workspace_bytes);
+  TTLH_REQUIRE((h + 3) / 4 < (int64_t(1) << 31) && w / 64 < (int64_t(1) << 31), TTLH_EUNSUPPORTED,
+               "ttlh_reduce: region too large");
+  a.h = h;
+  a.w = w;
+  a.scaler = scaler;
+  a.scaler_dtype = scaler_dtype;
+  a.scale_imm = scale_imm;
+  a.out = out;
+  a.out_ld = out_ld;
+  a.out_dtype = out_dtype;
+  a.out_pad = out_pad;
+  a.ws = static_cast<float*>(workspace);
+  a.kind = kind;
+  a.splits = 1;
+  a.rows_per_split = h;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 block(256);
+  // kernel variant (see the reduction kernels): the pipelined 8-wide modes
+  // need aligned operands and at most four of them
+  const bool plain = n_instr == 1 && prog[0].form == TTLH_FORM_LOAD;
+  const int mode = !pi.vec || pi.n_ops < 1 || pi.n_ops > 4 ? 0 : (plain ? 1 : (pi.full ? 0 : 2));
+  const int variant = mode == 0 ? (pi.vec ? 1 : 0) : mode + 1;
+  if (dims != TTLH_REDUCE_DIM0) {
+    const dim3 grid(static_cast<uint32_t>((h + 3) / 4));
+#define TTLH_ROWS(WS)                                                                        \
+  switch (variant) {                                                                         \
+    case 0: hipLaunchKernelGGL((reduce_rows_kernel<1, WS, 0>), grid, block, 0, s, a); break; \
+    case 1: hipLaunchKernelGGL((reduce_rows_kernel<8, WS, 0>), grid, block, 0, s, a); break; \
+    case 2: hipLaunchKernelGGL((reduce_rows_kernel<8, WS, 1>), grid, block, 0, s, a); break; \
+    default: hipLaunchKernelGGL((reduce_rows_kernel<8, WS, 2>), grid, block, 0, s, a); break; \
+  }
+    if (dims == TTLH_REDUCE_DIM1) {
+      TTLH_ROWS(false)
+      return check_launch("reduce_rows_kernel");
+    }
+    TTLH_ROWS(true)
+#undef TTLH_ROWS
+    int rc = check_launch("reduce_rows_kernel");
+    if (rc != TTLH_OK) return rc;
+    hipLaunchKernelGGL(reduce_all_finish_kernel, dim3(1), block, 0, s, a);
+    return check_launch("reduce_all_finish_kernel");
+  }
+  {
+    a.rows_per_split = red_rows_per_split(h, w);
+    a.splits = static_cast<int32_t>((h + a.rows_per_split - 1) / a.rows_per_split);
+    const int vw = pi.vec ? 8 : 1;
+    const dim3 grid(static_cast<uint32_t>((w + 64 * vw - 1) / (64 * vw)),
+                    static_cast<uint32_t>(a.splits));
+    switch (variant) {
+      case 0: hipLaunchKernelGGL((reduce_cols_kernel<1, 0>), grid, block, 0, s, a); break;
+      case 1: hipLaunchKernelGGL((reduce_cols_kernel<8, 0>), grid, block, 0, s, a); break;
+      case 2: hipLaunchKernelGGL((reduce_cols_kernel<8, 1>), grid, block, 0, s, a); break;
+      default: hipLaunchKernelGGL((reduce_cols_kernel<8, 2>), grid, block, 0, s, a); break;
+    }
+    int rc = check_launch("reduce_cols_kernel");
+    if (rc != TTLH_OK || a.splits == 1) return rc;
+    hipLaunchKernelGGL(reduce_cols_finish_kernel, dim3(static_cast<uint32_t>((w + 31) / 32)),
+                       block, 0, s, a);
+    return check_launch("reduce_cols_finish_kernel");
+  }
 }

@@ -53,6 +53,11 @@ class Instr(C.Structure):
     ]
 
 
+# ttlh_reduce kinds and dimension bits
+REDUCE_SUM, REDUCE_MAX = 0, 1
+REDUCE_DIM0, REDUCE_DIM1 = 1, 2
+
+
 class Operand(C.Structure):
     _fields_ = [
         ("ptr", C.c_void_p), ("dtype", C.c_int32), ("pad", C.c_int32),
@@ -67,6 +72,10 @@ _i64, _vp, _int = C.c_int64, C.c_void_p, C.c_int
 SIGNATURES = {
     "ttlh_eltwise": (_int, [C.POINTER(Instr), C.POINTER(Operand), _int, _vp, _int, _i64, _i64,
                             _i64, _i64, _i64, _vp]),
+    "ttlh_reduce_workspace_bytes": (_i64, [_int, _i64, _i64]),
+    "ttlh_reduce": (_int, [C.POINTER(Instr), C.POINTER(Operand), _int, _int, _int, _vp, _int,
+                           C.c_float, _vp, _int, _i64, _int, _i64, _i64, _i64, _i64, _vp, _i64,
+                           _vp]),
     "ttlh_matmul": (_int, [_vp, _int, _i64, _vp, _int, _i64, _vp, _int, _i64, _i64, _i64, _i64,
                            _int, _vp]),
     "ttlh_bfp8_pack_host": (_int, [_vp, _vp, _i64, _i64]),

@@ -316,6 +316,14 @@ def _as_bexpr(x) -> BExpr:
     raise TypeError(f"expected a block or block expression, got {type(x).__name__}")
 
 
+def _check_not_reduced(e: BExpr) -> None:
+    if e.tree[0] == "reduce":
+        raise NotImplementedError(
+            "using the result of ttl.math.reduce_sum / reduce_max inside a larger expression is "
+            "not supported by the MI355X backend: store() the reduction on its own and copy it "
+            "to a tensor")
+
+
 def _remap(tree, axis: int, new_len: int):
     """Broadcast a size-1 axis of every leaf map in `tree` to `new_len`."""
     tag = tree[0]
@@ -336,11 +344,15 @@ def _remap(tree, axis: int, new_len: int):
 def _binary(op: str, a, b) -> BExpr:
     if isinstance(a, (int, float)) and not isinstance(a, bool):
         bb = _as_bexpr(b)
+        _check_not_reduced(bb)
         return BExpr(bb.shape, (op, ("const", float(a)), bb.tree), bb.dtype)
     if isinstance(b, (int, float)) and not isinstance(b, bool):
         aa = _as_bexpr(a)
+        _check_not_reduced(aa)
         return BExpr(aa.shape, (op, aa.tree, ("const", float(b))), aa.dtype)
     aa, bb = _as_bexpr(a), _as_bexpr(b)
+    _check_not_reduced(aa)
+    _check_not_reduced(bb)
     sa, sb = aa.shape, bb.shape
     if len(sa) != len(sb):
         raise ValueError(f"Cannot broadcast: dimension mismatch between shapes {sa} and {sb}. "
@@ -363,7 +375,40 @@ def _binary(op: str, a, b) -> BExpr:
 
 def _unary(op: str, a, imm: Optional[float] = None) -> BExpr:
     aa = _as_bexpr(a)
+    _check_not_reduced(aa)
     return BExpr(aa.shape, (op, aa.tree), aa.dtype)
+
+
+def _reduce(kind: str, x, scaler, dims) -> BExpr:
+    """ttl.math.reduce_sum / reduce_max (docs/sphinx/specs/
+    TTLangSpecification.md:754-755).  The reference specifies only the
+    signature; the semantics implemented: every element of `x` times the
+    scaler (the first element of a (1, 1) block, or a number), summed or
+    maximised (NaN-propagating) over the element rows (dims [0]), columns
+    ([1]) or both of the block, in fp32, rounded once to the block's dtype.
+    The result block has size 1 along the reduced dims; each of its tiles
+    holds the values in its first row / column ([0, 0] for both) and zeros
+    elsewhere, so it can be copied to a full 32-wide tensor tile or to a
+    size-1 tensor dimension."""
+    if dims is None:
+        raise ValueError(f"dims parameter is required for reduce_{kind}()")
+    dl = [int(d) for d in dims]
+    if not dl or len(set(dl)) != len(dl) or any(d not in (0, 1) for d in dl):
+        raise ValueError(f"reduce_{kind}() dims must be [0], [1] or [0, 1], got {list(dims)}")
+    e = _as_bexpr(x)
+    _check_not_reduced(e)
+    if isinstance(scaler, (int, float)) and not isinstance(scaler, bool):
+        st = ("const", float(scaler))
+    else:
+        se = _as_bexpr(scaler)
+        if tuple(se.shape) != (1, 1):
+            raise ValueError(f"reduce_{kind}() scaler must be a (1, 1) block, got shape {se.shape}")
+        if se.tree[0] != "leaf":
+            raise NotImplementedError(f"reduce_{kind}() scaler must be a block read from a CB "
+                                      "(an expression as scaler is not supported)")
+        st = se.tree
+    shape = tuple(1 if i in dl else n for i, n in enumerate(e.shape))
+    return BExpr(shape, ("reduce", kind, tuple(sorted(dl)), e.tree, tuple(e.shape), st), e.dtype)
 
 
 class Block:
@@ -460,6 +505,9 @@ class Block:
         e = _as_bexpr(items)
         if len(e) != len(self):
             raise ValueError("Length mismatch in store()")
+        if e.tree[0] == "reduce" and tuple(e.shape) != tuple(self.shape):
+            raise ValueError(f"store() of a reduction of shape {tuple(e.shape)} into a block of "
+                             f"shape {tuple(self.shape)}: the block must have the reduced shape")
         ctx.add(Event("store", self.cb, ctx.cur,
                       {"target": self, "expr": e, "acc": bool(acc), "thread": ctx.thread,
                        "loc": _user_location()}))
@@ -683,7 +731,7 @@ def _check_slice_shape(s: TensorSlice, blk: Block) -> None:
 
 
 class _Math:
-    """ttl.math: broadcast plus the elementwise tile ops."""
+    """ttl.math: broadcast, the elementwise tile ops and the scaled reductions."""
 
     @staticmethod
     def broadcast(block, _unused=None, dims: Optional[Sequence[int]] = None) -> BExpr:
@@ -727,6 +775,16 @@ class _Math:
     def min(a, b): return _binary("min", a, b)
     maximum = max
     minimum = min
+
+    @staticmethod
+    def reduce_sum(expr, scaler, dims=None) -> BExpr:
+        """Scaled sum over `dims` (spec TTLangSpecification.md:754)."""
+        return _reduce("sum", expr, scaler, dims)
+
+    @staticmethod
+    def reduce_max(expr, scaler, dims=None) -> BExpr:
+        """Scaled maximum over `dims` (spec TTLangSpecification.md:755)."""
+        return _reduce("max", expr, scaler, dims)
 
 
 math = _Math()

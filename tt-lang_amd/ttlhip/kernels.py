@@ -99,6 +99,66 @@ def eltwise(prog: StackProgram, operands: Sequence[Optional[OperandMap]], out: t
            out.stride(0), y0, x0, h, w, L.stream_ptr(stream))
 
 
+def reduce(prog: StackProgram, operands: Sequence[Optional[OperandMap]], kind: str,
+           dims: Sequence[int], out: torch.Tensor, region, out_origin=(0, 0),
+           out_pad: bool = False, scaler: Optional[torch.Tensor] = None, scale: float = 1.0,
+           stream=None) -> None:
+    """Scaled reduction (kind "sum" or "max") of a stack program over the
+    iteration `region` = (y0, x0, h, w), operands addressed as in eltwise()
+    from iteration element (y, x).  dims: the reduced axes (0: over rows, 1:
+    over columns).  The results are written into `out` from `out_origin`
+    (one per column, one per row, or one value; out_pad: whole zero-padded
+    32-wide result tiles).  scaler: a device tensor whose first element
+    multiplies every value (times `scale`)."""
+    _check_device(out, "reduce output")
+    if out.stride(1) != 1:
+        raise ValueError("reduce output must have unit column stride")
+    if kind not in ("sum", "max"):
+        raise ValueError(f"reduce kind must be 'sum' or 'max', got {kind!r}")
+    dset = set(int(d) for d in dims)
+    if not dset or not dset <= {0, 1}:
+        raise ValueError(f"reduce dims must be a non-empty subset of [0, 1], got {list(dims)}")
+    dbits = (L.REDUCE_DIM0 if 0 in dset else 0) | (L.REDUCE_DIM1 if 1 in dset else 0)
+    n = len(prog.steps)
+    if len(operands) != n:
+        raise ValueError(f"{n} steps but {len(operands)} operand slots")
+    y0, x0, h, w = region
+    if h <= 0 or w <= 0 or y0 < 0 or x0 < 0:
+        raise ValueError(f"bad reduce region {tuple(region)}")
+    oy, ox = out_origin
+    # output extent: the result rows / columns (plus the tile padding)
+    rows = (1 if 0 in dset else h) if not out_pad else (32 if 0 in dset else h)
+    cols = (1 if 1 in dset else w) if not out_pad else (32 if 1 in dset else w)
+    if oy < 0 or ox < 0 or oy + rows > out.shape[0] or ox + cols > out.shape[1]:
+        raise ValueError(f"reduce result ({rows}x{cols} at {(oy, ox)}) outside output "
+                         f"{tuple(out.shape)}")
+    instrs = (L.Instr * n)()
+    ops = (L.Operand * n)()
+    for k, (s, m) in enumerate(zip(prog.steps, operands)):
+        instrs[k] = L.Instr(s.op, s.form, s.rnd, 0, s.imm)
+        if s.form in (L.FORM_LOAD, L.FORM_PUSH, L.FORM_BIN, L.FORM_BIN_REV):
+            if m is None:
+                raise ValueError(f"step {k} needs an operand")
+            ops[k] = _operand_struct(m, y0, x0, h, w)
+    sp, sdt = 0, 0
+    if scaler is not None:
+        if not scaler.is_cuda or scaler.numel() < 1:
+            raise ValueError("reduce scaler must be a non-empty device tensor")
+        sp, sdt = scaler.data_ptr(), L.dtype_code(scaler.dtype)
+    ws_bytes = int(L.load().ttlh_reduce_workspace_bytes(dbits, h, w))
+    ws = None
+    if ws_bytes:
+        # from torch's caching allocator; freed on return, reused in stream order
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=out.device)
+        if stream is not None:
+            ws.record_stream(stream)
+    optr = out.data_ptr() + (oy * out.stride(0) + ox) * out.element_size()
+    L.call("ttlh_reduce", instrs, ops, n, L.REDUCE_SUM if kind == "sum" else L.REDUCE_MAX,
+           dbits, sp, sdt, float(scale), optr, L.dtype_code(out.dtype), out.stride(0),
+           int(bool(out_pad)), y0, x0, h, w, ws.data_ptr() if ws is not None else 0, ws_bytes,
+           L.stream_ptr(stream))
+
+
 def matmul(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, accumulate: bool = False,
            stream=None) -> None:
     """c (=|+=) a @ b on the GPU, fp32 accumulation (bf16 or f32 MFMA)."""

@@ -14,7 +14,11 @@ becomes one launch:
     (+offset), fixed-tile reuse or size-1 broadcast (what the simulator's
     block broadcasting and degenerate tiles produce);
   * A(m,k) @ B(k,n) accumulated with store(acc=True) over all k into every
-    output tile of a rectangle -> one ttlh_matmul.
+    output tile of a rectangle -> one ttlh_matmul;
+  * ttl.math.reduce_sum / reduce_max of an elementwise expression, every
+    output tile reducing the same contiguous run of expression tiles (one
+    block, or several accumulated with store(acc=True) for sums) -> one
+    ttlh_reduce.
 Anything else raises NotImplementedError naming the unsupported pattern.
 """
 
@@ -102,6 +106,27 @@ class MatmulLaunch:
 
 
 @dataclass
+class ReduceLaunch:
+    prog: X.StackProgram
+    operands: List[Optional[OperandSpec]]  # per step, addressed from iteration (y, x)
+    out: TensorRef
+    kind: str                              # "sum" or "max"
+    dims: Tuple[int, ...]                  # reduced axes
+    region: Tuple[int, int, int, int]      # iteration y0, x0, h, w (elements)
+    out_origin: Tuple[int, int]            # first result element of `out`
+    out_pad: bool                          # whole zero-padded 32-wide result tiles
+    scaler: Optional[TensorRef] = None     # tensor holding the scaler tile, or None
+    scaler_at: Tuple[int, int] = (0, 0)    # its element (row, col)
+    scale: float = 1.0                     # constant scaler (times the tensor's)
+    tiles: int = 0
+    loc: Optional[Tuple[str, int]] = None
+
+    def describe(self) -> str:
+        return (f"reduce_{self.kind} over dims {list(self.dims)} of {self.region[2]}x"
+                f"{self.region[3]} elements at ({self.region[0]}, {self.region[1]})")
+
+
+@dataclass
 class Plan:
     launches: List[Any] = field(default_factory=list)
     # tensors the kernel body created at trace time (bound by creation order
@@ -183,9 +208,14 @@ class _Group:
     out_rc: List[np.ndarray] = field(default_factory=list)     # [(N,2)]
     leaf_rc: List[List[np.ndarray]] = field(default_factory=list)
     order: List[np.ndarray] = field(default_factory=list)
+    # reductions: the scaler's tensor and its tile per store instance
+    scaler_tensor: Any = None
+    scaler_rc: List[np.ndarray] = field(default_factory=list)
 
 
 def _tree_leaves(tree, out: List):
+    """Leaves of an elementwise tree (of the reduced expression for a
+    reduction; its scaler is not an operand)."""
     tag = tree[0]
     if tag == "leaf":
         out.append(tree)
@@ -193,6 +223,8 @@ def _tree_leaves(tree, out: List):
         pass
     elif tag == "powi":
         _tree_leaves(tree[1], out)
+    elif tag == "reduce":
+        _tree_leaves(tree[3], out)
     else:
         for t in tree[1:]:
             _tree_leaves(t, out)
@@ -207,6 +239,10 @@ def _tree_key(tree, leaf_ids: Dict[int, int]):
         return ("const", tree[1])
     if tag == "powi":
         return ("powi", _tree_key(tree[1], leaf_ids), tree[2])
+    if tag == "reduce":
+        _, kind, dims, inner, ishape, scaler = tree
+        sk = ("const", scaler[1]) if scaler[0] == "const" else ("scaler", str(scaler[1].cb.dtype))
+        return ("reduce", kind, dims, _tree_key(inner, leaf_ids), ishape, sk)
     return (tag,) + tuple(_tree_key(t, leaf_ids) for t in tree[1:])
 
 
@@ -330,6 +366,9 @@ def resolve(core_traces: List[Dict[str, Any]]) -> List[_Group]:
                 rout = T.broadcast_to_domain(target.event.index, shape).ravel()
                 dt = drain[cid]
                 R, C = target.shape
+                if e.tree[0] == "reduce":
+                    _resolve_reduce(ev, e, target, rout, dt, fill, shape, groups)
+                    continue
                 er, ec = e.shape
                 nslot = R * C
                 # output tile of every (instance, slot)
@@ -365,6 +404,61 @@ def resolve(core_traces: List[Dict[str, Any]]) -> List[_Group]:
                 g.leaf_rc.append(leaf_rc)
                 g.order.append(order)
     return list(groups.values())
+
+
+def _resolve_reduce(ev, e, target, rout, dt, fill, shape, groups) -> None:
+    """Store of a reduction: every (instance, slot of the reduced expression)
+    contributes its expression tile to the output tile of the target slot it
+    collapses onto."""
+    _, kind, dims, inner, ishape, stree = e.tree
+    R, C = target.shape
+    if tuple(e.shape) != (R, C):
+        raise PlanError(f"a reduction of shape {tuple(e.shape)} stored into a block of shape "
+                        f"{(R, C)}: the target block must have the reduced shape")
+    IR, IC = ishape
+    islot = np.arange(IR * IC)
+    ii, ij = islot // IC, islot % IC
+    ti = np.zeros_like(ii) if 0 in dims else ii
+    tj = np.zeros_like(ij) if 1 in dims else ij
+    out_r = (dt.r0[rout][:, None] + ti[None, :]).ravel()
+    out_c = (dt.c0[rout][:, None] + tj[None, :]).ravel()
+    leaves = _tree_leaves(inner, [])
+    if not leaves:
+        raise PlanError("a reduction needs at least one operand read from a tensor")
+    leaf_rc, leaf_tensors = [], []
+    for lf in leaves:
+        _, blk, rmap, cmap = lf
+        if blk.cb.id not in fill:
+            raise PlanError("expression operands must come from blocks filled by ttl.copy from a "
+                            "tensor")
+        ft = fill[blk.cb.id]
+        w = T.broadcast_to_domain(blk.event.index, shape).ravel()
+        lr = (ft.r0[w][:, None] + np.asarray(rmap)[ii][None, :]).ravel()
+        lc = (ft.c0[w][:, None] + np.asarray(cmap)[ij][None, :]).ravel()
+        leaf_rc.append(np.stack([lr, lc], 1))
+        leaf_tensors.append(ft.tensor)
+    s_tensor, s_rc = None, None
+    if stree[0] == "leaf":
+        _, sblk, srm, scm = stree
+        if sblk.cb.id not in fill:
+            raise PlanError("a reduction's scaler block must be filled by ttl.copy from a tensor")
+        ft = fill[sblk.cb.id]
+        w = T.broadcast_to_domain(sblk.event.index, shape).ravel()
+        s_tensor = ft.tensor
+        s_rc = np.stack([ft.r0[w] + int(srm[0]), ft.c0[w] + int(scm[0])], 1)
+    order = np.repeat(np.arange(rout.size), IR * IC)
+    key = (_tree_key(e.tree, {}), tuple(id(t) for t in leaf_tensors), id(s_tensor),
+           id(dt.tensor), ev.data["acc"])
+    g = groups.get(key)
+    if g is None:
+        g = _Group(e.tree, leaves, leaf_tensors, dt.tensor, ev.data["acc"], e.dtype,
+                   ev.data.get("loc"), scaler_tensor=s_tensor)
+        groups[key] = g
+    g.out_rc.append(np.stack([out_r, out_c], 1))
+    g.leaf_rc.append(leaf_rc)
+    g.order.append(order + sum(o.size for o in g.order))
+    if s_rc is not None:
+        g.scaler_rc.append(s_rc)
 
 
 # ---------------------------------------------------------------------------
@@ -432,6 +526,8 @@ def _has(tree, tag) -> bool:
         return True
     if tree[0] in ("leaf", "const"):
         return False
+    if tree[0] == "reduce":
+        return _has(tree[3], tag)
     return any(_has(t, tag) for t in tree[1:] if isinstance(t, tuple))
 
 
@@ -440,7 +536,9 @@ def build_plan(groups: List[_Group], tensor_ref) -> Plan:
     for g in groups:
         out_rc = np.concatenate(g.out_rc, 0)
         leaf_rc = [np.concatenate([li[k] for li in g.leaf_rc], 0) for k in range(len(g.leaf_blocks))]
-        if g.tree[0] == "matmul" and g.tree[1][0] == "leaf" and g.tree[2][0] == "leaf":
+        if g.tree[0] == "reduce":
+            launch = _plan_reduce(g, out_rc, leaf_rc, np.concatenate(g.order), tensor_ref)
+        elif g.tree[0] == "matmul" and g.tree[1][0] == "leaf" and g.tree[2][0] == "leaf":
             launch = _plan_matmul(g, out_rc, leaf_rc, tensor_ref)
         elif _has(g.tree, "matmul"):
             raise PlanError("a tile matmul combined with other ops in one store() is not "
@@ -487,6 +585,100 @@ def _plan_eltwise(g: _Group, out_rc, leaf_rc, tensor_ref) -> EltwiseLaunch:
     h = min(r1 * TILE, H) - y0
     w = min(c1 * TILE, W) - x0
     return EltwiseLaunch(prog, operands, tensor_ref(out_t), (y0, x0, h, w), n)
+
+
+def _plan_reduce(g: _Group, out_rc, leaf_rc, order, tensor_ref) -> ReduceLaunch:
+    """Iteration space: output tile coordinates along the kept axes, the tile
+    coordinates of the first operand that varies along a reduced axis there.
+    Every operand must be an affine image of it (as for eltwise), every
+    output tile must collect one rectangle row / column of it."""
+    _, kind, dims, inner, ishape, stree = g.tree
+    n = out_rc.shape[0]
+    out_t = g.out_tensor
+    if getattr(out_t, "is_block_float", False) or any(
+            getattr(t, "is_block_float", False) for t in g.leaf_tensors):
+        raise PlanError("block-float tensors are supported as the B operand of a tile matmul only")
+    it = np.empty((n, 2), dtype=np.int64)
+    degenerate = [False, False]  # iteration axis of one element (size-1 tensor dimension)
+    for ax in (0, 1):
+        if ax not in dims:
+            it[:, ax] = out_rc[:, ax]
+            degenerate[ax] = out_t.shape[ax] == 1
+            continue
+        cands = [k for k in range(len(leaf_rc)) if g.leaf_tensors[k].shape[ax] > 1]
+        varying = [k for k in cands if not np.all(leaf_rc[k][:, ax] == leaf_rc[k][0, ax])]
+        prim = varying[0] if varying else (cands[0] if cands else 0)
+        it[:, ax] = leaf_rc[prim][:, ax]
+        degenerate[ax] = not cands
+    key = it[:, 0] * (int(it[:, 1].max()) + 1) + it[:, 1]
+    if np.unique(key).size != n:
+        raise PlanError("a reduction reads an expression tile twice (every output tile must "
+                        "reduce distinct tiles of its operands)")
+    r0, r1, c0, c1 = _rect(it)
+    if (r1 - r0) * (c1 - c0) != n:
+        raise PlanError("the tiles a reduction reads do not form a rectangle")
+    out_tile = [0, 0]
+    for ax in (0, 1):
+        o = out_rc[:, ax]
+        if ax in dims:
+            if not np.all(o == o[0]):
+                raise PlanError("the reduced tiles of one store site land in more than one output "
+                                "tile along the reduced dimension (only one run of tiles per "
+                                "output tile is supported)")
+            out_tile[ax] = int(o[0])
+        else:
+            d = o - it[:, ax]
+            if not np.all(d == d[0]):
+                raise PlanError("reduction output tiles are not an offset of the reduced tiles")
+            out_tile[ax] = int(d[0]) + (r0 if ax == 0 else c0)
+    # stores per output tile: several only when they accumulate a sum
+    okey = out_rc[:, 0] * (int(out_rc[:, 1].max()) + 1) + out_rc[:, 1]
+    pairs = np.unique(np.stack([okey, order], 1), axis=0)
+    multi = np.unique(pairs[:, 0]).size != pairs.shape[0]
+    if multi and not g.acc:
+        raise PlanError("an output tile is stored more than once without acc=True")
+    if multi and kind == "max":
+        raise PlanError("reduce_max partial results accumulated with store(acc=True) would be "
+                        "added (store acc semantics); reduce over one block per output tile")
+    # operands
+    leaf_nodes: Dict[int, X.Leaf] = {}
+    specs: Dict[int, OperandSpec] = {}
+    for k, lf in enumerate(g.leaf_blocks):
+        tens = g.leaf_tensors[k]
+        h, w = tens.shape
+        rm, ro = _axis_map(it[:, 0], leaf_rc[k][:, 0], h)
+        cm, co = _axis_map(it[:, 1], leaf_rc[k][:, 1], w)
+        leaf = X.Leaf(k, lf[1].cb.dtype)
+        leaf_nodes[id(lf)] = leaf
+        specs[k] = OperandSpec(tensor_ref(tens), rm, cm, ro, co)
+    prog = X.compile_expr(_to_expr(inner, leaf_nodes))
+    operands = [specs[s.leaf.ref] if s.leaf is not None else None for s in prog.steps]
+    y0, x0 = r0 * TILE, c0 * TILE
+    h = 1 if degenerate[0] else (r1 - r0) * TILE
+    w = 1 if degenerate[1] else (c1 - c0) * TILE
+    # result placement: size-1 tensor dimensions take the value only, full
+    # tiles the zero-padded result tile
+    red_sizes = [out_t.shape[ax] for ax in dims]
+    pads = {sz > 1 for sz in red_sizes}
+    if len(pads) != 1:
+        raise PlanError("a reduction over both dims needs an output that is size 1 in both or "
+                        "whole tiles in both")
+    out_pad = pads.pop()
+    oy = 0 if (0 in dims and out_t.shape[0] == 1) else out_tile[0] * TILE
+    ox = 0 if (1 in dims and out_t.shape[1] == 1) else out_tile[1] * TILE
+    scaler_ref, scaler_at, scale = None, (0, 0), 1.0
+    if stree[0] == "const":
+        scale = float(stree[1])
+    else:
+        src = np.concatenate(g.scaler_rc, 0)
+        if not np.all(src == src[0]):
+            raise PlanError("a reduction's scaler must be the same tile for every store")
+        st_ = g.scaler_tensor
+        sr = int(src[0, 0]) * TILE if st_.shape[0] > 1 else 0
+        sc = int(src[0, 1]) * TILE if st_.shape[1] > 1 else 0
+        scaler_ref, scaler_at = tensor_ref(st_), (sr, sc)
+    return ReduceLaunch(prog, operands, tensor_ref(out_t), kind, tuple(dims), (y0, x0, h, w),
+                        (oy, ox), out_pad, scaler_ref, scaler_at, scale, n)
 
 
 def _plan_matmul(g: _Group, out_rc, leaf_rc, tensor_ref) -> MatmulLaunch:
@@ -559,6 +751,16 @@ def _execute_one(l, args, stream, Kn) -> None:
             ops.append(Kn.OperandMap(spec.ref.resolve(args), spec.row_mask, spec.col_mask,
                                      spec.row_off, spec.col_off))
         Kn.eltwise(l.prog, ops, l.out.resolve(args), region=l.region, stream=stream)
+    elif isinstance(l, ReduceLaunch):
+        ops = [None if spec is None else
+               Kn.OperandMap(spec.ref.resolve(args), spec.row_mask, spec.col_mask, spec.row_off,
+                             spec.col_off) for spec in l.operands]
+        sc = None
+        if l.scaler is not None:
+            r, c = l.scaler_at
+            sc = l.scaler.resolve(args)[r:r + 1, c:c + 1]
+        Kn.reduce(l.prog, ops, l.kind, l.dims, l.out.resolve(args), l.region, l.out_origin,
+                  l.out_pad, sc, l.scale, stream=stream)
     else:
         a, b, c = l.a.resolve(args), l.b.resolve(args), l.c.resolve(args)
         if c.data_ptr() in (a.data_ptr(), b.data_ptr()):

@@ -33,10 +33,14 @@ def launch_work(l, args: Dict[Any, Any]) -> Tuple[float, str, float]:
     """(algorithmic work, unit, peak) of one launch: bytes read + written for
     an elementwise launch (an operand counted over the rows / columns it
     actually spans), 2 M N K flops for a tile matmul."""
-    if isinstance(l, P.EltwiseLaunch):
+    if isinstance(l, (P.EltwiseLaunch, P.ReduceLaunch)):
         _, _, h, w = l.region
         out = l.out.resolve(args)
-        total = h * w * _elem_size(out.dtype)
+        if isinstance(l, P.ReduceLaunch):  # one result per kept row / column
+            nres = (1 if 0 in l.dims else h) * (1 if 1 in l.dims else w)
+            total = nres * _elem_size(out.dtype)
+        else:
+            total = h * w * _elem_size(out.dtype)
         seen = set()
         for spec in l.operands:
             if spec is None or id(spec.ref) in seen:
@@ -56,6 +60,9 @@ def launch_work(l, args: Dict[Any, Any]) -> Tuple[float, str, float]:
 
 
 def _launch_name(l, args) -> str:
+    if isinstance(l, P.ReduceLaunch):
+        _, _, h, w = l.region
+        return f"ttlh_reduce {l.kind} dims {list(l.dims)} over {h}x{w}, {len(l.prog.steps)} steps"
     if isinstance(l, P.EltwiseLaunch):
         _, _, h, w = l.region
         nops = len({id(s.ref) for s in l.operands if s is not None})

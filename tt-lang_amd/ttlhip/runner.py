@@ -36,11 +36,13 @@ def _trace_print(*args, **kwargs):
 
 def _refs(plan: P.Plan):
     for l in plan.launches:
-        if isinstance(l, P.EltwiseLaunch):
+        if isinstance(l, (P.EltwiseLaunch, P.ReduceLaunch)):
             yield l.out
             for spec in l.operands:
                 if spec is not None:
                     yield spec.ref
+            if isinstance(l, P.ReduceLaunch) and l.scaler is not None:
+                yield l.scaler
         else:
             yield from (l.a, l.b, l.c)
 
