@@ -183,6 +183,23 @@ int ttlh_reduce(const ttlh_instr* prog, const ttlh_operand* in, int n_instr,
                 void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Tilized element order (the TILE_LAYOUT storage of ttnn tensors, which the
+ * reference's compiled path requires: python/ttl/ttl_api.py:489-506; the
+ * tilize itself lives in un-vendored tt-metal).  Tiles of 32x32 row-major
+ * over the tile grid; a tile is four 16x16 faces (f0 rows 0-15 / cols 0-15,
+ * f1 rows 0-15 / cols 16-31, f2 rows 16-31 / cols 0-15, f3 rows 16-31 /
+ * cols 16-31), each face row-major: element (i, j) of a tensor with C
+ * columns sits at tile (i / 32) * (C / 32) + j / 32, offset
+ * 256 * (2 * ((i % 32) / 16) + (j % 32) / 16) + 16 * (i % 16) + j % 16.
+ * rows, cols: multiples of 32; elem_bytes 2 (bf16) or 4 (f32); the
+ * row-major side has row stride `ld` elements; device pointers, 16-byte
+ * aligned.  Used to exchange tensors with tilized ttnn buffers.          */
+int ttlh_tilize(const void* src, int64_t src_ld, void* dst, int64_t rows,
+                int64_t cols, int elem_bytes, void* stream);
+int ttlh_untilize(const void* src, void* dst, int64_t dst_ld, int64_t rows,
+                  int64_t cols, int elem_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
  * Tile matmul:  C[M,N] (=|+=) A[M,K] . B[K,N]
  *
  * Replaces Block.__matmul__ + store(acc=True) over the K tiles

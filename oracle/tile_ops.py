@@ -129,6 +129,26 @@ def sdpa_ref(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
     return torch.matmul(p / l, vd)
 
 
+# ---- tilized element order ------------------------------------------------
+# The storage order of a TILE_LAYOUT tensor (which the reference's compiled
+# path requires, python/ttl/ttl_api.py:489-506; the tilize itself is in
+# un-vendored tt-metal): 32x32 tiles row-major over the tile grid, each tile
+# four 16x16 faces (rows 0-15 / cols 0-15, rows 0-15 / cols 16-31, rows 16-31 /
+# cols 0-15, rows 16-31 / cols 16-31), each face row-major - the face split of
+# the bfloat8_b tiles (oracle/bfp8_ref.c).
+
+def tilize_ref(x: torch.Tensor) -> torch.Tensor:
+    """[R, C] (multiples of 32) -> 1-D tensor in tilized order."""
+    r, c = x.shape
+    t = x.reshape(r // TILE, 2, 16, c // TILE, 2, 16)  # (tr, fr, i, tc, fc, j)
+    return t.permute(0, 3, 1, 4, 2, 5).reshape(-1)
+
+
+def untilize_ref(d: torch.Tensor, rows: int, cols: int) -> torch.Tensor:
+    t = d.reshape(rows // TILE, cols // TILE, 2, 2, 16, 16)  # (tr, tc, fr, fc, i, j)
+    return t.permute(0, 2, 4, 1, 3, 5).reshape(rows, cols)
+
+
 # ---- seeded inputs shared by the CPU oracle and the GPU path --------------
 
 def seeded(shape: Tuple[int, ...], dist: str, seed: int, dtype=torch.bfloat16,

@@ -20,7 +20,7 @@ OUT_DIR = PKG / "ttlhip"
 LIB = OUT_DIR / "libttlhip.so"
 OBJ_DIR = CSRC / "_build"
 
-SOURCES = ["runtime.hip", "eltwise.hip", "matmul.hip", "bfp8.hip", "sdpa.hip"]
+SOURCES = ["runtime.hip", "eltwise.hip", "matmul.hip", "bfp8.hip", "sdpa.hip", "layout.hip"]
 
 ARCH = "gfx950"
 

@@ -175,6 +175,39 @@ def matmul(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, accumulate: bool =
            M, N, K, int(bool(accumulate)), L.stream_ptr(stream))
 
 
+def tilize(x: torch.Tensor, stream=None) -> torch.Tensor:
+    """Row-major bf16 / f32 [rows, cols] (device) -> its tilized element order
+    (tiles row-major over the tile grid, four 16x16 faces per tile), as a 1-D
+    device tensor of rows * cols elements."""
+    _check_device(x, "tilize input")
+    if x.dtype not in (torch.bfloat16, torch.float32) or x.stride(1) != 1:
+        raise ValueError("tilize takes a bf16 / f32 tensor with unit column stride")
+    rows, cols = x.shape
+    out = torch.empty(rows * cols, dtype=x.dtype, device=x.device)
+    L.call("ttlh_tilize", x.data_ptr(), x.stride(0), out.data_ptr(), rows, cols,
+           x.element_size(), L.stream_ptr(stream))
+    return out
+
+
+def untilize(data: torch.Tensor, rows: int, cols: int, out: Optional[torch.Tensor] = None,
+             stream=None) -> torch.Tensor:
+    """Tilized elements (device, rows * cols of them) -> row-major [rows, cols]
+    (into `out` when given, which may have a row stride larger than cols)."""
+    if not data.is_cuda:
+        raise RuntimeError("untilize input must be a device (HIP) tensor; there is no CPU path")
+    if data.dtype not in (torch.bfloat16, torch.float32) or data.numel() != rows * cols:
+        raise ValueError(f"untilize needs {rows * cols} bf16 / f32 elements, got "
+                         f"{data.numel()} {data.dtype}")
+    if out is None:
+        out = torch.empty(rows, cols, dtype=data.dtype, device=data.device)
+    _check_device(out, "untilize output")
+    if out.dtype != data.dtype or tuple(out.shape) != (rows, cols) or out.stride(1) != 1:
+        raise ValueError("untilize output must match the data dtype and [rows, cols] shape")
+    L.call("ttlh_untilize", data.contiguous().data_ptr(), out.data_ptr(), out.stride(0), rows,
+           cols, data.element_size(), L.stream_ptr(stream))
+    return out
+
+
 def bfp8_tiles_bytes(rows: int, cols: int) -> int:
     if rows % 32 or cols % 32:
         raise ValueError(f"bfloat8_b needs whole 32x32 tiles, got {rows}x{cols}")

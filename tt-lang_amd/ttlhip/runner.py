@@ -78,9 +78,20 @@ class KernelRunner:
         return (tuple(self._key_of(a) for a in args),
                 tuple(sorted((k, self._key_of(v)) for k, v in kwargs.items())))
 
+    @staticmethod
+    def _check_layouts(args, kwargs) -> None:
+        """Kernel tensors must be tilized (python/ttl/ttl_api.py:489-506)."""
+        for i, a in enumerate(list(args) + list(kwargs.values())):
+            lay = getattr(a, "layout", None)
+            if isinstance(a, ttnn.Tensor) and "TILE" not in str(lay):
+                raise ValueError(
+                    f"TTNN interop requires tilized tensors, but tensor {i} has layout {lay}. "
+                    "Use ttnn.to_layout(tensor, ttnn.TILE_LAYOUT) to convert.")
+
     # -- tracing ---------------------------------------------------------------
     def trace(self, *args, **kwargs) -> P.Plan:
         """Runs the kernel body and traces every core; returns the plan (no GPU)."""
+        self._check_layouts(args, kwargs)
         g = dict(self.func.__globals__)
         g["grid"] = self.grid
         body = types.FunctionType(self.func.__code__, g, self.func.__name__,

@@ -103,10 +103,14 @@ class Tensor:
     """
 
     def __init__(self, tensor: torch.Tensor, *, block: Optional[BlockFloatType] = None,
-                 logical_shape: Optional[Tuple[int, ...]] = None) -> None:
+                 logical_shape: Optional[Tuple[int, ...]] = None, layout: Any = None) -> None:
         if not isinstance(tensor, torch.Tensor):
             raise TypeError(f"ttnn.Tensor wraps a torch.Tensor, got {type(tensor)}")
         self._tensor = tensor
+        # storage stays row-major either way (the kernels address it so); the
+        # layout is the one the tensor was created / converted with, checked
+        # at kernel calls like the reference's compiled path does
+        self._layout = TILE_LAYOUT if layout is None else layout
         if _created is not None:  # created while a kernel body runs
             _created.append(self)
         # block-float tensors: _tensor holds the packed tile bytes (uint8)
@@ -130,7 +134,18 @@ class Tensor:
 
     @property
     def layout(self):
-        return TILE_LAYOUT
+        return self._layout
+
+    def tiled_data(self) -> torch.Tensor:
+        """The tensor in tilized element order (32x32 tiles row-major over the
+        tile grid, four 16x16 faces each: the storage order of a TILE_LAYOUT
+        ttnn tensor), as a 1-D device tensor; block-float tensors return their
+        packed tile bytes."""
+        if self._block is not None:
+            return self._tensor
+        from ttlhip import kernels as K
+
+        return K.tilize(self._tensor)
 
     def to_torch(self) -> torch.Tensor:
         """Host copy; block-float tensors come back as float32 values (the
@@ -233,45 +248,46 @@ def _block_from_fp32(t: torch.Tensor, block: BlockFloatType) -> Tensor:
     return Tensor(packed.to(_device()), block=block, logical_shape=tuple(t.shape))
 
 
-def rand(shape, dtype=bfloat16, **_: Any) -> Tensor:
+def rand(shape, dtype=bfloat16, layout: Any = None, **_: Any) -> Tensor:
     """U[0, 1) drawn in fp32 from torch's global generator, then cast - the
     same stream and rounding as python/sim/ttnnsim.py:521-531."""
     t = torch.rand(_shape(shape), dtype=torch.float32)
     if isinstance(dtype, BlockFloatType):
         return _block_from_fp32(t, dtype)
-    return Tensor(t.to(dtype).to(_device()))
+    return Tensor(t.to(dtype).to(_device()), layout=layout)
 
 
-def empty(shape, dtype=bfloat16, **_: Any) -> Tensor:
+def empty(shape, dtype=bfloat16, layout: Any = None, **_: Any) -> Tensor:
     if isinstance(dtype, BlockFloatType):
         return _block_from_fp32(torch.zeros(_shape(shape)), dtype)
-    return Tensor(torch.empty(_shape(shape), dtype=dtype, device=_device()))
+    return Tensor(torch.empty(_shape(shape), dtype=dtype, device=_device()), layout=layout)
 
 
-def zeros(shape, dtype=bfloat16, **_: Any) -> Tensor:
+def zeros(shape, dtype=bfloat16, layout: Any = None, **_: Any) -> Tensor:
     if isinstance(dtype, BlockFloatType):
         return _block_from_fp32(torch.zeros(_shape(shape)), dtype)
-    return Tensor(torch.zeros(_shape(shape), dtype=dtype, device=_device()))
+    return Tensor(torch.zeros(_shape(shape), dtype=dtype, device=_device()), layout=layout)
 
 
-def ones(shape, dtype=bfloat16, **_: Any) -> Tensor:
+def ones(shape, dtype=bfloat16, layout: Any = None, **_: Any) -> Tensor:
     if isinstance(dtype, BlockFloatType):
         return _block_from_fp32(torch.ones(_shape(shape)), dtype)
-    return Tensor(torch.ones(_shape(shape), dtype=dtype, device=_device()))
+    return Tensor(torch.ones(_shape(shape), dtype=dtype, device=_device()), layout=layout)
 
 
-def full(shape, fill_value: float, dtype=bfloat16, **_: Any) -> Tensor:
+def full(shape, fill_value: float, dtype=bfloat16, layout: Any = None, **_: Any) -> Tensor:
     if isinstance(dtype, BlockFloatType):
         return _block_from_fp32(torch.full(_shape(shape), float(fill_value)), dtype)
-    return Tensor(torch.full(_shape(shape), fill_value, dtype=dtype, device=_device()))
+    return Tensor(torch.full(_shape(shape), fill_value, dtype=dtype, device=_device()),
+                  layout=layout)
 
 
 def zeros_like(t: Tensor, dtype=None, **_: Any) -> Tensor:
-    return Tensor(torch.zeros_like(t._tensor, dtype=dtype))
+    return Tensor(torch.zeros_like(t._tensor, dtype=dtype), layout=t.layout)
 
 
 def empty_like(t: Tensor, dtype=None, **_: Any) -> Tensor:
-    return Tensor(torch.empty_like(t._tensor, dtype=dtype))
+    return Tensor(torch.empty_like(t._tensor, dtype=dtype), layout=t.layout)
 
 
 def from_torch(tensor: torch.Tensor, dtype=None, layout: Any = None,
@@ -284,7 +300,21 @@ def from_torch(tensor: torch.Tensor, dtype=None, layout: Any = None,
         return _block_from_fp32(t.cpu(), dtype)
     if dtype is not None:
         t = t.to(dtype)
-    return Tensor(t.to(_device()).contiguous())
+    return Tensor(t.to(_device()).contiguous(), layout=layout)
+
+
+def from_tiled_data(data: torch.Tensor, shape: Sequence[int], dtype=None,
+                    **_: Any) -> Tensor:
+    """A tensor from elements in tilized order (see Tensor.tiled_data), e.g.
+    the storage of a TILE_LAYOUT ttnn tensor read from a file or another
+    process."""
+    from ttlhip import kernels as K
+
+    rows, cols = (int(d) for d in shape)
+    d = data.detach()
+    if dtype is not None:
+        d = d.to(dtype)
+    return Tensor(K.untilize(d.to(_device()).reshape(-1), rows, cols))
 
 
 def to_torch(t: Union[Tensor, torch.Tensor], **_: Any) -> torch.Tensor:
@@ -294,7 +324,21 @@ def to_torch(t: Union[Tensor, torch.Tensor], **_: Any) -> torch.Tensor:
 
 
 def to_layout(t: Tensor, layout: Any, **_: Any) -> Tensor:
-    return t
+    """The same data with `layout` (TILE_LAYOUT / ROW_MAJOR_LAYOUT); storage is
+    row-major in both, see Tensor.tiled_data for the tilized element order."""
+    if t.is_block_float:
+        if "TILE" not in str(layout):
+            raise ValueError(f"a {t.dtype.name} tensor exists in TILE_LAYOUT only")
+        return t
+    return Tensor(t._tensor, layout=layout)
+
+
+def tilize(t: Tensor, **_: Any) -> Tensor:
+    return to_layout(t, TILE_LAYOUT)
+
+
+def untilize(t: Tensor, **_: Any) -> Tensor:
+    return to_layout(t, ROW_MAJOR_LAYOUT)
 
 
 def repeat(t: Tensor, repeats: Sequence[int], **_: Any) -> Tensor:
