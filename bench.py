@@ -13,6 +13,7 @@ own roofline figures:
   C4 bf16 x bfp8 4096x4096x11008   ttlh_matmul_bfp8w_ws (two-pass)  TFLOP/s
   C5 SDPA [4,32,4096,128]     ttlh_sdpa_fwd                        TFLOP/s
   row sums 4096^2 (spec reduce_sum)  tt-lang kernel (reduce_rows)  HBM GB/s
+  tilize 4096^2 bf16 (TILE_LAYOUT)   ttlh_tilize                  HBM GB/s
 
 A "step" is one pass of the hot path over one batch of synthetic input: one
 execution of the kernel's launch plan over one resident buffer set.  Inputs
@@ -224,6 +225,46 @@ class ReduceWorkload(PlanWorkload):
                 "oracle": "float64 row sums rounded once to bf16"}
 
 
+class TilizeWorkload(Workload):
+    """Row-major bf16 -> tilized element order (ttnn TILE_LAYOUT storage,
+    16x16 faces) through ttlh_tilize; HBM-bound byte permutation, buffer sets
+    rotated over > 256 MB."""
+
+    def __init__(self, name, n, seed=5678):
+        self.name, self.n, self.seed = name, n, seed
+        self.config = (f"tilize bf16 {n}x{n} row-major -> 32x32 tiles of four 16x16 faces "
+                       "(ttnn TILE_LAYOUT storage order)")
+
+    def kernel_name(self):
+        return "layout_kernel"
+
+    def work_per_step(self):
+        return 2 * self.n * self.n * 2
+
+    def setup(self):
+        from oracle.tile_ops import seeded
+        from ttlhip import _lib as L
+        self.L = L
+        self.x = seeded((self.n, self.n), "uniform", self.seed, lo=-1, hi=1)
+        x = self.x.cuda()
+        nsets = max(3, math.ceil(300e6 / self.work_per_step()))
+        self.sets = [(x if i == 0 else x.clone(),
+                      torch.empty(self.n * self.n, dtype=torch.bfloat16, device="cuda"))
+                     for i in range(nsets)]
+
+    def launch(self, i):
+        src, dst = self.sets[i % len(self.sets)]
+        self.L.call("ttlh_tilize", src.data_ptr(), self.n, dst.data_ptr(), self.n, self.n, 2,
+                    self.L.stream_ptr())
+
+    def check(self):
+        from oracle import tile_ops as O
+        self.launch(0)
+        torch.cuda.synchronize()
+        ok = torch.equal(self.sets[0][1].cpu(), O.tilize_ref(self.x))
+        return {"bit_exact": bool(ok), "oracle": "reshape / permute restatement (tilize_ref)"}
+
+
 class MatmulWorkload(PlanWorkload):
     """C3 through the multicore-style tt-lang kernel (13x10 grid, (1,1) CBs,
     store(acc=True) over K) -> one MFMA GEMM launch."""
@@ -376,6 +417,7 @@ WORKLOADS = {
                                                           11008, 4096),
     "sdpa_4x32x4096x128": lambda: SdpaWorkload("sdpa_4x32x4096x128", 4, 32, 4096, 128),
     "reduce_sum_rows_4096": lambda: ReduceWorkload("reduce_sum_rows_4096", 4096),
+    "tilize_4096": lambda: TilizeWorkload("tilize_4096", 4096),
 }
 HEADLINE = "exp_bcast_mul_4096"
 
