@@ -910,6 +910,45 @@ __global__ __launch_bounds__(256) void reduce_rows_kernel(const RedArgs a) {
   }
 }
 
+// Row reduce of wide rows (w >= 2048, MODE 1 / 2): one workgroup per row, so
+// a row's reads spread over four waves (a quarter of the chunks each, two
+// chunks per lane in flight) and 4x as many waves hide each other's latency;
+// the four wave results combine through LDS in wave order.
+template <bool TO_WS, int MODE>
+__global__ __launch_bounds__(256) void reduce_rows_wide_kernel(const RedArgs a) {
+  __shared__ float part[4];
+  const int64_t row = blockIdx.x;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const float s = red_scale(a);
+  const int64_t y = a.e.y0 + row;
+  constexpr int64_t S = 256 * 8;
+  const int64_t xf = int64_t(t) * 8;  // a.w >= 2048: every lane has a chunk
+  auto at = [&](int64_t xo) { return a.e.x0 + (xo < a.w ? xo : xf); };
+  RedChunk c[2];
+  red_unroll([&](auto i) { c[i] = red_fetch<MODE>(a.e, y, at(xf + i * S)); },
+             std::make_integer_sequence<int, 2>());
+  float r = red_identity(a.kind);
+  for (int64_t xb = xf; xb < a.w; xb += 2 * S) {
+    red_unroll([&](auto i) {
+      const int64_t xo = xb + i * S;
+      if (xo < a.w) {
+        const f32x8 v = red_eval<MODE>(a.e, c[i], y, a.e.x0 + xo);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) r = red_combine(a.kind, r, v[k] * s);
+      }
+      c[i] = red_fetch<MODE>(a.e, y, at(xo + 2 * S));
+    }, std::make_integer_sequence<int, 2>());
+  }
+  r = red_wave(a.kind, r);
+  if (lane == 0) part[wave] = r;
+  __syncthreads();
+  if (t != 0) return;
+  r = red_combine(a.kind, red_combine(a.kind, part[0], part[1]),
+                  red_combine(a.kind, part[2], part[3]));
+  if constexpr (TO_WS) a.ws[row] = r;
+  else red_write<TTLH_REDUCE_DIM1>(a, row, r);
+}
+
 // Column reduce; MODE as for the row reduce (the pipeline runs over the
 // wave's rows: rows r, r + 4, ... in flight).
 template <int VEC, int MODE>
@@ -1290,9 +1329,14 @@ extern "C" int ttlh_reduce(const ttlh_instr* prog, const ttlh_operand* in, int n
   const int mode = !pi.vec || pi.n_ops < 1 || pi.n_ops > 4 ? 0 : (plain ? 1 : (pi.full ? 0 : 2));
   const int variant = mode == 0 ? (pi.vec ? 1 : 0) : mode + 1;
   if (dims != TTLH_REDUCE_DIM0) {
-    const dim3 grid(static_cast<uint32_t>((h + 3) / 4));
+    const bool wide = mode != 0 && w >= 2048;
+    const dim3 grid(static_cast<uint32_t>(wide ? h : (h + 3) / 4));
 #define TTLH_ROWS(WS)                                                                        \
-  switch (variant) {                                                                         \
+  if (wide && mode == 1)                                                                     \
+    hipLaunchKernelGGL((reduce_rows_wide_kernel<WS, 1>), grid, block, 0, s, a);             \
+  else if (wide)                                                                             \
+    hipLaunchKernelGGL((reduce_rows_wide_kernel<WS, 2>), grid, block, 0, s, a);             \
+  else switch (variant) {                                                                    \
     case 0: hipLaunchKernelGGL((reduce_rows_kernel<1, WS, 0>), grid, block, 0, s, a); break; \
     case 1: hipLaunchKernelGGL((reduce_rows_kernel<8, WS, 0>), grid, block, 0, s, a); break; \
     case 2: hipLaunchKernelGGL((reduce_rows_kernel<8, WS, 1>), grid, block, 0, s, a); break; \
