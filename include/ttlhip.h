@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define TTLH_ABI_VERSION 1
+#define TTLH_ABI_VERSION 2
 
 /* status codes */
 #define TTLH_OK 0
@@ -89,7 +89,33 @@ enum ttlh_opcode {
   TTLH_OP_RELU = 23,
   TTLH_OP_SIGMOID = 24,
   TTLH_OP_RECIP = 25,
-  TTLH_OP_POWI = 26     /* acc ** imm (integer exponent, Block.__pow__)    */
+  TTLH_OP_POWI = 26,    /* acc ** imm (integer exponent, Block.__pow__)    */
+  /* the spec's further math functions (docs/sphinx/specs/
+   * TTLangSpecification.md:700-750; neither the reference compiler's op
+   * table nor its simulator implements them): computed in fp32 and rounded
+   * once, as the torch functions the spec links do on bfloat16 tensors */
+  TTLH_OP_EXP2 = 27,
+  TTLH_OP_EXPM1 = 28,
+  TTLH_OP_LOG1P = 29,   /* ttl.math.logp1                                  */
+  TTLH_OP_SIN = 30,
+  TTLH_OP_COS = 31,
+  TTLH_OP_TAN = 32,
+  TTLH_OP_ASIN = 33,
+  TTLH_OP_ACOS = 34,
+  TTLH_OP_ATAN = 35,
+  TTLH_OP_ASINH = 36,
+  TTLH_OP_ACOSH = 37,
+  TTLH_OP_ATANH = 38,
+  TTLH_OP_GELU = 39,    /* x / 2 (1 + erf(x / sqrt 2)) (torch's exact GELU) */
+  TTLH_OP_SILU = 40,    /* x / (1 + exp(-x))                               */
+  TTLH_OP_SOFTSIGN = 41,/* x / (1 + |x|), rounded once (the drop-in's
+                           ttl.math.softsign composes abs, add, div
+                           instead, rounding per op like torch's)        */
+  TTLH_OP_HARDSIGMOID = 42, /* min(max(x + 3, 0), 6) / 6                   */
+  TTLH_OP_ELU = 43,     /* x > 0 ? x : imm (exp(x) - 1)                    */
+  TTLH_OP_CELU = 44,    /* max(x, 0) + min(imm (exp(x / imm) - 1), 0)      */
+  TTLH_OP_SELU = 45,    /* imm (max(x, 0) + min(imm2 (exp(x) - 1), 0))     */
+  TTLH_OP_SOFTPLUS = 46 /* imm x > imm2 ? x : log(1 + exp(imm x)) / imm    */
 };
 
 enum ttlh_form {
@@ -110,7 +136,10 @@ typedef struct ttlh_instr {
   uint8_t form; /* ttlh_form                                      */
   uint8_t rnd;  /* TTLH_BF16 or TTLH_F32                          */
   uint8_t pad;
-  float imm;    /* CONST value / immediate operand / POWI exponent */
+  float imm;    /* CONST value / immediate operand / POWI exponent /
+                   first parameter of ELU, CELU, SELU, SOFTPLUS   */
+  float imm2;   /* second parameter of SELU (alpha), SOFTPLUS
+                   (threshold); 0 otherwise                       */
 } ttlh_instr;
 
 #define TTLH_MAX_INSTR 12

@@ -347,6 +347,30 @@ def make_ttl():
         setattr(_Math, name, staticmethod(lambda x, _f=fn: _tiles_of(x).map(_f)))
     _Math.max = staticmethod(lambda a, b: _tiles_of(a)._bin(b, torch.maximum))
     _Math.min = staticmethod(lambda a, b: _tiles_of(a)._bin(b, torch.minimum))
+    # the spec's further math functions (TTLangSpecification.md:700-750) as
+    # the torch functions it links, one op per tile in the tile dtype
+    from oracle.tile_ops import PARAM_UNARY, UNARY
+    for name in ("exp2", "expm1", "logp1", "sin", "cos", "tan", "asin", "acos", "atan", "asinh",
+                 "acosh", "atanh", "gelu", "silu", "softsign", "hardsigmoid"):
+        setattr(_Math, name, staticmethod(lambda x, _f=UNARY[name]: _tiles_of(x).map(_f)))
+    _Math.square = staticmethod(lambda x: _tiles_of(x).map(torch.square))
+    _Math.rsub = staticmethod(lambda a, b: _tiles_of(a).map(lambda t: b - t))
+    _Math.relu_max = staticmethod(
+        lambda x, u: _tiles_of(x).map(lambda t: torch.relu(torch.clamp(t, max=u))))
+    _Math.relu_min = staticmethod(
+        lambda x, lo: _tiles_of(x).map(lambda t: torch.relu(torch.clamp(t, min=lo))))
+    _Math.hardtanh = staticmethod(lambda x, mn, mx: _tiles_of(x).map(
+        lambda t: torch.nn.functional.hardtanh(t, mn, mx)))
+    _Math.leaky_relu = staticmethod(lambda x, s: _tiles_of(x).map(
+        lambda t: torch.nn.functional.leaky_relu(t, s)))
+    _Math.prelu = staticmethod(_Math.leaky_relu)
+    _Math.elu = staticmethod(lambda x, a: _tiles_of(x).map(lambda t: PARAM_UNARY["elu"](t, a, 0)))
+    _Math.celu = staticmethod(lambda x, a, _ar=None: _tiles_of(x).map(
+        lambda t: PARAM_UNARY["celu"](t, a, 0)))
+    _Math.selu = staticmethod(lambda x, sc, a: _tiles_of(x).map(
+        lambda t: PARAM_UNARY["selu"](t, sc, a)))
+    _Math.softplus = staticmethod(lambda x, beta, _br=None, threshold=20.0: _tiles_of(x).map(
+        lambda t: PARAM_UNARY["softplus"](t, beta, threshold)))
     _Math.reduce_sum = staticmethod(lambda x, scaler, dims=None: _reduce("sum", x, scaler, dims))
     _Math.reduce_max = staticmethod(lambda x, scaler, dims=None: _reduce("max", x, scaler, dims))
 

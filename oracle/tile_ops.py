@@ -44,6 +44,50 @@ UNARY = {
     "relu": torch.relu,
     "sigmoid": torch.sigmoid,
     "recip": torch.reciprocal,
+    # the spec's further math functions (TTLangSpecification.md:700-750),
+    # the torch functions the spec links
+    "exp2": torch.exp2,
+    "expm1": torch.expm1,
+    "logp1": torch.log1p,
+    "sin": torch.sin,
+    "cos": torch.cos,
+    "tan": torch.tan,
+    "asin": torch.asin,
+    "acos": torch.acos,
+    "atan": torch.atan,
+    "asinh": torch.asinh,
+    "acosh": torch.acosh,
+    "atanh": torch.atanh,
+    "gelu": lambda t: gelu_exact(t),
+    "silu": torch.nn.functional.silu,
+    "softsign": torch.nn.functional.softsign,
+    "hardsigmoid": torch.nn.functional.hardsigmoid,
+}
+
+
+def gelu_exact(x: torch.Tensor) -> torch.Tensor:
+    """GELU x / 2 (1 + erf(x / sqrt 2)) evaluated as x / 2 erfc(-x / sqrt 2) in
+    float64 and rounded (via fp32) to x's dtype.  torch's CPU kernel (the
+    function the spec links) cancels in 1 + erf for x << 0 and is up to 32
+    bf16 ulp off at x = -5, so the oracle takes the mathematical value."""
+    d = x.double()
+    return (0.5 * d * torch.erfc(-d / math.sqrt(2.0))).to(torch.float32).to(x.dtype)
+
+
+def selu_p(x: torch.Tensor, scale: float, alpha: float) -> torch.Tensor:
+    """scale (max(x, 0) + min(alpha (exp(x) - 1), 0)) in fp32, rounded once
+    (torch.nn.SELU with the spec's explicit parameters)."""
+    f = x.float()
+    r = scale * (torch.clamp(f, min=0) + torch.clamp(alpha * torch.expm1(f), max=0))
+    return r.to(x.dtype)
+
+
+# parameterised unary functions: name -> f(x, p0, p1)
+PARAM_UNARY = {
+    "elu": lambda x, a, _b: torch.nn.functional.elu(x, alpha=a),
+    "celu": lambda x, a, _b: torch.nn.functional.celu(x, alpha=a),
+    "selu": selu_p,
+    "softplus": lambda x, beta, thr: torch.nn.functional.softplus(x, beta=beta, threshold=thr),
 }
 
 

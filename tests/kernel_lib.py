@@ -770,3 +770,46 @@ def make_row_dot(ttl, gr=2, gc=4, grid=(2, 2)):
                     ttl.copy(ob, out[r:r + gr, 0]).wait()
 
     return row_dot
+
+
+def make_unary_map(ttl, name, params=(), g=2, grid=(2, 2)):
+    """y = ttl.math.<name>(x, *params) over (g, g)-tile blocks (the spec's
+    math functions, TTLangSpecification.md:700-750)."""
+
+    @ttl.kernel(grid=grid)
+    def unary_map(x, y):
+        gx, gy = ttl.grid_size(dims=2)
+        rows_per_core = x.shape[0] // TILE // gx // g
+        cols_per_core = x.shape[1] // TILE // gy // g
+        x_cb = ttl.make_circular_buffer_like(x, shape=(g, g), buffer_factor=2)
+        y_cb = ttl.make_circular_buffer_like(y, shape=(g, g), buffer_factor=2)
+        fn = getattr(ttl.math, name)
+
+        @ttl.compute()
+        def comp():
+            for _ in range(rows_per_core):
+                for _ in range(cols_per_core):
+                    with x_cb.wait() as xb, y_cb.reserve() as yb:
+                        yb.store(fn(xb, *params))
+
+        @ttl.datamovement()
+        def reader():
+            cx, cy = ttl.core(dims=2)
+            for i in range(rows_per_core):
+                r = (cx * rows_per_core + i) * g
+                for j in range(cols_per_core):
+                    col = (cy * cols_per_core + j) * g
+                    with x_cb.reserve() as xb:
+                        ttl.copy(x[r:r + g, col:col + g], xb).wait()
+
+        @ttl.datamovement()
+        def writer():
+            cx, cy = ttl.core(dims=2)
+            for i in range(rows_per_core):
+                r = (cx * rows_per_core + i) * g
+                for j in range(cols_per_core):
+                    col = (cy * cols_per_core + j) * g
+                    with y_cb.wait() as yb:
+                        ttl.copy(yb, y[r:r + g, col:col + g]).wait()
+
+    return unary_map

@@ -8,6 +8,7 @@ against the oracle's eager executor without a GPU.
 
 import torch
 
+from oracle import tile_ops as O
 from ttlhip import _lib as L
 from ttlhip.plan import EltwiseLaunch, MatmulLaunch, ReduceLaunch
 
@@ -22,6 +23,9 @@ _TORCH_UN = {
     L.OP["neg"]: torch.neg, L.OP["relu"]: torch.relu, L.OP["sigmoid"]: torch.sigmoid,
     L.OP["recip"]: torch.reciprocal,
 }
+for _name, _fn in O.UNARY.items():  # the spec's further functions
+    _TORCH_UN.setdefault(L.OP[_name], _fn)
+_PARAM_UN = {L.OP[k]: f for k, f in O.PARAM_UNARY.items()}
 
 
 def _operand(t: torch.Tensor, spec, y0, x0, h, w) -> torch.Tensor:
@@ -57,7 +61,12 @@ def _values(l, args):
                 stack.append(acc)
             acc = torch.full((h, w), s.imm)
         elif s.form == L.FORM_UNARY:
-            acc = acc ** s.imm if s.op == L.OP["powi"] else _TORCH_UN[s.op](acc)
+            if s.op == L.OP["powi"]:
+                acc = acc ** s.imm
+            elif s.op in _PARAM_UN:
+                acc = _PARAM_UN[s.op](acc, s.imm, s.imm2)
+            else:
+                acc = _TORCH_UN[s.op](acc)
         elif s.form == L.FORM_BIN:
             acc = _TORCH_BIN[s.op](acc, v)
         elif s.form == L.FORM_BIN_REV:

@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
     for s in declared_symbols():
         assert hasattr(lib, s), f"{s} declared in ttlhip.h but not exported"
         assert s in _lib.SIGNATURES, f"{s} has no ctypes signature"
-    assert lib.ttlh_version() == 1
+    assert lib.ttlh_version() == 2
 
 
 def test_validation_errors_need_no_gpu():

@@ -63,7 +63,7 @@ struct Ins {
   uint8_t kind, src, op, rnd;
   uint8_t arg;  // operand index (consumption order) for SRC_OPERAND steps
   uint8_t pad[3];
-  float imm;
+  float imm, imm2;
 };
 
 struct EltArgs {
@@ -262,8 +262,45 @@ __device__ __forceinline__ f32x8 binary(int op, f32x8 a, f32x8 b) {
   }
 }
 
+// The spec's further math functions (TTLH_OP_EXP2 ..), out of line: they are
+// rare, and inlining their libm expansions would grow every every-op
+// interpreter copy.
+__device__ __attribute__((noinline)) f32x8 unary_ext(int op, f32x8 a, float p, float q) {
+  f32x8 t;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float x = a[e];
+    float r;
+    switch (op) {
+      case TTLH_OP_EXP2: r = exp2f(x); break;
+      case TTLH_OP_EXPM1: r = expm1f(x); break;
+      case TTLH_OP_LOG1P: r = log1pf(x); break;
+      case TTLH_OP_SIN: r = sinf(x); break;
+      case TTLH_OP_COS: r = cosf(x); break;
+      case TTLH_OP_TAN: r = tanf(x); break;
+      case TTLH_OP_ASIN: r = asinf(x); break;
+      case TTLH_OP_ACOS: r = acosf(x); break;
+      case TTLH_OP_ATAN: r = atanf(x); break;
+      case TTLH_OP_ASINH: r = asinhf(x); break;
+      case TTLH_OP_ACOSH: r = acoshf(x); break;
+      case TTLH_OP_ATANH: r = atanhf(x); break;
+      // x / 2 (1 + erf(x / sqrt 2)) = x / 2 erfc(-x / sqrt 2): no cancellation for x << 0
+      case TTLH_OP_GELU: r = 0.5f * x * erfcf(-x * 0.70710678118654752f); break;
+      case TTLH_OP_SILU: r = x / (1.0f + expf(-x)); break;
+      case TTLH_OP_SOFTSIGN: r = x / (1.0f + fabsf(x)); break;
+      case TTLH_OP_HARDSIGMOID: r = fminf(fmaxf(x + 3.0f, 0.0f), 6.0f) / 6.0f; break;
+      case TTLH_OP_ELU: r = x > 0.0f ? x : p * expm1f(x); break;
+      case TTLH_OP_CELU: r = fmaxf(x, 0.0f) + fminf(p * expm1f(x / p), 0.0f); break;
+      case TTLH_OP_SELU: r = p * (fmaxf(x, 0.0f) + fminf(q * expm1f(x), 0.0f)); break;
+      default: r = p * x > q ? x : log1pf(expf(p * x)) / p; break;  // TTLH_OP_SOFTPLUS
+    }
+    t[e] = x != x ? x : r;  // NaN in, NaN out (fmaxf / fminf would drop it)
+  }
+  return t;
+}
+
 template <bool FULL>
-__device__ __forceinline__ f32x8 unary(int op, f32x8 a, float imm) {
+__device__ __forceinline__ f32x8 unary(int op, f32x8 a, float imm, float imm2 = 0.0f) {
   if constexpr (!FULL) {
     switch (op) {
       case TTLH_OP_EXP: return vexp(a);
@@ -284,7 +321,8 @@ __device__ __forceinline__ f32x8 unary(int op, f32x8 a, float imm) {
     case TTLH_OP_RELU: return map8(a, [](float v) { return v != v ? v : fmaxf(v, 0.0f); });
     case TTLH_OP_SIGMOID: return map8(a, [](float v) { return 1.0f / (1.0f + expf(-v)); });
     case TTLH_OP_RECIP: return 1.0f / a;
-    default: return map8(a, [imm](float v) { return powf(v, imm); });  // TTLH_OP_POWI
+    case TTLH_OP_POWI: return map8(a, [imm](float v) { return powf(v, imm); });
+    default: return unary_ext(op, a, imm, imm2);
   }
 }
 
@@ -343,7 +381,7 @@ __device__ __forceinline__ void run_step(const EltArgs& args, const Ins ins, f32
       }
       acc = v;
       break;
-    case K_UNARY: acc = unary<FULL>(ins.op, acc, ins.imm); break;
+    case K_UNARY: acc = unary<FULL>(ins.op, acc, ins.imm, ins.imm2); break;
     case K_BIN: acc = binary<FULL>(ins.op, acc, v); break;
     default: acc = binary<FULL>(ins.op, v, acc); break;  // K_BIN_REV
   }
@@ -1066,7 +1104,7 @@ __global__ __launch_bounds__(256) void reduce_all_finish_kernel(const RedArgs a)
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 bool is_binary(int op) { return op >= TTLH_OP_ADD && op <= TTLH_OP_MOD; }
-bool is_unary(int op) { return op >= TTLH_OP_EXP && op <= TTLH_OP_POWI; }
+bool is_unary(int op) { return op >= TTLH_OP_EXP && op <= TTLH_OP_SOFTPLUS; }
 // ops the common (fast) variants implement
 bool is_common(int op) {
   return op == TTLH_OP_ADD || op == TTLH_OP_SUB || op == TTLH_OP_MUL || op == TTLH_OP_EXP || op == TTLH_OP_NEG || op == TTLH_OP_ABS || op == TTLH_OP_RELU ||
@@ -1151,6 +1189,7 @@ int decode_program(const char* who, const ttlh_instr* prog, const ttlh_operand* 
     q.op = p.op;
     q.rnd = p.rnd;
     q.imm = p.imm;
+    q.imm2 = p.imm2;
     switch (f) {
       case TTLH_FORM_LOAD: q.kind = K_SET; q.src = SRC_OPERAND; break;
       case TTLH_FORM_PUSH: q.kind = K_PUSH; q.src = SRC_OPERAND; break;

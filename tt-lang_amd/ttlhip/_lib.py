@@ -37,9 +37,14 @@ OP = {
     "floordiv": 8, "mod": 9,
     "exp": 16, "log": 17, "sqrt": 18, "rsqrt": 19, "tanh": 20, "abs": 21,
     "neg": 22, "relu": 23, "sigmoid": 24, "recip": 25, "powi": 26,
+    "exp2": 27, "expm1": 28, "logp1": 29, "sin": 30, "cos": 31, "tan": 32, "asin": 33,
+    "acos": 34, "atan": 35, "asinh": 36, "acosh": 37, "atanh": 38, "gelu": 39, "silu": 40,
+    "softsign": 41, "hardsigmoid": 42, "elu": 43, "celu": 44, "selu": 45, "softplus": 46,
 }
 BINARY_OPS = {k for k, v in OP.items() if 1 <= v <= 9}
-UNARY_OPS = {k for k, v in OP.items() if 16 <= v <= 26}
+UNARY_OPS = {k for k, v in OP.items() if 16 <= v <= 46}
+# unary ops with parameters (imm, imm2)
+PARAM_UNARY_OPS = {"powi", "elu", "celu", "selu", "softplus"}
 
 # forms (enum ttlh_form)
 FORM_LOAD, FORM_PUSH, FORM_CONST, FORM_PUSH_CONST, FORM_UNARY = 0, 1, 2, 3, 4
@@ -49,7 +54,7 @@ FORM_BIN, FORM_BIN_REV, FORM_BIN_IMM, FORM_BIN_IMM_REV, FORM_BIN_POP = 5, 6, 7, 
 class Instr(C.Structure):
     _fields_ = [
         ("op", C.c_uint8), ("form", C.c_uint8), ("rnd", C.c_uint8), ("pad", C.c_uint8),
-        ("imm", C.c_float),
+        ("imm", C.c_float), ("imm2", C.c_float),
     ]
 
 

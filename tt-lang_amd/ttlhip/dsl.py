@@ -338,6 +338,8 @@ def _remap(tree, axis: int, new_len: int):
         return tree
     if tag == "powi":
         return ("powi", _remap(tree[1], axis, new_len), tree[2])
+    if tag == "upar":
+        return ("upar", _remap(tree[1], axis, new_len)) + tuple(tree[2:])
     return (tag,) + tuple(_remap(t, axis, new_len) for t in tree[1:])
 
 
@@ -377,6 +379,14 @@ def _unary(op: str, a, imm: Optional[float] = None) -> BExpr:
     aa = _as_bexpr(a)
     _check_not_reduced(aa)
     return BExpr(aa.shape, (op, aa.tree), aa.dtype)
+
+
+def _unary_param(op: str, a, p0: float, p1: float = 0.0) -> BExpr:
+    """A unary op with numeric parameters (the spec types them PositiveInt;
+    their numeric value is used)."""
+    aa = _as_bexpr(a)
+    _check_not_reduced(aa)
+    return BExpr(aa.shape, ("upar", aa.tree, op, float(p0), float(p1)), aa.dtype)
 
 
 def _reduce(kind: str, x, scaler, dims) -> BExpr:
@@ -775,6 +785,73 @@ class _Math:
     def min(a, b): return _binary("min", a, b)
     maximum = max
     minimum = min
+
+    # the spec's further math functions (TTLangSpecification.md:700-750;
+    # the reference compiler's op table and simulator implement none of
+    # them).  Each follows the torch function the spec links applied to a
+    # bfloat16 tile: native ops compute in fp32 and round once, as those
+    # torch kernels do; the compositions round where torch does (exact
+    # partial results, or torch's own composition for softsign).
+    @staticmethod
+    def exp2(x): return _unary("exp2", x)
+    @staticmethod
+    def expm1(x): return _unary("expm1", x)
+    @staticmethod
+    def logp1(x): return _unary("logp1", x)
+    @staticmethod
+    def square(x): return _binary("mul", x, x)
+    @staticmethod
+    def rsub(a, b): return _binary("sub", b, a)
+    @staticmethod
+    def sin(x): return _unary("sin", x)
+    @staticmethod
+    def cos(x): return _unary("cos", x)
+    @staticmethod
+    def tan(x): return _unary("tan", x)
+    @staticmethod
+    def asin(x): return _unary("asin", x)
+    @staticmethod
+    def acos(x): return _unary("acos", x)
+    @staticmethod
+    def atan(x): return _unary("atan", x)
+    @staticmethod
+    def asinh(x): return _unary("asinh", x)
+    @staticmethod
+    def acosh(x): return _unary("acosh", x)
+    @staticmethod
+    def atanh(x): return _unary("atanh", x)
+    @staticmethod
+    def gelu(x): return _unary("gelu", x)
+    @staticmethod
+    def silu(x): return _unary("silu", x)
+    @staticmethod
+    def softsign(x):
+        # torch's softsign is the composition x / (|x| + 1), rounded per op
+        return _binary("div", x, _binary("add", _unary("abs", x), 1.0))
+    @staticmethod
+    def hardsigmoid(x): return _unary("hardsigmoid", x)
+    @staticmethod
+    def relu_max(x, upper_limit): return _unary("relu", _binary("min", x, upper_limit))
+    @staticmethod
+    def relu_min(x, lower_limit): return _unary("relu", _binary("max", x, lower_limit))
+    @staticmethod
+    def hardtanh(x, min, max):  # noqa: A002 (the spec's parameter names)
+        return _binary("min", _binary("max", x, min), max)
+    @staticmethod
+    def leaky_relu(x, slope):
+        # relu(x) + slope * min(x, 0): one of the two terms is zero
+        return _binary("add", _unary("relu", x), _binary("mul", _binary("min", x, 0.0), slope))
+    @staticmethod
+    def prelu(x, alpha): return _Math.leaky_relu(x, alpha)
+    @staticmethod
+    def elu(x, slope): return _unary_param("elu", x, slope)
+    @staticmethod
+    def celu(x, alpha, alpha_recip=None): return _unary_param("celu", x, alpha)
+    @staticmethod
+    def selu(x, scale, alpha): return _unary_param("selu", x, scale, alpha)
+    @staticmethod
+    def softplus(x, beta, beta_reciprocal=None, threshold=20.0):
+        return _unary_param("softplus", x, beta, threshold)
 
     @staticmethod
     def reduce_sum(expr, scaler, dims=None) -> BExpr:

@@ -68,9 +68,10 @@ class Unary(Expr):
     x: Expr
     dtype: torch.dtype
     imm: float = 0.0
+    imm2: float = 0.0
 
     def key(self) -> Tuple:
-        return ("un", self.op, self.imm, str(self.dtype), self.x.key())
+        return ("un", self.op, self.imm, self.imm2, str(self.dtype), self.x.key())
 
     def _collect(self, out: List["Leaf"]) -> None:
         self.x._collect(out)
@@ -106,6 +107,7 @@ class Step:
     rnd: int = L.TTLH_F32
     imm: float = 0.0
     leaf: Optional[Leaf] = None  # operand owned by this step
+    imm2: float = 0.0
 
 
 @dataclass
@@ -150,7 +152,7 @@ def compile_expr(e: Expr) -> StackProgram:
             if n.op not in L.UNARY_OPS:
                 raise NotImplementedError(f"unsupported unary tile op {n.op!r}")
             gen(n.x)
-            emit(Step(L.FORM_UNARY, op=L.OP[n.op], imm=n.imm, rnd=_rnd(n.dtype)), 0)
+            emit(Step(L.FORM_UNARY, op=L.OP[n.op], imm=n.imm, imm2=n.imm2, rnd=_rnd(n.dtype)), 0)
         elif isinstance(n, Binary):
             if n.op not in L.BINARY_OPS:
                 raise NotImplementedError(f"unsupported binary tile op {n.op!r}")
@@ -199,7 +201,7 @@ def structure_key(e: Expr, leaf_ids: Dict[int, int]) -> Tuple:
     if isinstance(e, Const):
         return ("C", float(e.value), str(e.dtype))
     if isinstance(e, Unary):
-        return ("U", e.op, e.imm, str(e.dtype), structure_key(e.x, leaf_ids))
+        return ("U", e.op, e.imm, e.imm2, str(e.dtype), structure_key(e.x, leaf_ids))
     if isinstance(e, Binary):
         return ("B", e.op, str(e.dtype), structure_key(e.a, leaf_ids), structure_key(e.b, leaf_ids))
     raise TypeError(e)

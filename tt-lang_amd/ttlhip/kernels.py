@@ -90,7 +90,7 @@ def eltwise(prog: StackProgram, operands: Sequence[Optional[OperandMap]], out: t
     instrs = (L.Instr * n)()
     ops = (L.Operand * n)()
     for k, (s, m) in enumerate(zip(prog.steps, operands)):
-        instrs[k] = L.Instr(s.op, s.form, s.rnd, 0, s.imm)
+        instrs[k] = L.Instr(s.op, s.form, s.rnd, 0, s.imm, s.imm2)
         if s.form in (L.FORM_LOAD, L.FORM_PUSH, L.FORM_BIN, L.FORM_BIN_REV):
             if m is None:
                 raise ValueError(f"step {k} needs an operand")
@@ -135,7 +135,7 @@ def reduce(prog: StackProgram, operands: Sequence[Optional[OperandMap]], kind: s
     instrs = (L.Instr * n)()
     ops = (L.Operand * n)()
     for k, (s, m) in enumerate(zip(prog.steps, operands)):
-        instrs[k] = L.Instr(s.op, s.form, s.rnd, 0, s.imm)
+        instrs[k] = L.Instr(s.op, s.form, s.rnd, 0, s.imm, s.imm2)
         if s.form in (L.FORM_LOAD, L.FORM_PUSH, L.FORM_BIN, L.FORM_BIN_REV):
             if m is None:
                 raise ValueError(f"step {k} needs an operand")

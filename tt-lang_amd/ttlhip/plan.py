@@ -221,7 +221,7 @@ def _tree_leaves(tree, out: List):
         out.append(tree)
     elif tag == "const":
         pass
-    elif tag == "powi":
+    elif tag in ("powi", "upar"):
         _tree_leaves(tree[1], out)
     elif tag == "reduce":
         _tree_leaves(tree[3], out)
@@ -239,6 +239,8 @@ def _tree_key(tree, leaf_ids: Dict[int, int]):
         return ("const", tree[1])
     if tag == "powi":
         return ("powi", _tree_key(tree[1], leaf_ids), tree[2])
+    if tag == "upar":
+        return ("upar", _tree_key(tree[1], leaf_ids)) + tuple(tree[2:])
     if tag == "reduce":
         _, kind, dims, inner, ishape, scaler = tree
         sk = ("const", scaler[1]) if scaler[0] == "const" else ("scaler", str(scaler[1].cb.dtype))
@@ -491,7 +493,9 @@ def _axis_map(out_t: np.ndarray, in_t: np.ndarray, dim: int) -> Tuple[int, int]:
 
 
 _BIN = {"add", "sub", "mul", "div", "max", "min", "pow", "floordiv", "mod"}
-_UN = {"exp", "log", "sqrt", "rsqrt", "tanh", "abs", "neg", "relu", "sigmoid", "recip"}
+_UN = {"exp", "log", "sqrt", "rsqrt", "tanh", "abs", "neg", "relu", "sigmoid", "recip",
+       "exp2", "expm1", "logp1", "sin", "cos", "tan", "asin", "acos", "atan", "asinh", "acosh",
+       "atanh", "gelu", "silu", "softsign", "hardsigmoid"}
 
 
 def _to_expr(tree, leaf_nodes: Dict[int, X.Leaf]) -> X.Expr:
@@ -503,6 +507,9 @@ def _to_expr(tree, leaf_nodes: Dict[int, X.Leaf]) -> X.Expr:
     if tag == "powi":
         x = _to_expr(tree[1], leaf_nodes)
         return X.Unary("powi", x, x.dtype, imm=float(tree[2]))
+    if tag == "upar":
+        x = _to_expr(tree[1], leaf_nodes)
+        return X.Unary(tree[2], x, x.dtype, imm=float(tree[3]), imm2=float(tree[4]))
     if tag in _UN:
         x = _to_expr(tree[1], leaf_nodes)
         return X.Unary(tag, x, x.dtype)
@@ -528,6 +535,8 @@ def _has(tree, tag) -> bool:
         return False
     if tree[0] == "reduce":
         return _has(tree[3], tag)
+    if tree[0] in ("powi", "upar"):
+        return _has(tree[1], tag)
     return any(_has(t, tag) for t in tree[1:] if isinstance(t, tuple))
 
 
