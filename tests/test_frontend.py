@@ -457,6 +457,37 @@ def test_reference_tutorials(cpu_exec, name, n, bcast):
 
 
 @needs_ref
+def test_reference_deadlock_report(cpu_exec, tmp_path):
+    # the reference's own deadlock check (test/sim/test_examples.py:194-300):
+    # tutorial/multicore_grid_auto.py with the compute thread's y_cb.reserve()
+    # turned into y_cb.wait() must report every blocked thread, its
+    # operation, the CB and the source line of the blocking call
+    import re
+    src = open(os.path.join(REF, "tutorial/multicore_grid_auto.py")).read()
+    bad = src.replace("y_cb.reserve() as y_blk,", "y_cb.wait() as y_blk,")
+    assert bad != src
+    path = tmp_path / "multicore_grid_auto_deadlock.py"
+    path.write_text(bad)
+    g = {"__name__": "example", "device": None}
+    exec(compile(bad.split("torch.manual_seed(42)")[0], str(path), "exec"), g)
+    n = 2048  # the script's own size: the reader fills a_cb before compute blocks
+    with pytest.raises(RuntimeError) as ei:
+        g["demo_kernel"](ttnn.from_torch(_bf((n, n), 1)), ttnn.from_torch(_bf((n, n), 2)),
+                         ttnn.from_torch(_bf((n, n), 3)))
+    out = str(ei.value)
+    assert "Deadlock detected: all generators blocked" in out
+    assert "CircularBuffer(y_cb)" in out
+    assert "blocked on wait()" in out and "blocked on reserve()" in out
+    for t in ("core0-compute:", "core0-dm0:", "core0-dm1:"):
+        assert t in out
+    lines = bad.splitlines()
+    for thread, line in re.findall(r"core0-(\w+).*? at .*?:(\d+)", out):
+        text = lines[int(line) - 1]
+        assert (".wait()" if thread in ("compute", "dm1") else ".reserve()") in text, (thread, text)
+    assert "y_cb.wait()" in lines[int(re.search(r"core0-compute.*?:(\d+)", out).group(1)) - 1]
+
+
+@needs_ref
 @pytest.mark.parametrize("bshape,cshape", [((1024, 1024), (1024, 1024)), ((1024, 1), (1, 1024)),
                                            ((1, 1024), (1, 1)), ((1, 1), (1024, 1))])
 def test_reference_general_broadcast(cpu_exec, bshape, cshape):

@@ -19,6 +19,7 @@ from __future__ import annotations
 
 import inspect
 import itertools
+import re
 import os
 import sys
 import types
@@ -203,6 +204,7 @@ class CircularBuffer:
         self.buffer_factor = int(buffer_factor)
         self.dtype = element.dtype
         self.capacity_tiles = self.shape[0] * self.shape[1] * self.buffer_factor
+        self.name = _assigned_name(_user_location(), f"cb{self.id}")
         if _kstate is not None:
             _kstate.cbs.append(self)
             if len(_kstate.cbs) > MAX_CBS:
@@ -223,7 +225,8 @@ class CircularBuffer:
             raise RuntimeError("Cannot call reserve() again before push(): CircularBuffer already "
                                "has a pending reserved block. You must call push() before calling "
                                "reserve() again.")
-        ev = ctx.add(Event("reserve", self, ctx.cur, {"thread": ctx.thread}))
+        ev = ctx.add(Event("reserve", self, ctx.cur, {"thread": ctx.thread,
+                                                       "loc": _user_location()}))
         blk = Block(self, "reserve", ev)
         ctx.pending_reserve[self.id] = blk
         return blk
@@ -234,7 +237,8 @@ class CircularBuffer:
             raise RuntimeError("Cannot call wait() again before pop(): CircularBuffer already "
                                "has a pending waited block. You must call pop() before calling "
                                "wait() again.")
-        ev = ctx.add(Event("wait", self, ctx.cur, {"thread": ctx.thread}))
+        ev = ctx.add(Event("wait", self, ctx.cur, {"thread": ctx.thread,
+                                                    "loc": _user_location()}))
         blk = Block(self, "wait", ev)
         ctx.pending_wait[self.id] = blk
         return blk
@@ -529,6 +533,15 @@ class Block:
 
 
 _PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+
+
+def _assigned_name(loc: Tuple[str, int], default: str) -> str:
+    """The variable a `name = ...` source line assigns (the name a deadlock
+    report shows, as the simulator does: python/sim/program.py:184)."""
+    import linecache
+
+    m = re.match(r"\s*([A-Za-z_]\w*)\s*=[^=]", linecache.getline(loc[0], loc[1]))
+    return m.group(1) if m else default
 
 
 def _user_location() -> Tuple[str, int]:

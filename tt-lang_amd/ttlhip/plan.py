@@ -25,7 +25,7 @@ Anything else raises NotImplementedError naming the unsupported pattern.
 from __future__ import annotations
 
 from dataclasses import dataclass, field
-from typing import Any, Dict, List, Optional, Tuple
+from typing import Any, Dict, List, Optional, Sequence, Tuple
 
 import numpy as np
 import torch
@@ -281,6 +281,92 @@ def _pipe_sends(core_traces, per_core) -> Dict[int, List[Tuple[Any, np.ndarray, 
     return sends
 
 
+_SIM_OP_LIMIT = 2_000_000  # operations replayed per core by the deadlock report
+
+
+def _raise_deadlock_or(ct: Dict[str, Any], err: Exception) -> None:
+    """A CB inconsistency: raise the simulator-style deadlock report when the
+    threads of the core really block, else `err`."""
+    rep = _deadlock_report(ct)
+    if rep is not None:
+        raise RuntimeError(rep)
+    raise err
+
+
+def _flat_ops(node):
+    """The CB operations of a traced thread in program order, loops unrolled."""
+    for ch in node.children:
+        if isinstance(ch, T.Event):
+            if ch.kind in ("reserve", "push", "wait", "pop"):
+                yield ch
+        else:
+            for _ in range(ch.n):
+                yield from _flat_ops(ch)
+
+
+def _deadlock_report(ct: Dict[str, Any], failed: Sequence[int] = ()) -> Optional[str]:
+    """Replays one core's three threads cooperatively against its CBs (the
+    simulator's scheduler, python/sim/program.py:363-647: a reserve needs a
+    free block, a wait a visible one) and, if they block, returns the
+    simulator's report: "Deadlock detected: all generators blocked" with one
+    line per blocked thread (operation, CB variable, source line).  None when
+    the threads run to completion (or past the replay limit).  `failed` names
+    the threads whose trace stopped at an error: one that reaches the end of
+    its partial trace raises that error before any deadlock, so the replay
+    returns None as soon as one does."""
+    names, it, nxt = [], [], []
+    ndm = 0
+    for tmpl, root in ct["threads"]:
+        if tmpl.kind == "compute":
+            names.append(f"core{ct['core']}-compute")
+        else:
+            names.append(f"core{ct['core']}-dm{ndm}")
+            ndm += 1
+        g = _flat_ops(root)
+        it.append(g)
+        nxt.append(next(g, None))
+        if nxt[-1] is None and len(it) - 1 in failed:
+            return None
+    visible: Dict[int, int] = {}
+    reserved: Dict[int, int] = {}
+    steps = 0
+    while any(e is not None for e in nxt):
+        progress = False
+        for k in range(len(it)):
+            while nxt[k] is not None:
+                ev = nxt[k]
+                cid, bf = ev.cb.id, ev.cb.buffer_factor
+                if ev.kind == "reserve":
+                    if visible.get(cid, 0) + reserved.get(cid, 0) >= bf:
+                        break
+                    reserved[cid] = reserved.get(cid, 0) + 1
+                elif ev.kind == "push":
+                    reserved[cid] = reserved.get(cid, 0) - 1
+                    visible[cid] = visible.get(cid, 0) + 1
+                elif ev.kind == "wait":
+                    if visible.get(cid, 0) < 1:
+                        break
+                else:  # pop
+                    visible[cid] = visible.get(cid, 0) - 1
+                nxt[k] = next(it[k], None)
+                if nxt[k] is None and k in failed:
+                    return None
+                progress = True
+                steps += 1
+                if steps > _SIM_OP_LIMIT:
+                    return None
+        if not progress:
+            lines = []
+            for k, ev in enumerate(nxt):
+                if ev is None:
+                    continue
+                f, ln = ev.data.get("loc", ("?", 0))
+                lines.append(f"  {names[k]}: blocked on {ev.kind}() on "
+                             f"CircularBuffer({ev.cb.name}) at {f}:{ln}")
+            return "Deadlock detected: all generators blocked\n" + "\n".join(lines)
+    return None
+
+
 def resolve(core_traces: List[Dict[str, Any]]) -> List[_Group]:
     """core_traces[c] = {"threads": [(template, root_node), ...]} for core c."""
     groups: Dict[Tuple, _Group] = {}
@@ -330,19 +416,22 @@ def resolve(core_traces: List[Dict[str, Any]]) -> List[_Group]:
             for ev in events[id(tmpl)]:
                 if ev.kind == "reserve":
                     if producers.setdefault(ev.cb.id, tmpl) is not tmpl:
-                        raise PlanError(f"CB {ev.cb.id} is reserved by two threads")
+                        _raise_deadlock_or(ct, PlanError(
+                            f"CB {ev.cb.name} is reserved by two threads"))
                     cbs[ev.cb.id] = ev.cb
                 elif ev.kind == "wait":
                     if consumers.setdefault(ev.cb.id, tmpl) is not tmpl:
-                        raise PlanError(f"CB {ev.cb.id} is waited on by two threads")
+                        _raise_deadlock_or(ct, PlanError(
+                            f"CB {ev.cb.name} is waited on by two threads"))
                     cbs[ev.cb.id] = ev.cb
         count = {}
         for cid, cb in cbs.items():
             np_ = totals[id(producers[cid])].get((cid, "reserve"), 0) if cid in producers else 0
             nc_ = totals[id(consumers[cid])].get((cid, "wait"), 0) if cid in consumers else 0
             if np_ != nc_:
-                raise RuntimeError(f"Deadlock: CB {cid} has {np_} blocks pushed but {nc_} blocks "
-                                   f"waited on core {ct['core']} (producer and consumer disagree)")
+                _raise_deadlock_or(ct, RuntimeError(
+                    f"Deadlock: CB {cb.name} has {np_} blocks pushed but {nc_} blocks waited on "
+                    f"core {ct['core']} (producer and consumer disagree)"))
             count[cid] = np_
         # copy tables
         fill: Dict[int, _CopyTable] = {}

@@ -125,9 +125,26 @@ class KernelRunner:
         ncores = int(np.prod(self.grid))
         core_traces = []
         for c in range(ncores):
-            traced = []
+            traced, errors, failed = [], [], []
             for t in ordered:
-                traced.append((t, self._trace_thread(t, c)))
+                try:
+                    traced.append((t, self._trace_thread(t, c)))
+                except Exception as e:  # noqa: BLE001 - re-raised below
+                    root = getattr(e, "_ttlh_partial_root", None)
+                    if root is None:
+                        raise
+                    failed.append(len(traced))
+                    traced.append((t, root))
+                    errors.append(e)
+            if errors:
+                # the simulator raises a thread's error only if that thread
+                # gets there: when every thread blocks first (e.g. a store into
+                # a waited block behind a wait nobody satisfies) the deadlock
+                # is what it reports
+                rep = P._deadlock_report({"core": c, "threads": traced}, failed)
+                if rep is not None:
+                    raise RuntimeError(rep) from None
+                raise errors[0]
             core_traces.append({"core": c, "threads": traced})
         groups = P.resolve(core_traces)
 
@@ -182,11 +199,16 @@ class KernelRunner:
                 if scalar:
                     raise
                 continue
+            except Exception as e:
+                e._ttlh_partial_root = ctx.root  # the operations traced up to the error
+                raise
             finally:
                 T._ctx = prev
             if ctx.pending_reserve or ctx.pending_wait:
-                raise RuntimeError(f"thread {t.__name__} on core {core} ended with a reserved or "
+                err = RuntimeError(f"thread {t.__name__} on core {core} ended with a reserved or "
                                    "waited block that was never pushed / popped")
+                err._ttlh_partial_root = ctx.root
+                raise err
             return ctx.root
         raise AssertionError("unreachable")
 
