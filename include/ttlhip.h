@@ -148,10 +148,14 @@ typedef struct ttlh_instr {
 /* An input operand, addressed from the output element (y, x):
  *   iy = (y & row_mask) + row_off ;  ix = (x & col_mask) + col_off
  *   element = ptr[iy * row_stride + ix * col_stride]
- * row_mask/col_mask = -1 (identity) or 31 (a fixed tile re-used across the
- * tile grid, simulator block broadcasting, python/sim/block.py:886-920);
- * a stride of 0 broadcasts a degenerate (size-1) tensor dimension across the
- * tile (python/sim/copyhandlers.py:103-131).  The caller guarantees every
+ * row_mask/col_mask = -1 (identity), 31 (a fixed tile re-used across the
+ * tile grid, simulator block broadcasting, python/sim/block.py:886-920),
+ * ~31 (row / column 0 of every tile: the compiler's in-tile broadcast
+ * tile_bcast Row / Col / Scalar, TTLElementwiseOps.def:82,
+ * python/ttl/operators.py:333-360) or 0 (one fixed row / column: both at
+ * once); a stride of 0 broadcasts a degenerate (size-1) tensor dimension
+ * across the tile (python/sim/copyhandlers.py:103-131).  Offsets are
+ * multiples of 32 for the masks other than -1.  The caller guarantees every
  * addressed element lies inside the allocation.                          */
 typedef struct ttlh_operand {
   const void* ptr;

@@ -140,7 +140,10 @@ class _Tiles:
         self.tiles = tiles
         self.shape = shape
 
-    def _bin(self, other, op):
+    def _bin(self, other, op, rev=False):
+        if isinstance(other, (int, float)) and not isinstance(other, bool):
+            # a Python number: one op per tile in the tile dtype (block.py:963-1010)
+            return self.map((lambda t: op(other, t)) if rev else (lambda t: op(t, other)))
         other = _tiles_of(other)
         if self.shape == other.shape:
             return _Tiles([op(a, b) for a, b in zip(self.tiles, other.tiles)], self.shape)
@@ -156,8 +159,11 @@ class _Tiles:
         return _Tiles([flat[i] for i in range(flat.shape[0])], shape)
 
     def __add__(self, o): return self._bin(o, operator.add)
+    def __radd__(self, o): return self._bin(o, operator.add, True)
     def __sub__(self, o): return self._bin(o, operator.sub)
+    def __rsub__(self, o): return self._bin(o, operator.sub, True)
     def __mul__(self, o): return self._bin(o, operator.mul)
+    def __rmul__(self, o): return self._bin(o, operator.mul, True)
     def __truediv__(self, o): return self._bin(o, operator.truediv)
     def __floordiv__(self, o): return self._bin(o, operator.floordiv)
     def __mod__(self, o): return self._bin(o, operator.mod)
@@ -333,12 +339,36 @@ def make_ttl():
 
     class _Math:
         @staticmethod
-        def broadcast(block, _u=None, dims=None):
+        def broadcast(block, out=None, dims=None):
+            """The compiler's tile broadcast (python/ttl/operators.py:333-360;
+            unary_bcast Row / Col / Scalar, TTLElementwiseOps.def:82): every
+            tile replaced by its row 0 (dims [0]), column 0 ([1]) or element
+            [0, 0] ([0, 1]) repeated over the tile; a size-1 block dimension
+            along a broadcast dim repeated to `out`'s block size.  Without
+            `out`, broadcast block dims must be 1 (python/sim/math.py:69-83)."""
+            if dims is None:
+                raise ValueError("dims parameter is required for broadcast()")
             t = _tiles_of(block)
+            target = tuple(out.shape) if out is not None else None
             for d in dims:
-                if t.shape[d] != 1:
+                if t.shape[d] != 1 and (target is None or target[d] != t.shape[d]):
                     raise ValueError("broadcast dimension must have size 1")
-            return _Tiles(list(t.tiles), t.shape)
+
+            def rep(x):
+                if 0 in dims:
+                    x = x[:1, :].expand(x.shape[0], x.shape[1])
+                if 1 in dims:
+                    x = x[:, :1].expand(x.shape[0], x.shape[1])
+                return x.clone()
+            tiles = [rep(x) for x in t.tiles]
+            R, C = t.shape
+            if target is not None:
+                nr = target[0] if (0 in dims and R == 1) else R
+                nc = target[1] if (1 in dims and C == 1) else C
+                tiles = [tiles[(i if R > 1 else 0) * C + (j if C > 1 else 0)]
+                         for i in range(nr) for j in range(nc)]
+                R, C = nr, nc
+            return _Tiles(tiles, (R, C))
 
     for name, fn in (("exp", torch.exp), ("log", torch.log), ("sqrt", torch.sqrt),
                      ("rsqrt", torch.rsqrt), ("tanh", torch.tanh), ("abs", torch.abs),

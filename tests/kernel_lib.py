@@ -813,3 +813,140 @@ def make_unary_map(ttl, name, params=(), g=2, grid=(2, 2)):
                         ttl.copy(yb, y[r:r + g, col:col + g]).wait()
 
     return unary_map
+
+
+def make_tile_bcast(ttl, dims, ib=(2, 2), ob=(2, 2), grid=(2, 2), expr="plain"):
+    """The compiler's in-tile broadcast ttl.math.broadcast(in, out, dims) over a
+    grid of blocks: every core owns a run of block rows; block (r, c) reads
+    input tiles [r ib0, c ib1] and writes output tiles [r ob0, c ob1].
+    expr: "plain" stores the broadcast, "fma" stores a * 2 + broadcast(x),
+    "exp" stores exp(broadcast(x)) * a (a: an output-shaped operand)."""
+    @ttl.kernel(grid=grid)
+    def tile_bcast(x, a, out):
+        rows = out.shape[0] // TILE // ob[0]
+        cols = out.shape[1] // TILE // ob[1]
+        ncores = grid[0] * grid[1]
+        per = -(-rows // ncores)
+        x_cb = ttl.make_circular_buffer_like(x, shape=ib, buffer_factor=2)
+        a_cb = ttl.make_circular_buffer_like(a, shape=ob, buffer_factor=2)
+        o_cb = ttl.make_circular_buffer_like(out, shape=ob, buffer_factor=2)
+
+        @ttl.compute()
+        def comp():
+            c = ttl.core(dims=1)
+            for r in range(c * per, min(rows, (c + 1) * per)):
+                for _ in range(cols):
+                    with x_cb.wait() as xb, a_cb.wait() as ab, o_cb.reserve() as o:
+                        b = ttl.math.broadcast(xb, o, dims=dims)
+                        if expr == "plain":
+                            o.store(b)
+                        elif expr == "fma":
+                            o.store(ab * 2.0 + b)
+                        else:
+                            o.store(ttl.math.exp(b) * ab)
+
+        @ttl.datamovement()
+        def rd():
+            c = ttl.core(dims=1)
+            for r in range(c * per, min(rows, (c + 1) * per)):
+                for k in range(cols):
+                    with x_cb.reserve() as xb, a_cb.reserve() as ab:
+                        tx = ttl.copy(x[r * ib[0]:(r + 1) * ib[0], k * ib[1]:(k + 1) * ib[1]], xb)
+                        ta = ttl.copy(a[r * ob[0]:(r + 1) * ob[0], k * ob[1]:(k + 1) * ob[1]], ab)
+                        tx.wait()
+                        ta.wait()
+
+        @ttl.datamovement()
+        def wr():
+            c = ttl.core(dims=1)
+            for r in range(c * per, min(rows, (c + 1) * per)):
+                for k in range(cols):
+                    with o_cb.wait() as o:
+                        ttl.copy(o, out[r * ob[0]:(r + 1) * ob[0], k * ob[1]:(k + 1) * ob[1]]).wait()
+
+    return tile_bcast
+
+
+def make_two_stage(ttl, g=2, grid=(2, 2)):
+    """An intermediate CB on every core: stage 1 stores relu(x) * 0.5 into
+    t_cb, stage 2 waits on it and stores exp(t) + y (two launches through a
+    scratch tensor)."""
+    @ttl.kernel(grid=grid)
+    def two_stage(x, y, out):
+        rows = out.shape[0] // TILE // g
+        cols = out.shape[1] // TILE // g
+        ncores = grid[0] * grid[1]
+        per = -(-rows // ncores)
+        x_cb = ttl.make_circular_buffer_like(x, shape=(g, g), buffer_factor=2)
+        y_cb = ttl.make_circular_buffer_like(y, shape=(g, g), buffer_factor=2)
+        t_cb = ttl.make_circular_buffer_like(x, shape=(g, g), buffer_factor=2)
+        o_cb = ttl.make_circular_buffer_like(out, shape=(g, g), buffer_factor=2)
+
+        @ttl.compute()
+        def comp():
+            c = ttl.core(dims=1)
+            for r in range(c * per, min(rows, (c + 1) * per)):
+                for _ in range(cols):
+                    with x_cb.wait() as xb, t_cb.reserve() as tb:
+                        tb.store(ttl.math.relu(xb) * 0.5)
+                    with t_cb.wait() as tb, y_cb.wait() as yb, o_cb.reserve() as o:
+                        o.store(ttl.math.exp(tb) + yb)
+
+        @ttl.datamovement()
+        def rd():
+            c = ttl.core(dims=1)
+            for r in range(c * per, min(rows, (c + 1) * per)):
+                for k in range(cols):
+                    with x_cb.reserve() as xb, y_cb.reserve() as yb:
+                        tx = ttl.copy(x[r * g:(r + 1) * g, k * g:(k + 1) * g], xb)
+                        ty = ttl.copy(y[r * g:(r + 1) * g, k * g:(k + 1) * g], yb)
+                        tx.wait()
+                        ty.wait()
+
+        @ttl.datamovement()
+        def wr():
+            c = ttl.core(dims=1)
+            for r in range(c * per, min(rows, (c + 1) * per)):
+                for k in range(cols):
+                    with o_cb.wait() as o:
+                        ttl.copy(o, out[r * g:(r + 1) * g, k * g:(k + 1) * g]).wait()
+
+    return two_stage
+
+
+def make_held_tile(ttl, n=4, grid=(2, 2)):
+    """Core (y, x) holds tile c[y, x] in scope while it adds it to the n x n
+    tiles of a it owns: the operand tile is the output tile divided by n, so
+    the store site is split into one launch per held tile."""
+    @ttl.kernel(grid=grid)
+    def held_tile(a, c, out):
+        a_cb = ttl.make_circular_buffer_like(a, shape=(1, 1), buffer_factor=2)
+        c_cb = ttl.make_circular_buffer_like(c, shape=(1, 1), buffer_factor=2)
+        o_cb = ttl.make_circular_buffer_like(out, shape=(1, 1), buffer_factor=2)
+
+        @ttl.compute()
+        def comp():
+            with c_cb.wait() as cv:
+                for _ in range(n * n):
+                    with a_cb.wait() as av, o_cb.reserve() as o:
+                        o.store(av * 1.5 + cv)
+
+        @ttl.datamovement()
+        def rd():
+            x, y = ttl.core(dims=2)
+            with c_cb.reserve() as cb:
+                ttl.copy(c[y, x], cb).wait()
+            for i in range(n):
+                for j in range(n):
+                    with a_cb.reserve() as ab:
+                        ttl.copy(a[y * n + i, x * n + j], ab).wait()
+
+        @ttl.datamovement()
+        def wr():
+            x, y = ttl.core(dims=2)
+            for i in range(n):
+                for j in range(n):
+                    with o_cb.wait() as o:
+                        ttl.copy(o, out[y * n + i, x * n + j]).wait()
+
+    return held_tile

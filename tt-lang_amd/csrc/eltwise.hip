@@ -48,11 +48,23 @@ typedef const __attribute__((address_space(1))) u32x4 gu32x4;
 struct EltOperand {
   const void* ptr;
   int64_t rs, cs;          // row / col stride (elements)
-  int64_t rmask, cmask;    // coordinate masks (-1 or 31)
+  int64_t rmask, cmask;    // coordinate masks (-1, 31, 0 or ~31)
   int64_t roff, coff;      // coordinate offsets
   int32_t dtype;
   int32_t vec;             // 1: 16-byte vector loads are legal for this operand
 };
+
+// the operand coordinate masks: identity, a fixed tile re-used over the
+// grid (31), one fixed row / column (0), row / column 0 of every tile (~31)
+bool valid_mask(int64_t m) { return m == -1 || m == 31 || m == 0 || m == ~int64_t(31); }
+
+// largest masked coordinate (before the offset) over [0, hi]
+int64_t mask_max(int64_t m, int64_t hi) {
+  if (m == -1) return hi;
+  if (m == 31) return 31;
+  if (m == 0) return 0;
+  return hi & ~int64_t(31);
+}
 
 // Internal step encoding, decoded on the host from the ABI forms.
 //   src:  where the step's input value comes from
@@ -731,7 +743,7 @@ bool try_stream(const ChainArgs& c, int n, hipStream_t s, int* status) {
     if (reads) {
       const EltOperand& o = c.ops[k];
       if (o.dtype != TTLH_BF16 || !o.vec || o.rs >= (int64_t(1) << 24)) return false;
-      const int64_t ymax = o.rmask == -1 ? c.y0 + int64_t(c.total / c.cpr) - 1 + o.roff : 31 + o.roff;
+      const int64_t ymax = mask_max(o.rmask, c.y0 + int64_t(c.total / c.cpr) - 1) + o.roff;
       if (ymax >= (int64_t(1) << 24)) return false;
       mask |= 1u << k;
       a.ops[k] = StreamOp{static_cast<const uint16_t*>(o.ptr), static_cast<uint32_t>(o.rs),
@@ -1124,8 +1136,8 @@ void division_magic(uint32_t d, uint32_t* m, uint32_t* s) {
 // largest element offset an operand can reach over the region (decides the
 // 32-bit offset path)
 int64_t max_offset(const ttlh_operand& o, int64_t y0, int64_t x0, int64_t h, int64_t w) {
-  const int64_t ymax = o.row_mask == -1 ? y0 + h - 1 + o.row_off : 31 + o.row_off;
-  const int64_t xmax = o.col_mask == -1 ? x0 + w - 1 + o.col_off : 31 + o.col_off;
+  const int64_t ymax = mask_max(o.row_mask, y0 + h - 1) + o.row_off;
+  const int64_t xmax = mask_max(o.col_mask, x0 + w - 1) + o.col_off;
   return ymax * o.row_stride + xmax * o.col_stride;
 }
 
@@ -1207,10 +1219,10 @@ int decode_program(const char* who, const ttlh_instr* prog, const ttlh_operand* 
     const ttlh_operand& o = in[k];
     TTLH_REQUIRE(o.ptr && (o.dtype == TTLH_BF16 || o.dtype == TTLH_F32), TTLH_EINVAL,
                  "%s: operand %d has a null pointer or bad dtype", who, k);
-    TTLH_REQUIRE(o.row_mask == -1 || o.row_mask == 31, TTLH_EINVAL,
-                 "%s: operand %d row_mask must be -1 or 31", who, k);
-    TTLH_REQUIRE(o.col_mask == -1 || o.col_mask == 31, TTLH_EINVAL,
-                 "%s: operand %d col_mask must be -1 or 31", who, k);
+    TTLH_REQUIRE(valid_mask(o.row_mask), TTLH_EINVAL,
+                 "%s: operand %d row_mask must be -1, 31, 0 or ~31", who, k);
+    TTLH_REQUIRE(valid_mask(o.col_mask), TTLH_EINVAL,
+                 "%s: operand %d col_mask must be -1, 31, 0 or ~31", who, k);
     TTLH_REQUIRE(o.row_stride >= 0 && o.col_stride >= 0, TTLH_EINVAL,
                  "%s: operand %d has a negative stride", who, k);
     EltOperand& e = a.ops[pi.n_ops++];
@@ -1224,10 +1236,14 @@ int decode_program(const char* who, const ttlh_instr* prog, const ttlh_operand* 
     e.dtype = o.dtype;
     pi.all_bf16 = pi.all_bf16 && o.dtype == TTLH_BF16;
     const int esz = o.dtype == TTLH_BF16 ? 2 : 4;
-    e.vec = o.col_stride == 1 && aligned16(o.ptr) && ((o.row_stride * esz) % 16 == 0) &&
-            ((o.col_off * esz) % 16 == 0) && ((x0 * esz) % 16 == 0);
-    // stride-0 (broadcast) operands keep the 8-wide path; others need alignment
-    if (o.col_stride != 0 && !e.vec) pi.vec = false;
+    // column masks 0 / ~31 give every 8-element chunk (8-aligned, inside one
+    // tile) a single column: such operands are splatted like stride-0 ones
+    const bool col_uniform = o.col_stride == 0 || o.col_mask == 0 || o.col_mask == ~int64_t(31);
+    e.vec = !col_uniform && o.col_stride == 1 && aligned16(o.ptr) &&
+            ((o.row_stride * esz) % 16 == 0) && ((o.col_off * esz) % 16 == 0) &&
+            ((x0 * esz) % 16 == 0);
+    // chunk-uniform operands keep the 8-wide path; others need alignment
+    if (!col_uniform && !e.vec) pi.vec = false;
     const int64_t mo = max_offset(o, y0, x0, h, w);
     if (mo >= (int64_t(1) << 31) || o.row_off < 0 || o.col_off < 0) pi.off32 = false;
   }

@@ -35,3 +35,9 @@ from ttnn import CoreCoord, CoreRange  # noqa: F401,E402
 
 Shape = tuple
 Size = int
+
+# `from ttl import ttl` (the compiler package's python/ttl/ttl.py namespace
+# module, used by its hardware tests) names this same namespace
+import sys as _sys  # noqa: E402
+
+ttl = _sys.modules[__name__]

@@ -51,14 +51,23 @@ class _KernelState:
 
 
 _kstate: Optional[_KernelState] = None
+# grid of the most recent kernel body run in this process
+_last_grid: Optional[Tuple[int, ...]] = None
 
 
 def _grid() -> Tuple[int, ...]:
+    """Inside a kernel its grid.  Outside one, the grid of the last kernel
+    called, as the compiler's module-level grid (python/ttl/operators.py:36-47,
+    read back by its hardware tests after a call, test/python/test_multicore.py:
+    146-149); before any kernel, the simulator's error (python/sim/kernel.py:
+    110-118)."""
     ctx = T.current()
     if ctx is not None:
         return ctx.grid
     if _kstate is not None:
         return _kstate.grid
+    if _last_grid is not None:
+        return _last_grid
     raise RuntimeError("grid not available - function must be called within a kernel context")
 
 
@@ -278,9 +287,11 @@ def make_circular_buffer_like(element, shape: Tuple[int, int],
 
 class BExpr:
     """A block-shaped expression.  `tree` is one per-tile expression shared by
-    every tile of the block; its leaves are ("leaf", block, rmap, cmap) where
-    rmap[i] / cmap[j] give the leaf block's tile feeding output tile (i, j)
-    (that is how block broadcasting, python/sim/block.py:886-920, is kept)."""
+    every tile of the block; its leaves are ("leaf", block, rmap, cmap[, rep])
+    where rmap[i] / cmap[j] give the leaf block's tile feeding output tile
+    (i, j) (that is how block broadcasting, python/sim/block.py:886-920, is
+    kept) and rep = (rows, cols) marks the in-tile broadcast of
+    ttl.math.broadcast: each tile's row 0 / column 0 repeated over the tile."""
 
     __slots__ = ("shape", "tree", "dtype")
 
@@ -332,12 +343,12 @@ def _remap(tree, axis: int, new_len: int):
     """Broadcast a size-1 axis of every leaf map in `tree` to `new_len`."""
     tag = tree[0]
     if tag == "leaf":
-        _, blk, rmap, cmap = tree
+        blk, rmap, cmap = tree[1], tree[2], tree[3]
         if axis == 0:
             rmap = np.repeat(rmap[:1], new_len)
         else:
             cmap = np.repeat(cmap[:1], new_len)
-        return ("leaf", blk, rmap, cmap)
+        return ("leaf", blk, rmap, cmap) + tuple(tree[4:])
     if tag == "const":
         return tree
     if tag == "powi":
@@ -345,6 +356,31 @@ def _remap(tree, axis: int, new_len: int):
     if tag == "upar":
         return ("upar", _remap(tree[1], axis, new_len)) + tuple(tree[2:])
     return (tag,) + tuple(_remap(t, axis, new_len) for t in tree[1:])
+
+
+def leaf_rep(leaf) -> Tuple[bool, bool]:
+    """(rows, cols) in-tile broadcast flags of an expression leaf."""
+    return leaf[4] if len(leaf) > 4 else (False, False)
+
+
+def _tile_rep(tree, rows: bool, cols: bool):
+    """Marks every leaf of `tree` for the in-tile broadcast of row 0 (rows)
+    and / or column 0 (cols): elementwise ops commute with picking one row or
+    column of every tile, so the broadcast of an expression is the expression
+    of broadcast operands."""
+    tag = tree[0]
+    if tag == "leaf":
+        r0, c0 = leaf_rep(tree)
+        return tuple(tree[:4]) + ((r0 or rows, c0 or cols),)
+    if tag == "const":
+        return tree
+    if tag in ("powi", "upar"):
+        return (tag, _tile_rep(tree[1], rows, cols)) + tuple(tree[2:])
+    if tag in ("reduce", "matmul"):
+        raise NotImplementedError(f"ttl.math.broadcast of a {tag} result inside one store() is not "
+                                  "supported; store the result into a CB first and broadcast the "
+                                  "block waited from it")
+    return (tag,) + tuple(_tile_rep(t, rows, cols) for t in tree[1:])
 
 
 def _binary(op: str, a, b) -> BExpr:
@@ -757,20 +793,37 @@ class _Math:
     """ttl.math: broadcast, the elementwise tile ops and the scaled reductions."""
 
     @staticmethod
-    def broadcast(block, _unused=None, dims: Optional[Sequence[int]] = None) -> BExpr:
-        """Validates that `block` has size 1 along `dims`; the broadcast itself
-        happens in the enclosing binary op (python/sim/math.py:20-106)."""
+    def broadcast(block, out=None, dims: Optional[Sequence[int]] = None) -> BExpr:
+        """The compiler's tile broadcast (python/ttl/operators.py:333-360, tile
+        op unary_bcast Row / Col / Scalar, TTLElementwiseOps.def:82): every
+        tile becomes its row 0 (dims=[0]), column 0 ([1]) or element [0, 0]
+        ([0, 1]) repeated over the tile, and a block dimension of size 1
+        along a broadcast dim takes the size of the output block `out`
+        (shape expansion, test/python/test_bcast_shape_expansion.py).  Without
+        `out` the broadcast block dims must have size 1 and the enclosing
+        binary op broadcasts them (python/sim/math.py:20-106).  For operands
+        of a size-1 tensor dimension, the simulator's use, picking row /
+        column 0 changes nothing."""
         if dims is None:
             raise ValueError("dims parameter is required for broadcast()")
         e = _as_bexpr(block)
+        target = tuple(out.shape) if out is not None else None
+        shape, tree = list(e.shape), e.tree
         for d in dims:
             if d >= len(e.shape):
                 raise ValueError(f"Cannot broadcast along dimension {d}: block has shape {e.shape} "
                                  f"with only {len(e.shape)} dimensions")
-            if e.shape[d] != 1:
+            n = e.shape[d]
+            if n == 1 and target is not None and target[d] != 1:
+                tree = _remap(tree, d, target[d])
+                shape[d] = target[d]
+            elif n != 1 and (target is None or target[d] != n):
                 raise ValueError(f"Cannot broadcast along dimension {d}: dimension must have size "
-                                 f"1, but has size {e.shape[d]}")
-        return e
+                                 f"1, but has size {n}")
+        if set(dims) - {0, 1}:
+            raise ValueError(f"Invalid dims: {list(dims)}. Must be [0], [1], or [0, 1]")
+        tree = _tile_rep(tree, 0 in dims, 1 in dims)
+        return BExpr(tuple(shape), tree, e.dtype)
 
     @staticmethod
     def exp(x): return _unary("exp", x)

@@ -22,8 +22,10 @@ from .expr import StackProgram
 @dataclass
 class OperandMap:
     """How an eltwise operand is addressed from output element (y, x):
-    iy = (y & row_mask) + row_off, ix = (x & col_mask) + col_off; a size-1
-    tensor dimension is broadcast (stride 0)."""
+    iy = (y & row_mask) + row_off, ix = (x & col_mask) + col_off with masks
+    -1 (identity), 31 (one tile re-used), ~31 (row / column 0 of every tile)
+    or 0 (one fixed row / column); a size-1 tensor dimension is broadcast
+    (stride 0)."""
 
     tensor: torch.Tensor
     row_mask: int = -1
@@ -45,6 +47,12 @@ def _axis_range(lo: int, n: int, mask: int, off: int):
         return None
     if mask == -1:
         return lo + off, lo + n - 1 + off
+    if mask == 0:
+        return off, off
+    if mask == ~31:
+        return (lo & ~31) + off, ((lo + n - 1) & ~31) + off
+    if mask != 31:
+        raise ValueError(f"operand mask must be -1, 31, 0 or ~31, got {mask}")
     vals_lo, vals_hi = 31, 0
     if n >= 32:
         vals_lo, vals_hi = 0, 31

@@ -194,6 +194,118 @@ def _copy_table(events: List[T.Event], cb, n: int, kind: str, received=None) -> 
     return _CopyTable(tensor, r0, c0)
 
 
+class _Scratch:
+    """Device memory standing in for an intermediate CB: one the compute
+    thread both stores into and waits on (test/python/test_intermediate_cb.py,
+    the two-stage broadcast kernels of test/python/test_bcast_ops.py).  Every
+    block of the CB gets its own tiles, placed at the tile coordinates of the
+    store that reads it, so the storing launch writes the block there and the
+    reading launch finds it where an operand filled by ttl.copy from a tensor
+    would be.  The two launches run in trace order (the store first)."""
+
+    is_block_float = False
+
+    def __init__(self, cb):
+        if not isinstance(cb.dtype, torch.dtype):
+            raise PlanError(f"CB {cb.name}: an intermediate CB of a block-float dtype is not "
+                            "supported")
+        self.cb = cb
+        self.dtype = cb.dtype
+        self.rows = 0
+        self.cols = 0
+        self._tiles: List[np.ndarray] = []
+        self._t: Optional[torch.Tensor] = None
+
+    @property
+    def shape(self) -> Tuple[int, int]:
+        return (self.rows * TILE, self.cols * TILE)
+
+    def place(self, r0: np.ndarray, c0: np.ndarray) -> None:
+        R, C = self.cb.shape
+        if r0.size:
+            self.rows = max(self.rows, int(r0.max()) + R)
+            self.cols = max(self.cols, int(c0.max()) + C)
+        i, j = np.divmod(np.arange(R * C), C)
+        self._tiles.append(np.stack([(r0[:, None] + i[None, :]).ravel(),
+                                     (c0[:, None] + j[None, :]).ravel()], 1))
+
+    def check(self) -> None:
+        rc = np.concatenate(self._tiles, 0)
+        if rc.size and _unique_tiles(rc) != rc.shape[0]:
+            raise PlanError(f"CB {self.cb.name}: its blocks are read by stores whose output blocks "
+                            "overlap once laid out at the CB's block shape; an intermediate CB "
+                            "needs one output block of the reading store per block")
+
+    @property
+    def _tensor(self) -> torch.Tensor:
+        if self._t is None or tuple(self._t.shape) != self.shape:
+            dev = "cuda" if torch.cuda.is_available() else "cpu"
+            self._t = torch.zeros(self.shape, dtype=self.dtype, device=dev)
+        return self._t
+
+
+def _intermediate_tables(threads, events, cbs, count, inter, fill, drain,
+                         scratch: Dict[int, _Scratch]) -> None:
+    """Copy tables of the intermediate CBs `inter` on one core: block k of
+    such a CB sits at the output tile origin of the store that reads it
+    (resolved through chains of intermediate CBs); the table serves both as
+    the CB's drain (for the store into it) and its fill (for the reads)."""
+    comp = [tmpl for tmpl, _ in threads if tmpl.kind == "compute"]
+    stores = [ev for ev in events[id(comp[0])] if ev.kind == "store"] if comp else []
+    inter_set = set(inter)
+    state: Dict[int, str] = {}
+
+    def table(cid):
+        if cid in drain:
+            return drain[cid]
+        if state.get(cid) == "busy":
+            raise PlanError("intermediate CBs feed each other in a cycle")
+        state[cid] = "busy"
+        cb = cbs[cid]
+        n = count[cid]
+        r0 = np.full(n, -1, dtype=np.int64)
+        c0 = np.full(n, -1, dtype=np.int64)
+        for ev in stores:
+            tree = ev.data["expr"].tree
+            leaves = _tree_leaves(tree, [])
+            if tree[0] == "reduce" and tree[5][0] == "leaf":
+                leaves.append(tree[5])
+            mine = [lf for lf in leaves if lf[1].cb.id == cid]
+            if not mine:
+                continue
+            target = ev.data["target"]
+            tcid = target.cb.id
+            if tcid not in drain and tcid not in inter_set:
+                raise PlanError(f"CB {target.cb.name} is stored into but never copied to a tensor "
+                                "or read by the compute thread")
+            dt = table(tcid)
+            shape = ev.domain_shape()
+            rout = T.broadcast_to_domain(target.event.index, shape).ravel()
+            sr, sc = dt.r0[rout], dt.c0[rout]
+            for lf in mine:
+                w = T.broadcast_to_domain(lf[1].event.index, shape).ravel()
+                seen = r0[w] >= 0
+                if np.any(seen & ((r0[w] != sr) | (c0[w] != sc))):
+                    raise PlanError(f"a block of intermediate CB {cb.name} is read by stores "
+                                    "into different output positions")
+                r0[w] = sr
+                c0[w] = sc
+        if np.any(r0 < 0):
+            raise PlanError(f"every block stored into CB {cb.name} must be read by a later "
+                            "store of the compute thread")
+        sc_ = scratch.get(cid)
+        if sc_ is None:
+            sc_ = scratch[cid] = _Scratch(cb)
+        sc_.place(r0, c0)
+        tab = _CopyTable(sc_, r0, c0)
+        drain[cid] = fill[cid] = tab
+        state[cid] = "done"
+        return tab
+
+    for cid in inter:
+        table(cid)
+
+
 @dataclass
 class _Group:
     """All instances of one store site (same expression, tensors, acc)."""
@@ -211,6 +323,11 @@ class _Group:
     # reductions: the scaler's tensor and its tile per store instance
     scaler_tensor: Any = None
     scaler_rc: List[np.ndarray] = field(default_factory=list)
+
+
+def _leaf_rep(leaf) -> Tuple[bool, bool]:
+    """(rows, cols) in-tile broadcast flags of an expression leaf (5th item)."""
+    return leaf[4] if len(leaf) > 4 else (False, False)
 
 
 def _tree_leaves(tree, out: List):
@@ -234,7 +351,8 @@ def _tree_leaves(tree, out: List):
 def _tree_key(tree, leaf_ids: Dict[int, int]):
     tag = tree[0]
     if tag == "leaf":
-        return ("leaf", leaf_ids.setdefault(id(tree), len(leaf_ids)), str(tree[1].cb.dtype))
+        return ("leaf", leaf_ids.setdefault(id(tree), len(leaf_ids)), str(tree[1].cb.dtype),
+                _leaf_rep(tree))
     if tag == "const":
         return ("const", tree[1])
     if tag == "powi":
@@ -388,6 +506,7 @@ def resolve(core_traces: List[Dict[str, Any]]) -> List[_Group]:
                 direct[cb.id] = _copy_table(evs, cb, n, "copy_in", received=_no_forwarding)
         pre.append((events, direct, totals))
     sends = _pipe_sends(core_traces, [(e, d) for e, d, _ in pre])
+    scratch: Dict[int, _Scratch] = {}
 
     for ct, (events, _, totals) in zip(core_traces, pre):
         threads = ct["threads"]
@@ -442,6 +561,11 @@ def resolve(core_traces: List[Dict[str, Any]]) -> List[_Group]:
                                         received)
             if cid in consumers and consumers[cid].kind == "dm":
                 drain[cid] = _copy_table(events[id(consumers[cid])], cb, count[cid], "copy_out")
+        inter = [cid for cid in cbs if producers.get(cid) is not None
+                 and consumers.get(cid) is not None and producers[cid].kind == "compute"
+                 and consumers[cid].kind == "compute"]
+        if inter:
+            _intermediate_tables(threads, events, cbs, count, inter, fill, drain, scratch)
         # stores
         for tmpl, root in threads:
             for ev in events[id(tmpl)]:
@@ -451,8 +575,9 @@ def resolve(core_traces: List[Dict[str, Any]]) -> List[_Group]:
                 e = ev.data["expr"]
                 cid = target.cb.id
                 if cid not in drain:
-                    raise PlanError("stored blocks must be copied to a tensor by a data-movement "
-                                    "thread (CB-to-CB chains are not supported)")
+                    raise PlanError(f"blocks stored into CB {target.cb.name} must be copied to a "
+                                    "tensor by a data-movement thread or read back by the compute "
+                                    "thread")
                 shape = ev.domain_shape()
                 rout = T.broadcast_to_domain(target.event.index, shape).ravel()
                 dt = drain[cid]
@@ -472,7 +597,7 @@ def resolve(core_traces: List[Dict[str, Any]]) -> List[_Group]:
                 leaf_tensors = []
                 ei, ej = slot // ec, slot % ec  # expression slot of each target slot
                 for lf in leaves:
-                    _, blk, rmap, cmap = lf
+                    blk, rmap, cmap = lf[1], lf[2], lf[3]
                     lcid = blk.cb.id
                     if lcid not in fill:
                         raise PlanError("expression operands must come from blocks filled by "
@@ -494,6 +619,8 @@ def resolve(core_traces: List[Dict[str, Any]]) -> List[_Group]:
                 g.out_rc.append(np.stack([out_r, out_c], 1))
                 g.leaf_rc.append(leaf_rc)
                 g.order.append(order)
+    for sc in scratch.values():
+        sc.check()
     return list(groups.values())
 
 
@@ -518,7 +645,7 @@ def _resolve_reduce(ev, e, target, rout, dt, fill, shape, groups) -> None:
         raise PlanError("a reduction needs at least one operand read from a tensor")
     leaf_rc, leaf_tensors = [], []
     for lf in leaves:
-        _, blk, rmap, cmap = lf
+        blk, rmap, cmap = lf[1], lf[2], lf[3]
         if blk.cb.id not in fill:
             raise PlanError("expression operands must come from blocks filled by ttl.copy from a "
                             "tensor")
@@ -530,7 +657,7 @@ def _resolve_reduce(ev, e, target, rout, dt, fill, shape, groups) -> None:
         leaf_tensors.append(ft.tensor)
     s_tensor, s_rc = None, None
     if stree[0] == "leaf":
-        _, sblk, srm, scm = stree
+        sblk, srm, scm = stree[1], stree[2], stree[3]
         if sblk.cb.id not in fill:
             raise PlanError("a reduction's scaler block must be filled by ttl.copy from a tensor")
         ft = fill[sblk.cb.id]
@@ -567,18 +694,32 @@ def _unique_tiles(rc: np.ndarray) -> int:
     return int(np.unique(key).size)
 
 
-def _axis_map(out_t: np.ndarray, in_t: np.ndarray, dim: int) -> Tuple[int, int]:
-    """(mask, element offset) reproducing in_tile = f(out_tile) on one axis."""
+def _axis_map(out_t: np.ndarray, in_t: np.ndarray, dim: int,
+              rep: bool = False) -> Tuple[int, int]:
+    """(mask, element offset) reproducing in_tile = f(out_tile) on one axis;
+    rep: element 0 of the axis in every tile (in-tile broadcast)."""
     if dim == 1:  # degenerate tensor dimension: stride 0, only tile 0 exists
         return 31, 0
     d = in_t - out_t
     if np.all(d == d[0]):
-        return -1, int(d[0]) * TILE
+        return (~31 if rep else -1), int(d[0]) * TILE
     if np.all(in_t == in_t[0]):
-        return 31, int(in_t[0]) * TILE
-    raise PlanError("an operand's tiles are not an affine image of the output tiles "
-                    "(only identity, offset, fixed-tile reuse and size-1 broadcast map onto the "
-                    "grid-wide kernel)")
+        return (0 if rep else 31), int(in_t[0]) * TILE
+    raise _NotAffine("an operand's tiles are not an affine image of the output tiles "
+                     "(only identity, offset, fixed-tile reuse and size-1 broadcast map onto the "
+                     "grid-wide kernel)")
+
+
+class _NotAffine(PlanError):
+    """An operand's tile map is not one the kernels address; `leaf` and
+    `axis` name it."""
+
+    leaf: int = -1
+    axis: int = -1
+
+
+# most launches one store site may be split into (see _plan_eltwise_parts)
+_MAX_PARTS = 4096
 
 
 _BIN = {"add", "sub", "mul", "div", "max", "min", "pow", "floordiv", "mod"}
@@ -642,7 +783,10 @@ def build_plan(groups: List[_Group], tensor_ref) -> Plan:
             raise PlanError("a tile matmul combined with other ops in one store() is not "
                             "supported; store the product on its own")
         else:
-            launch = _plan_eltwise(g, out_rc, leaf_rc, tensor_ref)
+            for launch in _plan_eltwise_parts(g, out_rc, leaf_rc, tensor_ref):
+                launch.loc = g.loc
+                plan.launches.append(launch)
+            continue
         launch.loc = g.loc
         plan.launches.append(launch)
     return plan
@@ -671,8 +815,15 @@ def _plan_eltwise(g: _Group, out_rc, leaf_rc, tensor_ref) -> EltwiseLaunch:
             raise PlanError(f"a {tens.dtype.name} tensor as an elementwise operand is not "
                             "supported; it can be the B operand of a tile matmul")
         h, w = tens.shape
-        rm, ro = _axis_map(out_rc[:, 0], leaf_rc[k][:, 0], h)
-        cm, co = _axis_map(out_rc[:, 1], leaf_rc[k][:, 1], w)
+        rr, cr = _leaf_rep(lf)
+        try:
+            axis = 0
+            rm, ro = _axis_map(out_rc[:, 0], leaf_rc[k][:, 0], h, rr)
+            axis = 1
+            cm, co = _axis_map(out_rc[:, 1], leaf_rc[k][:, 1], w, cr)
+        except _NotAffine as err:
+            err.leaf, err.axis = k, axis
+            raise
         leaf = X.Leaf(k, lf[1].cb.dtype)
         leaf_nodes[id(lf)] = leaf
         specs[k] = OperandSpec(tensor_ref(tens), rm, cm, ro, co)
@@ -683,6 +834,33 @@ def _plan_eltwise(g: _Group, out_rc, leaf_rc, tensor_ref) -> EltwiseLaunch:
     h = min(r1 * TILE, H) - y0
     w = min(c1 * TILE, W) - x0
     return EltwiseLaunch(prog, operands, tensor_ref(out_t), (y0, x0, h, w), n)
+
+
+def _plan_eltwise_parts(g: _Group, out_rc, leaf_rc, tensor_ref) -> List[EltwiseLaunch]:
+    """One launch when every operand is an affine image of the output tiles;
+    otherwise the store's instances are split by the tile of the first
+    operand that is not (that operand is then one fixed tile in each part)
+    and each part planned the same way, e.g. a tile held across a loop over
+    a block of output tiles (test/python/test_bcast_multicore.py).  Each part
+    must still write a rectangle of output tiles.  The split is along the
+    axis whose map failed only."""
+    try:
+        return [_plan_eltwise(g, out_rc, leaf_rc, tensor_ref)]
+    except _NotAffine as err:
+        k = err.leaf
+        if k < 0:
+            raise
+        uniq, inv = np.unique(leaf_rc[k][:, err.axis], return_inverse=True)
+        if uniq.size > _MAX_PARTS or uniq.size == 1:
+            raise
+        out: List[EltwiseLaunch] = []
+        for u in range(uniq.size):
+            sel = inv == u
+            out += _plan_eltwise_parts(g, out_rc[sel], [x[sel] for x in leaf_rc], tensor_ref)
+            if len(out) > _MAX_PARTS:
+                raise PlanError(f"a store site needs more than {_MAX_PARTS} launches: its "
+                                "operands' tiles follow the output tiles in no affine way") from err
+        return out
 
 
 def _plan_reduce(g: _Group, out_rc, leaf_rc, order, tensor_ref) -> ReduceLaunch:
@@ -744,8 +922,9 @@ def _plan_reduce(g: _Group, out_rc, leaf_rc, order, tensor_ref) -> ReduceLaunch:
     for k, lf in enumerate(g.leaf_blocks):
         tens = g.leaf_tensors[k]
         h, w = tens.shape
-        rm, ro = _axis_map(it[:, 0], leaf_rc[k][:, 0], h)
-        cm, co = _axis_map(it[:, 1], leaf_rc[k][:, 1], w)
+        rr, cr = _leaf_rep(lf)
+        rm, ro = _axis_map(it[:, 0], leaf_rc[k][:, 0], h, rr)
+        cm, co = _axis_map(it[:, 1], leaf_rc[k][:, 1], w, cr)
         leaf = X.Leaf(k, lf[1].cb.dtype)
         leaf_nodes[id(lf)] = leaf
         specs[k] = OperandSpec(tensor_ref(tens), rm, cm, ro, co)

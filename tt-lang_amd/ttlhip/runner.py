@@ -98,6 +98,7 @@ class KernelRunner:
                                   self.func.__defaults__, self.func.__closure__)
         prev = dsl._kstate
         dsl._kstate = dsl._KernelState(self.grid)
+        dsl._last_grid = tuple(self.grid)
         prev_created, ttnn._created = ttnn._created, []
         try:
             body(*args, **kwargs)

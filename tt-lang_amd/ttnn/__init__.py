@@ -34,8 +34,29 @@ class _Layout:
 
 TILE_LAYOUT = _Layout("TILE")
 ROW_MAJOR_LAYOUT = _Layout("ROW_MAJOR")
-DRAM_MEMORY_CONFIG = None
-L1_MEMORY_CONFIG = None
+class MemoryConfig:
+    """Where a ttnn tensor lives (DRAM or L1, interleaved).  On the MI355X
+    every tensor is in HBM; the config is kept only so programs can read it
+    back (tensor.memory_config())."""
+
+    def __init__(self, buffer_type: str, layout: str = "INTERLEAVED") -> None:
+        self.buffer_type = buffer_type
+        self.memory_layout = layout
+
+    def __repr__(self) -> str:
+        return (f"MemoryConfig(memory_layout=TensorMemoryLayout::{self.memory_layout}, "
+                f"buffer_type=BufferType::{self.buffer_type})")
+
+    def __eq__(self, o) -> bool:
+        return isinstance(o, MemoryConfig) and (o.buffer_type, o.memory_layout) == (
+            self.buffer_type, self.memory_layout)
+
+    def __hash__(self) -> int:
+        return hash((self.buffer_type, self.memory_layout))
+
+
+DRAM_MEMORY_CONFIG = MemoryConfig("DRAM")
+L1_MEMORY_CONFIG = MemoryConfig("L1")
 
 bfloat16 = torch.bfloat16
 float32 = torch.float32
@@ -116,6 +137,10 @@ class Tensor:
         # block-float tensors: _tensor holds the packed tile bytes (uint8)
         self._block = block
         self._logical_shape = tuple(logical_shape) if logical_shape is not None else None
+        self._memory_config = DRAM_MEMORY_CONFIG
+
+    def memory_config(self) -> MemoryConfig:
+        return self._memory_config
 
     # -- metadata -----------------------------------------------------------
     @property
@@ -300,7 +325,10 @@ def from_torch(tensor: torch.Tensor, dtype=None, layout: Any = None,
         return _block_from_fp32(t.cpu(), dtype)
     if dtype is not None:
         t = t.to(dtype)
-    return Tensor(t.to(_device()).contiguous(), layout=layout)
+    out = Tensor(t.to(_device()).contiguous(), layout=layout)
+    if isinstance(memory_config, MemoryConfig):
+        out._memory_config = memory_config
+    return out
 
 
 def from_tiled_data(data: torch.Tensor, shape: Sequence[int], dtype=None,
@@ -321,6 +349,18 @@ def to_torch(t: Union[Tensor, torch.Tensor], **_: Any) -> torch.Tensor:
     if isinstance(t, Tensor):
         return t.to_torch()
     return t
+
+
+def to_memory_config(t: Tensor, memory_config: Any = None, **_: Any) -> Tensor:
+    """A copy of `t` tagged with `memory_config` (ttnn moves the data; here
+    every tensor stays in HBM, so only the tag differs)."""
+    if t.is_block_float:
+        out = Tensor(t._tensor.clone(), block=t._block, logical_shape=t.shape, layout=t._layout)
+    else:
+        out = Tensor(t._tensor.clone(), layout=t._layout)
+    if isinstance(memory_config, MemoryConfig):
+        out._memory_config = memory_config
+    return out
 
 
 def to_layout(t: Tensor, layout: Any, **_: Any) -> Tensor:
@@ -515,9 +555,11 @@ def _ordered_cores(core_grid: Union[CoreCoord, CoreRangeSet], row_wise: bool) ->
         return [CoreCoord(x, y) for x in range(core_grid.x) for y in range(core_grid.y)]
     out = []
     for r in core_grid.ranges():
-        for y in range(r.start.y, r.end.y + 1):
-            for x in range(r.start.x, r.end.x + 1):
-                out.append(CoreCoord(x, y))
+        ys, xs = range(r.start.y, r.end.y + 1), range(r.start.x, r.end.x + 1)
+        if row_wise:
+            out.extend(CoreCoord(x, y) for y in ys for x in xs)
+        else:
+            out.extend(CoreCoord(x, y) for x in xs for y in ys)
     return out
 
 
@@ -528,8 +570,11 @@ def split_work_to_cores(core_grid: Union[CoreCoord, CoreRangeSet], units_to_divi
     Same assignment as the reference (python/sim/ttnnsim.py:583-752): min(cores,
     units) cores are used; with a remainder, the first `remainder` cores
     (group 1) get one unit more than the rest (group 2); cores are taken y-outer
-    / x-inner when row_wise (x-outer otherwise) for a CoreCoord grid and range
-    by range for a CoreRangeSet.  Each group lists single-core ranges.
+    / x-inner when row_wise (x-outer otherwise), range by range for a
+    CoreRangeSet.  (The simulator takes a CoreRangeSet's cores y-outer either
+    way; tt-metal's ttnn, which the reference's hardware tests compare with,
+    test/python/test_block_allocation.py:54-120, honours row_wise.)  Each
+    group lists single-core ranges.
     Returns (num_cores, all_cores, group_1, group_2, units_1, units_2).
     """
     if isinstance(core_grid, CoreCoord):

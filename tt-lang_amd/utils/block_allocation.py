@@ -121,3 +121,130 @@ def split_work_to_cores(grid_size: Tuple[int, ...], units_to_divide: int, row_wi
     start2 = pre + (sy, sx)
     last2 = num_cores_to_grid_ranges(start2, total - extra, grid_size, row_wise)[-1][1]
     return (total, (origin, last1), (start2, last2), per + 1, per)
+
+
+# ---------------------------------------------------------------------------
+# per-core matmul block sizes (python/utils/block_allocation.py:292-487): the
+# heuristic a Tensix matmul host program uses to size its per-core output
+# blocks under a 400-tile L1 budget.  Kept identical because callers size
+# their grids and loops from its answer (the metal multicore_reuse_matmul
+# example); the MI355X kernels do not use it.
+
+from collections import namedtuple  # noqa: E402
+
+MatmulParams = namedtuple("MatmulParams", ["block_h", "block_w", "subblock_h", "subblock_w"])
+
+# (subblock_h, subblock_w) in the order they are tried (the reference's table)
+SUBBLOCK_HW_CHOICES = [(4, 2), (2, 4), (8, 1), (1, 8), (7, 1), (1, 7), (3, 2), (2, 3), (6, 1),
+                       (1, 6), (5, 1), (1, 5), (2, 2), (4, 1), (1, 4), (3, 1), (1, 3), (2, 1),
+                       (1, 2), (1, 1)]
+
+_L1_TILE_BUDGET = 400
+
+
+def filter_factor_pairs_by_2d_grid(factor_pairs, grid):
+    """Pairs that fit the 2-D grid as given or transposed (transposed ones
+    are returned transposed)."""
+    out = []
+    for a, b in factor_pairs:
+        if a <= grid[0] and b <= grid[1]:
+            out.append((a, b))
+        elif b <= grid[0] and a <= grid[1]:
+            out.append((b, a))
+    return out
+
+
+def get_prime_factors_with_multiplicity(n: int) -> List[int]:
+    """Prime factors of n in ascending order, repeated by multiplicity."""
+    out, p = [], 2
+    while p * p <= n:
+        while n % p == 0:
+            out.append(p)
+            n //= p
+        p += 1
+    if n > 1:
+        out.append(n)
+    return out
+
+
+def get_possible_products(factors: List[int]) -> List[int]:
+    """Every distinct product of a sub-multiset of `factors`, ascending (1 included)."""
+    prods = {1}
+    for f in factors:
+        prods |= {q * f for q in prods}
+    return sorted(prods)
+
+
+def get_maximum_block_dim(block_dim: int, in0_block_w: int) -> int:
+    """Largest other block dimension o with 2 k b + 2 k o + b o <= 400 tiles
+    (double-buffered A and B plus C, k = in0_block_w, b = block_dim); 0 when
+    none fits."""
+    o = (_L1_TILE_BUDGET - 2 * in0_block_w * block_dim) // (2 * in0_block_w + block_dim)
+    return o if o > 0 else 0
+
+
+def _subblock(mpc: int, npc: int):
+    for sh, sw in SUBBLOCK_HW_CHOICES:
+        if mpc % sh == 0 and npc % sw == 0:
+            return MatmulParams(mpc, npc, sh, sw)
+    return None
+
+
+def get_large_matmul_params(Mt: int, Nt: int, num_cores_y: int, num_cores_x: int,
+                            in0_block_w: int) -> MatmulParams:
+    """Per-core block (block_h x block_w tiles of the Mt x Nt output) and
+    subblock for a num_cores_y x num_cores_x grid, or MatmulParams(0, 0, 0, 0)
+    when no block fits.  Prime factors of Mt / Nt larger than the grid side
+    must stay inside one core's block; the rest are grown greedily within the
+    L1 budget (the larger dimension first when only one side has such
+    factors)."""
+    none = MatmulParams(0, 0, 0, 0)
+    mf = get_prime_factors_with_multiplicity(Mt)
+    nf = get_prime_factors_with_multiplicity(Nt)
+    mpc_min = 1
+    for f in (f for f in mf if f > num_cores_y):
+        mpc_min *= f
+    npc_min = 1
+    for f in (f for f in nf if f > num_cores_x):
+        npc_min *= f
+    mf = [f for f in mf if f <= num_cores_y]
+    nf = [f for f in nf if f <= num_cores_x]
+    if npc_min > get_maximum_block_dim(mpc_min, in0_block_w):
+        return none
+
+    def fits(mpc, npc):
+        return Mt // mpc <= num_cores_y and Nt // npc <= num_cores_x
+
+    def grow(base, choices, limit):
+        best = base
+        for c in choices:
+            if c * base > limit:
+                break
+            best = c * base
+        return best
+
+    if mpc_min > 1:
+        mpc = mpc_min
+        npc = grow(npc_min, get_possible_products(nf), get_maximum_block_dim(mpc_min, in0_block_w))
+        if not fits(mpc, npc):
+            return none
+        return _subblock(mpc, npc) or none
+    if npc_min > 1:
+        npc = npc_min
+        mpc = grow(mpc_min, get_possible_products(mf), get_maximum_block_dim(npc_min, in0_block_w))
+        if not fits(mpc, npc):
+            return none
+        return _subblock(mpc, npc) or none
+    mchoices = get_possible_products(mf)
+    mpc = 1
+    for npc in get_possible_products(nf):
+        lim = get_maximum_block_dim(npc, in0_block_w)
+        for c in mchoices:
+            if c <= lim:
+                mpc = c
+        if not fits(mpc, npc):
+            continue
+        r = _subblock(mpc, npc)
+        if r is not None:
+            return r
+    return none
