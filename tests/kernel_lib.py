@@ -950,3 +950,60 @@ def make_held_tile(ttl, n=4, grid=(2, 2)):
                         ttl.copy(o, out[y * n + i, x * n + j]).wait()
 
     return held_tile
+
+
+def make_long_chain(ttl, g=2, grid=(2, 2)):
+    """A 22-op fused expression (more steps than one kernel program holds):
+    the planner computes part of it into a temporary first."""
+    @ttl.kernel(grid=grid)
+    def long_chain(a, b, c, out):
+        rows = out.shape[0] // TILE // g
+        cols = out.shape[1] // TILE // g
+        ncores = grid[0] * grid[1]
+        per = -(-rows // ncores)
+        a_cb = ttl.make_circular_buffer_like(a, shape=(g, g), buffer_factor=2)
+        b_cb = ttl.make_circular_buffer_like(b, shape=(g, g), buffer_factor=2)
+        c_cb = ttl.make_circular_buffer_like(c, shape=(g, g), buffer_factor=2)
+        o_cb = ttl.make_circular_buffer_like(out, shape=(g, g), buffer_factor=2)
+
+        @ttl.compute()
+        def comp():
+            c_ = ttl.core(dims=1)
+            for r in range(c_ * per, min(rows, (c_ + 1) * per)):
+                for _ in range(cols):
+                    with a_cb.wait() as av, b_cb.wait() as bv, c_cb.wait() as cv, \
+                            o_cb.reserve() as o:
+                        v = ttl.math.sigmoid(av)
+                        v = ttl.math.tanh(v) * 3.0
+                        v = ttl.math.abs(v - bv)
+                        v = ttl.math.sigmoid(v + cv)
+                        v = ttl.math.neg(v) * bv
+                        v = ttl.math.relu(v + 0.25)
+                        v = ttl.math.tanh(v * cv)
+                        v = ttl.math.max(v, bv) - ttl.math.min(av, cv)
+                        v = ttl.math.sigmoid(v) * 2.0 + av
+                        o.store(ttl.math.tanh(v))
+
+        @ttl.datamovement()
+        def rd():
+            c_ = ttl.core(dims=1)
+            for r in range(c_ * per, min(rows, (c_ + 1) * per)):
+                for k in range(cols):
+                    with a_cb.reserve() as ab, b_cb.reserve() as bb, c_cb.reserve() as cb:
+                        sl = (slice(r * g, (r + 1) * g), slice(k * g, (k + 1) * g))
+                        t1 = ttl.copy(a[sl[0].start:sl[0].stop, sl[1].start:sl[1].stop], ab)
+                        t2 = ttl.copy(b[sl[0].start:sl[0].stop, sl[1].start:sl[1].stop], bb)
+                        t3 = ttl.copy(c[sl[0].start:sl[0].stop, sl[1].start:sl[1].stop], cb)
+                        t1.wait()
+                        t2.wait()
+                        t3.wait()
+
+        @ttl.datamovement()
+        def wr():
+            c_ = ttl.core(dims=1)
+            for r in range(c_ * per, min(rows, (c_ + 1) * per)):
+                for k in range(cols):
+                    with o_cb.wait() as o:
+                        ttl.copy(o, out[r * g:(r + 1) * g, k * g:(k + 1) * g]).wait()
+
+    return long_chain

@@ -42,8 +42,16 @@ PYTEST_FILES = {
     "test_tensor_slice.py": 241,
     "test_uneven_grids.py": 14,
 }
+# lit-style scripts that check their result and print PASS
 SCRIPT_FILES = ["test_ttnn_interop_add.py", "test_dram_interleaved_add.py",
-                "test_large_dram_streaming.py"]
+                "test_large_dram_streaming.py", "many_fused_ops.py", "simple_bcast.py",
+                "mixed_l1_dram.py", "program_cache_lit.py"]
+# lit-style compile checks (their FileCheck patterns are MLIR / C++ of the
+# reference compiler): the kernels must trace, plan and run cleanly
+CLEAN_FILES = ["simple_add.py", "simple_add_dram.py", "simple_add_f32.py",
+               "simple_add_loop.py", "simple_add_multitile.py", "simple_add_with_stmt.py",
+               "simple_fused.py", "simple_multicore.py", "debug_locations.py",
+               "auto_profile_signposts.py"]
 
 
 def _env():
@@ -77,3 +85,12 @@ def test_reference_script(name, tmp_path):
     tail = r.stdout[-3000:] + r.stderr[-2000:]
     assert r.returncode == 0, tail
     assert "PASS" in r.stdout and "FAIL" not in r.stdout, tail
+
+
+@needs_ref
+@pytest.mark.parametrize("name", CLEAN_FILES)
+def test_reference_compile_script_runs(name, tmp_path):
+    cmd = [sys.executable, os.path.join(HERE, "refsuite_plugin.py"), os.path.join(SUITE, name)]
+    r = subprocess.run(cmd, cwd=tmp_path, env=_env(), capture_output=True, text=True,
+                       timeout=600)
+    assert r.returncode == 0, r.stdout[-3000:] + r.stderr[-2000:]

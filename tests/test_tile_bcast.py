@@ -154,3 +154,15 @@ def test_broadcast_validation():
     t = ttnn.Tensor(torch.zeros(64, 64, dtype=torch.bfloat16))
     with pytest.raises(ValueError, match="dimension must have size 1, but has size 2"):
         k.trace(t, ttnn.Tensor(torch.zeros(64, 64, dtype=torch.bfloat16)))
+
+
+def test_long_chain_split_through_temporaries():
+    a = O.seeded((256, 128), "uniform", 21, lo=-2, hi=2)
+    b = O.seeded((256, 128), "uniform", 22, lo=-2, hi=2)
+    c = O.seeded((256, 128), "uniform", 23, lo=-2, hi=2)
+    out = torch.zeros(256, 128, dtype=torch.bfloat16)
+    got, plan = _plan_run(KL.make_long_chain, [a, b, c, out], 3)
+    assert len(plan.launches) >= 2
+    assert all(len(l.prog.steps) <= 12 for l in plan.launches)
+    assert isinstance(plan.launches[0].out.obj, P._Temp)
+    assert torch.equal(got, _oracle(KL.make_long_chain, [a, b, c, out], 3))

@@ -24,6 +24,7 @@ Anything else raises NotImplementedError naming the unsupported pattern.
 
 from __future__ import annotations
 
+import dataclasses
 from dataclasses import dataclass, field
 from typing import Any, Dict, List, Optional, Sequence, Tuple
 
@@ -194,7 +195,31 @@ def _copy_table(events: List[T.Event], cb, n: int, kind: str, received=None) -> 
     return _CopyTable(tensor, r0, c0)
 
 
-class _Scratch:
+class _Temp:
+    """A device tensor the plan owns (allocated on first use, then kept with
+    the cached plan): the value of a subexpression split off a store whose
+    fused program exceeds the kernel's limits, in the output's coordinates."""
+
+    is_block_float = False
+
+    def __init__(self, shape: Tuple[int, int], dtype: torch.dtype) -> None:
+        self._shape = tuple(shape)
+        self.dtype = dtype
+        self._t: Optional[torch.Tensor] = None
+
+    @property
+    def shape(self) -> Tuple[int, int]:
+        return self._shape
+
+    @property
+    def _tensor(self) -> torch.Tensor:
+        if self._t is None or tuple(self._t.shape) != tuple(self.shape):
+            dev = "cuda" if torch.cuda.is_available() else "cpu"
+            self._t = torch.zeros(self.shape, dtype=self.dtype, device=dev)
+        return self._t
+
+
+class _Scratch(_Temp):
     """Device memory standing in for an intermediate CB: one the compute
     thread both stores into and waits on (test/python/test_intermediate_cb.py,
     the two-stage broadcast kernels of test/python/test_bcast_ops.py).  Every
@@ -202,8 +227,6 @@ class _Scratch:
     store that reads it, so the storing launch writes the block there and the
     reading launch finds it where an operand filled by ttl.copy from a tensor
     would be.  The two launches run in trace order (the store first)."""
-
-    is_block_float = False
 
     def __init__(self, cb):
         if not isinstance(cb.dtype, torch.dtype):
@@ -236,12 +259,6 @@ class _Scratch:
                             "overlap once laid out at the CB's block shape; an intermediate CB "
                             "needs one output block of the reading store per block")
 
-    @property
-    def _tensor(self) -> torch.Tensor:
-        if self._t is None or tuple(self._t.shape) != self.shape:
-            dev = "cuda" if torch.cuda.is_available() else "cpu"
-            self._t = torch.zeros(self.shape, dtype=self.dtype, device=dev)
-        return self._t
 
 
 def _intermediate_tables(threads, events, cbs, count, inter, fill, drain,
@@ -792,7 +809,7 @@ def build_plan(groups: List[_Group], tensor_ref) -> Plan:
     return plan
 
 
-def _plan_eltwise(g: _Group, out_rc, leaf_rc, tensor_ref) -> EltwiseLaunch:
+def _plan_eltwise(g: _Group, out_rc, leaf_rc, tensor_ref) -> List[EltwiseLaunch]:
     n = out_rc.shape[0]
     if _unique_tiles(out_rc) != n:
         if g.acc:
@@ -828,12 +845,73 @@ def _plan_eltwise(g: _Group, out_rc, leaf_rc, tensor_ref) -> EltwiseLaunch:
         leaf_nodes[id(lf)] = leaf
         specs[k] = OperandSpec(tensor_ref(tens), rm, cm, ro, co)
     e = _to_expr(g.tree, leaf_nodes)
-    prog = X.compile_expr(e)
-    operands = [specs[s.leaf.ref] if s.leaf is not None else None for s in prog.steps]
     y0, x0 = r0 * TILE, c0 * TILE
     h = min(r1 * TILE, H) - y0
     w = min(c1 * TILE, W) - x0
-    return EltwiseLaunch(prog, operands, tensor_ref(out_t), (y0, x0, h, w), n)
+    pre, prog, operands = _fit_program(e, specs, (H, W), (y0, x0, h, w), n)
+    return pre + [EltwiseLaunch(prog, operands, tensor_ref(out_t), (y0, x0, h, w), n)]
+
+
+def _expr_nodes(e: X.Expr, out: List[X.Expr]) -> List[X.Expr]:
+    out.append(e)
+    if isinstance(e, X.Unary):
+        _expr_nodes(e.x, out)
+    elif isinstance(e, X.Binary):
+        _expr_nodes(e.a, out)
+        _expr_nodes(e.b, out)
+    return out
+
+
+def _expr_replace(e: X.Expr, old: X.Expr, new: X.Expr) -> X.Expr:
+    if e is old:
+        return new
+    if isinstance(e, X.Unary):
+        x = _expr_replace(e.x, old, new)
+        return e if x is e.x else dataclasses.replace(e, x=x)
+    if isinstance(e, X.Binary):
+        a, b = _expr_replace(e.a, old, new), _expr_replace(e.b, old, new)
+        return e if (a is e.a and b is e.b) else dataclasses.replace(e, a=a, b=b)
+    return e
+
+
+def _program_size(e: X.Expr) -> int:
+    """Steps of e's program, or 0 when it exceeds the kernel's limits."""
+    try:
+        return len(X.compile_expr(e).steps)
+    except NotImplementedError as err:
+        if "fused tile expression needs" in str(err):
+            return 0
+        raise
+
+
+def _fit_program(e: X.Expr, specs: Dict[int, OperandSpec], out_shape, region, n_tiles):
+    """Compiles e.  When its fused program exceeds the kernel's step or stack
+    limit (test/python/many_fused_ops.py chains 20 ops), the largest proper
+    subexpression that fits is computed first, by a launch of its own into a
+    temporary tensor of the output's shape (in its dtype, so the value is
+    stored exactly), and read back as an operand; repeated until the rest
+    fits.  Returns (launches to run first, program, operands)."""
+    pre: List[EltwiseLaunch] = []
+    while _program_size(e) == 0:
+        best, size = None, 1
+        for node in _expr_nodes(e, [])[1:]:
+            if isinstance(node, (X.Leaf, X.Const)):
+                continue
+            k = _program_size(node)
+            if k > size:
+                best, size = node, k
+        if best is None:
+            X.compile_expr(e)  # raises the limit error
+        tmp = _Temp(out_shape, best.dtype)
+        sprog = X.compile_expr(best)
+        pre.append(EltwiseLaunch(sprog, [specs[st.leaf.ref] if st.leaf is not None else None
+                                         for st in sprog.steps], TensorRef(obj=tmp), region,
+                                 n_tiles))
+        k = max(specs) + 1 if specs else 0
+        specs[k] = OperandSpec(TensorRef(obj=tmp), -1, -1, 0, 0)
+        e = _expr_replace(e, best, X.Leaf(k, best.dtype))
+    prog = X.compile_expr(e)
+    return pre, prog, [specs[st.leaf.ref] if st.leaf is not None else None for st in prog.steps]
 
 
 def _plan_eltwise_parts(g: _Group, out_rc, leaf_rc, tensor_ref) -> List[EltwiseLaunch]:
@@ -845,7 +923,7 @@ def _plan_eltwise_parts(g: _Group, out_rc, leaf_rc, tensor_ref) -> List[EltwiseL
     must still write a rectangle of output tiles.  The split is along the
     axis whose map failed only."""
     try:
-        return [_plan_eltwise(g, out_rc, leaf_rc, tensor_ref)]
+        return _plan_eltwise(g, out_rc, leaf_rc, tensor_ref)
     except _NotAffine as err:
         k = err.leaf
         if k < 0:
