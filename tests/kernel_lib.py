@@ -1007,3 +1007,56 @@ def make_long_chain(ttl, g=2, grid=(2, 2)):
                         ttl.copy(o, out[r * g:(r + 1) * g, k * g:(k + 1) * g]).wait()
 
     return long_chain
+
+
+def make_softmax_rows(ttl, w=4, grid=(2, 2)):
+    """Row softmax the tt-lang way: per block of one tile row x w tiles,
+    m = reduce_max(x) -> e = exp(x - broadcast(m)) -> s = reduce_sum(e) ->
+    y = e * broadcast(recip(s)), every stage through an intermediate CB
+    (reductions fill column 0 of their result tile; the in-tile broadcast
+    spreads it)."""
+    @ttl.kernel(grid=grid)
+    def softmax_rows(x, scaler, out):
+        rows = out.shape[0] // TILE
+        ncores = grid[0] * grid[1]
+        per = -(-rows // ncores)
+        x_cb = ttl.make_circular_buffer_like(x, shape=(1, w), buffer_factor=2)
+        s_cb = ttl.make_circular_buffer_like(scaler, shape=(1, 1), buffer_factor=1)
+        m_cb = ttl.make_circular_buffer_like(x, shape=(1, 1), buffer_factor=2)
+        e_cb = ttl.make_circular_buffer_like(x, shape=(1, w), buffer_factor=2)
+        z_cb = ttl.make_circular_buffer_like(x, shape=(1, 1), buffer_factor=2)
+        o_cb = ttl.make_circular_buffer_like(out, shape=(1, w), buffer_factor=2)
+
+        @ttl.compute()
+        def comp():
+            c = ttl.core(dims=1)
+            with s_cb.wait() as sc:
+                for _ in range(c * per, min(rows, (c + 1) * per)):
+                    with x_cb.wait() as xb:
+                        with m_cb.reserve() as mb:
+                            mb.store(ttl.math.reduce_max(xb, sc, dims=[1]))
+                        with m_cb.wait() as mb, e_cb.reserve() as eb:
+                            eb.store(ttl.math.exp(xb - ttl.math.broadcast(mb, eb, dims=[1])))
+                    with e_cb.wait() as eb:
+                        with z_cb.reserve() as zb:
+                            zb.store(ttl.math.reduce_sum(eb, sc, dims=[1]))
+                        with z_cb.wait() as zb, o_cb.reserve() as ob:
+                            ob.store(eb * ttl.math.broadcast(ttl.math.recip(zb), ob, dims=[1]))
+
+        @ttl.datamovement()
+        def rd():
+            c = ttl.core(dims=1)
+            with s_cb.reserve() as sb:
+                ttl.copy(scaler[0, 0], sb).wait()
+            for r in range(c * per, min(rows, (c + 1) * per)):
+                with x_cb.reserve() as xb:
+                    ttl.copy(x[r, 0:w], xb).wait()
+
+        @ttl.datamovement()
+        def wr():
+            c = ttl.core(dims=1)
+            for r in range(c * per, min(rows, (c + 1) * per)):
+                with o_cb.wait() as ob:
+                    ttl.copy(ob, out[r, 0:w]).wait()
+
+    return softmax_rows

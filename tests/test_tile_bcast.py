@@ -166,3 +166,15 @@ def test_long_chain_split_through_temporaries():
     assert all(len(l.prog.steps) <= 12 for l in plan.launches)
     assert isinstance(plan.launches[0].out.obj, P._Temp)
     assert torch.equal(got, _oracle(KL.make_long_chain, [a, b, c, out], 3))
+
+
+def test_softmax_rows_through_intermediate_cbs():
+    x = O.seeded((256, 128), "uniform", 31, lo=-3, hi=3)
+    s = torch.full((32, 32), 1.0, dtype=torch.bfloat16)
+    out = torch.zeros(256, 128, dtype=torch.bfloat16)
+    got, plan = _plan_run(KL.make_softmax_rows, [x, s, out], 2)
+    assert [type(l).__name__ for l in plan.launches] == ["ReduceLaunch", "EltwiseLaunch",
+                                                         "ReduceLaunch", "EltwiseLaunch"]
+    assert torch.equal(got, _oracle(KL.make_softmax_rows, [x, s, out], 2))
+    # and it is a softmax: rows sum to 1, close to torch's
+    assert float((got.float() - torch.softmax(x.float(), 1)).abs().max()) < 2e-3

@@ -124,3 +124,19 @@ def test_long_chain_split_through_temporaries():
     ref = _oracle(KL.make_long_chain, [a, b, c, out], 3)
     d = O.bf16_ulp_diff(got, ref)
     assert float((d > 2).float().mean()) < 1e-3 and int(d.max()) <= 64
+
+
+def test_softmax_rows_through_intermediate_cbs():
+    # 1024 rows of 16 tiles: reduce -> broadcast -> exp -> reduce -> scale on
+    # the device, four launches through three scratch tensors
+    x = O.seeded((1024, 512), "uniform", 32, lo=-4, hi=4)
+    s = torch.full((32, 32), 1.0, dtype=torch.bfloat16)
+    out = torch.zeros(1024, 512, dtype=torch.bfloat16)
+    got, k = _gpu(KL.make_softmax_rows, [x, s, out], 2, w=16, grid=(4, 4))
+    assert len(k.last_plan.launches) == 4
+    ref = _oracle(KL.make_softmax_rows, [x, s, out], 2, w=16, grid=(4, 4))
+    # the row maxima are exact; exp and the fp32 row sums (summed in another
+    # order than the oracle's float64) may move a value by one bf16 ulp
+    d = O.bf16_ulp_diff(got, ref)
+    assert int(d.max()) <= 2 and float((d > 0).float().mean()) < 0.05
+    assert float((got.float() - torch.softmax(x.float(), 1)).abs().max()) < 2e-3
