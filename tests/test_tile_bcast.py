@@ -115,10 +115,36 @@ def test_two_stage_intermediate_cb():
     y = O.seeded((256, 128), "uniform", 8, lo=-2, hi=2)
     out = torch.zeros(256, 128, dtype=torch.bfloat16)
     got, plan = _plan_run(KL.make_two_stage, [x, y, out], 2)
-    assert len(plan.launches) == 2  # stage 1 into the scratch tensor, then stage 2
-    scratch = plan.launches[0].out.obj
-    assert isinstance(scratch, P._Scratch) and scratch.shape == (256, 128)
+    # stage 1 (elementwise, bf16 into a bf16 CB) is inlined into stage 2: one
+    # launch reading x and y, no scratch round trip
+    (l,) = plan.launches
+    assert not any(isinstance(s.ref.obj, P._Temp) for s in l.operands if s is not None)
     assert torch.equal(got, _oracle(KL.make_two_stage, [x, y, out], 2))
+
+
+def test_compose_axis_matches_brute_force():
+    # ((c & mb) + ob) & ma) + oa == (c & m) + o for every mask pair
+    masks = [-1, 31, 0, ~31]
+    c = torch.arange(0, 512)
+    for mb in masks:
+        for ma in masks:
+            for ob in (0, 64):
+                for oa in (0, 96):
+                    m, o = P._compose_axis(mb, ob, ma, oa)
+                    s = (c & mb) + ob
+                    assert torch.equal((s & ma) + oa, (c & m) + o), (mb, ob, ma, oa)
+
+
+def test_intermediate_stage_kept_when_read_by_matmul_or_reduced():
+    # softmax: the reduce stages still go through scratch tensors, the
+    # elementwise exp stage is inlined into both of its readers
+    x = O.seeded((128, 128), "uniform", 33, lo=-3, hi=3)
+    s = torch.full((32, 32), 1.0, dtype=torch.bfloat16)
+    _, plan = _plan_run(KL.make_softmax_rows, [x, s, torch.zeros(128, 128, dtype=torch.bfloat16)],
+                        2)
+    kinds = [type(l).__name__ for l in plan.launches]
+    assert kinds == ["ReduceLaunch", "ReduceLaunch", "EltwiseLaunch"]
+    assert isinstance(plan.launches[0].out.obj, P._Scratch)
 
 
 def test_held_tile_split_into_parts():
@@ -173,8 +199,8 @@ def test_softmax_rows_through_intermediate_cbs():
     s = torch.full((32, 32), 1.0, dtype=torch.bfloat16)
     out = torch.zeros(256, 128, dtype=torch.bfloat16)
     got, plan = _plan_run(KL.make_softmax_rows, [x, s, out], 2)
-    assert [type(l).__name__ for l in plan.launches] == ["ReduceLaunch", "EltwiseLaunch",
-                                                         "ReduceLaunch", "EltwiseLaunch"]
+    assert [type(l).__name__ for l in plan.launches] == ["ReduceLaunch", "ReduceLaunch",
+                                                         "EltwiseLaunch"]
     assert torch.equal(got, _oracle(KL.make_softmax_rows, [x, s, out], 2))
     # and it is a softmax: rows sum to 1, close to torch's
     assert float((got.float() - torch.softmax(x.float(), 1)).abs().max()) < 2e-3

@@ -787,29 +787,141 @@ def _has(tree, tag) -> bool:
     return any(_has(t, tag) for t in tree[1:] if isinstance(t, tuple))
 
 
+def _compose_axis(mb: int, ob: int, ma: int, oa: int) -> Tuple[int, int]:
+    """(mask, offset) of c -> (((c & mb) + ob) & ma) + oa, for masks in
+    {-1, 31, 0, ~31} and offsets that are multiples of 32."""
+    if mb == -1:
+        return ma, oa + (ob if ma in (-1, ~31) else 0)
+    if mb == ~31:
+        return (~31, ob + oa) if ma in (-1, ~31) else (0, oa)
+    if mb == 31:
+        if ma == -1:
+            return 31, ob + oa
+        if ma == ~31:
+            return 0, ob + oa
+        return ma, oa
+    return 0, oa + (ob if ma in (-1, ~31) else 0)
+
+
+class _Inliner:
+    """Elementwise stages into intermediate CBs, inlined into their readers:
+    a scratch tensor written by one plain elementwise launch (no acc, its
+    value's dtype = the CB's, so the store rounds nothing) is replaced in
+    every reading program by the writer's expression, operand maps composed
+    (_compose_axis); when every reader took it, the writer's launch is
+    dropped and the intermediate never touches HBM."""
+
+    def __init__(self, groups: List[_Group]) -> None:
+        self.writers: Dict[int, int] = {}
+        for g in groups:
+            if isinstance(g.out_tensor, _Scratch):
+                self.writers[id(g.out_tensor)] = self.writers.get(id(g.out_tensor), 0) + 1
+        self.exprs: Dict[int, Tuple[X.Expr, Dict[int, OperandSpec], Any]] = {}
+        self.reads: Dict[int, List[bool]] = {}
+
+    def register(self, g: _Group, launch) -> None:
+        out = g.out_tensor
+        e = getattr(launch, "_expr", None)
+        if (isinstance(out, _Scratch) and not g.acc and self.writers.get(id(out)) == 1
+                and e is not None and e.dtype == out.dtype):
+            self.exprs[id(out)] = (e, launch._specs, launch)
+
+    def substitute(self, tens, rspec: OperandSpec, specs: Dict[int, OperandSpec]):
+        """The writer's expression for a read of `tens` through rspec (new
+        leaves added to specs), or None."""
+        if id(tens) not in self.exprs:
+            return None
+        e, wspecs, _ = self.exprs[id(tens)]
+        memo: Dict[int, X.Expr] = {}
+
+        def remap(n):
+            if isinstance(n, X.Leaf):
+                if id(n) not in memo:
+                    ws = wspecs[n.ref]
+                    rm, ro = _compose_axis(rspec.row_mask, rspec.row_off, ws.row_mask, ws.row_off)
+                    cm, co = _compose_axis(rspec.col_mask, rspec.col_off, ws.col_mask, ws.col_off)
+                    k = max(specs) + 1 if specs else 0
+                    specs[k] = OperandSpec(ws.ref, rm, cm, ro, co)
+                    memo[id(n)] = X.Leaf(k, n.dtype)
+                return memo[id(n)]
+            if isinstance(n, X.Unary):
+                return dataclasses.replace(n, x=remap(n.x))
+            if isinstance(n, X.Binary):
+                return dataclasses.replace(n, a=remap(n.a), b=remap(n.b))
+            return n
+        return remap(e)
+
+    def note_read(self, tens, inlined: bool) -> None:
+        if isinstance(tens, _Scratch):
+            self.reads.setdefault(id(tens), []).append(inlined)
+
+    def finish(self, plan: "Plan") -> None:
+        drop = {id(l) for sid, (_, _, l) in self.exprs.items()
+                if self.reads.get(sid) and all(self.reads[sid])}
+        plan.launches = [l for l in plan.launches if id(l) not in drop]
+
+
+def _leaf_operands(g: _Group, it_rc, leaf_rc, tensor_ref, inl: Optional[_Inliner]):
+    """Operand specs and expression nodes of a group's leaves over iteration
+    tiles it_rc, with intermediate stages inlined where inl allows.  Returns
+    (specs, leaf_nodes, plain_nodes): plain_nodes maps every leaf to its own
+    operand (the fallback when the inlined program does not fit)."""
+    specs: Dict[int, OperandSpec] = {}
+    plain: Dict[int, X.Expr] = {}
+    for k, lf in enumerate(g.leaf_blocks):
+        tens = g.leaf_tensors[k]
+        h, w = tens.shape
+        rr, cr = _leaf_rep(lf)
+        try:
+            axis = 0
+            rm, ro = _axis_map(it_rc[:, 0], leaf_rc[k][:, 0], h, rr)
+            axis = 1
+            cm, co = _axis_map(it_rc[:, 1], leaf_rc[k][:, 1], w, cr)
+        except _NotAffine as err:
+            err.leaf, err.axis = k, axis
+            raise
+        specs[k] = OperandSpec(tensor_ref(tens), rm, cm, ro, co)
+        plain[id(lf)] = X.Leaf(k, lf[1].cb.dtype)
+    nodes = dict(plain)
+    if inl is not None:
+        for k, lf in enumerate(g.leaf_blocks):
+            sub = inl.substitute(g.leaf_tensors[k], specs[k], specs)
+            if sub is not None:
+                nodes[id(lf)] = sub
+    return specs, nodes, plain
+
+
 def build_plan(groups: List[_Group], tensor_ref) -> Plan:
     plan = Plan()
+    inl = _Inliner(groups)
     for g in groups:
         out_rc = np.concatenate(g.out_rc, 0)
         leaf_rc = [np.concatenate([li[k] for li in g.leaf_rc], 0) for k in range(len(g.leaf_blocks))]
         if g.tree[0] == "reduce":
-            launch = _plan_reduce(g, out_rc, leaf_rc, np.concatenate(g.order), tensor_ref)
+            launch = _plan_reduce(g, out_rc, leaf_rc, np.concatenate(g.order), tensor_ref, inl)
         elif g.tree[0] == "matmul" and g.tree[1][0] == "leaf" and g.tree[2][0] == "leaf":
             launch = _plan_matmul(g, out_rc, leaf_rc, tensor_ref)
+            for t in g.leaf_tensors:
+                inl.note_read(t, False)
         elif _has(g.tree, "matmul"):
             raise PlanError("a tile matmul combined with other ops in one store() is not "
                             "supported; store the product on its own")
         else:
-            for launch in _plan_eltwise_parts(g, out_rc, leaf_rc, tensor_ref):
+            launches = _plan_eltwise_parts(g, out_rc, leaf_rc, tensor_ref, inl)
+            for launch in launches:
                 launch.loc = g.loc
                 plan.launches.append(launch)
+            if len(launches) == 1:
+                inl.register(g, launches[0])
             continue
         launch.loc = g.loc
         plan.launches.append(launch)
+    inl.finish(plan)
     return plan
 
 
-def _plan_eltwise(g: _Group, out_rc, leaf_rc, tensor_ref) -> List[EltwiseLaunch]:
+def _plan_eltwise(g: _Group, out_rc, leaf_rc, tensor_ref,
+                  inl: Optional["_Inliner"] = None) -> List[EltwiseLaunch]:
     n = out_rc.shape[0]
     if _unique_tiles(out_rc) != n:
         if g.acc:
@@ -821,35 +933,29 @@ def _plan_eltwise(g: _Group, out_rc, leaf_rc, tensor_ref) -> List[EltwiseLaunch]
         raise PlanError("the stored output tiles do not form a rectangle of the output tensor")
     out_t = g.out_tensor
     H, W = out_t.shape
-    leaf_nodes: Dict[int, X.Leaf] = {}
-    specs: Dict[int, OperandSpec] = {}
     if getattr(out_t, "is_block_float", False):
         raise PlanError(f"storing into a {out_t.dtype.name} tensor is not supported (block-float "
                         "tensors are read-only tile-matmul weights here)")
-    for k, lf in enumerate(g.leaf_blocks):
-        tens = g.leaf_tensors[k]
+    for tens in g.leaf_tensors:
         if getattr(tens, "is_block_float", False):
             raise PlanError(f"a {tens.dtype.name} tensor as an elementwise operand is not "
                             "supported; it can be the B operand of a tile matmul")
-        h, w = tens.shape
-        rr, cr = _leaf_rep(lf)
-        try:
-            axis = 0
-            rm, ro = _axis_map(out_rc[:, 0], leaf_rc[k][:, 0], h, rr)
-            axis = 1
-            cm, co = _axis_map(out_rc[:, 1], leaf_rc[k][:, 1], w, cr)
-        except _NotAffine as err:
-            err.leaf, err.axis = k, axis
-            raise
-        leaf = X.Leaf(k, lf[1].cb.dtype)
-        leaf_nodes[id(lf)] = leaf
-        specs[k] = OperandSpec(tensor_ref(tens), rm, cm, ro, co)
-    e = _to_expr(g.tree, leaf_nodes)
+    specs, nodes, plain = _leaf_operands(g, out_rc, leaf_rc, tensor_ref, inl)
+    e = _to_expr(g.tree, nodes)
+    inlined = nodes != plain
+    if inlined and _program_size(e) == 0:  # the fused program does not fit: keep the stage
+        e, inlined = _to_expr(g.tree, plain), False
+    if inl is not None:
+        for tens in g.leaf_tensors:
+            inl.note_read(tens, inlined and id(tens) in inl.exprs)
     y0, x0 = r0 * TILE, c0 * TILE
     h = min(r1 * TILE, H) - y0
     w = min(c1 * TILE, W) - x0
     pre, prog, operands = _fit_program(e, specs, (H, W), (y0, x0, h, w), n)
-    return pre + [EltwiseLaunch(prog, operands, tensor_ref(out_t), (y0, x0, h, w), n)]
+    launch = EltwiseLaunch(prog, operands, tensor_ref(out_t), (y0, x0, h, w), n)
+    if not pre:
+        launch._expr, launch._specs = e, dict(specs)
+    return pre + [launch]
 
 
 def _expr_nodes(e: X.Expr, out: List[X.Expr]) -> List[X.Expr]:
@@ -914,7 +1020,8 @@ def _fit_program(e: X.Expr, specs: Dict[int, OperandSpec], out_shape, region, n_
     return pre, prog, [specs[st.leaf.ref] if st.leaf is not None else None for st in prog.steps]
 
 
-def _plan_eltwise_parts(g: _Group, out_rc, leaf_rc, tensor_ref) -> List[EltwiseLaunch]:
+def _plan_eltwise_parts(g: _Group, out_rc, leaf_rc, tensor_ref,
+                        inl: Optional["_Inliner"] = None) -> List[EltwiseLaunch]:
     """One launch when every operand is an affine image of the output tiles;
     otherwise the store's instances are split by the tile of the first
     operand that is not (that operand is then one fixed tile in each part)
@@ -923,7 +1030,7 @@ def _plan_eltwise_parts(g: _Group, out_rc, leaf_rc, tensor_ref) -> List[EltwiseL
     must still write a rectangle of output tiles.  The split is along the
     axis whose map failed only."""
     try:
-        return _plan_eltwise(g, out_rc, leaf_rc, tensor_ref)
+        return _plan_eltwise(g, out_rc, leaf_rc, tensor_ref, inl)
     except _NotAffine as err:
         k = err.leaf
         if k < 0:
@@ -934,14 +1041,15 @@ def _plan_eltwise_parts(g: _Group, out_rc, leaf_rc, tensor_ref) -> List[EltwiseL
         out: List[EltwiseLaunch] = []
         for u in range(uniq.size):
             sel = inv == u
-            out += _plan_eltwise_parts(g, out_rc[sel], [x[sel] for x in leaf_rc], tensor_ref)
+            out += _plan_eltwise_parts(g, out_rc[sel], [x[sel] for x in leaf_rc], tensor_ref)  # no inlining in parts
             if len(out) > _MAX_PARTS:
                 raise PlanError(f"a store site needs more than {_MAX_PARTS} launches: its "
                                 "operands' tiles follow the output tiles in no affine way") from err
         return out
 
 
-def _plan_reduce(g: _Group, out_rc, leaf_rc, order, tensor_ref) -> ReduceLaunch:
+def _plan_reduce(g: _Group, out_rc, leaf_rc, order, tensor_ref,
+                 inl: Optional["_Inliner"] = None) -> ReduceLaunch:
     """Iteration space: output tile coordinates along the kept axes, the tile
     coordinates of the first operand that varies along a reduced axis there.
     Every operand must be an affine image of it (as for eltwise), every
@@ -995,18 +1103,15 @@ def _plan_reduce(g: _Group, out_rc, leaf_rc, order, tensor_ref) -> ReduceLaunch:
         raise PlanError("reduce_max partial results accumulated with store(acc=True) would be "
                         "added (store acc semantics); reduce over one block per output tile")
     # operands
-    leaf_nodes: Dict[int, X.Leaf] = {}
-    specs: Dict[int, OperandSpec] = {}
-    for k, lf in enumerate(g.leaf_blocks):
-        tens = g.leaf_tensors[k]
-        h, w = tens.shape
-        rr, cr = _leaf_rep(lf)
-        rm, ro = _axis_map(it[:, 0], leaf_rc[k][:, 0], h, rr)
-        cm, co = _axis_map(it[:, 1], leaf_rc[k][:, 1], w, cr)
-        leaf = X.Leaf(k, lf[1].cb.dtype)
-        leaf_nodes[id(lf)] = leaf
-        specs[k] = OperandSpec(tensor_ref(tens), rm, cm, ro, co)
-    prog = X.compile_expr(_to_expr(inner, leaf_nodes))
+    specs, nodes, plain = _leaf_operands(g, it, leaf_rc, tensor_ref, inl)
+    e = _to_expr(inner, nodes)
+    inlined = nodes != plain
+    if inlined and _program_size(e) == 0:
+        e, inlined = _to_expr(inner, plain), False
+    if inl is not None:
+        for tens in g.leaf_tensors:
+            inl.note_read(tens, inlined and id(tens) in inl.exprs)
+    prog = X.compile_expr(e)
     operands = [specs[s.leaf.ref] if s.leaf is not None else None for s in prog.steps]
     y0, x0 = r0 * TILE, c0 * TILE
     h = 1 if degenerate[0] else (r1 - r0) * TILE
