@@ -94,3 +94,35 @@ def test_reference_compile_script_runs(name, tmp_path):
     r = subprocess.run(cmd, cwd=tmp_path, env=_env(), capture_output=True, text=True,
                        timeout=600)
     assert r.returncode == 0, r.stdout[-3000:] + r.stderr[-2000:]
+
+
+EXAMPLES = "/root/reference/examples"
+
+
+def _run_example(name, tmp_path):
+    cmd = [sys.executable, os.path.join(HERE, "refsuite_plugin.py"), os.path.join(EXAMPLES, name)]
+    return subprocess.run(cmd, cwd=tmp_path, env=_env(), capture_output=True, text=True,
+                          timeout=600)
+
+
+@needs_ref
+def test_reference_broadcast_demo(tmp_path):
+    r = _run_example("broadcast_demo.py", tmp_path)
+    assert r.returncode == 0 and "Result matches expected output" in r.stdout, r.stderr[-2000:]
+
+
+@needs_ref
+def test_reference_error_examples(tmp_path):
+    # the simulator's errors for the reference's two broken examples
+    # (test/sim/test_examples.py:125-193): the copy lock error (not a
+    # deadlock: the failing thread reaches its error before anything blocks)
+    # and the block / slice shape mismatch with its source line
+    r = _run_example("copy_lock_error.py", tmp_path)
+    assert r.returncode != 0
+    assert "locked as copy destination until tx.wait() completes (copy lock error)" in r.stderr
+    assert "Deadlock" not in r.stderr
+    r = _run_example("eltwise_add_error.py", tmp_path)
+    assert r.returncode != 0
+    assert ("Tensor shape (32, 32) (=(1, 1) tiles) does not match Block shape (2, 2) tiles"
+            in r.stderr)
+    assert 'eltwise_add_error.py", line 37' in r.stderr

@@ -780,8 +780,12 @@ def _check_slice_shape(s: TensorSlice, blk: Block) -> None:
         raise ValueError(f"Tensor must be 2-dimensional, got shape {s.tensor.shape}")
     tiles = s.shape_in_tiles()
     if tiles != tuple(blk.shape):
-        raise ValueError(f"Tensor shape {tuple(s.tensor.shape)} slice (={tiles} tiles) does not "
-                         f"match Block shape {tuple(blk.shape)} tiles")
+        h, w = s.tensor.shape
+        elems = (1 if h == 1 else tiles[0] * TILE_SHAPE[0], 1 if w == 1 else tiles[1] * TILE_SHAPE[1])
+        # the simulator's wording (the slice's element shape), which the
+        # reference's tests match (test/sim/test_examples.py:134-145)
+        raise ValueError(f"Tensor shape {elems} (={tiles} tiles) does not match Block shape "
+                         f"{tuple(blk.shape)} tiles")
     s.check_bounds()
 
 

@@ -190,6 +190,7 @@ class KernelRunner:
     def _trace_thread(self, t: dsl.ThreadTemplate, core: int):
         fn = t.rewritten()
         fn.__globals__["print"] = _trace_print
+        first_err = None
         for scalar in (False, True):
             ctx = T.TraceContext(core, self.grid, t, scalar=scalar)
             prev = T._ctx
@@ -201,10 +202,19 @@ class KernelRunner:
                     raise
                 continue
             except Exception as e:
+                if not scalar:
+                    # a vectorised trace holds every iteration of the loops
+                    # around the error; trace again with scalar loops so the
+                    # operations before it are those of the simulator's run,
+                    # which stops in the first iteration that fails
+                    first_err = e
+                    continue
                 e._ttlh_partial_root = ctx.root  # the operations traced up to the error
                 raise
             finally:
                 T._ctx = prev
+            if first_err is not None:  # the scalar run got through: keep the first error
+                raise first_err
             if ctx.pending_reserve or ctx.pending_wait:
                 err = RuntimeError(f"thread {t.__name__} on core {core} ended with a reserved or "
                                    "waited block that was never pushed / popped")
