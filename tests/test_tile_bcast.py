@@ -204,3 +204,18 @@ def test_softmax_rows_through_intermediate_cbs():
     assert torch.equal(got, _oracle(KL.make_softmax_rows, [x, s, out], 2))
     # and it is a softmax: rows sum to 1, close to torch's
     assert float((got.float() - torch.softmax(x.float(), 1)).abs().max()) < 2e-3
+
+
+def test_inliner_keeps_stage_read_by_split_store():
+    # a scratch read by a store site that has to be split into parts keeps its
+    # writer's launch (the parts read the scratch itself)
+    sc = P._Scratch.__new__(P._Scratch)
+    inl = P._Inliner([])
+    inl.exprs[id(sc)] = (None, {}, object())
+    inl.note_read(sc, True)
+    inl.note_read(sc, False)
+    plan = P.Plan()
+    writer = inl.exprs[id(sc)][2]
+    plan.launches = [writer]
+    inl.finish(plan)
+    assert plan.launches == [writer]

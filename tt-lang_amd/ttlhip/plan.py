@@ -1035,6 +1035,9 @@ def _plan_eltwise_parts(g: _Group, out_rc, leaf_rc, tensor_ref,
         k = err.leaf
         if k < 0:
             raise
+        if inl is not None:  # the parts read their operands as they are
+            for t in g.leaf_tensors:
+                inl.note_read(t, False)
         uniq, inv = np.unique(leaf_rc[k][:, err.axis], return_inverse=True)
         if uniq.size > _MAX_PARTS or uniq.size == 1:
             raise
