@@ -240,3 +240,39 @@ def test_chain_exp_special_values():
     both_nan = torch.isnan(got) & torch.isnan(ref)
     ulp = O.bf16_ulp_diff(got, ref)
     assert bool(((ulp <= 1) | both_nan).all()), got[~((ulp <= 1) | both_nan)]
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_flat_path_region_rows_and_matrix_row_vector(out_dtype):
+    # whole-row regions of bf16 operands take the 1-D flat kernel: a region
+    # starting below row 0 of the output, an operand addressed with a row
+    # offset, a row vector that is one row (row 5) of a matrix, a flat operand
+    # read through a larger tensor's leading rows
+    a = _u((128, 256), 90)
+    m = _u((16, 256), 91)
+    c = _u((160, 256), 92)
+    env = {"a": a, "m": m, "c": c}
+    maps = {"a": {"row_off": -32}, "m": {"row_mask": 0, "row_off": 5}, "c": {"row_off": -32}}
+    e = ("mul", ("exp", ("add", ("leaf", "a"), ("leaf", "m"))), ("leaf", "c"))
+    got = run_gpu(e, env, maps, (192, 256), out_dtype, region=(32, 0, 128, 256))
+    ref = O.eval_expr(e, {"a": a, "m": m[5:6], "c": c[:128]})
+    ulp = O.bf16_ulp_diff(got[32:160].bfloat16(), ref.bfloat16())
+    assert int(ulp.max()) <= 1
+    assert (got[:32] == 7.0).all() and (got[160:] == 7.0).all()
+    e2 = ("sub", ("add", ("leaf", "m"), ("leaf", "a")), ("const", 0.5))
+    got = run_gpu(e2, env, maps, (192, 256), out_dtype, region=(32, 0, 128, 256))
+    assert_bitexact(got[32:160], O.eval_expr(e2, {"a": a, "m": m[5:6]}).to(out_dtype))
+
+
+@pytest.mark.parametrize("w", [8, 64, 2048, 8192])
+def test_flat_path_widths(w):
+    # power-of-two row widths (row vectors allowed) and the C1 add shape class
+    h = max(1, 65536 // w) + 3
+    a, b = _u((h, w), 93), _u((h, w), 94)
+    r = _u((1, w), 95)
+    env = {"a": a, "b": b, "r": r}
+    for e in (("add", ("leaf", "a"), ("leaf", "b")),
+              ("add", ("mul", ("leaf", "a"), ("leaf", "r")), ("leaf", "b")),
+              ("neg", ("leaf", "a"))):
+        got = run_gpu(e, env, {}, (h, w), torch.bfloat16)
+        assert_bitexact(got, O.eval_expr(e, env))

@@ -75,8 +75,16 @@ class KernelRunner:
             return ("id", id(v))
 
     def _cache_key(self, args, kwargs):
+        # The plan binds every tensor to the first argument position holding
+        # it, so which positions hold the same object is part of the key:
+        # k(a, a, out) and k(a, b, out) must not share a plan.
+        first: Dict[int, Any] = {}
+        alias = []
+        for p, v in list(enumerate(args)) + sorted(kwargs.items()):
+            alias.append(first.setdefault(id(v), p))
         return (tuple(self._key_of(a) for a in args),
-                tuple(sorted((k, self._key_of(v)) for k, v in kwargs.items())))
+                tuple(sorted((k, self._key_of(v)) for k, v in kwargs.items())),
+                tuple(alias))
 
     @staticmethod
     def _check_layouts(args, kwargs) -> None:
