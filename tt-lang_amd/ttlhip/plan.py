@@ -809,7 +809,13 @@ class _Inliner:
     value's dtype = the CB's, so the store rounds nothing) is replaced in
     every reading program by the writer's expression, operand maps composed
     (_compose_axis); when every reader took it, the writer's launch is
-    dropped and the intermediate never touches HBM."""
+    dropped and the intermediate never touches HBM.
+
+    Inlining moves the stage's operand reads to its reader's launch, so a
+    stage stops being inlinable once a later store writes a tensor it reads
+    (the reader would see the new values), and a reader that itself writes
+    such a tensor does not take it (its lanes would read elements other
+    lanes of the same launch overwrite)."""
 
     def __init__(self, groups: List[_Group]) -> None:
         self.writers: Dict[int, int] = {}
@@ -817,19 +823,33 @@ class _Inliner:
             if isinstance(g.out_tensor, _Scratch):
                 self.writers[id(g.out_tensor)] = self.writers.get(id(g.out_tensor), 0) + 1
         self.exprs: Dict[int, Tuple[X.Expr, Dict[int, OperandSpec], Any]] = {}
+        # scratch id -> ids of the tensors its inlined expression reads
+        self.sources: Dict[int, set] = {}
         self.reads: Dict[int, List[bool]] = {}
 
-    def register(self, g: _Group, launch) -> None:
+    def register(self, g: _Group, launch, subbed=()) -> None:
         out = g.out_tensor
         e = getattr(launch, "_expr", None)
         if (isinstance(out, _Scratch) and not g.acc and self.writers.get(id(out)) == 1
                 and e is not None and e.dtype == out.dtype):
+            src = {id(t) for t in g.leaf_tensors}
+            for t in subbed:  # stages this one inlined: their operands too
+                src |= self.sources.get(t, set())
             self.exprs[id(out)] = (e, launch._specs, launch)
+            self.sources[id(out)] = src
 
-    def substitute(self, tens, rspec: OperandSpec, specs: Dict[int, OperandSpec]):
+    def note_write(self, tens) -> None:
+        """A store into `tens` ran: stages reading it can no longer be inlined
+        into later readers (their launches stay, in trace order)."""
+        for sid in [s for s, src in self.sources.items() if id(tens) in src and s in self.exprs]:
+            del self.exprs[sid]
+
+    def substitute(self, tens, rspec: OperandSpec, specs: Dict[int, OperandSpec], out=None):
         """The writer's expression for a read of `tens` through rspec (new
-        leaves added to specs), or None."""
+        leaves added to specs), or None.  `out` is the reader's output."""
         if id(tens) not in self.exprs:
+            return None
+        if out is not None and id(out) in self.sources[id(tens)]:
             return None
         e, wspecs, _ = self.exprs[id(tens)]
         memo: Dict[int, X.Expr] = {}
@@ -855,6 +875,12 @@ class _Inliner:
         if isinstance(tens, _Scratch):
             self.reads.setdefault(id(tens), []).append(inlined)
 
+    def note_reads(self, tensors, subbed=()) -> None:
+        """Reads of a launch's operand tensors; `subbed` = ids of those it
+        inlined."""
+        for t in tensors:
+            self.note_read(t, id(t) in subbed)
+
     def finish(self, plan: "Plan") -> None:
         drop = {id(l) for sid, (_, _, l) in self.exprs.items()
                 if self.reads.get(sid) and all(self.reads[sid])}
@@ -864,8 +890,9 @@ class _Inliner:
 def _leaf_operands(g: _Group, it_rc, leaf_rc, tensor_ref, inl: Optional[_Inliner]):
     """Operand specs and expression nodes of a group's leaves over iteration
     tiles it_rc, with intermediate stages inlined where inl allows.  Returns
-    (specs, leaf_nodes, plain_nodes): plain_nodes maps every leaf to its own
-    operand (the fallback when the inlined program does not fit)."""
+    (specs, leaf_nodes, plain_nodes, subbed): plain_nodes maps every leaf to
+    its own operand (the fallback when the inlined program does not fit),
+    subbed holds the ids of the tensors whose stage was inlined."""
     specs: Dict[int, OperandSpec] = {}
     plain: Dict[int, X.Expr] = {}
     for k, lf in enumerate(g.leaf_blocks):
@@ -883,12 +910,14 @@ def _leaf_operands(g: _Group, it_rc, leaf_rc, tensor_ref, inl: Optional[_Inliner
         specs[k] = OperandSpec(tensor_ref(tens), rm, cm, ro, co)
         plain[id(lf)] = X.Leaf(k, lf[1].cb.dtype)
     nodes = dict(plain)
+    subbed = set()
     if inl is not None:
         for k, lf in enumerate(g.leaf_blocks):
-            sub = inl.substitute(g.leaf_tensors[k], specs[k], specs)
+            sub = inl.substitute(g.leaf_tensors[k], specs[k], specs, out=g.out_tensor)
             if sub is not None:
                 nodes[id(lf)] = sub
-    return specs, nodes, plain
+                subbed.add(id(g.leaf_tensors[k]))
+    return specs, nodes, plain, subbed
 
 
 def build_plan(groups: List[_Group], tensor_ref) -> Plan:
@@ -901,8 +930,7 @@ def build_plan(groups: List[_Group], tensor_ref) -> Plan:
             launch = _plan_reduce(g, out_rc, leaf_rc, np.concatenate(g.order), tensor_ref, inl)
         elif g.tree[0] == "matmul" and g.tree[1][0] == "leaf" and g.tree[2][0] == "leaf":
             launch = _plan_matmul(g, out_rc, leaf_rc, tensor_ref)
-            for t in g.leaf_tensors:
-                inl.note_read(t, False)
+            inl.note_reads(g.leaf_tensors)
         elif _has(g.tree, "matmul"):
             raise PlanError("a tile matmul combined with other ops in one store() is not "
                             "supported; store the product on its own")
@@ -912,10 +940,12 @@ def build_plan(groups: List[_Group], tensor_ref) -> Plan:
                 launch.loc = g.loc
                 plan.launches.append(launch)
             if len(launches) == 1:
-                inl.register(g, launches[0])
+                inl.register(g, launches[0], getattr(launches[0], "_subbed", ()))
+            inl.note_write(g.out_tensor)
             continue
         launch.loc = g.loc
         plan.launches.append(launch)
+        inl.note_write(g.out_tensor)
     inl.finish(plan)
     return plan
 
@@ -940,21 +970,19 @@ def _plan_eltwise(g: _Group, out_rc, leaf_rc, tensor_ref,
         if getattr(tens, "is_block_float", False):
             raise PlanError(f"a {tens.dtype.name} tensor as an elementwise operand is not "
                             "supported; it can be the B operand of a tile matmul")
-    specs, nodes, plain = _leaf_operands(g, out_rc, leaf_rc, tensor_ref, inl)
+    specs, nodes, plain, subbed = _leaf_operands(g, out_rc, leaf_rc, tensor_ref, inl)
     e = _to_expr(g.tree, nodes)
-    inlined = nodes != plain
-    if inlined and _program_size(e) == 0:  # the fused program does not fit: keep the stage
-        e, inlined = _to_expr(g.tree, plain), False
+    if subbed and _program_size(e) == 0:  # the fused program does not fit: keep the stage
+        e, subbed = _to_expr(g.tree, plain), set()
     if inl is not None:
-        for tens in g.leaf_tensors:
-            inl.note_read(tens, inlined and id(tens) in inl.exprs)
+        inl.note_reads(g.leaf_tensors, subbed)
     y0, x0 = r0 * TILE, c0 * TILE
     h = min(r1 * TILE, H) - y0
     w = min(c1 * TILE, W) - x0
     pre, prog, operands = _fit_program(e, specs, (H, W), (y0, x0, h, w), n)
     launch = EltwiseLaunch(prog, operands, tensor_ref(out_t), (y0, x0, h, w), n)
     if not pre:
-        launch._expr, launch._specs = e, dict(specs)
+        launch._expr, launch._specs, launch._subbed = e, dict(specs), subbed
     return pre + [launch]
 
 
@@ -1036,8 +1064,7 @@ def _plan_eltwise_parts(g: _Group, out_rc, leaf_rc, tensor_ref,
         if k < 0:
             raise
         if inl is not None:  # the parts read their operands as they are
-            for t in g.leaf_tensors:
-                inl.note_read(t, False)
+            inl.note_reads(g.leaf_tensors)
         uniq, inv = np.unique(leaf_rc[k][:, err.axis], return_inverse=True)
         if uniq.size > _MAX_PARTS or uniq.size == 1:
             raise
@@ -1106,14 +1133,14 @@ def _plan_reduce(g: _Group, out_rc, leaf_rc, order, tensor_ref,
         raise PlanError("reduce_max partial results accumulated with store(acc=True) would be "
                         "added (store acc semantics); reduce over one block per output tile")
     # operands
-    specs, nodes, plain = _leaf_operands(g, it, leaf_rc, tensor_ref, inl)
+    specs, nodes, plain, subbed = _leaf_operands(g, it, leaf_rc, tensor_ref, inl)
     e = _to_expr(inner, nodes)
-    inlined = nodes != plain
-    if inlined and _program_size(e) == 0:
-        e, inlined = _to_expr(inner, plain), False
+    if subbed and _program_size(e) == 0:
+        e, subbed = _to_expr(inner, plain), set()
     if inl is not None:
-        for tens in g.leaf_tensors:
-            inl.note_read(tens, inlined and id(tens) in inl.exprs)
+        inl.note_reads(g.leaf_tensors, subbed)
+        if g.scaler_tensor is not None:  # the scaler is read as it is
+            inl.note_read(g.scaler_tensor, False)
     prog = X.compile_expr(e)
     operands = [specs[s.leaf.ref] if s.leaf is not None else None for s in prog.steps]
     y0, x0 = r0 * TILE, c0 * TILE
