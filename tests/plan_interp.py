@@ -125,6 +125,32 @@ def run_matmul(l: MatmulLaunch, args):
     c[r0:r1, c0:c1] = (a[r0:r1].double() @ b[:, c0:c1].double()).to(c.dtype)
 
 
+class _MapRef:
+    def __init__(self, t):
+        self.t = t
+
+    def resolve(self, args):
+        return self.t
+
+
+class _MapSpec:
+    """An OperandMap (kernels.OperandMap) in a launch operand's shape."""
+
+    def __init__(self, m):
+        self.ref = _MapRef(m.tensor)
+        self.row_mask, self.col_mask = m.row_mask, m.col_mask
+        self.row_off, self.col_off = m.row_off, m.col_off
+
+
+def eltwise_cpu(prog, operands, out, region=None, stream=None):
+    """CPU stand-in for ttlhip.kernels.eltwise (same arguments): the ttnn
+    elementwise ops of the drop-in on the CPU test path."""
+    region = region if region is not None else (0, 0, out.shape[0], out.shape[1])
+    l = EltwiseLaunch(prog, [None if m is None else _MapSpec(m) for m in operands],
+                      _MapRef(out), tuple(region))
+    run_eltwise(l, {})
+
+
 def run(plan, args):
     for l in plan.launches:
         if isinstance(l, ReduceLaunch):

@@ -205,3 +205,15 @@ def test_body_created_tensor_rebound_across_calls():
         k(ttnn.from_torch(a), ttnn.from_torch(torch.full((1, 1), cval, dtype=torch.bfloat16)), y)
         assert torch.equal(ttnn.to_torch(y), a + torch.tensor(cval, dtype=torch.bfloat16))
     assert len(k._cache) == 1
+
+
+def test_bcast_fma_example_config():
+    # examples/broadcast.py's own configuration (GRANULARITY 4, grid (8, 8),
+    # bf16 2048x2048, c of shape (2048, 1)); the unmodified example plans to
+    # these launches (test_examples_unchanged.py)
+    n = 2048
+    a, b = O.seeded((n, n), "uniform", 40, lo=0, hi=1), O.seeded((n, n), "uniform", 41, lo=0, hi=1)
+    c = O.seeded((n, 1), "uniform", 42, lo=0, hi=1)
+    got, k = _gpu(KL.make_bcast_fma, [a, b, c, torch.zeros(n, n, dtype=torch.bfloat16)], 3)
+    assert len(k.last_plan.launches) == 1
+    assert torch.equal(got, a * b + c)  # per-op bf16 rounding, vectorised

@@ -950,8 +950,30 @@ def build_plan(groups: List[_Group], tensor_ref) -> Plan:
     return plan
 
 
+def _dedupe_writes(g: _Group, out_rc, leaf_rc):
+    """Store instances that repeat another exactly (same output tile, same
+    tile of every operand), e.g. every core of a grid running the same loop
+    (examples/broadcast_demo.py with grid="auto"): the simulator writes the
+    same values several times, one launch writes them once.  Only for plain
+    stores whose output is not also an operand (then repeats are not
+    idempotent); instances that write one tile with different operands stay
+    and are refused by the caller."""
+    n = out_rc.shape[0]
+    if g.acc or n == 0 or _unique_tiles(out_rc) == n:
+        return out_rc, leaf_rc
+    if any(t is g.out_tensor for t in g.leaf_tensors):
+        return out_rc, leaf_rc
+    rows = np.concatenate([out_rc] + list(leaf_rc), 1)
+    _, keep = np.unique(rows, axis=0, return_index=True)
+    keep.sort()
+    if _unique_tiles(out_rc[keep]) != keep.size:
+        return out_rc, leaf_rc
+    return out_rc[keep], [x[keep] for x in leaf_rc]
+
+
 def _plan_eltwise(g: _Group, out_rc, leaf_rc, tensor_ref,
                   inl: Optional["_Inliner"] = None) -> List[EltwiseLaunch]:
+    out_rc, leaf_rc = _dedupe_writes(g, out_rc, leaf_rc)
     n = out_rc.shape[0]
     if _unique_tiles(out_rc) != n:
         if g.acc:
