@@ -215,6 +215,25 @@ int ttlh_reduce(const ttlh_instr* prog, const ttlh_operand* in, int n_instr,
                 int out_pad, int64_t y0, int64_t x0, int64_t h, int64_t w,
                 void* workspace, int64_t workspace_bytes, void* stream);
 
+/* ttlh_reduce without a workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference (its
+ * kernels allocate nothing a caller sees).  The fp32 partial results live in
+ * a fixed array of TTLH_REDUCE_SCRATCH_BYTES per GPU inside the library
+ * (held until the process ends); reductions whose
+ * ttlh_reduce_workspace_bytes() exceeds it are refused with TTLH_EUNSUPPORTED.
+ * Nothing is allocated or freed.  Every call on one GPU shares that array:
+ * calls that overlap on one GPU (different streams, or host threads racing
+ * on one) race on it; calls ordered on one stream are safe.  The stream must
+ * belong to the current device.  Results are identical to ttlh_reduce's. */
+#define TTLH_REDUCE_SCRATCH_BYTES (4 << 20)
+
+int ttlh_reduce_noalloc(const ttlh_instr* prog, const ttlh_operand* in,
+                        int n_instr, int kind, int dims, const void* scaler,
+                        int scaler_dtype, float scale_imm, void* out,
+                        int out_dtype, int64_t out_ld, int out_pad, int64_t y0,
+                        int64_t x0, int64_t h, int64_t w, void* stream);
+
 /* ------------------------------------------------------------------------
  * Tilized element order (the TILE_LAYOUT storage of ttnn tensors, which the
  * reference's compiled path requires: python/ttl/ttl_api.py:489-506; the

@@ -35,6 +35,7 @@
 //    separate "full" kernel variants so the common-op variants fit 8 waves
 //    per SIMD (<= 64 VGPRs) without spilling.
 
+#include <mutex>
 #include <utility>
 
 #include "ttlh_common.h"
@@ -1441,34 +1442,116 @@ extern "C" int64_t ttlh_reduce_workspace_bytes(int dims, int64_t h, int64_t w) {
   return h * int64_t(sizeof(float));
 }
 
+// The fixed device array behind ttlh_reduce_noalloc: fp32 partial results
+// of column and full reductions (every launch writes the partials it later
+// reads, so nothing in it has to start at zero).  Each GPU the library runs
+// on holds its own copy until the process ends.
+static __device__ __align__(256) float scratch[TTLH_REDUCE_SCRATCH_BYTES / sizeof(float)];
+
+namespace ttlh {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the device `stream` runs on, looked up
+// once per device (with that device current) and kept.  Host code uses this
+// pointer, never the array's name, which on the host is only a stand-in.
+int reduce_scratch(const char* who, hipStream_t stream, float** ptr) {
+  int cur = 0;
+  TTLH_REQUIRE(hipGetDevice(&cur) == hipSuccess, TTLH_EHIP, "%s: hipGetDevice failed", who);
+  if (stream != nullptr) {
+    int sdev = cur;
+    TTLH_REQUIRE(hipStreamGetDevice(stream, &sdev) == hipSuccess, TTLH_EHIP,
+                 "%s: hipStreamGetDevice failed", who);
+    TTLH_REQUIRE(sdev == cur, TTLH_EINVAL,
+                 "%s: the stream belongs to device %d but device %d is current", who, sdev, cur);
+  }
+  TTLH_REQUIRE(cur >= 0 && cur < kMaxDevices, TTLH_EUNSUPPORTED, "%s: device %d out of range",
+               who, cur);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[cur] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    TTLH_REQUIRE(e == hipSuccess && p != nullptr, TTLH_EHIP,
+                 "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", who, cur,
+                 hipGetErrorString(e));
+    g_scratch_ptr[cur] = static_cast<float*>(p);
+  }
+  *ptr = g_scratch_ptr[cur];
+  return TTLH_OK;
+}
+
+int reduce_impl(const char* who, const ttlh_instr* prog, const ttlh_operand* in, int n_instr,
+                int kind, int dims, const void* scaler, int scaler_dtype, float scale_imm,
+                void* out, int out_dtype, int64_t out_ld, int out_pad, int64_t y0, int64_t x0,
+                int64_t h, int64_t w, float* workspace, int64_t workspace_bytes, void* stream);
+
+}  // namespace
+}  // namespace ttlh
+
 extern "C" int ttlh_reduce(const ttlh_instr* prog, const ttlh_operand* in, int n_instr, int kind,
                            int dims, const void* scaler, int scaler_dtype, float scale_imm,
                            void* out, int out_dtype, int64_t out_ld, int out_pad, int64_t y0,
                            int64_t x0, int64_t h, int64_t w, void* workspace,
                            int64_t workspace_bytes, void* stream) {
   clear_error();
+  return reduce_impl("ttlh_reduce", prog, in, n_instr, kind, dims, scaler, scaler_dtype,
+                     scale_imm, out, out_dtype, out_ld, out_pad, y0, x0, h, w,
+                     static_cast<float*>(workspace), workspace_bytes, stream);
+}
+
+extern "C" int ttlh_reduce_noalloc(const ttlh_instr* prog, const ttlh_operand* in, int n_instr,
+                                   int kind, int dims, const void* scaler, int scaler_dtype,
+                                   float scale_imm, void* out, int out_dtype, int64_t out_ld,
+                                   int out_pad, int64_t y0, int64_t x0, int64_t h, int64_t w,
+                                   void* stream) {
+  clear_error();
+  const int64_t need = ttlh_reduce_workspace_bytes(dims, h, w);
+  TTLH_REQUIRE(need <= TTLH_REDUCE_SCRATCH_BYTES, TTLH_EUNSUPPORTED,
+               "ttlh_reduce_noalloc: a %lld x %lld reduction needs %lld bytes of partial results; "
+               "the library's fixed scratch holds %lld (use ttlh_reduce with a workspace)",
+               (long long)h, (long long)w, (long long)need, (long long)TTLH_REDUCE_SCRATCH_BYTES);
+  float* ws = nullptr;
+  if (need > 0) {
+    const int st = reduce_scratch("ttlh_reduce_noalloc", static_cast<hipStream_t>(stream), &ws);
+    if (st != TTLH_OK) return st;
+  }
+  return reduce_impl("ttlh_reduce_noalloc", prog, in, n_instr, kind, dims, scaler, scaler_dtype,
+                     scale_imm, out, out_dtype, out_ld, out_pad, y0, x0, h, w, ws,
+                     TTLH_REDUCE_SCRATCH_BYTES, stream);
+}
+
+namespace ttlh {
+namespace {
+
+int reduce_impl(const char* who, const ttlh_instr* prog, const ttlh_operand* in, int n_instr,
+                int kind, int dims, const void* scaler, int scaler_dtype, float scale_imm,
+                void* out, int out_dtype, int64_t out_ld, int out_pad, int64_t y0, int64_t x0,
+                int64_t h, int64_t w, float* workspace, int64_t workspace_bytes, void* stream) {
   TTLH_REQUIRE(kind == TTLH_REDUCE_SUM || kind == TTLH_REDUCE_MAX, TTLH_EINVAL,
-               "ttlh_reduce: kind must be TTLH_REDUCE_SUM or TTLH_REDUCE_MAX");
+               "%s: kind must be TTLH_REDUCE_SUM or TTLH_REDUCE_MAX", who);
   TTLH_REQUIRE(dims >= 1 && dims <= 3, TTLH_EINVAL,
-               "ttlh_reduce: dims must be TTLH_REDUCE_DIM0, TTLH_REDUCE_DIM1 or both");
+               "%s: dims must be TTLH_REDUCE_DIM0, TTLH_REDUCE_DIM1 or both", who);
   TTLH_REQUIRE(out && (out_dtype == TTLH_BF16 || out_dtype == TTLH_F32), TTLH_EINVAL,
-               "ttlh_reduce: bad output pointer or dtype");
+               "%s: bad output pointer or dtype", who);
   TTLH_REQUIRE(!scaler || scaler_dtype == TTLH_BF16 || scaler_dtype == TTLH_F32, TTLH_EINVAL,
-               "ttlh_reduce: bad scaler dtype");
-  TTLH_REQUIRE(out_pad == 0 || out_pad == 1, TTLH_EINVAL, "ttlh_reduce: out_pad must be 0 or 1");
+               "%s: bad scaler dtype", who);
+  TTLH_REQUIRE(out_pad == 0 || out_pad == 1, TTLH_EINVAL, "%s: out_pad must be 0 or 1", who);
   TTLH_REQUIRE(h >= 1 && w >= 1 && y0 >= 0 && x0 >= 0, TTLH_EINVAL,
-               "ttlh_reduce: empty or negative region");
-  TTLH_REQUIRE(out_ld >= (out_pad ? 32 : 1), TTLH_EINVAL, "ttlh_reduce: out_ld too small");
+               "%s: empty or negative region", who);
+  TTLH_REQUIRE(out_ld >= (out_pad ? 32 : 1), TTLH_EINVAL, "%s: out_ld too small", who);
   RedArgs a = {};
   ProgInfo pi;
-  const int st = decode_program("ttlh_reduce", prog, in, n_instr, y0, x0, h, w, a.e, pi);
+  const int st = decode_program(who, prog, in, n_instr, y0, x0, h, w, a.e, pi);
   if (st != TTLH_OK) return st;
   const int64_t need = ttlh_reduce_workspace_bytes(dims, h, w);
   TTLH_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), TTLH_EINVAL,
-               "ttlh_reduce: needs a workspace of %lld bytes (got %lld)", (long long)need,
+               "%s: needs a workspace of %lld bytes (got %lld)", who, (long long)need,
                (long long)workspace_bytes);
   TTLH_REQUIRE((h + 3) / 4 < (int64_t(1) << 31) && w / 64 < (int64_t(1) << 31), TTLH_EUNSUPPORTED,
-               "ttlh_reduce: region too large");
+               "%s: region too large", who);
   a.h = h;
   a.w = w;
   a.scaler = scaler;
@@ -1478,7 +1561,7 @@ extern "C" int ttlh_reduce(const ttlh_instr* prog, const ttlh_operand* in, int n
   a.out_ld = out_ld;
   a.out_dtype = out_dtype;
   a.out_pad = out_pad;
-  a.ws = static_cast<float*>(workspace);
+  a.ws = workspace;
   a.kind = kind;
   a.splits = 1;
   a.rows_per_split = h;
@@ -1533,3 +1616,6 @@ extern "C" int ttlh_reduce(const ttlh_instr* prog, const ttlh_operand* in, int n
     return check_launch("reduce_cols_finish_kernel");
   }
 }
+
+}  // namespace
+}  // namespace ttlh

@@ -83,6 +83,9 @@ SIGNATURES = {
     "ttlh_reduce": (_int, [C.POINTER(Instr), C.POINTER(Operand), _int, _int, _int, _vp, _int,
                            C.c_float, _vp, _int, _i64, _int, _i64, _i64, _i64, _i64, _vp, _i64,
                            _vp]),
+    "ttlh_reduce_noalloc": (_int, [C.POINTER(Instr), C.POINTER(Operand), _int, _int, _int, _vp,
+                                   _int, C.c_float, _vp, _int, _i64, _int, _i64, _i64, _i64, _i64,
+                                   _vp]),
     "ttlh_matmul": (_int, [_vp, _int, _i64, _vp, _int, _i64, _vp, _int, _i64, _i64, _i64, _i64,
                            _int, _vp]),
     "ttlh_bfp8_pack_host": (_int, [_vp, _vp, _i64, _i64]),

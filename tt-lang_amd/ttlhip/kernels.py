@@ -110,14 +110,16 @@ def eltwise(prog: StackProgram, operands: Sequence[Optional[OperandMap]], out: t
 def reduce(prog: StackProgram, operands: Sequence[Optional[OperandMap]], kind: str,
            dims: Sequence[int], out: torch.Tensor, region, out_origin=(0, 0),
            out_pad: bool = False, scaler: Optional[torch.Tensor] = None, scale: float = 1.0,
-           stream=None) -> None:
+           stream=None, noalloc: bool = False) -> None:
     """Scaled reduction (kind "sum" or "max") of a stack program over the
     iteration `region` = (y0, x0, h, w), operands addressed as in eltwise()
     from iteration element (y, x).  dims: the reduced axes (0: over rows, 1:
     over columns).  The results are written into `out` from `out_origin`
     (one per column, one per row, or one value; out_pad: whole zero-padded
     32-wide result tiles).  scaler: a device tensor whose first element
-    multiplies every value (times `scale`)."""
+    multiplies every value (times `scale`).  noalloc: run through
+    ttlh_reduce_noalloc (partial results in the library's fixed per-GPU
+    scratch array, nothing allocated; calls overlapping on one GPU race)."""
     _check_device(out, "reduce output")
     if out.stride(1) != 1:
         raise ValueError("reduce output must have unit column stride")
@@ -153,6 +155,13 @@ def reduce(prog: StackProgram, operands: Sequence[Optional[OperandMap]], kind: s
         if not scaler.is_cuda or scaler.numel() < 1:
             raise ValueError("reduce scaler must be a non-empty device tensor")
         sp, sdt = scaler.data_ptr(), L.dtype_code(scaler.dtype)
+    optr = out.data_ptr() + (oy * out.stride(0) + ox) * out.element_size()
+    kcode = L.REDUCE_SUM if kind == "sum" else L.REDUCE_MAX
+    if noalloc:
+        L.call("ttlh_reduce_noalloc", instrs, ops, n, kcode, dbits, sp, sdt, float(scale), optr,
+               L.dtype_code(out.dtype), out.stride(0), int(bool(out_pad)), y0, x0, h, w,
+               L.stream_ptr(stream))
+        return
     ws_bytes = int(L.load().ttlh_reduce_workspace_bytes(dbits, h, w))
     ws = None
     if ws_bytes:
@@ -160,8 +169,7 @@ def reduce(prog: StackProgram, operands: Sequence[Optional[OperandMap]], kind: s
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=out.device)
         if stream is not None:
             ws.record_stream(stream)
-    optr = out.data_ptr() + (oy * out.stride(0) + ox) * out.element_size()
-    L.call("ttlh_reduce", instrs, ops, n, L.REDUCE_SUM if kind == "sum" else L.REDUCE_MAX,
+    L.call("ttlh_reduce", instrs, ops, n, kcode,
            dbits, sp, sdt, float(scale), optr, L.dtype_code(out.dtype), out.stride(0),
            int(bool(out_pad)), y0, x0, h, w, ws.data_ptr() if ws is not None else 0, ws_bytes,
            L.stream_ptr(stream))
