@@ -340,18 +340,30 @@ def make_ttl():
     class _Math:
         @staticmethod
         def broadcast(block, out=None, dims=None):
-            """The compiler's tile broadcast (python/ttl/operators.py:333-360;
-            unary_bcast Row / Col / Scalar, TTLElementwiseOps.def:82): every
-            tile replaced by its row 0 (dims [0]), column 0 ([1]) or element
-            [0, 0] ([0, 1]) repeated over the tile; a size-1 block dimension
-            along a broadcast dim repeated to `out`'s block size.  Without
-            `out`, broadcast block dims must be 1 (python/sim/math.py:69-83)."""
+            """Two forms.  With `out` (the compiler's only form,
+            python/ttl/operators.py:333-360; unary_bcast Row / Col / Scalar,
+            TTLElementwiseOps.def:82): every tile replaced by its row 0 (dims
+            [0]), column 0 ([1]) or element [0, 0] ([0, 1]) repeated over the
+            tile, and a size-1 block dimension along a broadcast dim repeated
+            to `out`'s block size.  Without `out` (the simulator's form,
+            python/sim/math.py:20-106): validation only (each broadcast block
+            dim must be 1), the block returned unchanged, and the enclosing
+            binary op broadcasts over the tile grid and inside size-1 tiles."""
             if dims is None:
                 raise ValueError("dims parameter is required for broadcast()")
             t = _tiles_of(block)
-            target = tuple(out.shape) if out is not None else None
+            if out is None:
+                for d in dims:
+                    if d >= len(t.shape):
+                        raise ValueError(f"Cannot broadcast along dimension {d}: block has shape "
+                                         f"{t.shape} with only {len(t.shape)} dimensions")
+                    if t.shape[d] != 1:
+                        raise ValueError(f"Cannot broadcast along dimension {d}: dimension must "
+                                         f"have size 1, but has size {t.shape[d]}")
+                return _Tiles([x.clone() for x in t.tiles], t.shape)
+            target = tuple(out.shape)
             for d in dims:
-                if t.shape[d] != 1 and (target is None or target[d] != t.shape[d]):
+                if t.shape[d] != 1 and target[d] != t.shape[d]:
                     raise ValueError("broadcast dimension must have size 1")
 
             def rep(x):
@@ -362,13 +374,11 @@ def make_ttl():
                 return x.clone()
             tiles = [rep(x) for x in t.tiles]
             R, C = t.shape
-            if target is not None:
-                nr = target[0] if (0 in dims and R == 1) else R
-                nc = target[1] if (1 in dims and C == 1) else C
-                tiles = [tiles[(i if R > 1 else 0) * C + (j if C > 1 else 0)]
-                         for i in range(nr) for j in range(nc)]
-                R, C = nr, nc
-            return _Tiles(tiles, (R, C))
+            nr = target[0] if (0 in dims and R == 1) else R
+            nc = target[1] if (1 in dims and C == 1) else C
+            tiles = [tiles[(i if R > 1 else 0) * C + (j if C > 1 else 0)]
+                     for i in range(nr) for j in range(nc)]
+            return _Tiles(tiles, (nr, nc))
 
     for name, fn in (("exp", torch.exp), ("log", torch.log), ("sqrt", torch.sqrt),
                      ("rsqrt", torch.rsqrt), ("tanh", torch.tanh), ("abs", torch.abs),

@@ -1060,3 +1060,46 @@ def make_softmax_rows(ttl, w=4, grid=(2, 2)):
                     ttl.copy(ob, out[r, 0:w]).wait()
 
     return softmax_rows
+
+
+def make_row_bcast_forms(ttl, with_out: bool, grid=(1, 1)):
+    """out = a + broadcast(b, [out,] dims=[0]) with a (2, 2)-tile block and b
+    a (1, 2)-tile block of full 32x32 tiles.  With `out` (the compiler's
+    form) each b tile is its row 0 repeated; without it (the simulator's
+    form) the b tiles are added as they are, re-used over the tile rows."""
+    @ttl.kernel(grid=grid)
+    def row_bcast_forms(a, b, out):
+        a_cb = ttl.make_circular_buffer_like(a, shape=(2, 2), buffer_factor=2)
+        b_cb = ttl.make_circular_buffer_like(b, shape=(1, 2), buffer_factor=2)
+        o_cb = ttl.make_circular_buffer_like(out, shape=(2, 2), buffer_factor=2)
+        nr = a.shape[0] // TILE // 2
+        nc = a.shape[1] // TILE // 2
+
+        @ttl.compute()
+        def comp():
+            for _ in range(nr):
+                for _ in range(nc):
+                    with a_cb.wait() as ab, b_cb.wait() as bb, o_cb.reserve() as ob:
+                        if with_out:
+                            ob.store(ab + ttl.math.broadcast(bb, ob, dims=[0]))
+                        else:
+                            ob.store(ab + ttl.math.broadcast(bb, dims=[0]))
+
+        @ttl.datamovement()
+        def rd():
+            for i in range(nr):
+                for j in range(nc):
+                    with a_cb.reserve() as ab, b_cb.reserve() as bb:
+                        ta = ttl.copy(a[2 * i:2 * i + 2, 2 * j:2 * j + 2], ab)
+                        tb = ttl.copy(b[0:1, 2 * j:2 * j + 2], bb)
+                        ta.wait()
+                        tb.wait()
+
+        @ttl.datamovement()
+        def wr():
+            for i in range(nr):
+                for j in range(nc):
+                    with o_cb.wait() as ob:
+                        ttl.copy(ob, out[2 * i:2 * i + 2, 2 * j:2 * j + 2]).wait()
+
+    return row_bcast_forms

@@ -219,3 +219,25 @@ def test_inliner_keeps_stage_read_by_split_store():
     plan.launches = [writer]
     inl.finish(plan)
     assert plan.launches == [writer]
+
+
+@pytest.mark.parametrize("with_out", [False, True])
+def test_broadcast_forms_differ_on_full_tiles(with_out):
+    # b holds full 32-row tiles whose rows differ: the simulator's form (no
+    # `out`, python/sim/math.py:20-106) adds the tiles as they are, the
+    # compiler's form (with `out`, python/ttl/operators.py:333-360) adds row
+    # 0 of each tile; closed forms with one bf16 rounding per element
+    a = O.seeded((128, 128), "uniform", 41, lo=-2, hi=2)
+    b = O.seeded((32, 128), "uniform", 42, lo=-2, hi=2)
+    out = torch.zeros(128, 128, dtype=torch.bfloat16)
+    if with_out:
+        expect = a + b[0:1, :].expand(128, 128)
+    else:
+        expect = a + b.repeat(4, 1)
+    ref = _oracle(KL.make_row_bcast_forms, [a, b, out], 2, with_out=with_out)
+    got, plan = _plan_run(KL.make_row_bcast_forms, [a, b, out], 2, with_out=with_out)
+    assert torch.equal(ref, expect) and torch.equal(got, expect)
+    assert len(plan.launches) == 1
+    other = a + (b.repeat(4, 1) if with_out else b[0:1, :].expand(128, 128))
+    assert not torch.equal(expect, other)  # the two forms really differ here
+

@@ -141,3 +141,17 @@ def test_softmax_rows_through_intermediate_cbs():
     d = O.bf16_ulp_diff(got, ref)
     assert int(d.max()) <= 2 and float((d > 0).float().mean()) < 0.05
     assert float((got.float() - torch.softmax(x.float(), 1)).abs().max()) < 2e-3
+
+
+@pytest.mark.parametrize("with_out", [False, True])
+def test_broadcast_forms_on_full_tiles_gpu(with_out):
+    # the simulator's form (no `out`: tiles added as they are) and the
+    # compiler's form (with `out`: row 0 of each tile) on the device
+    a = O.seeded((512, 256), "uniform", 51, lo=-2, hi=2)
+    b = O.seeded((32, 256), "uniform", 52, lo=-2, hi=2)
+    expect = a + (b[0:1, :].expand(512, 256) if with_out else b.repeat(16, 1))
+    k = KL.make_row_bcast_forms(ttl, with_out, grid=(2, 2))
+    args = [ttnn.from_torch(t) for t in (a, b, torch.zeros(512, 256, dtype=torch.bfloat16))]
+    k(*args)
+    assert len(k.last_plan.launches) == 1
+    assert torch.equal(ttnn.to_torch(args[2]), expect)

@@ -798,30 +798,40 @@ class _Math:
 
     @staticmethod
     def broadcast(block, out=None, dims: Optional[Sequence[int]] = None) -> BExpr:
-        """The compiler's tile broadcast (python/ttl/operators.py:333-360, tile
-        op unary_bcast Row / Col / Scalar, TTLElementwiseOps.def:82): every
-        tile becomes its row 0 (dims=[0]), column 0 ([1]) or element [0, 0]
-        ([0, 1]) repeated over the tile, and a block dimension of size 1
-        along a broadcast dim takes the size of the output block `out`
-        (shape expansion, test/python/test_bcast_shape_expansion.py).  Without
-        `out` the broadcast block dims must have size 1 and the enclosing
-        binary op broadcasts them (python/sim/math.py:20-106).  For operands
-        of a size-1 tensor dimension, the simulator's use, picking row /
-        column 0 changes nothing."""
+        """Two forms.  With `out`, the compiler's tile broadcast (the only form
+        it has, python/ttl/operators.py:333-360; tile op unary_bcast Row / Col
+        / Scalar, TTLElementwiseOps.def:82): every tile becomes its row 0
+        (dims=[0]), column 0 ([1]) or element [0, 0] ([0, 1]) repeated over
+        the tile, and a block dimension of size 1 along a broadcast dim takes
+        the size of the output block `out` (shape expansion,
+        test/python/test_bcast_shape_expansion.py).  Without `out`, the
+        simulator's form (python/sim/math.py:20-106): the broadcast block
+        dims must have size 1, the block is returned unchanged and the
+        enclosing binary op broadcasts it over the tile grid (and inside
+        size-1 tensor dimensions); the tiles' own rows / columns are kept."""
         if dims is None:
             raise ValueError("dims parameter is required for broadcast()")
         e = _as_bexpr(block)
-        target = tuple(out.shape) if out is not None else None
+        if out is None:
+            for d in dims:
+                if d >= len(e.shape):
+                    raise ValueError(f"Cannot broadcast along dimension {d}: block has shape "
+                                     f"{e.shape} with only {len(e.shape)} dimensions")
+                if e.shape[d] != 1:
+                    raise ValueError(f"Cannot broadcast along dimension {d}: dimension must have "
+                                     f"size 1, but has size {e.shape[d]}")
+            return e
+        target = tuple(out.shape)
         shape, tree = list(e.shape), e.tree
         for d in dims:
             if d >= len(e.shape):
                 raise ValueError(f"Cannot broadcast along dimension {d}: block has shape {e.shape} "
                                  f"with only {len(e.shape)} dimensions")
             n = e.shape[d]
-            if n == 1 and target is not None and target[d] != 1:
+            if n == 1 and target[d] != 1:
                 tree = _remap(tree, d, target[d])
                 shape[d] = target[d]
-            elif n != 1 and (target is None or target[d] != n):
+            elif n != 1 and target[d] != n:
                 raise ValueError(f"Cannot broadcast along dimension {d}: dimension must have size "
                                  f"1, but has size {n}")
         if set(dims) - {0, 1}:
