@@ -52,6 +52,44 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+def _timed(fn, threads=None):
+    """(seconds, result) of fn() on the host, with torch limited to `threads`."""
+    nthr = torch.get_num_threads()
+    if threads is not None:
+        torch.set_num_threads(threads)
+    try:
+        t0 = time.perf_counter()
+        r = fn()
+        return time.perf_counter() - t0, r
+    finally:
+        torch.set_num_threads(nthr)
+
+
+CPU_SAMPLE_S = 10.0  # host seconds each CPU baseline aims for (repeated samples)
+
+
+def _repeat(fn, threads=None, min_s: float = CPU_SAMPLE_S, max_reps: int = 64):
+    """(seconds per repetition, repetitions) of fn() repeated on the host until
+    min_s seconds have passed (at least once, at most max_reps times)."""
+    total, reps = 0.0, 0
+    while reps < max_reps and (reps == 0 or total < min_s):
+        dt, _ = _timed(fn, threads)
+        total += dt
+        reps += 1
+    return total / reps, reps
+
+
+def _eager(make, tensors):
+    """The oracle's eager executor (simulator execution model: threads
+    blocking on circular-buffer rings, one torch op per 32x32 tile) running a
+    tt-lang kernel over CPU tensors on 1 thread, repeated to about
+    CPU_SAMPLE_S seconds; returns (seconds per run, runs)."""
+    from oracle import sim_exec
+    k = make(sim_exec.make_ttl())
+    args = [sim_exec.OracleTensor(t) for t in tensors]
+    return _repeat(lambda: k(*args), threads=1)
+
+
 # --------------------------------------------------------------------------
 # workloads
 
@@ -76,6 +114,11 @@ class Workload:
 
     def check(self) -> dict:
         raise NotImplementedError
+
+    def cpu_baseline(self):
+        """The reference's CPU path for this workload (the oracle's
+        restatement of the simulator), timed on a bounded sample."""
+        return None
 
 
 class PlanWorkload(Workload):
@@ -158,29 +201,20 @@ class EltwiseWorkload(PlanWorkload):
         """The oracle's eager executor (one torch op per 32x32 tile, CB ring
         bookkeeping, three threads per core under the GIL: the simulator's
         execution model) on the same tt-lang kernel and the full-size input."""
-        from oracle import sim_exec, tile_ops as O
-        k = self.make_kernel(sim_exec.make_ttl())
-        ins = [sim_exec.OracleTensor(t) for t in self.cpu_inputs()]
-        out = sim_exec.OracleTensor(torch.zeros(self.n, self.n, dtype=torch.bfloat16))
-        nthr = torch.get_num_threads()
-        torch.set_num_threads(1)
-        try:
-            t0 = time.perf_counter()
-            k(*ins, out)
-            dt = time.perf_counter() - t0
-        finally:
-            torch.set_num_threads(nthr)
-        env = dict(zip("abc", self.cpu_inputs()))
-        t0 = time.perf_counter()
-        O.eval_expr(self.expr(), env)
-        dtv = time.perf_counter() - t0
+        from oracle import tile_ops as O
+        ins = self.cpu_inputs()
+        out = torch.zeros(self.n, self.n, dtype=torch.bfloat16)
+        dt, reps = _eager(self.make_kernel, ins + [out])
+        env = dict(zip("abc", ins))
+        dtv, _ = _repeat(lambda: O.eval_expr(self.expr(), env), min_s=1.0)
         return {"value": round(self.work_per_step() / dt / 1e9, 4), "unit": "GB/s", "cores": 1,
                 "kind": "port",
                 "sample": f"the full {self.n}x{self.n} workload through the eager tile-by-tile "
-                          f"oracle executor (simulator execution model, 1 thread): {dt:.2f} s",
+                          f"oracle executor (simulator execution model, 1 thread), {reps} runs "
+                          f"of {dt:.2f} s",
                 "host_cpu_count": os.cpu_count(),
                 "vectorised_torch_cpu": {"value": round(self.work_per_step() / dtv / 1e9, 3),
-                                         "unit": "GB/s", "cores": nthr}}
+                                         "unit": "GB/s", "cores": torch.get_num_threads()}}
 
 
 class ReduceWorkload(PlanWorkload):
@@ -224,6 +258,19 @@ class ReduceWorkload(PlanWorkload):
         return {"max_ulp": int(ulp.max()), "mismatch_frac": float((ulp > 0).float().mean()),
                 "oracle": "float64 row sums rounded once to bf16"}
 
+    def cpu_baseline(self):
+        import kernel_lib as KL
+        from oracle.tile_ops import seeded
+        x = seeded((self.n, self.n), "uniform", self.seed, lo=-2, hi=2)
+        t = [x, torch.ones(32, 32, dtype=torch.bfloat16),
+             torch.zeros(self.n, 1, dtype=torch.bfloat16)]
+        dt, reps = _eager(lambda ns: KL.make_reduce_rows(ns, kind="sum", gr=2, gc=16,
+                                                         grid=(8, 8)), t)
+        return {"value": round(self.work_per_step() / dt / 1e9, 4), "unit": "GB/s", "cores": 1,
+                "kind": "port",
+                "sample": f"the full {self.n}x{self.n} workload through the eager tile-by-tile "
+                          f"oracle executor (1 thread), {reps} runs of {dt:.2f} s"}
+
 
 class TilizeWorkload(Workload):
     """Row-major bf16 -> tilized element order (ttnn TILE_LAYOUT storage,
@@ -263,6 +310,14 @@ class TilizeWorkload(Workload):
         torch.cuda.synchronize()
         ok = torch.equal(self.sets[0][1].cpu(), O.tilize_ref(self.x))
         return {"bit_exact": bool(ok), "oracle": "reshape / permute restatement (tilize_ref)"}
+
+    def cpu_baseline(self):
+        from oracle import tile_ops as O
+        dt, reps = _repeat(lambda: O.tilize_ref(self.x).contiguous(), max_reps=2000)
+        return {"value": round(self.work_per_step() / dt / 1e9, 4), "unit": "GB/s",
+                "cores": torch.get_num_threads(), "kind": "port",
+                "sample": f"the full {self.n}x{self.n} tilize through the oracle's reshape / "
+                          f"permute restatement, {reps} runs of {dt * 1e3:.2f} ms"}
 
 
 class MatmulWorkload(PlanWorkload):
@@ -304,6 +359,25 @@ class MatmulWorkload(PlanWorkload):
         got = c[rows].double()
         return {"max_abs_err_rel": float((got - exact).abs().max() / exact.abs().max()),
                 "rows_checked": int(rows.numel()), "oracle": "float64 product"}
+
+    def cpu_baseline(self):
+        import kernel_lib as KL
+        import ttnn
+        from oracle.tile_ops import seeded
+        n = 1024
+        std = 1.0 / math.sqrt(n)
+        t = [seeded((n, n), "normal", self.seed, std=std),
+             seeded((n, n), "normal", self.seed + 1, std=std),
+             torch.zeros(n, n, dtype=torch.bfloat16)]
+        dt, reps = _eager(lambda ns: KL.make_matmul_multi(ns, ttnn), t)
+        steps = (n // 32) ** 3
+        full = (self.M // 32) * (self.N // 32) * (self.K // 32)
+        return {"value": round(2.0 * n ** 3 / dt / 1e12, 8), "unit": "TFLOP/s", "cores": 1,
+                "kind": "port",
+                "sample": f"{n}^3 ({steps} tile steps) through the eager tile-by-tile oracle "
+                          f"executor (1 thread), {reps} runs of {dt:.2f} s; extrapolated to "
+                          f"{self.M}x{self.K}x{self.N} ({full} tile steps) at the same rate: "
+                          f"{dt * full / steps:.0f} s"}
 
 
 class Bfp8MatmulWorkload(Workload):
@@ -364,6 +438,22 @@ class Bfp8MatmulWorkload(Workload):
                 "rows_checked": int(rows.numel()),
                 "oracle": "float64 product of the C oracle's dequantisation"}
 
+    def cpu_baseline(self):
+        from oracle import bfp8 as OB
+        rows = 256
+        bq = self.bq.cpu()
+        a = self.a[:rows].cpu()
+
+        def work():
+            w = OB.unpack_c(bq, self.K, self.N)
+            return (a.float() @ w.float()).bfloat16()
+        dt, reps = _repeat(work)
+        return {"value": round(2.0 * rows * self.N * self.K / dt / 1e12, 6), "unit": "TFLOP/s",
+                "cores": torch.get_num_threads(), "kind": "port",
+                "sample": f"{rows} of the {self.M} rows of A: the C oracle's bfloat8_b decode of "
+                          f"all of Bq plus a float32 torch CPU product, {reps} runs of {dt:.2f} s "
+                          "(no simulator path exists for bfloat8_b)"}
+
 
 class SdpaWorkload(Workload):
     """C5: softmax(Q K^T / sqrt(D)) V, bf16 [B, H, S, D], non-causal (C ABI)."""
@@ -407,6 +497,17 @@ class SdpaWorkload(Workload):
         got = self.o[:1, :1].cpu().double()
         return {"max_abs_err_rel": float((got - ref).abs().max() / ref.abs().max()),
                 "heads_checked": 1, "oracle": "float64 softmax(QK^T s)V"}
+
+    def cpu_baseline(self):
+        from oracle.tile_ops import sdpa_ref
+        heads = 2
+        q, k, v = (t[:1, :heads].cpu() for t in (self.q, self.k, self.v))
+        dt, reps = _repeat(lambda: sdpa_ref(q, k, v, self.scale, dtype=torch.float32))
+        return {"value": round(4.0 * heads * self.S * self.S * self.D / dt / 1e12, 6),
+                "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port",
+                "sample": f"{heads} of the {self.B * self.H} (batch, head) pairs through the "
+                          f"oracle's softmax(Q K^T s) V in float32 torch on the CPU, {reps} runs "
+                          f"of {dt:.2f} s (no simulator path exists for attention)"}
 
 
 WORKLOADS = {
@@ -475,6 +576,40 @@ def measure(w: Workload, steps: int, warmup: int, use_graph: bool = True,
             "unit": w.unit, "peak": peak, "frac": achieved / peak, "work_per_step": work}
 
 
+def copy_ceiling(reps: int = 50) -> dict:
+    """Empirical HBM ceiling: a plain copy (the one-step program `load a`,
+    which ttlh_eltwise runs on its flat streaming kernel) of 256 MiB, read +
+    write counted, two buffer pairs alternating so the 256 MB Infinity Cache
+    cannot serve them, timed with HIP events on the launch stream."""
+    from ttlhip import expr as X
+    from ttlhip import kernels as K
+    rows, cols = 8192, 16384  # bf16: 256 MiB
+    pairs = [(torch.ones(rows, cols, dtype=torch.bfloat16, device="cuda"),
+              torch.empty(rows, cols, dtype=torch.bfloat16, device="cuda")) for _ in range(2)]
+    prog = X.compile_expr(X.Leaf(0, torch.bfloat16))
+    for src, dst in pairs:
+        K.eltwise(prog, [K.OperandMap(src)], dst)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(reps):
+        src, dst = pairs[i % 2]
+        K.eltwise(prog, [K.OperandMap(src)], dst)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    per = e0.elapsed_time(e1) / reps
+    nbytes = 2 * rows * cols * 2
+    ok = bool(torch.equal(pairs[1][1][:64], pairs[1][0][:64]))
+    del pairs
+    torch.cuda.empty_cache()
+    return {"value": round(nbytes / (per * 1e-3) / 1e9, 1), "unit": "GB/s", "copy_ok": ok,
+            "how": "plain copy of 256 MiB of bf16 through ttlh_eltwise's flat streaming kernel "
+                   f"(read + write), two buffer pairs alternating, {reps} copies timed with HIP "
+                   "events"}
+
+
 def traffic_for(name: str):
     """HBM bytes per launch measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
     (scaled by a copy kernel's readings), from the committed profile summary."""
@@ -514,6 +649,8 @@ def main() -> int:
     names = [n for n in (args.only.split(",") if args.only else WORKLOADS) if n]
     if HEADLINE not in names:
         names.insert(0, HEADLINE)
+    ceiling = copy_ceiling()
+    log(f"[bench] empirical copy ceiling {ceiling['value']} GB/s")
     results = {}
     for n in names:
         w = WORKLOADS[n]()
@@ -527,17 +664,20 @@ def main() -> int:
         r = measure(w, steps, warm, use_graph=not args.no_graph, min_ms=min_ms)
         r["parity"] = w.check()
         r["traffic"] = traffic_for(n)
+        if w.unit == "GB/s":
+            r["empirical_peak"] = ceiling["value"]
+            r["frac_of_empirical"] = r["achieved"] / ceiling["value"]
         results[n] = r
         log(f"[bench] {n}: {r['steps']} steps, {r['ms_per_step'] * 1e3:.2f} us/step {r['achieved']:.1f} {r['unit']} "
             f"({r['frac'] * 100:.1f}%) parity={r['parity']}")
+        if not args.no_cpu:
+            r["cpu_baseline"] = w.cpu_baseline()
+            log(f"[bench] {n}: cpu baseline {r['cpu_baseline']['value']} {r['unit']} "
+                f"({r['cpu_baseline']['sample']})")
         del w
         torch.cuda.empty_cache()
     h = results[HEADLINE]
-    cpu = None
-    if not args.no_cpu:
-        log("[bench] cpu baseline ...")
-        cpu = WORKLOADS[HEADLINE]().cpu_baseline()
-        log(f"[bench] cpu baseline {cpu['value']} GB/s")
+    cpu = h.get("cpu_baseline")
     line = {
         "metric": "eltwise GB/s (% HBM peak); matmul/SDPA bf16 TFLOP/s (% MFMA peak) @1 GPU",
         "value": round(h["achieved"], 2),
@@ -555,10 +695,14 @@ def main() -> int:
                    "ttlh_eltwise stream_kernel", "tiles": "32x32", "cb_block": "4x4 tiles",
                    "grid": "(8, 8) tt-lang cores -> one grid-wide launch"},
         "roofline": {"bound": h["bound"], "achieved": round(h["achieved"], 2), "peak": h["peak"],
-                     "unit": h["unit"], "frac": round(h["frac"], 4), "traffic": h["traffic"]},
+                     "unit": h["unit"], "frac": round(h["frac"], 4), "traffic": h["traffic"],
+                     "empirical_peak": ceiling["value"],
+                     "frac_of_empirical": round(h["achieved"] / ceiling["value"], 4)},
+        "copy_ceiling": ceiling,
         "cpu_baseline": cpu,
-        "workloads": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
-                      for r in results.values()],
+        "workloads": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()
+                       if k != "cpu_baseline" or n != HEADLINE}
+                      for n, r in results.items()],
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -530,16 +530,10 @@ __device__ __forceinline__ f32x8 chain_op(uint8_t code, f32x8 acc, f32x8 v) {
 // contiguous per operand); every load of every chunk is issued before the
 // first arithmetic.  Lanes past the end clamp their chunk index for the loads
 // (an in-bounds re-read) and skip the store.
-#ifndef TTLH_CHAIN_U
-#define TTLH_CHAIN_U 1
-#endif
-constexpr int kChainU = TTLH_CHAIN_U;
+constexpr int kChainU = 1;
 
-#ifndef TTLH_CHAIN_WAVES
-#define TTLH_CHAIN_WAVES 8
-#endif
 template <int N, bool BF16, bool ALLVEC>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BF16 ? TTLH_CHAIN_WAVES : 6, BF16 ? TTLH_CHAIN_WAVES : 6)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BF16 ? 8 : 6, BF16 ? 8 : 6)))
 void chain_kernel(const ChainArgs args) {
   constexpr int U = kChainU;
   const uint32_t base = blockIdx.x * (256u * U) + threadIdx.x;

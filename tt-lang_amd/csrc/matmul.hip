@@ -1069,18 +1069,11 @@ bool launch_mm256(MmArgs a, hipStream_t s, int* status) {
   if constexpr (BQ) {
     return launch_mm256_as<true, true, false>(a, s, status);
   } else {
-#ifndef TTLH_MM_NO_DMA
     if (a.c_dtype == TTLH_BF16)
       return a.accumulate ? launch_mm_dma_as<true, true>(a, s, status)
                           : launch_mm_dma_as<true, false>(a, s, status);
     return a.accumulate ? launch_mm_dma_as<false, true>(a, s, status)
                         : launch_mm_dma_as<false, false>(a, s, status);
-#endif
-    if (a.c_dtype == TTLH_BF16)
-      return a.accumulate ? launch_mm256_as<false, true, true>(a, s, status)
-                          : launch_mm256_as<false, true, false>(a, s, status);
-    return a.accumulate ? launch_mm256_as<false, false, true>(a, s, status)
-                        : launch_mm256_as<false, false, false>(a, s, status);
   }
 }
 

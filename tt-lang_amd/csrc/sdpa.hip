@@ -374,19 +374,6 @@ __device__ __forceinline__ void sd_static_for(F&& f) {
   }
 }
 
-#ifdef TTLH_SDPA_TRACE
-__device__ unsigned long long g_pp_trace[16][8][320];
-#define PP_MARK(w)                                                                  \
-  do {                                                                              \
-    if ((w).lane == 0 && blockIdx.x < 16 && (w).ev < 320)                           \
-      g_pp_trace[blockIdx.x][(w).wave][(w).ev] = __builtin_amdgcn_s_memtime();      \
-    ++(w).ev;                                                                       \
-  } while (0)
-#else
-#define PP_MARK(w) \
-  do {             \
-  } while (0)
-#endif
 
 template <int D>
 __device__ __forceinline__ void pp_load(const uint16_t* X, int64_t base, int kv0,
@@ -444,7 +431,6 @@ struct SdpaPP {
   bf16x8 pb[4];
   float m, l;
   u32x4 stk[D / 64], stv[D / 64];
-  int ev = 0;
 
   // stage j = {K(j) if j < n, V(j - 1) if j >= 1} into registers / into LDS
   __device__ __forceinline__ void load_stage(int j) {
@@ -563,11 +549,7 @@ struct SdpaPP {
       ex = xor32_min(fminf(fminf(p4[0], p4[1]), fminf(p4[2], p4[3])));
     }
     const float m_blk = ex * sc;
-#ifdef TTLH_SDPA_NO_LAZY
-    const bool grow = m_blk > m;
-#else
     const bool grow = m_blk > m + kLazy;
-#endif
     if (__any(grow)) {
       const float m_new = grow ? m_blk : m;
       const float alpha = __builtin_amdgcn_exp2f(m - m_new);  // 1 where m stays, 0 at first
@@ -608,26 +590,18 @@ struct SdpaPP {
   // group 0: X(i), write stage i+1 | load stage i+2, Y(i).  The first and
   // last X phases (S only, O only) are peeled so the steady loop has one body.
   __device__ __forceinline__ void run_group0() {
-    PP_MARK(*this);
     x_phase<false, true>(0);
     write_stage(1);
-    PP_MARK(*this);
     pp_boundary();
-    PP_MARK(*this);
     load_stage(2);
     y_phase(0);
-    PP_MARK(*this);
     pp_boundary();
     for (int i = 1; i < n; ++i) {
-      PP_MARK(*this);
       x_phase<true, true>(i);
       write_stage(i + 1);
-      PP_MARK(*this);
       pp_boundary();
-      PP_MARK(*this);
       load_stage(i + 2);
       y_phase(i);
-      PP_MARK(*this);
       pp_boundary();
     }
     x_phase<true, false>(n);
@@ -635,25 +609,17 @@ struct SdpaPP {
   }
   // group 1, one phase behind: Y(i-1), write stage i+1 | load stage i+2, X(i)
   __device__ __forceinline__ void run_group1() {
-    PP_MARK(*this);
     write_stage(1);
-    PP_MARK(*this);
     pp_boundary();
-    PP_MARK(*this);
     load_stage(2);
     x_phase<false, true>(0);
-    PP_MARK(*this);
     pp_boundary();
     for (int i = 1; i < n; ++i) {
-      PP_MARK(*this);
       y_phase(i - 1);
       write_stage(i + 1);
-      PP_MARK(*this);
       pp_boundary();
-      PP_MARK(*this);
       load_stage(i + 2);
       x_phase<true, true>(i);
-      PP_MARK(*this);
       pp_boundary();
     }
     y_phase(n - 1);
