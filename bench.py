@@ -467,10 +467,10 @@ class SdpaWorkload(Workload):
                        "non-causal, fp32 online softmax (BASELINE configs[4])")
 
     def kernel_name(self):
-        # the 64-query kernel serves D = 128, non-causal, positive scale,
+        # the eight-wave kernel serves D = 128, non-causal, positive scale,
         # S % 256 == 0; the ping-pong kernel the other multiples of 256
         if self.D == 128 and self.S % 256 == 0:
-            return "sdpa_q64_kernel"
+            return "sdpa_w8_kernel"
         return "sdpa_pp_kernel" if self.S % 256 == 0 else "sdpa_fwd_kernel"
 
     def work_per_step(self):

@@ -22,10 +22,10 @@
 // 4 consecutive kv of one d column each.
 //
 // Three kernels share that per-wave math:
-//  * sdpa_q64_kernel (D = 128, non-causal, positive scale, S a multiple of
-//    256): 4 waves of 64 queries each, so every K / V fragment read from LDS
-//    feeds two MFMAs; one wave per SIMD interleaves the MFMAs of a KV block
-//    with the softmax of the previous one (details at its definition);
+//  * sdpa_w8_kernel (D = 128, non-causal, positive scale, S a multiple of
+//    256): 8 waves of 32 queries, two per SIMD, each interleaving the MFMAs
+//    of a KV block with the softmax of the previous one, the second wave's
+//    VALU issuing under the first one's MFMAs (details at its definition);
 //  * sdpa_pp_kernel (other cases with S a multiple of 256): 8 waves, 256
 //    queries per workgroup, the two groups of four waves in ping-pong, one
 //    issuing the MFMAs of a block while the other runs the softmax of the
@@ -687,72 +687,75 @@ __global__ __launch_bounds__(PP_THREADS, 1) void sdpa_pp_kernel(const SdpaArgs p
 }
 
 // ---------------------------------------------------------------------------
-// 64 queries per wave, one wave per SIMD (D = 128, positive scale,
-// non-causal): each wave owns two 32-query tiles, so every K / V fragment read
-// from LDS feeds two MFMAs.  KV blocks of 32 rows; step i of the loop is one
-// straight-line block:
-//     MFMAs: S(i) = K(i) Q^T for both tiles and O += V(i-2)^T P(i-2)^T (32)
+// 32 queries per wave, eight waves (two per SIMD) per workgroup of 256
+// queries (D = 128, positive scale, non-causal: C5).  KV blocks of 32 rows;
+// step i of the loop is one straight-line block:
+//     MFMAs: S(i) = K(i) Q^T and O += V(i-2)^T P(i-2)^T (16)
 //     VALU:  the softmax of S(i-1) -> P(i-1), running max / sum
-// A step is eight sections, one per K / V fragment: the section's four
-// MFMAs, each followed by a share of the softmax VALU (a wave issues in
-// order, so the matrix core only overlaps VALU placed between its MFMAs),
-// and the LDS reads of the fragments two sections ahead.  The S accumulators
-// are copied to VGPRs once, after their last MFMA (in the light last
-// section), for the softmax of the next step.  K and V reach
-// LDS by direct-to-LDS DMA (global_load_lds_dwordx4, lane l's 16 bytes at the
-// wave's base + 16 l) into two K and two V buffers: step i reads K(i) and
-// V(i - 2) from buffers i & 1 and fetches K(i + 1), V(i - 1) into the others.
-// Rows are unpadded with XOR-swizzled 16-byte chunks: K chunk c of row r at
-// c ^ (r & 15) (the S operand reads 16 rows of one chunk per 16 lanes), V at
-// c ^ 4 (r & 3) (a transpose read covers 4 rows x 4 chunks per 32 lanes).
-constexpr int Q64_BQ = 256;
-constexpr int Q64_THREADS = 256;
-constexpr int Q64_D = 128;
-constexpr int Q64_KV = 32;
+// in eight sections, one per K / V fragment: the section's two MFMAs, a
+// share of the softmax VALU, and the LDS reads of the fragments two sections
+// ahead.  Two waves per SIMD because a wave alone cannot hide its VALU work:
+// on gfx950 an MFMA holds its own wave's issue for about half of its 32
+// cycles, so VALU placed between one wave's MFMAs mostly adds to them, while
+// a second wave's VALU issues under them (measured: MFMA + 16 FMAs takes 80
+// cycles for one wave, 62 for two).  The cost is LDS traffic: each K / V
+// fragment feeds one MFMA (128 KB per step per CU).  The accumulators fit in
+// the architectural VGPRs (203, no AGPRs), so the softmax reads S without
+// copies.  The waves raise their priority (s_setprio 1) over the first six
+// sections, where MFMAs and LDS reads are densest, so a SIMD's matrix core
+// is fed first and the other wave's VALU fills the gaps.
+// K and V reach LDS by direct-to-LDS DMA (global_load_lds_dwordx4, lane l's
+// 16 bytes at the wave's base + 16 l) into two K and two V buffers: step i
+// reads K(i) and V(i - 2) from buffers i & 1 and fetches K(i + 1), V(i - 1)
+// into the others; one workgroup barrier per step.  Rows are unpadded with
+// XOR-swizzled 16-byte chunks: K chunk c of row r at c ^ (r & 15) (the S
+// operand reads 16 rows of one chunk per 16 lanes), V at c ^ 4 (r & 3) (a
+// transpose read covers 4 rows x 4 chunks per 32 lanes).
+constexpr int W8_BQ = 256;
+constexpr int W8_THREADS = 512;
+constexpr int W8_D = 128;
+constexpr int W8_KV = 32;
 
-__shared__ __attribute__((aligned(16))) uint16_t q64K0[Q64_KV * Q64_D], q64K1[Q64_KV * Q64_D];
-__shared__ __attribute__((aligned(16))) uint16_t q64V0[Q64_KV * Q64_D], q64V1[Q64_KV * Q64_D];
+__shared__ __attribute__((aligned(16))) uint16_t w8K0[W8_KV * W8_D], w8K1[W8_KV * W8_D];
+__shared__ __attribute__((aligned(16))) uint16_t w8V0[W8_KV * W8_D], w8V1[W8_KV * W8_D];
 
 template <int B>
-__device__ __forceinline__ uint16_t* q64_kbuf() {
-  if constexpr (B == 0) return q64K0;
-  else return q64K1;
+__device__ __forceinline__ uint16_t* w8_kbuf() {
+  if constexpr (B == 0) return w8K0;
+  else return w8K1;
 }
 template <int B>
-__device__ __forceinline__ uint16_t* q64_vbuf() {
-  if constexpr (B == 0) return q64V0;
-  else return q64V1;
+__device__ __forceinline__ uint16_t* w8_vbuf() {
+  if constexpr (B == 0) return w8V0;
+  else return w8V1;
 }
 
-typedef __attribute__((address_space(3))) void q64_lds_void;
+typedef __attribute__((address_space(3))) void w8_lds_void;
 
-struct SdpaQ64 {
-  static constexpr int D = Q64_D, ND = D / 32, NDC = D / 16;
+struct SdpaW8 {
+  static constexpr int D = W8_D, ND = D / 32, NDC = D / 16;
   static constexpr float kLazy = 8.0f;
 
   const SdpaArgs& p;
   int64_t base;
   int qb, wave, lane, l32, h, n;
   float sc;
-  bf16x8 qop[2][NDC];       // Q^T operands of the two query tiles
-  f32x16 o[2][ND];          // O^T accumulators
-  f32x16 s[2];              // [tile]: S(i) accumulating
-  f32x16 sv[2];             // [tile]: S(i - 1), copied out after its last MFMA
-  u32x4 pw[2][2][2];        // [parity][tile][kv chunk]: P(i - 1), P(i - 2) as bf16 pairs
-  float m[2], l[2], alpha[2];
-  int k_src[2], v_src[2];   // per-lane DMA source offsets (elements)
+  bf16x8 qop[NDC];          // Q^T operands
+  f32x16 o[ND];             // O^T accumulators
+  f32x16 s;                 // S(i) accumulating
+  f32x16 sv;                // S(i - 1) (renamed, not copied: both live in VGPRs)
+  u32x4 pw[2][2];           // [parity][kv chunk]: P(i - 1), P(i - 2) as bf16 pairs
+  float m, l, alpha;
+  int k_src, v_src;         // per-lane DMA source offsets (elements)
   int v_frag[ND];           // LDS offsets of the V transpose reads
   uint32_t lds_wave;        // the wave's byte offset in a K / V buffer (uniform)
 
   __device__ __forceinline__ void setup() {
-    lds_wave = __builtin_amdgcn_readfirstlane(wave * 2048);
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int pos = (wave * 2 + q) * 64 + lane;  // 16-byte chunk position in the buffer
-      const int r = pos >> 4, c = pos & 15;
-      k_src[q] = r * D + ((c ^ (r & 15)) << 3);
-      v_src[q] = r * D + ((c ^ ((r & 3) << 2)) << 3);
-    }
+    lds_wave = __builtin_amdgcn_readfirstlane(wave * 1024);
+    const int pos = wave * 64 + lane;  // 16-byte chunk position in the buffer
+    const int r = pos >> 4, c = pos & 15;
+    k_src = r * D + ((c ^ (r & 15)) << 3);
+    v_src = r * D + ((c ^ ((r & 3) << 2)) << 3);
     // V transpose reads: row kv0 + (lane & 15) / 4, logical column d0 + 4 (lane & 3),
     // d0 = 32 j + 16 ((lane >> 4) & 1), i.e. chunk 4 j + 2 ((lane >> 4) & 1) + (lane & 3) / 2
     const int vr = (lane & 15) >> 2;
@@ -763,28 +766,26 @@ struct SdpaQ64 {
     }
   }
 
-  // 32 K or V rows from kv0 into a buffer: 2 DMA instructions per thread.
-  // Issued as inline asm: the compiler's wait-count model treats an
-  // outstanding LDS DMA as making LDS reads complete out of order and then
-  // waits for every LDS read (lgkmcnt(0)) before each use, which defeats the
-  // fragment prefetch.  The DMA only counts on vmcnt (waited explicitly at
-  // the end of every step, before any wave reads the buffer), and the loop
-  // has no other vector-memory loads the compiler's counts would have to
-  // include.  M0 carries the wave's LDS base (one wait state before use).
+  // 32 K or V rows from kv0 into a buffer: one DMA instruction per thread,
+  // issued as inline asm: with a compiler-visible LDS DMA outstanding, the
+  // compiler's wait-count model treats LDS reads as completing out of order
+  // and waits for every LDS read (lgkmcnt(0)) before each use, which defeats
+  // the fragment prefetch.  The DMA counts only on vmcnt, waited explicitly
+  // at the end of every step, before any wave reads the buffer; the loop has
+  // no other vector-memory loads.  M0 carries the wave's LDS base (one wait
+  // state before use).
   template <int BUF>
-  __device__ __forceinline__ void dma(const uint16_t* X, const int (&src)[2], int kv0) {
+  __device__ __forceinline__ void dma(const uint16_t* X, int src, int kv0) {
     const uint16_t* g = X + base + static_cast<int64_t>(kv0) * D;
     const uint32_t buf = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
-        (q64_lds_void*)(BUF < 2 ? q64_kbuf<BUF & 1>() : q64_vbuf<BUF & 1>())));
-#pragma unroll
-    for (int q = 0; q < 2; ++q)
-      asm volatile(
-          "s_mov_b32 m0, %0\n\t"
-          "s_nop 0\n\t"
-          "global_load_lds_dwordx4 %1, off"
-          :
-          : "s"(buf + lds_wave + 1024 * q), "v"(g + src[q])
-          : "memory", "m0");
+        (w8_lds_void*)(BUF < 2 ? w8_kbuf<BUF & 1>() : w8_vbuf<BUF & 1>())));
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, off"
+        :
+        : "s"(buf + lds_wave), "v"(g + src)
+        : "memory", "m0");
   }
 
   // K fragment (d chunk dc): row l32, 8 elements at 16 dc + 8 h (chunk 2 dc + h)
@@ -802,14 +803,13 @@ struct SdpaQ64 {
     return __builtin_bit_cast(bf16x8, w);
   }
 
-  // The softmax of S(i - 1) (sv, both tiles) into pw[PAR], cut into
-  // sections of similar VALU cost, one per MFMA section of a step:
-  //   0, 1: block max and running max of tile 0, 1
-  //   1..5: exponentials of S values (4 per unit) with bf16 packing and the
-  //         partial row sums
-  //   5:    running row sums
+  // The softmax of S(i - 1) (sv) into pw[PAR], cut into sections of similar
+  // VALU cost, one per MFMA section of a step:
+  //   0:    block max and running max (lazy: moves only by > kLazy log2 units)
+  //   1..4: exponentials of 4 S values each, bf16 packing, partial row sums
+  //   5:    running row sum
   // Row maxima use v_maximum3 (NaN-propagating, no canonicalisation).
-  float mnew_[2], rsum_[2];
+  float mnew_, rsum_;
 
   __device__ __forceinline__ static float max16(const f32x16& c) {
     const float a = __builtin_elementwise_maximum(__builtin_elementwise_maximum(c[0], c[1]), c[2]);
@@ -818,73 +818,48 @@ struct SdpaQ64 {
     const float e = __builtin_elementwise_maximum(__builtin_elementwise_maximum(c[9], c[10]), c[11]);
     const float f = __builtin_elementwise_maximum(__builtin_elementwise_maximum(c[12], c[13]), c[14]);
     const float g = __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), d);
-    const float h = __builtin_elementwise_maximum(__builtin_elementwise_maximum(e, f), c[15]);
-    return __builtin_elementwise_maximum(g, h);
+    const float hh = __builtin_elementwise_maximum(__builtin_elementwise_maximum(e, f), c[15]);
+    return __builtin_elementwise_maximum(g, hh);
   }
 
-  // running max of tile qt from its block max (lazy: moves only by > kLazy)
-  template <int QT>
   __device__ __forceinline__ void run_max(float mx) {
     const float m_blk = xor32_max(mx) * sc;
-    mnew_[QT] = m_blk > m[QT] + kLazy ? m_blk : m[QT];
-    alpha[QT] = __builtin_amdgcn_exp2f(m[QT] - mnew_[QT]);
-    m[QT] = mnew_[QT];
+    mnew_ = m_blk > m + kLazy ? m_blk : m;
+    alpha = __builtin_amdgcn_exp2f(m - mnew_);
+    m = mnew_;
   }
 
-  // exponentials of S values 4G .. 4G + 3 of tile QT into P (two dwords)
-  template <int PAR, int QT, int G>
+  // exponentials of S values 4G .. 4G + 3 into P (two dwords)
+  template <int PAR, int G>
   __device__ __forceinline__ void expo4() {
-    const f32x16& cur = sv[QT];
     float e[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      e[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(cur[4 * G + r], sc, -mnew_[QT]));
-    pw[PAR][QT][G >> 1][2 * (G & 1)] = pk_bf16(e[0], e[1]);
-    pw[PAR][QT][G >> 1][2 * (G & 1) + 1] = pk_bf16(e[2], e[3]);
+      e[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[4 * G + r], sc, -mnew_));
+    pw[PAR][G >> 1][2 * (G & 1)] = pk_bf16(e[0], e[1]);
+    pw[PAR][G >> 1][2 * (G & 1) + 1] = pk_bf16(e[2], e[3]);
     const float part = (e[0] + e[1]) + (e[2] + e[3]);
-    rsum_[QT] = G == 0 ? part : rsum_[QT] + part;
+    rsum_ = G == 0 ? part : rsum_ + part;
   }
 
   template <int PAR, int X>
   __device__ __forceinline__ void softmax_section() {
-    if constexpr (X == 0) {
-      run_max<0>(max16(sv[0]));
-    } else if constexpr (X == 1) {
-      run_max<1>(max16(sv[1]));
-      expo4<PAR, 0, 0>();
-    } else if constexpr (X == 2) {
-      expo4<PAR, 0, 1>();
-      expo4<PAR, 0, 2>();
-    } else if constexpr (X == 3) {
-      expo4<PAR, 0, 3>();
-      expo4<PAR, 1, 0>();
-    } else if constexpr (X == 4) {
-      expo4<PAR, 1, 1>();
-      expo4<PAR, 1, 2>();
-    } else if constexpr (X == 5) {
-      expo4<PAR, 1, 3>();
-#pragma unroll
-      for (int qt = 0; qt < 2; ++qt) l[qt] = l[qt] * alpha[qt] + xor32_add(rsum_[qt]);
-    }
+    if constexpr (X == 0) run_max(max16(sv));
+    else if constexpr (X >= 1 && X <= 4) expo4<PAR, X - 1>();
+    else if constexpr (X == 5) l = l * alpha + xor32_add(rsum_);
   }
 
-  // VALU slots of a section (for the interleave below); section 7 holds the
-  // copy of S(i) out of the accumulators
-  static constexpr int kSectionValu[8] = {16, 34, 36, 36, 36, 26, 0, 32};
+  // VALU slots of a section (for the interleave below)
+  static constexpr int kSectionValu[8] = {12, 18, 18, 18, 18, 6, 0, 16};
 
-  // one step (see the header): S(i) into s (copied to sv at the end), softmax of sv into
-  // pw[PAR ^ 1], O += V(i-2) P(i-2) with P(i-2) in pw[PAR].  Explicitly
-  // sequenced in eight sections (one per 16-wide d chunk / V fragment): a
-  // section issues its MFMAs one at a time with a share of the section's
-  // softmax VALU after each (a wave issues in order, so back-to-back MFMAs
-  // would stall the VALU behind the matrix core), and requests the LDS
-  // fragments of the section two ahead.
+  // one step (see the header): S(i) into s (renamed to sv at the end),
+  // softmax of sv into pw[PAR ^ 1], O += V(i-2) P(i-2) with P(i-2) in pw[PAR]
   template <int PAR, bool DO_S, bool DO_SM, bool DO_O>
   __device__ __forceinline__ void step(int i) {
-    const uint16_t* Kc = q64_kbuf<PAR>();
-    const uint16_t* Vc = q64_vbuf<PAR>();
-    if (i + 1 < n) dma<PAR ^ 1>(p.K, k_src, (i + 1) * Q64_KV);
-    if (i >= 1 && i - 1 < n) dma<2 + (PAR ^ 1)>(p.V, v_src, (i - 1) * Q64_KV);
+    const uint16_t* Kc = w8_kbuf<PAR>();
+    const uint16_t* Vc = w8_vbuf<PAR>();
+    if (i + 1 < n) dma<PAR ^ 1>(p.K, k_src, (i + 1) * W8_KV);
+    if (i >= 1 && i - 1 < n) dma<2 + (PAR ^ 1)>(p.V, v_src, (i - 1) * W8_KV);
     __builtin_amdgcn_sched_barrier(0);
     bf16x8 kf[8], vf[8];
     auto issue = [&](auto xc) {
@@ -897,24 +872,19 @@ struct SdpaQ64 {
     __builtin_amdgcn_sched_barrier(0);
     sd_static_for<8>([&](auto xc) {
       constexpr int x = decltype(xc)::value;
+      if constexpr (x == 0) __builtin_amdgcn_s_setprio(1);
+      if constexpr (x == 6) __builtin_amdgcn_s_setprio(0);
       if constexpr (DO_S) {
         const f32x16 z = {};
-        s[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[x], qop[0][x], x == 0 ? z : s[0], 0, 0, 0);
-        s[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[x], qop[1][x], x == 0 ? z : s[1], 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[x], qop[x], x == 0 ? z : s, 0, 0, 0);
       }
-      if constexpr (DO_O) {
-        o[0][x >> 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            vf[x], __builtin_bit_cast(bf16x8, pw[PAR][0][x & 1]), o[0][x >> 1], 0, 0, 0);
-        o[1][x >> 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            vf[x], __builtin_bit_cast(bf16x8, pw[PAR][1][x & 1]), o[1][x >> 1], 0, 0, 0);
-      }
+      if constexpr (DO_O)
+        o[x >> 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            vf[x], __builtin_bit_cast(bf16x8, pw[PAR][x & 1]), o[x >> 1], 0, 0, 0);
       if constexpr (x + 2 < 8) issue(std::integral_constant<int, x + 2>());
       if constexpr (DO_SM) softmax_section<PAR ^ 1, x>();
-      if constexpr (DO_S && x == 7) {
-        sv[0] = s[0];  // the softmax of the next step reads S(i) from VGPRs
-        sv[1] = s[1];
-      }
-      constexpr int nm = (DO_S ? 2 : 0) + (DO_O ? 2 : 0);
+      if constexpr (DO_S && x == 7) sv = s;  // the next step's softmax reads S(i)
+      constexpr int nm = (DO_S ? 1 : 0) + (DO_O ? 1 : 0);
       constexpr int nv = DO_SM ? (kSectionValu[x] + nm - 1) / nm : 0;
       sd_static_for<nm>([&](auto) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
@@ -925,11 +895,9 @@ struct SdpaQ64 {
     });
     if constexpr (DO_SM) {
       // O rescale for P(i-1) (rare: the running max moves by more than kLazy)
-      if (__any(alpha[0] != 1.0f || alpha[1] != 1.0f)) {
+      if (__any(alpha != 1.0f)) {
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-          for (int j = 0; j < ND; ++j) o[qt][j] *= alpha[qt];
+        for (int j = 0; j < ND; ++j) o[j] *= alpha;
       }
     }
     // the next stage landed, this stage's reads are done: release / publish
@@ -941,38 +909,30 @@ struct SdpaQ64 {
   }
 };
 
-__global__ __launch_bounds__(Q64_THREADS, 1) void sdpa_q64_kernel(const SdpaArgs p) {
-  SdpaQ64 w{p};
+__global__ __launch_bounds__(W8_THREADS, 1) void sdpa_w8_kernel(const SdpaArgs p) {
+  SdpaW8 w{p};
   int bh;
   block_coords(p, bh, w.qb);
   w.lane = threadIdx.x & 63;
   w.wave = threadIdx.x >> 6;
   w.l32 = w.lane & 31;
   w.h = w.lane >> 5;
-  w.base = static_cast<int64_t>(bh) * p.S * Q64_D;
+  w.base = static_cast<int64_t>(bh) * p.S * W8_D;
   w.sc = p.scale_log2;
-  w.n = p.S / Q64_KV;
-#pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    w.m[qt] = -INFINITY;
-    w.l[qt] = 0.0f;
-    w.alpha[qt] = 1.0f;
-  }
+  w.n = p.S / W8_KV;
+  w.m = -INFINITY;
+  w.l = 0.0f;
+  w.alpha = 1.0f;
   w.setup();
-  // Q^T of the wave's two tiles: query row qb*256 + 64 wave + 32 qt + l32
+  // Q^T of the wave's tile: query row qb * 256 + 32 wave + l32
+  const int64_t q = static_cast<int64_t>(w.qb) * W8_BQ + 32 * w.wave + w.l32;
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    const int64_t q = static_cast<int64_t>(w.qb) * Q64_BQ + 64 * w.wave + 32 * qt + w.l32;
+  for (int dc = 0; dc < SdpaW8::NDC; ++dc)
+    w.qop[dc] = *reinterpret_cast<const bf16x8*>(p.Q + w.base + q * W8_D + dc * 16 + 8 * w.h);
 #pragma unroll
-    for (int dc = 0; dc < SdpaQ64::NDC; ++dc)
-      w.qop[qt][dc] = *reinterpret_cast<const bf16x8*>(p.Q + w.base + q * Q64_D + dc * 16 + 8 * w.h);
-  }
+  for (int j = 0; j < SdpaW8::ND; ++j)
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-    for (int j = 0; j < SdpaQ64::ND; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) w.o[qt][j][r] = 0.0f;
+    for (int r = 0; r < 16; ++r) w.o[j][r] = 0.0f;
   // K(0) into buffer 0 (with Q landed), then the pipeline
   w.dma<0>(p.K, w.k_src, 0);
   __builtin_amdgcn_s_waitcnt(0x0070);
@@ -991,32 +951,28 @@ __global__ __launch_bounds__(Q64_THREADS, 1) void sdpa_q64_kernel(const SdpaArgs
   w.step<0, false, true, true>(i);
   w.step<1, false, false, true>(i + 1);
   // O[q][d], d = 32j + 8u + 4h + i
+  const float inv = 1.0f / w.l;
+  uint16_t* orow = p.O + w.base + q * W8_D;
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
-    const float inv = 1.0f / w.l[qt];
-    const int64_t q = static_cast<int64_t>(w.qb) * Q64_BQ + 64 * w.wave + 32 * qt + w.l32;
-    uint16_t* orow = p.O + w.base + q * Q64_D;
+  for (int j = 0; j < SdpaW8::ND; ++j)
 #pragma unroll
-    for (int j = 0; j < SdpaQ64::ND; ++j)
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int d = 32 * j + 8 * u + 4 * w.h;
-        const u32x2 v = {pk_bf16(w.o[qt][j][4 * u] * inv, w.o[qt][j][4 * u + 1] * inv),
-                         pk_bf16(w.o[qt][j][4 * u + 2] * inv, w.o[qt][j][4 * u + 3] * inv)};
-        *reinterpret_cast<u32x2*>(orow + d) = v;
-      }
-  }
+    for (int u = 0; u < 4; ++u) {
+      const int d = 32 * j + 8 * u + 4 * w.h;
+      const u32x2 v = {pk_bf16(w.o[j][4 * u] * inv, w.o[j][4 * u + 1] * inv),
+                       pk_bf16(w.o[j][4 * u + 2] * inv, w.o[j][4 * u + 3] * inv)};
+      *reinterpret_cast<u32x2*>(orow + d) = v;
+    }
 }
 
 template <int D, bool CAUSAL>
 int launch(const SdpaArgs& a, hipStream_t s) {
-  // the 64-query kernel takes its running max from the raw block max, which
+  // the eight-wave kernel takes its running max from the raw block max, which
   // needs a positive scale
-  if (D == Q64_D && !CAUSAL && a.S % Q64_BQ == 0 && a.scale_log2 > 0.0f) {
+  if (D == W8_D && !CAUSAL && a.S % W8_BQ == 0 && a.scale_log2 > 0.0f) {
     SdpaArgs b = a;
-    b.nqb = a.S / Q64_BQ;
-    hipLaunchKernelGGL(sdpa_q64_kernel, dim3(b.nbh * b.nqb), dim3(Q64_THREADS), 0, s, b);
-    return check_launch("sdpa_q64_kernel");
+    b.nqb = a.S / W8_BQ;
+    hipLaunchKernelGGL(sdpa_w8_kernel, dim3(b.nbh * b.nqb), dim3(W8_THREADS), 0, s, b);
+    return check_launch("sdpa_w8_kernel");
   }
   if (a.S % PP_BQ == 0) {
     SdpaArgs b = a;
