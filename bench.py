@@ -455,8 +455,12 @@ class Bfp8MatmulWorkload(Workload):
                           "(no simulator path exists for bfloat8_b)"}
 
 
-class SdpaWorkload(Workload):
-    """C5: softmax(Q K^T / sqrt(D)) V, bf16 [B, H, S, D], non-causal (C ABI)."""
+class SdpaWorkload(PlanWorkload):
+    """C5 through the drop-in: attention written tile by tile with the spec's
+    ops (tests/kernel_lib.py make_attention: @, reduce_max, exp, broadcast,
+    reduce_sum, recip over intermediate CBs, 8x8 grid), planned onto one
+    fused ttlh_sdpa_fwd launch; Q, V, out [B*H*S, D] and K^T as the
+    transposed view of K rows (no staging copy)."""
 
     bound = "mfma"
     unit = "TFLOP/s"
@@ -464,7 +468,9 @@ class SdpaWorkload(Workload):
     def __init__(self, name, B, H, S, D, seed=7):
         self.name, self.B, self.H, self.S, self.D, self.seed = name, B, H, S, D, seed
         self.config = (f"fused SDPA fwd Q,K,V bf16 [{B},{H},{S},{D}], N(0,1), scale 1/sqrt({D}), "
-                       "non-causal, fp32 online softmax (BASELINE configs[4])")
+                       "non-causal, fp32 online softmax (BASELINE configs[4]); tile program "
+                       "of @ / reduce_max / exp / broadcast / reduce_sum / recip through the "
+                       "drop-in")
 
     def kernel_name(self):
         # the eight-wave kernel serves D = 128, non-causal, positive scale,
@@ -476,38 +482,48 @@ class SdpaWorkload(Workload):
     def work_per_step(self):
         return 4.0 * self.B * self.H * self.S * self.S * self.D
 
-    def setup(self):
+    def make_sets(self):
+        import kernel_lib as KL
+        import ttl
+        import ttnn
         from oracle.tile_ops import seeded
-        shape = (self.B, self.H, self.S, self.D)
-        self.q, self.k, self.v = (seeded(shape, "normal", self.seed + i).cuda() for i in range(3))
-        self.o = torch.empty_like(self.q)
+        n = self.B * self.H * self.S
         self.scale = 1.0 / math.sqrt(self.D)
-        self._args = (self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.o.data_ptr(),
-                      self.B, self.H, self.S, self.D, self.scale, 0)
+        self.kernel = KL.make_attention(ttl, self.S, self.scale, grid=(8, 8))
+        q, k, v = (seeded((n, self.D), "normal", self.seed + i).cuda() for i in range(3))
+        return [[ttnn.Tensor(q), ttnn.Tensor(k.t()), ttnn.Tensor(v),
+                 ttnn.empty((n, self.D), dtype=torch.bfloat16)]]
 
-    def launch(self, i):
-        from ttlhip import _lib as L
-        L.call("ttlh_sdpa_fwd", *self._args, L.stream_ptr())
+    def setup(self):
+        super().setup()
+        from ttlhip import plan as P
+        assert isinstance(self.plan.launches[0], P.SdpaLaunch), self.plan.describe()
 
     def check(self):
         from oracle.tile_ops import sdpa_ref
         self.launch(0)
         torch.cuda.synchronize()
-        ref = sdpa_ref(self.q[:1, :1].cpu(), self.k[:1, :1].cpu(), self.v[:1, :1].cpu(), self.scale)
-        got = self.o[:1, :1].cpu().double()
+        q, kt, v, o = (x._tensor for x in self.sets[0])
+        S, D = self.S, self.D
+        h = self.B * self.H - 1  # the last (batch, head) pair
+        rows = slice(h * S, (h + 1) * S)
+        ref = sdpa_ref(*(x[rows].cpu().view(1, 1, S, D) for x in (q, kt.t(), v)), self.scale)
+        got = o[rows].cpu().double().view(1, 1, S, D)
         return {"max_abs_err_rel": float((got - ref).abs().max() / ref.abs().max()),
                 "heads_checked": 1, "oracle": "float64 softmax(QK^T s)V"}
 
     def cpu_baseline(self):
-        from oracle.tile_ops import sdpa_ref
-        heads = 2
-        q, k, v = (t[:1, :heads].cpu() for t in (self.q, self.k, self.v))
-        dt, reps = _repeat(lambda: sdpa_ref(q, k, v, self.scale, dtype=torch.float32))
-        return {"value": round(4.0 * heads * self.S * self.S * self.D / dt / 1e12, 6),
-                "unit": "TFLOP/s", "cores": torch.get_num_threads(), "kind": "port",
-                "sample": f"{heads} of the {self.B * self.H} (batch, head) pairs through the "
-                          f"oracle's softmax(Q K^T s) V in float32 torch on the CPU, {reps} runs "
-                          f"of {dt:.2f} s (no simulator path exists for attention)"}
+        import kernel_lib as KL
+        from oracle.tile_ops import seeded
+        S, D = self.S, self.D
+        q, k, v = (seeded((S, D), "normal", self.seed + 10 + i) for i in range(3))
+        t = [q, k.t().contiguous(), v, torch.zeros(S, D, dtype=torch.bfloat16)]
+        dt, reps = _eager(lambda ns: KL.make_attention(ns, S, self.scale, grid=(1, 1)), t)
+        return {"value": round(4.0 * S * S * D / dt / 1e12, 8), "unit": "TFLOP/s", "cores": 1,
+                "kind": "port",
+                "sample": f"one of the {self.B * self.H} (batch, head) pairs (S {S}, D {D}) "
+                          f"through the eager tile-by-tile oracle executor running the same "
+                          f"attention tile program (1 thread), {reps} run(s) of {dt:.2f} s"}
 
 
 WORKLOADS = {

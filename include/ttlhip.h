@@ -251,6 +251,16 @@ int ttlh_tilize(const void* src, int64_t src_ld, void* dst, int64_t rows,
 int ttlh_untilize(const void* src, void* dst, int64_t dst_ld, int64_t rows,
                   int64_t cols, int elem_bytes, void* stream);
 
+/* dst[c, r] = src[r, c] for a bf16 [rows, cols] matrix (row strides in
+ * elements).  No counterpart in the reference: it stages the K^T operand
+ * [D, B*H*S] of an attention tile program (matmul of Q by K^T) as the K
+ * [B*H*S, D] rows ttlh_sdpa_fwd reads, when K^T is not already the
+ * transposed view of such rows.  rows, cols, strides: multiples of 8;
+ * buffers 16-byte aligned and disjoint.                                  */
+int ttlh_transpose_bf16(const void* src, int64_t src_ld, void* dst,
+                        int64_t dst_ld, int64_t rows, int64_t cols,
+                        void* stream);
+
 /* ------------------------------------------------------------------------
  * Tile matmul:  C[M,N] (=|+=) A[M,K] . B[K,N]
  *

@@ -167,7 +167,23 @@ class _Tiles:
     def __truediv__(self, o): return self._bin(o, operator.truediv)
     def __floordiv__(self, o): return self._bin(o, operator.floordiv)
     def __mod__(self, o): return self._bin(o, operator.mod)
-    def __matmul__(self, o): return self._bin(o, operator.matmul)
+    def __matmul__(self, o):
+        o = _tiles_of(o)
+        (m, k), (k2, n) = self.shape, o.shape
+        if k == k2 and k > 1 and any(l != r and l != 1 and r != 1
+                                     for l, r in zip(self.shape, o.shape)):
+            # the spec's block matmul (TTLangSpecification.md:693), defined
+            # where the simulator's tile-wise pairing raises: tile (i, j) =
+            # sum over k of a(i, k) @ b(k, j) in fp32, rounded once
+            dt = torch.promote_types(self.tiles[0].dtype, o.tiles[0].dtype)
+            out = []
+            for i in range(m):
+                for j in range(n):
+                    acc = sum(self.tiles[i * k + t].float() @ o.tiles[t * n + j].float()
+                              for t in range(k))
+                    out.append(acc.to(dt))
+            return _Tiles(out, (m, n))
+        return self._bin(o, operator.matmul)
 
     def __pow__(self, o):
         if isinstance(o, int):

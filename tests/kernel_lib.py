@@ -1103,3 +1103,126 @@ def make_row_bcast_forms(ttl, with_out: bool, grid=(1, 1)):
                         ttl.copy(ob, out[2 * i:2 * i + 2, 2 * j:2 * j + 2]).wait()
 
     return row_bcast_forms
+
+
+def make_attention(ttl, seq, scale, grid=(8, 8), exp_form="scaled_max", norm="recip",
+                   sum_scale=1.0, max_scale=None, own_head=True):
+    """O = softmax(Q K^T * scale) V written with the spec's block ops
+    (TTLangSpecification.md:693-761: block matmul `@`, reduce_max,
+    exp, broadcast, reduce_sum, recip), one query tile row of one (batch,
+    head) per work item: q, v, out are [B*H*seq, D] and kt is K^T of every
+    head side by side, [D, B*H*seq] (the spec has no transpose: the caller
+    passes it, e.g. as a transposed view of K).  Every stage goes through an
+    intermediate CB: the score row S (1 x seq/32 tiles), its scaled maximum,
+    P = exp(S * scale - max), its row sum, P @ V, and the normalised output.
+
+    Variants: exp_form "scaled_diff" writes P = exp((S - max) * scale) over
+    an unscaled maximum; norm "div" writes O / L instead of O * recip(L);
+    sum_scale / max_scale are the reductions' scalers (default 1 and
+    `scale`, or 1 for "scaled_diff"); own_head=False reads the keys and
+    values of the first head for every query (not attention per head)."""
+    if max_scale is None:
+        max_scale = scale if exp_form == "scaled_max" else 1.0
+    @ttl.kernel(grid=grid)
+    def attention(q, kt, v, out):
+        dt = q.shape[1] // TILE
+        st = seq // TILE
+        items = q.shape[0] // TILE
+        ncores = grid[0] * grid[1]
+        per = -(-items // ncores)
+        q_cb = ttl.make_circular_buffer_like(q, shape=(1, dt), buffer_factor=2)
+        k_cb = ttl.make_circular_buffer_like(kt, shape=(dt, st), buffer_factor=2)
+        v_cb = ttl.make_circular_buffer_like(v, shape=(st, dt), buffer_factor=2)
+        s_cb = ttl.make_circular_buffer_like(q, shape=(1, st), buffer_factor=2)
+        m_cb = ttl.make_circular_buffer_like(q, shape=(1, 1), buffer_factor=2)
+        p_cb = ttl.make_circular_buffer_like(q, shape=(1, st), buffer_factor=2)
+        l_cb = ttl.make_circular_buffer_like(q, shape=(1, 1), buffer_factor=2)
+        o_cb = ttl.make_circular_buffer_like(q, shape=(1, dt), buffer_factor=2)
+        y_cb = ttl.make_circular_buffer_like(out, shape=(1, dt), buffer_factor=2)
+
+        @ttl.compute()
+        def comp():
+            c = ttl.core(dims=1)
+            for _ in range(c * per, min(items, (c + 1) * per)):
+                with q_cb.wait() as qb, k_cb.wait() as kb, s_cb.reserve() as sb:
+                    sb.store(qb @ kb)
+                with s_cb.wait() as sb:
+                    with m_cb.reserve() as mb:
+                        mb.store(ttl.math.reduce_max(sb, max_scale, dims=[1]))
+                    with m_cb.wait() as mb, p_cb.reserve() as pb:
+                        mx = ttl.math.broadcast(mb, pb, dims=[1])
+                        if exp_form == "scaled_max":
+                            pb.store(ttl.math.exp(sb * scale - mx))
+                        else:
+                            pb.store(ttl.math.exp((sb - mx) * scale))
+                with p_cb.wait() as pb:
+                    with l_cb.reserve() as lb:
+                        lb.store(ttl.math.reduce_sum(pb, sum_scale, dims=[1]))
+                    with v_cb.wait() as vb, o_cb.reserve() as ob:
+                        ob.store(pb @ vb)
+                with o_cb.wait() as ob, l_cb.wait() as lb, y_cb.reserve() as yb:
+                    if norm == "recip":
+                        yb.store(ob * ttl.math.broadcast(ttl.math.recip(lb), yb, dims=[1]))
+                    else:
+                        yb.store(ob / ttl.math.broadcast(lb, yb, dims=[1]))
+
+        @ttl.datamovement()
+        def rd():
+            c = ttl.core(dims=1)
+            for r in range(c * per, min(items, (c + 1) * per)):
+                h0 = (r // st) * st if own_head else 0
+                with q_cb.reserve() as qb, k_cb.reserve() as kb:
+                    tq = ttl.copy(q[r:r + 1, 0:dt], qb)
+                    tk = ttl.copy(kt[0:dt, h0:h0 + st], kb)
+                    tq.wait()
+                    tk.wait()
+                with v_cb.reserve() as vb:
+                    ttl.copy(v[h0:h0 + st, 0:dt], vb).wait()
+
+        @ttl.datamovement()
+        def wr():
+            c = ttl.core(dims=1)
+            for r in range(c * per, min(items, (c + 1) * per)):
+                with y_cb.wait() as yb:
+                    ttl.copy(yb, out[r:r + 1, 0:dt]).wait()
+
+    return attention
+
+
+def make_block_matmul(ttl, bm, bk, bn):
+    """out = a @ b with one (bm, bk) @ (bk, bn) block matmul per output block
+    (the spec's block matmul, TTLangSpecification.md:693), the whole K of a
+    and b in one block each: a [bm*32*R, bk*32], b [bk*32, bn*32*C]."""
+    @ttl.kernel(grid=(1, 1))
+    def block_mm(a, b, out):
+        R = a.shape[0] // (bm * TILE)
+        C = b.shape[1] // (bn * TILE)
+        a_cb = ttl.make_circular_buffer_like(a, shape=(bm, bk), buffer_factor=2)
+        b_cb = ttl.make_circular_buffer_like(b, shape=(bk, bn), buffer_factor=2)
+        o_cb = ttl.make_circular_buffer_like(out, shape=(bm, bn), buffer_factor=2)
+
+        @ttl.compute()
+        def comp():
+            for _ in range(R):
+                for _ in range(C):
+                    with a_cb.wait() as ab, b_cb.wait() as bb, o_cb.reserve() as ob:
+                        ob.store(ab @ bb)
+
+        @ttl.datamovement()
+        def reader():
+            for r in range(R):
+                for c in range(C):
+                    with a_cb.reserve() as ab, b_cb.reserve() as bb:
+                        ta = ttl.copy(a[r * bm:(r + 1) * bm, 0:bk], ab)
+                        tb = ttl.copy(b[0:bk, c * bn:(c + 1) * bn], bb)
+                        ta.wait()
+                        tb.wait()
+
+        @ttl.datamovement()
+        def writer():
+            for r in range(R):
+                for c in range(C):
+                    with o_cb.wait() as ob:
+                        ttl.copy(ob, out[r * bm:(r + 1) * bm, c * bn:(c + 1) * bn]).wait()
+
+    return block_mm

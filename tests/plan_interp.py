@@ -10,7 +10,7 @@ import torch
 
 from oracle import tile_ops as O
 from ttlhip import _lib as L
-from ttlhip.plan import EltwiseLaunch, MatmulLaunch, ReduceLaunch
+from ttlhip.plan import EltwiseLaunch, MatmulLaunch, ReduceLaunch, SdpaLaunch
 
 _TORCH_BIN = {
     L.OP["add"]: torch.add, L.OP["sub"]: torch.sub, L.OP["mul"]: torch.mul,
@@ -125,6 +125,18 @@ def run_matmul(l: MatmulLaunch, args):
     c[r0:r1, c0:c1] = (a[r0:r1].double() @ b[:, c0:c1].double()).to(c.dtype)
 
 
+def run_sdpa(l: SdpaLaunch, args):
+    """Fused attention: the oracle's softmax(Q K^T s) V in float32 per head
+    (the fused kernel keeps S, P and the row statistics in fp32), rounded
+    once to the output dtype."""
+    q, kt, v, y = (r.resolve(args) for r in (l.q, l.kt, l.v, l.out))
+    D = q.shape[1]
+    shape = (l.heads, l.seq, D)
+    res = O.sdpa_ref(q.reshape(shape), kt.t().reshape(shape), v.reshape(shape), l.scale,
+                     dtype=torch.float32)
+    y.copy_(res.reshape(y.shape).to(y.dtype))
+
+
 class _MapRef:
     def __init__(self, t):
         self.t = t
@@ -157,5 +169,7 @@ def run(plan, args):
             run_reduce(l, args)
         elif isinstance(l, EltwiseLaunch):
             run_eltwise(l, args)
+        elif isinstance(l, SdpaLaunch):
+            run_sdpa(l, args)
         else:
             run_matmul(l, args)

@@ -20,7 +20,8 @@ def test_header_declares_the_expected_entry_points():
     for s in ("ttlh_eltwise", "ttlh_matmul", "ttlh_matmul_bfp8w", "ttlh_matmul_bfp8w_ws",
               "ttlh_bfp4_pack_host", "ttlh_bfp4_unpack_host", "ttlh_bfp4_unpack", "ttlh_matmul_bfp4w_ws",
               "ttlh_matmul_bfp8w_workspace_bytes", "ttlh_bfp8_pack_host",
-              "ttlh_bfp8_unpack_host", "ttlh_bfp8_unpack", "ttlh_sdpa_fwd", "ttlh_last_error",
+              "ttlh_bfp8_unpack_host", "ttlh_bfp8_unpack", "ttlh_sdpa_fwd", "ttlh_transpose_bf16",
+              "ttlh_last_error",
               "ttlh_version"):
         assert s in syms, s
 

@@ -217,3 +217,18 @@ def test_bcast_fma_example_config():
     got, k = _gpu(KL.make_bcast_fma, [a, b, c, torch.zeros(n, n, dtype=torch.bfloat16)], 3)
     assert len(k.last_plan.launches) == 1
     assert torch.equal(got, a * b + c)  # per-op bf16 rounding, vectorised
+
+
+@pytest.mark.parametrize("bm,bk,bn,R,C", [(1, 3, 4, 2, 1), (2, 4, 2, 2, 3)])
+def test_block_matmul_kernel_gpu(bm, bk, bn, R, C):
+    # the spec's (M, K) @ (K, N) block matmul planned onto one tile matmul
+    # launch: within one bf16 ulp of the oracle and of the float64 product
+    a = O.seeded((bm * 32 * R, bk * 32), "normal", 3 * bm + bk)
+    b = O.seeded((bk * 32, bn * 32 * C), "normal", 5 * bn + C)
+    out = torch.zeros(a.shape[0], b.shape[1], dtype=torch.bfloat16)
+    got, k = _gpu(KL.make_block_matmul, [a, b, out], 2, bm=bm, bk=bk, bn=bn)
+    assert len(k.last_plan.launches) == 1
+    orc = _oracle(KL.make_block_matmul, [a, b, out], 2, bm=bm, bk=bk, bn=bn)
+    exact = (a.double() @ b.double()).to(torch.bfloat16)
+    assert int(O.bf16_ulp_diff(got, orc).abs().max()) <= 1
+    assert int(O.bf16_ulp_diff(got, exact).abs().max()) <= 1

@@ -1,4 +1,6 @@
-// Row-major <-> tilized element order (ttlh_tilize / ttlh_untilize).
+// Row-major <-> tilized element order (ttlh_tilize / ttlh_untilize), and the
+// bf16 transpose that stages a K^T operand as K for fused attention
+// (ttlh_transpose_bf16).
 //
 // A tilized 2-D tensor (the TILE_LAYOUT storage of ttnn tensors the
 // reference's compiled path requires, python/ttl/ttl_api.py:489-506) holds
@@ -86,8 +88,92 @@ int run_layout(const char* who, bool tilize, const void* src, void* dst, int64_t
   return check_launch("layout_kernel");
 }
 
+// Transpose of a bf16 matrix through LDS: a 256-thread workgroup moves one
+// 64 x 64 tile.  Loads: 16-byte chunks along source rows (eight lanes cover
+// one 128-byte row run).  Stores: each lane gathers eight source rows of one
+// source column into one 16-byte chunk of a destination row.  The LDS row
+// pitch of 66 elements (33 dwords) spreads those column reads over the banks.
+constexpr int kTr = 64;
+constexpr int kTrPitch = kTr + 2;
+
+struct TransposeArgs {
+  const uint16_t* src;
+  uint16_t* dst;
+  int64_t src_ld, dst_ld;   // row strides, elements
+  int32_t rows, cols;       // of the source
+};
+
+__global__ __launch_bounds__(256) void transpose_bf16_kernel(TransposeArgs a) {
+  __shared__ uint16_t t[kTr * kTrPitch];
+  const int r0 = blockIdx.y * kTr, c0 = blockIdx.x * kTr;
+  for (int i = threadIdx.x; i < kTr * kTr / 8; i += 256) {
+    const int r = i >> 3, ch = i & 7;
+    const int gr = r0 + r, gc = c0 + 8 * ch;
+    if (gr < a.rows && gc < a.cols) {
+      const uint4 v = *reinterpret_cast<const uint4*>(a.src + int64_t(gr) * a.src_ld + gc);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        t[r * kTrPitch + 8 * ch + 2 * e] = uint16_t(w[e] & 0xffffu);
+        t[r * kTrPitch + 8 * ch + 2 * e + 1] = uint16_t(w[e] >> 16);
+      }
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < kTr * kTr / 8; i += 256) {
+    const int c = i >> 3, ch = i & 7;           // destination row c0 + c
+    const int gr = r0 + 8 * ch, gc = c0 + c;    // first source row of the chunk
+    if (gr < a.rows && gc < a.cols) {
+      uint32_t w[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        w[e] = uint32_t(t[(8 * ch + 2 * e) * kTrPitch + c]) |
+               (uint32_t(t[(8 * ch + 2 * e + 1) * kTrPitch + c]) << 16);
+      *reinterpret_cast<uint4*>(a.dst + int64_t(gc) * a.dst_ld + gr) =
+          uint4{w[0], w[1], w[2], w[3]};
+    }
+  }
+}
+
 }  // namespace
 }  // namespace ttlh
+
+extern "C" int ttlh_transpose_bf16(const void* src, int64_t src_ld, void* dst, int64_t dst_ld,
+                                   int64_t rows, int64_t cols, void* stream) {
+  using namespace ttlh;
+  clear_error();
+  TTLH_REQUIRE(src && dst, TTLH_EINVAL, "ttlh_transpose_bf16: null pointer");
+  TTLH_REQUIRE(rows >= 0 && cols >= 0 && rows % 8 == 0 && cols % 8 == 0, TTLH_EINVAL,
+               "ttlh_transpose_bf16: rows and cols must be multiples of 8 (got %lld x %lld)",
+               (long long)rows, (long long)cols);
+  TTLH_REQUIRE(src_ld >= cols && dst_ld >= rows && src_ld % 8 == 0 && dst_ld % 8 == 0,
+               TTLH_EINVAL, "ttlh_transpose_bf16: row strides must cover the rows and be "
+               "multiples of 8 elements");
+  TTLH_REQUIRE((reinterpret_cast<uintptr_t>(src) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(dst) & 15) == 0,
+               TTLH_EINVAL, "ttlh_transpose_bf16: buffers must be 16-byte aligned");
+  TTLH_REQUIRE((rows + kTr - 1) / kTr <= 65535 && (cols + kTr - 1) / kTr <= (int64_t(1) << 24),
+               TTLH_EUNSUPPORTED, "ttlh_transpose_bf16: matrix too large");
+  const char* s0 = static_cast<const char*>(src);
+  const char* d0 = static_cast<const char*>(dst);
+  const int64_t sbytes = (rows ? (rows - 1) * src_ld + cols : 0) * 2;
+  const int64_t dbytes = (cols ? (cols - 1) * dst_ld + rows : 0) * 2;
+  TTLH_REQUIRE(d0 + dbytes <= s0 || s0 + sbytes <= d0, TTLH_EINVAL,
+               "ttlh_transpose_bf16: source and destination overlap");
+  if (rows == 0 || cols == 0) return TTLH_OK;
+  TransposeArgs a;
+  a.src = static_cast<const uint16_t*>(src);
+  a.dst = static_cast<uint16_t*>(dst);
+  a.src_ld = src_ld;
+  a.dst_ld = dst_ld;
+  a.rows = static_cast<int32_t>(rows);
+  a.cols = static_cast<int32_t>(cols);
+  const dim3 grid(static_cast<uint32_t>((cols + kTr - 1) / kTr),
+                  static_cast<uint32_t>((rows + kTr - 1) / kTr));
+  hipLaunchKernelGGL(transpose_bf16_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
+                     a);
+  return check_launch("transpose_bf16_kernel");
+}
 
 extern "C" int ttlh_tilize(const void* src, int64_t src_ld, void* dst, int64_t rows, int64_t cols,
                            int elem_bytes, void* stream) {

@@ -79,6 +79,7 @@ SIGNATURES = {
                             _i64, _i64, _i64, _vp]),
     "ttlh_tilize": (_int, [_vp, _i64, _vp, _i64, _i64, _int, _vp]),
     "ttlh_untilize": (_int, [_vp, _vp, _i64, _i64, _i64, _int, _vp]),
+    "ttlh_transpose_bf16": (_int, [_vp, _i64, _vp, _i64, _i64, _i64, _vp]),
     "ttlh_reduce_workspace_bytes": (_i64, [_int, _i64, _i64]),
     "ttlh_reduce": (_int, [C.POINTER(Instr), C.POINTER(Operand), _int, _int, _int, _vp, _int,
                            C.c_float, _vp, _int, _i64, _int, _i64, _i64, _i64, _i64, _vp, _i64,

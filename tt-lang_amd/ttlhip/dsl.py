@@ -376,11 +376,36 @@ def _tile_rep(tree, rows: bool, cols: bool):
         return tree
     if tag in ("powi", "upar"):
         return (tag, _tile_rep(tree[1], rows, cols)) + tuple(tree[2:])
-    if tag in ("reduce", "matmul"):
+    if tag in ("reduce", "matmul", "bmatmul"):
         raise NotImplementedError(f"ttl.math.broadcast of a {tag} result inside one store() is not "
                                   "supported; store the result into a CB first and broadcast the "
                                   "block waited from it")
     return (tag,) + tuple(_tile_rep(t, rows, cols) for t in tree[1:])
+
+
+def _is_block_matmul(sa, sb) -> bool:
+    """Block shapes for which `a @ b` is the spec's block matmul
+    (docs/sphinx/specs/TTLangSpecification.md:693: (M, K) @ (K, N) -> (M, N)):
+    inner dimensions equal and above 1, and the shapes not compatible for
+    the simulator's tile-wise pairing (python/sim/block.py:870-920, which
+    raises for them).  Where both readings apply, the simulator's wins."""
+    if len(sa) != 2 or len(sb) != 2 or sa[1] != sb[0] or sa[1] <= 1:
+        return False
+    return any(la != lb and la != 1 and lb != 1 for la, lb in zip(sa, sb))
+
+
+def _block_matmul(aa: "BExpr", bb: "BExpr") -> "BExpr":
+    """Output tile (i, j) = sum over k of a(i, k) @ b(k, j), accumulated in
+    fp32 and rounded once (as a store(acc=True) loop of tile matmuls over k
+    runs on the MI355X)."""
+    for x in (aa, bb):
+        if x.tree[0] != "leaf" or any(leaf_rep(x.tree)):
+            raise NotImplementedError("a block matmul of computed or broadcast blocks is not "
+                                      "supported by the MI355X backend; store the operand into a "
+                                      "CB first")
+    K = aa.shape[1]
+    return BExpr((aa.shape[0], bb.shape[1]), ("bmatmul", aa.tree, bb.tree, K),
+                 torch.promote_types(aa.dtype, bb.dtype))
 
 
 def _binary(op: str, a, b) -> BExpr:
@@ -396,6 +421,8 @@ def _binary(op: str, a, b) -> BExpr:
     _check_not_reduced(aa)
     _check_not_reduced(bb)
     sa, sb = aa.shape, bb.shape
+    if op == "matmul" and _is_block_matmul(sa, sb):
+        return _block_matmul(aa, bb)
     if len(sa) != len(sb):
         raise ValueError(f"Cannot broadcast: dimension mismatch between shapes {sa} and {sb}. "
                          "Shapes must have the same number of dimensions.")

@@ -224,6 +224,19 @@ def untilize(data: torch.Tensor, rows: int, cols: int, out: Optional[torch.Tenso
     return out
 
 
+def transpose(src: torch.Tensor, dst: torch.Tensor, stream=None) -> None:
+    """dst = src^T for bf16 device matrices with unit column stride."""
+    for t, nm in ((src, "source"), (dst, "destination")):
+        _check_device(t, f"transpose {nm}")
+        if t.dtype != torch.bfloat16 or t.dim() != 2 or t.stride(1) != 1:
+            raise ValueError(f"transpose {nm} must be a bf16 matrix with unit column stride")
+    rows, cols = src.shape
+    if tuple(dst.shape) != (cols, rows):
+        raise ValueError(f"transpose of {tuple(src.shape)} into {tuple(dst.shape)}")
+    L.call("ttlh_transpose_bf16", src.data_ptr(), src.stride(0), dst.data_ptr(), dst.stride(0),
+           rows, cols, L.stream_ptr(stream))
+
+
 def bfp8_tiles_bytes(rows: int, cols: int) -> int:
     if rows % 32 or cols % 32:
         raise ValueError(f"bfloat8_b needs whole 32x32 tiles, got {rows}x{cols}")

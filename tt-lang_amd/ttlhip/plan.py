@@ -19,6 +19,10 @@ becomes one launch:
     output tile reducing the same contiguous run of expression tiles (one
     block, or several accumulated with store(acc=True) for sums) -> one
     ttlh_reduce.
+Six consecutive store sites that spell out attention over intermediate CBs
+(S = Q K^T, M = row max, P = exp(S*scale - M), L = row sum of P, O = P V,
+Y = O / L, every tile where the attention indexing puts it) become one
+ttlh_sdpa_fwd instead (_match_attention).
 Anything else raises NotImplementedError naming the unsupported pattern.
 """
 
@@ -125,6 +129,32 @@ class ReduceLaunch:
     def describe(self) -> str:
         return (f"reduce_{self.kind} over dims {list(self.dims)} of {self.region[2]}x"
                 f"{self.region[3]} elements at ({self.region[0]}, {self.region[1]})")
+
+
+@dataclass
+class SdpaLaunch:
+    """Attention spelled out tile by tile with the spec's ops
+    (docs/sphinx/specs/TTLangSpecification.md:693-761: @, reduce_max, exp,
+    broadcast, reduce_sum, recip): for every 32-row tile of queries of
+    Q [B*H*S, D], the S key rows of its head in K (read as K^T [D, B*H*S]),
+    Y = softmax(Q K^T * scale) V, as one ttlh_sdpa_fwd over [1, B*H, S, D]."""
+
+    q: TensorRef
+    kt: TensorRef           # K^T: the transposed view of a contiguous K [B*H*S, D]
+    v: TensorRef
+    out: TensorRef
+    heads: int              # B*H
+    seq: int                # S
+    scale: float
+    loc: Optional[Tuple[str, int]] = None
+    # plan-owned K [B*H*S, D], written from K^T by ttlh_transpose_bf16 when
+    # K^T is not the transposed view of contiguous K rows (allocated on the
+    # first such call, kept with the cached plan)
+    kbuf: Any = None
+
+    def describe(self) -> str:
+        return (f"sdpa over {self.heads} heads of {self.seq} rows, scale {self.scale:g} "
+                "(fused attention)")
 
 
 @dataclass
@@ -359,6 +389,9 @@ def _tree_leaves(tree, out: List):
         _tree_leaves(tree[1], out)
     elif tag == "reduce":
         _tree_leaves(tree[3], out)
+    elif tag == "bmatmul":
+        _tree_leaves(tree[1], out)
+        _tree_leaves(tree[2], out)
     else:
         for t in tree[1:]:
             _tree_leaves(t, out)
@@ -380,6 +413,8 @@ def _tree_key(tree, leaf_ids: Dict[int, int]):
         _, kind, dims, inner, ishape, scaler = tree
         sk = ("const", scaler[1]) if scaler[0] == "const" else ("scaler", str(scaler[1].cb.dtype))
         return ("reduce", kind, dims, _tree_key(inner, leaf_ids), ishape, sk)
+    if tag == "bmatmul":
+        return ("bmatmul", _tree_key(tree[1], leaf_ids), _tree_key(tree[2], leaf_ids), tree[3])
     return (tag,) + tuple(_tree_key(t, leaf_ids) for t in tree[1:])
 
 
@@ -602,6 +637,9 @@ def resolve(core_traces: List[Dict[str, Any]]) -> List[_Group]:
                 if e.tree[0] == "reduce":
                     _resolve_reduce(ev, e, target, rout, dt, fill, shape, groups)
                     continue
+                if e.tree[0] == "bmatmul":
+                    _resolve_block_matmul(ev, e, target, rout, dt, fill, shape, groups)
+                    continue
                 er, ec = e.shape
                 nslot = R * C
                 # output tile of every (instance, slot)
@@ -639,6 +677,52 @@ def resolve(core_traces: List[Dict[str, Any]]) -> List[_Group]:
     for sc in scratch.values():
         sc.check()
     return list(groups.values())
+
+
+def _resolve_block_matmul(ev, e, target, rout, dt, fill, shape, groups) -> None:
+    """Store of a block matmul (the spec's (M, K) @ (K, N) blocks): output
+    tile (i, j) accumulates a(i, k) @ b(k, j) over k, which is the tile
+    matmul accumulation of K store(acc=True) instances; it joins that group
+    (`("matmul", a, b)` with acc), one instance per (store, k)."""
+    _, la, lb, K = e.tree
+    R, C = target.shape
+    if tuple(e.shape) != (R, C):
+        raise PlanError(f"a block matmul of shape {tuple(e.shape)} stored into a block of shape "
+                        f"{(R, C)}")
+    slot = np.arange(R * C)
+    oi, oj = slot // C, slot % C
+    out_r = (dt.r0[rout][:, None] + oi[None, :]).ravel()
+    out_c = (dt.c0[rout][:, None] + oj[None, :]).ravel()
+    ops = []
+    for lf in (la, lb):
+        blk = lf[1]
+        if blk.cb.id not in fill:
+            raise PlanError("expression operands must come from blocks filled by ttl.copy from a "
+                            "tensor")
+        ft = fill[blk.cb.id]
+        w = T.broadcast_to_domain(blk.event.index, shape).ravel()
+        ops.append((ft, w, np.asarray(lf[2]), np.asarray(lf[3])))
+    (fa, wa, ra, ca), (fb, wb, rb, cb) = ops
+    outs, a_rc, b_rc = [], [], []
+    for k in range(K):
+        a_r = (fa.r0[wa][:, None] + ra[oi][None, :]).ravel()
+        a_c = (fa.c0[wa][:, None] + np.full(slot.size, ca[k])[None, :]).ravel()
+        b_r = (fb.r0[wb][:, None] + np.full(slot.size, rb[k])[None, :]).ravel()
+        b_c = (fb.c0[wb][:, None] + cb[oj][None, :]).ravel()
+        outs.append(np.stack([out_r, out_c], 1))
+        a_rc.append(np.stack([a_r, a_c], 1))
+        b_rc.append(np.stack([b_r, b_c], 1))
+    tree = ("matmul", la, lb)
+    key = (_tree_key(tree, {}), (id(fa.tensor), id(fb.tensor)), id(dt.tensor), True)
+    g = groups.get(key)
+    if g is None:
+        g = _Group(tree, [la, lb], [fa.tensor, fb.tensor], dt.tensor, True, e.dtype,
+                   ev.data.get("loc"))
+        groups[key] = g
+    base = sum(o.size for o in g.order)
+    g.out_rc.append(np.concatenate(outs, 0))
+    g.leaf_rc.append([np.concatenate(a_rc, 0), np.concatenate(b_rc, 0)])
+    g.order.append(base + np.tile(np.repeat(np.arange(rout.size), R * C), K))
 
 
 def _resolve_reduce(ev, e, target, rout, dt, fill, shape, groups) -> None:
@@ -920,10 +1004,259 @@ def _leaf_operands(g: _Group, it_rc, leaf_rc, tensor_ref, inl: Optional[_Inliner
     return specs, nodes, plain, subbed
 
 
+# ---------------------------------------------------------------------------
+# attention
+
+
+def _plain_leaf(t, rep=(False, False)) -> bool:
+    return t[0] == "leaf" and _leaf_rep(t) == rep
+
+
+def _is_const(t) -> bool:
+    return t[0] == "const" and isinstance(t[1], (int, float))
+
+
+def _scaled(t) -> Optional[Tuple[Any, float]]:
+    """(x, c) for x * c or c * x with x a plain leaf; (x, 1.0) for x."""
+    if _plain_leaf(t):
+        return t, 1.0
+    if t[0] == "mul":
+        a, b = t[1], t[2]
+        if _plain_leaf(a) and _is_const(b):
+            return a, float(b[1])
+        if _plain_leaf(b) and _is_const(a):
+            return b, float(a[1])
+    return None
+
+
+def _softmax_numerator(t, m_scale: float):
+    """(S leaf, M leaf, scale) of exp(S*c - bcast(M)) with M = reduce_max(S, c)
+    (`m_scale` = c), or of exp((S - bcast(M)) * c) with M = reduce_max(S, 1);
+    both are exp(c*S - max_j c*S) for c > 0.  None for anything else."""
+    if t[0] != "exp":
+        return None
+    x, col = t[1], (False, True)
+    if x[0] == "sub" and _plain_leaf(x[2], col):
+        sx = _scaled(x[1])
+        if sx is not None and sx[1] == m_scale:
+            return sx[0], x[2], sx[1]
+    if x[0] == "mul" and m_scale == 1.0:
+        diff, c = (x[1], x[2]) if _is_const(x[2]) else (x[2], x[1])
+        if (_is_const(c) and diff[0] == "sub" and _plain_leaf(diff[1])
+                and _plain_leaf(diff[2], col)):
+            return diff[1], diff[2], float(c[1])
+    return None
+
+
+def _attention_trees(gs: Sequence[_Group]):
+    """The six store sites' expressions, if they have the attention shape:
+    (S leaf of P, M leaf of P, L leaf of Y, O leaf of Y, scale) else None.
+    S and O are tile matmuls accumulated over K, M = reduce_max(S) and
+    L = reduce_sum(P, 1) along dim 1, P as _softmax_numerator takes it, Y is
+    O * recip(bcast(L)) or O / bcast(L)."""
+    g1, g2, g3, g4, g5, g6 = gs
+    for g in (g1, g5):
+        if not (g.tree[0] == "matmul" and _plain_leaf(g.tree[1]) and _plain_leaf(g.tree[2])
+                and g.acc):
+            return None
+    for g, kind in ((g2, "max"), (g4, "sum")):
+        t = g.tree
+        if not (t[0] == "reduce" and t[1] == kind and tuple(t[2]) == (1,) and _plain_leaf(t[3])
+                and _is_const(t[5]) and not g.acc):
+            return None
+    if g3.acc or g6.acc or float(g4.tree[5][1]) != 1.0:
+        return None
+    num = _softmax_numerator(g3.tree, float(g2.tree[5][1]))
+    if num is None:
+        return None
+    s_leaf, m_leaf, scale = num
+    col = (False, True)
+    t6 = g6.tree
+    if t6[0] == "mul" and _plain_leaf(t6[1]) and t6[2][0] == "recip" and _plain_leaf(t6[2][1], col):
+        o_leaf, l_leaf = t6[1], t6[2][1]
+    elif t6[0] == "mul" and _plain_leaf(t6[2]) and t6[1][0] == "recip" and _plain_leaf(t6[1][1], col):
+        o_leaf, l_leaf = t6[2], t6[1][1]
+    elif t6[0] == "div" and _plain_leaf(t6[1]) and _plain_leaf(t6[2], col):
+        o_leaf, l_leaf = t6[1], t6[2]
+    else:
+        return None
+    return s_leaf, m_leaf, l_leaf, o_leaf, scale
+
+
+def _leaf_index(g: _Group, leaf) -> int:
+    for i, lf in enumerate(_tree_leaves(g.tree, [])):
+        if lf is leaf:
+            return i
+    raise AssertionError("leaf not in the group's tree")
+
+
+def _tile_keys(rc: np.ndarray) -> np.ndarray:
+    return rc[:, 0].astype(np.int64) * (1 << 31) + rc[:, 1]
+
+
+class _TileMap:
+    """A bijection from logical indices 0..n-1 to the tiles (keys) of one
+    tensor, read off the instances of one store site and checked: every index
+    lands on one tile, distinct indices on distinct tiles."""
+
+    def __init__(self, n: int, idx: np.ndarray, keys: np.ndarray, what: str) -> None:
+        tab = np.full(n, -1, dtype=np.int64)
+        tab[idx] = keys
+        if np.any(tab[idx] != keys) or np.any(tab < 0) or np.unique(tab).size != n:
+            raise _NoAttention(what)
+        self.tab = tab
+        self.order = np.argsort(tab)
+
+    def index(self, keys: np.ndarray, what: str) -> np.ndarray:
+        pos = np.searchsorted(self.tab, keys, sorter=self.order)
+        pos = np.minimum(pos, self.tab.size - 1)
+        idx = self.order[pos]
+        if np.any(self.tab[idx] != keys):
+            raise _NoAttention(what)
+        return idx
+
+
+class _NoAttention(Exception):
+    pass
+
+
+def _all_once(keys: np.ndarray, n: int, what: str) -> None:
+    if keys.size != n or np.unique(keys).size != n:
+        raise _NoAttention(what)
+
+
+def _match_attention(gs: Sequence[_Group], tensor_ref) -> Optional[SdpaLaunch]:
+    """The six store sites as one SdpaLaunch, or None when they are not
+    attention.  Checked beyond the expression shapes: Q, K^T, V and the
+    output are bf16 kernel tensors [N, D] / [D, N] with D = 64 or 128 and
+    S, M, P, L, O intermediate CBs; and every tile instance is where
+    attention puts it — for query tile r of head h = r // (S/32), S(r, j)
+    accumulates Q(r, k) K^T(k, h*S/32 + j) over all k, M(r) reduces
+    S(r, 0..), P(r, j) reads S(r, j) and M(r), L(r) reduces P(r, 0..),
+    O(r, d) accumulates P(r, j) V(h*S/32 + j, d) over all j, and Y(r, d)
+    reads O(r, d) and L(r)."""
+    g1, g2, g3, g4, g5, g6 = gs
+    m = _attention_trees(gs)
+    if m is None:
+        return None
+    s_leaf, m_leaf, l_leaf, o_leaf, scale = m
+    q_t, kt_t = g1.leaf_tensors
+    p_t, v_t = g5.leaf_tensors
+    s_t, m_t, p_out, l_t, o_t, y_t = (g.out_tensor for g in gs)
+    if not all(isinstance(t, _Scratch) for t in (s_t, m_t, p_out, l_t, o_t)):
+        return None
+    if (g2.leaf_tensors[0] is not s_t or g4.leaf_tensors[0] is not p_out or p_t is not p_out
+            or g3.leaf_tensors[_leaf_index(g3, s_leaf)] is not s_t
+            or g3.leaf_tensors[_leaf_index(g3, m_leaf)] is not m_t
+            or g6.leaf_tensors[_leaf_index(g6, o_leaf)] is not o_t
+            or g6.leaf_tensors[_leaf_index(g6, l_leaf)] is not l_t):
+        return None
+    for t in (q_t, kt_t, v_t, y_t):
+        if isinstance(t, _Temp) or getattr(t, "is_block_float", False) or len(t.shape) != 2:
+            return None
+    if any(t.dtype != torch.bfloat16 for t in (q_t, kt_t, v_t, y_t)):
+        raise PlanError("fused attention takes bfloat16 Q, K^T, V and output tensors")
+    N, D = q_t.shape
+    if (tuple(kt_t.shape) != (D, N) or tuple(v_t.shape) != (N, D) or tuple(y_t.shape) != (N, D)
+            or D not in (64, 128) or N % TILE):
+        raise PlanError("fused attention takes Q, V, output [B*H*S, D] and K^T [D, B*H*S] with "
+                        "D = 64 or 128")
+    if not scale > 0:
+        raise PlanError("fused attention needs a positive softmax scale")
+    R, dt = N // TILE, D // TILE
+    try:
+        # S(r, j) = sum_k Q(r, k) K^T(k, h*st + j)
+        out1 = np.concatenate(g1.out_rc)
+        qrc, krc = (np.concatenate([li[i] for li in g1.leaf_rc]) for i in (0, 1))
+        if out1.shape[0] % (R * dt):
+            raise _NoAttention("S instances")
+        st = out1.shape[0] // (R * dt)
+        if st == 0 or N % (st * TILE):
+            raise _NoAttention("sequence length")
+        r, k = qrc[:, 0], qrc[:, 1]
+        j = krc[:, 1] - (r // st) * st
+        if (np.any(krc[:, 0] != k) or np.any((k < 0) | (k >= dt)) or np.any((r < 0) | (r >= R))
+                or np.any((j < 0) | (j >= st))):
+            raise _NoAttention("S operands")
+        _all_once((r * st + j) * dt + k, R * st * dt, "S products")
+        smap = _TileMap(R * st, r * st + j, _tile_keys(out1), "S tiles")
+        # M(r) = max_j S(r, j)
+        out2, in2 = np.concatenate(g2.out_rc), np.concatenate([li[0] for li in g2.leaf_rc])
+        si = smap.index(_tile_keys(in2), "M operand")
+        _all_once(si, R * st, "M reads")
+        mmap = _TileMap(R, si // st, _tile_keys(out2), "M tiles")
+        # P(r, j) = exp(S(r, j) * c - M(r))
+        out3 = np.concatenate(g3.out_rc)
+        s3 = np.concatenate([li[_leaf_index(g3, s_leaf)] for li in g3.leaf_rc])
+        m3 = np.concatenate([li[_leaf_index(g3, m_leaf)] for li in g3.leaf_rc])
+        si = smap.index(_tile_keys(s3), "P operand")
+        _all_once(si, R * st, "P reads")
+        if np.any(mmap.index(_tile_keys(m3), "P max operand") != si // st):
+            raise _NoAttention("P max operand")
+        pmap = _TileMap(R * st, si, _tile_keys(out3), "P tiles")
+        # L(r) = sum_j P(r, j)
+        out4, in4 = np.concatenate(g4.out_rc), np.concatenate([li[0] for li in g4.leaf_rc])
+        pi = pmap.index(_tile_keys(in4), "L operand")
+        _all_once(pi, R * st, "L reads")
+        lmap = _TileMap(R, pi // st, _tile_keys(out4), "L tiles")
+        # O(r, d) = sum_j P(r, j) V(h*st + j, d)
+        out5 = np.concatenate(g5.out_rc)
+        prc, vrc = (np.concatenate([li[i] for li in g5.leaf_rc]) for i in (0, 1))
+        pi = pmap.index(_tile_keys(prc), "O operand")
+        r, j, d = pi // st, pi % st, vrc[:, 1]
+        if np.any(vrc[:, 0] != (r // st) * st + j) or np.any((d < 0) | (d >= dt)):
+            raise _NoAttention("O operands")
+        _all_once((r * st + j) * dt + d, R * st * dt, "O products")
+        omap = _TileMap(R * dt, r * dt + d, _tile_keys(out5), "O tiles")
+        # Y(r, d) = O(r, d) / L(r)
+        out6 = np.concatenate(g6.out_rc)
+        o6 = np.concatenate([li[_leaf_index(g6, o_leaf)] for li in g6.leaf_rc])
+        l6 = np.concatenate([li[_leaf_index(g6, l_leaf)] for li in g6.leaf_rc])
+        oi = omap.index(_tile_keys(o6), "Y operand")
+        _all_once(oi, R * dt, "Y reads")
+        if np.any(lmap.index(_tile_keys(l6), "Y sum operand") != oi // dt):
+            raise _NoAttention("Y sum operand")
+        if np.any(out6[:, 0] != oi // dt) or np.any(out6[:, 1] != oi % dt):
+            raise _NoAttention("Y tiles")
+    except _NoAttention:
+        return None
+    launch = SdpaLaunch(tensor_ref(q_t), tensor_ref(kt_t), tensor_ref(v_t), tensor_ref(y_t),
+                        N // (st * TILE), st * TILE, float(scale), kbuf=_Temp((N, D), torch.bfloat16))
+    launch._reads, launch._writes = (q_t, kt_t, v_t), y_t
+    return launch
+
+
+def _fuse_attention(groups: List[_Group], tensor_ref) -> List[Any]:
+    """The groups with every run of six that is attention (_match_attention)
+    replaced by its SdpaLaunch; its intermediates must be read by nothing
+    else."""
+    out: List[Any] = []
+    i = 0
+    while i < len(groups):
+        win = groups[i:i + 6]
+        launch = _match_attention(win, tensor_ref) if len(win) == 6 else None
+        if launch is not None:
+            inter = {id(g.out_tensor) for g in win[:5]}
+            rest = groups[:i] + groups[i + 6:]
+            if not any(id(t) in inter for g in rest for t in g.leaf_tensors + [g.out_tensor]):
+                launch.loc = win[-1].loc
+                out.append(launch)
+                i += 6
+                continue
+        out.append(groups[i])
+        i += 1
+    return out
+
+
 def build_plan(groups: List[_Group], tensor_ref) -> Plan:
     plan = Plan()
     inl = _Inliner(groups)
-    for g in groups:
+    for g in _fuse_attention(groups, tensor_ref):
+        if isinstance(g, SdpaLaunch):
+            plan.launches.append(g)
+            inl.note_reads(g._reads)
+            inl.note_write(g._writes)
+            continue
         out_rc = np.concatenate(g.out_rc, 0)
         leaf_rc = [np.concatenate([li[k] for li in g.leaf_rc], 0) for k in range(len(g.leaf_blocks))]
         if g.tree[0] == "reduce":
@@ -1273,6 +1606,21 @@ def _execute_one(l, args, stream, Kn) -> None:
             sc = l.scaler.resolve(args)[r:r + 1, c:c + 1]
         Kn.reduce(l.prog, ops, l.kind, l.dims, l.out.resolve(args), l.region, l.out_origin,
                   l.out_pad, sc, l.scale, stream=stream)
+    elif isinstance(l, SdpaLaunch):
+        q, kt, v, y = (r.resolve(args) for r in (l.q, l.kt, l.v, l.out))
+        k = kt.t()
+        if not k.is_contiguous():  # K^T stored as such: its rows transposed once more
+            k = l.kbuf._tensor
+            Kn.transpose(kt, k, stream=stream)
+        if not (q.is_contiguous() and v.is_contiguous() and y.is_contiguous()):
+            raise ValueError("fused attention takes contiguous Q, V and output tensors")
+        lo, hi = y.data_ptr(), y.data_ptr() + y.numel() * y.element_size()
+        for t in (q, k, v):
+            if t.data_ptr() < hi and lo < t.data_ptr() + t.numel() * t.element_size():
+                raise ValueError("fused attention output overlaps an input")
+        shape = (1, l.heads, l.seq, q.shape[1])
+        Kn.sdpa_fwd(q.view(shape), k.view(shape), v.view(shape), y.view(shape), l.scale,
+                    stream=stream)
     else:
         a, b, c = l.a.resolve(args), l.b.resolve(args), l.c.resolve(args)
         if c.data_ptr() in (a.data_ptr(), b.data_ptr()):

@@ -32,7 +32,8 @@ def _elem_size(dtype) -> int:
 def launch_work(l, args: Dict[Any, Any]) -> Tuple[float, str, float]:
     """(algorithmic work, unit, peak) of one launch: bytes read + written for
     an elementwise launch (an operand counted over the rows / columns it
-    actually spans), 2 M N K flops for a tile matmul."""
+    actually spans), 2 M N K flops for a tile matmul, 4 S^2 D per head for
+    fused attention."""
     if isinstance(l, (P.EltwiseLaunch, P.ReduceLaunch)):
         _, _, h, w = l.region
         out = l.out.resolve(args)
@@ -51,6 +52,9 @@ def launch_work(l, args: Dict[Any, Any]) -> Tuple[float, str, float]:
             cols = 1 if t.shape[1] == 1 else (32 if spec.col_mask == 31 else w)
             total += rows * cols * _elem_size(t.dtype)
         return float(total), "GB/s", HBM_PEAK_GBS
+    if isinstance(l, P.SdpaLaunch):  # Q K^T and P V: 4 S^2 D flops per head
+        d = l.q.resolve(args).shape[1]
+        return 4.0 * l.heads * l.seq * l.seq * d, "TFLOP/s", BF16_PEAK_TFLOPS
     m = l.rows[1] - l.rows[0]
     n = l.cols[1] - l.cols[0]
     a = l.a.resolve(args)
@@ -67,6 +71,8 @@ def _launch_name(l, args) -> str:
         _, _, h, w = l.region
         nops = len({id(s.ref) for s in l.operands if s is not None})
         return f"ttlh_eltwise {h}x{w}, {len(l.prog.steps)} steps, {nops} operands"
+    if isinstance(l, P.SdpaLaunch):
+        return f"ttlh_sdpa_fwd {l.heads} heads x {l.seq} rows, D {l.q.resolve(args).shape[1]}"
     m = l.rows[1] - l.rows[0]
     n = l.cols[1] - l.cols[0]
     fmt = f" x {l.b.resolve_obj(args).dtype.name}" if l.b_block else ""

@@ -43,6 +43,8 @@ def _refs(plan: P.Plan):
                     yield spec.ref
             if isinstance(l, P.ReduceLaunch) and l.scaler is not None:
                 yield l.scaler
+        elif isinstance(l, P.SdpaLaunch):
+            yield from (l.q, l.kt, l.v, l.out)
         else:
             yield from (l.a, l.b, l.c)
 
