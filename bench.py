@@ -228,7 +228,7 @@ class ReduceWorkload(PlanWorkload):
                        f"bf16 out {n}x1 (spec reduce_sum, dims=[1])")
 
     def kernel_name(self):
-        return "reduce_rows_kernel"
+        return "reduce_rows_bf16_kernel"
 
     def work_per_step(self):
         return self.n * self.n * 2 + self.n * 2

@@ -202,3 +202,33 @@ def test_abi_rejects_bad_arguments():
         K.reduce(_load_prog(), [K.OperandMap(x)], "sum", [0], out, (0, 0, 64, 64))
     with pytest.raises(ValueError, match="out of range"):
         K.reduce(_load_prog(), [K.OperandMap(x)], "sum", [1], out, (0, 32, 64, 64))
+
+
+@pytest.mark.parametrize("at", [(3, 5), (0, 4), (31, 31)])
+def test_abi_bf16_scaler_either_half_of_its_dword(at):
+    # the scaler element is read through the aligned 32-bit word holding it:
+    # odd columns sit in the upper half, even ones in the lower
+    x = O.seeded((256, 4096), "uniform", 40, lo=-1, hi=1).cuda()
+    tile = torch.zeros(32, 32, dtype=torch.bfloat16)
+    tile[at] = -0.375
+    tile[at[0], at[1] ^ 1] = 8.0  # the other half of the word
+    sc = tile.cuda()[at[0]:at[0] + 1, at[1]:at[1] + 1]
+    got = _reduce(x, "sum", [1], (256, 1), scaler=sc).double().reshape(-1)
+    xs = x.cpu().double() * -0.375
+    assert bool(((got - xs.sum(1)).abs() <= _fp32_sum_bound(xs, 1)).all())
+    got = _reduce(x, "max", [1], (256, 1), scaler=sc).reshape(-1)
+    assert torch.equal(got, (x.cpu().float() * -0.375).amax(1))
+
+
+def test_abi_wide_rows_of_a_broadcast_operand():
+    # every iteration row reads row 0 of the operand (row mask 0): cached
+    # loads, and every result equals row 0's sum
+    x = O.seeded((1, 4096), "normal", 41).cuda()
+    out = torch.full((64, 1), 7.0, dtype=torch.float32, device="cuda")
+    K.reduce(_load_prog(), [K.OperandMap(x, row_mask=0)], "sum", [1], out, (0, 0, 64, 4096))
+    torch.cuda.synchronize()
+    xs = x.cpu().double()
+    exact = xs.sum()
+    bound = float(_fp32_sum_bound(xs, None))
+    assert bool(((out.cpu().double().reshape(-1) - exact).abs() <= bound).all())
+    assert bool((out == out[0]).all())

@@ -922,11 +922,20 @@ __device__ __forceinline__ float red_combine(int kind, float a, float b) {
   return a + b;
 }
 
+// The scaler value through a 32-bit load of its (4-byte aligned, so in-bounds)
+// dword: a uniform 32-bit load compiles to s_load_dword, which the row loads
+// do not wait behind; a 16-bit load is a vector load whose vmcnt(0) wait
+// sat in front of every workgroup's first row load (9.7 -> 7 us on a
+// 4096 x 4096 row sum).
 __device__ __forceinline__ float red_scale(const RedArgs& a) {
   float s = a.scale_imm;
-  if (a.scaler)
-    s *= a.scaler_dtype == TTLH_BF16 ? bf16_to_f32(*static_cast<const uint16_t*>(a.scaler))
-                                     : *static_cast<const float*>(a.scaler);
+  if (a.scaler) {
+    const uintptr_t u = reinterpret_cast<uintptr_t>(a.scaler);
+    const uint32_t w =
+        *reinterpret_cast<const __attribute__((address_space(1))) uint32_t*>(u & ~uintptr_t(3));
+    s *= a.scaler_dtype == TTLH_BF16 ? __uint_as_float((u & 2) ? (w & 0xffff0000u) : (w << 16))
+                                     : __uint_as_float(w);
+  }
   return s;
 }
 
@@ -966,7 +975,8 @@ __device__ __forceinline__ float red_wave(int kind, float v) {
 //   2: up to four operands, common ops (add sub mul exp neg abs relu recip).
 // Modes 1 and 2 read 8-wide chunks in a four-deep software pipeline (chunk
 // k + 4 is fetched as soon as chunk k is consumed, so four loads per lane
-// stay in flight; past the end the fetch re-reads the lane's first chunk).
+// stay in flight; nothing is fetched past the end: a wave does not wait on
+// loads whose values it never reads).
 // Programs with other ops take mode 0: four inlined copies of the every-op
 // interpreter (pow, fmod, log, ...) would overflow the instruction cache.
 struct RedChunk {
@@ -1020,10 +1030,10 @@ __global__ __launch_bounds__(256) void reduce_rows_kernel(const RedArgs a) {
   const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= a.h) return;  // wave-uniform
-  const float s = red_scale(a);
   const int64_t y = a.e.y0 + row;
   float r = red_identity(a.kind);
   if constexpr (MODE == 0) {
+    const float s = red_scale(a);
     const Raw q{};
     for (int64_t xo = int64_t(lane) * VEC; xo < a.w; xo += 64 * VEC) {
       const f32x8 v =
@@ -1036,10 +1046,11 @@ __global__ __launch_bounds__(256) void reduce_rows_kernel(const RedArgs a) {
     constexpr int64_t S = 64 * 8;
     const int64_t xf = int64_t(lane) * 8;
     if (xf < a.w) {
-      auto at = [&](int64_t xo) { return a.e.x0 + (xo < a.w ? xo : xf); };
-      RedChunk c[D];
-      red_unroll([&](auto i) { c[i] = red_fetch<MODE>(a.e, y, at(xf + i * S)); },
-                 std::make_integer_sequence<int, D>());
+      RedChunk c[D];  // chunk slots past the row's end are neither fetched nor read
+      red_unroll([&](auto i) {
+        if (xf + i * S < a.w) c[i] = red_fetch<MODE>(a.e, y, a.e.x0 + xf + i * S);
+      }, std::make_integer_sequence<int, D>());
+      const float s = red_scale(a);  // after the first row loads are in flight
       for (int64_t xb = xf; xb < a.w; xb += D * S) {
         red_unroll([&](auto i) {
           const int64_t xo = xb + i * S;
@@ -1048,7 +1059,7 @@ __global__ __launch_bounds__(256) void reduce_rows_kernel(const RedArgs a) {
 #pragma unroll
             for (int k = 0; k < 8; ++k) r = red_combine(a.kind, r, v[k] * s);
           }
-          c[i] = red_fetch<MODE>(a.e, y, at(xo + D * S));
+          if (xo + D * S < a.w) c[i] = red_fetch<MODE>(a.e, y, a.e.x0 + xo + D * S);
         }, std::make_integer_sequence<int, D>());
       }
     }
@@ -1069,14 +1080,14 @@ __global__ __launch_bounds__(256) void reduce_rows_wide_kernel(const RedArgs a) 
   __shared__ float part[4];
   const int64_t row = blockIdx.x;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const float s = red_scale(a);
   const int64_t y = a.e.y0 + row;
   constexpr int64_t S = 256 * 8;
   const int64_t xf = int64_t(t) * 8;  // a.w >= 2048: every lane has a chunk
-  auto at = [&](int64_t xo) { return a.e.x0 + (xo < a.w ? xo : xf); };
-  RedChunk c[2];
-  red_unroll([&](auto i) { c[i] = red_fetch<MODE>(a.e, y, at(xf + i * S)); },
-             std::make_integer_sequence<int, 2>());
+  RedChunk c[2];  // chunk slots past the row's end are neither fetched nor read
+  red_unroll([&](auto i) {
+    if (xf + i * S < a.w) c[i] = red_fetch<MODE>(a.e, y, a.e.x0 + xf + i * S);
+  }, std::make_integer_sequence<int, 2>());
+  const float s = red_scale(a);  // after the first row loads are in flight
   float r = red_identity(a.kind);
   for (int64_t xb = xf; xb < a.w; xb += 2 * S) {
     red_unroll([&](auto i) {
@@ -1086,7 +1097,7 @@ __global__ __launch_bounds__(256) void reduce_rows_wide_kernel(const RedArgs a) 
 #pragma unroll
         for (int k = 0; k < 8; ++k) r = red_combine(a.kind, r, v[k] * s);
       }
-      c[i] = red_fetch<MODE>(a.e, y, at(xo + 2 * S));
+      if (xo + 2 * S < a.w) c[i] = red_fetch<MODE>(a.e, y, a.e.x0 + xo + 2 * S);
     }, std::make_integer_sequence<int, 2>());
   }
   r = red_wave(a.kind, r);
@@ -1095,6 +1106,64 @@ __global__ __launch_bounds__(256) void reduce_rows_wide_kernel(const RedArgs a) 
   if (t != 0) return;
   r = red_combine(a.kind, red_combine(a.kind, part[0], part[1]),
                   red_combine(a.kind, part[2], part[3]));
+  if constexpr (TO_WS) a.ws[row] = r;
+  else red_write<TTLH_REDUCE_DIM1>(a, row, r);
+}
+
+// Row reduce of the commonest program, one plain bf16 operand over rows of
+// at least 2048 elements (the wide kernel's layout: one workgroup per row,
+// lane t reads 16-byte chunks t, t + 256, ..., two in flight), with the
+// reduction kind a template parameter and nothing interpreted per element:
+// bf16 values are exact in fp32 and the operand's bf16 rounding is the
+// identity on them.  NT: streaming loads, chosen by the host when the
+// operand is read exactly once (no broadcast).  4096 x 4096 row sum: 6.5 us
+// against 8.4 us through the wide kernel.
+template <int KIND>
+__device__ __forceinline__ float red_combine_k(float a, float b) {
+  if constexpr (KIND == TTLH_REDUCE_MAX) return (a != a || b != b) ? __builtin_nanf("") : fmaxf(a, b);
+  else return a + b;
+}
+
+template <bool NT>
+__device__ __forceinline__ u32x4 ld16(uintptr_t u) {
+  if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<gu32x4*>(u));
+  else return *reinterpret_cast<gu32x4*>(u);
+}
+
+template <int KIND, bool TO_WS, bool NT>
+__global__ __launch_bounds__(256) void reduce_rows_bf16_kernel(const RedArgs a) {
+  __shared__ float part[4];
+  const int64_t row = blockIdx.x;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const EltOperand& op = a.e.ops[0];
+  const int64_t y = a.e.y0 + row;
+  constexpr int64_t S = 256 * 8;
+  const int64_t xf = int64_t(t) * 8;
+  u32x4 c[2];  // chunk slots past the row's end are neither fetched nor read
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+    if (xf + i * S < a.w) c[i] = ld16<NT>(operand_addr<false>(op, y, a.e.x0 + xf + i * S));
+  const float s = red_scale(a);  // after the first row loads are in flight
+  float r = red_identity(KIND);
+  for (int64_t xb = xf; xb < a.w; xb += 2 * S) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int64_t xo = xb + i * S;
+      if (xo < a.w) {
+        const f32x8 v = unpack_bf16x8(c[i]);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) r = red_combine_k<KIND>(r, v[k] * s);
+      }
+      if (xo + 2 * S < a.w) c[i] = ld16<NT>(operand_addr<false>(op, y, a.e.x0 + xo + 2 * S));
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) r = red_combine_k<KIND>(r, __shfl_xor(r, off, 64));
+  if (lane == 0) part[wave] = r;
+  __syncthreads();
+  if (t != 0) return;
+  r = red_combine_k<KIND>(red_combine_k<KIND>(part[0], part[1]),
+                          red_combine_k<KIND>(part[2], part[3]));
   if constexpr (TO_WS) a.ws[row] = r;
   else red_write<TTLH_REDUCE_DIM1>(a, row, r);
 }
@@ -1127,10 +1196,10 @@ __global__ __launch_bounds__(256) void reduce_cols_kernel(const RedArgs a) {
       const int64_t rf = rb + wave;
       if (rf < re) {
         const int64_t x = a.e.x0 + xo;
-        auto at = [&](int64_t row) { return a.e.y0 + (row < re ? row : rf); };
-        RedChunk c[D];
-        red_unroll([&](auto i) { c[i] = red_fetch<MODE>(a.e, at(rf + 4 * i), x); },
-                   std::make_integer_sequence<int, D>());
+        RedChunk c[D];  // slots past the last row are neither fetched nor read
+        red_unroll([&](auto i) {
+          if (rf + 4 * i < re) c[i] = red_fetch<MODE>(a.e, a.e.y0 + rf + 4 * i, x);
+        }, std::make_integer_sequence<int, D>());
         for (int64_t rr = rf; rr < re; rr += 4 * D) {
           red_unroll([&](auto i) {
             const int64_t row = rr + 4 * i;
@@ -1139,7 +1208,7 @@ __global__ __launch_bounds__(256) void reduce_cols_kernel(const RedArgs a) {
 #pragma unroll
               for (int k = 0; k < VEC; ++k) acc[k] = red_combine(a.kind, acc[k], v[k] * s);
             }
-            c[i] = red_fetch<MODE>(a.e, at(row + 4 * D), x);
+            if (row + 4 * D < re) c[i] = red_fetch<MODE>(a.e, a.e.y0 + row + 4 * D, x);
           }, std::make_integer_sequence<int, D>());
         }
       }
@@ -1569,8 +1638,20 @@ int reduce_impl(const char* who, const ttlh_instr* prog, const ttlh_operand* in,
   if (dims != TTLH_REDUCE_DIM0) {
     const bool wide = mode != 0 && w >= 2048;
     const dim3 grid(static_cast<uint32_t>(wide ? h : (h + 3) / 4));
+    // the specialised kernel: a plain bf16 operand; streaming loads when no
+    // element of it is read twice
+    const EltOperand& o0 = a.e.ops[0];
+    const bool plain_bf16 = wide && mode == 1 && o0.dtype == TTLH_BF16;
+    const bool nt = o0.rmask == -1 && o0.cmask == -1 && (o0.rs != 0 || h == 1);
+#define TTLH_ROWS_BF16(K, WS)                                                                \
+  if (nt) hipLaunchKernelGGL((reduce_rows_bf16_kernel<K, WS, true>), grid, block, 0, s, a);  \
+  else hipLaunchKernelGGL((reduce_rows_bf16_kernel<K, WS, false>), grid, block, 0, s, a);
 #define TTLH_ROWS(WS)                                                                        \
-  if (wide && mode == 1)                                                                     \
+  if (plain_bf16 && kind == TTLH_REDUCE_SUM) {                                               \
+    TTLH_ROWS_BF16(TTLH_REDUCE_SUM, WS)                                                      \
+  } else if (plain_bf16) {                                                                   \
+    TTLH_ROWS_BF16(TTLH_REDUCE_MAX, WS)                                                      \
+  } else if (wide && mode == 1)                                                              \
     hipLaunchKernelGGL((reduce_rows_wide_kernel<WS, 1>), grid, block, 0, s, a);             \
   else if (wide)                                                                             \
     hipLaunchKernelGGL((reduce_rows_wide_kernel<WS, 2>), grid, block, 0, s, a);             \
@@ -1586,6 +1667,7 @@ int reduce_impl(const char* who, const ttlh_instr* prog, const ttlh_operand* in,
     }
     TTLH_ROWS(true)
 #undef TTLH_ROWS
+#undef TTLH_ROWS_BF16
     int rc = check_launch("reduce_rows_kernel");
     if (rc != TTLH_OK) return rc;
     hipLaunchKernelGGL(reduce_all_finish_kernel, dim3(1), block, 0, s, a);
