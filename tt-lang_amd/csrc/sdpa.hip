@@ -773,18 +773,27 @@ struct SdpaW8 {
   // the fragment prefetch.  The DMA counts only on vmcnt, waited explicitly
   // at the end of every step, before any wave reads the buffer; the loop has
   // no other vector-memory loads.  M0 carries the wave's LDS base (one wait
-  // state before use).
+  // state before use).  The address is the uniform row base in an SGPR pair
+  // plus the lane's 32-bit byte offset: no 64-bit VGPR address, which would
+  // need an even-aligned register pair the asm constraint cannot request.
+  // Both uniform operands pass through readfirstlane, so they are SGPRs
+  // whatever the register allocator made of them (free when they already
+  // are); readfirstlane returns int, so each pointer half widens unsigned.
   template <int BUF>
   __device__ __forceinline__ void dma(const uint16_t* X, int src, int kv0) {
-    const uint16_t* g = X + base + static_cast<int64_t>(kv0) * D;
+    const uint64_t g = reinterpret_cast<uint64_t>(X + base + static_cast<int64_t>(kv0) * D);
+    const uint64_t gs =
+        (uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(g >> 32)))) << 32) |
+        uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(g))));
     const uint32_t buf = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
         (w8_lds_void*)(BUF < 2 ? w8_kbuf<BUF & 1>() : w8_vbuf<BUF & 1>())));
     asm volatile(
         "s_mov_b32 m0, %0\n\t"
         "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %1, off"
+        "global_load_lds_dwordx4 %1, %2"
         :
-        : "s"(buf + lds_wave), "v"(g + src)
+        : "s"(__builtin_amdgcn_readfirstlane(buf + lds_wave)),
+          "v"(static_cast<uint32_t>(src) * 2u), "s"(gs)
         : "memory", "m0");
   }
 
