@@ -360,7 +360,9 @@ int ttlh_matmul_bfp4w_ws(const void* A, int64_t lda, const void* Bq4, void* C,
  * reference: composed from spec ops @, exp, recip, reduce_max, reduce_sum,
  * broadcast, docs/sphinx/specs/TTLangSpecification.md:693-761).
  * Q, K, V, O: bf16 [B, H, S, D] contiguous; O = softmax(Q K^T * scale) V
- * with fp32 online softmax; D = 128 (or 64). causal = 1 masks j > i.     */
+ * with fp32 online softmax; D = 128 (or 64); S a multiple of 32 (whole
+ * 32-row tiles; S not a multiple of 128 takes a masked tail). causal = 1
+ * masks j > i.                                                            */
 int ttlh_sdpa_fwd(const void* Q, const void* K, const void* V, void* O,
                   int64_t B, int64_t H, int64_t S, int64_t D, float scale,
                   int causal, void* stream);

@@ -53,7 +53,8 @@ def _gpu(q, k, v, S, scale, kt_view=True, kern=None, **kw):
     return ttnn.to_torch(args[3]), kern
 
 
-@pytest.mark.parametrize("BH,S,D", [(2, 256, 128), (3, 128, 64), (1, 512, 128), (2, 384, 128)])
+@pytest.mark.parametrize("BH,S,D", [(2, 256, 128), (3, 128, 64), (1, 512, 128), (2, 384, 128),
+                                    (2, 96, 128), (3, 160, 64)])
 @pytest.mark.parametrize("exp_form,norm", [("scaled_max", "recip"), ("scaled_diff", "div")])
 def test_attention_program_on_gpu_matches_exact_and_oracle(BH, S, D, exp_form, norm):
     q, k, v = _qkv(BH, S, D, 7 * S + D)

@@ -6,6 +6,8 @@ max |O - ref| <= 1e-2 * max |ref| and mean |O - ref| <= 4e-3 * mean |ref|
 (bf16 rounding of P and of O contribute about 1e-3 each),
 plus invariants that catch layout / indexing slips exactly: V = 1 gives
 O = 1 (rows of P sum to one), a one-hot V column selects that column of P.
+Sequence lengths that are multiples of 32 but not of 128 (a masked tail)
+run with a guard region after the output.
 """
 
 import math
@@ -139,3 +141,32 @@ def test_sdpa_running_max_growth(jump):
     for causal in (False, True):
         out = _run(q, k, v, 1.0, causal=causal)
         _check(out, O.sdpa_ref(q, k, v, 1.0, causal=causal))
+
+
+@pytest.mark.parametrize("S", [32, 96, 160, 224, 416])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_sdpa_ragged_seq(S, D, causal):
+    # S a multiple of 32 but not of 128: the last query block holds waves past
+    # the sequence and the last KV block rows past it (masked, read as zero).
+    # The output sits in a larger buffer whose tail must stay untouched.
+    B, H = 1, 3
+    q, k, v = _qkv(B, H, S, D, S + D)
+    scale = 1.0 / math.sqrt(D)
+    from ttlhip import kernels as K
+    n = B * H * S * D
+    big = torch.full((n + 64 * D,), 3.0, dtype=torch.bfloat16, device="cuda")
+    out = big[:n].view(B, H, S, D)
+    K.sdpa_fwd(q.cuda(), k.cuda(), v.cuda(), out, scale, causal)
+    torch.cuda.synchronize()
+    _check(out.cpu(), O.sdpa_ref(q, k, v, scale, causal=causal))
+    assert bool((big[n:] == 3.0).all()), "write past the output"
+    ones = torch.ones_like(v)
+    out1 = _run(q, k, ones, scale, causal=causal)
+    assert float((out1.float() - 1.0).abs().max()) <= 2 ** -7
+
+
+@pytest.mark.parametrize("scale", [-0.11, 0.0])
+def test_sdpa_ragged_negative_and_zero_scale(scale):
+    q, k, v = _qkv(1, 2, 96, 128, 77)
+    _check(_run(q, k, v, scale), O.sdpa_ref(q, k, v, scale))

@@ -107,15 +107,21 @@ constexpr int kKPitch = D + 8;   // K rows in LDS (elements)
 template <int D>
 constexpr int kVPitch = D + 32;  // V rows in LDS (elements)
 
-// K or V rows kv0 .. kv0 + 63 as 16-byte chunks, D / 32 per thread
-template <int D>
-__device__ __forceinline__ void load_rows(const uint16_t* X, int64_t base, int kv0, u32x4 (&r)[D / 32]) {
+// K or V rows kv0 .. kv0 + 63 as 16-byte chunks, D / 32 per thread; with
+// RAGGED, rows from `end` on (past the sequence) read as zeros
+template <int D, bool RAGGED = false>
+__device__ __forceinline__ void load_rows(const uint16_t* X, int64_t base, int kv0, u32x4 (&r)[D / 32],
+                                          int end = 0) {
   const int t = threadIdx.x;
   constexpr int kChunksPerRow = D / 8;
 #pragma unroll
   for (int i = 0; i < D / 32; ++i) {
     const int c = t + i * kThreads;
     const int row = c / kChunksPerRow, dc = (c % kChunksPerRow) * 8;
+    if (RAGGED && kv0 + row >= end) {
+      r[i] = u32x4{0u, 0u, 0u, 0u};
+      continue;
+    }
     r[i] = *reinterpret_cast<gu32x4*>(
         reinterpret_cast<uintptr_t>(X + base + static_cast<int64_t>(kv0 + row) * D + dc));
   }
@@ -154,7 +160,7 @@ __device__ __forceinline__ void block_coords(const SdpaArgs& p, int& bh, int& qb
   qb = id - bh * p.nqb;
 }
 
-template <int D, bool CAUSAL>
+template <int D, bool CAUSAL, bool RAGGED = false>
 struct Sdpa {
   static constexpr int ND = D / 32;   // d tiles of O^T
   static constexpr int NDC = D / 16;  // 16-wide d chunks of the S^T contraction
@@ -197,22 +203,25 @@ struct Sdpa {
     const uint16_t* Kc = Ks[kb & 1];
     const uint16_t* Vc = Vs[kb & 1];
     if (kb + 1 < nkv) {
-      load_rows<D>(p.K, base, (kb + 1) * BKV, stk);
-      load_rows<D>(p.V, base, (kb + 1) * BKV, stv);
+      load_rows<D, RAGGED>(p.K, base, (kb + 1) * BKV, stk, p.S);
+      load_rows<D, RAGGED>(p.V, base, (kb + 1) * BKV, stv, p.S);
     }
     f32x16 cur[2];
     scores(Kc, cur);
 
     // causal: only blocks that reach past this wave's first query need a
-    // mask (masked scores drop out of the block extreme and get exp 0)
-    const bool diag = CAUSAL && kb * BKV + BKV - 1 > qb * BQ + wave * 32;
+    // mask; ragged: the block that runs past the sequence end masks the kv
+    // beyond it (masked scores drop out of the block extreme and get exp 0)
+    const bool diag = (CAUSAL && kb * BKV + BKV - 1 > qb * BQ + wave * 32) ||
+                      (RAGGED && kb * BKV + BKV > p.S);
+    auto masked = [&](int kv) { return (CAUSAL && kv > q) || (RAGGED && kv >= p.S); };
     if (diag) {
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int kv = kb * BKV + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
-          if (kv > q) cur[t][r] = sc >= 0.0f ? -INFINITY : INFINITY;
+          if (masked(kv)) cur[t][r] = sc >= 0.0f ? -INFINITY : INFINITY;
         }
     }
     // block extreme of the raw scores: max if the scale is positive, else min
@@ -246,7 +255,7 @@ struct Sdpa {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int kv = kb * BKV + 32 * t + 8 * (r >> 2) + 4 * h + (r & 3);
-          const float e = kv > q ? 0.0f : expo(cur[t][r]);
+          const float e = masked(kv) ? 0.0f : expo(cur[t][r]);
           cur[t][r] = e;
           rs += e;
         }
@@ -297,11 +306,15 @@ struct Sdpa {
   }
 };
 
-template <int D, bool CAUSAL>
+// RAGGED: S a multiple of 32 only.  The last query block holds waves past
+// the sequence (S % 32 == 0 keeps each wave wholly in or out): they read a
+// clamped Q row, take part in the K / V staging and barriers, store nothing.
+// The last KV block reads rows past S as zeros and masks their scores.
+template <int D, bool CAUSAL, bool RAGGED = false>
 __global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(const SdpaArgs p) {
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2][BKV * kKPitch<D>];
   __shared__ __attribute__((aligned(16))) uint16_t Vs[2][BKV * kVPitch<D>];
-  Sdpa<D, CAUSAL> w{p, Ks, Vs};
+  Sdpa<D, CAUSAL, RAGGED> w{p, Ks, Vs};
   int bh;
   block_coords(p, bh, w.qb);
   w.lane = threadIdx.x & 63;
@@ -313,14 +326,20 @@ __global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(const SdpaArgs p)
   w.sc = p.scale_log2;
   w.m = -INFINITY;  // running max of s * scale * log2 e
   w.l = 0.0f;
-  w.nkv = CAUSAL ? (w.qb * BQ + BQ) / BKV : p.S / BKV;
+  if constexpr (RAGGED) {
+    const int nall = (p.S + BKV - 1) / BKV;
+    w.nkv = CAUSAL ? min(nall, (w.qb * BQ + BQ) / BKV) : nall;
+  } else {
+    w.nkv = CAUSAL ? (w.qb * BQ + BQ) / BKV : p.S / BKV;
+  }
+  const int qload = RAGGED ? min(w.q, p.S - 1) : w.q;  // a wave past S reads a valid row
 
   // prologue: K(0), V(0) into LDS; Q^T into VGPRs
-  load_rows<D>(p.K, w.base, 0, w.stk);
-  load_rows<D>(p.V, w.base, 0, w.stv);
+  load_rows<D, RAGGED>(p.K, w.base, 0, w.stk, p.S);
+  load_rows<D, RAGGED>(p.V, w.base, 0, w.stv, p.S);
 #pragma unroll
   for (int dc = 0; dc < D / 16; ++dc)
-    w.qop[dc] = *reinterpret_cast<const bf16x8*>(p.Q + w.base + static_cast<int64_t>(w.q) * D +
+    w.qop[dc] = *reinterpret_cast<const bf16x8*>(p.Q + w.base + static_cast<int64_t>(qload) * D +
                                                  dc * 16 + 8 * w.h);
 #pragma unroll
   for (int j = 0; j < D / 32; ++j)
@@ -335,6 +354,7 @@ __global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(const SdpaArgs p)
   __syncthreads();
 
   for (int kb = 0; kb < w.nkv; ++kb) w.step(kb);
+  if (RAGGED && w.q >= p.S) return;  // wave-uniform (S % 32 == 0); no barrier follows
 
   // O[q][d], d = 32j + 8u + 4h + i: four contiguous bf16 per (j, u)
   const float inv = 1.0f / w.l;
@@ -1008,6 +1028,11 @@ int launch(const SdpaArgs& a, hipStream_t s) {
     hipLaunchKernelGGL((sdpa_pp_kernel<D, CAUSAL>), dim3(b.nbh * b.nqb), dim3(PP_THREADS), 0, s, b);
     return check_launch("sdpa_pp_kernel");
   }
+  if (a.S % BQ != 0) {  // a ragged tail (S % 32 == 0)
+    hipLaunchKernelGGL((sdpa_fwd_kernel<D, CAUSAL, true>), dim3(a.nbh * a.nqb), dim3(kThreads), 0,
+                       s, a);
+    return check_launch("sdpa_fwd_kernel");
+  }
   hipLaunchKernelGGL((sdpa_fwd_kernel<D, CAUSAL>), dim3(a.nbh * a.nqb), dim3(kThreads), 0, s, a);
   return check_launch("sdpa_fwd_kernel");
 }
@@ -1024,9 +1049,8 @@ extern "C" int ttlh_sdpa_fwd(const void* Q, const void* K, const void* V, void* 
   TTLH_REQUIRE(Q && K && V && O, TTLH_EINVAL, "ttlh_sdpa_fwd: null pointer");
   TTLH_REQUIRE(B > 0 && H > 0 && S > 0, TTLH_EINVAL, "ttlh_sdpa_fwd: empty problem");
   TTLH_REQUIRE(D == 64 || D == 128, TTLH_EUNSUPPORTED, "ttlh_sdpa_fwd: head_dim must be 64 or 128");
-  TTLH_REQUIRE(S % BQ == 0, TTLH_EUNSUPPORTED, "ttlh_sdpa_fwd: seq_len must be a multiple of %d",
-               BQ);
-  TTLH_REQUIRE(B * H * (S / BQ) < (int64_t(1) << 31), TTLH_EUNSUPPORTED,
+  TTLH_REQUIRE(S % 32 == 0, TTLH_EUNSUPPORTED, "ttlh_sdpa_fwd: seq_len must be a multiple of 32");
+  TTLH_REQUIRE(B * H * ((S + BQ - 1) / BQ) < (int64_t(1) << 31), TTLH_EUNSUPPORTED,
                "ttlh_sdpa_fwd: too many query blocks");
   TTLH_REQUIRE(S * D < (int64_t(1) << 31), TTLH_EUNSUPPORTED, "ttlh_sdpa_fwd: seq_len too long");
   for (const void* ptr : {Q, K, V, static_cast<const void*>(O)})
@@ -1039,7 +1063,7 @@ extern "C" int ttlh_sdpa_fwd(const void* Q, const void* K, const void* V, void* 
   a.V = static_cast<const uint16_t*>(V);
   a.O = static_cast<uint16_t*>(O);
   a.S = static_cast<int32_t>(S);
-  a.nqb = static_cast<int32_t>(S / BQ);
+  a.nqb = static_cast<int32_t>((S + BQ - 1) / BQ);
   a.nbh = static_cast<int32_t>(B * H);
   a.scale_log2 = scale * 1.4426950408889634f;
   hipStream_t s = static_cast<hipStream_t>(stream);
