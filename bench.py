@@ -650,8 +650,9 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
-              f"--gpus {args.gpus}). Every config shards without communication; see DESIGN.md "
-              "'More than one GPU'.", file=sys.stderr)
+              f"--gpus {args.gpus}). Every config would shard without communication: the "
+              "elementwise ones by tile rows, the matmuls by output columns, attention by "
+              "(batch, head).", file=sys.stderr)
         return 2
     if not torch.cuda.is_available():
         print("bench.py needs an MI355X (no HIP device visible)", file=sys.stderr)
