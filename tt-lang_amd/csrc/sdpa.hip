@@ -22,10 +22,11 @@
 // 4 consecutive kv of one d column each.
 //
 // Three kernels share that per-wave math:
-//  * sdpa_w8_kernel (D = 128, non-causal, positive scale, S a multiple of
-//    256): 8 waves of 32 queries, two per SIMD, each interleaving the MFMAs
-//    of a KV block with the softmax of the previous one, the second wave's
-//    VALU issuing under the first one's MFMAs (details at its definition);
+//  * sdpa_w8_kernel (D = 128, non-causal, S a multiple of 256): 8 waves of
+//    32 queries, two per SIMD, each interleaving the MFMAs of a KV block with
+//    the softmax of the previous one, the second wave's VALU issuing under
+//    the first one's MFMAs; Q pre-scaled and the S accumulation started from
+//    -m, so the softmax is one exp2 per score (details at its definition);
 //  * sdpa_pp_kernel (other cases with S a multiple of 256): 8 waves, 256
 //    queries per workgroup, the two groups of four waves in ping-pong, one
 //    issuing the MFMAs of a block while the other runs the softmax of the
@@ -40,8 +41,9 @@
 // D + 32 elements (V: 4 rows x 4 chunks per 32 lanes of a transpose read)
 // meet that.  The next block's K and V are fetched into registers while the
 // current block computes.
-// Softmax runs in the log2 domain: exp2(fma(s, scale log2 e, -m)), with the
-// block max taken on the raw scores; the causal mask touches only the blocks
+// Softmax runs in the log2 domain: exp2(fma(s, scale log2 e, -m)) in the
+// other two kernels, with the block max taken on the raw scores (sign of the
+// scale handled by taking the min instead); the causal mask touches only the blocks
 // that straddle the diagonal.  P is rounded to bf16 for the MFMA; O is
 // divided by l at the end.  Workgroup ids are regrouped so the query blocks
 // of one (batch, head) land on the same XCD and share K/V in its L2.
@@ -719,9 +721,11 @@ __global__ __launch_bounds__(PP_THREADS, 1) void sdpa_pp_kernel(const SdpaArgs p
 // cycles, so VALU placed between one wave's MFMAs mostly adds to them, while
 // a second wave's VALU issues under them (measured: MFMA + 16 FMAs takes 80
 // cycles for one wave, 62 for two).  The cost is LDS traffic: each K / V
-// fragment feeds one MFMA (128 KB per step per CU).  The accumulators fit in
-// the architectural VGPRs (203, no AGPRs), so the softmax reads S without
-// copies.  The waves raise their priority (s_setprio 1) over the first six
+// fragment feeds one MFMA (128 KB per step per CU; gfx950's LDS serves 256
+// bytes per clock to ds_read_b128 and ~186 to ds_read_b64_tr_b16, measured,
+// so the reads take ~600 of the step's 1024 MFMA cycles).  The accumulators
+// fit in the architectural VGPRs (214, no AGPRs), so the softmax reads S
+// without copies.  The waves raise their priority (s_setprio 1) over the first six
 // sections, where MFMAs and LDS reads are densest, so a SIMD's matrix core
 // is fed first and the other wave's VALU fills the gaps.
 // K and V reach LDS by direct-to-LDS DMA (global_load_lds_dwordx4, lane l's
@@ -754,18 +758,17 @@ typedef __attribute__((address_space(3))) void w8_lds_void;
 
 struct SdpaW8 {
   static constexpr int D = W8_D, ND = D / 32, NDC = D / 16;
-  static constexpr float kLazy = 8.0f;
 
   const SdpaArgs& p;
   int64_t base;
   int qb, wave, lane, l32, h, n;
-  float sc;
-  bf16x8 qop[NDC];          // Q^T operands
+  bf16x8 qop[NDC];          // Q^T operands, scaled by scale * log2(e)
   f32x16 o[ND];             // O^T accumulators
-  f32x16 s;                 // S(i) accumulating
-  f32x16 sv;                // S(i - 1) (renamed, not copied: both live in VGPRs)
+  f32x16 s;                 // S(i) - m accumulating
+  f32x16 sv;                // S(i - 1) - m (renamed, not copied: both live in VGPRs)
+  f32x16 negm;              // -m in every element: where each S accumulation starts
   u32x4 pw[2][2];           // [parity][kv chunk]: P(i - 1), P(i - 2) as bf16 pairs
-  float m, l, alpha;
+  float m, l;               // running max (log2 units), this lane's share of the row sum
   int k_src, v_src;         // per-lane DMA source offsets (elements)
   int v_frag[ND];           // LDS offsets of the V transpose reads
   uint32_t lds_wave;        // the wave's byte offset in a K / V buffer (uniform)
@@ -832,16 +835,17 @@ struct SdpaW8 {
     return __builtin_bit_cast(bf16x8, w);
   }
 
-  // The softmax of S(i - 1) (sv) into pw[PAR], cut into sections of similar
-  // VALU cost, one per MFMA section of a step:
-  //   0:    block max and running max (lazy: moves only by > kLazy log2 units)
-  //   1..5: two exponentials each, one bf16 pair, partial row sums
-  //   6:    four exponentials
-  //   7:    two exponentials and the running row sum
-  // An MFMA hides about two v_exp_f32 of the other wave on its SIMD; four per
-  // section (two per MFMA, as packed before) measured 1.7% slower.
-  // Row maxima use v_maximum3 (NaN-propagating, no canonicalisation).
-  float mnew_, rsum_;
+  // The softmax of S(i - 1) - m (sv) into pw[PAR]: one pair of scores per
+  // section (two exponentials, one bf16 pair, their sum).  Q is pre-scaled
+  // by scale * log2(e) and every S accumulation starts from -m (negm), so the
+  // exponent argument comes out of the MFMAs.  The running max m does not
+  // move on the common path: a lane's block sum above kSumLimit (some P above
+  // 2^8) sends the wave to rescale(), which moves m by the block max where
+  // that exceeds kLazy.  Otherwise every P = exp2(s - m) <= 2^12, which fp32
+  // O and l absorb.  Row maxima use v_maximum3 (NaN-propagating).
+  static constexpr float kLazy = 8.0f;
+  static constexpr float kSumLimit = 4096.0f;
+  float rsum_;
 
   __device__ __forceinline__ static float max16(const f32x16& c) {
     const float a = __builtin_elementwise_maximum(__builtin_elementwise_maximum(c[0], c[1]), c[2]);
@@ -854,41 +858,62 @@ struct SdpaW8 {
     return __builtin_elementwise_maximum(g, hh);
   }
 
-  __device__ __forceinline__ void run_max(float mx) {
-    const float m_blk = xor32_max(mx) * sc;
-    mnew_ = m_blk > m + kLazy ? m_blk : m;
-    alpha = __builtin_amdgcn_exp2f(m - mnew_);
-    m = mnew_;
-  }
-
   // exponentials of S values 2g, 2g + 1 into one P dword.  The empty asm
   // keeps the bf16 packing in this section: left alone the compiler sinks it
-  // into the next step, in front of that step's first LDS reads.
+  // into the next step, in front of that step's first LDS reads.  (Summing
+  // the bf16 pair with v_dot2c_f32_bf16 instead of two adds measured 4%
+  // slower.)
   template <int PAR, int g>
   __device__ __forceinline__ void expo2() {
-    const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[2 * g], sc, -mnew_));
-    const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[2 * g + 1], sc, -mnew_));
+    const float e0 = __builtin_amdgcn_exp2f(sv[2 * g]);
+    const float e1 = __builtin_amdgcn_exp2f(sv[2 * g + 1]);
     uint32_t c = pk_bf16(e0, e1);
     asm volatile("" : "+v"(c));
     pw[PAR][g >> 2][g & 3] = c;
     rsum_ = g == 0 ? e0 + e1 : rsum_ + (e0 + e1);
   }
 
-  template <int PAR, int X>
-  __device__ __forceinline__ void softmax_section() {
-    if constexpr (X == 0) run_max(max16(sv));
-    else if constexpr (X <= 5) expo2<PAR, X - 1>();
-    else if constexpr (X == 6) {
-      expo2<PAR, 5>();
-      expo2<PAR, 6>();
-    } else {
-      expo2<PAR, 7>();
-      l = l * alpha + xor32_add(rsum_);
+  // The rare path for P(i - 1) (its scores in sp): move m by the block max d
+  // where that exceeds kLazy, recompute P(i - 1), scale O (blocks <= i - 2)
+  // and l by 2^-d, shift S(i) (accumulated from the old -m, now in sv) and
+  // the start value of the next accumulation.  The updates of O, S and -m
+  // are inline asm with tied operands: written as C++, they made the compiler
+  // keep a second copy of those registers across the branch (256 VGPRs and
+  // spills in the main loop, against 214).  The asm is invisible to the
+  // compiler's hazard tracking, so the wait states are explicit: the MFMA
+  // results it reads were written before the ~40 VALU instructions above it,
+  // and the s_nop after it precedes any MFMA that reads what it wrote.
+  template <int PAR, bool SHIFT_S>
+  __device__ __forceinline__ void rescale(const f32x16& sp) {
+    const float bm = xor32_max(max16(sp));
+    const float d = bm > kLazy ? bm : 0.0f;
+    const float alpha = __builtin_amdgcn_exp2f(-d);
+    m += d;
+    float rs = 0.0f;
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      const float e0 = __builtin_amdgcn_exp2f(sp[2 * g] - d);
+      const float e1 = __builtin_amdgcn_exp2f(sp[2 * g + 1] - d);
+      pw[PAR][g >> 2][g & 3] = pk_bf16(e0, e1);
+      rs += e0 + e1;
     }
+    rsum_ = rs;
+    l *= alpha;
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7");
+#pragma unroll
+    for (int j = 0; j < ND; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) asm volatile("v_mul_f32 %0, %1, %0" : "+v"(o[j][r]) : "v"(alpha));
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      if constexpr (SHIFT_S) asm volatile("v_sub_f32 %0, %0, %1" : "+v"(sv[r]) : "v"(d));
+      asm volatile("v_mov_b32 %0, %1" : "+v"(negm[r]) : "v"(-m));
+    }
+    asm volatile("s_nop 7");
   }
 
   // VALU slots of a section (for the interleave below)
-  static constexpr int kSectionValu[8] = {12, 10, 10, 10, 10, 10, 20, 14};
+  static constexpr int kSectionValu[8] = {5, 4, 4, 4, 4, 4, 4, 4};
 
   // one step (see the header): S(i) into s (renamed to sv at the end),
   // softmax of sv into pw[PAR ^ 1], O += V(i-2) P(i-2) with P(i-2) in pw[PAR]
@@ -896,6 +921,7 @@ struct SdpaW8 {
   __device__ __forceinline__ void step(int i) {
     const uint16_t* Kc = w8_kbuf<PAR>();
     const uint16_t* Vc = w8_vbuf<PAR>();
+    const f32x16 sp = sv;  // S(i - 1) - m, for the rare path
     bf16x8 kf[8], vf[8];
     auto issue = [&](auto xc) {
       constexpr int x = decltype(xc)::value;
@@ -922,15 +948,13 @@ struct SdpaW8 {
       constexpr int x = decltype(xc)::value;
       if constexpr (x == 0) __builtin_amdgcn_s_setprio(1);
       if constexpr (x == 6) __builtin_amdgcn_s_setprio(0);
-      if constexpr (DO_S) {
-        const f32x16 z = {};
-        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[x], qop[x], x == 0 ? z : s, 0, 0, 0);
-      }
+      if constexpr (DO_S)
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[x], qop[x], x == 0 ? negm : s, 0, 0, 0);
       if constexpr (DO_O)
         o[x >> 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
             vf[x], __builtin_bit_cast(bf16x8, pw[PAR][x & 1]), o[x >> 1], 0, 0, 0);
       if constexpr (x + 2 < 8) issue(std::integral_constant<int, x + 2>());
-      if constexpr (DO_SM) softmax_section<PAR ^ 1, x>();
+      if constexpr (DO_SM) expo2<PAR ^ 1, x>();
       if constexpr (DO_S && x == 7) sv = s;  // the next step's softmax reads S(i)
       constexpr int nm = (DO_S ? 1 : 0) + (DO_O ? 1 : 0);
       constexpr int nv = DO_SM ? (kSectionValu[x] + nm - 1) / nm : 0;
@@ -942,11 +966,8 @@ struct SdpaW8 {
       __builtin_amdgcn_sched_barrier(0);
     });
     if constexpr (DO_SM) {
-      // O rescale for P(i-1) (rare: the running max moves by more than kLazy)
-      if (__any(alpha != 1.0f)) {
-#pragma unroll
-        for (int j = 0; j < ND; ++j) o[j] *= alpha;
-      }
+      if (__builtin_expect(__any(rsum_ > kSumLimit), 0)) rescale<PAR ^ 1, DO_S>(sp);
+      l += rsum_;
     }
     // the next stage landed, this stage's reads are done: release / publish
     __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
@@ -966,17 +987,20 @@ __global__ __launch_bounds__(W8_THREADS, 1) void sdpa_w8_kernel(const SdpaArgs p
   w.l32 = w.lane & 31;
   w.h = w.lane >> 5;
   w.base = static_cast<int64_t>(bh) * p.S * W8_D;
-  w.sc = p.scale_log2;
   w.n = p.S / W8_KV;
-  w.m = -INFINITY;
   w.l = 0.0f;
-  w.alpha = 1.0f;
   w.setup();
   // Q^T of the wave's tile: query row qb * 256 + 32 wave + l32
   const int64_t q = static_cast<int64_t>(w.qb) * W8_BQ + 32 * w.wave + w.l32;
 #pragma unroll
-  for (int dc = 0; dc < SdpaW8::NDC; ++dc)
-    w.qop[dc] = *reinterpret_cast<const bf16x8*>(p.Q + w.base + q * W8_D + dc * 16 + 8 * w.h);
+  for (int dc = 0; dc < SdpaW8::NDC; ++dc) {
+    const bf16x8 x = *reinterpret_cast<const bf16x8*>(p.Q + w.base + q * W8_D + dc * 16 + 8 * w.h);
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      w.qop[dc][e] = static_cast<__bf16>(static_cast<float>(x[e]) * p.scale_log2);
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) w.negm[r] = 0.0f;
 #pragma unroll
   for (int j = 0; j < SdpaW8::ND; ++j)
 #pragma unroll
@@ -989,6 +1013,14 @@ __global__ __launch_bounds__(W8_THREADS, 1) void sdpa_w8_kernel(const SdpaArgs p
   asm volatile("" ::: "memory");
   const int n = w.n;  // >= 8 (S >= 256)
   w.step<0, true, false, false>(0);
+  // m starts at block 0's maximum; S(0) is shifted by it here, every later
+  // block accumulates from -m
+  w.m = xor32_max(SdpaW8::max16(w.sv));
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    w.sv[r] -= w.m;
+    w.negm[r] = -w.m;
+  }
   w.step<1, true, true, false>(1);
   int i = 2;
   for (; i + 1 < n; i += 2) {
@@ -999,7 +1031,7 @@ __global__ __launch_bounds__(W8_THREADS, 1) void sdpa_w8_kernel(const SdpaArgs p
   w.step<0, false, true, true>(i);
   w.step<1, false, false, true>(i + 1);
   // O[q][d], d = 32j + 8u + 4h + i
-  const float inv = 1.0f / w.l;
+  const float inv = 1.0f / xor32_add(w.l);
   uint16_t* orow = p.O + w.base + q * W8_D;
 #pragma unroll
   for (int j = 0; j < SdpaW8::ND; ++j)
@@ -1014,9 +1046,7 @@ __global__ __launch_bounds__(W8_THREADS, 1) void sdpa_w8_kernel(const SdpaArgs p
 
 template <int D, bool CAUSAL>
 int launch(const SdpaArgs& a, hipStream_t s) {
-  // the eight-wave kernel takes its running max from the raw block max, which
-  // needs a positive scale
-  if (D == W8_D && !CAUSAL && a.S % W8_BQ == 0 && a.scale_log2 > 0.0f) {
+  if (D == W8_D && !CAUSAL && a.S % W8_BQ == 0) {
     SdpaArgs b = a;
     b.nqb = a.S / W8_BQ;
     hipLaunchKernelGGL(sdpa_w8_kernel, dim3(b.nbh * b.nqb), dim3(W8_THREADS), 0, s, b);
