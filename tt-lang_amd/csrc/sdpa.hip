@@ -710,7 +710,7 @@ __global__ __launch_bounds__(PP_THREADS, 1) void sdpa_pp_kernel(const SdpaArgs p
 
 // ---------------------------------------------------------------------------
 // 32 queries per wave, eight waves (two per SIMD) per workgroup of 256
-// queries (D = 128, positive scale, non-causal: C5).  KV blocks of 32 rows;
+// queries (D = 128, non-causal: C5).  KV blocks of 32 rows;
 // step i of the loop is one straight-line block:
 //     MFMAs: S(i) = K(i) Q^T and O += V(i-2)^T P(i-2)^T (16)
 //     VALU:  the softmax of S(i-1) -> P(i-1), running max / sum
@@ -729,9 +729,11 @@ __global__ __launch_bounds__(PP_THREADS, 1) void sdpa_pp_kernel(const SdpaArgs p
 // sections, where MFMAs and LDS reads are densest, so a SIMD's matrix core
 // is fed first and the other wave's VALU fills the gaps.
 // K and V reach LDS by direct-to-LDS DMA (global_load_lds_dwordx4, lane l's
-// 16 bytes at the wave's base + 16 l) into two K and two V buffers: step i
-// reads K(i) and V(i - 2) from buffers i & 1 and fetches K(i + 1), V(i - 1)
-// into the others; one workgroup barrier per step.  Rows are unpadded with
+// 16 bytes at the wave's base + 16 l) into rings of three K and three V
+// buffers (48 KB): step i reads K(i) from K buffer i % 3 and V(i - 2) from V
+// buffer (i - 2) % 3, and fetches K(i + 2) and V(i), two steps ahead of their
+// use (one step ahead, with two buffers each, measured 2% slower); one
+// workgroup barrier per step.  Rows are unpadded with
 // XOR-swizzled 16-byte chunks: K chunk c of row r at c ^ (r & 15) (the S
 // operand reads 16 rows of one chunk per 16 lanes), V at c ^ 4 (r & 3) (a
 // transpose read covers 4 rows x 4 chunks per 32 lanes).
@@ -740,18 +742,18 @@ constexpr int W8_THREADS = 512;
 constexpr int W8_D = 128;
 constexpr int W8_KV = 32;
 
-__shared__ __attribute__((aligned(16))) uint16_t w8K0[W8_KV * W8_D], w8K1[W8_KV * W8_D];
-__shared__ __attribute__((aligned(16))) uint16_t w8V0[W8_KV * W8_D], w8V1[W8_KV * W8_D];
+// one array per ring, so a buffer is a constant offset from the others (an
+// immediate in the LDS instructions, not another address register)
+__shared__ __attribute__((aligned(16))) uint16_t w8K[3][W8_KV * W8_D];
+__shared__ __attribute__((aligned(16))) uint16_t w8V[3][W8_KV * W8_D];
 
 template <int B>
 __device__ __forceinline__ uint16_t* w8_kbuf() {
-  if constexpr (B == 0) return w8K0;
-  else return w8K1;
+  return w8K[B];
 }
 template <int B>
 __device__ __forceinline__ uint16_t* w8_vbuf() {
-  if constexpr (B == 0) return w8V0;
-  else return w8V1;
+  return w8V[B];
 }
 
 typedef __attribute__((address_space(3))) void w8_lds_void;
@@ -789,27 +791,25 @@ struct SdpaW8 {
     }
   }
 
-  // 32 K or V rows from kv0 into a buffer: one DMA instruction per thread,
+  // 32 K or V rows from kv0 into an LDS buffer: one DMA instruction per thread,
   // issued as inline asm: with a compiler-visible LDS DMA outstanding, the
   // compiler's wait-count model treats LDS reads as completing out of order
   // and waits for every LDS read (lgkmcnt(0)) before each use, which defeats
   // the fragment prefetch.  The DMA counts only on vmcnt, waited explicitly
-  // at the end of every step, before any wave reads the buffer; the loop has
-  // no other vector-memory loads.  M0 carries the wave's LDS base (one wait
+  // at the end of every step, before any wave reads the buffer (the loop has
+  // no other vector-memory loads, so vmcnt counts exactly these).  M0 carries the wave's LDS base (one wait
   // state before use).  The address is the uniform row base in an SGPR pair
   // plus the lane's 32-bit byte offset: no 64-bit VGPR address, which would
   // need an even-aligned register pair the asm constraint cannot request.
   // Both uniform operands pass through readfirstlane, so they are SGPRs
   // whatever the register allocator made of them (free when they already
   // are); readfirstlane returns int, so each pointer half widens unsigned.
-  template <int BUF>
-  __device__ __forceinline__ void dma(const uint16_t* X, int src, int kv0) {
+  __device__ __forceinline__ void dma(const uint16_t* X, int src, int kv0, const uint16_t* lds) {
     const uint64_t g = reinterpret_cast<uint64_t>(X + base + static_cast<int64_t>(kv0) * D);
     const uint64_t gs =
         (uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(g >> 32)))) << 32) |
         uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(g))));
-    const uint32_t buf = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
-        (w8_lds_void*)(BUF < 2 ? w8_kbuf<BUF & 1>() : w8_vbuf<BUF & 1>())));
+    const uint32_t buf = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((w8_lds_void*)lds));
     asm volatile(
         "s_mov_b32 m0, %0\n\t"
         "s_nop 0\n\t"
@@ -916,11 +916,14 @@ struct SdpaW8 {
   static constexpr int kSectionValu[8] = {5, 4, 4, 4, 4, 4, 4, 4};
 
   // one step (see the header): S(i) into s (renamed to sv at the end),
-  // softmax of sv into pw[PAR ^ 1], O += V(i-2) P(i-2) with P(i-2) in pw[PAR]
-  template <int PAR, bool DO_S, bool DO_SM, bool DO_O>
+  // softmax of sv into pw[PAR ^ 1], O += V(i-2) P(i-2) with P(i-2) in pw[PAR];
+  // PAR = i % 2, KB = i % 3 (KB < 0: taken from i at run time, for the two
+  // drain steps, which read no K)
+  template <int PAR, int KB, bool DO_S, bool DO_SM, bool DO_O>
   __device__ __forceinline__ void step(int i) {
-    const uint16_t* Kc = w8_kbuf<PAR>();
-    const uint16_t* Vc = w8_vbuf<PAR>();
+    static_assert(KB >= 0 || !DO_S, "a step computing S needs its K buffer at compile time");
+    const uint16_t* Kc = w8_kbuf<KB < 0 ? 0 : KB>();
+    const uint16_t* Vc = KB < 0 ? w8V[(i + 1) % 3] : w8_vbuf<(KB + 1) % 3>();
     const f32x16 sp = sv;  // S(i - 1) - m, for the rare path
     bf16x8 kf[8], vf[8];
     auto issue = [&](auto xc) {
@@ -933,15 +936,12 @@ struct SdpaW8 {
     issue(std::integral_constant<int, 0>());
     issue(std::integral_constant<int, 1>());
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (DO_S && DO_SM && DO_O) {
-      // main loop (2 <= i < n, so V(i - 1) exists): no branch, K(i + 1)
-      // clamped to K(n - 1) (the last step's load refills a buffer no later
-      // step reads)
-      dma<PAR ^ 1>(p.K, k_src, min(i + 1, n - 1) * W8_KV);
-      dma<2 + (PAR ^ 1)>(p.V, v_src, (i - 1) * W8_KV);
-    } else {
-      if (i + 1 < n) dma<PAR ^ 1>(p.K, k_src, (i + 1) * W8_KV);
-      if (i >= 1 && i - 1 < n) dma<2 + (PAR ^ 1)>(p.V, v_src, (i - 1) * W8_KV);
+    if constexpr (DO_S) {
+      // steps 0 .. n - 1: K(i + 2), clamped to K(n - 1) (past the end it
+      // refills a buffer that no later step reads: the last two steps read
+      // no K), and V(i)
+      dma(p.K, k_src, min(i + 2, n - 1) * W8_KV, w8_kbuf<(KB + 2) % 3>());
+      dma(p.V, v_src, i * W8_KV, w8_vbuf<KB>());
     }
     __builtin_amdgcn_sched_barrier(0);
     sd_static_for<8>([&](auto xc) {
@@ -969,8 +969,10 @@ struct SdpaW8 {
       if (__builtin_expect(__any(rsum_ > kSumLimit), 0)) rescale<PAR ^ 1, DO_S>(sp);
       l += rsum_;
     }
-    // the next stage landed, this stage's reads are done: release / publish
-    __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+    // the previous step's loads landed (this step's two may stay in flight),
+    // this step's reads are done: publish / release
+    if constexpr (DO_S) __builtin_amdgcn_s_waitcnt(0x0072);  // vmcnt(2) lgkmcnt(0)
+    else __builtin_amdgcn_s_waitcnt(0x0070);                 // vmcnt(0) lgkmcnt(0)
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
@@ -1005,14 +1007,15 @@ __global__ __launch_bounds__(W8_THREADS, 1) void sdpa_w8_kernel(const SdpaArgs p
   for (int j = 0; j < SdpaW8::ND; ++j)
 #pragma unroll
     for (int r = 0; r < 16; ++r) w.o[j][r] = 0.0f;
-  // K(0) into buffer 0 (with Q landed), then the pipeline
-  w.dma<0>(p.K, w.k_src, 0);
+  // K(0), K(1) into K buffers 0, 1 (with Q landed), then the pipeline
+  w.dma(p.K, w.k_src, 0, w8_kbuf<0>());
+  w.dma(p.K, w.k_src, W8_KV, w8_kbuf<1>());
   __builtin_amdgcn_s_waitcnt(0x0070);
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   const int n = w.n;  // >= 8 (S >= 256)
-  w.step<0, true, false, false>(0);
+  w.step<0, 0, true, false, false>(0);
   // m starts at block 0's maximum; S(0) is shifted by it here, every later
   // block accumulates from -m
   w.m = xor32_max(SdpaW8::max16(w.sv));
@@ -1021,15 +1024,33 @@ __global__ __launch_bounds__(W8_THREADS, 1) void sdpa_w8_kernel(const SdpaArgs p
     w.sv[r] -= w.m;
     w.negm[r] = -w.m;
   }
-  w.step<1, true, true, false>(1);
+  w.step<1, 1, true, true, false>(1);
+  // main steps 2 .. n - 1 (step i: PAR = i % 2, KB = i % 3, period 6), then
+  // the drain of P(n - 1) and O(n - 1); n is a multiple of 8, so n - 2 main
+  // steps leave 0, 2 or 4 after the unrolled loop, which continue its
+  // pattern (KB 2, 0, then 1, 2).  (Three separate tails, one per n % 3,
+  // made the compiler spill.)
   int i = 2;
-  for (; i + 1 < n; i += 2) {
-    w.step<0, true, true, true>(i);
-    w.step<1, true, true, true>(i + 1);
+  for (; i + 5 < n; i += 6) {
+    w.step<0, 2, true, true, true>(i);
+    w.step<1, 0, true, true, true>(i + 1);
+    w.step<0, 1, true, true, true>(i + 2);
+    w.step<1, 2, true, true, true>(i + 3);
+    w.step<0, 0, true, true, true>(i + 4);
+    w.step<1, 1, true, true, true>(i + 5);
   }
-  // n is even (S a multiple of 256): drain P(n-1), then O(n-1)
-  w.step<0, false, true, true>(i);
-  w.step<1, false, false, true>(i + 1);
+  if (i < n) {
+    w.step<0, 2, true, true, true>(i);
+    w.step<1, 0, true, true, true>(i + 1);
+    i += 2;
+  }
+  if (i < n) {
+    w.step<0, 1, true, true, true>(i);
+    w.step<1, 2, true, true, true>(i + 1);
+    i += 2;
+  }
+  w.step<0, -1, false, true, true>(i);
+  w.step<1, -1, false, false, true>(i + 1);
   // O[q][d], d = 32j + 8u + 4h + i
   const float inv = 1.0f / xor32_add(w.l);
   uint16_t* orow = p.O + w.base + q * W8_D;
