@@ -1226,3 +1226,62 @@ def make_block_matmul(ttl, bm, bk, bn):
                         ttl.copy(ob, out[r * bm:(r + 1) * bm, c * bn:(c + 1) * bn]).wait()
 
     return block_mm
+
+
+def make_matmul_epilogue(ttl, bm, bk, bn, epi="relu_bias", grid=(2, 2)):
+    """out = f(a @ b, c) in one store per output block: the spec's block
+    matmul (bm, bk) @ (bk, bn) over the whole K of a and b (bk = K / 32) or,
+    with bk = 1, the simulator's tile-wise product; c is a bias block of
+    the output's shape (or a row vector broadcast over the block's rows).
+    epi: "relu_bias" relu(a @ b + c), "row_bias" a @ b + broadcast(c_row),
+    "scale_exp" exp(a @ b * 0.125) * c.  Output blocks are dealt to the
+    cores of the grid row by row."""
+
+    @ttl.kernel(grid=grid)
+    def matmul_epilogue(a, b, c, out):
+        gx, gy = ttl.grid_size(dims=2)
+        rows = a.shape[0] // (bm * TILE)
+        cols = b.shape[1] // (bn * TILE)
+        per_core = rows * cols // (gx * gy)
+        a_cb = ttl.make_circular_buffer_like(a, shape=(bm, bk), buffer_factor=2)
+        b_cb = ttl.make_circular_buffer_like(b, shape=(bk, bn), buffer_factor=2)
+        c_cb = ttl.make_circular_buffer_like(c, shape=(1 if epi == "row_bias" else bm, bn),
+                                             buffer_factor=2)
+        o_cb = ttl.make_circular_buffer_like(out, shape=(bm, bn), buffer_factor=2)
+
+        @ttl.compute()
+        def comp():
+            for _ in range(per_core):
+                with a_cb.wait() as ab, b_cb.wait() as bb, c_cb.wait() as cc, \
+                        o_cb.reserve() as ob:
+                    if epi == "relu_bias":
+                        ob.store(ttl.math.relu(ab @ bb + cc))
+                    elif epi == "row_bias":
+                        ob.store(ab @ bb + ttl.math.broadcast(cc, dims=[0]))
+                    else:
+                        ob.store(ttl.math.exp(ab @ bb * 0.125) * cc)
+
+        @ttl.datamovement()
+        def reader():
+            cx, cy = ttl.core(dims=2)
+            first = (cx * gy + cy) * per_core
+            for t in range(per_core):
+                r, col = (first + t) // cols, (first + t) % cols
+                with a_cb.reserve() as ab, b_cb.reserve() as bb, c_cb.reserve() as cc:
+                    ttl.copy(a[r * bm:(r + 1) * bm, 0:bk], ab).wait()
+                    ttl.copy(b[0:bk, col * bn:(col + 1) * bn], bb).wait()
+                    if epi == "row_bias":
+                        ttl.copy(c[0, col * bn:(col + 1) * bn], cc).wait()
+                    else:
+                        ttl.copy(c[r * bm:(r + 1) * bm, col * bn:(col + 1) * bn], cc).wait()
+
+        @ttl.datamovement()
+        def writer():
+            cx, cy = ttl.core(dims=2)
+            first = (cx * gy + cy) * per_core
+            for t in range(per_core):
+                r, col = (first + t) // cols, (first + t) % cols
+                with o_cb.wait() as ob:
+                    ttl.copy(ob, out[r * bm:(r + 1) * bm, col * bn:(col + 1) * bn]).wait()
+
+    return matmul_epilogue

@@ -1,0 +1,55 @@
+"""A tile or block matmul inside a larger store expression on the MI355X:
+the plan's product launch (ttlh_matmul into a plan-owned tensor) and its
+elementwise launch, against a float64 evaluation of the same program and
+against the oracle's execution of the same kernel.
+
+Bar (as for the CPU plan in test_matmul_epilogue.py): within 2^-7 max |exact|
+of the float64 evaluation (product rounded to bf16 once, the other ops exact)
+and no worse than the oracle's error plus 2^-9 max |exact|.
+"""
+
+import pytest
+import torch
+
+import kernel_lib as KL
+import ttl
+import ttnn
+from ttlhip import plan as P
+from test_matmul_epilogue import CASES, exact, inputs, run_oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _gpu(case, tensors, kern=None):
+    bm, bk, bn, _, _, epi = case
+    kern = kern or KL.make_matmul_epilogue(ttl, bm, bk, bn, epi)
+    args = [ttnn.from_torch(t) for t in tensors]
+    kern(*args)
+    torch.cuda.synchronize()
+    return ttnn.to_torch(args[3]), kern
+
+
+def _check(case, seed=1, kern=None):
+    a, b, c, out = inputs(*case, seed=seed)
+    got, kern = _gpu(case, (a, b, c, out), kern)
+    ex = exact(a, b, c, case[5])
+    top = float(ex.abs().max())
+    e_gpu = float((got.double() - ex).abs().max())
+    e_orc = float((run_oracle(case, (a, b, c, out)).double() - ex).abs().max())
+    assert e_gpu <= 2 ** -7 * top, e_gpu
+    assert e_gpu <= e_orc + 2 ** -9 * top, (e_gpu, e_orc)
+    return kern
+
+
+@pytest.mark.parametrize("case", CASES + [(2, 8, 2, 8, 8, "relu_bias")])
+def test_matmul_epilogue_on_gpu(case):
+    kern = _check(case)
+    mm, ew = kern.last_plan.launches
+    assert isinstance(mm, P.MatmulLaunch) and isinstance(ew, P.EltwiseLaunch)
+
+
+def test_matmul_epilogue_plan_reused_with_new_inputs():
+    case = CASES[2]
+    kern = _check(case, seed=5)
+    _check(case, seed=9, kern=kern)
+    assert len(kern._cache) == 1

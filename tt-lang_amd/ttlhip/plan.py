@@ -540,6 +540,7 @@ def _deadlock_report(ct: Dict[str, Any], failed: Sequence[int] = ()) -> Optional
 def resolve(core_traces: List[Dict[str, Any]]) -> List[_Group]:
     """core_traces[c] = {"threads": [(template, root_node), ...]} for core c."""
     groups: Dict[Tuple, _Group] = {}
+    hoisted: Dict[Tuple, Tuple[Any, Any]] = {}
     # pass 1: events and tensor-filled copy tables of every core, for pipe sends
     pre = []
     for ct in core_traces:
@@ -640,6 +641,8 @@ def resolve(core_traces: List[Dict[str, Any]]) -> List[_Group]:
                 if e.tree[0] == "bmatmul":
                     _resolve_block_matmul(ev, e, target, rout, dt, fill, shape, groups)
                     continue
+                if e.tree[0] != "matmul" and (_has(e.tree, "matmul") or _has(e.tree, "bmatmul")):
+                    e = _hoist_matmuls(ev, e, target, rout, dt, fill, shape, groups, hoisted)
                 er, ec = e.shape
                 nslot = R * C
                 # output tile of every (instance, slot)
@@ -677,6 +680,105 @@ def resolve(core_traces: List[Dict[str, Any]]) -> List[_Group]:
     for sc in scratch.values():
         sc.check()
     return list(groups.values())
+
+
+class _HoistedCB:
+    """The stand-in CB of a product split off a store expression."""
+
+    def __init__(self, cid: int, dtype, name: str) -> None:
+        self.id, self.dtype, self.name = cid, dtype, name
+
+
+class _HoistedBlock:
+    def __init__(self, cb: _HoistedCB, event) -> None:
+        self.cb, self.event = cb, event
+
+
+class _Expr:
+    def __init__(self, tree, shape, dtype) -> None:
+        self.tree, self.shape, self.dtype = tree, tuple(shape), dtype
+
+
+def _hoist_matmuls(ev, e, target, rout, dt, fill, shape, groups, hoisted):
+    """A store whose expression holds a tile or block matmul below its root,
+    e.g. relu(a @ b + c): the simulator materialises the product block (in
+    the dtype its operands promote to) before the other ops read it
+    (python/sim/block.py:870-920), so the plan does the same: each product
+    becomes a matmul launch into a plan-owned tensor laid out like the
+    output, and the expression reads that tensor at the output's tile
+    positions as an ordinary operand.  Only products of blocks filled from
+    tensors, of the target's block shape, in stores without acc."""
+    if ev.data["acc"]:
+        raise PlanError("store(acc=True) of an expression that contains a tile matmul is not "
+                        "supported; store the product on its own")
+    R, C = target.shape
+    if tuple(e.shape) != (R, C):
+        raise PlanError(f"an expression of block shape {tuple(e.shape)} holding a tile matmul, "
+                        f"stored into a block of shape {(R, C)}")
+    slot = np.arange(R * C)
+    oi, oj = slot // C, slot % C
+    out_r = (dt.r0[rout][:, None] + oi[None, :]).ravel()
+    out_c = (dt.c0[rout][:, None] + oj[None, :]).ravel()
+    order = np.repeat(np.arange(rout.size), R * C)
+
+    def walk(tree):
+        tag = tree[0]
+        if tag in ("matmul", "bmatmul"):
+            la, lb = tree[1], tree[2]
+            if la[0] != "leaf" or lb[0] != "leaf":
+                raise PlanError("a tile matmul's operands must be blocks filled by ttl.copy from "
+                                "a tensor")
+            # leaf maps: a block matmul's over its operand blocks (M, K) / (K, N), a tile-wise
+            # product's over the expression's slots
+            shp = (len(la[2]), len(lb[3]))
+            if shp != (R, C):
+                raise PlanError(f"a tile matmul of block shape {shp} inside a store into a "
+                                f"block of shape {(R, C)}")
+            fa, fb = fill.get(la[1].cb.id), fill.get(lb[1].cb.id)
+            if fa is None or fb is None:
+                raise PlanError("a tile matmul's operands must be blocks filled by ttl.copy from "
+                                "a tensor")
+            da, db = la[1].cb.dtype, lb[1].cb.dtype
+            pdt = (torch.promote_types(da, db) if isinstance(da, torch.dtype)
+                   and isinstance(db, torch.dtype) else da)
+            key = (ev.data.get("loc"), _tree_key(tree, {}), id(fa.tensor), id(fb.tensor),
+                   id(dt.tensor))
+            if key not in hoisted:
+                cb = _HoistedCB(-1 - len(hoisted), pdt, "(matmul product)")
+                hoisted[key] = (_Temp(tuple(dt.tensor.shape), pdt), cb)
+            temp, cb = hoisted[key]
+            tab = _CopyTable(temp, dt.r0, dt.c0)
+            if tag == "bmatmul":
+                _resolve_block_matmul(ev, _Expr(tree, (R, C), pdt), target, rout, tab, fill, shape,
+                                      groups)
+            else:
+                leaf_rc = []
+                for lf in (la, lb):
+                    ft = fill[lf[1].cb.id]
+                    w = T.broadcast_to_domain(lf[1].event.index, shape).ravel()
+                    lr = (ft.r0[w][:, None] + np.asarray(lf[2])[oi][None, :]).ravel()
+                    lc = (ft.c0[w][:, None] + np.asarray(lf[3])[oj][None, :]).ravel()
+                    leaf_rc.append(np.stack([lr, lc], 1))
+                gkey = (_tree_key(tree, {}), (id(fa.tensor), id(fb.tensor)), id(temp), False)
+                g = groups.get(gkey)
+                if g is None:
+                    g = groups[gkey] = _Group(tree, [la, lb], [fa.tensor, fb.tensor], temp, False,
+                                              pdt, ev.data.get("loc"))
+                g.out_rc.append(np.stack([out_r, out_c], 1))
+                g.leaf_rc.append(leaf_rc)
+                g.order.append(order)
+            fill[cb.id] = tab
+            return ("leaf", _HoistedBlock(cb, target.event), list(range(R)), list(range(C)))
+        if tag in ("leaf", "const"):
+            return tree
+        if tag in ("powi", "upar"):
+            return (tag, walk(tree[1])) + tuple(tree[2:])
+        if tag == "reduce":
+            raise PlanError("a reduction combined with a tile matmul in one store() is not "
+                            "supported")
+        return (tag,) + tuple(walk(t) for t in tree[1:])
+
+    return _Expr(walk(e.tree), e.shape, e.dtype)
 
 
 def _resolve_block_matmul(ev, e, target, rout, dt, fill, shape, groups) -> None:
