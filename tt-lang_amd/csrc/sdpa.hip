@@ -713,7 +713,8 @@ __global__ __launch_bounds__(PP_THREADS, 1) void sdpa_pp_kernel(const SdpaArgs p
 // queries (D = 128, non-causal: C5).  KV blocks of 32 rows;
 // step i of the loop is one straight-line block:
 //     MFMAs: S(i) = K(i) Q^T and O += V(i-2)^T P(i-2)^T (16)
-//     VALU:  the softmax of S(i-1) -> P(i-1), running max / sum
+//     VALU:  the softmax of S(i-1) -> P(i-1) and its row sum (the running
+//            max moves only on a rare path, see below)
 // in eight sections, one per K / V fragment: the section's two MFMAs, a
 // share of the softmax VALU, and the LDS reads of the fragments two sections
 // ahead.  Two waves per SIMD because a wave alone cannot hide its VALU work:
@@ -724,7 +725,7 @@ __global__ __launch_bounds__(PP_THREADS, 1) void sdpa_pp_kernel(const SdpaArgs p
 // fragment feeds one MFMA (128 KB per step per CU; gfx950's LDS serves 256
 // bytes per clock to ds_read_b128 and ~186 to ds_read_b64_tr_b16, measured,
 // so the reads take ~600 of the step's 1024 MFMA cycles).  The accumulators
-// fit in the architectural VGPRs (214, no AGPRs), so the softmax reads S
+// fit in the architectural VGPRs (213, no AGPRs), so the softmax reads S
 // without copies.  The waves raise their priority (s_setprio 1) over the first six
 // sections, where MFMAs and LDS reads are densest, so a SIMD's matrix core
 // is fed first and the other wave's VALU fills the gaps.
@@ -732,7 +733,7 @@ __global__ __launch_bounds__(PP_THREADS, 1) void sdpa_pp_kernel(const SdpaArgs p
 // 16 bytes at the wave's base + 16 l) into rings of three K and three V
 // buffers (48 KB): step i reads K(i) from K buffer i % 3 and V(i - 2) from V
 // buffer (i - 2) % 3, and fetches K(i + 2) and V(i), two steps ahead of their
-// use (one step ahead, with two buffers each, measured 2% slower); one
+// use (one step ahead, with two buffers each, measured 0.4-2% slower); one
 // workgroup barrier per step.  Rows are unpadded with
 // XOR-swizzled 16-byte chunks: K chunk c of row r at c ^ (r & 15) (the S
 // operand reads 16 rows of one chunk per 16 lanes), V at c ^ 4 (r & 3) (a
