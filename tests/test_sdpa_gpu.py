@@ -125,6 +125,19 @@ def test_sdpa_causal_d64_and_value_layout():
     assert float((out.double() - expect).abs().max()) <= 63 * 2 ** -7
 
 
+def test_sdpa_blocks_uneven_over_the_workgroups():
+    # 75 heads x 4 query blocks = 300 blocks over at most one workgroup per
+    # CU: workgroups walk one or two blocks (the eight-wave kernel's
+    # persistent grid); sampled heads of every part of the sequence
+    B, H, S, D = 1, 75, 1024, 128
+    q, k, v = _qkv(B, H, S, D, 71)
+    scale = 1.0 / math.sqrt(D)
+    out = _run(q, k, v, scale)
+    for h in (0, 37, 63, 64, 74):
+        sl = (slice(None), slice(h, h + 1))
+        _check(out[sl], O.sdpa_ref(q[sl], k[sl], v[sl], scale))
+
+
 @pytest.mark.parametrize("jump", [False, True])
 def test_sdpa_running_max_growth(jump):
     # scores that grow along kv (several rescales of O and l by the running

@@ -26,7 +26,8 @@
 //    32 queries, two per SIMD, each interleaving the MFMAs of a KV block with
 //    the softmax of the previous one, the second wave's VALU issuing under
 //    the first one's MFMAs; Q pre-scaled and the S accumulation started from
-//    -m, so the softmax is one exp2 per score (details at its definition);
+//    -m, so the softmax is one exp2 per score; a persistent grid of one
+//    workgroup per CU (details at its definition);
 //  * sdpa_pp_kernel (other cases with S a multiple of 256): 8 waves, 256
 //    queries per workgroup, the two groups of four waves in ping-pong, one
 //    issuing the MFMAs of a block while the other runs the softmax of the
@@ -709,9 +710,9 @@ __global__ __launch_bounds__(PP_THREADS, 1) void sdpa_pp_kernel(const SdpaArgs p
 }
 
 // ---------------------------------------------------------------------------
-// 32 queries per wave, eight waves (two per SIMD) per workgroup of 256
-// queries (D = 128, non-causal: C5).  KV blocks of 32 rows;
-// step i of the loop is one straight-line block:
+// 32 queries per wave, eight waves (two per SIMD) per block of 256 queries
+// (D = 128, non-causal: C5).  KV blocks of 32 rows; step i of a block is one
+// straight-line piece of code:
 //     MFMAs: S(i) = K(i) Q^T and O += V(i-2)^T P(i-2)^T (16)
 //     VALU:  the softmax of S(i-1) -> P(i-1) and its row sum (the running
 //            max moves only on a rare path, see below)
@@ -725,19 +726,29 @@ __global__ __launch_bounds__(PP_THREADS, 1) void sdpa_pp_kernel(const SdpaArgs p
 // fragment feeds one MFMA (128 KB per step per CU; gfx950's LDS serves 256
 // bytes per clock to ds_read_b128 and ~186 to ds_read_b64_tr_b16, measured,
 // so the reads take ~600 of the step's 1024 MFMA cycles).  The accumulators
-// fit in the architectural VGPRs (213, no AGPRs), so the softmax reads S
+// fit in the architectural VGPRs (239, no AGPRs), so the softmax reads S
 // without copies.  The waves raise their priority (s_setprio 1) over the first six
 // sections, where MFMAs and LDS reads are densest, so a SIMD's matrix core
 // is fed first and the other wave's VALU fills the gaps.
 // K and V reach LDS by direct-to-LDS DMA (global_load_lds_dwordx4, lane l's
-// 16 bytes at the wave's base + 16 l) into rings of three K and three V
-// buffers (48 KB): step i reads K(i) from K buffer i % 3 and V(i - 2) from V
-// buffer (i - 2) % 3, and fetches K(i + 2) and V(i), two steps ahead of their
-// use (one step ahead, with two buffers each, measured 0.4-2% slower); one
-// workgroup barrier per step.  Rows are unpadded with
-// XOR-swizzled 16-byte chunks: K chunk c of row r at c ^ (r & 15) (the S
-// operand reads 16 rows of one chunk per 16 lanes), V at c ^ 4 (r & 3) (a
-// transpose read covers 4 rows x 4 chunks per 32 lanes).
+// 16 bytes at the wave's base + 16 l) into rings of four K and four V
+// buffers (64 KB): step t reads K(t) from K buffer t % 4 and V(t - 2) from V
+// buffer (t - 2) % 4, and loads K(t + 3) and V(t + 1); one workgroup barrier
+// per step, and each step's first two K / V fragments are read before the
+// previous step's barrier (their blocks were published one barrier earlier).
+// Rows are unpadded with XOR-swizzled 16-byte chunks: K chunk c of row r at
+// c ^ (r & 15) (the S operand reads 16 rows of one chunk per 16 lanes), V at
+// c ^ 4 (r & 3) (a transpose read covers 4 rows x 4 chunks per 32 lanes).
+// The grid is persistent: one workgroup per CU walks a sequence of query
+// blocks, and the step pipeline runs across block boundaries (t counts steps
+// over the sequence; a block is n steps, a multiple of 4, so the ring phases
+// repeat).  A block's steps 0 and 1 also carry the previous block's last
+// softmax and O products, its first K / V blocks are the loads that follow
+// the previous block's, its Q is staged into LDS four steps ahead (64 KB, per
+// wave) and loaded into registers at the end of the previous block, and a
+// finished block's O is stored after the step holding its last product: per
+// block there is no pipeline fill or drain, no Q load latency and no
+// workgroup launch (3% faster than one workgroup per block).
 constexpr int W8_BQ = 256;
 constexpr int W8_THREADS = 512;
 constexpr int W8_D = 128;
@@ -745,8 +756,10 @@ constexpr int W8_KV = 32;
 
 // one array per ring, so a buffer is a constant offset from the others (an
 // immediate in the LDS instructions, not another address register)
-__shared__ __attribute__((aligned(16))) uint16_t w8K[3][W8_KV * W8_D];
-__shared__ __attribute__((aligned(16))) uint16_t w8V[3][W8_KV * W8_D];
+__shared__ __attribute__((aligned(16))) uint16_t w8K[4][W8_KV * W8_D];
+__shared__ __attribute__((aligned(16))) uint16_t w8V[4][W8_KV * W8_D];
+// per wave, the next block's 32 Q rows (staged four steps ahead)
+__shared__ __attribute__((aligned(16))) uint16_t w8Q[8][32 * W8_D];
 
 template <int B>
 __device__ __forceinline__ uint16_t* w8_kbuf() {
@@ -763,8 +776,7 @@ struct SdpaW8 {
   static constexpr int D = W8_D, ND = D / 32, NDC = D / 16;
 
   const SdpaArgs& p;
-  int64_t base;
-  int qb, wave, lane, l32, h, n;
+  int wave, lane, l32, h, n;
   bf16x8 qop[NDC];          // Q^T operands, scaled by scale * log2(e)
   f32x16 o[ND];             // O^T accumulators
   f32x16 s;                 // S(i) - m accumulating
@@ -775,6 +787,7 @@ struct SdpaW8 {
   int k_src, v_src;         // per-lane DMA source offsets (elements)
   int v_frag[ND];           // LDS offsets of the V transpose reads
   uint32_t lds_wave;        // the wave's byte offset in a K / V buffer (uniform)
+  bf16x8 kpf[2], vpf[2];    // the next step's first K / V fragments, read before the barrier
 
   __device__ __forceinline__ void setup() {
     lds_wave = __builtin_amdgcn_readfirstlane(wave * 1024);
@@ -805,7 +818,8 @@ struct SdpaW8 {
   // Both uniform operands pass through readfirstlane, so they are SGPRs
   // whatever the register allocator made of them (free when they already
   // are); readfirstlane returns int, so each pointer half widens unsigned.
-  __device__ __forceinline__ void dma(const uint16_t* X, int src, int kv0, const uint16_t* lds) {
+  __device__ __forceinline__ void dma(const uint16_t* X, int64_t base, int src, int kv0,
+                                      const uint16_t* lds) {
     const uint64_t g = reinterpret_cast<uint64_t>(X + base + static_cast<int64_t>(kv0) * D);
     const uint64_t gs =
         (uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(g >> 32)))) << 32) |
@@ -886,6 +900,8 @@ struct SdpaW8 {
   // and the s_nop after it precedes any MFMA that reads what it wrote.
   template <int PAR, bool SHIFT_S>
   __device__ __forceinline__ void rescale(const f32x16& sp) {
+    // SHIFT_S: S(i) was accumulated from the old -m (main steps); otherwise
+    // S(i) is a new block's raw first block or absent, and -m is reset
     const float bm = xor32_max(max16(sp));
     const float d = bm > kLazy ? bm : 0.0f;
     const float alpha = __builtin_amdgcn_exp2f(-d);
@@ -905,10 +921,12 @@ struct SdpaW8 {
     for (int j = 0; j < ND; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) asm volatile("v_mul_f32 %0, %1, %0" : "+v"(o[j][r]) : "v"(alpha));
+    if constexpr (SHIFT_S) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      if constexpr (SHIFT_S) asm volatile("v_sub_f32 %0, %0, %1" : "+v"(sv[r]) : "v"(d));
-      asm volatile("v_mov_b32 %0, %1" : "+v"(negm[r]) : "v"(-m));
+      for (int r = 0; r < 16; ++r) {
+        asm volatile("v_sub_f32 %0, %0, %1" : "+v"(sv[r]) : "v"(d));
+        asm volatile("v_mov_b32 %0, %1" : "+v"(negm[r]) : "v"(-m));
+      }
     }
     asm volatile("s_nop 7");
   }
@@ -916,47 +934,120 @@ struct SdpaW8 {
   // VALU slots of a section (for the interleave below)
   static constexpr int kSectionValu[8] = {5, 4, 4, 4, 4, 4, 4, 4};
 
-  // one step (see the header): S(i) into s (renamed to sv at the end),
-  // softmax of sv into pw[PAR ^ 1], O += V(i-2) P(i-2) with P(i-2) in pw[PAR];
-  // PAR = i % 2, KB = i % 3 (KB < 0: taken from i at run time, for the two
-  // drain steps, which read no K)
-  template <int PAR, int KB, bool DO_S, bool DO_SM, bool DO_O>
-  __device__ __forceinline__ void step(int i) {
-    static_assert(KB >= 0 || !DO_S, "a step computing S needs its K buffer at compile time");
-    const uint16_t* Kc = w8_kbuf<KB < 0 ? 0 : KB>();
-    const uint16_t* Vc = KB < 0 ? w8V[(i + 1) % 3] : w8_vbuf<(KB + 1) % 3>();
-    const f32x16 sp = sv;  // S(i - 1) - m, for the rare path
+  // ---- the workgroup's sequence of query blocks (persistent grid) ----
+  int G, g, nblk, nqb;
+  float l_prev;
+  __device__ __forceinline__ int perm() const {
+    return G % 8 == 0 ? (g % 8) * (G / 8) + g / 8 : g;
+  }
+  __device__ __forceinline__ void block(int jb, int64_t& base, int& qb) const {
+    const int L = jb * G + perm();
+    const int bh = L / nqb;
+    qb = L - bh * nqb;
+    base = static_cast<int64_t>(bh) * p.S * D;
+  }
+
+  // Q rows of a block into the wave's staging buffer (swizzled like K),
+  // 8 DMA instructions per wave; read back by the same wave only
+  __device__ __forceinline__ void stage_q(int64_t base, int qb) {
+    const int64_t row0 = static_cast<int64_t>(qb) * W8_BQ + 32 * wave;
+#pragma unroll
+    for (int ins = 0; ins < 8; ++ins) {
+      const int r = 4 * ins + (lane >> 4), pc = lane & 15;
+      const int src = r * D + ((pc ^ (r & 15)) << 3);
+      const uint64_t gq = reinterpret_cast<uint64_t>(p.Q + base + row0 * D);
+      const uint64_t gs =
+          (uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(gq >> 32)))) << 32) |
+          uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(gq))));
+      const uint32_t buf = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+          (w8_lds_void*)(w8Q[wave] + ins * 512)));
+      asm volatile(
+          "s_mov_b32 m0, %0\n\t"
+          "s_nop 0\n\t"
+          "global_load_lds_dwordx4 %1, %2"
+          :
+          : "s"(__builtin_amdgcn_readfirstlane(buf)), "v"(static_cast<uint32_t>(src) * 2u),
+            "s"(gs)
+          : "memory", "m0");
+    }
+  }
+  __device__ __forceinline__ void scale_q(const bf16x8 (&x)[NDC]) {
+#pragma unroll
+    for (int dc = 0; dc < NDC; ++dc)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        qop[dc][e] = static_cast<__bf16>(static_cast<float>(x[dc][e]) * p.scale_log2);
+  }
+
+  // O / l of a finished block into its rows: O[q][d], d = 32j + 8u + 4h + i
+  __device__ __forceinline__ void store_o(int64_t base, int qb, float lsum) {
+    const float inv = 1.0f / xor32_add(lsum);
+    const int64_t q = static_cast<int64_t>(qb) * W8_BQ + 32 * wave + l32;
+    uint16_t* orow = p.O + base + q * D;
+#pragma unroll
+    for (int j = 0; j < ND; ++j)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int d = 32 * j + 8 * u + 4 * h;
+        const u32x2 v = {pk_bf16(o[j][4 * u] * inv, o[j][4 * u + 1] * inv),
+                         pk_bf16(o[j][4 * u + 2] * inv, o[j][4 * u + 3] * inv)};
+        *reinterpret_cast<u32x2*>(orow + d) = v;
+      }
+  }
+
+  // one step at global step t (PAR = t % 2, KB = t % 4): S(t) = K(t) Q^T into
+  // s (renamed to sv at the end), the softmax of sv into pw[PAR ^ 1], and
+  // O += V(t - 2) P(t - 2) with P(t - 2) in pw[PAR]; K(t) in K buffer KB,
+  // V(t - 2) in V buffer (KB + 2) % 4.  Flags:
+  //   NEXT_S / NEXT_O  the next step computes S / O (its first fragments are
+  //                    read at the end of this step, before the barrier);
+  //   OZERO            O starts from zero (a block's first O step);
+  //   SZERO            S starts from zero (a block's first KV step);
+  //   CHECK / SHIFT    the rare-path check; whether it also shifts S(t), -m;
+  //   QPF              also stage the next block's Q (8 more loads);
+  //   QSW              at the end, load the next block's Q into qop.
+  //   kb, kk / vb, vk: base and KV step of the K / V block this step loads
+  //                    (K of step t + 3, V of step t + 1, possibly of the
+  //                    next block)
+  template <int PAR, int KB, bool DO_S, bool DO_SM, bool DO_O, bool NEXT_S, bool NEXT_O,
+            bool OZERO, bool SZERO, bool CHECK, bool SHIFT, bool QPF = false, bool QSW = false>
+  __device__ __forceinline__ void step(int64_t kb, int kk, int64_t vb, int vk,
+                                       int64_t nq_base = 0, int nq_qb = 0) {
+    const uint16_t* Kc = w8_kbuf<KB>();
+    const uint16_t* Vc = w8_vbuf<(KB + 2) % 4>();
+    const f32x16 sp = sv;  // S(t - 1) - m, for the rare path
     bf16x8 kf[8], vf[8];
     auto issue = [&](auto xc) {
       constexpr int x = decltype(xc)::value;
       if constexpr (DO_S) kf[x] = kfrag(Kc, x);
       if constexpr (DO_O) vf[x] = vfrag(Vc, x >> 1, x & 1);
     };
-    // the first fragments' LDS reads go out right after the barrier, the
-    // next stage's DMA behind them
-    issue(std::integral_constant<int, 0>());
-    issue(std::integral_constant<int, 1>());
-    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (DO_S) { kf[0] = kpf[0]; kf[1] = kpf[1]; }
+    if constexpr (DO_O) { vf[0] = vpf[0]; vf[1] = vpf[1]; }
     if constexpr (DO_S) {
-      // steps 0 .. n - 1: K(i + 2), clamped to K(n - 1) (past the end it
-      // refills a buffer that no later step reads: the last two steps read
-      // no K), and V(i)
-      dma(p.K, k_src, min(i + 2, n - 1) * W8_KV, w8_kbuf<(KB + 2) % 3>());
-      dma(p.V, v_src, i * W8_KV, w8_vbuf<KB>());
+      dma(p.K, kb, k_src, kk * W8_KV, w8_kbuf<(KB + 3) % 4>());
+      dma(p.V, vb, v_src, vk * W8_KV, w8_vbuf<(KB + 1) % 4>());
     }
+    if constexpr (QPF) stage_q(nq_base, nq_qb);
     __builtin_amdgcn_sched_barrier(0);
     sd_static_for<8>([&](auto xc) {
       constexpr int x = decltype(xc)::value;
       if constexpr (x == 0) __builtin_amdgcn_s_setprio(1);
       if constexpr (x == 6) __builtin_amdgcn_s_setprio(0);
-      if constexpr (DO_S)
-        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[x], qop[x], x == 0 ? negm : s, 0, 0, 0);
-      if constexpr (DO_O)
+      if constexpr (DO_S) {
+        const f32x16 z = {};
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[x], qop[x],
+                                                    x == 0 ? (SZERO ? z : negm) : s, 0, 0, 0);
+      }
+      if constexpr (DO_O) {
+        const f32x16 z = {};
         o[x >> 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            vf[x], __builtin_bit_cast(bf16x8, pw[PAR][x & 1]), o[x >> 1], 0, 0, 0);
+            vf[x], __builtin_bit_cast(bf16x8, pw[PAR][x & 1]),
+            (OZERO && (x & 1) == 0) ? z : o[x >> 1], 0, 0, 0);
+      }
       if constexpr (x + 2 < 8) issue(std::integral_constant<int, x + 2>());
       if constexpr (DO_SM) expo2<PAR ^ 1, x>();
-      if constexpr (DO_S && x == 7) sv = s;  // the next step's softmax reads S(i)
+      if constexpr (DO_S && x == 7) sv = s;  // the next step's softmax reads S(t)
       constexpr int nm = (DO_S ? 1 : 0) + (DO_O ? 1 : 0);
       constexpr int nv = DO_SM ? (kSectionValu[x] + nm - 1) / nm : 0;
       sd_static_for<nm>([&](auto) {
@@ -967,103 +1058,134 @@ struct SdpaW8 {
       __builtin_amdgcn_sched_barrier(0);
     });
     if constexpr (DO_SM) {
-      if (__builtin_expect(__any(rsum_ > kSumLimit), 0)) rescale<PAR ^ 1, DO_S>(sp);
+      if constexpr (CHECK) {
+        if (__builtin_expect(__any(rsum_ > kSumLimit), 0)) rescale<PAR ^ 1, SHIFT>(sp);
+      }
       l += rsum_;
     }
-    // the previous step's loads landed (this step's two may stay in flight),
-    // this step's reads are done: publish / release
-    if constexpr (DO_S) __builtin_amdgcn_s_waitcnt(0x0072);  // vmcnt(2) lgkmcnt(0)
-    else __builtin_amdgcn_s_waitcnt(0x0070);                 // vmcnt(0) lgkmcnt(0)
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (QSW) {
+      bf16x8 x[NDC];
+#pragma unroll
+      for (int dc = 0; dc < NDC; ++dc) x[dc] = kfrag(w8Q[wave], dc);
+      scale_q(x);
+    }
+    // the next step's first fragments: K(t + 1) and V(t - 1), published at
+    // the previous barrier (their loads were issued two steps ago)
+    if constexpr (NEXT_S) {
+      kpf[0] = kfrag(w8_kbuf<(KB + 1) % 4>(), 0);
+      kpf[1] = kfrag(w8_kbuf<(KB + 1) % 4>(), 1);
+    }
+    if constexpr (NEXT_O) {
+      vpf[0] = vfrag(w8_vbuf<(KB + 3) % 4>(), 0, 0);
+      vpf[1] = vfrag(w8_vbuf<(KB + 3) % 4>(), 0, 1);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // the previous step's loads landed (this step's may stay in flight), this
+    // step's reads are done except the prefetch: publish / release
+    constexpr int npf = (NEXT_S ? 2 : 0) + (NEXT_O ? 4 : 0);
+    constexpr int nvm = (DO_S ? 2 : 0) + (QPF ? 8 : 0);
+    __builtin_amdgcn_s_waitcnt((nvm & 15) | ((nvm >> 4) << 14) | 0x0070 | (npf << 8));
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
   }
+
+  // a block's S(0) (raw) is in sv: m = its maximum, S(0) and -m rebased
+  __device__ __forceinline__ void start_block() {
+    m = xor32_max(max16(sv));
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      sv[r] -= m;
+      negm[r] = -m;
+    }
+  }
 };
 
+// Block jb of workgroup g is query block jb * G + perm(g): perm puts the
+// workgroups of one XCD (g % 8 under round-robin dispatch) on consecutive
+// blocks, so at any time an XCD works on the query blocks of one or two heads
+// and its L2 serves their K / V to all of them.
 __global__ __launch_bounds__(W8_THREADS, 1) void sdpa_w8_kernel(const SdpaArgs p) {
   SdpaW8 w{p};
-  int bh;
-  block_coords(p, bh, w.qb);
   w.lane = threadIdx.x & 63;
   w.wave = threadIdx.x >> 6;
   w.l32 = w.lane & 31;
   w.h = w.lane >> 5;
-  w.base = static_cast<int64_t>(bh) * p.S * W8_D;
   w.n = p.S / W8_KV;
+  w.nqb = p.nqb;
+  w.G = gridDim.x;
+  w.g = blockIdx.x;
+  const int total = p.nbh * p.nqb;
+  w.nblk = (total - w.perm() + w.G - 1) / w.G;
   w.l = 0.0f;
   w.setup();
-  // Q^T of the wave's tile: query row qb * 256 + 32 wave + l32
-  const int64_t q = static_cast<int64_t>(w.qb) * W8_BQ + 32 * w.wave + w.l32;
+  const int n = w.n;  // >= 8, a multiple of 8
+  int64_t cur_base;
+  int cur_qb;
+  w.block(0, cur_base, cur_qb);
+  {
+    bf16x8 x[SdpaW8::NDC];
+    const int64_t q = static_cast<int64_t>(cur_qb) * W8_BQ + 32 * w.wave + w.l32;
 #pragma unroll
-  for (int dc = 0; dc < SdpaW8::NDC; ++dc) {
-    const bf16x8 x = *reinterpret_cast<const bf16x8*>(p.Q + w.base + q * W8_D + dc * 16 + 8 * w.h);
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      w.qop[dc][e] = static_cast<__bf16>(static_cast<float>(x[e]) * p.scale_log2);
+    for (int dc = 0; dc < SdpaW8::NDC; ++dc)
+      x[dc] = *reinterpret_cast<const bf16x8*>(p.Q + cur_base + q * W8_D + dc * 16 + 8 * w.h);
+    w.scale_q(x);
   }
-#pragma unroll
-  for (int r = 0; r < 16; ++r) w.negm[r] = 0.0f;
-#pragma unroll
-  for (int j = 0; j < SdpaW8::ND; ++j)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) w.o[j][r] = 0.0f;
-  // K(0), K(1) into K buffers 0, 1 (with Q landed), then the pipeline
-  w.dma(p.K, w.k_src, 0, w8_kbuf<0>());
-  w.dma(p.K, w.k_src, W8_KV, w8_kbuf<1>());
+  // K(0), K(1), K(2) and V(0) of block 0 (with Q landed), then the pipeline
+  w.dma(p.K, cur_base, w.k_src, 0, w8_kbuf<0>());
+  w.dma(p.K, cur_base, w.k_src, W8_KV, w8_kbuf<1>());
+  w.dma(p.K, cur_base, w.k_src, 2 * W8_KV, w8_kbuf<2>());
+  w.dma(p.V, cur_base, w.v_src, 0, w8_vbuf<0>());
   __builtin_amdgcn_s_waitcnt(0x0070);
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  const int n = w.n;  // >= 8 (S >= 256)
-  w.step<0, 0, true, false, false>(0);
-  // m starts at block 0's maximum; S(0) is shifted by it here, every later
-  // block accumulates from -m
-  w.m = xor32_max(SdpaW8::max16(w.sv));
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    w.sv[r] -= w.m;
-    w.negm[r] = -w.m;
-  }
-  w.step<1, 1, true, true, false>(1);
-  // main steps 2 .. n - 1 (step i: PAR = i % 2, KB = i % 3, period 6), then
-  // the drain of P(n - 1) and O(n - 1); n is a multiple of 8, so n - 2 main
-  // steps leave 0, 2 or 4 after the unrolled loop, which continue its
-  // pattern (KB 2, 0, then 1, 2).  (Three separate tails, one per n % 3,
-  // made the compiler spill.)
-  int i = 2;
-  for (; i + 5 < n; i += 6) {
-    w.step<0, 2, true, true, true>(i);
-    w.step<1, 0, true, true, true>(i + 1);
-    w.step<0, 1, true, true, true>(i + 2);
-    w.step<1, 2, true, true, true>(i + 3);
-    w.step<0, 0, true, true, true>(i + 4);
-    w.step<1, 1, true, true, true>(i + 5);
-  }
-  if (i < n) {
-    w.step<0, 2, true, true, true>(i);
-    w.step<1, 0, true, true, true>(i + 1);
-    i += 2;
-  }
-  if (i < n) {
-    w.step<0, 1, true, true, true>(i);
-    w.step<1, 2, true, true, true>(i + 1);
-    i += 2;
-  }
-  w.step<0, -1, false, true, true>(i);
-  w.step<1, -1, false, false, true>(i + 1);
-  // O[q][d], d = 32j + 8u + 4h + i
-  const float inv = 1.0f / xor32_add(w.l);
-  uint16_t* orow = p.O + w.base + q * W8_D;
-#pragma unroll
-  for (int j = 0; j < SdpaW8::ND; ++j)
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int d = 32 * j + 8 * u + 4 * w.h;
-      const u32x2 v = {pk_bf16(w.o[j][4 * u] * inv, w.o[j][4 * u + 1] * inv),
-                       pk_bf16(w.o[j][4 * u + 2] * inv, w.o[j][4 * u + 3] * inv)};
-      *reinterpret_cast<u32x2*>(orow + d) = v;
+  w.kpf[0] = w.kfrag(w8_kbuf<0>(), 0);
+  w.kpf[1] = w.kfrag(w8_kbuf<0>(), 1);
+  //          PAR KB S  SM O  NS NO OZ SZ CK SH
+  w.step<0, 0, 1, 0, 0, 1, 0, 0, 1, 0, 0>(cur_base, 3, cur_base, 1);
+  w.start_block();
+  w.step<1, 1, 1, 1, 0, 1, 1, 0, 0, 0, 0>(cur_base, 4, cur_base, 2);
+  // one path per block: steps 2 .. n - 1 of block jb, then the next block's
+  // steps 0 and 1, which also finish block jb (its last softmax and O
+  // products) before its O is stored.  After the last block the "next" block
+  // is the last one again: its first steps run for nothing, and no later
+  // step reads what they load.
+  for (int jb = 0;; ++jb) {
+    const int64_t cb = cur_base;
+    w.step<0, 2, 1, 1, 1, 1, 1, 1, 0, 1, 1>(cb, 5, cb, 3);
+    w.step<1, 3, 1, 1, 1, 1, 1, 0, 0, 1, 1>(cb, 6, cb, 4);
+    for (int i = 4; i + 4 < n; i += 4) {
+      w.step<0, 0, 1, 1, 1, 1, 1, 0, 0, 1, 1>(cb, i + 3, cb, i + 1);
+      w.step<1, 1, 1, 1, 1, 1, 1, 0, 0, 1, 1>(cb, i + 4, cb, i + 2);
+      w.step<0, 2, 1, 1, 1, 1, 1, 0, 0, 1, 1>(cb, i + 5, cb, i + 3);
+      w.step<1, 3, 1, 1, 1, 1, 1, 0, 0, 1, 1>(cb, i + 6, cb, i + 4);
     }
+    const bool last = jb + 1 == w.nblk;
+    int64_t nb = cb;
+    int nq = cur_qb;
+    if (!last) w.block(jb + 1, nb, nq);
+    // steps n - 4 .. n - 1: the next block's first K / V blocks, its Q staged
+    // and then loaded into qop
+    w.step<0, 0, 1, 1, 1, 1, 1, 0, 0, 1, 1, true, false>(cb, n - 1, cb, n - 3, nb, nq);
+    w.step<1, 1, 1, 1, 1, 1, 1, 0, 0, 1, 1>(nb, 0, cb, n - 2);
+    w.step<0, 2, 1, 1, 1, 1, 1, 0, 0, 1, 1>(nb, 1, cb, n - 1);
+    w.step<1, 3, 1, 1, 1, 1, 1, 0, 0, 1, 1, false, true>(nb, 2, nb, 0);
+    // the next block's steps 0 and 1 with this block's last softmax / O
+    w.step<0, 0, 1, 1, 1, 1, 1, 0, 1, 1, 0>(nb, 3, nb, 1);
+    w.l_prev = w.l;
+    w.l = 0.0f;
+    w.start_block();
+    w.step<1, 1, 1, 1, 1, 1, 1, 0, 0, 0, 0>(nb, 4, nb, 2);
+    w.store_o(cb, cur_qb, w.l_prev);
+    if (last) break;
+    cur_base = nb;
+    cur_qb = nq;
+  }
+  // the unused loads of the last block's "next" block land before the end
+  __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
 }
 
 template <int D, bool CAUSAL>
@@ -1071,7 +1193,14 @@ int launch(const SdpaArgs& a, hipStream_t s) {
   if (D == W8_D && !CAUSAL && a.S % W8_BQ == 0) {
     SdpaArgs b = a;
     b.nqb = a.S / W8_BQ;
-    hipLaunchKernelGGL(sdpa_w8_kernel, dim3(b.nbh * b.nqb), dim3(W8_THREADS), 0, s, b);
+    // persistent: one workgroup per CU (at most), each walking its blocks
+    int dev = 0, cus = 0;
+    TTLH_HIP_CHECK(hipGetDevice(&dev));
+    TTLH_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    TTLH_REQUIRE(cus > 0, TTLH_EHIP, "ttlh_sdpa_fwd: the device reports no CUs");
+    const int64_t total = static_cast<int64_t>(b.nbh) * b.nqb;
+    const int grid = static_cast<int>(total < cus ? total : cus);
+    hipLaunchKernelGGL(sdpa_w8_kernel, dim3(grid), dim3(W8_THREADS), 0, s, b);
     return check_launch("sdpa_w8_kernel");
   }
   if (a.S % PP_BQ == 0) {
