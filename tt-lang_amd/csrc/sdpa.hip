@@ -950,6 +950,7 @@ struct SdpaW8 {
   // Q rows of a block into the wave's staging buffer (swizzled like K),
   // 8 DMA instructions per wave; read back by the same wave only
   __device__ __forceinline__ void stage_q(int64_t base, int qb) {
+    if (qb < 0) return;  // no next block
     const int64_t row0 = static_cast<int64_t>(qb) * W8_BQ + 32 * wave;
 #pragma unroll
     for (int ins = 0; ins < 8; ++ins) {
@@ -1150,9 +1151,9 @@ __global__ __launch_bounds__(W8_THREADS, 1) void sdpa_w8_kernel(const SdpaArgs p
   w.step<1, 1, 1, 1, 0, 1, 1, 0, 0, 0, 0>(cur_base, 4, cur_base, 2);
   // one path per block: steps 2 .. n - 1 of block jb, then the next block's
   // steps 0 and 1, which also finish block jb (its last softmax and O
-  // products) before its O is stored.  After the last block the "next" block
-  // is the last one again: its first steps run for nothing, and no later
-  // step reads what they load.
+  // products) before its O is stored.  After the last block the "next"
+  // block's steps run for nothing: their loads repeat the last block's last
+  // K / V rows (still in L2), nothing reads them, and no Q is staged.
   for (int jb = 0;; ++jb) {
     const int64_t cb = cur_base;
     w.step<0, 2, 1, 1, 1, 1, 1, 1, 0, 1, 1>(cb, 5, cb, 3);
@@ -1165,20 +1166,21 @@ __global__ __launch_bounds__(W8_THREADS, 1) void sdpa_w8_kernel(const SdpaArgs p
     }
     const bool last = jb + 1 == w.nblk;
     int64_t nb = cb;
-    int nq = cur_qb;
+    int nq = -1;
     if (!last) w.block(jb + 1, nb, nq);
+    const auto nk = [&](int k) { return last ? n - 1 : k; };  // KV step of the next block
     // steps n - 4 .. n - 1: the next block's first K / V blocks, its Q staged
     // and then loaded into qop
     w.step<0, 0, 1, 1, 1, 1, 1, 0, 0, 1, 1, true, false>(cb, n - 1, cb, n - 3, nb, nq);
-    w.step<1, 1, 1, 1, 1, 1, 1, 0, 0, 1, 1>(nb, 0, cb, n - 2);
-    w.step<0, 2, 1, 1, 1, 1, 1, 0, 0, 1, 1>(nb, 1, cb, n - 1);
-    w.step<1, 3, 1, 1, 1, 1, 1, 0, 0, 1, 1, false, true>(nb, 2, nb, 0);
+    w.step<1, 1, 1, 1, 1, 1, 1, 0, 0, 1, 1>(nb, nk(0), cb, n - 2);
+    w.step<0, 2, 1, 1, 1, 1, 1, 0, 0, 1, 1>(nb, nk(1), cb, n - 1);
+    w.step<1, 3, 1, 1, 1, 1, 1, 0, 0, 1, 1, false, true>(nb, nk(2), nb, nk(0));
     // the next block's steps 0 and 1 with this block's last softmax / O
-    w.step<0, 0, 1, 1, 1, 1, 1, 0, 1, 1, 0>(nb, 3, nb, 1);
+    w.step<0, 0, 1, 1, 1, 1, 1, 0, 1, 1, 0>(nb, nk(3), nb, nk(1));
     w.l_prev = w.l;
     w.l = 0.0f;
     w.start_block();
-    w.step<1, 1, 1, 1, 1, 1, 1, 0, 0, 0, 0>(nb, 4, nb, 2);
+    w.step<1, 1, 1, 1, 1, 1, 1, 0, 0, 0, 0>(nb, nk(4), nb, nk(2));
     w.store_o(cb, cur_qb, w.l_prev);
     if (last) break;
     cur_base = nb;
