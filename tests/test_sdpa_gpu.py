@@ -159,6 +159,27 @@ def test_sdpa_running_max_growth(jump):
         _check(out, O.sdpa_ref(q, k, v, 1.0, causal=causal))
 
 
+def test_sdpa_running_max_growth_in_later_blocks_of_a_workgroup():
+    # 260 heads x 2 query blocks = 520 blocks over at most one workgroup per
+    # CU: workgroups walk 2 or 3 blocks, and the running-max rescales (scores
+    # growing along kv, one late key far above the rest) happen in every block,
+    # so a block's rescale state must not leak into the next
+    B, H, S, D = 1, 260, 512, 128
+    q = torch.zeros(B, H, S, D)
+    q[..., 0] = 1.0
+    q[..., 1] = torch.linspace(-1, 1, S)
+    k = torch.zeros(B, H, S, D)
+    k[..., 0] = torch.linspace(0, 30, S)
+    k[..., 1] = 0.5
+    k[:, 1::2, S - 70, 0] = 1000.0
+    v = O.seeded((B, H, S, D), "normal", 81)
+    q, k = q.bfloat16(), k.bfloat16()
+    out = _run(q, k, v, 1.0)
+    for h in (0, 1, 127, 200, 258, 259):
+        sl = (slice(None), slice(h, h + 1))
+        _check(out[sl], O.sdpa_ref(q[sl], k[sl], v[sl], 1.0))
+
+
 @pytest.mark.parametrize("S", [32, 96, 160, 224, 416])
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("causal", [False, True])
