@@ -118,11 +118,12 @@ def run_matmul(l: MatmulLaunch, args):
     a, b, c = l.a.resolve(args), l.b.resolve(args), l.c.resolve(args)
     r0, r1 = l.rows
     c0, c1 = l.cols
+    (ar0, ar1), (bc0, bc1) = l.operand_ranges()
     if l.b_block:  # packed block-float tiles: the oracle's integer decoders
         from oracle import bfp8 as OB
         fmt = l.b.resolve_obj(args).dtype.codec
         b = (OB.unpack_c if fmt == "bfp8" else OB.unpack4_c)(b.cpu(), a.shape[1], c.shape[1])
-    c[r0:r1, c0:c1] = (a[r0:r1].double() @ b[:, c0:c1].double()).to(c.dtype)
+    c[r0:r1, c0:c1] = (a[ar0:ar1].double() @ b[:, bc0:bc1].double()).to(c.dtype)
 
 
 def run_sdpa(l: SdpaLaunch, args):

@@ -129,6 +129,72 @@ def test_one_block_product_plus_bias_plans():
     assert [type(l) for l in plan.launches] == [P.MatmulLaunch, P.EltwiseLaunch]
 
 
+def _two_products_kernel(ns):
+    @ns.kernel(grid=(1, 1))
+    def k(a, b, out):
+        a0_cb = ns.make_circular_buffer_like(a, shape=(1, 2), buffer_factor=2)
+        a1_cb = ns.make_circular_buffer_like(a, shape=(1, 2), buffer_factor=2)
+        b_cb = ns.make_circular_buffer_like(b, shape=(2, 3), buffer_factor=2)
+        o_cb = ns.make_circular_buffer_like(out, shape=(1, 3), buffer_factor=2)
+
+        @ns.compute()
+        def comp():
+            with a0_cb.wait() as a0, a1_cb.wait() as a1, b_cb.wait() as bb, \
+                    o_cb.reserve() as ob:
+                ob.store(a0 @ bb + a1 @ bb)
+            with a0_cb.wait() as a0, b_cb.wait() as bb, o_cb.reserve() as ob:
+                ob.store(a0 @ bb * (a0 @ bb))
+            with a1_cb.wait() as a1, b_cb.wait() as bb, o_cb.reserve() as ob:
+                ob.store(a1 @ bb)
+
+        @ns.datamovement()
+        def rd():
+            with a0_cb.reserve() as x, a1_cb.reserve() as y, b_cb.reserve() as z:
+                ns.copy(a[0:1, 0:2], x).wait()
+                ns.copy(a[1:2, 0:2], y).wait()
+                ns.copy(b[0:2, 0:3], z).wait()
+            with a0_cb.reserve() as x, b_cb.reserve() as z:
+                ns.copy(a[0:1, 0:2], x).wait()
+                ns.copy(b[0:2, 0:3], z).wait()
+            with a1_cb.reserve() as y, b_cb.reserve() as z:
+                ns.copy(a[1:2, 0:2], y).wait()
+                ns.copy(b[0:2, 0:3], z).wait()
+
+        @ns.datamovement()
+        def wr():
+            for r in range(3):
+                with o_cb.wait() as ob:
+                    ns.copy(ob, out[r:r + 1, 0:3]).wait()
+
+    return k
+
+
+def two_products_case():
+    a = O.seeded((64, 64), "normal", 3)
+    b = O.seeded((64, 96), "normal", 4)
+    p0 = (a[:32].double() @ b.double()).to(torch.bfloat16).double()
+    p1 = (a[32:].double() @ b.double()).to(torch.bfloat16).double()
+    return (a, b, torch.zeros(96, 96, dtype=torch.bfloat16)), torch.cat([p0 + p1, p0 * p0, p1])
+
+
+def test_two_products_in_one_expression_and_an_offset_product():
+    # two products of blocks of the same tensors (a's tile rows 0 and 1, the
+    # same b) each get their own tensor: a0 @ b + a1 @ b, a0 @ b twice; and
+    # a1 @ b stored into output tile row 2 (A read at a fixed row offset)
+    tensors, ex = two_products_case()
+    args = [ttnn.Tensor(t.clone()) for t in tensors]
+    plan = _two_products_kernel(ttl).trace(*args)
+    assert sum(isinstance(l, P.MatmulLaunch) for l in plan.launches) == 5
+    plan_interp.run(plan, dict(enumerate(args)))
+    oargs = [sim_exec.OracleTensor(t.clone()) for t in tensors]
+    _two_products_kernel(sim_exec.make_ttl())(*oargs)
+    top = float(ex.abs().max())
+    e_plan = float((args[2]._tensor.double() - ex).abs().max())
+    e_orc = float((oargs[2].t.double() - ex).abs().max())
+    assert e_orc <= 2 ** -7 * top, e_orc
+    assert e_plan <= 2 ** -7 * top and e_plan <= e_orc + 2 ** -9 * top, (e_plan, e_orc)
+
+
 @pytest.mark.parametrize("body,msg", [
     (lambda ob, ab, bb, cc: ob.store(ab @ bb + cc, acc=True), "acc=True"),
     # refused while tracing (a PlanError is a NotImplementedError)

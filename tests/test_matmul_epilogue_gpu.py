@@ -15,7 +15,8 @@ import kernel_lib as KL
 import ttl
 import ttnn
 from ttlhip import plan as P
-from test_matmul_epilogue import CASES, exact, inputs, run_oracle
+from test_matmul_epilogue import (CASES, _two_products_kernel, exact, inputs, run_oracle,
+                                  two_products_case)
 
 pytestmark = pytest.mark.gpu
 
@@ -53,3 +54,12 @@ def test_matmul_epilogue_plan_reused_with_new_inputs():
     kern = _check(case, seed=5)
     _check(case, seed=9, kern=kern)
     assert len(kern._cache) == 1
+
+
+def test_two_products_and_an_offset_product_on_gpu():
+    tensors, ex = two_products_case()
+    args = [ttnn.from_torch(t) for t in tensors]
+    _two_products_kernel(ttl)(*args)
+    torch.cuda.synchronize()
+    got = ttnn.to_torch(args[2]).double()
+    assert float((got - ex).abs().max()) <= 2 ** -7 * float(ex.abs().max())

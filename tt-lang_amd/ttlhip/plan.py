@@ -104,10 +104,15 @@ class MatmulLaunch:
     k: int
     b_block: bool = False   # B is a block-float (bfloat8_b / bfloat4_b) tensor
     loc: Optional[Tuple[str, int]] = None  # kernel source line of the store()
+    a_rows: Optional[Tuple[int, int]] = None  # A element rows (default: `rows`)
+    b_cols: Optional[Tuple[int, int]] = None  # B element cols (default: `cols`)
 
     def describe(self) -> str:
         return (f"matmul C[{self.rows[0]}:{self.rows[1]}, {self.cols[0]}:{self.cols[1]}] = "
                 f"A . B over K={self.k}")
+
+    def operand_ranges(self) -> Tuple[Tuple[int, int], Tuple[int, int]]:
+        return self.a_rows or self.rows, self.b_cols or self.cols
 
 
 @dataclass
@@ -720,10 +725,14 @@ def _hoist_matmuls(ev, e, target, rout, dt, fill, shape, groups, hoisted):
     out_r = (dt.r0[rout][:, None] + oi[None, :]).ravel()
     out_c = (dt.c0[rout][:, None] + oj[None, :]).ravel()
     order = np.repeat(np.arange(rout.size), R * C)
+    site = (ev.data.get("loc"), _tree_key(e.tree, {}), id(dt.tensor))
+    count = [0]
 
     def walk(tree):
         tag = tree[0]
         if tag in ("matmul", "bmatmul"):
+            node = count[0]  # the product's place in the expression: its temp's identity
+            count[0] += 1
             la, lb = tree[1], tree[2]
             if la[0] != "leaf" or lb[0] != "leaf":
                 raise PlanError("a tile matmul's operands must be blocks filled by ttl.copy from "
@@ -741,8 +750,7 @@ def _hoist_matmuls(ev, e, target, rout, dt, fill, shape, groups, hoisted):
             da, db = la[1].cb.dtype, lb[1].cb.dtype
             pdt = (torch.promote_types(da, db) if isinstance(da, torch.dtype)
                    and isinstance(db, torch.dtype) else da)
-            key = (ev.data.get("loc"), _tree_key(tree, {}), id(fa.tensor), id(fb.tensor),
-                   id(dt.tensor))
+            key = site + (node,)
             if key not in hoisted:
                 cb = _HoistedCB(-1 - len(hoisted), pdt, "(matmul product)")
                 hoisted[key] = (_Temp(tuple(dt.tensor.shape), pdt), cb)
@@ -1632,8 +1640,13 @@ def _plan_matmul(g: _Group, out_rc, leaf_rc, tensor_ref) -> MatmulLaunch:
     a_t, b_t = g.leaf_tensors
     (ar, ac), (br, bc) = leaf_rc[0].T, leaf_rc[1].T
     orow, ocol = out_rc[:, 0], out_rc[:, 1]
-    if not (np.array_equal(ar, orow) and np.array_equal(bc, ocol) and np.array_equal(ac, br)):
-        raise PlanError("tile matmul operands are not A(m, k) @ B(k, n) for output tile (m, n)")
+    # A's rows and B's columns may sit at a fixed offset from the output's
+    # (a product stored elsewhere, or split off a store expression)
+    da, db = (int(ar[0] - orow[0]), int(bc[0] - ocol[0])) if ar.size else (0, 0)
+    if not (np.array_equal(ar - orow, np.full_like(ar, da))
+            and np.array_equal(bc - ocol, np.full_like(bc, db)) and np.array_equal(ac, br)):
+        raise PlanError("tile matmul operands are not A(m + i, k) @ B(k, n + j) for output "
+                        "tile (m, n) with fixed offsets i, j")
     if len(a_t.shape) != 2 or len(b_t.shape) != 2 or a_t.shape[1] != b_t.shape[0]:
         raise PlanError("tile matmul operand shapes do not chain")
     K = a_t.shape[1]
@@ -1653,12 +1666,14 @@ def _plan_matmul(g: _Group, out_rc, leaf_rc, tensor_ref) -> MatmulLaunch:
         raise PlanError("block-float tensors are supported as the B operand of a tile matmul only")
     b_block = getattr(b_t, "is_block_float", False)
     if b_block:
-        if (c0, c1) != (0, b_t.shape[1] // TILE):
+        if (c0, c1) != (0, b_t.shape[1] // TILE) or db != 0:
             raise PlanError(f"a {b_t.dtype.name} B operand must be used over all of its columns")
         if a_t.dtype != torch.bfloat16 or g.out_tensor.dtype != torch.bfloat16:
             raise PlanError(f"the {b_t.dtype.name} matmul takes bfloat16 A and output tensors")
     return MatmulLaunch(tensor_ref(a_t), tensor_ref(b_t), tensor_ref(g.out_tensor),
-                        (r0 * TILE, r1 * TILE), (c0 * TILE, c1 * TILE), K, b_block)
+                        (r0 * TILE, r1 * TILE), (c0 * TILE, c1 * TILE), K, b_block,
+                        a_rows=((r0 + da) * TILE, (r1 + da) * TILE) if da else None,
+                        b_cols=((c0 + db) * TILE, (c1 + db) * TILE) if db else None)
 
 
 # ---------------------------------------------------------------------------
@@ -1729,7 +1744,9 @@ def _execute_one(l, args, stream, Kn) -> None:
             raise ValueError("matmul output aliases an input")
         r0, r1 = l.rows
         c0, c1 = l.cols
+        (ar0, ar1), (bc0, bc1) = l.operand_ranges()
         if l.b_block:
-            l.b.resolve_obj(args).dtype.matmul(a[r0:r1], b, c[r0:r1], stream=stream)
+            l.b.resolve_obj(args).dtype.matmul(a[ar0:ar1], b, c[r0:r1], stream=stream)
         else:
-            Kn.matmul(a[r0:r1], b[:, c0:c1], c[r0:r1, c0:c1], accumulate=False, stream=stream)
+            Kn.matmul(a[ar0:ar1], b[:, bc0:bc1], c[r0:r1, c0:c1], accumulate=False,
+                      stream=stream)
