@@ -150,7 +150,7 @@ class EltwiseWorkload(PlanWorkload):
                        "b_row 1x%d, U[-2,2] (BASELINE configs[1])" % (n, n, n))
 
     def kernel_name(self):
-        return "stream_kernel"
+        return "flat_kernel"
 
     def work_per_step(self):
         e = self.n * self.n * 2
@@ -709,7 +709,7 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic (seeded; resident in HBM; eltwise buffer sets rotated over > 256 MB)",
         "config": {"workload": h["config"], "kernel": "tt-lang kernel via drop-in ttl -> "
-                   "ttlh_eltwise stream_kernel", "tiles": "32x32", "cb_block": "4x4 tiles",
+                   "ttlh_eltwise flat_kernel", "tiles": "32x32", "cb_block": "4x4 tiles",
                    "grid": "(8, 8) tt-lang cores -> one grid-wide launch"},
         "roofline": {"bound": h["bound"], "achieved": round(h["achieved"], 2), "peak": h["peak"],
                      "unit": h["unit"], "frac": round(h["frac"], 4), "traffic": h["traffic"],

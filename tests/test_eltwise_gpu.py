@@ -276,3 +276,32 @@ def test_flat_path_widths(w):
               ("neg", ("leaf", "a"))):
         got = run_gpu(e, env, {}, (h, w), torch.bfloat16)
         assert_bitexact(got, O.eval_expr(e, env))
+
+
+@pytest.mark.parametrize("h", [1, 8, 24, 33])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_flat_path_two_chunks_per_lane(h, out_dtype):
+    # the flat kernel's lanes take two chunks 256 apart for programs of two or
+    # more steps (a workgroup covers 512 chunks): w = 256 gives 32 h chunks, so
+    # h = 1 and 8 leave whole halves of the one workgroup dead, h = 24 and 33
+    # end mid-workgroup; every op code goes through the shared dispatch, and a
+    # program loading four operands runs one chunk per lane
+    w = 256
+    a, b, c, d = (_u((h, w), 96 + i) for i in range(4))
+    r = _u((1, w), 100, lo=0.25, hi=2.0)
+    env = {"a": a, "b": b, "c": c, "d": d, "r": r}
+    exact = [
+        ("sub", ("leaf", "a"), ("leaf", "b")),
+        ("relu", ("sub", ("leaf", "a"), ("leaf", "r"))),
+        ("abs", ("mul", ("leaf", "a"), ("const", -3.0))),
+        ("neg", ("sub", ("const", 1.0), ("leaf", "a"))),
+        ("recip", ("mul", ("leaf", "r"), ("leaf", "c"))),
+        ("add", ("mul", ("add", ("leaf", "a"), ("leaf", "b")), ("leaf", "c")), ("leaf", "d")),
+    ]
+    for e in exact:
+        got = run_gpu(e, env, {}, (h, w), out_dtype)
+        assert_bitexact(got, O.eval_expr(e, env).to(out_dtype))
+    e = ("mul", ("exp", ("add", ("leaf", "a"), ("leaf", "r"))), ("leaf", "c"))
+    got = run_gpu(e, env, {}, (h, w), out_dtype)
+    ulp = O.bf16_ulp_diff(got.bfloat16(), O.eval_expr(e, env).bfloat16())
+    assert int(ulp.max()) <= 1

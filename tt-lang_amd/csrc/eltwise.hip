@@ -748,36 +748,75 @@ struct FlatArgs {
   int32_t out_dtype;
 };
 
+// A lane runs U chunks 256 apart: all loads first, then each step's op code
+// is dispatched once for the lane's U accumulators, which halves the per-wave
+// cost of the runtime op dispatch and of the argument loads (C2 15.9 -> 15.7
+// us).  U = 1 for a plain copy (faster with one chunk per lane) and for four
+// loaded operands (two chunks of each would not fit 64 VGPRs).
 template <int N, unsigned MASK>
+constexpr int flat_u() { return N > 1 && __builtin_popcount(MASK) < 4 ? 2 : 1; }
+
+template <int U>
+__device__ __forceinline__ void chain_op_u(uint8_t code, f32x8 (&acc)[U], const f32x8 (&v)[U]) {
+  switch (code) {
+#define TTLH_CHAIN_ALL(EXPR) _Pragma("unroll") for (int j = 0; j < U; ++j) acc[j] = EXPR; return;
+    case C_ADD: TTLH_CHAIN_ALL(acc[j] + v[j])
+    case C_SUB: TTLH_CHAIN_ALL(acc[j] - v[j])
+    case C_RSUB: TTLH_CHAIN_ALL(v[j] - acc[j])
+    case C_MUL: TTLH_CHAIN_ALL(acc[j] * v[j])
+    case C_EXP: TTLH_CHAIN_ALL(vexp_uniform(acc[j]))
+    default: TTLH_CHAIN_ALL(chain_op(code, acc[j], v[j]))
+#undef TTLH_CHAIN_ALL
+  }
+}
+
+template <int N, unsigned MASK, bool OUT_BF16>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8)))
 void flat_kernel(const FlatArgs a) {
-  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
-  const uint32_t q = min(i, a.n - 1u);  // dead lanes re-read the last chunk and store nothing
-  u32x4 v[N];
+  constexpr int U = flat_u<N, MASK>();
+  uint32_t i[U], q[U];
+#pragma unroll
+  for (int j = 0; j < U; ++j) {
+    i[j] = blockIdx.x * (256u * U) + 256u * j + threadIdx.x;
+    q[j] = min(i[j], a.n - 1u);  // dead lanes re-read the last chunk and store nothing
+  }
+  u32x4 v[U][N];
 #pragma unroll
   for (int k = 0; k < N; ++k)
-    if ((MASK >> k) & 1u) v[k] = a.ptr[k][q & a.imask[k]];
+    if ((MASK >> k) & 1u)
+#pragma unroll
+      for (int j = 0; j < U; ++j) v[j][k] = a.ptr[k][q[j] & a.imask[k]];
   asm volatile("" ::: "memory");  // every load above the arithmetic (see stream_kernel)
-  f32x8 acc = unpack_bf16x8(v[0]);
+  f32x8 acc[U];
+#pragma unroll
+  for (int j = 0; j < U; ++j) acc[j] = unpack_bf16x8(v[j][0]);
 #pragma unroll
   for (int k = 1; k < N; ++k) {
-    const f32x8 x = ((MASK >> k) & 1u) ? unpack_bf16x8(v[k]) : splat(a.imm[k]);
-    acc = chain_op(a.code[k], acc, x);
-    const bool last_into_bf16 = k == N - 1 && a.out_dtype == TTLH_BF16;
-    if (a.rnd[k] == TTLH_BF16 && !last_into_bf16) acc = round_bf16x8(acc);
+    f32x8 x[U];
+#pragma unroll
+    for (int j = 0; j < U; ++j)
+      x[j] = ((MASK >> k) & 1u) ? unpack_bf16x8(v[j][k]) : splat(a.imm[k]);
+    chain_op_u<U>(a.code[k], acc, x);
+    const bool last_into_bf16 = k == N - 1 && OUT_BF16;
+    if (a.rnd[k] == TTLH_BF16 && !last_into_bf16)
+#pragma unroll
+      for (int j = 0; j < U; ++j) acc[j] = round_bf16x8(acc[j]);
   }
-  if (i >= a.n) return;
-  if (a.out_dtype == TTLH_BF16) {
-    u32x4 r;
-    r.x = cvt_pk_bf16(acc[0], acc[1]);
-    r.y = cvt_pk_bf16(acc[2], acc[3]);
-    r.z = cvt_pk_bf16(acc[4], acc[5]);
-    r.w = cvt_pk_bf16(acc[6], acc[7]);
-    __builtin_nontemporal_store(r, static_cast<u32x4*>(a.out) + i);
-  } else {
-    f32x4* p = static_cast<f32x4*>(a.out) + 2u * i;
-    __builtin_nontemporal_store(f32x4{acc[0], acc[1], acc[2], acc[3]}, p);
-    __builtin_nontemporal_store(f32x4{acc[4], acc[5], acc[6], acc[7]}, p + 1);
+#pragma unroll
+  for (int j = 0; j < U; ++j) {
+    if (i[j] >= a.n) break;
+    if constexpr (OUT_BF16) {
+      u32x4 r;
+      r.x = cvt_pk_bf16(acc[j][0], acc[j][1]);
+      r.y = cvt_pk_bf16(acc[j][2], acc[j][3]);
+      r.z = cvt_pk_bf16(acc[j][4], acc[j][5]);
+      r.w = cvt_pk_bf16(acc[j][6], acc[j][7]);
+      __builtin_nontemporal_store(r, static_cast<u32x4*>(a.out) + i[j]);
+    } else {
+      f32x4* p = static_cast<f32x4*>(a.out) + 2u * i[j];
+      __builtin_nontemporal_store(f32x4{acc[j][0], acc[j][1], acc[j][2], acc[j][3]}, p);
+      __builtin_nontemporal_store(f32x4{acc[j][4], acc[j][5], acc[j][6], acc[j][7]}, p + 1);
+    }
   }
 }
 
@@ -814,11 +853,15 @@ bool try_flat(const ChainArgs& c, int n, hipStream_t s, int* status) {
   a.out = static_cast<char*>(c.out) + c.y0 * c.out_ld * esz;
   a.n = c.total;
   a.out_dtype = c.out_dtype;
-  const dim3 grid((c.total + 255u) / 256u), block(256);
-#define TTLH_FLAT_CASE(NN, MM)                                                     \
-  case (NN << 4) | MM:                                                              \
-    hipLaunchKernelGGL((flat_kernel<NN, MM>), grid, block, 0, s, a);               \
-    break;
+#define TTLH_FLAT_CASE(NN, MM)                                                         \
+  case (NN << 4) | MM: {                                                                \
+    const dim3 grid((c.total + 256u * flat_u<NN, MM>() - 1u) / (256u * flat_u<NN, MM>())); \
+    if (a.out_dtype == TTLH_BF16)                                                       \
+      hipLaunchKernelGGL((flat_kernel<NN, MM, true>), grid, dim3(256), 0, s, a);        \
+    else                                                                                \
+      hipLaunchKernelGGL((flat_kernel<NN, MM, false>), grid, dim3(256), 0, s, a);       \
+    break;                                                                              \
+  }
   switch ((n << 4) | mask) {
     TTLH_FLAT_CASE(1, 1)
     TTLH_FLAT_CASE(2, 1) TTLH_FLAT_CASE(2, 3)
