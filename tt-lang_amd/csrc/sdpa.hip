@@ -1084,9 +1084,17 @@ struct SdpaW8 {
     __builtin_amdgcn_sched_barrier(0);
     // the previous step's loads landed (this step's may stay in flight), this
     // step's reads are done except the prefetch: publish / release
+    // The count covers exactly the loads this step issued: a QPF step whose
+    // block has no next block stages no Q (stage_q returns), and allowing 8
+    // more would leave the previous step's K / V loads unwaited, which the
+    // next step's fragment prefetch reads.
     constexpr int npf = (NEXT_S ? 2 : 0) + (NEXT_O ? 4 : 0);
-    constexpr int nvm = (DO_S ? 2 : 0) + (QPF ? 8 : 0);
-    __builtin_amdgcn_s_waitcnt((nvm & 15) | ((nvm >> 4) << 14) | 0x0070 | (npf << 8));
+    constexpr int nvm = DO_S ? 2 : 0;
+    constexpr int nvq = nvm + (QPF ? 8 : 0);
+    if (QPF && nq_qb >= 0)
+      __builtin_amdgcn_s_waitcnt((nvq & 15) | ((nvq >> 4) << 14) | 0x0070 | (npf << 8));
+    else
+      __builtin_amdgcn_s_waitcnt((nvm & 15) | ((nvm >> 4) << 14) | 0x0070 | (npf << 8));
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
