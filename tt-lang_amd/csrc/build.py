@@ -43,9 +43,18 @@ COMMON_FLAGS = [
 ]
 
 
+# Per-source flags.  eltwise.hip: kernarg preloading of the first four
+# arguments, so the flat kernel's operand bases and chunk count arrive in
+# SGPRs at wave start (its other kernels take one struct argument, which is
+# never preloaded).
+EXTRA_FLAGS = {
+    "eltwise.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=4"],
+}
+
+
 def _compile(src: str) -> Path:
     obj = OBJ_DIR / (Path(src).stem + ".o")
-    cmd = [hipcc(), *COMMON_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+    cmd = [hipcc(), *COMMON_FLAGS, *EXTRA_FLAGS.get(src, []), "-c", str(CSRC / src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")

@@ -733,19 +733,22 @@ void stream_kernel(const StreamArgs a) {
 // pitch read at the same element (chunk i of the region is chunk i of the
 // operand) or one row of 8 * cpr elements re-read by every output row (a row
 // vector, cpr a power of two).  Chunk i of the region is then base + 8 i in
-// every array, so a lane's address is one 64-bit add off a 1-D index, the
-// kernel argument block stays small and there is no row / column split at
-// all: on a 25 MB stream this saves about 0.35 us per launch over the 2-D
-// stream kernel, most of the gap to a bare copy kernel.
-struct FlatArgs {
-  const u32x4* ptr[4];  // operand base of chunk 0
-  void* out;            // output base of chunk 0
-  uint32_t imask[4];    // chunk index mask: ~0 (same chunk) or cpr - 1 (row vector)
+// every array, so a lane's address is one 64-bit add off a 1-D index and
+// there is no row / column split at all: on a 25 MB stream this saves about
+// 0.35 us per launch over the 2-D stream kernel.
+//
+// The arguments the first loads need come first and as scalars: eltwise.hip
+// is compiled with kernarg preloading of four arguments, so the first three
+// operand bases and the chunk count are in SGPRs when the wave starts and
+// the address arithmetic does not wait for a scalar load of the argument
+// block (C1 add 4.58 -> 4.41 us, C2 15.66 -> 15.59 us; preloading all
+// thirteen scalar dwords measured 4.39 / 15.68: each preloaded SGPR costs
+// every wave's launch).  The rest, including the op codes needed only once
+// the data is in, is fetched by s_load while the first loads are in flight.
+struct FlatOps {
   uint8_t code[4];
   uint8_t rnd[4];
   float imm[4];
-  uint32_t n;           // chunks in the region
-  int32_t out_dtype;
 };
 
 // A lane runs U chunks 256 apart: all loads first, then each step's op code
@@ -770,22 +773,31 @@ __device__ __forceinline__ void chain_op_u(uint8_t code, f32x8 (&acc)[U], const 
   }
 }
 
+// p0..p3: chunk 0 of the program's loaded operands in step order (the
+// operand of step k is p[popcount(MASK & ((1 << k) - 1))], unused slots
+// null); n: chunks in the region; bit c of bcast: p[c] is a row vector, read
+// at chunk i & rowmask (rowmask = chunks per row - 1) instead of chunk i.
 template <int N, unsigned MASK, bool OUT_BF16>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8)))
-void flat_kernel(const FlatArgs a) {
+void flat_kernel(const u32x4* p0, const u32x4* p1, const u32x4* p2, uint32_t n, uint32_t bcast,
+                 uint32_t rowmask, const u32x4* p3, void* out, const FlatOps a) {
   constexpr int U = flat_u<N, MASK>();
+  const u32x4* const ptr[4] = {p0, p1, p2, p3};
   uint32_t i[U], q[U];
 #pragma unroll
   for (int j = 0; j < U; ++j) {
     i[j] = blockIdx.x * (256u * U) + 256u * j + threadIdx.x;
-    q[j] = min(i[j], a.n - 1u);  // dead lanes re-read the last chunk and store nothing
+    q[j] = min(i[j], n - 1u);  // dead lanes re-read the last chunk and store nothing
   }
   u32x4 v[U][N];
 #pragma unroll
   for (int k = 0; k < N; ++k)
-    if ((MASK >> k) & 1u)
+    if ((MASK >> k) & 1u) {
+      const int c = __builtin_popcount(MASK & ((1u << k) - 1u));
+      const uint32_t im = ((bcast >> c) & 1u) ? rowmask : ~0u;
 #pragma unroll
-      for (int j = 0; j < U; ++j) v[j][k] = a.ptr[k][q[j] & a.imask[k]];
+      for (int j = 0; j < U; ++j) v[j][k] = ptr[c][q[j] & im];
+    }
   asm volatile("" ::: "memory");  // every load above the arithmetic (see stream_kernel)
   f32x8 acc[U];
 #pragma unroll
@@ -804,16 +816,16 @@ void flat_kernel(const FlatArgs a) {
   }
 #pragma unroll
   for (int j = 0; j < U; ++j) {
-    if (i[j] >= a.n) break;
+    if (i[j] >= n) break;
     if constexpr (OUT_BF16) {
       u32x4 r;
       r.x = cvt_pk_bf16(acc[j][0], acc[j][1]);
       r.y = cvt_pk_bf16(acc[j][2], acc[j][3]);
       r.z = cvt_pk_bf16(acc[j][4], acc[j][5]);
       r.w = cvt_pk_bf16(acc[j][6], acc[j][7]);
-      __builtin_nontemporal_store(r, static_cast<u32x4*>(a.out) + i[j]);
+      __builtin_nontemporal_store(r, static_cast<u32x4*>(out) + i[j]);
     } else {
-      f32x4* p = static_cast<f32x4*>(a.out) + 2u * i[j];
+      f32x4* p = static_cast<f32x4*>(out) + 2u * i[j];
       __builtin_nontemporal_store(f32x4{acc[j][0], acc[j][1], acc[j][2], acc[j][3]}, p);
       __builtin_nontemporal_store(f32x4{acc[j][4], acc[j][5], acc[j][6], acc[j][7]}, p + 1);
     }
@@ -825,21 +837,22 @@ void flat_kernel(const FlatArgs a) {
 bool try_flat(const ChainArgs& c, int n, hipStream_t s, int* status) {
   if (n > 4 || c.x0 != 0 || int64_t(c.cpr) * 8 != c.out_ld) return false;
   const bool pow2 = (c.cpr & (c.cpr - 1u)) == 0;
-  FlatArgs a{};
-  unsigned mask = 0;
+  const u32x4* ptr[4] = {};
+  FlatOps a{};
+  unsigned mask = 0, bcast = 0;
   for (int k = 0; k < n; ++k) {
     const bool reads = k == 0 || c.imm_src[k] == 0;
     if (reads) {
       const EltOperand& o = c.ops[k];
       if (o.dtype != TTLH_BF16 || !o.vec || o.cs != 1 || o.cmask != -1) return false;
       const uint16_t* p = static_cast<const uint16_t*>(o.ptr);
+      const int ci = __builtin_popcount(mask);
       if (o.rmask == -1 && o.rs == c.out_ld) {  // same element as the output
-        a.ptr[k] = reinterpret_cast<const u32x4*>(p + (c.y0 + o.roff) * o.rs + o.coff);
-        a.imask[k] = ~0u;
+        ptr[ci] = reinterpret_cast<const u32x4*>(p + (c.y0 + o.roff) * o.rs + o.coff);
       } else if ((o.rmask == 0 || o.rs == 0) && pow2) {  // one row, re-read by every row
         const int64_t row = o.rs == 0 ? 0 : o.roff;
-        a.ptr[k] = reinterpret_cast<const u32x4*>(p + row * o.rs + o.coff);
-        a.imask[k] = c.cpr - 1u;
+        ptr[ci] = reinterpret_cast<const u32x4*>(p + row * o.rs + o.coff);
+        bcast |= 1u << ci;
       } else {
         return false;
       }
@@ -850,16 +863,17 @@ bool try_flat(const ChainArgs& c, int n, hipStream_t s, int* status) {
     a.imm[k] = c.imm[k];
   }
   const int esz = c.out_dtype == TTLH_BF16 ? 2 : 4;
-  a.out = static_cast<char*>(c.out) + c.y0 * c.out_ld * esz;
-  a.n = c.total;
-  a.out_dtype = c.out_dtype;
+  void* const out = static_cast<char*>(c.out) + c.y0 * c.out_ld * esz;
+  const uint32_t rowmask = c.cpr - 1u;
 #define TTLH_FLAT_CASE(NN, MM)                                                         \
   case (NN << 4) | MM: {                                                                \
     const dim3 grid((c.total + 256u * flat_u<NN, MM>() - 1u) / (256u * flat_u<NN, MM>())); \
-    if (a.out_dtype == TTLH_BF16)                                                       \
-      hipLaunchKernelGGL((flat_kernel<NN, MM, true>), grid, dim3(256), 0, s, a);        \
+    if (c.out_dtype == TTLH_BF16)                                                       \
+      hipLaunchKernelGGL((flat_kernel<NN, MM, true>), grid, dim3(256), 0, s, ptr[0], ptr[1], \
+                         ptr[2], c.total, bcast, rowmask, ptr[3], out, a);               \
     else                                                                                \
-      hipLaunchKernelGGL((flat_kernel<NN, MM, false>), grid, dim3(256), 0, s, a);       \
+      hipLaunchKernelGGL((flat_kernel<NN, MM, false>), grid, dim3(256), 0, s, ptr[0], ptr[1], \
+                         ptr[2], c.total, bcast, rowmask, ptr[3], out, a);               \
     break;                                                                              \
   }
   switch ((n << 4) | mask) {
