@@ -44,9 +44,9 @@ COMMON_FLAGS = [
 
 
 # Per-source flags.  eltwise.hip: kernarg preloading of the first four
-# arguments, so the flat kernel's operand bases and chunk count arrive in
-# SGPRs at wave start (its other kernels take one struct argument, which is
-# never preloaded).
+# arguments, so the flat kernel's operand bases and chunk count and the bf16
+# row reduction's row base, stride and width arrive in SGPRs at wave start
+# (the other kernels take one struct argument, which is never preloaded).
 EXTRA_FLAGS = {
     "eltwise.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=4"],
 }

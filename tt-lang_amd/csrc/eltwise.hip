@@ -1173,8 +1173,11 @@ __global__ __launch_bounds__(256) void reduce_rows_wide_kernel(const RedArgs a) 
 // reduction kind a template parameter and nothing interpreted per element:
 // bf16 values are exact in fp32 and the operand's bf16 rounding is the
 // identity on them.  NT: streaming loads, chosen by the host when the
-// operand is read exactly once (no broadcast).  4096 x 4096 row sum: 6.5 us
-// against 8.4 us through the wide kernel.
+// operand is read exactly once (no row stride 0).  4096 x 4096 row sum: 6.5
+// us against 8.4 us through the wide kernel.  Element x of row r is at
+// base[r rs + x]: the operand has no row or column mask (the host sends
+// masked operands to the wide kernel), and base / rs / w lead the argument
+// list as scalars, preloaded into SGPRs like the flat kernel's.
 template <int KIND>
 __device__ __forceinline__ float red_combine_k(float a, float b) {
   if constexpr (KIND == TTLH_REDUCE_MAX) return (a != a || b != b) ? __builtin_nanf("") : fmaxf(a, b);
@@ -1188,30 +1191,30 @@ __device__ __forceinline__ u32x4 ld16(uintptr_t u) {
 }
 
 template <int KIND, bool TO_WS, bool NT>
-__global__ __launch_bounds__(256) void reduce_rows_bf16_kernel(const RedArgs a) {
+__global__ __launch_bounds__(256) void reduce_rows_bf16_kernel(const uint16_t* base, int64_t rs,
+                                                               int64_t w, const RedArgs a) {
   __shared__ float part[4];
   const int64_t row = blockIdx.x;
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const EltOperand& op = a.e.ops[0];
-  const int64_t y = a.e.y0 + row;
+  const uintptr_t rowp = reinterpret_cast<uintptr_t>(base + row * rs);
   constexpr int64_t S = 256 * 8;
   const int64_t xf = int64_t(t) * 8;
   u32x4 c[2];  // chunk slots past the row's end are neither fetched nor read
 #pragma unroll
   for (int i = 0; i < 2; ++i)
-    if (xf + i * S < a.w) c[i] = ld16<NT>(operand_addr<false>(op, y, a.e.x0 + xf + i * S));
+    if (xf + i * S < w) c[i] = ld16<NT>(rowp + 2 * (xf + i * S));
   const float s = red_scale(a);  // after the first row loads are in flight
   float r = red_identity(KIND);
-  for (int64_t xb = xf; xb < a.w; xb += 2 * S) {
+  for (int64_t xb = xf; xb < w; xb += 2 * S) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int64_t xo = xb + i * S;
-      if (xo < a.w) {
+      if (xo < w) {
         const f32x8 v = unpack_bf16x8(c[i]);
 #pragma unroll
         for (int k = 0; k < 8; ++k) r = red_combine_k<KIND>(r, v[k] * s);
       }
-      if (xo + 2 * S < a.w) c[i] = ld16<NT>(operand_addr<false>(op, y, a.e.x0 + xo + 2 * S));
+      if (xo + 2 * S < w) c[i] = ld16<NT>(rowp + 2 * (xo + 2 * S));
     }
   }
 #pragma unroll
@@ -1698,11 +1701,17 @@ int reduce_impl(const char* who, const ttlh_instr* prog, const ttlh_operand* in,
     // the specialised kernel: a plain bf16 operand; streaming loads when no
     // element of it is read twice
     const EltOperand& o0 = a.e.ops[0];
-    const bool plain_bf16 = wide && mode == 1 && o0.dtype == TTLH_BF16;
-    const bool nt = o0.rmask == -1 && o0.cmask == -1 && (o0.rs != 0 || h == 1);
+    const bool plain_bf16 = wide && mode == 1 && o0.dtype == TTLH_BF16 && o0.rmask == -1 &&
+                            o0.cmask == -1 && o0.cs == 1;
+    const bool nt = o0.rs != 0 || h == 1;
+    // element x of region row r: base[r rs + x] (no masks on this path)
+    const uint16_t* const rbase = static_cast<const uint16_t*>(o0.ptr) +
+                                  (a.e.y0 + o0.roff) * o0.rs + a.e.x0 + o0.coff;
 #define TTLH_ROWS_BF16(K, WS)                                                                \
-  if (nt) hipLaunchKernelGGL((reduce_rows_bf16_kernel<K, WS, true>), grid, block, 0, s, a);  \
-  else hipLaunchKernelGGL((reduce_rows_bf16_kernel<K, WS, false>), grid, block, 0, s, a);
+  if (nt) hipLaunchKernelGGL((reduce_rows_bf16_kernel<K, WS, true>), grid, block, 0, s, rbase, \
+                             int64_t(o0.rs), int64_t(w), a);                                 \
+  else hipLaunchKernelGGL((reduce_rows_bf16_kernel<K, WS, false>), grid, block, 0, s, rbase,  \
+                          int64_t(o0.rs), int64_t(w), a);
 #define TTLH_ROWS(WS)                                                                        \
   if (plain_bf16 && kind == TTLH_REDUCE_SUM) {                                               \
     TTLH_ROWS_BF16(TTLH_REDUCE_SUM, WS)                                                      \
