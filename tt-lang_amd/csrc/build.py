@@ -47,8 +47,12 @@ COMMON_FLAGS = [
 # arguments, so the flat kernel's operand bases and chunk count and the bf16
 # row reduction's row base, stride and width arrive in SGPRs at wave start
 # (the other kernels take one struct argument, which is never preloaded).
+# layout.hip: all five arguments of the tilize / untilize kernel (4096^2 bf16
+# tilize 10.6 -> 10.2 us).  Not bfp8.hip: its unpack kernel (44k waves at C4)
+# measured 0.5% slower with its arguments preloaded.
 EXTRA_FLAGS = {
     "eltwise.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=4"],
+    "layout.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=5"],
 }
 
 

@@ -21,6 +21,8 @@
 namespace ttlh {
 namespace {
 
+// The kernel takes these as scalar arguments (layout.hip is built with
+// kernarg preloading, so they are in SGPRs when a wave starts).
 struct LayoutArgs {
   const char* src;
   char* dst;
@@ -44,7 +46,9 @@ __device__ __forceinline__ int64_t rowmajor_offset(const LayoutArgs& a, uint32_t
 }
 
 template <int E, bool TILIZE>
-__global__ __launch_bounds__(256) void layout_kernel(const LayoutArgs a) {
+__global__ __launch_bounds__(256) void layout_kernel(const char* src, char* dst, int64_t ld_bytes,
+                                                     uint32_t tiles_per_row, uint32_t chunks) {
+  const LayoutArgs a{src, dst, ld_bytes, tiles_per_row, chunks};
   const uint32_t k = blockIdx.x * 256u + threadIdx.x;
   if (k >= a.chunks) return;
   const int64_t rm = rowmajor_offset<E>(a, k);
@@ -79,11 +83,15 @@ int run_layout(const char* who, bool tilize, const void* src, void* dst, int64_t
   const dim3 grid(static_cast<uint32_t>((chunks + 255) / 256)), block(256);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (elem_bytes == 2) {
-    if (tilize) hipLaunchKernelGGL((layout_kernel<2, true>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((layout_kernel<2, false>), grid, block, 0, s, a);
+    if (tilize) hipLaunchKernelGGL((layout_kernel<2, true>), grid, block, 0, s, a.src, a.dst, a.ld_bytes,
+                                  a.tiles_per_row, a.chunks);
+    else hipLaunchKernelGGL((layout_kernel<2, false>), grid, block, 0, s, a.src, a.dst, a.ld_bytes,
+                                  a.tiles_per_row, a.chunks);
   } else {
-    if (tilize) hipLaunchKernelGGL((layout_kernel<4, true>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((layout_kernel<4, false>), grid, block, 0, s, a);
+    if (tilize) hipLaunchKernelGGL((layout_kernel<4, true>), grid, block, 0, s, a.src, a.dst, a.ld_bytes,
+                                  a.tiles_per_row, a.chunks);
+    else hipLaunchKernelGGL((layout_kernel<4, false>), grid, block, 0, s, a.src, a.dst, a.ld_bytes,
+                                  a.tiles_per_row, a.chunks);
   }
   return check_launch("layout_kernel");
 }
