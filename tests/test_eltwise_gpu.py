@@ -297,6 +297,10 @@ def test_flat_path_two_chunks_per_lane(h, out_dtype):
         ("neg", ("sub", ("const", 1.0), ("leaf", "a"))),
         ("recip", ("mul", ("leaf", "r"), ("leaf", "c"))),
         ("add", ("mul", ("add", ("leaf", "a"), ("leaf", "b")), ("leaf", "c")), ("leaf", "d")),
+        # the row vector as the third and as the fourth loaded operand (the
+        # kernel numbers loaded operands in step order)
+        ("mul", ("add", ("leaf", "a"), ("leaf", "b")), ("leaf", "r")),
+        ("add", ("mul", ("add", ("leaf", "a"), ("leaf", "b")), ("leaf", "c")), ("leaf", "r")),
     ]
     for e in exact:
         got = run_gpu(e, env, {}, (h, w), out_dtype)
