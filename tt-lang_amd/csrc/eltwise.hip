@@ -1705,8 +1705,10 @@ int reduce_impl(const char* who, const ttlh_instr* prog, const ttlh_operand* in,
                             o0.cmask == -1 && o0.cs == 1;
     const bool nt = o0.rs != 0 || h == 1;
     // element x of region row r: base[r rs + x] (no masks on this path)
-    const uint16_t* const rbase = static_cast<const uint16_t*>(o0.ptr) +
-                                  (a.e.y0 + o0.roff) * o0.rs + a.e.x0 + o0.coff;
+    const uint16_t* const rbase =
+        plain_bf16 ? static_cast<const uint16_t*>(o0.ptr) + (a.e.y0 + o0.roff) * o0.rs +
+                         a.e.x0 + o0.coff
+                   : nullptr;
 #define TTLH_ROWS_BF16(K, WS)                                                                \
   if (nt) hipLaunchKernelGGL((reduce_rows_bf16_kernel<K, WS, true>), grid, block, 0, s, rbase, \
                              int64_t(o0.rs), int64_t(w), a);                                 \
