@@ -10,8 +10,9 @@ configs are measured in the same run and listed under "workloads" with their
 own roofline figures:
   C1 eltwise add 2048^2       tt-lang kernel (eltwise_add style)   HBM GB/s
   C3 bf16 matmul 4096^3       tt-lang kernel (multicore style)     TFLOP/s
-  C4 bf16 x bfp8 4096x4096x11008   ttlh_matmul_bfp8w_ws (two-pass)  TFLOP/s
-  C5 SDPA [4,32,4096,128]     ttlh_sdpa_fwd                        TFLOP/s
+  C4 bf16 x bfp8 4096x4096x11008   tt-lang kernel (multicore style, ttnn.bfloat8_b B)
+                              -> ttlh_matmul_bfp8w_ws (two-pass)   TFLOP/s
+  C5 SDPA [4,32,4096,128]     tt-lang attention program -> ttlh_sdpa_fwd   TFLOP/s
   row sums 4096^2 (spec reduce_sum)  tt-lang kernel (reduce_rows)  HBM GB/s
   tilize 4096^2 bf16 (TILE_LAYOUT)   ttlh_tilize                  HBM GB/s
 
@@ -380,12 +381,14 @@ class MatmulWorkload(PlanWorkload):
                           f"{dt * full / steps:.0f} s"}
 
 
-class Bfp8MatmulWorkload(Workload):
-    """C4: C = A (bf16 [M,K], N(0,1)) . dequant(Bq), Bq the bfloat8_b tiles of
-    an N(0, 0.02) fp32 [K,N] matrix (C ABI).  At M = 4096 the step is the
-    two-pass entry point: one dequantisation pass into a bf16 workspace
-    (allocated once, outside the timed region) and the bf16 GEMM; both
-    kernels are inside the timed step."""
+class Bfp8MatmulWorkload(PlanWorkload):
+    """C4 through the drop-in: the multicore tt-lang matmul kernel (13x10
+    grid, store(acc=True) over K) with B a ttnn.bfloat8_b tensor, C = A (bf16
+    [M,K], N(0,1)) . dequant(Bq), Bq the bfloat8_b tiles of an N(0, 0.02)
+    fp32 [K,N] matrix.  The plan is one bf16 x bfloat8_b GEMM launch; at M =
+    4096 that is the two-pass entry point (one dequantisation pass into a
+    bf16 workspace from torch's caching allocator, then the bf16 GEMM), both
+    kernels inside the timed step."""
 
     bound = "mfma"
     unit = "TFLOP/s"
@@ -396,44 +399,38 @@ class Bfp8MatmulWorkload(Workload):
                        "accumulate, bf16 out (BASELINE configs[3])")
 
     def kernel_name(self):
-        return "bfp8_unpack_kernel + mm_dma_kernel" if self.two_pass else "mm256_kernel<bfp8>"
+        from ttlhip import kernels as K
+        return ("bfp8_unpack_kernel + mm_dma_kernel" if self.M >= K.BFP8_TWO_PASS_MIN_M
+                else "mm256_kernel<bfp8>")
 
     def work_per_step(self):
         return 2.0 * self.M * self.N * self.K
 
-    def setup(self):
+    def make_sets(self):
+        import kernel_lib as KL
+        import ttl
+        import ttnn
         from oracle.tile_ops import seeded
-        from ttlhip import kernels as K
-        self.a = seeded((self.M, self.K), "normal", self.seed).cuda()
-        w = seeded((self.K, self.N), "normal", self.seed + 1, torch.float32, std=0.02)
-        self.bq = K.bfp8_pack_host(w).cuda()
-        self.c = torch.empty((self.M, self.N), dtype=torch.bfloat16, device="cuda")
-        self._args = (self.a.data_ptr(), self.K, self.bq.data_ptr(), self.c.data_ptr(), self.N,
-                      self.M, self.N, self.K)
-        if self.two_pass:
-            from ttlhip import _lib as L
-            nb = int(L.load().ttlh_matmul_bfp8w_workspace_bytes(self.M, self.N, self.K))
-            self.ws = torch.empty(nb, dtype=torch.uint8, device="cuda")
-            self._args += (self.ws.data_ptr(), nb)
+        self.kernel = KL.make_matmul_multi(ttl, ttnn)
+        self.a = seeded((self.M, self.K), "normal", self.seed)
+        self.w = seeded((self.K, self.N), "normal", self.seed + 1, torch.float32, std=0.02)
+        wq = ttnn.from_torch(self.w, dtype=ttnn.bfloat8_b)
+        c = ttnn.empty((self.M, self.N), dtype=torch.bfloat16)
+        return [[ttnn.from_torch(self.a), wq, c]]
 
-    @property
-    def two_pass(self):
-        from ttlhip import kernels as K
-        return self.M >= K.BFP8_TWO_PASS_MIN_M
-
-    def launch(self, i):
-        from ttlhip import _lib as L
-        fn = "ttlh_matmul_bfp8w_ws" if self.two_pass else "ttlh_matmul_bfp8w"
-        L.call(fn, *self._args, L.stream_ptr())
+    def setup(self):
+        super().setup()
+        (l,) = self.plan.launches
+        assert l.b_block, self.plan.describe()
 
     def check(self):
         from oracle import bfp8 as OB
         self.launch(0)
         torch.cuda.synchronize()
         rows = torch.arange(0, self.M, max(1, self.M // 32))
-        wd = OB.unpack_c(self.bq.cpu(), self.K, self.N).double()
-        exact = self.a.cpu()[rows].double() @ wd
-        got = self.c.cpu()[rows].double()
+        wd = OB.unpack_c(OB.pack_c(self.w), self.K, self.N).double()
+        exact = self.a[rows].double() @ wd
+        got = self.sets[0][2].to_torch()[rows].double()
         return {"max_abs_err_rel": float((got - exact).abs().max() / exact.abs().max()),
                 "rows_checked": int(rows.numel()),
                 "oracle": "float64 product of the C oracle's dequantisation"}
@@ -441,8 +438,8 @@ class Bfp8MatmulWorkload(Workload):
     def cpu_baseline(self):
         from oracle import bfp8 as OB
         rows = 256
-        bq = self.bq.cpu()
-        a = self.a[:rows].cpu()
+        bq = OB.pack_c(self.w)
+        a = self.a[:rows]
 
         def work():
             w = OB.unpack_c(bq, self.K, self.N)
