@@ -232,3 +232,26 @@ def test_block_matmul_kernel_gpu(bm, bk, bn, R, C):
     exact = (a.double() @ b.double()).to(torch.bfloat16)
     assert int(O.bf16_ulp_diff(got, orc).abs().max()) <= 1
     assert int(O.bf16_ulp_diff(got, exact).abs().max()) <= 1
+
+
+@pytest.mark.parametrize("K", [96, 1024])
+def test_dma_gemm_with_slow_operand_loads(K):
+    # A and B in pinned host memory: every operand load of the 256x256 DMA
+    # GEMM crosses PCIe and takes far longer than a stage, so a wait that let
+    # a stage be read before its loads landed would show as wrong products
+    # (K = 96: the three-stage tail path only; K = 1024: the steady loop)
+    from ttlhip import _lib as L
+    M = N = 4096
+    g = torch.Generator().manual_seed(K)
+    a = (torch.randn(M, K, generator=g) / K ** 0.5).bfloat16()
+    b = (torch.randn(K, N, generator=g) / K ** 0.5).bfloat16()
+    ah, bh = a.pin_memory(), b.pin_memory()
+    c = torch.zeros(M, N, dtype=torch.bfloat16, device="cuda")
+    L.call("ttlh_matmul", ah.data_ptr(), L.dtype_code(a.dtype), K, bh.data_ptr(),
+           L.dtype_code(b.dtype), N, c.data_ptr(), L.dtype_code(c.dtype), N, M, N, K, 0,
+           L.stream_ptr())
+    torch.cuda.synchronize()
+    rows = torch.arange(0, M, 61)
+    exact = a[rows].double() @ b.double()
+    err = float((c.cpu()[rows].double() - exact).abs().max())
+    assert err <= 1e-2 * float(exact.abs().max()), err
