@@ -160,3 +160,21 @@ def test_ttl_kernel_with_bfloat8_b_weights(M, K, N):
     assert l.b_block
     exact = a.double() @ OB.unpack_c(OB.pack_c(w), K, N).double()
     _bound_check(ttnn.to_torch(c), exact, K)
+
+
+def test_fused_bfp8_gemm_with_slow_loads():
+    # the fused path (weights decoded between MFMAs) with A and the packed
+    # weights in pinned host memory: every load far slower than a k step
+    from ttlhip import _lib as L
+    from ttlhip import kernels as K
+    M, N, Kd = 256, 1024, 512
+    g = torch.Generator().manual_seed(8)
+    a = torch.randn(M, Kd, generator=g).bfloat16()
+    w = torch.randn(Kd, N, generator=g) * 0.02
+    bq = K.bfp8_pack_host(w)
+    ah, bqh = a.pin_memory(), bq.pin_memory()
+    c = torch.zeros(M, N, dtype=torch.bfloat16, device="cuda")
+    L.call("ttlh_matmul_bfp8w", ah.data_ptr(), Kd, bqh.data_ptr(), c.data_ptr(), N, M, N, Kd,
+           L.stream_ptr())
+    torch.cuda.synchronize()
+    _bound_check(c.cpu(), a.double() @ OB.unpack_c(bq, Kd, N).double(), Kd)

@@ -229,3 +229,20 @@ def test_sdpa_ragged_seq(S, D, causal):
 def test_sdpa_ragged_negative_and_zero_scale(scale):
     q, k, v = _qkv(1, 2, 96, 128, 77)
     _check(_run(q, k, v, scale), O.sdpa_ref(q, k, v, scale))
+
+
+@pytest.mark.parametrize("S,D,causal", [(384, 128, False), (256, 64, False), (96, 128, False),
+                                        (512, 128, True), (256, 64, True)])
+def test_sdpa_other_kernels_with_slow_loads(S, D, causal):
+    # the kernels other than the eight-wave one (ping-pong, 4-wave, ragged,
+    # causal) with Q, K and V in pinned host memory: loads far slower than
+    # any step of their pipelines
+    from ttlhip import _lib as L
+    g = torch.Generator().manual_seed(S + D)
+    q, k, v = (torch.randn(1, 2, S, D, generator=g).bfloat16() for _ in range(3))
+    qh, kh, vh = q.pin_memory(), k.pin_memory(), v.pin_memory()
+    out = torch.zeros(1, 2, S, D, dtype=torch.bfloat16, device="cuda")
+    L.call("ttlh_sdpa_fwd", qh.data_ptr(), kh.data_ptr(), vh.data_ptr(), out.data_ptr(), 1, 2, S,
+           D, 0.1, int(causal), L.stream_ptr())
+    torch.cuda.synchronize()
+    _check(out.cpu(), O.sdpa_ref(q, k, v, 0.1, causal))
