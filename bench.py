@@ -22,9 +22,12 @@ are in HBM before the timed region; elementwise configs rotate buffer sets
 totalling > 256 MB so the Infinity Cache cannot serve them.  The K timed
 steps are captured once into a HIP graph and replayed, so host overhead does
 not pad short kernels; HIP events on the launch stream bracket the replay.
-MFMA workloads time at least MFMA_MIN_MS of work (their step count is raised
-from a short probe): the engine clock ramps up after the idle gap before a
-replay, and 20 steps of a 0.1 ms GEMM would mostly measure that ramp.
+Every workload times exactly K steps, at steady state: the K-step graph is
+first replayed back to back, without a host synchronisation, over at least
+PREROLL_MS (MFMA workloads MFMA_PREROLL_MS) and PREROLL_MIN_STEPS steps, so
+the engine clock has ramped and no idle gap or graph start-up precedes a
+timed step; then SAMPLES replays are timed, each between its own HIP events,
+and the median per-step time is reported.
 """
 
 from __future__ import annotations
@@ -44,7 +47,10 @@ for _p in (os.path.join(ROOT, "tests"), os.path.join(ROOT, "tt-lang_amd"), ROOT)
 import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
-MFMA_MIN_MS = 30.0             # timed work per MFMA workload (ms), at least
+PREROLL_MS = 10.0              # steady work queued ahead of the timed steps (ms), at least
+PREROLL_MIN_STEPS = 50         # ... and at least this many steps
+MFMA_PREROLL_MS = 30.0         # MFMA workloads: the clock settles at the power cap
+SAMPLES = 5                    # timed replays of the K-step graph (median reported)
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
@@ -537,24 +543,32 @@ HEADLINE = "exp_bcast_mul_4096"
 
 
 def measure(w: Workload, steps: int, warmup: int, use_graph: bool = True,
-            min_ms: float = 0.0) -> dict:
-    """Times `steps` steps (at least `min_ms` of work when min_ms > 0: the step
-    count is raised from a probe of a few eager steps, capped at 1000)."""
+            samples: int = SAMPLES) -> dict:
+    """Times exactly `steps` steps, `samples` times, at steady state.
+
+    The `steps` launches are captured once into a HIP graph.  Before the timed
+    replays, the same graph is replayed back to back (no host synchronisation)
+    until at least PREROLL_MS of work and PREROLL_MIN_STEPS steps (MFMA
+    workloads: MFMA_PREROLL_MS) are queued ahead of the first timing event, so
+    the engine clock has ramped, the graph's launch overhead is hidden behind
+    queued work, and no idle gap precedes a timed step.  Each timed replay is
+    bracketed by its own pair of HIP events on the launch stream; the reported
+    per-step time is the median over the samples (all samples are listed)."""
     w.setup()
     for i in range(warmup):
         w.launch(i)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    if min_ms > 0.0:
-        p0 = torch.cuda.Event(enable_timing=True)
-        p1 = torch.cuda.Event(enable_timing=True)
-        p0.record(stream)
-        for i in range(3):
-            w.launch(i)
-        p1.record(stream)
-        torch.cuda.synchronize()
-        est = max(p0.elapsed_time(p1) / 3, 1e-3)
-        steps = max(steps, min(1000, math.ceil(min_ms / est)))
+    p0 = torch.cuda.Event(enable_timing=True)
+    p1 = torch.cuda.Event(enable_timing=True)
+    p0.record(stream)
+    for i in range(3):
+        w.launch(i)
+    p1.record(stream)
+    torch.cuda.synchronize()
+    est = max(p0.elapsed_time(p1) / 3, 1e-4)  # ms per step, eager
+    pre_ms = MFMA_PREROLL_MS if w.unit != "GB/s" else PREROLL_MS
+    pre_steps = max(PREROLL_MIN_STEPS, math.ceil(pre_ms / est))
     g = None
     if use_graph:
         s = torch.cuda.Stream()
@@ -567,25 +581,35 @@ def measure(w: Workload, steps: int, warmup: int, use_graph: bool = True,
         torch.cuda.synchronize()
         g.replay()  # untimed warm replay
         torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
+
+    def run():
+        if g is not None:
+            g.replay()
+        else:
+            for i in range(steps):
+                w.launch(i)
+
+    pre_reps = math.ceil(pre_steps / steps)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(samples)]
     torch.cuda.synchronize()
-    e0.record(stream)
-    if g is not None:
-        g.replay()
-    else:
-        for i in range(steps):
-            w.launch(i)
-    e1.record(stream)
+    for _ in range(pre_reps):
+        run()
+    for e0, e1 in ev:
+        e0.record(stream)
+        run()
+        e1.record(stream)
     torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1)
-    per = ms / steps
+    per_s = sorted(e0.elapsed_time(e1) / steps for e0, e1 in ev)
+    per = per_s[len(per_s) // 2]
     work = w.work_per_step()
     scale = 1e9 if w.unit == "GB/s" else 1e12
     achieved = work / (per * 1e-3) / scale
     peak = HBM_PEAK_GBS if w.unit == "GB/s" else BF16_PEAK_TFLOPS
     return {"name": w.name, "config": w.config, "kernel": w.kernel_name(), "bound": w.bound,
-            "steps": steps, "ms_total": ms, "ms_per_step": per, "achieved": achieved,
+            "steps": steps, "samples": samples, "preroll_steps": pre_reps * steps,
+            "ms_total": per * steps * samples, "ms_per_step": per,
+            "ms_per_step_min": per_s[0], "ms_per_step_max": per_s[-1], "achieved": achieved,
             "unit": w.unit, "peak": peak, "frac": achieved / peak, "work_per_step": work}
 
 
@@ -634,17 +658,67 @@ def traffic_for(name: str):
         return None
 
 
+def summarize_trace(path: str, steps: int, samples: int = SAMPLES, gap_us: float = 10.0) -> str:
+    """Markdown table of kernel durations from a rocprofv3 kernel trace
+    (`*_kernel_trace.csv`) of a bench.py run, taken from the timed replays
+    only.  Per kernel (name and workgroup count), the dispatches are split
+    into bursts that run back to back (less than `gap_us` between one
+    dispatch's end and the next one's start); the longest burst is the
+    pre-roll plus the timed replays, and its last `samples * steps`
+    dispatches are the timed ones.  Warm-up, probe and check dispatches, which
+    run at a cold clock or behind a host synchronisation, fall outside it."""
+    import csv
+    groups = {}
+    with open(path, newline="") as f:
+        for row in csv.DictReader(f):
+            name = row["Kernel_Name"].replace("(anonymous namespace)::", "")
+            name = name.removeprefix("void ").removeprefix("ttlh::").split("(")[0][:72]
+            wgs = int(row["Grid_Size_X"]) * int(row["Grid_Size_Y"]) * int(row["Grid_Size_Z"]) // max(
+                1, int(row["Workgroup_Size_X"]) * int(row["Workgroup_Size_Y"]) * int(row["Workgroup_Size_Z"]))
+            groups.setdefault((name, wgs), []).append(
+                (int(row["Start_Timestamp"]), int(row["End_Timestamp"])))
+    lines = ["| kernel | workgroups | dispatches | back-to-back burst | timed | median us | "
+             "mean us | min us | max us |", "|---|---|---|---|---|---|---|---|---|"]
+    rows = []
+    for (name, wgs), d in groups.items():
+        d.sort()
+        best, cur = [d[0]], [d[0]]
+        for prev, nxt in zip(d, d[1:]):
+            if (nxt[0] - prev[1]) * 1e-3 < gap_us:
+                cur.append(nxt)
+            else:
+                cur = [nxt]
+            if len(cur) > len(best):
+                best = cur
+        timed = best[-samples * steps:]
+        if len(best) < samples * steps:
+            continue  # not a timed workload kernel (set-up, fills, copies)
+        us = sorted((e - s) * 1e-3 for s, e in timed)
+        rows.append((name, wgs, len(d), len(best), len(timed), us[len(us) // 2],
+                     sum(us) / len(us), us[0], us[-1]))
+    for r in sorted(rows, key=lambda r: -r[5]):
+        lines.append(f"| `{r[0]}` | {r[1]} | {r[2]} | {r[3]} | {r[4]} | {r[5]:.2f} | {r[6]:.2f} | "
+                     f"{r[7]:.2f} | {r[8]:.2f} |")
+    return "\n".join(lines)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--only", default="", help="comma-separated workload names")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--trace-summary", metavar="CSV",
+                    help="print the timed-replay kernel durations of a rocprofv3 kernel trace of "
+                         "a bench.py run made with the same --steps, then exit (no GPU used)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run one 256 MiB device copy (PMC byte-counter calibration)")
     args = ap.parse_args()
+    if args.trace_summary:
+        print(summarize_trace(args.trace_summary, args.steps))
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for "
               f"--gpus {args.gpus}). Every config would shard without communication: the "
@@ -668,14 +742,8 @@ def main() -> int:
     results = {}
     for n in names:
         w = WORKLOADS[n]()
-        # MFMA workloads: the timed graph covers >= MFMA_MIN_MS of steady work
-        # (the clock ramps after the idle gap before a replay; a 20-step
-        # replay of a 0.1 ms GEMM is mostly ramp)
-        steps = args.steps if w.unit == "GB/s" else max(1, min(args.steps, 20))
-        warm = args.warmup if w.unit == "GB/s" else max(1, min(args.warmup, 3))
-        min_ms = 0.0 if w.unit == "GB/s" else MFMA_MIN_MS
-        log(f"[bench] {n}: steps={steps}{'+' if min_ms else ''} warmup={warm}")
-        r = measure(w, steps, warm, use_graph=not args.no_graph, min_ms=min_ms)
+        log(f"[bench] {n}: steps={args.steps} warmup={args.warmup}")
+        r = measure(w, args.steps, args.warmup, use_graph=not args.no_graph)
         r["parity"] = w.check()
         r["traffic"] = traffic_for(n)
         if w.unit == "GB/s":

@@ -196,3 +196,97 @@ def test_cache_key_distinguishes_aliasing(aliased):
     k2 = runner.KernelRunner._cache_key(runner.KernelRunner, (b, b if aliased else a, o), {})
     k3 = runner.KernelRunner._cache_key(runner.KernelRunner, (a, b if aliased else a, o), {})
     assert k1 == k2 and k1 != k3
+
+
+def _make_repeat_with_overwrite(ttl):
+    """Two iterations of { out[0, 0] = x[0, 0] + 1; x[0, 0] = y[0, 0] * 2 }:
+    the two instances of the first store read the same tiles but different
+    values of x.  One data-movement thread both writes x and reads it again,
+    so the second read follows the first write in program order."""
+    @ttl.kernel(grid=(1, 1))
+    def repeat_overwrite(x, y, out):
+        x_cb = ttl.make_circular_buffer_like(x, shape=(1, 1), buffer_factor=2)
+        y_cb = ttl.make_circular_buffer_like(y, shape=(1, 1), buffer_factor=2)
+        o_cb = ttl.make_circular_buffer_like(out, shape=(1, 1), buffer_factor=2)
+        w_cb = ttl.make_circular_buffer_like(x, shape=(1, 1), buffer_factor=2)
+
+        @ttl.compute()
+        def comp():
+            for _ in range(2):
+                with x_cb.wait() as xb, o_cb.reserve() as ob:
+                    ob.store(xb + 1)
+                with y_cb.wait() as yb, w_cb.reserve() as wb:
+                    wb.store(yb * 2)
+
+        @ttl.datamovement()
+        def dm_x():
+            for _ in range(2):
+                with x_cb.reserve() as xb:
+                    ttl.copy(x[0, 0], xb).wait()
+                with w_cb.wait() as wb:
+                    ttl.copy(wb, x[0, 0]).wait()
+
+        @ttl.datamovement()
+        def dm_y():
+            for _ in range(2):
+                with y_cb.reserve() as yb:
+                    ttl.copy(y[0, 0], yb).wait()
+                with o_cb.wait() as ob:
+                    ttl.copy(ob, out[0, 0]).wait()
+
+    return repeat_overwrite
+
+
+def test_repeated_store_not_merged_across_an_overwrite_of_its_operand():
+    # merging the two `out = x + 1` instances into one launch would compute
+    # out from the first value of x only; the simulator's second instance
+    # reads x after `x = y * 2` wrote it
+    x = torch.ones(32, 32, dtype=torch.bfloat16)
+    y = torch.ones(32, 32, dtype=torch.bfloat16)
+    out = torch.zeros(32, 32, dtype=torch.bfloat16)
+    ok = _make_repeat_with_overwrite(sim_exec.make_ttl())
+    oargs = [sim_exec.OracleTensor(t.clone()) for t in (x, y, out)]
+    ok(*oargs)
+    assert torch.equal(oargs[2].t, torch.full((32, 32), 3.0, dtype=torch.bfloat16))
+    k = _make_repeat_with_overwrite(ttl)
+    args = [ttnn.Tensor(t.clone()) for t in (x, y, out)]
+    with pytest.raises(P.PlanError, match="written more than once"):
+        k.trace(*args)
+
+
+def test_repeated_store_still_merged_when_nothing_else_touches_it():
+    # every core of the grid running the same loop (broadcast_demo.py style)
+    # writes the same tile from the same operands: planned once
+    a = O.seeded((64, 64), "uniform", 11, lo=-1, hi=1)
+    b = O.seeded((64, 64), "uniform", 12, lo=-1, hi=1)
+    (_, _, po), (_, _, oo), plan = _both(_make_same_tile_all_cores,
+                                         [a, b, torch.zeros(64, 64, dtype=torch.bfloat16)])
+    assert torch.equal(po, oo)
+    assert len(plan.launches) == 1 and plan.launches[0].tiles == 1
+
+
+def _make_same_tile_all_cores(ttl):
+    @ttl.kernel(grid=(2, 2))
+    def same_tile(a, b, out):
+        a_cb = ttl.make_circular_buffer_like(a, shape=(1, 1), buffer_factor=2)
+        b_cb = ttl.make_circular_buffer_like(b, shape=(1, 1), buffer_factor=2)
+        o_cb = ttl.make_circular_buffer_like(out, shape=(1, 1), buffer_factor=2)
+
+        @ttl.compute()
+        def comp():
+            with a_cb.wait() as ab, b_cb.wait() as bb, o_cb.reserve() as ob:
+                ob.store(ab + bb)
+
+        @ttl.datamovement()
+        def rd():
+            with a_cb.reserve() as ab:
+                ttl.copy(a[0, 0], ab).wait()
+            with b_cb.reserve() as bb:
+                ttl.copy(b[0, 0], bb).wait()
+
+        @ttl.datamovement()
+        def wr():
+            with o_cb.wait() as ob:
+                ttl.copy(ob, out[0, 0]).wait()
+
+    return same_tile

@@ -375,6 +375,10 @@ class _Group:
     # reductions: the scaler's tensor and its tile per store instance
     scaler_tensor: Any = None
     scaler_rc: List[np.ndarray] = field(default_factory=list)
+    # repeated store instances may be planned once (_dedupe_writes): set by
+    # build_plan when no other store site writes an operand of this one or
+    # reads its output, so no value changes between the repeats
+    dedupe_ok: bool = True
 
 
 def _leaf_rep(leaf) -> Tuple[bool, bool]:
@@ -1358,8 +1362,28 @@ def _fuse_attention(groups: List[_Group], tensor_ref) -> List[Any]:
     return out
 
 
+def _mark_dedupe(groups: List[_Group]) -> None:
+    """Repeats of a store site are one launch only when nothing else touches
+    its tensors in between.  Store sites run one launch each in trace order,
+    so if another site writes one of this site's operands, or reads its
+    output, the simulator's interleaving of the repeats with that site
+    matters (loop { out = x + 1; x = y * 2 } writes out from two values of x)
+    and the repeated writes are refused instead of merged."""
+    for g in groups:
+        reads = [t for t in g.leaf_tensors] + ([g.scaler_tensor] if g.scaler_tensor is not None else [])
+        g.dedupe_ok = True
+        for h in groups:
+            if h is g:
+                continue
+            h_reads = list(h.leaf_tensors) + ([h.scaler_tensor] if h.scaler_tensor is not None else [])
+            if any(h.out_tensor is t for t in reads) or any(t is g.out_tensor for t in h_reads):
+                g.dedupe_ok = False
+                break
+
+
 def build_plan(groups: List[_Group], tensor_ref) -> Plan:
     plan = Plan()
+    _mark_dedupe(groups)
     inl = _Inliner(groups)
     for g in _fuse_attention(groups, tensor_ref):
         if isinstance(g, SdpaLaunch):
@@ -1399,10 +1423,11 @@ def _dedupe_writes(g: _Group, out_rc, leaf_rc):
     (examples/broadcast_demo.py with grid="auto"): the simulator writes the
     same values several times, one launch writes them once.  Only for plain
     stores whose output is not also an operand (then repeats are not
-    idempotent); instances that write one tile with different operands stay
-    and are refused by the caller."""
+    idempotent) and whose tensors no other store site writes or reads
+    between the repeats (g.dedupe_ok, _mark_dedupe); instances that write one
+    tile with different operands stay and are refused by the caller."""
     n = out_rc.shape[0]
-    if g.acc or n == 0 or _unique_tiles(out_rc) == n:
+    if g.acc or n == 0 or _unique_tiles(out_rc) == n or not g.dedupe_ok:
         return out_rc, leaf_rc
     if any(t is g.out_tensor for t in g.leaf_tensors):
         return out_rc, leaf_rc
