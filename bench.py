@@ -19,15 +19,14 @@ own roofline figures:
 A "step" is one pass of the hot path over one batch of synthetic input: one
 execution of the kernel's launch plan over one resident buffer set.  Inputs
 are in HBM before the timed region; elementwise configs rotate buffer sets
-totalling > 256 MB so the Infinity Cache cannot serve them.  The K timed
-steps are captured once into a HIP graph and replayed, so host overhead does
-not pad short kernels; HIP events on the launch stream bracket the replay.
-Every workload times exactly K steps, at steady state: the K-step graph is
-first replayed back to back, without a host synchronisation, over at least
-PREROLL_MS (MFMA workloads MFMA_PREROLL_MS) and PREROLL_MIN_STEPS steps, so
-the engine clock has ramped and no idle gap or graph start-up precedes a
-timed step; then SAMPLES replays are timed, each between its own HIP events,
-and the median per-step time is reported.
+totalling > 256 MB so the Infinity Cache cannot serve them.
+Every workload times exactly K steps, at steady state: a HIP graph of the K
+steps is first replayed back to back, without a host synchronisation, over at
+least PREROLL_MS (MFMA workloads MFMA_PREROLL_MS) and PREROLL_MIN_STEPS
+steps; behind that queued work the K launches of each of SAMPLES samples are
+enqueued between their own HIP events, so the engine clock has ramped and no
+idle gap, host delay or graph start-up lies inside a timed sample.  The
+median per-step time is reported.
 """
 
 from __future__ import annotations
@@ -50,7 +49,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 PREROLL_MS = 10.0              # steady work queued ahead of the timed steps (ms), at least
 PREROLL_MIN_STEPS = 50         # ... and at least this many steps
 MFMA_PREROLL_MS = 30.0         # MFMA workloads: the clock settles at the power cap
-SAMPLES = 5                    # timed replays of the K-step graph (median reported)
+SAMPLES = 5                    # timed samples of K steps each (median reported)
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
@@ -546,14 +545,15 @@ def measure(w: Workload, steps: int, warmup: int, use_graph: bool = True,
             samples: int = SAMPLES) -> dict:
     """Times exactly `steps` steps, `samples` times, at steady state.
 
-    The `steps` launches are captured once into a HIP graph.  Before the timed
-    replays, the same graph is replayed back to back (no host synchronisation)
-    until at least PREROLL_MS of work and PREROLL_MIN_STEPS steps (MFMA
-    workloads: MFMA_PREROLL_MS) are queued ahead of the first timing event, so
-    the engine clock has ramped, the graph's launch overhead is hidden behind
-    queued work, and no idle gap precedes a timed step.  Each timed replay is
-    bracketed by its own pair of HIP events on the launch stream; the reported
-    per-step time is the median over the samples (all samples are listed)."""
+    Each timed sample is `steps` launches of the plan enqueued on the launch
+    stream between a pair of HIP events.  Before them, back-to-back work of
+    at least PREROLL_MS (MFMA workloads: MFMA_PREROLL_MS) and
+    PREROLL_MIN_STEPS steps is queued (replays of a HIP graph of the same
+    steps, no host synchronisation), and at least three times the host's
+    enqueue time of every timed launch: so the engine clock has ramped, the
+    host has enqueued every timed launch before the GPU reaches the first
+    event, and no idle gap or graph start-up lies inside a timed sample.  The
+    reported per-step time is the median over the samples (all listed)."""
     w.setup()
     for i in range(warmup):
         w.launch(i)
@@ -562,12 +562,15 @@ def measure(w: Workload, steps: int, warmup: int, use_graph: bool = True,
     p0 = torch.cuda.Event(enable_timing=True)
     p1 = torch.cuda.Event(enable_timing=True)
     p0.record(stream)
+    t0 = time.perf_counter()
     for i in range(3):
         w.launch(i)
+    host = (time.perf_counter() - t0) / 3 * 1e3  # ms of host time per launch
     p1.record(stream)
     torch.cuda.synchronize()
-    est = max(p0.elapsed_time(p1) / 3, 1e-4)  # ms per step, eager
-    pre_ms = MFMA_PREROLL_MS if w.unit != "GB/s" else PREROLL_MS
+    est = max(p0.elapsed_time(p1) / 3, 1e-4)  # ms per step on the GPU
+    pre_ms = max(MFMA_PREROLL_MS if w.unit != "GB/s" else PREROLL_MS,
+                 3.0 * host * steps * samples)
     pre_steps = max(PREROLL_MIN_STEPS, math.ceil(pre_ms / est))
     g = None
     if use_graph:
@@ -581,23 +584,20 @@ def measure(w: Workload, steps: int, warmup: int, use_graph: bool = True,
         torch.cuda.synchronize()
         g.replay()  # untimed warm replay
         torch.cuda.synchronize()
-
-    def run():
-        if g is not None:
-            g.replay()
-        else:
-            for i in range(steps):
-                w.launch(i)
-
     pre_reps = math.ceil(pre_steps / steps)
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(samples)]
     torch.cuda.synchronize()
     for _ in range(pre_reps):
-        run()
+        if g is not None:
+            g.replay()
+        else:
+            for i in range(steps):
+                w.launch(i)
     for e0, e1 in ev:
         e0.record(stream)
-        run()
+        for i in range(steps):
+            w.launch(i)
         e1.record(stream)
     torch.cuda.synchronize()
     per_s = sorted(e0.elapsed_time(e1) / steps for e0, e1 in ev)
@@ -608,6 +608,7 @@ def measure(w: Workload, steps: int, warmup: int, use_graph: bool = True,
     peak = HBM_PEAK_GBS if w.unit == "GB/s" else BF16_PEAK_TFLOPS
     return {"name": w.name, "config": w.config, "kernel": w.kernel_name(), "bound": w.bound,
             "steps": steps, "samples": samples, "preroll_steps": pre_reps * steps,
+            "host_ms_per_launch": host,
             "ms_total": per * steps * samples, "ms_per_step": per,
             "ms_per_step_min": per_s[0], "ms_per_step_max": per_s[-1], "achieved": achieved,
             "unit": w.unit, "peak": peak, "frac": achieved / peak, "work_per_step": work}
@@ -660,42 +661,43 @@ def traffic_for(name: str):
 
 def summarize_trace(path: str, steps: int, samples: int = SAMPLES, gap_us: float = 10.0) -> str:
     """Markdown table of kernel durations from a rocprofv3 kernel trace
-    (`*_kernel_trace.csv`) of a bench.py run, taken from the timed replays
-    only.  Per kernel (name and workgroup count), the dispatches are split
-    into bursts that run back to back (less than `gap_us` between one
-    dispatch's end and the next one's start); the longest burst is the
-    pre-roll plus the timed replays, and its last `samples * steps`
-    dispatches are the timed ones.  Warm-up, probe and check dispatches, which
-    run at a cold clock or behind a host synchronisation, fall outside it."""
+    (`*_kernel_trace.csv`) of a bench.py run, taken from its steady stretch.
+    All dispatches, in start order, are split into bursts that run back to
+    back (less than `gap_us` between one dispatch's end and the next one's
+    start, whatever the kernels).  Per kernel (name and workgroup count), the
+    burst holding most of its dispatches is the pre-roll plus the timed
+    samples; its last `samples * steps` dispatches of that kernel (fewer if
+    the burst is shorter) are reported.  Warm-up, probe and check dispatches,
+    which run at a cold clock or behind a host synchronisation, fall outside
+    it."""
     import csv
-    groups = {}
+    rows_in = []
     with open(path, newline="") as f:
         for row in csv.DictReader(f):
             name = row["Kernel_Name"].replace("(anonymous namespace)::", "")
             name = name.removeprefix("void ").removeprefix("ttlh::").split("(")[0][:72]
             wgs = int(row["Grid_Size_X"]) * int(row["Grid_Size_Y"]) * int(row["Grid_Size_Z"]) // max(
                 1, int(row["Workgroup_Size_X"]) * int(row["Workgroup_Size_Y"]) * int(row["Workgroup_Size_Z"]))
-            groups.setdefault((name, wgs), []).append(
-                (int(row["Start_Timestamp"]), int(row["End_Timestamp"])))
-    lines = ["| kernel | workgroups | dispatches | back-to-back burst | timed | median us | "
-             "mean us | min us | max us |", "|---|---|---|---|---|---|---|---|---|"]
+            rows_in.append((int(row["Start_Timestamp"]), int(row["End_Timestamp"]), (name, wgs)))
+    rows_in.sort()
+    burst, prev_end = 0, None
+    per = {}  # kernel -> {burst: [durations in start order]}
+    for s, e, key in rows_in:
+        if prev_end is not None and (s - prev_end) * 1e-3 >= gap_us:
+            burst += 1
+        prev_end = e if prev_end is None else max(prev_end, e)
+        per.setdefault(key, {}).setdefault(burst, []).append((e - s) * 1e-3)
+    lines = ["| kernel | workgroups | dispatches | in its longest back-to-back burst | reported | "
+             "median us | mean us | min us | max us |", "|---|---|---|---|---|---|---|---|---|"]
     rows = []
-    for (name, wgs), d in groups.items():
-        d.sort()
-        best, cur = [d[0]], [d[0]]
-        for prev, nxt in zip(d, d[1:]):
-            if (nxt[0] - prev[1]) * 1e-3 < gap_us:
-                cur.append(nxt)
-            else:
-                cur = [nxt]
-            if len(cur) > len(best):
-                best = cur
-        timed = best[-samples * steps:]
-        if len(best) < samples * steps:
+    for (name, wgs), bursts in per.items():
+        best = max(bursts.values(), key=len)
+        if len(best) < PREROLL_MIN_STEPS:
             continue  # not a timed workload kernel (set-up, fills, copies)
-        us = sorted((e - s) * 1e-3 for s, e in timed)
-        rows.append((name, wgs, len(d), len(best), len(timed), us[len(us) // 2],
-                     sum(us) / len(us), us[0], us[-1]))
+        timed = best[-samples * steps:]
+        us = sorted(timed)
+        rows.append((name, wgs, sum(map(len, bursts.values())), len(best), len(timed),
+                     us[len(us) // 2], sum(us) / len(us), us[0], us[-1]))
     for r in sorted(rows, key=lambda r: -r[5]):
         lines.append(f"| `{r[0]}` | {r[1]} | {r[2]} | {r[3]} | {r[4]} | {r[5]:.2f} | {r[6]:.2f} | "
                      f"{r[7]:.2f} | {r[8]:.2f} |")
