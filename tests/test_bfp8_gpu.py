@@ -178,3 +178,89 @@ def test_fused_bfp8_gemm_with_slow_loads():
            L.stream_ptr())
     torch.cuda.synchronize()
     _bound_check(c.cpu(), a.double() @ OB.unpack_c(bq, Kd, N).double(), Kd)
+
+
+# --- the fused entry's large-problem kernel: weights dequantised in LDS -----
+# (ttlh_matmul_bfp8w with >= 192 output blocks of 256 x 256, N a multiple of
+# 256 and K of 128).  It runs the DMA GEMM's MFMAs in the same k order on the
+# same bf16 values as the two-pass path (bfp8_unpack_kernel, itself bit-exact
+# against the oracle, then the DMA GEMM), so the two agree bit for bit.
+
+
+def _lds_decode_vs_two_pass(a, q, M, K, N):
+    from ttlhip import kernels as Kn
+    c1 = torch.full((M, N), 7.0, dtype=torch.bfloat16, device="cuda")
+    c2 = torch.full((M, N), 5.0, dtype=torch.bfloat16, device="cuda")
+    Kn.matmul_bfp8w(a, q, c1, two_pass=False)
+    Kn.matmul_bfp8w(a, q, c2, two_pass=True)
+    torch.cuda.synchronize()
+    return c1, c2
+
+
+@pytest.mark.parametrize("M,K,N", [(4096, 4096, 11008), (2048, 128, 6144), (3072, 512, 4096)])
+def test_lds_decode_gemm_equals_two_pass(M, K, N):
+    print(f"lds-decode gemm vs two-pass M={M} K={K} N={N}", flush=True)
+    a = O.seeded((M, K), "normal", 21).cuda()
+    q = OB.pack_c(O.seeded((K, N), "normal", 22, torch.float32, std=0.02)).cuda()
+    c1, c2 = _lds_decode_vs_two_pass(a, q, M, K, N)
+    assert torch.equal(c1.view(torch.int16), c2.view(torch.int16))
+
+
+def _all_pairs_weights(K, N, e_lo, e_hi):
+    """bfloat8_b tiles of a K x N matrix whose face rows take every exponent in
+    [e_lo, e_hi] with every element byte 0..255 (16 face rows per exponent)."""
+    nt = (K // 32) * (N // 32)
+    q = np.zeros((nt, 1088), dtype=np.uint8)
+    ne = e_hi - e_lo + 1
+    g = 0
+    for t in range(nt):
+        for x in range(64):
+            q[t, x] = e_lo + g % ne
+            q[t, 64 + 16 * x:64 + 16 * x + 16] = 16 * ((g // ne) % 16) + np.arange(16)
+            g += 1
+    assert g >= 16 * ne
+    return torch.from_numpy(q.ravel().copy())
+
+
+def test_lds_decode_gemm_all_pairs_equals_two_pass():
+    # every (exponent, byte) pair the packer can produce (e <= 254), subnormal
+    # products included, through the in-LDS decode: equal to the two-pass path
+    M, K, N = 4096, 128, 3072
+    q = _all_pairs_weights(K, N, 0, 254).cuda()
+    a = O.seeded((M, K), "normal", 23).cuda()
+    c1, c2 = _lds_decode_vs_two_pass(a, q, M, K, N)
+    assert torch.equal(c1.view(torch.int16), c2.view(torch.int16))
+
+
+def test_lds_decode_gemm_selects_decoded_rows_exactly():
+    # A row i is the unit vector e_(i mod K), so C row i is weight row i mod K
+    # itself: exact against the oracle's dequantisation (normal values only,
+    # e >= 7, so no subnormal operand is involved; -0 reads as +0)
+    M, K, N = 4096, 128, 3072
+    q = _all_pairs_weights(K, N, 7, 254)
+    a = torch.zeros(M, K, dtype=torch.bfloat16)
+    a[torch.arange(M), torch.arange(M) % K] = 1.0
+    from ttlhip import kernels as Kn
+    c = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    Kn.matmul_bfp8w(a.cuda(), q.cuda(), c, two_pass=False)
+    torch.cuda.synchronize()
+    wd = OB.unpack_c(q, K, N)
+    assert torch.equal(c.cpu(), wd[torch.arange(M) % K])
+
+
+def test_lds_decode_gemm_with_slow_loads():
+    # A and the packed weights in pinned host memory: every load of a stage
+    # far slower than a stage's MFMAs; the waits must still cover them
+    from ttlhip import _lib as L
+    from ttlhip import kernels as Kn
+    M, K, N = 2048, 256, 6144
+    a = O.seeded((M, K), "normal", 24)
+    q = OB.pack_c(O.seeded((K, N), "normal", 25, torch.float32, std=0.02))
+    ah, qh = a.pin_memory(), q.pin_memory()
+    c = torch.zeros(M, N, dtype=torch.bfloat16, device="cuda")
+    L.call("ttlh_matmul_bfp8w", ah.data_ptr(), K, qh.data_ptr(), c.data_ptr(), N, M, N, K,
+           L.stream_ptr())
+    ref = torch.empty_like(c)
+    Kn.matmul_bfp8w(a.cuda(), q.cuda(), ref, two_pass=True)
+    torch.cuda.synchronize()
+    assert torch.equal(c.view(torch.int16), ref.view(torch.int16))

@@ -1061,6 +1061,285 @@ bool launch_mm_dma_as(const MmArgs& a, hipStream_t s, int* status) {
   return true;
 }
 
+// ---------------------------------------------------------------------------
+// bf16 x bfloat8_b with the weights dequantised in LDS ahead of the MFMAs.
+// Tiling, A pipeline, fragment reads and MFMA sequence are mm_dma_kernel's
+// (256x256 block, four waves of 128x128, 32-k stages, A in a ring of four
+// LDS buffers by global_load_lds).  B arrives packed:
+//  - the eight bfloat8_b tiles of a stage (tile row s of Bq, n tiles
+//    8 bn .. 8 bn + 7) are one contiguous 8704-byte range in HBM; it reaches
+//    a ring of four LDS slots by global_load_lds: two 16-byte loads and one
+//    4-byte load per thread (waves 2 and 3 repeat the 4-byte part of waves 0
+//    and 1, so every wave issues the same number of loads);
+//  - a decode pass turns a slot into its stage's bf16 B buffer (two buffers,
+//    32 k rows x 256 n, row-major).  A thread decodes one face row (the 16
+//    elements sharing an exponent) per substep: one 16-byte LDS read of the
+//    element bytes and one of the exponent byte, per element
+//    v_cvt_f32_ubyte + v_ldexp_f32 (exact) with the top half of the fp32
+//    pattern and the sign bit packed by v_perm_b32 / v_and_or_b32, then two
+//    16-byte LDS writes.  The work sits between the MFMAs like the fragment
+//    reads and the loads;
+//  - stage s + 1 is decoded over the window between the barriers of stages
+//    s - 1 and s (first half of its face rows in the second substep of
+//    s - 1, second half in the first substep of s): B buffer (s + 1) & 1 is
+//    read by nobody then, and stage s + 1's fragments are read only after
+//    stage s's barrier;
+//  - 16-byte chunk c of B row r sits at c ^ 5 (r & 3), which keeps the
+//    transpose reads (4 rows x 4 chunks per 32 lanes), the decode's writes
+//    and its element reads (16 lanes = 4 tiles x 4 face rows) conflict-free;
+//  - load group G(s) = {A(s + 4), Bq(s + 5)} is issued in stage s's second
+//    substep (Bq(s + 5) into the slot Bq(s + 1) was decoded from); before
+//    stage s's barrier a wave waits for G(s - 3) (A(s + 1), Bq(s + 2)), so
+//    at most two groups (14 loads) stay in flight.  Groups and decodes past
+//    the last stage load / decode the last stage again (L2 hits, results
+//    never read), so every stage runs the same code.
+constexpr int kDqSlot = 8 * TTLH_BFP8_TILE_BYTES;  // 8704 bytes: one stage's packed tiles
+
+__shared__ __attribute__((aligned(16))) uint8_t dqQ0[kDqSlot], dqQ1[kDqSlot], dqQ2[kDqSlot],
+    dqQ3[kDqSlot];
+__shared__ __attribute__((aligned(16))) uint16_t dqB0[DK * LN], dqB1[DK * LN];
+
+template <int Q>
+__device__ __forceinline__ uint8_t* dq_qbuf() {
+  if constexpr (Q == 0) return dqQ0;
+  else if constexpr (Q == 1) return dqQ1;
+  else if constexpr (Q == 2) return dqQ2;
+  else return dqQ3;
+}
+template <int Q>
+__device__ __forceinline__ uint16_t* dq_bbuf() {
+  if constexpr (Q == 0) return dqB0;
+  else return dqB1;
+}
+
+struct DqGeo {
+  const uint8_t* q_src;   // 16-byte load 0 of stage 0 (+4096: load 1)
+  const uint8_t* q_src2;  // 4-byte load of stage 0
+  int64_t q_stage;        // bytes between stages (one tile row of Bq)
+  int d_elem;             // decode: element bytes of this thread's face row (first half)
+  int d_exp;              // ... its exponent byte
+  int d_out;              // byte offset of its first output chunk in the B buffer
+  int d_out1;             // ... of the second
+};
+
+// B operand offsets for the c ^ 5 (r & 3) chunk swizzle (the transpose-read
+// lane pattern is mm_dma_kernel's: row kb + (lane & 15) / 4, chunk
+// wn / 8 + 4 j + e)
+__device__ __forceinline__ void dq_fb(DmaGeo& g, int wn, int lane) {
+  const int brow = (lane & 15) >> 2;
+  const int e = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    g.fb[j] = brow * 512 + (wn / 8 + ((4 * j + e) ^ (5 * brow))) * 16 + 8 * (lane & 1);
+}
+
+__device__ __forceinline__ DqGeo make_dq_geo(const MmArgs& p, int bn, int lane) {
+  DqGeo d;
+  const int t = threadIdx.x, w = t >> 6;
+  const uint8_t* base = p.Bq + static_cast<int64_t>(bn) * 8 * TTLH_BFP8_TILE_BYTES;
+  d.q_src = base + 16 * t;
+  d.q_src2 = base + 8192 + 4 * ((w & 1) * 64 + lane);
+  d.q_stage = static_cast<int64_t>(p.bq_tiles_n) * TTLH_BFP8_TILE_BYTES;
+  // face row of the first half: tile nt = (lane >> 2) & 3, face f = lane >> 4,
+  // row r = 4 w + (lane & 3); the second half is tile nt + 4
+  const int nt = (lane >> 2) & 3, f = lane >> 4, r = 4 * w + (lane & 3);
+  d.d_elem = nt * TTLH_BFP8_TILE_BYTES + 64 + 256 * f + 16 * r;
+  d.d_exp = nt * TTLH_BFP8_TILE_BYTES + 16 * f + r;
+  const int k = 16 * (f >> 1) + r, sw = 5 * (r & 3), c0 = 4 * nt + 2 * (f & 1);
+  d.d_out = k * 512 + (c0 ^ sw) * 16;
+  d.d_out1 = k * 512 + ((c0 + 1) ^ sw) * 16;
+  return d;
+}
+
+// stage x (clamped to the last) of Bq into slot Q: load i of 3
+template <int Q>
+__device__ __forceinline__ void dq_qload(const DqGeo& d, int x, int i) {
+  const int wbase = threadIdx.x & ~63;
+  const int64_t so = static_cast<int64_t>(x) * d.q_stage;
+  uint8_t* slot = dq_qbuf<Q>();
+  if (i < 2)
+    __builtin_amdgcn_global_load_lds(d.q_src + so + 4096 * i,
+                                     (lds_void*)(slot + 16 * (i * kThreads + wbase)), 16, 0, 0);
+  else
+    __builtin_amdgcn_global_load_lds(d.q_src2 + so,
+                                     (lds_void*)(slot + 8192 + 4 * (wbase & 64)), 4, 0, 0);
+}
+
+// one face row being decoded: element bytes, exponent, bf16 pairs
+struct DqDec {
+  u32x4 w;
+  uint32_t e;
+  int sh;
+  uint32_t m[4];
+  uint32_t o[8];
+};
+
+__device__ __forceinline__ void dq_read(const uint8_t* slot, const DqGeo& d, int half, DqDec& s) {
+  s.w = *reinterpret_cast<const u32x4*>(slot + d.d_elem + half * 4 * TTLH_BFP8_TILE_BYTES);
+  s.e = slot[d.d_exp + half * 4 * TTLH_BFP8_TILE_BYTES];
+}
+
+// bf16 pair p (elements 2p, 2p + 1): value (-1)^s m 2^(e - 133), exact
+__device__ __forceinline__ void dq_pair(DqDec& s, int p) {
+  const int i = p >> 1, h = p & 1;
+  if (p == 0) s.sh = static_cast<int>(s.e) - 133;
+  if (h == 0) s.m[i] = s.w[i] & 0x7f7f7f7fu;
+  const float f0 = __builtin_amdgcn_ldexpf(static_cast<float>((s.m[i] >> (16 * h)) & 0xffu), s.sh);
+  const float f1 = __builtin_amdgcn_ldexpf(static_cast<float>((s.m[i] >> (16 * h + 8)) & 0xffu), s.sh);
+  const uint32_t hi = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+  const uint32_t sg = __builtin_amdgcn_perm(s.w[i], s.w[i], h ? 0x030C020Cu : 0x010C000Cu);
+  s.o[p] = (sg & 0x80008000u) | hi;
+}
+
+__device__ __forceinline__ void dq_write(uint16_t* bbuf, const DqGeo& d, int half, int h,
+                                         const DqDec& s) {
+  char* b = reinterpret_cast<char*>(bbuf) + (h ? d.d_out1 : d.d_out) + half * 256;
+  *reinterpret_cast<u32x4*>(b) = u32x4{s.o[4 * h], s.o[4 * h + 1], s.o[4 * h + 2], s.o[4 * h + 3]};
+}
+
+// whole decode of one half of a slot (prologue)
+__device__ __forceinline__ void dq_decode_half(const uint8_t* slot, uint16_t* bbuf, const DqGeo& d,
+                                               int half) {
+  DqDec s;
+  dq_read(slot, d, half, s);
+#pragma unroll
+  for (int p = 0; p < 8; ++p) dq_pair(s, p);
+  dq_write(bbuf, d, half, 0, s);
+  dq_write(bbuf, d, half, 1, s);
+}
+
+// decode work of substep slot x (0..15): the reads at 0, the eight pairs
+// spread over 2..13, the two 16-byte writes once their pairs exist
+__device__ __forceinline__ void dq_piece(const uint8_t* slot, uint16_t* bbuf, const DqGeo& d,
+                                         int half, DqDec& s, int x) {
+  switch (x) {
+    case 0: dq_read(slot, d, half, s); break;
+    case 2: dq_pair(s, 0); break;
+    case 4: dq_pair(s, 1); break;
+    case 5: dq_pair(s, 2); break;
+    case 7: dq_pair(s, 3); break;
+    case 8: dq_write(bbuf, d, half, 0, s); dq_pair(s, 4); break;
+    case 10: dq_pair(s, 5); break;
+    case 11: dq_pair(s, 6); break;
+    case 13: dq_pair(s, 7); break;
+    case 14: dq_write(bbuf, d, half, 1, s); break;
+    default: break;
+  }
+}
+
+template <bool OUT_BF16, bool ACC>
+__global__ __launch_bounds__(kThreads, 1) void mm_dq_kernel(const MmArgs p) {
+  int bm, bn;
+  block_coords2(p, bm, bn);
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = (wave >> 1) * 128;
+  const int wn = (wave & 1) * 128;
+  DmaGeo g = make_dma_geo(p, bm, bn, wm, wn, lane);  // A loads and A fragment offsets
+  dq_fb(g, wn, lane);                                // B fragment offsets (5 (r & 3) swizzle)
+  const DqGeo d = make_dq_geo(p, bn, lane);
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  const int nk = p.K / DK;  // a multiple of 4 (launcher)
+  auto a_load = [&](auto qq, int x, int i) {  // stage x (clamped) of A into buffer Q: load i of 4
+    constexpr int Q = decltype(qq)::value;
+    const int wbase = threadIdx.x & ~63;
+    __builtin_amdgcn_global_load_lds(g.a_src[i] + min(x, nk - 1) * DK,
+                                     (lds_void*)(dma_abuf<Q>() + (i * kThreads + wbase) * 8), 16, 0, 0);
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+
+  // prologue: Bq(0), then groups G(-4) .. G(-2) = {A(0), Bq(1)}, {A(1), Bq(2)},
+  // {A(2), Bq(3)}
+  for (int i = 0; i < 3; ++i) dq_qload<0>(d, 0, i);
+  for (int i = 0; i < 4; ++i) a_load(I0(), 0, i);
+  for (int i = 0; i < 3; ++i) dq_qload<1>(d, min(1, nk - 1), i);
+  for (int i = 0; i < 4; ++i) a_load(I1(), 1, i);
+  for (int i = 0; i < 3; ++i) dq_qload<2>(d, min(2, nk - 1), i);
+  for (int i = 0; i < 4; ++i) a_load(I2(), 2, i);
+  for (int i = 0; i < 3; ++i) dq_qload<3>(d, min(3, nk - 1), i);
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(14));  // Bq(0), A(0), Bq(1) landed
+  stage_barrier();
+  dq_decode_half(dq_qbuf<0>(), dq_bbuf<0>(), d, 0);  // stage 0 whole, stage 1 first half
+  dq_decode_half(dq_qbuf<0>(), dq_bbuf<0>(), d, 1);
+  dq_decode_half(dq_qbuf<1>(), dq_bbuf<1>(), d, 0);
+  __builtin_amdgcn_s_waitcnt(0xC07F);          // lgkmcnt(0): decode reads / writes done
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(14));  // (same groups as above)
+  stage_barrier();
+  // G(-1) = {A(3), Bq(4)}: slot 0 is free now
+  for (int i = 0; i < 4; ++i) a_load(I3(), 3, i);
+  for (int i = 0; i < 3; ++i) dq_qload<0>(d, min(4, nk - 1), i);
+  DFrags f0, f1;
+  dma_read_frags(dma_abuf<0>(), dq_bbuf<0>(), g, 0, lane, f0);
+
+  auto stage = [&](auto qq, int s) {
+    constexpr int q = decltype(qq)::value;  // A buffer / Bq slot of stage s
+    uint16_t* Ab = dma_abuf<q>();
+    uint16_t* Bb = dq_bbuf<q & 1>();
+    uint16_t* An = dma_abuf<(q + 1) & 3>();
+    uint16_t* Bn = dq_bbuf<(q + 1) & 1>();
+    // substep 0: MFMAs on f0; this stage's substep-1 fragments; second half
+    // of stage s + 1's decode (slot (q + 1) & 3 -> B buffer (q + 1) & 1)
+    {
+      DFragParts parts;
+      DqDec dec;
+#pragma unroll
+      for (int x = 0; x < 16; ++x) {
+        dma_mfma_one(f0, acc, x);
+        if (x < 12) dma_read_piece(Ab, Bb, g, 1, lane, parts, x);
+        dq_piece(dq_qbuf<(q + 1) & 3>(), Bn, d, 1, dec, x);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      parts.to_frags(f1);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);         // lgkmcnt(0): this wave's LDS reads / writes done
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(14));  // G(s - 3) landed: A(s + 1), Bq(s + 2)
+    stage_barrier();
+    // substep 1: MFMAs on f1; stage s + 1's substep-0 fragments; G(s) =
+    // {A(s + 4) -> A buffer q, Bq(s + 5) -> slot (q + 1) & 3}; first half of
+    // stage s + 2's decode (slot (q + 2) & 3 -> B buffer q & 1)
+    {
+      DFragParts nparts;
+      DqDec dec;
+#pragma unroll
+      for (int x = 0; x < 16; ++x) {
+        dma_mfma_one(f1, acc, x);
+        if (x < 12) dma_read_piece(An, Bn, g, 0, lane, nparts, x);
+        if ((x & 1) && x < 8) a_load(qq, s + 4, x >> 1);
+        if ((x & 1) && x >= 9) dq_qload<(q + 1) & 3>(d, min(s + 5, nk - 1), (x - 9) >> 1);
+        dq_piece(dq_qbuf<(q + 2) & 3>(), Bb, d, 0, dec, x);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      nparts.to_frags(f0);
+    }
+  };
+
+  for (int s = 0; s < nk; s += 4) {
+    stage(I0(), s);
+    stage(I1(), s + 1);
+    stage(I2(), s + 2);
+    stage(I3(), s + 3);
+  }
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // the last (unused) groups
+
+  const int r0 = bm * LM + wm, c0 = bn * LN + wn;
+  static_for<16>([&](auto ij) {
+    constexpr int i = decltype(ij)::value / 4, j = decltype(ij)::value % 4;
+    if (r0 + i * 32 < p.M)
+      store_acc_tile_pairs<OUT_BF16, ACC>(p, acc[i][j], r0 + i * 32, c0 + j * 32, lane);
+  });
+}
+
 // Launches the 256x256 kernel when the problem has enough 256x256 blocks to
 // fill the chip; returns false otherwise.
 template <bool BQ>
@@ -1071,6 +1350,14 @@ bool launch_mm256(MmArgs a, hipStream_t s, int* status) {
   a.grid_m = gm;
   a.grid_n = gn;
   if constexpr (BQ) {
+    // weights dequantised in LDS: whole 256-column blocks of whole stage
+    // quads, tiles 16-byte aligned
+    if (a.N % LN == 0 && a.K % (4 * DK) == 0 && (reinterpret_cast<uintptr_t>(a.Bq) & 15) == 0) {
+      hipLaunchKernelGGL((mm_dq_kernel<true, false>), dim3(a.grid_m * a.grid_n), dim3(kThreads), 0,
+                         s, a);
+      *status = check_launch("mm_dq_kernel");
+      return true;
+    }
     return launch_mm256_as<true, true, false>(a, s, status);
   } else {
     if (a.c_dtype == TTLH_BF16)
