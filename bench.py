@@ -12,6 +12,7 @@ own roofline figures:
   C3 bf16 matmul 4096^3       tt-lang kernel (multicore style)     TFLOP/s
   C4 bf16 x bfp8 4096x4096x11008   tt-lang kernel (multicore style, ttnn.bfloat8_b B)
                               -> ttlh_matmul_bfp8w_ws (two-pass)   TFLOP/s
+  C4, weights dequantised in LDS   ttlh_matmul_bfp8w (mm_dq_kernel)  TFLOP/s
   C5 SDPA [4,32,4096,128]     tt-lang attention program -> ttlh_sdpa_fwd   TFLOP/s
   row sums 4096^2 (spec reduce_sum)  tt-lang kernel (reduce_rows)  HBM GB/s
   tilize 4096^2 bf16 (TILE_LAYOUT)   ttlh_tilize                  HBM GB/s
@@ -457,6 +458,28 @@ class Bfp8MatmulWorkload(PlanWorkload):
                           "(no simulator path exists for bfloat8_b)"}
 
 
+class Bfp8LdsMatmulWorkload(Bfp8MatmulWorkload):
+    """C4 on the north-star design: the same operands as the plan's launch,
+    through the fused entry point ttlh_matmul_bfp8w (no workspace): the
+    bfloat8_b tiles go into LDS packed and are dequantised there between the
+    MFMAs (mm_dq_kernel).  At M = 4096 every weight tile is decoded once per
+    256-row block of A (16 times), which is why the two-pass launch of the
+    plan is faster at this M; this line reports the kernel itself."""
+
+    def kernel_name(self):
+        return "mm_dq_kernel"
+
+    def setup(self):
+        super().setup()
+        from ttlhip import kernels as Kn
+        a, wq, c = self.sets[0]
+        self._a, self._q, self._c = a._tensor, wq._tensor, c._tensor
+        self._mm = Kn.matmul_bfp8w
+
+    def launch(self, i):
+        self._mm(self._a, self._q, self._c, two_pass=False)
+
+
 class SdpaWorkload(PlanWorkload):
     """C5 through the drop-in: attention written tile by tile with the spec's
     ops (tests/kernel_lib.py make_attention: @, reduce_max, exp, broadcast,
@@ -534,6 +557,8 @@ WORKLOADS = {
     "matmul_bf16_4096": lambda: MatmulWorkload("matmul_bf16_4096", 4096, 4096, 4096),
     "matmul_bfp8w_4096x11008": lambda: Bfp8MatmulWorkload("matmul_bfp8w_4096x11008", 4096,
                                                           11008, 4096),
+    "matmul_bfp8w_lds_4096x11008": lambda: Bfp8LdsMatmulWorkload("matmul_bfp8w_lds_4096x11008",
+                                                                 4096, 11008, 4096),
     "sdpa_4x32x4096x128": lambda: SdpaWorkload("sdpa_4x32x4096x128", 4, 32, 4096, 128),
     "reduce_sum_rows_4096": lambda: ReduceWorkload("reduce_sum_rows_4096", 4096),
     "tilize_4096": lambda: TilizeWorkload("tilize_4096", 4096),

@@ -1068,7 +1068,7 @@ bool launch_mm_dma_as(const MmArgs& a, hipStream_t s, int* status) {
 // LDS buffers by global_load_lds).  B arrives packed:
 //  - the eight bfloat8_b tiles of a stage (tile row s of Bq, n tiles
 //    8 bn .. 8 bn + 7) are one contiguous 8704-byte range in HBM; it reaches
-//    a ring of four LDS slots by global_load_lds: two 16-byte loads and one
+//    a ring of LDS slots by global_load_lds: two 16-byte loads and one
 //    4-byte load per thread (waves 2 and 3 repeat the 4-byte part of waves 0
 //    and 1, so every wave issues the same number of loads);
 //  - a decode pass turns a slot into its stage's bf16 B buffer (two buffers,
@@ -1087,25 +1087,21 @@ bool launch_mm_dma_as(const MmArgs& a, hipStream_t s, int* status) {
 //  - 16-byte chunk c of B row r sits at c ^ 5 (r & 3), which keeps the
 //    transpose reads (4 rows x 4 chunks per 32 lanes), the decode's writes
 //    and its element reads (16 lanes = 4 tiles x 4 face rows) conflict-free;
-//  - load group G(s) = {A(s + 4), Bq(s + 5)} is issued in stage s's second
-//    substep (Bq(s + 5) into the slot Bq(s + 1) was decoded from); before
-//    stage s's barrier a wave waits for G(s - 3) (A(s + 1), Bq(s + 2)), so
-//    at most two groups (14 loads) stay in flight.  Groups and decodes past
+//  - the packed ring has five slots; load group G(s) = {A(s + 4), Bq(s + 6)}
+//    is issued in stage s's second substep (Bq(s + 6) into the slot Bq(s + 1)
+//    was decoded from); before stage s's barrier a wave waits for G(s - 3)
+//    (A(s + 1), Bq(s + 3)), so at most two groups (14 loads) stay in flight,
+//    and a stage's packed bytes are visible two barriers before its decode
+//    window closes, early enough to read each substep's bytes one substep
+//    ahead.  Groups and decodes past
 //    the last stage load / decode the last stage again (L2 hits, results
 //    never read), so every stage runs the same code.
 constexpr int kDqSlot = 8 * TTLH_BFP8_TILE_BYTES;  // 8704 bytes: one stage's packed tiles
 
-__shared__ __attribute__((aligned(16))) uint8_t dqQ0[kDqSlot], dqQ1[kDqSlot], dqQ2[kDqSlot],
-    dqQ3[kDqSlot];
+constexpr int kDqSlots = 5;                          // ring of packed stages
+__shared__ __attribute__((aligned(16))) uint8_t dqQ[kDqSlots * kDqSlot];
 __shared__ __attribute__((aligned(16))) uint16_t dqB0[DK * LN], dqB1[DK * LN];
 
-template <int Q>
-__device__ __forceinline__ uint8_t* dq_qbuf() {
-  if constexpr (Q == 0) return dqQ0;
-  else if constexpr (Q == 1) return dqQ1;
-  else if constexpr (Q == 2) return dqQ2;
-  else return dqQ3;
-}
 template <int Q>
 __device__ __forceinline__ uint16_t* dq_bbuf() {
   if constexpr (Q == 0) return dqB0;
@@ -1113,8 +1109,9 @@ __device__ __forceinline__ uint16_t* dq_bbuf() {
 }
 
 struct DqGeo {
-  const uint8_t* q_src;   // 16-byte load 0 of stage 0 (+4096: load 1)
-  const uint8_t* q_src2;  // 4-byte load of stage 0
+  uint32_t q_off;         // byte offset in Bq of 16-byte load 0 of stage 0 (+4096: load 1)
+  uint32_t q_off2;        // ... of the 4-byte load
+  uint32_t a_off[4];      // byte offsets in A of this thread's four A loads, at k = 0
   int64_t q_stage;        // bytes between stages (one tile row of Bq)
   int d_elem;             // decode: element bytes of this thread's face row (first half)
   int d_exp;              // ... its exponent byte
@@ -1136,9 +1133,9 @@ __device__ __forceinline__ void dq_fb(DmaGeo& g, int wn, int lane) {
 __device__ __forceinline__ DqGeo make_dq_geo(const MmArgs& p, int bn, int lane) {
   DqGeo d;
   const int t = threadIdx.x, w = t >> 6;
-  const uint8_t* base = p.Bq + static_cast<int64_t>(bn) * 8 * TTLH_BFP8_TILE_BYTES;
-  d.q_src = base + 16 * t;
-  d.q_src2 = base + 8192 + 4 * ((w & 1) * 64 + lane);
+  const uint32_t base = static_cast<uint32_t>(bn) * 8 * TTLH_BFP8_TILE_BYTES;
+  d.q_off = base + 16 * t;
+  d.q_off2 = base + 8192 + 4 * ((w & 1) * 64 + lane);
   d.q_stage = static_cast<int64_t>(p.bq_tiles_n) * TTLH_BFP8_TILE_BYTES;
   // face row of the first half: tile nt = (lane >> 2) & 3, face f = lane >> 4,
   // row r = 4 w + (lane & 3); the second half is tile nt + 4
@@ -1151,18 +1148,50 @@ __device__ __forceinline__ DqGeo make_dq_geo(const MmArgs& p, int bn, int lane) 
   return d;
 }
 
-// stage x (clamped to the last) of Bq into slot Q: load i of 3
-template <int Q>
-__device__ __forceinline__ void dq_qload(const DqGeo& d, int x, int i) {
+// Direct-to-LDS loads written as inline asm, uniform 64-bit base in SGPRs
+// plus a 32-bit lane offset (the launcher keeps A and Bq below 2 GiB).  A
+// compiler-visible LDS DMA makes the compiler treat LDS reads as completing
+// out of order and wait for all of them (lgkmcnt(0)) before the decode's
+// first use of its own read, stalling on the fragment reads issued after
+// it; this kernel waits for its DMA explicitly (vmcnt before each barrier).
+// The uniform operands pass through readfirstlane; M0 = the wave's LDS
+// destination, one wait state before the load.
+__device__ __forceinline__ uint64_t dq_sbase(const void* base) {
+  const uint64_t g = reinterpret_cast<uint64_t>(base);
+  return (uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(g >> 32)))) << 32) |
+         uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(uint32_t(g))));
+}
+__device__ __forceinline__ void dq_dma16(uint64_t sbase, uint32_t off, const void* lds) {
+  const uint32_t m0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)lds));
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %2"
+      :
+      : "s"(__builtin_amdgcn_readfirstlane(m0)), "v"(off), "s"(sbase)
+      : "memory", "m0");
+}
+__device__ __forceinline__ void dq_dma4(uint64_t sbase, uint32_t off, const void* lds) {
+  const uint32_t m0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)lds));
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dword %1, %2"
+      :
+      : "s"(__builtin_amdgcn_readfirstlane(m0)), "v"(off), "s"(sbase)
+      : "memory", "m0");
+}
+
+// stage x (clamped to the last) of Bq into the slot at byte `slot` of the
+// ring: load i of 3
+__device__ __forceinline__ void dq_qload(const MmArgs& p, const DqGeo& d, int x, int slot, int i) {
   const int wbase = threadIdx.x & ~63;
-  const int64_t so = static_cast<int64_t>(x) * d.q_stage;
-  uint8_t* slot = dq_qbuf<Q>();
+  const uint64_t sb = dq_sbase(p.Bq + static_cast<int64_t>(x) * d.q_stage);
+  uint8_t* s = dqQ + slot;
   if (i < 2)
-    __builtin_amdgcn_global_load_lds(d.q_src + so + 4096 * i,
-                                     (lds_void*)(slot + 16 * (i * kThreads + wbase)), 16, 0, 0);
+    dq_dma16(sb, d.q_off + 4096 * i, s + 16 * (i * kThreads + wbase));
   else
-    __builtin_amdgcn_global_load_lds(d.q_src2 + so,
-                                     (lds_void*)(slot + 8192 + 4 * (wbase & 64)), 4, 0, 0);
+    dq_dma4(sb, d.q_off2, s + 8192 + 4 * (wbase & 64));
 }
 
 // one face row being decoded: element bytes, exponent, bf16 pairs
@@ -1174,21 +1203,45 @@ struct DqDec {
   uint32_t o[8];
 };
 
-__device__ __forceinline__ void dq_read(const uint8_t* slot, const DqGeo& d, int half, DqDec& s) {
-  s.w = *reinterpret_cast<const u32x4*>(slot + d.d_elem + half * 4 * TTLH_BFP8_TILE_BYTES);
-  s.e = slot[d.d_exp + half * 4 * TTLH_BFP8_TILE_BYTES];
+__device__ __forceinline__ void dq_read(int slot, const DqGeo& d, int half, DqDec& s) {
+  const uint8_t* b = dqQ + slot;
+  s.w = *reinterpret_cast<const u32x4*>(b + d.d_elem + half * 4 * TTLH_BFP8_TILE_BYTES);
+  s.e = b[d.d_exp + half * 4 * TTLH_BFP8_TILE_BYTES];
 }
 
-// bf16 pair p (elements 2p, 2p + 1): value (-1)^s m 2^(e - 133), exact
-__device__ __forceinline__ void dq_pair(DqDec& s, int p) {
+// bf16 pair p (elements 2p, 2p + 1): value (-1)^s m 2^(e - 133), exact.
+// Two pieces, so the work can be spread between MFMAs: the conversions
+// (piece 0: v_cvt_f32_ubyte + v_ldexp_f32 of both elements, the magnitude
+// mask on a dword's first pair, the shift on the first pair) and the packing
+// (piece 1: the top halves and the sign bits).
+__device__ __forceinline__ void dq_pair_cvt(DqDec& s, int p, float& f0, float& f1) {
   const int i = p >> 1, h = p & 1;
   if (p == 0) s.sh = static_cast<int>(s.e) - 133;
   if (h == 0) s.m[i] = s.w[i] & 0x7f7f7f7fu;
-  const float f0 = __builtin_amdgcn_ldexpf(static_cast<float>((s.m[i] >> (16 * h)) & 0xffu), s.sh);
-  const float f1 = __builtin_amdgcn_ldexpf(static_cast<float>((s.m[i] >> (16 * h + 8)) & 0xffu), s.sh);
+  // v_cvt_f32_ubyte{0..3} of the masked dword, one instruction per element
+  // (written out: from the C++ shift-and-mask form the compiler extracts each
+  // 7-bit field first, an extra instruction per element)
+  float c0, c1;
+  if (h == 0) {
+    asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(c0) : "v"(s.m[i]));
+    asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(c1) : "v"(s.m[i]));
+  } else {
+    asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(c0) : "v"(s.m[i]));
+    asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(c1) : "v"(s.m[i]));
+  }
+  f0 = __builtin_amdgcn_ldexpf(c0, s.sh);
+  f1 = __builtin_amdgcn_ldexpf(c1, s.sh);
+}
+__device__ __forceinline__ void dq_pair_pack(DqDec& s, int p, float f0, float f1) {
+  const int i = p >> 1, h = p & 1;
   const uint32_t hi = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
   const uint32_t sg = __builtin_amdgcn_perm(s.w[i], s.w[i], h ? 0x030C020Cu : 0x010C000Cu);
   s.o[p] = (sg & 0x80008000u) | hi;
+}
+__device__ __forceinline__ void dq_pair(DqDec& s, int p) {
+  float f0, f1;
+  dq_pair_cvt(s, p, f0, f1);
+  dq_pair_pack(s, p, f0, f1);
 }
 
 __device__ __forceinline__ void dq_write(uint16_t* bbuf, const DqGeo& d, int half, int h,
@@ -1198,8 +1251,7 @@ __device__ __forceinline__ void dq_write(uint16_t* bbuf, const DqGeo& d, int hal
 }
 
 // whole decode of one half of a slot (prologue)
-__device__ __forceinline__ void dq_decode_half(const uint8_t* slot, uint16_t* bbuf, const DqGeo& d,
-                                               int half) {
+__device__ __forceinline__ void dq_decode_half(int slot, uint16_t* bbuf, const DqGeo& d, int half) {
   DqDec s;
   dq_read(slot, d, half, s);
 #pragma unroll
@@ -1208,22 +1260,20 @@ __device__ __forceinline__ void dq_decode_half(const uint8_t* slot, uint16_t* bb
   dq_write(bbuf, d, half, 1, s);
 }
 
-// decode work of substep slot x (0..15): the reads at 0, the eight pairs
-// spread over 2..13, the two 16-byte writes once their pairs exist
-__device__ __forceinline__ void dq_piece(const uint8_t* slot, uint16_t* bbuf, const DqGeo& d,
-                                         int half, DqDec& s, int x) {
-  switch (x) {
-    case 0: dq_read(slot, d, half, s); break;
-    case 2: dq_pair(s, 0); break;
-    case 4: dq_pair(s, 1); break;
-    case 5: dq_pair(s, 2); break;
-    case 7: dq_pair(s, 3); break;
-    case 8: dq_write(bbuf, d, half, 0, s); dq_pair(s, 4); break;
-    case 10: dq_pair(s, 5); break;
-    case 11: dq_pair(s, 6); break;
-    case 13: dq_pair(s, 7); break;
-    case 14: dq_write(bbuf, d, half, 1, s); break;
-    default: break;
+// Decode work placed after MFMA x of a substep, for a face row whose element
+// and exponent bytes are already in registers (read at the end of the
+// previous substep): piece 2p / 2p + 1 = conversions / packing of pair p (at
+// most six VALU instructions per MFMA), the first 16-byte write after pair 3
+// is packed, the second after pair 7.
+__device__ __forceinline__ void dq_piece_ready(uint16_t* bbuf, const DqGeo& d, int half,
+                                               DqDec& s, float (&f)[2], int x) {
+  const int p = x >> 1;
+  if ((x & 1) == 0) {
+    if (x == 8) dq_write(bbuf, d, half, 0, s);
+    dq_pair_cvt(s, p, f[0], f[1]);
+  } else {
+    dq_pair_pack(s, p, f[0], f[1]);
+    if (x == 15) dq_write(bbuf, d, half, 1, s);
   }
 }
 
@@ -1237,7 +1287,11 @@ __global__ __launch_bounds__(kThreads, 1) void mm_dq_kernel(const MmArgs p) {
   const int wn = (wave & 1) * 128;
   DmaGeo g = make_dma_geo(p, bm, bn, wm, wn, lane);  // A loads and A fragment offsets
   dq_fb(g, wn, lane);                                // B fragment offsets (5 (r & 3) swizzle)
-  const DqGeo d = make_dq_geo(p, bn, lane);
+  DqGeo d = make_dq_geo(p, bn, lane);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    d.a_off[i] = static_cast<uint32_t>(reinterpret_cast<const char*>(g.a_src[i]) -
+                                       reinterpret_cast<const char*>(p.A));
 
   f32x16 acc[4][4];
 #pragma unroll
@@ -1251,75 +1305,93 @@ __global__ __launch_bounds__(kThreads, 1) void mm_dq_kernel(const MmArgs p) {
   auto a_load = [&](auto qq, int x, int i) {  // stage x (clamped) of A into buffer Q: load i of 4
     constexpr int Q = decltype(qq)::value;
     const int wbase = threadIdx.x & ~63;
-    __builtin_amdgcn_global_load_lds(g.a_src[i] + min(x, nk - 1) * DK,
-                                     (lds_void*)(dma_abuf<Q>() + (i * kThreads + wbase) * 8), 16, 0, 0);
+    dq_dma16(dq_sbase(p.A + min(x, nk - 1) * DK), d.a_off[i],
+             dma_abuf<Q>() + (i * kThreads + wbase) * 8);
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
   using I3 = std::integral_constant<int, 3>;
 
-  // prologue: Bq(0), then groups G(-4) .. G(-2) = {A(0), Bq(1)}, {A(1), Bq(2)},
-  // {A(2), Bq(3)}
-  for (int i = 0; i < 3; ++i) dq_qload<0>(d, 0, i);
+  // prologue: Bq(0), Bq(1), then groups G(-4) .. G(-2) = {A(0), Bq(2)},
+  // {A(1), Bq(3)}, {A(2), Bq(4)}; slot of stage x = x % 5
+  auto slot_of = [](int x) { return (x % kDqSlots) * kDqSlot; };
+  for (int i = 0; i < 3; ++i) dq_qload(p, d, 0, slot_of(0), i);
+  for (int i = 0; i < 3; ++i) dq_qload(p, d, min(1, nk - 1), slot_of(1), i);
   for (int i = 0; i < 4; ++i) a_load(I0(), 0, i);
-  for (int i = 0; i < 3; ++i) dq_qload<1>(d, min(1, nk - 1), i);
+  for (int i = 0; i < 3; ++i) dq_qload(p, d, min(2, nk - 1), slot_of(2), i);
   for (int i = 0; i < 4; ++i) a_load(I1(), 1, i);
-  for (int i = 0; i < 3; ++i) dq_qload<2>(d, min(2, nk - 1), i);
+  for (int i = 0; i < 3; ++i) dq_qload(p, d, min(3, nk - 1), slot_of(3), i);
   for (int i = 0; i < 4; ++i) a_load(I2(), 2, i);
-  for (int i = 0; i < 3; ++i) dq_qload<3>(d, min(3, nk - 1), i);
-  __builtin_amdgcn_s_waitcnt(vmcnt_imm(14));  // Bq(0), A(0), Bq(1) landed
+  for (int i = 0; i < 3; ++i) dq_qload(p, d, min(4, nk - 1), slot_of(4), i);
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(14));  // Bq(0), Bq(1), G(-4) landed
   stage_barrier();
-  dq_decode_half(dq_qbuf<0>(), dq_bbuf<0>(), d, 0);  // stage 0 whole, stage 1 first half
-  dq_decode_half(dq_qbuf<0>(), dq_bbuf<0>(), d, 1);
-  dq_decode_half(dq_qbuf<1>(), dq_bbuf<1>(), d, 0);
+  dq_decode_half(slot_of(0), dq_bbuf<0>(), d, 0);  // stage 0 whole, stage 1 first half
+  dq_decode_half(slot_of(0), dq_bbuf<0>(), d, 1);
+  dq_decode_half(slot_of(1), dq_bbuf<1>(), d, 0);
+  DqDec dnext;  // bytes of the face row the next substep decodes
+  dq_read(slot_of(1), d, 1, dnext);
   __builtin_amdgcn_s_waitcnt(0xC07F);          // lgkmcnt(0): decode reads / writes done
-  __builtin_amdgcn_s_waitcnt(vmcnt_imm(14));  // (same groups as above)
   stage_barrier();
-  // G(-1) = {A(3), Bq(4)}: slot 0 is free now
+  // G(-1) = {A(3), Bq(5)}: slot 0 is free now
   for (int i = 0; i < 4; ++i) a_load(I3(), 3, i);
-  for (int i = 0; i < 3; ++i) dq_qload<0>(d, min(4, nk - 1), i);
+  for (int i = 0; i < 3; ++i) dq_qload(p, d, min(5, nk - 1), slot_of(5), i);
   DFrags f0, f1;
   dma_read_frags(dma_abuf<0>(), dq_bbuf<0>(), g, 0, lane, f0);
 
+  // Stage s.  The bytes a substep decodes were read at the end of the
+  // previous substep: the second half of stage s + 1's face rows (its slot
+  // visible since stage s - 2's barrier) and the first half of stage s + 2's
+  // (visible since stage s - 1's barrier: Bq(s + 2) is in G(s - 4), which
+  // that barrier's wait covers).  Those two reads may stay in flight across
+  // the barrier (lgkmcnt(2)); their slot is reloaded only after the next
+  // barrier, by which every wave has consumed them.
   auto stage = [&](auto qq, int s) {
-    constexpr int q = decltype(qq)::value;  // A buffer / Bq slot of stage s
+    constexpr int q = decltype(qq)::value;  // A buffer of stage s
     uint16_t* Ab = dma_abuf<q>();
     uint16_t* Bb = dq_bbuf<q & 1>();
     uint16_t* An = dma_abuf<(q + 1) & 3>();
     uint16_t* Bn = dq_bbuf<(q + 1) & 1>();
+    const int slot2 = slot_of(s + 2);  // Bq(s + 2)
     // substep 0: MFMAs on f0; this stage's substep-1 fragments; second half
-    // of stage s + 1's decode (slot (q + 1) & 3 -> B buffer (q + 1) & 1)
+    // of stage s + 1's decode into B buffer (q + 1) & 1; at the end, the
+    // bytes of stage s + 2's first half
     {
       DFragParts parts;
-      DqDec dec;
+      float fv[2];
 #pragma unroll
       for (int x = 0; x < 16; ++x) {
         dma_mfma_one(f0, acc, x);
         if (x < 12) dma_read_piece(Ab, Bb, g, 1, lane, parts, x);
-        dq_piece(dq_qbuf<(q + 1) & 3>(), Bn, d, 1, dec, x);
+        dq_piece_ready(Bn, d, 1, dnext, fv, x);
         __builtin_amdgcn_sched_barrier(0);
       }
+      dq_read(slot2, d, 0, dnext);
+      __builtin_amdgcn_sched_barrier(0);
       parts.to_frags(f1);
     }
-    __builtin_amdgcn_s_waitcnt(0xC07F);         // lgkmcnt(0): this wave's LDS reads / writes done
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(14));  // G(s - 3) landed: A(s + 1), Bq(s + 2)
+    __builtin_amdgcn_s_waitcnt(0xC27F);         // lgkmcnt(2): all but the two byte reads done
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(14));  // G(s - 3) landed: A(s + 1), Bq(s + 3)
     stage_barrier();
     // substep 1: MFMAs on f1; stage s + 1's substep-0 fragments; G(s) =
-    // {A(s + 4) -> A buffer q, Bq(s + 5) -> slot (q + 1) & 3}; first half of
-    // stage s + 2's decode (slot (q + 2) & 3 -> B buffer q & 1)
+    // {A(s + 4) -> A buffer q, Bq(s + 6) -> the slot of Bq(s + 1)}; first
+    // half of stage s + 2's decode into B buffer q & 1; at the end, the bytes
+    // of stage s + 2's second half
     {
       DFragParts nparts;
-      DqDec dec;
+      float fv[2];
+      const int slot6 = slot_of(s + 6);
 #pragma unroll
       for (int x = 0; x < 16; ++x) {
         dma_mfma_one(f1, acc, x);
         if (x < 12) dma_read_piece(An, Bn, g, 0, lane, nparts, x);
         if ((x & 1) && x < 8) a_load(qq, s + 4, x >> 1);
-        if ((x & 1) && x >= 9) dq_qload<(q + 1) & 3>(d, min(s + 5, nk - 1), (x - 9) >> 1);
-        dq_piece(dq_qbuf<(q + 2) & 3>(), Bb, d, 0, dec, x);
+        if ((x & 1) && x >= 9) dq_qload(p, d, min(s + 6, nk - 1), slot6, (x - 9) >> 1);
+        dq_piece_ready(Bb, d, 0, dnext, fv, x);
         __builtin_amdgcn_sched_barrier(0);
       }
+      dq_read(slot2, d, 1, dnext);
+      __builtin_amdgcn_sched_barrier(0);
       nparts.to_frags(f0);
     }
   };
@@ -1352,7 +1424,9 @@ bool launch_mm256(MmArgs a, hipStream_t s, int* status) {
   if constexpr (BQ) {
     // weights dequantised in LDS: whole 256-column blocks of whole stage
     // quads, tiles 16-byte aligned
-    if (a.N % LN == 0 && a.K % (4 * DK) == 0 && (reinterpret_cast<uintptr_t>(a.Bq) & 15) == 0) {
+    if (a.N % LN == 0 && a.K % (4 * DK) == 0 && (reinterpret_cast<uintptr_t>(a.Bq) & 15) == 0 &&
+        static_cast<int64_t>(a.M) * a.lda * 2 < (int64_t(1) << 31) &&
+        static_cast<int64_t>(a.K / 32) * (a.N / 32) * TTLH_BFP8_TILE_BYTES < (int64_t(1) << 31)) {
       hipLaunchKernelGGL((mm_dq_kernel<true, false>), dim3(a.grid_m * a.grid_n), dim3(kThreads), 0,
                          s, a);
       *status = check_launch("mm_dq_kernel");
