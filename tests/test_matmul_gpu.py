@@ -131,3 +131,32 @@ def test_bf16_large_block_kernel_accumulate_f32():
     got = _mm(a, b, torch.float32, accumulate=True, c0=c0).double()
     exact = O.matmul_fp64(a, b) + c0.double()
     torch.testing.assert_close(got, exact, rtol=1e-5, atol=1e-5)
+
+
+# Large problems whose 256x256 block count does not fill whole rounds of the
+# 256 CUs, some with N ragged against 256: every output tile is the same MFMA
+# sequence over k whatever the grid, so the result equals, bit for bit, the
+# same product with B padded by zero columns to a block count the CUs divide
+# evenly (and stays within the float64 bound).
+@pytest.mark.parametrize("M,N,K", [(4096, 5120, 256), (4096, 6144, 256), (2048, 11008, 256),
+                                   (4096, 11008, 128), (4096, 5216, 256)])
+def test_large_gemm_independent_of_padding(M, N, K):
+    print(f"padding invariance M={M} N={N} K={K}", flush=True)
+    from ttlhip import kernels as Kn
+    a, b = _inputs(M, K, N, 71)
+    # padded width: whole rounds of blocks (256 per round, M / 256 per column)
+    unit = 256 * 256 // (M // 256)
+    npad = -(-N // unit) * unit
+    bp = torch.zeros(K, npad, dtype=torch.bfloat16)
+    bp[:, :N] = b
+    c = torch.full((M, N), 3.0, dtype=torch.bfloat16, device="cuda")
+    cp = torch.empty((M, npad), dtype=torch.bfloat16, device="cuda")
+    Kn.matmul(a.cuda(), b.cuda(), c, accumulate=False)
+    Kn.matmul(a.cuda(), bp.cuda(), cp, accumulate=False)
+    torch.cuda.synchronize()
+    assert torch.equal(c.cpu().view(torch.int16), cp.cpu()[:, :N].view(torch.int16))
+    rows = torch.arange(0, M, 97)
+    exact = a[rows].double() @ b.double()
+    err = (c.cpu()[rows].double() - exact).abs()
+    bound = exact.abs() * 2.0 ** -8 + 1e-6 * math.sqrt(K) * float(exact.abs().max())
+    assert bool((err <= bound).all()), float(err.max())
