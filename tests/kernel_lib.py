@@ -1285,3 +1285,53 @@ def make_matmul_epilogue(ttl, bm, bk, bn, epi="relu_bias", grid=(2, 2)):
                     ttl.copy(ob, out[r * bm:(r + 1) * bm, col * bn:(col + 1) * bn]).wait()
 
     return matmul_epilogue
+
+
+def make_pipe_chain(ttl, n_blocks=2):
+    """y[j, c] = x_j + b[j, c] on a 1 x 3 grid, x_j = a[0, j] read by core 0
+    only: core 0 sends it to core 1 on one pipe, core 1 forwards the block it
+    received to core 2 on a second pipe (python/sim/copyhandlers.py:229: a
+    pipe send takes any block), and every core adds its own bias tile."""
+
+    @ttl.kernel(grid=(1, 3))
+    def pipe_chain(a, b, y):
+        x_cb = ttl.make_circular_buffer_like(a, shape=(1, 1), buffer_factor=2)
+        b_cb = ttl.make_circular_buffer_like(b, shape=(1, 1), buffer_factor=2)
+        y_cb = ttl.make_circular_buffer_like(y, shape=(1, 1), buffer_factor=2)
+        net01 = ttl.PipeNet([ttl.Pipe((0, 0), (0, 1))])
+        net12 = ttl.PipeNet([ttl.Pipe((0, 1), (0, 2))])
+
+        @ttl.compute()
+        def comp():
+            for _ in range(n_blocks):
+                with x_cb.wait() as xb, b_cb.wait() as bb, y_cb.reserve() as yb:
+                    yb.store(xb + bb)
+
+        @ttl.datamovement()
+        def reader():
+            c = ttl.core(dims=1)
+            for j in range(n_blocks):
+                with x_cb.reserve() as xb:
+                    if c == 0:
+                        ttl.copy(a[0, j], xb).wait()
+
+                    def recv(p):
+                        ttl.copy(p, xb).wait()
+
+                    def send(p):
+                        ttl.copy(xb, p).wait()
+                    net01.if_dst(recv)
+                    net01.if_src(send)
+                    net12.if_dst(recv)
+                    net12.if_src(send)
+                with b_cb.reserve() as bb:
+                    ttl.copy(b[j, c], bb).wait()
+
+        @ttl.datamovement()
+        def writer():
+            c = ttl.core(dims=1)
+            for j in range(n_blocks):
+                with y_cb.wait() as yb:
+                    ttl.copy(yb, y[j, c]).wait()
+
+    return pipe_chain

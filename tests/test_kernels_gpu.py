@@ -195,6 +195,18 @@ def test_row_bias_multicast_pipe_kernel_bitexact():
     assert torch.equal(got, a + bias)
 
 
+def test_forwarded_pipe_block_kernel_bitexact():
+    # core 1 forwards on a second pipe the block it received from core 0:
+    # core 2's launch reads the tile core 0 copied (closed form: one bf16 add)
+    a = O.seeded((32, 64), "uniform", 33)
+    b = O.seeded((64, 96), "uniform", 34)
+    got, k = _gpu(KL.make_pipe_chain, [a, b, torch.zeros(64, 96, dtype=torch.bfloat16)], 2)
+    want = torch.cat([torch.cat([a[:, 32 * j:32 * (j + 1)] + b[32 * j:32 * (j + 1),
+                                                               32 * c:32 * (c + 1)]
+                                 for c in range(3)], 1) for j in range(2)], 0)
+    assert torch.equal(got, want)
+
+
 def test_body_created_tensor_rebound_across_calls():
     # the kernel body expands c to a tile with ttnn ops; a second call with a
     # new c reuses the cached plan but must read the new expansion

@@ -126,3 +126,63 @@ def test_reference_pipe_examples_run_unmodified(name, monkeypatch):
     for m in list(sys.modules.values()):
         f = getattr(m, "__file__", None) or ""
         assert not f.startswith("/root/reference"), f"reference module imported: {f}"
+
+
+def _chain_case():
+    a = O.seeded((32, 64), "uniform", 11)
+    b = O.seeded((64, 96), "uniform", 12)
+    return [a, b, torch.zeros(64, 96, dtype=torch.bfloat16)]
+
+
+def test_forwarded_pipe_block_matches_closed_form():
+    # core 1 sends on a second pipe the block it received on the first: the
+    # plan gives core 2's reads the tile origin core 0 copied it from.  The
+    # oracle executor has no pipes; the result is pinned by its closed form
+    # (one bf16 add of known tiles, exact in fp32 then rounded once, which is
+    # torch's bf16 add)
+    tensors = _chain_case()
+    args = [ttnn.Tensor(t.clone()) for t in tensors]
+    plan = KL.make_pipe_chain(ttl).trace(*args)
+    plan_interp.run(plan, dict(enumerate(args)))
+    a, b, _ = tensors
+    want = torch.cat([torch.cat([a[:, 32 * j:32 * (j + 1)] + b[32 * j:32 * (j + 1),
+                                                               32 * c:32 * (c + 1)]
+                                 for c in range(3)], 1) for j in range(2)], 0)
+    assert torch.equal(args[2]._tensor, want)
+    # x_j = a tile (0, j) feeds output tile row j: one launch per row
+    assert len(plan.launches) == 2
+
+
+def test_pipes_forwarding_in_a_cycle_are_refused():
+    @ttl.kernel(grid=(1, 2))
+    def k(a, y):
+        x_cb = ttl.make_circular_buffer_like(a, shape=(1, 1), buffer_factor=2)
+        y_cb = ttl.make_circular_buffer_like(y, shape=(1, 1), buffer_factor=2)
+        n01 = ttl.PipeNet([ttl.Pipe((0, 0), (0, 1))])
+        n10 = ttl.PipeNet([ttl.Pipe((0, 1), (0, 0))])
+
+        @ttl.compute()
+        def comp():
+            with x_cb.wait() as xb, y_cb.reserve() as yb:
+                yb.store(xb)
+
+        @ttl.datamovement()
+        def reader():
+            with x_cb.reserve() as xb:
+                def recv(p):
+                    ttl.copy(p, xb).wait()
+
+                def send(p):
+                    ttl.copy(xb, p).wait()
+                n01.if_dst(recv)
+                n10.if_dst(recv)
+                n01.if_src(send)
+                n10.if_src(send)
+
+        @ttl.datamovement()
+        def writer():
+            with y_cb.wait() as yb:
+                ttl.copy(yb, y[0, ttl.core(dims=1)]).wait()
+
+    with pytest.raises((P.PlanError, RuntimeError), match="cycle|Deadlock"):
+        k.trace(ttnn.Tensor(torch.zeros(32, 64)), ttnn.Tensor(torch.zeros(32, 64)))

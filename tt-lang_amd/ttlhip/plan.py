@@ -427,37 +427,93 @@ def _tree_key(tree, leaf_ids: Dict[int, int]):
     return (tag,) + tuple(_tree_key(t, leaf_ids) for t in tree[1:])
 
 
-def _no_forwarding(ev: T.Event):
-    raise PlanError("a block received from one pipe and sent on another is not supported")
-
-
 def _pipe_instances(ev: T.Event) -> int:
     return int(np.prod(ev.domain_shape())) if ev.domain_shape() else 1
 
 
-def _pipe_sends(core_traces, per_core) -> Dict[int, List[Tuple[Any, np.ndarray, np.ndarray]]]:
+class _PipeSends:
     """pipe id -> origins of the blocks its source core sends, in send order:
-    one (tensor, r0, c0) per send event (arrays over the event's instances).
-    A sent block must have been filled from a tensor on the source core."""
-    sends: Dict[int, List] = {}
-    src_of: Dict[int, int] = {}
-    for ct, (events, fill_direct) in zip(core_traces, per_core):
+    one (tensor, r0, c0) per send event (arrays over the event's instances),
+    resolved on demand.  A sent block is filled by ttl.copy from a tensor on
+    the source core, or received there from another pipe and forwarded (the
+    simulator's BlockToPipeHandler takes any block, python/sim/
+    copyhandlers.py:229): its origin is then that pipe's matching send,
+    resolved the same way; pipes that forward to each other in a cycle never
+    deliver a first block (the simulator deadlocks) and are refused."""
+
+    def __init__(self, core_traces, pre) -> None:
+        self.cores, self.pre = core_traces, pre
+        self.src: Dict[int, int] = {}
+        for ci, (ct, (events, _)) in enumerate(zip(core_traces, pre)):
+            for tmpl, _ in ct["threads"]:
+                for ev in events[id(tmpl)]:
+                    if ev.kind != "pipe_send":
+                        continue
+                    pipe = ev.data["pipe"]
+                    if self.src.setdefault(pipe.id, ci) != ci:
+                        raise PlanError(f"{pipe} is sent on from two cores")
+        self.memo: Dict[int, List[Tuple[Any, np.ndarray, np.ndarray]]] = {}
+        self.busy: set = set()
+
+    def receiver(self, core: int):
+        """The `received` resolver of core `core`: its k-th receive on a pipe
+        takes the origin of that pipe's k-th send."""
+        pos: Dict[int, int] = {}
+
+        def received(ev):
+            pipe = ev.data["pipe"]
+            k = pos.get(pipe.id, 0)
+            pos[pipe.id] = k + 1
+            lst = self.get(pipe.id)
+            if k >= len(lst):
+                raise RuntimeError(f"Deadlock: core {core} receives more blocks on {pipe} than its "
+                                   "source core sends")
+            tens, r0, c0 = lst[k]
+            n = _pipe_instances(ev)
+            if r0.size != n:
+                raise PlanError(f"{pipe}: a receive and the matching send run a different number "
+                                "of times")
+            return tens, r0, c0
+        return received
+
+    def get(self, pid: int) -> List[Tuple[Any, np.ndarray, np.ndarray]]:
+        if pid in self.memo:
+            return self.memo[pid]
+        if pid not in self.src:
+            return []
+        if pid in self.busy:
+            raise PlanError("pipes forward blocks to each other in a cycle (the simulator "
+                            "deadlocks: no block is ever delivered)")
+        self.busy.add(pid)
+        ci = self.src[pid]
+        ct, (events, totals) = self.cores[ci], self.pre[ci]
+        received = self.receiver(ct["core"])
+        out = []
         for tmpl, _ in ct["threads"]:
-            for ev in events[id(tmpl)]:
-                if ev.kind != "pipe_send":
+            if tmpl.kind != "dm":
+                continue
+            evs = events[id(tmpl)]
+            tables: Dict[int, _CopyTable] = {}
+            for ev in evs:
+                if ev.kind != "pipe_send" or ev.data["pipe"].id != pid:
                     continue
-                pipe = ev.data["pipe"]
-                if src_of.setdefault(pipe.id, ct["core"]) != ct["core"]:
-                    raise PlanError(f"{pipe} is sent on from two cores")
                 blk = ev.data["block"]
-                ft = fill_direct.get(blk.cb.id)
-                if ft is None:
-                    raise PlanError("a block sent on a pipe must be filled by ttl.copy from a "
-                                    "tensor on the sending core")
+                cb = blk.cb
+                if cb.id not in tables:
+                    n = totals[id(tmpl)].get((cb.id, "reserve"), 0)
+                    try:
+                        tables[cb.id] = _copy_table(evs, cb, n, "copy_in", received)
+                    except PlanError as err:
+                        raise PlanError("a block sent on a pipe must be filled by ttl.copy from a "
+                                        "tensor on the sending core, or received there from "
+                                        f"another pipe ({err})") from None
+                ft = tables[cb.id]
                 shape = ev.domain_shape()
                 idx = T.broadcast_to_domain(blk.event.index, shape).ravel()
-                sends.setdefault(pipe.id, []).append((ft.tensor, ft.r0[idx], ft.c0[idx]))
-    return sends
+                out.append((ft.tensor, ft.r0[idx], ft.c0[idx]))
+        self.busy.discard(pid)
+        self.memo[pid] = out
+        return out
 
 
 _SIM_OP_LIMIT = 2_000_000  # operations replayed per core by the deadlock report
@@ -550,45 +606,21 @@ def resolve(core_traces: List[Dict[str, Any]]) -> List[_Group]:
     """core_traces[c] = {"threads": [(template, root_node), ...]} for core c."""
     groups: Dict[Tuple, _Group] = {}
     hoisted: Dict[Tuple, Tuple[Any, Any]] = {}
-    # pass 1: events and tensor-filled copy tables of every core, for pipe sends
+    # pass 1: events of every core; the blocks each pipe carries are resolved
+    # on demand (a forwarded block through the pipe it was received from)
     pre = []
     for ct in core_traces:
         threads = ct["threads"]
         events = {id(tmpl): _thread_events(root) for tmpl, root in threads}
         totals = {id(tmpl): T.assign_indices(root) for tmpl, root in threads}
-        direct: Dict[int, _CopyTable] = {}
-        for tmpl, _ in threads:
-            if tmpl.kind != "dm":
-                continue
-            evs = events[id(tmpl)]
-            if not any(e.kind == "pipe_send" for e in evs):
-                continue
-            for cb in {id(e.cb): e.cb for e in evs if e.kind == "copy_in"}.values():
-                n = totals[id(tmpl)].get((cb.id, "reserve"), 0)
-                direct[cb.id] = _copy_table(evs, cb, n, "copy_in", received=_no_forwarding)
-        pre.append((events, direct, totals))
-    sends = _pipe_sends(core_traces, [(e, d) for e, d, _ in pre])
+        pre.append((events, totals))
+    sends = _PipeSends(core_traces, pre)
     scratch: Dict[int, _Scratch] = {}
 
-    for ct, (events, _, totals) in zip(core_traces, pre):
+    for ct, (events, totals) in zip(core_traces, pre):
         threads = ct["threads"]
         # k-th receive of a pipe on this core <-> k-th send of that pipe
-        recv_pos: Dict[int, int] = {}
-
-        def received(ev, _pos=recv_pos, _core=ct["core"]):
-            pipe = ev.data["pipe"]
-            k = _pos.get(pipe.id, 0)
-            _pos[pipe.id] = k + 1
-            lst = sends.get(pipe.id, [])
-            if k >= len(lst):
-                raise RuntimeError(f"Deadlock: core {_core} receives more blocks on {pipe} than its "
-                                   "source core sends")
-            tens, r0, c0 = lst[k]
-            n = _pipe_instances(ev)
-            if r0.size != n:
-                raise PlanError(f"{pipe}: a receive and the matching send run a different number "
-                                "of times")
-            return tens, r0, c0
+        received = sends.receiver(ct["core"])
         # producer / consumer of every CB on this core
         producers: Dict[int, Any] = {}
         consumers: Dict[int, Any] = {}
