@@ -1335,3 +1335,113 @@ def make_pipe_chain(ttl, n_blocks=2):
                     ttl.copy(yb, y[j, c]).wait()
 
     return pipe_chain
+
+
+def make_softmax_one_store(ttl, gc=4, grid=(2, 2), form="softmax"):
+    """Row softmax of x (rows of gc tiles, one block per row band) written as
+    ONE store whose expression holds the reductions (the spec's reduce_max /
+    reduce_sum are BlockExpr -> BlockExpr, TTLangSpecification.md:754-755):
+      m = broadcast(reduce_max(x, s, dims=[1]), out, dims=[1])
+      e = exp(x - m)
+      y = e * broadcast(recip(reduce_sum(e, s, dims=[1])), out, dims=[1])
+    form "center": y = x - broadcast(reduce_sum(x, s, dims=[1]), out, dims=[1]) * (1 / W)
+    (a row mean subtracted)."""
+
+    @ttl.kernel(grid=grid)
+    def softmax_one_store(x, s, y):
+        gx, gy = ttl.grid_size(dims=2)
+        rows_per_core = x.shape[0] // TILE // (gx * gy)
+        width = x.shape[1]
+        x_cb = ttl.make_circular_buffer_like(x, shape=(1, gc), buffer_factor=2)
+        s_cb = ttl.make_circular_buffer_like(s, shape=(1, 1), buffer_factor=1)
+        y_cb = ttl.make_circular_buffer_like(y, shape=(1, gc), buffer_factor=2)
+
+        @ttl.compute()
+        def comp():
+            with s_cb.wait() as sb:
+                for _ in range(rows_per_core):
+                    with x_cb.wait() as xb, y_cb.reserve() as yb:
+                        if form == "softmax":
+                            m = ttl.math.broadcast(ttl.math.reduce_max(xb, sb, dims=[1]), yb,
+                                                   dims=[1])
+                            e = ttl.math.exp(xb - m)
+                            r = ttl.math.recip(ttl.math.reduce_sum(e, sb, dims=[1]))
+                            yb.store(e * ttl.math.broadcast(r, yb, dims=[1]))
+                        else:
+                            tot = ttl.math.broadcast(ttl.math.reduce_sum(xb, sb, dims=[1]), yb,
+                                                     dims=[1])
+                            yb.store(xb - tot * (1.0 / width))
+
+        @ttl.datamovement()
+        def reader():
+            c = ttl.core(dims=1)
+            with s_cb.reserve() as sb:
+                ttl.copy(s[0, 0], sb).wait()
+            for i in range(rows_per_core):
+                r = c * rows_per_core + i
+                with x_cb.reserve() as xb:
+                    ttl.copy(x[r, 0:gc], xb).wait()
+
+        @ttl.datamovement()
+        def writer():
+            c = ttl.core(dims=1)
+            for i in range(rows_per_core):
+                r = c * rows_per_core + i
+                with y_cb.wait() as yb:
+                    ttl.copy(yb, y[r, 0:gc]).wait()
+
+    return softmax_one_store
+
+
+def make_matmul_computed_operand(ttl, bm=2, bk=2, bn=2, grid=(2, 2), form="scale"):
+    """out = f(a) @ g(b) per (bm, bn) output block over the whole K = bk
+    tiles (the spec's block matmul of computed BlockExprs,
+    TTLangSpecification.md:693): form "scale" (a * 0.25) @ b, "relu_b"
+    a @ relu(b) + c... with c = a bias block of the output's shape,
+    "both" (a + a) @ (b * 2) (every a block is read by several output
+    blocks, so the same operand tile is computed more than once)."""
+
+    @ttl.kernel(grid=grid)
+    def matmul_computed(a, b, c, out):
+        gx, gy = ttl.grid_size(dims=2)
+        rows = a.shape[0] // (bm * TILE)
+        cols = b.shape[1] // (bn * TILE)
+        per_core = rows * cols // (gx * gy)
+        a_cb = ttl.make_circular_buffer_like(a, shape=(bm, bk), buffer_factor=2)
+        b_cb = ttl.make_circular_buffer_like(b, shape=(bk, bn), buffer_factor=2)
+        c_cb = ttl.make_circular_buffer_like(c, shape=(bm, bn), buffer_factor=2)
+        o_cb = ttl.make_circular_buffer_like(out, shape=(bm, bn), buffer_factor=2)
+
+        @ttl.compute()
+        def comp():
+            for _ in range(per_core):
+                with a_cb.wait() as ab, b_cb.wait() as bb, c_cb.wait() as cc, \
+                        o_cb.reserve() as ob:
+                    if form == "scale":
+                        ob.store((ab * 0.25) @ bb)
+                    elif form == "relu_b":
+                        ob.store(ab @ ttl.math.relu(bb) + cc)
+                    else:
+                        ob.store((ab + ab) @ (bb * 2.0))
+
+        @ttl.datamovement()
+        def reader():
+            cx, cy = ttl.core(dims=2)
+            first = (cx * gy + cy) * per_core
+            for t in range(per_core):
+                r, col = (first + t) // cols, (first + t) % cols
+                with a_cb.reserve() as ab, b_cb.reserve() as bb, c_cb.reserve() as cc:
+                    ttl.copy(a[r * bm:(r + 1) * bm, 0:bk], ab).wait()
+                    ttl.copy(b[0:bk, col * bn:(col + 1) * bn], bb).wait()
+                    ttl.copy(c[r * bm:(r + 1) * bm, col * bn:(col + 1) * bn], cc).wait()
+
+        @ttl.datamovement()
+        def writer():
+            cx, cy = ttl.core(dims=2)
+            first = (cx * gy + cy) * per_core
+            for t in range(per_core):
+                r, col = (first + t) // cols, (first + t) % cols
+                with o_cb.wait() as ob:
+                    ttl.copy(ob, out[r * bm:(r + 1) * bm, col * bn:(col + 1) * bn]).wait()
+
+    return matmul_computed

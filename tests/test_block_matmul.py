@@ -58,7 +58,9 @@ def test_block_matmul_oracle_and_drop_in(bm, bk, bn, R, C):
     assert int(O.bf16_ulp_diff(got, orc).abs().max()) <= 1
 
 
-def test_block_matmul_of_a_computed_block_is_refused():
+def test_block_matmul_of_a_computed_block_matches_oracle():
+    # (a * 2) @ b: the operand is materialised in bf16 first, as the
+    # simulator does; exact here (a * 2 is exact in bf16, one product rounding)
     @ttl.kernel(grid=(1, 1))
     def bad(a, b, out):
         a_cb = ttl.make_circular_buffer_like(a, shape=(1, 3), buffer_factor=2)
@@ -81,8 +83,10 @@ def test_block_matmul_of_a_computed_block_is_refused():
             with o_cb.wait() as ob:
                 ttl.copy(ob, out[0:1, 0:2]).wait()
 
-    args = [ttnn.Tensor(torch.zeros(32, 96, dtype=torch.bfloat16)),
-            ttnn.Tensor(torch.zeros(96, 64, dtype=torch.bfloat16)),
-            ttnn.Tensor(torch.zeros(32, 64, dtype=torch.bfloat16))]
-    with pytest.raises(NotImplementedError, match="block matmul of computed"):
-        bad.trace(*args)
+    a = O.seeded((32, 96), "normal", 81)
+    b = O.seeded((96, 64), "normal", 82)
+    args = [ttnn.Tensor(a), ttnn.Tensor(b), ttnn.Tensor(torch.zeros(32, 64, dtype=torch.bfloat16))]
+    plan = bad.trace(*args)
+    plan_interp.run(plan, dict(enumerate(args)))
+    exact = ((a.double() * 2.0) @ b.double()).to(torch.bfloat16)
+    assert torch.equal(args[2]._tensor, exact)

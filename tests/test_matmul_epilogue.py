@@ -197,9 +197,15 @@ def test_two_products_in_one_expression_and_an_offset_product():
 
 @pytest.mark.parametrize("body,msg", [
     (lambda ob, ab, bb, cc: ob.store(ab @ bb + cc, acc=True), "acc=True"),
-    # refused while tracing (a PlanError is a NotImplementedError)
-    (lambda ob, ab, bb, cc: ob.store((ab * 2.0) @ bb + cc), "computed or broadcast blocks"),
 ])
 def test_unsupported_forms_are_refused(body, msg):
     with pytest.raises(NotImplementedError, match=msg):
         _trace(body)
+
+
+def test_computed_operand_plans_the_operand_first():
+    # (a * 2) @ b + c: the operand is materialised in bf16 first (an
+    # elementwise launch into a tensor laid out like a), then the product,
+    # then the epilogue (tests/test_expr_forms.py checks the values)
+    plan = _trace(lambda ob, ab, bb, cc: ob.store((ab * 2.0) @ bb + cc))
+    assert [type(l) for l in plan.launches] == [P.EltwiseLaunch, P.MatmulLaunch, P.EltwiseLaunch]

@@ -196,14 +196,19 @@ def _one_block_kernel(body):
     (lambda ob, xb, sb: ob.store(ttl.math.reduce_sum(xb, sb, dims=[2])), ValueError, "dims must"),
     (lambda ob, xb, sb: ob.store(ttl.math.reduce_sum(xb, xb, dims=[1])), ValueError,
      "scaler must be a \\(1, 1\\) block"),
-    (lambda ob, xb, sb: ob.store(ttl.math.reduce_sum(xb, sb, dims=[1]) * 2.0),
-     NotImplementedError, "inside a larger expression"),
     (lambda ob, xb, sb: ob.store(ttl.math.reduce_max(xb, sb, dims=[0])), ValueError,
      "must have the reduced shape"),
 ])
 def test_reduce_validation(body, exc, msg):
     with pytest.raises(exc, match=msg):
         _one_block_kernel(body)
+
+
+def test_reduction_inside_a_larger_expression_plans_it_first():
+    # reduce_sum(...) * 2: the reduction into a plan-owned tensor, then the
+    # scale reading it (tests/test_expr_forms.py checks values end to end)
+    plan = _one_block_kernel(lambda ob, xb, sb: ob.store(ttl.math.reduce_sum(xb, sb, dims=[1]) * 2.0))
+    assert [type(l) for l in plan.launches] == [P.ReduceLaunch, P.EltwiseLaunch]
 
 
 def test_reduce_max_accumulated_over_stores_is_rejected():

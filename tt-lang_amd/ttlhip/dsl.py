@@ -331,12 +331,36 @@ def _as_bexpr(x) -> BExpr:
     raise TypeError(f"expected a block or block expression, got {type(x).__name__}")
 
 
-def _check_not_reduced(e: BExpr) -> None:
+class _SubCB:
+    """Stand-in CB of a sub-expression leaf: its dtype and a name."""
+
+    __slots__ = ("dtype", "id", "name")
+
+    def __init__(self, dtype) -> None:
+        self.dtype, self.id, self.name = dtype, None, "(reduction)"
+
+
+class SubExpr:
+    """A reduction used as an operand of a larger expression (the spec types
+    reduce_sum / reduce_max BlockExpr -> BlockExpr, TTLangSpecification.md:
+    754-755): a leaf of the enclosing tree whose block is this object.  The
+    planner computes it into a plan-owned tensor first, as the simulator
+    materialises every intermediate value of an expression in its dtype, and
+    the enclosing program reads it there like any operand."""
+
+    __slots__ = ("expr", "cb")
+
+    def __init__(self, e: "BExpr") -> None:
+        self.expr = e
+        self.cb = _SubCB(e.dtype)
+
+
+def _lift(e: BExpr) -> BExpr:
+    """A reduction about to become an operand: a leaf over its own block."""
     if e.tree[0] == "reduce":
-        raise NotImplementedError(
-            "using the result of ttl.math.reduce_sum / reduce_max inside a larger expression is "
-            "not supported by the MI355X backend: store() the reduction on its own and copy it "
-            "to a tensor")
+        r, c = e.shape
+        return BExpr(e.shape, ("leaf", SubExpr(e), np.arange(r), np.arange(c)), e.dtype)
+    return e
 
 
 def _remap(tree, axis: int, new_len: int):
@@ -397,12 +421,10 @@ def _is_block_matmul(sa, sb) -> bool:
 def _block_matmul(aa: "BExpr", bb: "BExpr") -> "BExpr":
     """Output tile (i, j) = sum over k of a(i, k) @ b(k, j), accumulated in
     fp32 and rounded once (as a store(acc=True) loop of tile matmuls over k
-    runs on the MI355X)."""
-    for x in (aa, bb):
-        if x.tree[0] != "leaf" or any(leaf_rep(x.tree)):
-            raise NotImplementedError("a block matmul of computed or broadcast blocks is not "
-                                      "supported by the MI355X backend; store the operand into a "
-                                      "CB first")
+    runs on the MI355X).  Operands may be computed block expressions
+    (the spec types __matmul__(self, other: BlockExpr), TTLangSpecification.md:
+    693); the planner materialises such an operand in its dtype first, as the
+    simulator does (python/sim/block.py:1012-1013 pairs any blocks)."""
     K = aa.shape[1]
     return BExpr((aa.shape[0], bb.shape[1]), ("bmatmul", aa.tree, bb.tree, K),
                  torch.promote_types(aa.dtype, bb.dtype))
@@ -410,16 +432,12 @@ def _block_matmul(aa: "BExpr", bb: "BExpr") -> "BExpr":
 
 def _binary(op: str, a, b) -> BExpr:
     if isinstance(a, (int, float)) and not isinstance(a, bool):
-        bb = _as_bexpr(b)
-        _check_not_reduced(bb)
+        bb = _lift(_as_bexpr(b))
         return BExpr(bb.shape, (op, ("const", float(a)), bb.tree), bb.dtype)
     if isinstance(b, (int, float)) and not isinstance(b, bool):
-        aa = _as_bexpr(a)
-        _check_not_reduced(aa)
+        aa = _lift(_as_bexpr(a))
         return BExpr(aa.shape, (op, aa.tree, ("const", float(b))), aa.dtype)
-    aa, bb = _as_bexpr(a), _as_bexpr(b)
-    _check_not_reduced(aa)
-    _check_not_reduced(bb)
+    aa, bb = _lift(_as_bexpr(a)), _lift(_as_bexpr(b))
     sa, sb = aa.shape, bb.shape
     if op == "matmul" and _is_block_matmul(sa, sb):
         return _block_matmul(aa, bb)
@@ -443,16 +461,14 @@ def _binary(op: str, a, b) -> BExpr:
 
 
 def _unary(op: str, a, imm: Optional[float] = None) -> BExpr:
-    aa = _as_bexpr(a)
-    _check_not_reduced(aa)
+    aa = _lift(_as_bexpr(a))
     return BExpr(aa.shape, (op, aa.tree), aa.dtype)
 
 
 def _unary_param(op: str, a, p0: float, p1: float = 0.0) -> BExpr:
     """A unary op with numeric parameters (the spec types them PositiveInt;
     their numeric value is used)."""
-    aa = _as_bexpr(a)
-    _check_not_reduced(aa)
+    aa = _lift(_as_bexpr(a))
     return BExpr(aa.shape, ("upar", aa.tree, op, float(p0), float(p1)), aa.dtype)
 
 
@@ -472,8 +488,7 @@ def _reduce(kind: str, x, scaler, dims) -> BExpr:
     dl = [int(d) for d in dims]
     if not dl or len(set(dl)) != len(dl) or any(d not in (0, 1) for d in dl):
         raise ValueError(f"reduce_{kind}() dims must be [0], [1] or [0, 1], got {list(dims)}")
-    e = _as_bexpr(x)
-    _check_not_reduced(e)
+    e = _lift(_as_bexpr(x))
     if isinstance(scaler, (int, float)) and not isinstance(scaler, bool):
         st = ("const", float(scaler))
     else:
@@ -848,6 +863,7 @@ class _Math:
                     raise ValueError(f"Cannot broadcast along dimension {d}: dimension must have "
                                      f"size 1, but has size {e.shape[d]}")
             return e
+        e = _lift(e)
         target = tuple(out.shape)
         shape, tree = list(e.shape), e.tree
         for d in dims:

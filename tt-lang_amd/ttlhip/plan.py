@@ -35,6 +35,7 @@ from typing import Any, Dict, List, Optional, Sequence, Tuple
 import numpy as np
 import torch
 
+from . import dsl as D
 from . import expr as X
 from . import trace as T
 
@@ -379,6 +380,9 @@ class _Group:
     # build_plan when no other store site writes an operand of this one or
     # reads its output, so no value changes between the repeats
     dedupe_ok: bool = True
+    # the output is a tensor the plan owns for this site alone (a hoisted
+    # matmul operand), read only by the consuming matmul
+    private_out: bool = False
 
 
 def _leaf_rep(leaf) -> Tuple[bool, bool]:
@@ -676,6 +680,9 @@ def resolve(core_traces: List[Dict[str, Any]]) -> List[_Group]:
                 rout = T.broadcast_to_domain(target.event.index, shape).ravel()
                 dt = drain[cid]
                 R, C = target.shape
+                site = (ev.data.get("loc"), _tree_key(e.tree, {}), id(dt.tensor))
+                e = _hoist_subexprs(ev, e, target, rout, dt, fill, shape, groups, hoisted, site)
+                e = _hoist_operands(ev, e, fill, shape, groups, hoisted, site)
                 if e.tree[0] == "reduce":
                     _resolve_reduce(ev, e, target, rout, dt, fill, shape, groups)
                     continue
@@ -820,6 +827,167 @@ def _hoist_matmuls(ev, e, target, rout, dt, fill, shape, groups, hoisted):
         if tag == "reduce":
             raise PlanError("a reduction combined with a tile matmul in one store() is not "
                             "supported")
+        return (tag,) + tuple(walk(t) for t in tree[1:])
+
+    return _Expr(walk(e.tree), e.shape, e.dtype)
+
+
+def _is_sub(leaf) -> bool:
+    return leaf[0] == "leaf" and isinstance(leaf[1], D.SubExpr)
+
+
+def _tree_dtype(tree):
+    """dtype of an elementwise tree: its leaves' dtypes promoted (numbers do
+    not promote a block, as in torch)."""
+    dt = None
+    for lf in _tree_leaves(tree, []):
+        d = lf[1].cb.dtype
+        dt = d if dt is None else torch.promote_types(dt, d)
+    return dt
+
+
+class _SubTarget:
+    """The block a hoisted sub-expression is stored into: the store's target
+    block's instances, the sub-expression's block shape."""
+
+    def __init__(self, shape, event) -> None:
+        self.shape, self.event = tuple(shape), event
+
+
+def _hoist_subexprs(ev, e, target, rout, dt, fill, shape, groups, hoisted, site, done=None):
+    """Leaves whose block is a sub-expression (a reduction used as an operand,
+    dsl.SubExpr): the reduction is planned first into a plan-owned tensor laid
+    out like the output, its result tile (i, j) at the target block's tile
+    (i, j) (a reduced block is never larger than the expression it feeds),
+    and the leaf reads that tensor with the leaf's own maps and in-tile
+    broadcast.  Nested sub-expressions are hoisted first; one sub-expression
+    used at several places (x - m and a reduction of exp(x - m)) is computed
+    once."""
+    count = [0]
+    done = {} if done is None else done  # id(SubExpr) -> its hoisted block
+
+    def walk(tree):
+        tag = tree[0]
+        if tag == "leaf":
+            if not _is_sub(tree):
+                return tree
+            if id(tree[1]) in done:
+                return ("leaf", done[id(tree[1])]) + tuple(tree[2:])
+            sub = tree[1].expr
+            node = count[0]
+            count[0] += 1
+            inner = _hoist_subexprs(ev, sub, target, rout, dt, fill, shape, groups, hoisted,
+                                    site + (("sub", node),), done)
+            if inner.tree[0] != "reduce":
+                raise PlanError("only reductions are computed ahead of the expression using them")
+            Rr, Cr = inner.shape
+            R, C = target.shape
+            if Rr > R or Cr > C:
+                raise PlanError(f"a reduction of block shape {(Rr, Cr)} inside a store into a "
+                                f"block of shape {(R, C)}")
+            key = site + ("sub", node)
+            if key not in hoisted:
+                cb = _HoistedCB(-1 - len(hoisted), inner.dtype, "(reduction)")
+                hoisted[key] = (_Temp(tuple(dt.tensor.shape), inner.dtype), cb)
+            temp, cb = hoisted[key]
+            tab = _CopyTable(temp, dt.r0, dt.c0)
+            _resolve_reduce(ev, inner, _SubTarget((Rr, Cr), target.event), rout, tab, fill, shape,
+                            groups)
+            fill[cb.id] = tab
+            done[id(tree[1])] = _HoistedBlock(cb, target.event)
+            return ("leaf", done[id(tree[1])]) + tuple(tree[2:])
+        if tag == "const":
+            return tree
+        if tag in ("powi", "upar"):
+            return (tag, walk(tree[1])) + tuple(tree[2:])
+        if tag == "reduce":
+            _, kind, dims, inner, ishape, scaler = tree
+            return ("reduce", kind, dims, walk(inner), ishape, walk(scaler))
+        if tag == "bmatmul":
+            return ("bmatmul", walk(tree[1]), walk(tree[2]), tree[3])
+        return (tag,) + tuple(walk(t) for t in tree[1:])
+
+    return _Expr(walk(e.tree), e.shape, e.dtype)
+
+
+def _hoist_operands(ev, e, fill, shape, groups, hoisted, site):
+    """Tile or block matmuls whose operand is a computed block expression,
+    e.g. (a * s) @ b (the spec types __matmul__(self, other: BlockExpr),
+    TTLangSpecification.md:693; the simulator pairs any blocks,
+    python/sim/block.py:1012-1013, after materialising the operand in its
+    dtype): the operand is planned first as an elementwise store into a
+    plan-owned tensor laid out like one of its leaves (the anchor: a leaf
+    whose maps take every slot of the operand to a distinct tile), each
+    operand tile at its anchor tile, and the matmul reads that tensor where it
+    would have read the anchor.  Two instances that need different values in
+    one anchor tile make that store write a tile twice, which is refused."""
+    count = [0]
+
+    def hoist(t):
+        node = count[0]
+        count[0] += 1
+        if t[0] == "leaf" and not any(_leaf_rep(t)):
+            return t
+        leaves = _tree_leaves(t, [])
+        anchor = None
+        for lf in leaves:
+            rm, cm = np.asarray(lf[2]), np.asarray(lf[3])
+            if (lf[1].cb.id in fill and len(set(rm.tolist())) == rm.size
+                    and len(set(cm.tolist())) == cm.size):
+                anchor = lf
+                break
+        if anchor is None:
+            raise PlanError("a tile matmul operand computed from blocks none of which covers the "
+                            "operand tile for tile (all broadcast or not filled from a tensor)")
+        for lf in leaves:
+            if lf[1].cb.id not in fill:
+                raise PlanError("expression operands must come from blocks filled by ttl.copy from "
+                                "a tensor")
+        Ro, Co = len(anchor[2]), len(anchor[3])
+        slot = np.arange(Ro * Co)
+        oi, oj = slot // Co, slot % Co
+        fa = fill[anchor[1].cb.id]
+        wa = T.broadcast_to_domain(anchor[1].event.index, shape).ravel()
+        out_r = (fa.r0[wa][:, None] + np.asarray(anchor[2])[oi][None, :]).ravel()
+        out_c = (fa.c0[wa][:, None] + np.asarray(anchor[3])[oj][None, :]).ravel()
+        leaf_rc, leaf_tensors = [], []
+        for lf in leaves:
+            ft = fill[lf[1].cb.id]
+            w = T.broadcast_to_domain(lf[1].event.index, shape).ravel()
+            lr = (ft.r0[w][:, None] + np.asarray(lf[2])[oi][None, :]).ravel()
+            lc = (ft.c0[w][:, None] + np.asarray(lf[3])[oj][None, :]).ravel()
+            leaf_rc.append(np.stack([lr, lc], 1))
+            leaf_tensors.append(ft.tensor)
+        dtype = _tree_dtype(t)
+        key = site + ("operand", node)
+        if key not in hoisted:
+            cb = _HoistedCB(-1 - len(hoisted), dtype, "(matmul operand)")
+            hoisted[key] = (_Temp(tuple(fa.tensor.shape), dtype), cb)
+        temp, cb = hoisted[key]
+        gkey = (_tree_key(t, {}), tuple(id(x) for x in leaf_tensors), id(temp), False)
+        g = groups.get(gkey)
+        if g is None:
+            g = groups[gkey] = _Group(t, leaves, leaf_tensors, temp, False, dtype,
+                                      ev.data.get("loc"), private_out=True)
+        g.out_rc.append(np.stack([out_r, out_c], 1))
+        g.leaf_rc.append(leaf_rc)
+        g.order.append(np.repeat(np.arange(wa.size), Ro * Co))
+        fill[cb.id] = _CopyTable(temp, fa.r0, fa.c0)
+        return ("leaf", _HoistedBlock(cb, anchor[1].event), anchor[2], anchor[3])
+
+    def walk(tree):
+        tag = tree[0]
+        if tag in ("leaf", "const"):
+            return tree
+        if tag == "matmul":
+            return ("matmul", hoist(walk(tree[1])), hoist(walk(tree[2])))
+        if tag == "bmatmul":
+            return ("bmatmul", hoist(walk(tree[1])), hoist(walk(tree[2])), tree[3])
+        if tag in ("powi", "upar"):
+            return (tag, walk(tree[1])) + tuple(tree[2:])
+        if tag == "reduce":
+            _, kind, dims, inner, ishape, scaler = tree
+            return ("reduce", kind, dims, walk(inner), ishape, scaler)
         return (tag,) + tuple(walk(t) for t in tree[1:])
 
     return _Expr(walk(e.tree), e.shape, e.dtype)
@@ -1394,22 +1562,56 @@ def _fuse_attention(groups: List[_Group], tensor_ref) -> List[Any]:
     return out
 
 
+def _tile_codes(rcs: List[np.ndarray]) -> np.ndarray:
+    """Sorted unique tile coordinates of (N, 2) arrays, one int64 each."""
+    if not rcs:
+        return np.zeros(0, dtype=np.int64)
+    a = np.concatenate(rcs, 0).astype(np.int64)
+    return np.unique(a[:, 0] * (1 << 32) + a[:, 1])
+
+
 def _mark_dedupe(groups: List[_Group]) -> None:
     """Repeats of a store site are one launch only when nothing else touches
-    its tensors in between.  Store sites run one launch each in trace order,
-    so if another site writes one of this site's operands, or reads its
-    output, the simulator's interleaving of the repeats with that site
-    matters (loop { out = x + 1; x = y * 2 } writes out from two values of x)
-    and the repeated writes are refused instead of merged."""
+    their tiles in between.  Store sites run one launch each in trace order,
+    so the repeats of a site are merged (g.dedupe_ok) only if no other site
+    writes a tile they read (loop { out = x + 1; x = y * 2 } computes out
+    from two values of x), writes a tile they write (the last writer would
+    change), or reads a tile they write (unless the output is a tensor the
+    plan owns for this site alone, read back by its consumer at the tiles
+    each repeat wrote: a hoisted matmul operand)."""
     for g in groups:
-        reads = [t for t in g.leaf_tensors] + ([g.scaler_tensor] if g.scaler_tensor is not None else [])
         g.dedupe_ok = True
+    rep = [g for g in groups if sum(x.shape[0] for x in g.out_rc) >
+           _tile_codes(g.out_rc).size]
+    if not rep:
+        return
+
+    def reads(h: _Group) -> Dict[int, List[np.ndarray]]:
+        r: Dict[int, List[np.ndarray]] = {}
+        for k, t in enumerate(h.leaf_tensors):
+            r.setdefault(id(t), []).extend(li[k] for li in h.leaf_rc)
+        if h.scaler_tensor is not None:
+            r.setdefault(id(h.scaler_tensor), []).extend(h.scaler_rc)
+        return r
+
+    writes = {id(h): _tile_codes(h.out_rc) for h in groups}
+    read_sets = {id(h): reads(h) for h in groups}
+    for g in rep:
+        g_reads = {k: _tile_codes(v) for k, v in read_sets[id(g)].items()}
+        g_writes = writes[id(g)]
         for h in groups:
             if h is g:
                 continue
-            h_reads = list(h.leaf_tensors) + ([h.scaler_tensor] if h.scaler_tensor is not None else [])
-            if any(h.out_tensor is t for t in reads) or any(t is g.out_tensor for t in h_reads):
+            hw = writes[id(h)]
+            if id(h.out_tensor) in g_reads and np.intersect1d(hw, g_reads[id(h.out_tensor)]).size:
                 g.dedupe_ok = False
+            elif h.out_tensor is g.out_tensor and np.intersect1d(hw, g_writes).size:
+                g.dedupe_ok = False
+            elif (not getattr(g, "private_out", False) and id(g.out_tensor) in read_sets[id(h)]
+                  and np.intersect1d(_tile_codes(read_sets[id(h)][id(g.out_tensor)]),
+                                     g_writes).size):
+                g.dedupe_ok = False
+            if not g.dedupe_ok:
                 break
 
 
