@@ -5,8 +5,10 @@ and block matmuls of computed operands (the operand materialised in bf16
 first).  Bars: within 2 bf16 ulps of the oracle's eager executor for the
 reductions (fp32 sums in the kernel's order against the oracle's float64
 sums, each then rounded to bf16) and within 2^-6 of exact softmax; matmuls
-within 2^-7 max |exact| of the float64 evaluation and no worse than the
-oracle plus 2^-9."""
+within 2^-7 max |exact| of the float64 evaluation (as the oracle is), and per
+element within one bf16 rounding of the product and one of the result plus
+the fp32 accumulation error (the oracle's block matmul also accumulates in
+fp32, so its error here is below one rounding and is not the bar)."""
 
 import pytest
 import torch
@@ -59,4 +61,14 @@ def test_matmul_of_computed_operands_on_gpu(form):
     top = float(ex.abs().max())
     e_gpu = float((got.double() - ex).abs().max())
     e_orc = float((orc.double() - ex).abs().max())
-    assert e_gpu <= 2 ** -7 * top and e_gpu <= e_orc + 2 ** -9 * top, (e_gpu, e_orc)
+    assert e_gpu <= 2 ** -7 * top and e_orc <= 2 ** -7 * top, (e_gpu, e_orc)
+    # per element: one bf16 rounding of the fp32-accumulated product (which
+    # may fall on the other side of a rounding boundary than the float64 one)
+    # and one of the result, plus the fp32 accumulation error
+    r = lambda v: v.to(torch.bfloat16).double()
+    A, B = a.double(), b.double()
+    prod = {"scale": r(A * 0.25) @ B, "relu_b": A @ r(torch.relu(B)),
+            "both": r(A + A) @ r(B * 2.0)}[form]
+    bound = 2 ** -8 * (prod.abs() + ex.abs()) + 1e-6 * K ** 0.5 * float(prod.abs().max())
+    err = (got.double() - ex).abs()
+    assert bool((err <= bound).all()), float((err - bound).max())
