@@ -276,6 +276,35 @@ int ttlh_matmul(const void* A, int a_dtype, int64_t lda, const void* B,
                 int64_t M, int64_t N, int64_t K, int accumulate, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Tile matmul with its store's elementwise program fused:
+ *   out[y0 + i, x0 + j] = prog(round_bf16((A . B)[i, j]), operands...)
+ * for the M x N product of bf16 A [M,K] and B [K,N] (fp32 accumulation).
+ *
+ * Replaces a store whose expression holds a tile / block matmul below its
+ * root, e.g. store(relu(a @ b + c)) (spec TTLangSpecification.md:693-761):
+ * the simulator materialises the product block in its dtype before the
+ * other ops read it (python/sim/block.py:870-920, 1012-1013), so the product
+ * is rounded to bf16, then the program runs with ttlh_eltwise's semantics
+ * (same ops, per-step rounding) without the product passing through HBM.
+ * `prog` / `in` / n_instr are ttlh_eltwise's, over the output region
+ * (y0, x0, M, N); step `prod_step` reads the product: its in[] entry must
+ * have a NULL pointer (the rest of that entry is ignored).  The program must
+ * be stack-free (no PUSH / BIN_POP forms), may use + - * / max min exp sqrt
+ * rsqrt abs neg relu recip and read at most 4 bf16 operands (the product
+ * included); every operand must allow 8-wide chunks (16-byte aligned, unit
+ * column stride or broadcast); the output is bf16.  Runs on the
+ * large-problem GEMM only: >= 192 output blocks of 256 x 256.  Otherwise
+ * returns TTLH_EUNSUPPORTED before launching, and the caller runs
+ * ttlh_matmul into a buffer, then ttlh_eltwise.
+ * M, N, K multiples of 32; A, B rows 16-byte aligned; out 16-byte aligned
+ * with out_ld a multiple of 8; out must not overlap A, B or an operand.  */
+int ttlh_matmul_eltwise(const void* A, int64_t lda, const void* B, int64_t ldb,
+                        int64_t M, int64_t N, int64_t K, const ttlh_instr* prog,
+                        const ttlh_operand* in, int n_instr, int prod_step,
+                        void* out, int out_dtype, int64_t out_ld, int64_t y0,
+                        int64_t x0, void* stream);
+
+/* ------------------------------------------------------------------------
  * bfloat8_b weight tiles.  The reference only fixes the tile size
  * (32*32 + 64 = 1088 bytes, python/ttl/dtype_utils.py:174-175); the codec
  * lives in un-vendored tt-metal.  Format implemented here (byte layout of

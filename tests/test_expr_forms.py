@@ -83,7 +83,8 @@ def test_matmul_of_computed_operands(form):
     got, orc, plan = _both(KL.make_matmul_computed_operand, tensors, 3, bm=bm, bk=bk, bn=bn,
                            form=form)
     kinds = [type(l).__name__ for l in plan.launches]
-    assert kinds.count("MatmulLaunch") == 1 and kinds.index("MatmulLaunch") > 0, kinds
+    mm = "FusedMatmulLaunch" if form == "relu_b" else "MatmulLaunch"
+    assert kinds.count(mm) == 1 and kinds.index(mm) > 0, kinds
     ex = _mm_exact(a, b, c, form)
     top = float(ex.abs().max())
     e_plan = float((got.double() - ex).abs().max())

@@ -72,14 +72,17 @@ def test_exact_reference_catches_a_dropped_bias():
 
 
 @pytest.mark.parametrize("case", CASES)
-def test_plan_is_a_matmul_then_an_eltwise_launch_and_matches(case):
+def test_plan_is_a_matmul_with_its_program_fused_and_matches(case):
     bm, bk, bn, R, C, epi = case
     a, b, c, out = inputs(*case)
     orc = run_oracle(case, (a, b, c, out))
     args = [ttnn.Tensor(t.clone()) for t in (a, b, c, out)]
     plan = KL.make_matmul_epilogue(ttl, bm, bk, bn, epi).trace(*args)
-    mm, ew = plan.launches
+    (fl,) = plan.launches
+    assert isinstance(fl, P.FusedMatmulLaunch)
+    mm, ew = fl.mm, fl.ew
     assert isinstance(mm, P.MatmulLaunch) and isinstance(ew, P.EltwiseLaunch)
+    assert ew.operands[fl.prod_step].ref.obj is mm.c.obj
     assert mm.k == bk * 32
     plan_interp.run(plan, dict(enumerate(args)))
     ex = exact(a, b, c, epi)
@@ -126,7 +129,7 @@ def _trace(body):
 
 def test_one_block_product_plus_bias_plans():
     plan = _trace(lambda ob, ab, bb, cc: ob.store(ab @ bb + cc))
-    assert [type(l) for l in plan.launches] == [P.MatmulLaunch, P.EltwiseLaunch]
+    assert [type(l) for l in plan.launches] == [P.FusedMatmulLaunch]
 
 
 def _two_products_kernel(ns):
@@ -184,7 +187,11 @@ def test_two_products_in_one_expression_and_an_offset_product():
     tensors, ex = two_products_case()
     args = [ttnn.Tensor(t.clone()) for t in tensors]
     plan = _two_products_kernel(ttl).trace(*args)
-    assert sum(isinstance(l, P.MatmulLaunch) for l in plan.launches) == 5
+    mms = [l for l in plan.launches if isinstance(l, P.MatmulLaunch)]
+    fused = [l for l in plan.launches if isinstance(l, P.FusedMatmulLaunch)]
+    # a0 @ b + a1 @ b: two products read by one program (not fused); a0 @ b
+    # twice in one product: two products; a1 @ b stored on its own
+    assert len(mms) + len(fused) == 5
     plan_interp.run(plan, dict(enumerate(args)))
     oargs = [sim_exec.OracleTensor(t.clone()) for t in tensors]
     _two_products_kernel(sim_exec.make_ttl())(*oargs)
@@ -208,4 +215,4 @@ def test_computed_operand_plans_the_operand_first():
     # elementwise launch into a tensor laid out like a), then the product,
     # then the epilogue (tests/test_expr_forms.py checks the values)
     plan = _trace(lambda ob, ab, bb, cc: ob.store((ab * 2.0) @ bb + cc))
-    assert [type(l) for l in plan.launches] == [P.EltwiseLaunch, P.MatmulLaunch, P.EltwiseLaunch]
+    assert [type(l) for l in plan.launches] == [P.EltwiseLaunch, P.FusedMatmulLaunch]

@@ -31,6 +31,7 @@
 
 #include "ttlh_bfp8.h"
 #include "ttlh_common.h"
+#include "ttlh_eltprog.h"
 
 namespace ttlh {
 namespace {
@@ -938,17 +939,11 @@ __device__ __forceinline__ uint16_t* dma_bbuf() {
 // stages stay in flight across it.
 __device__ __forceinline__ void stage_barrier() { __builtin_amdgcn_s_barrier(); }
 
-template <bool OUT_BF16, bool ACC>
-__global__ __launch_bounds__(kThreads, 1) void mm_dma_kernel(const MmArgs p) {
-  int bm, bn;
-  block_coords2(p, bm, bn);
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int wm = (wave >> 1) * 128;
-  const int wn = (wave & 1) * 128;
+// The main loop of the DMA kernel for block (bm, bn): acc = this wave's
+// 128x128 quadrant (rows bm * 256 + wm, columns bn * 256 + wn) of A . B.
+__device__ __forceinline__ void dma_gemm_main(const MmArgs& p, int bm, int bn, int wm, int wn,
+                                              int lane, f32x16 (&acc)[4][4]) {
   const DmaGeo g = make_dma_geo(p, bm, bn, wm, wn, lane);
-
-  f32x16 acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -1044,13 +1039,317 @@ __global__ __launch_bounds__(kThreads, 1) void mm_dma_kernel(const MmArgs p) {
   if (s < nk) stage(I0(), std::false_type(), s);
   if (s + 1 < nk) stage(I1(), std::false_type(), s + 1);
   if (s + 2 < nk) stage(I2(), std::false_type(), s + 2);
+}
 
+// One 32x32 accumulator tile, rounded to bf16, into the wave's 128-column
+// LDS quadrant at q (row stride 128 elements): lane pairs swap halves so each
+// lane writes one dword of two adjacent columns.
+__device__ __forceinline__ void epi_tile_to_lds(const f32x16& t, uint16_t* q, int lane) {
+  const bool odd = lane & 1;
+  const int col = (lane & 31) & ~1;
+  const int rbase = 4 * (lane >> 5) + (odd ? 1 : 0);
+  static_for<8>([&](auto mm) {
+    constexpr int m = decltype(mm)::value;
+    const float e0 = t[2 * m], e1 = t[2 * m + 1];
+    const float n0 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(e0), 0xB1, 0xF, 0xF, false));
+    const float n1 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(e1), 0xB1, 0xF, 0xF, false));
+    const float lo = odd ? n1 : e0;  // column 2c
+    const float hi = odd ? e1 : n0;  // column 2c + 1
+    const int row = rbase + 8 * (m >> 1) + 2 * (m & 1);
+    *reinterpret_cast<uint32_t*>(q + row * 128 + col) = cvt_pk_bf16x2(lo, hi);
+  });
+}
+
+// The wave's 128x128 quadrant, rounded to bf16, into LDS (rows 0-63 in A
+// stage buffer `wave`, 64-127 in B stage buffer `wave`: the main loop is done
+// with them once every wave has passed the barrier); returns the two halves.
+__device__ __forceinline__ void quadrant_to_lds(const f32x16 (&acc)[4][4], int wave, int lane,
+                                                uint16_t*& top, uint16_t*& bot) {
+  stage_barrier();  // every wave is done with the stage buffers
+  top = wave == 0 ? dmaA0 : wave == 1 ? dmaA1 : wave == 2 ? dmaA2 : dmaA3;
+  bot = wave == 0 ? dmaB0 : wave == 1 ? dmaB1 : wave == 2 ? dmaB2 : dmaB3;
+  uint16_t* const t = top;
+  uint16_t* const b = bot;
+  static_for<16>([&](auto ij) {
+    constexpr int i = decltype(ij)::value / 4, j = decltype(ij)::value % 4;
+    epi_tile_to_lds(acc[i][j], (i < 2 ? t : b) + (i & 1) * 32 * 128 + j * 32, lane);
+  });
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the quadrant is in LDS
+  asm volatile("" ::: "memory");       // (lanes read what other lanes wrote)
+}
+
+template <bool OUT_BF16, bool ACC>
+__global__ __launch_bounds__(kThreads, 1) void mm_dma_kernel(const MmArgs p) {
+  int bm, bn;
+  block_coords2(p, bm, bn);
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = (wave >> 1) * 128;
+  const int wn = (wave & 1) * 128;
+  f32x16 acc[4][4];
+  dma_gemm_main(p, bm, bn, wm, wn, lane, acc);
   const int r0 = bm * LM + wm, c0 = bn * LN + wn;
   static_for<16>([&](auto ij) {
     constexpr int i = decltype(ij)::value / 4, j = decltype(ij)::value % 4;
     if (r0 + i * 32 < p.M && c0 + j * 32 < p.N)
       store_acc_tile_pairs<OUT_BF16, ACC>(p, acc[i][j], r0 + i * 32, c0 + j * 32, lane);
   });
+}
+
+// The DMA kernel with the elementwise program of the store fused into its
+// epilogue: out = prog(round_bf16(A . B), operands...) over the GEMM's
+// output, e.g. relu(a @ b + c).  The simulator materialises the product
+// block in its dtype before the other ops read it (python/sim/block.py:
+// 870-920), so the product is rounded to bf16 first; then the program runs
+// with ttlh_eltwise's op definitions and per-step rounding, the product
+// standing for the operand whose pointer is null.  The product never reaches
+// HBM: quadrant_to_lds puts each wave's rounded quadrant in LDS and
+// epi_groups walks it in chunks of 8 consecutive elements (the program's
+// chunk shape) with the accumulators dead, so the program has the registers.
+struct EpiArgs {
+  EltArgs e;
+  MmArgs p;
+};
+
+
+// element e (0..7) of eight bf16 values packed in q, as f32
+__device__ __forceinline__ float bf16_elem(const u32x4 q, int e) {
+  const uint32_t w = e < 2 ? q.x : e < 4 ? q.y : e < 6 ? q.z : q.w;
+  return __uint_as_float((e & 1) ? (w & 0xffff0000u) : (w << 16));
+}
+
+constexpr int kEpiG = 4;     // chunks per lane and group (8 groups per quadrant)
+constexpr int kEpiProd = 3;  // Ins.arg of the step that reads the product
+constexpr int kEpiSet = 0;   // pseudo-op of a K_SET step: the source value itself
+
+// One group's operand bits: the 16-byte block holding each chunk's first
+// element and that element's byte offset in it (used by broadcast operands).
+struct EpiGroup {
+  u32x4 q[3][kEpiG];
+  uint32_t sel[3][kEpiG];
+};
+
+template <int NG>
+__device__ __forceinline__ void epi_issue(const EltArgs& e, const MmArgs& p, int r0, int c0,
+                                          int lane, int g0, EpiGroup& s) {
+#pragma unroll
+  for (int u = 0; u < kEpiG; ++u) {
+    const int qi = (g0 + u) * 64 + lane, row = qi >> 4, c8 = (qi & 15) * 8;
+    const int64_t y = e.y0 + min(r0 + row, p.M - 1), x = e.x0 + min(c0 + c8, p.N - 8);
+#pragma unroll
+    for (int j = 0; j < NG; ++j) {
+      const uintptr_t a = operand_addr<true>(e.ops[j], y, x);
+      s.q[j][u] = *reinterpret_cast<gu32x4*>(a & ~uintptr_t(15));
+      s.sel[j][u] = static_cast<uint32_t>(a & 15u);
+    }
+  }
+}
+
+// a broadcast operand (one element per chunk): that element in all 8 slots
+template <int NG>
+__device__ __forceinline__ void epi_normalise(const EltArgs& e, EpiGroup& s) {
+#pragma unroll
+  for (int j = 0; j < NG; ++j) {
+    if (e.ops[j].vec) continue;
+#pragma unroll
+    for (int u = 0; u < kEpiG; ++u) {
+      const uint32_t d = pick_dword(s.q[j][u], s.sel[j][u]);
+      const uint32_t h = (s.sel[j][u] & 2) ? (d >> 16) : (d & 0xffffu);
+      const uint32_t w = h | (h << 16);
+      s.q[j][u] = u32x4{w, w, w, w};
+    }
+  }
+}
+
+// acc = op(acc, src) (op(src, acc) for REV), in place, for the group
+template <int OP, bool REV, class Src>
+__device__ __forceinline__ void epi_apply(float (&acc)[kEpiG][8], Src src) {
+#pragma unroll
+  for (int u = 0; u < kEpiG; ++u) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float b = src(u, i);
+      if constexpr (OP == kEpiSet) acc[u][i] = b;
+      else acc[u][i] = REV ? binary1<OP>(b, acc[u][i]) : binary1<OP>(acc[u][i], b);
+    }
+  }
+}
+
+template <int OP, bool REV, int NG>
+__device__ __forceinline__ void epi_bin_step(const Ins ins, float (&acc)[kEpiG][8],
+                                             const u32x4 (&pr)[kEpiG], const EpiGroup& s) {
+  if (ins.src == SRC_IMM) {
+    const float c = ins.imm;
+    epi_apply<OP, REV>(acc, [&](int, int) { return c; });
+    return;
+  }
+  switch (ins.arg) {  // uniform: no dynamic register indexing
+    case 0:
+      if constexpr (NG > 0) epi_apply<OP, REV>(acc, [&](int u, int i) { return bf16_elem(s.q[0][u], i); });
+      else __builtin_unreachable();  // the host numbers operands below NG
+      break;
+    case 1:
+      if constexpr (NG > 1) epi_apply<OP, REV>(acc, [&](int u, int i) { return bf16_elem(s.q[1][u], i); });
+      else __builtin_unreachable();  // the host numbers operands below NG
+      break;
+    case 2:
+      if constexpr (NG > 2) epi_apply<OP, REV>(acc, [&](int u, int i) { return bf16_elem(s.q[2][u], i); });
+      else __builtin_unreachable();  // the host numbers operands below NG
+      break;
+    default:  // kEpiProd
+      epi_apply<OP, REV>(acc, [&](int u, int i) { return bf16_elem(pr[u], i); });
+      break;
+  }
+}
+
+template <int OP>
+__device__ __forceinline__ void epi_un(float (&acc)[kEpiG][8]) {
+  if constexpr (OP == TTLH_OP_EXP) {
+    // the group's range check hoisted out of exp1, as vexp_uniform does
+    bool ok = true;
+#pragma unroll
+    for (int u = 0; u < kEpiG; ++u) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ok &= exp1_in_range(acc[u][i]);
+    }
+    if (__all(ok)) {
+#pragma unroll
+      for (int u = 0; u < kEpiG; ++u) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[u][i] = exp1_fast(acc[u][i]);
+      }
+      return;
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kEpiG; ++u) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[u][i] = unary1<OP>(acc[u][i]);
+  }
+}
+
+template <bool REV, int NG>
+__device__ __forceinline__ void epi_bin_op(const Ins ins, float (&acc)[kEpiG][8],
+                                           const u32x4 (&pr)[kEpiG], const EpiGroup& s) {
+  switch (ins.op) {
+    case TTLH_OP_ADD: epi_bin_step<TTLH_OP_ADD, REV, NG>(ins, acc, pr, s); break;
+    case TTLH_OP_SUB: epi_bin_step<TTLH_OP_SUB, REV, NG>(ins, acc, pr, s); break;
+    case TTLH_OP_MUL: epi_bin_step<TTLH_OP_MUL, REV, NG>(ins, acc, pr, s); break;
+    case TTLH_OP_DIV: epi_bin_step<TTLH_OP_DIV, REV, NG>(ins, acc, pr, s); break;
+    case TTLH_OP_MAX: epi_bin_step<TTLH_OP_MAX, REV, NG>(ins, acc, pr, s); break;
+    default: epi_bin_step<TTLH_OP_MIN, REV, NG>(ins, acc, pr, s); break;
+  }
+}
+
+// One program step over a group.  Every branch is on the (uniform) step and
+// is taken once per group; each (op, source) pair has its own straight-line
+// arm that updates the accumulators in place, so no arm copies values into
+// a shared temporary.
+template <int NG>
+__device__ __forceinline__ void epi_step(const Ins ins, float (&acc)[kEpiG][8],
+                                         const u32x4 (&pr)[kEpiG], const EpiGroup& s) {
+  if (ins.kind == K_UNARY) {
+    switch (ins.op) {
+      case TTLH_OP_EXP: epi_un<TTLH_OP_EXP>(acc); break;
+      case TTLH_OP_SQRT: epi_un<TTLH_OP_SQRT>(acc); break;
+      case TTLH_OP_RSQRT: epi_un<TTLH_OP_RSQRT>(acc); break;
+      case TTLH_OP_ABS: epi_un<TTLH_OP_ABS>(acc); break;
+      case TTLH_OP_NEG: epi_un<TTLH_OP_NEG>(acc); break;
+      case TTLH_OP_RELU: epi_un<TTLH_OP_RELU>(acc); break;
+      default: epi_un<TTLH_OP_RECIP>(acc); break;
+    }
+  } else if (ins.kind == K_SET) {
+    epi_bin_step<kEpiSet, false, NG>(ins, acc, pr, s);
+  } else if (ins.kind == K_BIN) {
+    epi_bin_op<false, NG>(ins, acc, pr, s);
+  } else {  // K_BIN_REV
+    epi_bin_op<true, NG>(ins, acc, pr, s);
+  }
+  if (ins.rnd == TTLH_BF16) {  // round_bf16x8's rounding, element pairs
+#pragma unroll
+    for (int u = 0; u < kEpiG; ++u) {
+#pragma unroll
+      for (int i = 0; i < 8; i += 2) {
+        const uint32_t w = cvt_pk_bf16x2(acc[u][i], acc[u][i + 1]);
+        acc[u][i] = __uint_as_float(w << 16);
+        acc[u][i + 1] = __uint_as_float(w & 0xffff0000u);
+      }
+    }
+  }
+}
+
+// The program and the store for one group whose operand loads were issued.
+template <int NG>
+__device__ __forceinline__ void epi_finish(const EltArgs& e, const MmArgs& p, const uint16_t* top,
+                                           const uint16_t* bot, int r0, int c0, int lane, int g0,
+                                           EpiGroup& s) {
+  u32x4 pr[kEpiG];
+#pragma unroll
+  for (int u = 0; u < kEpiG; ++u) {
+    const int qi = (g0 + u) * 64 + lane, row = qi >> 4, c8 = (qi & 15) * 8;
+    pr[u] = *reinterpret_cast<const u32x4*>((row < 64 ? top : bot) + (row & 63) * 128 + c8);
+  }
+  epi_normalise<NG>(e, s);
+  float acc[kEpiG][8];
+  // each step's scalar load is issued a step ahead: with one wave per SIMD
+  // nothing else would cover its latency
+  Ins cur = e.prog[0];
+  for (int k = 0; k < e.n_instr; ++k) {
+    const Ins nxt = e.prog[min(k + 1, e.n_instr - 1)];
+    epi_step<NG>(cur, acc, pr, s);
+    cur = nxt;
+  }
+#pragma unroll
+  for (int u = 0; u < kEpiG; ++u) {
+    const int qi = (g0 + u) * 64 + lane, row = qi >> 4, c8 = (qi & 15) * 8;
+    if (r0 + row < p.M && c0 + c8 < p.N) {
+      u32x4 w;
+      w.x = cvt_pk_bf16(acc[u][0], acc[u][1]);
+      w.y = cvt_pk_bf16(acc[u][2], acc[u][3]);
+      w.z = cvt_pk_bf16(acc[u][4], acc[u][5]);
+      w.w = cvt_pk_bf16(acc[u][6], acc[u][7]);
+      const int64_t y = e.y0 + r0 + row, x = e.x0 + c0 + c8;
+      __builtin_nontemporal_store(
+          w, reinterpret_cast<u32x4*>(static_cast<uint16_t*>(e.out) + y * e.out_ld + x));
+    }
+  }
+}
+
+// The program over the wave's quadrant, kEpiG chunks per lane at a time:
+// the next group's operand loads are in flight while a group is computed
+// and stored.  NG (the number of operands other than the product) is a
+// template argument, so every load sequence is straight-line code and the
+// waits for a group's loads count exactly the memory operations issued
+// after them (a load in a branch makes the compiler wait for everything,
+// the previous group's stores included).
+template <int NG>
+__device__ __forceinline__ void epi_groups(const EltArgs& e, const MmArgs& p, const uint16_t* top,
+                                           const uint16_t* bot, int r0, int c0, int lane) {
+  EpiGroup s0, s1;
+  epi_issue<NG>(e, p, r0, c0, lane, 0, s0);
+  for (int g0 = 0; g0 < 32; g0 += 2 * kEpiG) {
+    epi_issue<NG>(e, p, r0, c0, lane, g0 + kEpiG, s1);
+    epi_finish<NG>(e, p, top, bot, r0, c0, lane, g0, s0);
+    if (g0 + 2 * kEpiG < 32) epi_issue<NG>(e, p, r0, c0, lane, g0 + 2 * kEpiG, s0);
+    epi_finish<NG>(e, p, top, bot, r0, c0, lane, g0 + kEpiG, s1);
+  }
+}
+
+template <int NG>
+__global__ __launch_bounds__(kThreads, 1) void mm_dma_epi_kernel(const EpiArgs args) {
+  const MmArgs& p = args.p;
+  int bm, bn;
+  block_coords2(p, bm, bn);
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = (wave >> 1) * 128;
+  const int wn = (wave & 1) * 128;
+  f32x16 acc[4][4];
+  dma_gemm_main(p, bm, bn, wm, wn, lane, acc);
+  uint16_t *top, *bot;
+  quadrant_to_lds(acc, wave, lane, top, bot);
+  const int r0 = bm * LM + wm, c0 = bn * LN + wn;
+  epi_groups<NG>(args.e, p, top, bot, r0, c0, lane);
 }
 
 template <bool OUT_BF16, bool ACC>
@@ -1567,6 +1866,102 @@ extern "C" int ttlh_matmul(const void* A, int a_dtype, int64_t lda, const void* 
   dim3 grid(static_cast<unsigned>((N + FBN - 1) / FBN), static_cast<unsigned>((M + FBM - 1) / FBM));
   hipLaunchKernelGGL(mm_f32_kernel, grid, dim3(256), 0, s, a);
   return check_launch("mm_f32_kernel");
+}
+
+extern "C" int ttlh_matmul_eltwise(const void* A, int64_t lda, const void* B, int64_t ldb,
+                                   int64_t M, int64_t N, int64_t K, const ttlh_instr* prog,
+                                   const ttlh_operand* in, int n_instr, int prod_step, void* out,
+                                   int out_dtype, int64_t out_ld, int64_t y0, int64_t x0,
+                                   void* stream) {
+  clear_error();
+  TTLH_REQUIRE(A && B && out && prog && in, TTLH_EINVAL, "ttlh_matmul_eltwise: null pointer");
+  TTLH_REQUIRE(M > 0 && N > 0 && K > 0 && M % 32 == 0 && N % 32 == 0 && K % 32 == 0, TTLH_EINVAL,
+               "ttlh_matmul_eltwise: M, N, K must be positive multiples of 32 (got %lld, %lld, %lld)",
+               (long long)M, (long long)N, (long long)K);
+  TTLH_REQUIRE(M < (1 << 30) && N < (1 << 30) && K < (1 << 30), TTLH_EUNSUPPORTED,
+               "ttlh_matmul_eltwise: dimension too large");
+  TTLH_REQUIRE(lda >= K && ldb >= N && lda % 8 == 0 && ldb % 8 == 0 &&
+                   (reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(B) & 15) == 0,
+               TTLH_EINVAL, "ttlh_matmul_eltwise: A and B need 16-byte aligned rows");
+  TTLH_REQUIRE(out_dtype == TTLH_BF16 || out_dtype == TTLH_F32, TTLH_EINVAL,
+               "ttlh_matmul_eltwise: bad output dtype");
+  TTLH_REQUIRE(out_dtype == TTLH_BF16, TTLH_EUNSUPPORTED,
+               "ttlh_matmul_eltwise: the fused epilogue writes bf16 outputs only");
+  TTLH_REQUIRE(y0 >= 0 && x0 >= 0 && x0 % 8 == 0 && out_ld >= x0 + N && out_ld % 8 == 0 &&
+                   (reinterpret_cast<uintptr_t>(out) & 15) == 0,
+               TTLH_EINVAL, "ttlh_matmul_eltwise: bad output region or alignment");
+  TTLH_REQUIRE(n_instr > 0 && n_instr <= TTLH_MAX_INSTR && prod_step >= 0 && prod_step < n_instr,
+               TTLH_EINVAL, "ttlh_matmul_eltwise: bad product step %d", prod_step);
+  const int pf = prog[prod_step].form;
+  TTLH_REQUIRE(in[prod_step].ptr == nullptr &&
+                   (pf == TTLH_FORM_LOAD || pf == TTLH_FORM_PUSH || pf == TTLH_FORM_BIN ||
+                    pf == TTLH_FORM_BIN_REV),
+               TTLH_EINVAL,
+               "ttlh_matmul_eltwise: the product step must read an operand whose pointer is NULL");
+  const int gm = static_cast<int>((M + LM - 1) / LM), gn = static_cast<int>((N + LN - 1) / LN);
+  TTLH_REQUIRE(int64_t(gm) * gn >= 192 && (y0 + M) * out_ld < (int64_t(1) << 31), TTLH_EUNSUPPORTED,
+               "ttlh_matmul_eltwise: the fused epilogue runs on the large-problem GEMM only "
+               "(>= 192 blocks of 256x256, 32-bit output offsets)");
+  // the product slot gets a stand-in operand for validation (the output at
+  // the element itself), then a null pointer for the kernel
+  ttlh_operand ops[TTLH_MAX_INSTR];
+  for (int k = 0; k < n_instr; ++k) ops[k] = in[k];
+  ops[prod_step] = ttlh_operand{out, out_dtype, 0, out_ld, 1, -1, -1, 0, 0};
+  EltArgs e = {};
+  ProgInfo pi;
+  int st = decode_program("ttlh_matmul_eltwise", prog, ops, n_instr, y0, x0, M, N, e, pi);
+  if (st != TTLH_OK) return st;
+  TTLH_REQUIRE(pi.vec && pi.off32, TTLH_EUNSUPPORTED,
+               "ttlh_matmul_eltwise: every operand must allow 8-wide chunks with 32-bit offsets");
+  TTLH_REQUIRE(pi.n_ops <= 4 && pi.max_depth == 1 && pi.all_bf16, TTLH_EUNSUPPORTED,
+               "ttlh_matmul_eltwise: the fused epilogue takes stack-free programs of at most 4 "
+               "bf16 operand reads (the product included)");
+  for (int k = 0; k < n_instr; ++k)
+    TTLH_REQUIRE(is_inline_op(prog[k].form, prog[k].op), TTLH_EUNSUPPORTED,
+                 "ttlh_matmul_eltwise: op %d is not available in the fused epilogue (+ - * / max "
+                 "min exp sqrt rsqrt abs neg relu recip are)", prog[k].op);
+  // the kernel's operand numbering: the other operands compacted to
+  // 0 .. NG-1 in consumption order, the product as kEpiProd
+  const EltArgs d = e;
+  int ng = 0;
+  for (int k = 0; k < n_instr; ++k) {
+    if (e.prog[k].src != SRC_OPERAND) continue;
+    if (k == prod_step) {
+      e.prog[k].arg = kEpiProd;
+    } else {
+      e.ops[ng] = d.ops[d.prog[k].arg];
+      e.prog[k].arg = static_cast<uint8_t>(ng++);
+    }
+  }
+  e.n_ops = ng;
+  e.out = out;
+  e.out_ld = out_ld;
+  e.out_dtype = out_dtype;
+  MmArgs a = {};
+  a.A = static_cast<const uint16_t*>(A);
+  a.B = static_cast<const uint16_t*>(B);
+  a.C = out;
+  a.lda = lda;
+  a.ldb = ldb;
+  a.ldc = out_ld;
+  a.M = static_cast<int32_t>(M);
+  a.N = static_cast<int32_t>(N);
+  a.K = static_cast<int32_t>(K);
+  a.c_dtype = out_dtype;
+  a.grid_m = gm;
+  a.grid_n = gn;
+  EpiArgs ea;
+  ea.e = e;
+  ea.p = a;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (ng) {
+    case 0: hipLaunchKernelGGL(mm_dma_epi_kernel<0>, dim3(gm * gn), dim3(kThreads), 0, s, ea); break;
+    case 1: hipLaunchKernelGGL(mm_dma_epi_kernel<1>, dim3(gm * gn), dim3(kThreads), 0, s, ea); break;
+    case 2: hipLaunchKernelGGL(mm_dma_epi_kernel<2>, dim3(gm * gn), dim3(kThreads), 0, s, ea); break;
+    default: hipLaunchKernelGGL(mm_dma_epi_kernel<3>, dim3(gm * gn), dim3(kThreads), 0, s, ea); break;
+  }
+  return check_launch("mm_dma_epi_kernel");
 }
 
 extern "C" int ttlh_matmul_bfp8w(const void* A, int64_t lda, const void* Bq, void* C, int64_t ldc,

@@ -89,6 +89,9 @@ SIGNATURES = {
                                    _vp]),
     "ttlh_matmul": (_int, [_vp, _int, _i64, _vp, _int, _i64, _vp, _int, _i64, _i64, _i64, _i64,
                            _int, _vp]),
+    "ttlh_matmul_eltwise": (_int, [_vp, _i64, _vp, _i64, _i64, _i64, _i64, C.POINTER(Instr),
+                                   C.POINTER(Operand), _int, _int, _vp, _int, _i64, _i64, _i64,
+                                   _vp]),
     "ttlh_bfp8_pack_host": (_int, [_vp, _vp, _i64, _i64]),
     "ttlh_bfp8_unpack_host": (_int, [_vp, _vp, _i64, _i64]),
     "ttlh_bfp8_unpack": (_int, [_vp, _vp, _i64, _i64, _vp]),

@@ -191,6 +191,79 @@ def matmul(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, accumulate: bool =
            M, N, K, int(bool(accumulate)), L.stream_ptr(stream))
 
 
+# Ops the fused GEMM epilogue (ttlh_matmul_eltwise) runs: + - * / max min
+# and the unary exp sqrt rsqrt abs neg relu recip.
+EPILOGUE_OPS = {1, 2, 3, 4, 5, 6, 16, 18, 19, 21, 22, 23, 25}
+
+
+def matmul_eltwise_supported(M: int, N: int, K: int, prog: StackProgram) -> bool:
+    """Whether ttlh_matmul_eltwise takes a problem of this shape and program:
+    the large-problem GEMM (>= 192 output blocks of 256 x 256), a stack-free
+    program of at most four operand reads (the product included) and the
+    epilogue's op set (bf16 operands and output, and their alignment, are
+    checked by the call)."""
+    if M % 32 or N % 32 or K % 32 or ((M + 255) // 256) * ((N + 255) // 256) < 192:
+        return False
+    if any(s.form in (L.FORM_PUSH, L.FORM_PUSH_CONST, L.FORM_BIN_POP) for s in prog.steps):
+        return False
+    if sum(s.form in (L.FORM_LOAD, L.FORM_BIN, L.FORM_BIN_REV) for s in prog.steps) > 4:
+        return False
+    return all(s.op in EPILOGUE_OPS for s in prog.steps
+               if s.form in (L.FORM_UNARY, L.FORM_BIN, L.FORM_BIN_REV, L.FORM_BIN_IMM,
+                             L.FORM_BIN_IMM_REV))
+
+
+def matmul_eltwise_preferred(prog: StackProgram) -> bool:
+    """Whether the fused epilogue is expected to beat the GEMM + eltwise pair
+    it replaces: programs of one op after the product load.
+
+    The fused kernel runs its epilogue after the MFMA loop with one wave per
+    SIMD and, at the sizes it takes, one output block per CU, so the whole
+    chip runs the epilogue at once and nothing hides its VALU work or its
+    operand reads; the pair pays the product's round trip through HBM
+    (write + read, 4 bytes per element) instead.  Measured at 4096^3
+    (fused / two launches): one op after the load 0.99-1.11x faster (bias
+    add 1.03, row / column broadcast 1.00 / 1.01, scale 1.03, relu 1.02,
+    max 1.11, div 1.09, sqrt 1.08, rsqrt 1.06, recip 1.00, exp 0.99); two or
+    more ops 0.92-0.99x (relu(x + c) 0.99, x + c + d 0.98, exp(x s) c 0.94,
+    relu(x s + row) 0.93, three operands 0.92)."""
+    return len(prog.steps) <= 2
+
+
+def matmul_eltwise(a: torch.Tensor, b: torch.Tensor, prog: StackProgram,
+                   operands: Sequence[Optional[OperandMap]], prod_step: int, out: torch.Tensor,
+                   region, stream=None) -> None:
+    """out[region] = prog(round_bf16(a @ b), operands): step `prod_step`
+    reads the product (its operands[] entry is ignored), the other steps'
+    operands are addressed as in eltwise() from the output element.  region
+    = (y0, x0, M, N) with (M, N) the product's shape."""
+    for t, nm in ((a, "A"), (b, "B")):
+        _check_device(t, f"matmul_eltwise {nm}")
+        if t.dtype != torch.bfloat16 or t.stride(1) != 1:
+            raise ValueError(f"matmul_eltwise {nm} must be row-major bf16")
+    _check_device(out, "matmul_eltwise output")
+    if out.stride(1) != 1:
+        raise ValueError("matmul_eltwise output must have unit column stride")
+    M, K = a.shape
+    K2, N = b.shape
+    y0, x0, h, w = region
+    if K2 != K or (h, w) != (M, N) or y0 + h > out.shape[0] or x0 + w > out.shape[1]:
+        raise ValueError(f"matmul_eltwise shapes {tuple(a.shape)} @ {tuple(b.shape)} -> region "
+                         f"{tuple(region)} of {tuple(out.shape)}")
+    n = len(prog.steps)
+    instrs = (L.Instr * n)()
+    ops = (L.Operand * n)()
+    for k, (s, m) in enumerate(zip(prog.steps, operands)):
+        instrs[k] = L.Instr(s.op, s.form, s.rnd, 0, s.imm, s.imm2)
+        if k != prod_step and s.form in (L.FORM_LOAD, L.FORM_PUSH, L.FORM_BIN, L.FORM_BIN_REV):
+            if m is None:
+                raise ValueError(f"step {k} needs an operand")
+            ops[k] = _operand_struct(m, y0, x0, h, w)
+    L.call("ttlh_matmul_eltwise", a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0), M, N, K,
+           instrs, ops, n, prod_step, out.data_ptr(), L.dtype_code(out.dtype), out.stride(0),
+           y0, x0, L.stream_ptr(stream))
+
+
 def tilize(x: torch.Tensor, stream=None) -> torch.Tensor:
     """Row-major bf16 / f32 [rows, cols] (device) -> its tilized element order
     (tiles row-major over the tile grid, four 16x16 faces per tile), as a 1-D

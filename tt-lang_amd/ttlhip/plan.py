@@ -117,6 +117,26 @@ class MatmulLaunch:
 
 
 @dataclass
+class FusedMatmulLaunch:
+    """A tile matmul into a plan-owned tensor followed by the elementwise
+    launch that alone reads it, at each output element itself (the product
+    of `relu(a @ b + c)` and the like, laid out like the output): one
+    ttlh_matmul_eltwise launch, the product rounded to its dtype and handed
+    to the program in registers, never stored.  Where that entry point does
+    not take the problem (small GEMMs, ops outside its set) the two launches
+    run as planned."""
+
+    mm: MatmulLaunch
+    ew: EltwiseLaunch
+    prod_step: int          # the program step that reads the product
+    loc: Optional[Tuple[str, int]] = None
+
+    def describe(self) -> str:
+        return (f"{self.mm.describe()} with the store's {len(self.ew.prog.steps)}-step "
+                "program fused into the epilogue")
+
+
+@dataclass
 class ReduceLaunch:
     prog: X.StackProgram
     operands: List[Optional[OperandSpec]]  # per step, addressed from iteration (y, x)
@@ -1648,7 +1668,54 @@ def build_plan(groups: List[_Group], tensor_ref) -> Plan:
         plan.launches.append(launch)
         inl.note_write(g.out_tensor)
     inl.finish(plan)
+    _fuse_epilogues(plan)
     return plan
+
+
+def _launch_refs(l) -> List[TensorRef]:
+    if isinstance(l, FusedMatmulLaunch):
+        return _launch_refs(l.mm) + _launch_refs(l.ew)
+    if isinstance(l, (EltwiseLaunch, ReduceLaunch)):
+        r = [l.out] + [s.ref for s in l.operands if s is not None]
+        if isinstance(l, ReduceLaunch) and l.scaler is not None:
+            r.append(l.scaler)
+        return r
+    if isinstance(l, SdpaLaunch):
+        return [l.q, l.kt, l.v, l.out]
+    return [l.a, l.b, l.c]
+
+
+def _fuse_epilogues(plan: Plan) -> None:
+    """A matmul launch into a hoisted product tensor (_hoist_matmuls),
+    immediately followed by the elementwise launch over the same output
+    rectangle that reads the product at each output element (identity map)
+    from exactly one step, the product tensor referenced by no other launch:
+    the pair becomes one FusedMatmulLaunch."""
+    L = plan.launches
+    out: List[Any] = []
+    i = 0
+    while i < len(L):
+        l = L[i]
+        if (isinstance(l, MatmulLaunch) and not l.b_block and type(l.c.obj) is _Temp
+                and i + 1 < len(L) and isinstance(L[i + 1], EltwiseLaunch)):
+            ew = L[i + 1]
+            temp = l.c.obj
+            steps = [k for k, s in enumerate(ew.operands) if s is not None and s.ref.obj is temp]
+            (r0, r1), (c0, c1) = l.rows, l.cols
+            others = sum(1 for x in L if x is not l and x is not ew
+                         for r in _launch_refs(x) if r.obj is temp)
+            if (len(steps) == 1 and others == 0
+                    and (ew.operands[steps[0]].row_mask, ew.operands[steps[0]].col_mask,
+                         ew.operands[steps[0]].row_off, ew.operands[steps[0]].col_off)
+                    == (-1, -1, 0, 0)
+                    and tuple(ew.region) == (r0, c0, r1 - r0, c1 - c0)
+                    and temp.dtype == torch.bfloat16):
+                out.append(FusedMatmulLaunch(l, ew, steps[0], ew.loc or l.loc))
+                i += 2
+                continue
+        out.append(l)
+        i += 1
+    plan.launches = out
 
 
 def _dedupe_writes(g: _Group, out_rc, leaf_rc):
@@ -1982,6 +2049,10 @@ def _execute_one(l, args, stream, Kn) -> None:
             sc = l.scaler.resolve(args)[r:r + 1, c:c + 1]
         Kn.reduce(l.prog, ops, l.kind, l.dims, l.out.resolve(args), l.region, l.out_origin,
                   l.out_pad, sc, l.scale, stream=stream)
+    elif isinstance(l, FusedMatmulLaunch):
+        if not _execute_fused(l, args, stream, Kn):
+            _execute_one(l.mm, args, stream, Kn)
+            _execute_one(l.ew, args, stream, Kn)
     elif isinstance(l, SdpaLaunch):
         q, kt, v, y = (r.resolve(args) for r in (l.q, l.kt, l.v, l.out))
         k = kt.t()
@@ -2009,3 +2080,42 @@ def _execute_one(l, args, stream, Kn) -> None:
         else:
             Kn.matmul(a[ar0:ar1], b[:, bc0:bc1], c[r0:r1, c0:c1], accumulate=False,
                       stream=stream)
+
+
+def _execute_fused(l: FusedMatmulLaunch, args, stream, Kn, force: bool = False) -> bool:
+    """One ttlh_matmul_eltwise launch when it takes the problem and is
+    expected to be the faster of the two forms (always when `force`); False
+    (nothing launched) otherwise."""
+    from . import _lib as L
+    m, ew = l.mm, l.ew
+    a, b, out = m.a.resolve(args), m.b.resolve(args), ew.out.resolve(args)
+    (ar0, ar1), (bc0, bc1) = m.operand_ranges()
+    aa, bb = a[ar0:ar1], b[:, bc0:bc1]
+    M, K = aa.shape
+    N = bb.shape[1]
+    if aa.dtype != torch.bfloat16 or bb.dtype != torch.bfloat16:
+        return False
+    if not Kn.matmul_eltwise_supported(M, N, K, ew.prog):
+        return False
+    if not (force or Kn.matmul_eltwise_preferred(ew.prog)):
+        return False
+    lo, hi = out.data_ptr(), out.data_ptr() + out.numel() * out.element_size()
+    for t in (a, b):
+        if t.data_ptr() < hi and lo < t.data_ptr() + t.numel() * t.element_size():
+            return False
+    ops = []
+    for k, spec in enumerate(ew.operands):
+        if spec is None or k == l.prod_step:
+            ops.append(None)
+            continue
+        t = spec.ref.resolve(args)
+        if t.data_ptr() < hi and lo < t.data_ptr() + t.numel() * t.element_size():
+            return False  # the fused kernel reads operands ahead of its stores
+        ops.append(Kn.OperandMap(t, spec.row_mask, spec.col_mask, spec.row_off, spec.col_off))
+    try:
+        Kn.matmul_eltwise(aa, bb, ew.prog, ops, l.prod_step, out, ew.region, stream=stream)
+    except L.TTLHError as err:
+        if err.code != L.TTLH_EUNSUPPORTED:
+            raise
+        return False  # refused before launching (operand alignment): two launches
+    return True

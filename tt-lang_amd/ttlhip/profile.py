@@ -33,7 +33,10 @@ def launch_work(l, args: Dict[Any, Any]) -> Tuple[float, str, float]:
     """(algorithmic work, unit, peak) of one launch: bytes read + written for
     an elementwise launch (an operand counted over the rows / columns it
     actually spans), 2 M N K flops for a tile matmul, 4 S^2 D per head for
-    fused attention."""
+    fused attention; a matmul with its store's program fused counts as the
+    matmul (MFMA-bound)."""
+    if isinstance(l, P.FusedMatmulLaunch):
+        return launch_work(l.mm, args)
     if isinstance(l, (P.EltwiseLaunch, P.ReduceLaunch)):
         _, _, h, w = l.region
         out = l.out.resolve(args)
@@ -64,6 +67,9 @@ def launch_work(l, args: Dict[Any, Any]) -> Tuple[float, str, float]:
 
 
 def _launch_name(l, args) -> str:
+    if isinstance(l, P.FusedMatmulLaunch):
+        return (f"ttlh_matmul_eltwise {_launch_name(l.mm, args)[len('ttlh_matmul '):]} + "
+                f"{len(l.ew.prog.steps)}-step epilogue")
     if isinstance(l, P.ReduceLaunch):
         _, _, h, w = l.region
         return f"ttlh_reduce {l.kind} dims {list(l.dims)} over {h}x{w}, {len(l.prog.steps)} steps"

@@ -36,17 +36,7 @@ def _trace_print(*args, **kwargs):
 
 def _refs(plan: P.Plan):
     for l in plan.launches:
-        if isinstance(l, (P.EltwiseLaunch, P.ReduceLaunch)):
-            yield l.out
-            for spec in l.operands:
-                if spec is not None:
-                    yield spec.ref
-            if isinstance(l, P.ReduceLaunch) and l.scaler is not None:
-                yield l.scaler
-        elif isinstance(l, P.SdpaLaunch):
-            yield from (l.q, l.kt, l.v, l.out)
-        else:
-            yield from (l.a, l.b, l.c)
+        yield from P._launch_refs(l)
 
 
 class KernelRunner:
