@@ -216,3 +216,21 @@ def test_computed_operand_plans_the_operand_first():
     # then the epilogue (tests/test_expr_forms.py checks the values)
     plan = _trace(lambda ob, ab, bb, cc: ob.store((ab * 2.0) @ bb + cc))
     assert [type(l) for l in plan.launches] == [P.EltwiseLaunch, P.FusedMatmulLaunch]
+
+
+@pytest.mark.parametrize("epi,fused", [("relu_bias", True), ("row_bias", True),
+                                       ("scale_exp", False)])
+def test_fused_form_chosen_by_program_length(epi, fused):
+    # the executor's choice between ttlh_matmul_eltwise and the two launches
+    # (kernels.matmul_eltwise_preferred); both are supported at this size
+    from ttlhip import kernels as Kn
+    bm, bk, bn = 4, 8, 4
+    M, K, N = 4096, 256, 3072
+    tensors = [torch.zeros(M, K, dtype=torch.bfloat16), torch.zeros(K, N, dtype=torch.bfloat16),
+               torch.zeros((1, N) if epi == "row_bias" else (M, N), dtype=torch.bfloat16),
+               torch.zeros(M, N, dtype=torch.bfloat16)]
+    plan = KL.make_matmul_epilogue(ttl, bm, bk, bn, epi).trace(*[ttnn.Tensor(t) for t in tensors])
+    (fl,) = plan.launches
+    assert isinstance(fl, P.FusedMatmulLaunch)
+    assert Kn.matmul_eltwise_supported(M, N, K, fl.ew.prog)
+    assert Kn.matmul_eltwise_preferred(fl.ew.prog) == fused

@@ -214,8 +214,11 @@ def matmul_eltwise_supported(M: int, N: int, K: int, prog: StackProgram) -> bool
 
 
 def matmul_eltwise_preferred(prog: StackProgram) -> bool:
-    """Whether the fused epilogue is expected to beat the GEMM + eltwise pair
-    it replaces: programs of one op after the product load.
+    """Whether the executor runs the fused epilogue rather than the GEMM +
+    eltwise pair it replaces: programs of one op after the product load, and
+    of two without exp whose only other operand is one tensor (the
+    bias-and-activation form, at parity and one launch with the product's
+    HBM round trip gone).
 
     The fused kernel runs its epilogue after the MFMA loop with one wave per
     SIMD and, at the sizes it takes, one output block per CU, so the whole
@@ -227,7 +230,12 @@ def matmul_eltwise_preferred(prog: StackProgram) -> bool:
     max 1.11, div 1.09, sqrt 1.08, rsqrt 1.06, recip 1.00, exp 0.99); two or
     more ops 0.92-0.99x (relu(x + c) 0.99, x + c + d 0.98, exp(x s) c 0.94,
     relu(x s + row) 0.93, three operands 0.92)."""
-    return len(prog.steps) <= 2
+    steps = prog.steps
+    if len(steps) <= 2:
+        return True
+    reads = sum(s.form in (L.FORM_LOAD, L.FORM_BIN, L.FORM_BIN_REV) for s in steps)
+    return (len(steps) == 3 and reads <= 2
+            and not any(s.form == L.FORM_UNARY and s.op == L.OP["exp"] for s in steps))
 
 
 def matmul_eltwise(a: torch.Tensor, b: torch.Tensor, prog: StackProgram,
