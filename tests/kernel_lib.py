@@ -1287,6 +1287,64 @@ def make_matmul_epilogue(ttl, bm, bk, bn, epi="relu_bias", grid=(2, 2)):
     return matmul_epilogue
 
 
+def make_acc_expr(ttl, bm, bk, bn, form="mm_scale_bias", grid=(2, 2)):
+    """An output block accumulated with store(expr, acc=True) over the K
+    loop, expr not a lone product: the simulator assigns the first store and
+    adds the later ones, block = block + expr, rounded to the block's dtype
+    (python/sim/block.py:850-864).  form: "mm_scale_bias" a_k @ b_k * 0.5 + c,
+    "relu_mm" relu(a_k @ b_k), "eltwise" exp(a_k * 0.25) * 0.5 (a_k the k-th
+    (bm, bk) block of a row band; b and c unused).  Output blocks are dealt to
+    the cores row by row."""
+
+    @ttl.kernel(grid=grid)
+    def acc_expr(a, b, c, out):
+        gx, gy = ttl.grid_size(dims=2)
+        rows = out.shape[0] // (bm * TILE)
+        cols = out.shape[1] // (bn * TILE)
+        kt = a.shape[1] // (bk * TILE)
+        per_core = rows * cols // (gx * gy)
+        a_cb = ttl.make_circular_buffer_like(a, shape=(bm, bk), buffer_factor=2)
+        b_cb = ttl.make_circular_buffer_like(b, shape=(bk, bn), buffer_factor=2)
+        c_cb = ttl.make_circular_buffer_like(c, shape=(bm, bn), buffer_factor=2)
+        o_cb = ttl.make_circular_buffer_like(out, shape=(bm, bn), buffer_factor=2)
+
+        @ttl.compute()
+        def comp():
+            for _ in range(per_core):
+                with o_cb.reserve() as ob:
+                    for _ in range(kt):
+                        with a_cb.wait() as ab, b_cb.wait() as bb, c_cb.wait() as cc:
+                            if form == "mm_scale_bias":
+                                ob.store(ab @ bb * 0.5 + cc, acc=True)
+                            elif form == "relu_mm":
+                                ob.store(ttl.math.relu(ab @ bb), acc=True)
+                            else:
+                                ob.store(ttl.math.exp(ab * 0.25) * 0.5, acc=True)
+
+        @ttl.datamovement()
+        def reader():
+            cx, cy = ttl.core(dims=2)
+            first = (cx * gy + cy) * per_core
+            for t in range(per_core):
+                r, col = (first + t) // cols, (first + t) % cols
+                for k in range(kt):
+                    with a_cb.reserve() as ab, b_cb.reserve() as bb, c_cb.reserve() as cc:
+                        ttl.copy(a[r * bm:(r + 1) * bm, k * bk:(k + 1) * bk], ab).wait()
+                        ttl.copy(b[k * bk:(k + 1) * bk, col * bn:(col + 1) * bn], bb).wait()
+                        ttl.copy(c[r * bm:(r + 1) * bm, col * bn:(col + 1) * bn], cc).wait()
+
+        @ttl.datamovement()
+        def writer():
+            cx, cy = ttl.core(dims=2)
+            first = (cx * gy + cy) * per_core
+            for t in range(per_core):
+                r, col = (first + t) // cols, (first + t) % cols
+                with o_cb.wait() as ob:
+                    ttl.copy(ob, out[r * bm:(r + 1) * bm, col * bn:(col + 1) * bn]).wait()
+
+    return acc_expr
+
+
 def make_pipe_chain(ttl, n_blocks=2):
     """y[j, c] = x_j + b[j, c] on a 1 x 3 grid, x_j = a[0, j] read by core 0
     only: core 0 sends it to core 1 on one pipe, core 1 forwards the block it

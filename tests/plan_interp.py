@@ -123,7 +123,8 @@ def run_matmul(l: MatmulLaunch, args):
         from oracle import bfp8 as OB
         fmt = l.b.resolve_obj(args).dtype.codec
         b = (OB.unpack_c if fmt == "bfp8" else OB.unpack4_c)(b.cpu(), a.shape[1], c.shape[1])
-    c[r0:r1, c0:c1] = (a[ar0:ar1].double() @ b[:, bc0:bc1].double()).to(c.dtype)
+    ks = l.k_slice()
+    c[r0:r1, c0:c1] = (a[ar0:ar1, ks].double() @ b[ks, bc0:bc1].double()).to(c.dtype)
 
 
 def run_sdpa(l: SdpaLaunch, args):

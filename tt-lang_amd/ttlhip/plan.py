@@ -107,6 +107,7 @@ class MatmulLaunch:
     loc: Optional[Tuple[str, int]] = None  # kernel source line of the store()
     a_rows: Optional[Tuple[int, int]] = None  # A element rows (default: `rows`)
     b_cols: Optional[Tuple[int, int]] = None  # B element cols (default: `cols`)
+    k_range: Optional[Tuple[int, int]] = None  # A cols / B rows summed (default: [0, k))
 
     def describe(self) -> str:
         return (f"matmul C[{self.rows[0]}:{self.rows[1]}, {self.cols[0]}:{self.cols[1]}] = "
@@ -114,6 +115,10 @@ class MatmulLaunch:
 
     def operand_ranges(self) -> Tuple[Tuple[int, int], Tuple[int, int]]:
         return self.a_rows or self.rows, self.b_cols or self.cols
+
+    def k_slice(self) -> slice:
+        k0, k1 = self.k_range or (0, self.k)
+        return slice(k0, k1)
 
 
 @dataclass
@@ -685,6 +690,7 @@ def resolve(core_traces: List[Dict[str, Any]]) -> List[_Group]:
         if inter:
             _intermediate_tables(threads, events, cbs, count, inter, fill, drain, scratch)
         # stores
+        acc_count: Dict[Tuple[int, int], int] = {}  # (CB, block) -> acc stores so far
         for tmpl, root in threads:
             for ev in events[id(tmpl)]:
                 if ev.kind != "store":
@@ -701,6 +707,12 @@ def resolve(core_traces: List[Dict[str, Any]]) -> List[_Group]:
                 dt = drain[cid]
                 R, C = target.shape
                 site = (ev.data.get("loc"), _tree_key(e.tree, {}), id(dt.tensor))
+                rounds = None
+                if ev.data["acc"]:
+                    rounds = _acc_rounds(cid, rout, acc_count)
+                    if rounds.max(initial=0) > 0 and _has_sub(e.tree):
+                        raise PlanError("store(acc=True) into a block stored before, of an "
+                                        "expression with a reduction inside, is not supported")
                 e = _hoist_subexprs(ev, e, target, rout, dt, fill, shape, groups, hoisted, site)
                 e = _hoist_operands(ev, e, fill, shape, groups, hoisted, site)
                 if e.tree[0] == "reduce":
@@ -709,45 +721,126 @@ def resolve(core_traces: List[Dict[str, Any]]) -> List[_Group]:
                 if e.tree[0] == "bmatmul":
                     _resolve_block_matmul(ev, e, target, rout, dt, fill, shape, groups)
                     continue
-                if e.tree[0] != "matmul" and (_has(e.tree, "matmul") or _has(e.tree, "bmatmul")):
+                inner_mm = e.tree[0] != "matmul" and (_has(e.tree, "matmul")
+                                                      or _has(e.tree, "bmatmul"))
+                if rounds is not None and e.tree[0] != "matmul" and (
+                        inner_mm or rounds.max(initial=0) > 0):
+                    _resolve_acc_rounds(ev, e, target, rout, dt, fill, shape, groups, hoisted,
+                                        site, rounds)
+                    continue
+                if inner_mm:
                     e = _hoist_matmuls(ev, e, target, rout, dt, fill, shape, groups, hoisted)
-                er, ec = e.shape
-                nslot = R * C
-                # output tile of every (instance, slot)
-                slot = np.arange(nslot)
-                oi, oj = slot // C, slot % C
-                out_r = (dt.r0[rout][:, None] + oi[None, :]).ravel()
-                out_c = (dt.c0[rout][:, None] + oj[None, :]).ravel()
-                leaves = _tree_leaves(e.tree, [])
-                leaf_rc = []
-                leaf_tensors = []
-                ei, ej = slot // ec, slot % ec  # expression slot of each target slot
-                for lf in leaves:
-                    blk, rmap, cmap = lf[1], lf[2], lf[3]
-                    lcid = blk.cb.id
-                    if lcid not in fill:
-                        raise PlanError("expression operands must come from blocks filled by "
-                                        "ttl.copy from a tensor")
-                    ft = fill[lcid]
-                    w = T.broadcast_to_domain(blk.event.index, shape).ravel()
-                    lr = (ft.r0[w][:, None] + np.asarray(rmap)[ei][None, :]).ravel()
-                    lc = (ft.c0[w][:, None] + np.asarray(cmap)[ej][None, :]).ravel()
-                    leaf_rc.append(np.stack([lr, lc], 1))
-                    leaf_tensors.append(ft.tensor)
-                order = np.repeat(np.arange(rout.size), nslot)
-                key = (_tree_key(e.tree, {}), tuple(id(t) for t in leaf_tensors), id(dt.tensor),
-                       ev.data["acc"])
-                g = groups.get(key)
-                if g is None:
-                    g = _Group(e.tree, leaves, leaf_tensors, dt.tensor, ev.data["acc"], e.dtype,
-                               ev.data.get("loc"))
-                    groups[key] = g
-                g.out_rc.append(np.stack([out_r, out_c], 1))
-                g.leaf_rc.append(leaf_rc)
-                g.order.append(order)
+                _store_group(ev, e, target, rout, dt, fill, shape, groups)
     for sc in scratch.values():
         sc.check()
     return list(groups.values())
+
+
+def _dom(index, shape, sel=None) -> np.ndarray:
+    """An event's per-instance index over the store's domain (raveled), the
+    instances `sel` selects only."""
+    w = T.broadcast_to_domain(index, shape).ravel()
+    return w if sel is None else w[sel]
+
+
+def _store_group(ev, e, target, rout, dt, fill, shape, groups, sel=None, key_extra=()) -> None:
+    """The store's instances (those `sel` selects) join the group of their
+    expression, tensors and acc flag (extended by key_extra)."""
+    R, C = target.shape
+    er, ec = e.shape
+    nslot = R * C
+    rsel = rout if sel is None else rout[sel]
+    inst = np.arange(rout.size) if sel is None else np.nonzero(sel)[0]
+    # output tile of every (instance, slot)
+    slot = np.arange(nslot)
+    oi, oj = slot // C, slot % C
+    out_r = (dt.r0[rsel][:, None] + oi[None, :]).ravel()
+    out_c = (dt.c0[rsel][:, None] + oj[None, :]).ravel()
+    leaves = _tree_leaves(e.tree, [])
+    leaf_rc = []
+    leaf_tensors = []
+    ei, ej = slot // ec, slot % ec  # expression slot of each target slot
+    for lf in leaves:
+        blk, rmap, cmap = lf[1], lf[2], lf[3]
+        lcid = blk.cb.id
+        if lcid not in fill:
+            raise PlanError("expression operands must come from blocks filled by "
+                            "ttl.copy from a tensor")
+        ft = fill[lcid]
+        w = _dom(blk.event.index, shape, sel)
+        lr = (ft.r0[w][:, None] + np.asarray(rmap)[ei][None, :]).ravel()
+        lc = (ft.c0[w][:, None] + np.asarray(cmap)[ej][None, :]).ravel()
+        leaf_rc.append(np.stack([lr, lc], 1))
+        leaf_tensors.append(ft.tensor)
+    acc = ev.data["acc"] and not key_extra
+    order = np.repeat(inst, nslot)
+    key = (_tree_key(e.tree, {}), tuple(id(t) for t in leaf_tensors), id(dt.tensor),
+           acc) + tuple(key_extra)
+    g = groups.get(key)
+    if g is None:
+        g = _Group(e.tree, leaves, leaf_tensors, dt.tensor, acc, e.dtype, ev.data.get("loc"))
+        groups[key] = g
+    g.out_rc.append(np.stack([out_r, out_c], 1))
+    g.leaf_rc.append(leaf_rc)
+    g.order.append(order)
+
+
+def _acc_rounds(cid: int, rout: np.ndarray, acc_count: Dict[Tuple[int, int], int]) -> np.ndarray:
+    """Round of every instance of a store(acc=True) event: how many acc stores
+    into the same block came before it (earlier events, then earlier
+    instances of this one in loop order).  Counts the event's stores in."""
+    rounds = np.zeros(rout.size, dtype=np.int64)
+    if rout.size == 0:
+        return rounds
+    srt = np.argsort(rout, kind="stable")
+    rs = rout[srt]
+    start = np.r_[0, np.nonzero(np.diff(rs))[0] + 1]
+    rank = np.arange(rs.size) - np.repeat(start, np.diff(np.r_[start, rs.size]))
+    base = np.array([acc_count.get((cid, int(b)), 0) for b in rs], dtype=np.int64)
+    rounds[srt] = rank + base
+    for b, n in zip(*np.unique(rs, return_counts=True)):
+        acc_count[(cid, int(b))] = acc_count.get((cid, int(b)), 0) + int(n)
+    return rounds
+
+
+def _resolve_acc_rounds(ev, e, target, rout, dt, fill, shape, groups, hoisted, site,
+                        rounds) -> None:
+    """store(expr, acc=True) whose expression is not a lone tile matmul: the
+    simulator assigns on a block's first acc store and adds on the later ones,
+    block = block + value, rounded to the block's dtype (python/sim/block.py:
+    850-864).  The instances are split into rounds by how many acc stores into
+    their block came before; round 0 stores the expression, round r > 0 stores
+    out + expression, out read from the output tensor at the block's own
+    tiles, each round one store group planned after the one before (a tile
+    matmul inside the expression gets a plan-owned product tensor per round,
+    planned just before its round)."""
+    R, C = target.shape
+    for r in np.unique(rounds):
+        sel = rounds == r
+        rsite = site + (("acc", int(r)),)
+        er = e
+        if _has(e.tree, "matmul") or _has(e.tree, "bmatmul"):
+            er = _hoist_matmuls(ev, e, target, rout, dt, fill, shape, groups, hoisted, sel=sel,
+                                site=rsite)
+        if r > 0:
+            key = rsite + ("out",)
+            if key not in hoisted:
+                cb = _HoistedCB(-1 - len(hoisted), target.cb.dtype, "(accumulated block)")
+                hoisted[key] = (None, cb)
+            cb = hoisted[key][1]
+            fill[cb.id] = _CopyTable(dt.tensor, dt.r0, dt.c0)
+            out_leaf = ("leaf", _HoistedBlock(cb, target.event), list(range(R)), list(range(C)))
+            tree = ("add", out_leaf, er.tree)
+            dtype = (torch.promote_types(target.cb.dtype, er.dtype)
+                     if isinstance(er.dtype, torch.dtype)
+                     and isinstance(target.cb.dtype, torch.dtype) else er.dtype)
+            er = _Expr(tree, (R, C), dtype)
+        _store_group(ev, er, target, rout, dt, fill, shape, groups, sel=sel,
+                     key_extra=(("acc round", int(r)),))
+
+
+def _has_sub(tree) -> bool:
+    return any(_is_sub(lf) for lf in _tree_leaves(tree, []))
 
 
 class _HoistedCB:
@@ -767,7 +860,7 @@ class _Expr:
         self.tree, self.shape, self.dtype = tree, tuple(shape), dtype
 
 
-def _hoist_matmuls(ev, e, target, rout, dt, fill, shape, groups, hoisted):
+def _hoist_matmuls(ev, e, target, rout, dt, fill, shape, groups, hoisted, sel=None, site=None):
     """A store whose expression holds a tile or block matmul below its root,
     e.g. relu(a @ b + c): the simulator materialises the product block (in
     the dtype its operands promote to) before the other ops read it
@@ -775,20 +868,22 @@ def _hoist_matmuls(ev, e, target, rout, dt, fill, shape, groups, hoisted):
     becomes a matmul launch into a plan-owned tensor laid out like the
     output, and the expression reads that tensor at the output's tile
     positions as an ordinary operand.  Only products of blocks filled from
-    tensors, of the target's block shape, in stores without acc."""
-    if ev.data["acc"]:
-        raise PlanError("store(acc=True) of an expression that contains a tile matmul is not "
-                        "supported; store the product on its own")
+    tensors, of the target's block shape.  For the instances `sel` selects
+    (one accumulation round of an acc store: `site` names the round, so each
+    round's product gets its own tensor)."""
     R, C = target.shape
     if tuple(e.shape) != (R, C):
         raise PlanError(f"an expression of block shape {tuple(e.shape)} holding a tile matmul, "
                         f"stored into a block of shape {(R, C)}")
     slot = np.arange(R * C)
     oi, oj = slot // C, slot % C
-    out_r = (dt.r0[rout][:, None] + oi[None, :]).ravel()
-    out_c = (dt.c0[rout][:, None] + oj[None, :]).ravel()
-    order = np.repeat(np.arange(rout.size), R * C)
-    site = (ev.data.get("loc"), _tree_key(e.tree, {}), id(dt.tensor))
+    rsel = rout if sel is None else rout[sel]
+    inst = np.arange(rout.size) if sel is None else np.nonzero(sel)[0]
+    out_r = (dt.r0[rsel][:, None] + oi[None, :]).ravel()
+    out_c = (dt.c0[rsel][:, None] + oj[None, :]).ravel()
+    order = np.repeat(inst, R * C)
+    if site is None:
+        site = (ev.data.get("loc"), _tree_key(e.tree, {}), id(dt.tensor))
     count = [0]
 
     def walk(tree):
@@ -821,12 +916,12 @@ def _hoist_matmuls(ev, e, target, rout, dt, fill, shape, groups, hoisted):
             tab = _CopyTable(temp, dt.r0, dt.c0)
             if tag == "bmatmul":
                 _resolve_block_matmul(ev, _Expr(tree, (R, C), pdt), target, rout, tab, fill, shape,
-                                      groups)
+                                      groups, sel)
             else:
                 leaf_rc = []
                 for lf in (la, lb):
                     ft = fill[lf[1].cb.id]
-                    w = T.broadcast_to_domain(lf[1].event.index, shape).ravel()
+                    w = _dom(lf[1].event.index, shape, sel)
                     lr = (ft.r0[w][:, None] + np.asarray(lf[2])[oi][None, :]).ravel()
                     lc = (ft.c0[w][:, None] + np.asarray(lf[3])[oj][None, :]).ravel()
                     leaf_rc.append(np.stack([lr, lc], 1))
@@ -1013,7 +1108,7 @@ def _hoist_operands(ev, e, fill, shape, groups, hoisted, site):
     return _Expr(walk(e.tree), e.shape, e.dtype)
 
 
-def _resolve_block_matmul(ev, e, target, rout, dt, fill, shape, groups) -> None:
+def _resolve_block_matmul(ev, e, target, rout, dt, fill, shape, groups, sel=None) -> None:
     """Store of a block matmul (the spec's (M, K) @ (K, N) blocks): output
     tile (i, j) accumulates a(i, k) @ b(k, j) over k, which is the tile
     matmul accumulation of K store(acc=True) instances; it joins that group
@@ -1025,8 +1120,10 @@ def _resolve_block_matmul(ev, e, target, rout, dt, fill, shape, groups) -> None:
                         f"{(R, C)}")
     slot = np.arange(R * C)
     oi, oj = slot // C, slot % C
-    out_r = (dt.r0[rout][:, None] + oi[None, :]).ravel()
-    out_c = (dt.c0[rout][:, None] + oj[None, :]).ravel()
+    rsel = rout if sel is None else rout[sel]
+    inst = np.arange(rout.size) if sel is None else np.nonzero(sel)[0]
+    out_r = (dt.r0[rsel][:, None] + oi[None, :]).ravel()
+    out_c = (dt.c0[rsel][:, None] + oj[None, :]).ravel()
     ops = []
     for lf in (la, lb):
         blk = lf[1]
@@ -1034,7 +1131,7 @@ def _resolve_block_matmul(ev, e, target, rout, dt, fill, shape, groups) -> None:
             raise PlanError("expression operands must come from blocks filled by ttl.copy from a "
                             "tensor")
         ft = fill[blk.cb.id]
-        w = T.broadcast_to_domain(blk.event.index, shape).ravel()
+        w = _dom(blk.event.index, shape, sel)
         ops.append((ft, w, np.asarray(lf[2]), np.asarray(lf[3])))
     (fa, wa, ra, ca), (fb, wb, rb, cb) = ops
     outs, a_rc, b_rc = [], [], []
@@ -1056,7 +1153,7 @@ def _resolve_block_matmul(ev, e, target, rout, dt, fill, shape, groups) -> None:
     base = sum(o.size for o in g.order)
     g.out_rc.append(np.concatenate(outs, 0))
     g.leaf_rc.append([np.concatenate(a_rc, 0), np.concatenate(b_rc, 0)])
-    g.order.append(base + np.tile(np.repeat(np.arange(rout.size), R * C), K))
+    g.order.append(base + np.tile(np.repeat(inst, R * C), K))
 
 
 def _resolve_reduce(ev, e, target, rout, dt, fill, shape, groups) -> None:
@@ -1978,11 +2075,14 @@ def _plan_matmul(g: _Group, out_rc, leaf_rc, tensor_ref) -> MatmulLaunch:
     K = a_t.shape[1]
     kt = K // TILE
     n_out = _unique_tiles(out_rc)
-    triples = np.stack([orow, ocol, ac], 1)
     key = (orow * (int(ocol.max()) + 1) + ocol) * (kt + 1) + ac
     if np.unique(key).size != key.size:
         raise PlanError("a (output tile, k) product is accumulated twice")
-    if key.size != n_out * kt or (not g.acc and kt != 1):
+    # every output tile sums the same k tiles: all of K, or (one round of an
+    # accumulating store whose expression holds the product) one contiguous
+    # part of it
+    k0, k1 = (int(ac.min()), int(ac.max()) + 1) if ac.size else (0, kt)
+    if key.size != n_out * (k1 - k0) or (not g.acc and k1 - k0 != 1):
         raise PlanError("every output tile must accumulate A(m,k) @ B(k,n) over all k "
                         "(store(acc=True) inside the K loop)")
     r0, r1, c0, c1 = _rect(out_rc)
@@ -1994,12 +2094,16 @@ def _plan_matmul(g: _Group, out_rc, leaf_rc, tensor_ref) -> MatmulLaunch:
     if b_block:
         if (c0, c1) != (0, b_t.shape[1] // TILE) or db != 0:
             raise PlanError(f"a {b_t.dtype.name} B operand must be used over all of its columns")
+        if (k0, k1) != (0, kt):
+            raise PlanError(f"a {b_t.dtype.name} B operand must be used over all of its rows")
         if a_t.dtype != torch.bfloat16 or g.out_tensor.dtype != torch.bfloat16:
             raise PlanError(f"the {b_t.dtype.name} matmul takes bfloat16 A and output tensors")
+    part = (k0, k1) != (0, kt)
     return MatmulLaunch(tensor_ref(a_t), tensor_ref(b_t), tensor_ref(g.out_tensor),
-                        (r0 * TILE, r1 * TILE), (c0 * TILE, c1 * TILE), K, b_block,
+                        (r0 * TILE, r1 * TILE), (c0 * TILE, c1 * TILE), (k1 - k0) * TILE, b_block,
                         a_rows=((r0 + da) * TILE, (r1 + da) * TILE) if da else None,
-                        b_cols=((c0 + db) * TILE, (c1 + db) * TILE) if db else None)
+                        b_cols=((c0 + db) * TILE, (c1 + db) * TILE) if db else None,
+                        k_range=(k0 * TILE, k1 * TILE) if part else None)
 
 
 # ---------------------------------------------------------------------------
@@ -2075,10 +2179,11 @@ def _execute_one(l, args, stream, Kn) -> None:
         r0, r1 = l.rows
         c0, c1 = l.cols
         (ar0, ar1), (bc0, bc1) = l.operand_ranges()
+        ks = l.k_slice()
         if l.b_block:
             l.b.resolve_obj(args).dtype.matmul(a[ar0:ar1], b, c[r0:r1], stream=stream)
         else:
-            Kn.matmul(a[ar0:ar1], b[:, bc0:bc1], c[r0:r1, c0:c1], accumulate=False,
+            Kn.matmul(a[ar0:ar1, ks], b[ks, bc0:bc1], c[r0:r1, c0:c1], accumulate=False,
                       stream=stream)
 
 
@@ -2090,7 +2195,8 @@ def _execute_fused(l: FusedMatmulLaunch, args, stream, Kn, force: bool = False) 
     m, ew = l.mm, l.ew
     a, b, out = m.a.resolve(args), m.b.resolve(args), ew.out.resolve(args)
     (ar0, ar1), (bc0, bc1) = m.operand_ranges()
-    aa, bb = a[ar0:ar1], b[:, bc0:bc1]
+    ks = m.k_slice()
+    aa, bb = a[ar0:ar1, ks], b[ks, bc0:bc1]
     M, K = aa.shape
     N = bb.shape[1]
     if aa.dtype != torch.bfloat16 or bb.dtype != torch.bfloat16:
