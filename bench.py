@@ -51,6 +51,7 @@ PREROLL_MS = 10.0              # steady work queued ahead of the timed steps (ms
 PREROLL_MIN_STEPS = 50         # ... and at least this many steps
 MFMA_PREROLL_MS = 30.0         # MFMA workloads: the clock settles at the power cap
 SAMPLES = 5                    # timed samples of K steps each (median reported)
+COPY_BYTES = 8192 * 16384 * 2  # bytes the copy-ceiling kernel reads (and writes) per launch
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
@@ -127,6 +128,16 @@ class Workload:
         restatement of the simulator), timed on a bounded sample."""
         return None
 
+    def traffic_kernels(self):
+        """(kernel-name substring, workgroup count or None) of every kernel a
+        step launches, for the HBM byte counters."""
+        return [(self.kernel_name(), None)]
+
+    def algorithmic_bytes(self) -> float:
+        """Bytes a step must move at least: every operand read once, every
+        result written once."""
+        return self.work_per_step()
+
 
 class PlanWorkload(Workload):
     """A tt-lang kernel traced once by the drop-in `ttl`; each step executes
@@ -158,6 +169,10 @@ class EltwiseWorkload(PlanWorkload):
 
     def kernel_name(self):
         return "flat_kernel"
+
+    def traffic_kernels(self):  # the flat kernel's instantiation for this program
+        return [("flat_kernel<2, 3u, true>" if self.kind == "add" else "flat_kernel<4, 11u, true>",
+                 None)]
 
     def work_per_step(self):
         e = self.n * self.n * 2
@@ -345,6 +360,12 @@ class MatmulWorkload(PlanWorkload):
     def work_per_step(self):
         return 2.0 * self.M * self.N * self.K
 
+    def traffic_kernels(self):
+        return [("mm_dma_kernel", (self.M // 256) * (self.N // 256))]
+
+    def algorithmic_bytes(self):
+        return 2.0 * (self.M * self.K + self.K * self.N + self.M * self.N)
+
     def make_sets(self):
         import kernel_lib as KL
         import ttl
@@ -387,6 +408,76 @@ class MatmulWorkload(PlanWorkload):
                           f"{dt * full / steps:.0f} s"}
 
 
+class MatmulEpilogueWorkload(PlanWorkload):
+    """relu(A.B + C) at C3's shape through the drop-in: one store per output
+    block of the spec's block matmul plus a bias and an activation, planned
+    as one fused launch (the GEMM with the store's program in its epilogue,
+    the product never written to HBM)."""
+
+    bound = "mfma"
+    unit = "TFLOP/s"
+
+    def __init__(self, name, M, N, K, seed=71):
+        self.name, self.M, self.N, self.K, self.seed = name, M, N, K, seed
+        self.config = (f"relu(A.B + C) bf16 {M}x{K}x{N}, N(0,1)/sqrt(K) operands, C N(0,1), "
+                       "product rounded to bf16 before the bias (simulator semantics), "
+                       "4x4-tile output blocks, (4, K/32) @ (K/32, 4) block matmuls")
+
+    def kernel_name(self):
+        return "mm_dma_epi_kernel"
+
+    def work_per_step(self):
+        return 2.0 * self.M * self.N * self.K
+
+    def algorithmic_bytes(self):  # A, B, the bias and the output once (no product)
+        return 2.0 * (self.M * self.K + self.K * self.N + 2 * self.M * self.N)
+
+    def make_sets(self):
+        import kernel_lib as KL
+        import ttl
+        import ttnn
+        from oracle.tile_ops import seeded
+        self.kernel = KL.make_matmul_epilogue(ttl, 4, self.K // 32, 4, "relu_bias")
+        std = 1.0 / math.sqrt(self.K)
+        a = ttnn.from_torch(seeded((self.M, self.K), "normal", self.seed, std=std))
+        b = ttnn.from_torch(seeded((self.K, self.N), "normal", self.seed + 1, std=std))
+        c = ttnn.from_torch(seeded((self.M, self.N), "normal", self.seed + 2))
+        out = ttnn.empty((self.M, self.N), dtype=torch.bfloat16)
+        return [[a, b, c, out]]
+
+    def setup(self):
+        super().setup()
+        from ttlhip import plan as P
+        (fl,) = self.plan.launches
+        assert isinstance(fl, P.FusedMatmulLaunch), self.plan.describe()
+
+    def check(self):
+        self.launch(0)
+        torch.cuda.synchronize()
+        a, b, c, out = (t.to_torch() for t in self.sets[0])
+        rows = torch.arange(0, self.M, max(1, self.M // 64))
+        prod = (a[rows].double() @ b.double()).to(torch.bfloat16)
+        exact = torch.relu((prod.double() + c[rows].double()).to(torch.bfloat16).double())
+        got = out[rows].double()
+        return {"max_abs_err_rel": float((got - exact).abs().max() / exact.abs().max()),
+                "rows_checked": int(rows.numel()),
+                "oracle": "float64 product rounded to bf16, bf16 bias add, relu"}
+
+    def cpu_baseline(self):
+        import kernel_lib as KL
+        from oracle.tile_ops import seeded
+        n = 1024
+        std = 1.0 / math.sqrt(n)
+        t = [seeded((n, n), "normal", self.seed, std=std),
+             seeded((n, n), "normal", self.seed + 1, std=std),
+             seeded((n, n), "normal", self.seed + 2), torch.zeros(n, n, dtype=torch.bfloat16)]
+        dt, reps = _eager(lambda ns: KL.make_matmul_epilogue(ns, 4, n // 32, 4, "relu_bias"), t)
+        return {"value": round(2.0 * n ** 3 / dt / 1e12, 8), "unit": "TFLOP/s", "cores": 1,
+                "kind": "port",
+                "sample": f"{n}^3 through the eager tile-by-tile oracle executor running the "
+                          f"same kernel (1 thread), {reps} runs of {dt:.2f} s"}
+
+
 class Bfp8MatmulWorkload(PlanWorkload):
     """C4 through the drop-in: the multicore tt-lang matmul kernel (13x10
     grid, store(acc=True) over K) with B a ttnn.bfloat8_b tensor, C = A (bf16
@@ -411,6 +502,14 @@ class Bfp8MatmulWorkload(PlanWorkload):
 
     def work_per_step(self):
         return 2.0 * self.M * self.N * self.K
+
+    def traffic_kernels(self):
+        blocks = ((self.M + 255) // 256) * ((self.N + 255) // 256)
+        return [("bfp8_unpack_kernel", None), ("mm_dma_kernel", blocks)]
+
+    def algorithmic_bytes(self):  # A, the packed weight tiles and C once
+        return (2.0 * self.M * self.K + (self.K // 32) * (self.N // 32) * 1088
+                + 2.0 * self.M * self.N)
 
     def make_sets(self):
         import kernel_lib as KL
@@ -469,6 +568,9 @@ class Bfp8LdsMatmulWorkload(Bfp8MatmulWorkload):
     def kernel_name(self):
         return "mm_dq_kernel"
 
+    def traffic_kernels(self):
+        return [("mm_dq_kernel", None)]
+
     def setup(self):
         super().setup()
         from ttlhip import kernels as Kn
@@ -506,6 +608,9 @@ class SdpaWorkload(PlanWorkload):
 
     def work_per_step(self):
         return 4.0 * self.B * self.H * self.S * self.S * self.D
+
+    def algorithmic_bytes(self):  # Q, K, V and O once
+        return 4.0 * 2 * self.B * self.H * self.S * self.D
 
     def make_sets(self):
         import kernel_lib as KL
@@ -559,6 +664,8 @@ WORKLOADS = {
                                                           11008, 4096),
     "matmul_bfp8w_lds_4096x11008": lambda: Bfp8LdsMatmulWorkload("matmul_bfp8w_lds_4096x11008",
                                                                  4096, 11008, 4096),
+    "matmul_bias_relu_4096": lambda: MatmulEpilogueWorkload("matmul_bias_relu_4096", 4096, 4096,
+                                                            4096),
     "sdpa_4x32x4096x128": lambda: SdpaWorkload("sdpa_4x32x4096x128", 4, 32, 4096, 128),
     "reduce_sum_rows_4096": lambda: ReduceWorkload("reduce_sum_rows_4096", 4096),
     "tilize_4096": lambda: TilizeWorkload("tilize_4096", 4096),
@@ -646,7 +753,7 @@ def copy_ceiling(reps: int = 50) -> dict:
     cannot serve them, timed with HIP events on the launch stream."""
     from ttlhip import expr as X
     from ttlhip import kernels as K
-    rows, cols = 8192, 16384  # bf16: 256 MiB
+    rows, cols = 8192, 16384  # bf16: COPY_BYTES (256 MiB)
     pairs = [(torch.ones(rows, cols, dtype=torch.bfloat16, device="cuda"),
               torch.empty(rows, cols, dtype=torch.bfloat16, device="cuda")) for _ in range(2)]
     prog = X.compile_expr(X.Leaf(0, torch.bfloat16))
@@ -684,7 +791,80 @@ def traffic_for(name: str):
         return None
 
 
-def summarize_trace(path: str, steps: int, samples: int = SAMPLES, gap_us: float = 10.0) -> str:
+def summarize_traffic(fetch_csv: str, write_csv: str):
+    """(markdown, json) of HBM bytes per step from two rocprofv3 --pmc passes
+    over a bench.py run (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch).
+    Each counter is scaled by what it reads for the run's copy-ceiling
+    kernel, which moves COPY_BYTES each way; per workload the medians over
+    the dispatches of each kernel it launches (traffic_kernels) are summed
+    and compared with its algorithmic bytes."""
+    import csv
+    import statistics
+
+    def read(path, counter):
+        per = {}
+        with open(path, newline="") as f:
+            for row in csv.DictReader(f):
+                if row["Counter_Name"] != counter:
+                    continue
+                name = row["Kernel_Name"].replace("(anonymous namespace)::", "")
+                name = name.removeprefix("void ").removeprefix("ttlh::").split("(")[0]
+                wgs = int(row["Grid_Size"]) // max(1, int(row["Workgroup_Size"]))
+                per.setdefault((name, wgs), []).append(float(row["Counter_Value"]))
+        return per
+
+    fetch, write = read(fetch_csv, "FETCH_SIZE"), read(write_csv, "WRITE_SIZE")
+    cal = next(k for k in fetch if k[0].startswith("flat_kernel<1, 1u, true>"))
+    f_kib, w_kib = statistics.median(fetch[cal]), statistics.median(write[cal])
+    fs, ws = COPY_BYTES / (f_kib * 1024), COPY_BYTES / (w_kib * 1024)
+    out = {"_calibration": {"kernel": cal[0], "bytes_each_way": COPY_BYTES,
+                            "fetch_size_kib": round(f_kib, 1), "write_size_kib": round(w_kib, 1),
+                            "fetch_scale": round(fs, 5), "write_scale": round(ws, 5)}}
+    lines = ["| workload | kernels | HBM bytes / step | algorithmic bytes | ratio |",
+             "|---|---|---|---|---|"]
+    for name, make in WORKLOADS.items():
+        w = make()
+        ks, total = [], 0.0
+        for sub, wgs in w.traffic_kernels():
+            hits = [k for k in fetch if sub in k[0] and (wgs is None or k[1] == wgs) and k in write]
+            if not hits:
+                break
+            k = max(hits, key=lambda k: len(fetch[k]))
+            fm, wm = statistics.median(fetch[k]), statistics.median(write[k])
+            b = (fm * fs + wm * ws) * 1024
+            total += b
+            ks.append({"kernel": k[0], "workgroups": k[1], "dispatches": len(fetch[k]),
+                       "fetch_size_kib_median": round(fm, 1), "write_size_kib_median": round(wm, 1),
+                       "hbm_bytes": round(b)})
+        else:
+            alg = w.algorithmic_bytes()
+            out[name] = {"hbm_bytes_per_launch": round(total), "algorithmic_bytes": round(alg),
+                         "traffic_over_algorithmic": round(total / alg, 4), "kernels": ks}
+            names = " + ".join(f"`{k['kernel']}` ({k['workgroups']} WGs)" for k in ks)
+            lines.append(f"| {name} | {names} | {round(total):,} | {round(alg):,} | "
+                         f"{total / alg:.4f} |")
+    return "\n".join(lines), out
+
+
+def summarize_counters(paths, kernel: str, wgs: int = 0) -> dict:
+    """Median per dispatch of every counter in rocprofv3 --pmc passes
+    (`*_counter_collection.csv`) over the dispatches of the kernel whose name
+    contains `kernel` (and that has `wgs` workgroups, if given)."""
+    import csv
+    import statistics
+    per = {}
+    for path in paths:
+        with open(path, newline="") as f:
+            for row in csv.DictReader(f):
+                name = row["Kernel_Name"]
+                n_wg = int(row["Grid_Size"]) // max(1, int(row["Workgroup_Size"]))
+                if kernel not in name or (wgs and n_wg != wgs):
+                    continue
+                per.setdefault(row["Counter_Name"], []).append(float(row["Counter_Value"]))
+    return {c: {"median": statistics.median(v), "dispatches": len(v)} for c, v in per.items()}
+
+
+def summarize_trace(path: str, steps: int, samples: int = SAMPLES, gap_us: float = 200.0) -> str:
     """Markdown table of kernel durations from a rocprofv3 kernel trace
     (`*_kernel_trace.csv`) of a bench.py run, taken from its steady stretch.
     All dispatches, in start order, are split into bursts that run back to
@@ -740,9 +920,28 @@ def main() -> int:
     ap.add_argument("--trace-summary", metavar="CSV",
                     help="print the timed-replay kernel durations of a rocprofv3 kernel trace of "
                          "a bench.py run made with the same --steps, then exit (no GPU used)")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="print the HBM traffic table of two rocprofv3 --pmc passes (FETCH_SIZE, "
+                         "WRITE_SIZE) over a bench.py run and write profiles/traffic.json, then "
+                         "exit (no GPU used)")
+    ap.add_argument("--counter-summary", nargs="+", metavar="ARG",
+                    help="KERNEL[:WORKGROUPS] CSV...: medians per dispatch of the counters of "
+                         "rocprofv3 --pmc passes for one kernel, as JSON, then exit (no GPU used)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run one 256 MiB device copy (PMC byte-counter calibration)")
     args = ap.parse_args()
+    if args.counter_summary:
+        kern, _, wg = args.counter_summary[0].partition(":")
+        print(json.dumps(summarize_counters(args.counter_summary[1:], kern, int(wg or 0)),
+                         indent=1))
+        return 0
+    if args.traffic_summary:
+        md, js = summarize_traffic(*args.traffic_summary)
+        with open(TRAFFIC_FILE, "w") as f:
+            json.dump(js, f, indent=1)
+            f.write("\n")
+        print(md)
+        return 0
     if args.trace_summary:
         print(summarize_trace(args.trace_summary, args.steps))
         return 0
