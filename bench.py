@@ -19,8 +19,8 @@ own roofline figures:
 
 A "step" is one pass of the hot path over one batch of synthetic input: one
 execution of the kernel's launch plan over one resident buffer set.  Inputs
-are in HBM before the timed region; elementwise configs rotate buffer sets
-totalling > 256 MB so the Infinity Cache cannot serve them.
+are in HBM before the timed region; every workload rotates buffer sets
+spanning > 1.2 GB (ROTATE_BYTES) so the 256 MB Infinity Cache cannot serve them.
 Every workload times exactly K steps, at steady state: a HIP graph of the K
 steps is first replayed back to back, without a host synchronisation, over at
 least PREROLL_MS (MFMA workloads MFMA_PREROLL_MS) and PREROLL_MIN_STEPS
@@ -51,6 +51,10 @@ PREROLL_MS = 10.0              # steady work queued ahead of the timed steps (ms
 PREROLL_MIN_STEPS = 50         # ... and at least this many steps
 MFMA_PREROLL_MS = 30.0         # MFMA workloads: the clock settles at the power cap
 SAMPLES = 5                    # timed samples of K steps each (median reported)
+ROTATE_BYTES = 1.2e9           # the buffer sets a workload cycles through span at least this
+                               # (> 4 x the 256 MB Infinity Cache: every step's data comes from
+                               # HBM; with ~300 MB of sets the cache served part of it, C2 ran
+                               # 15.7 against 18.2 us)
 COPY_BYTES = 8192 * 16384 * 2  # bytes the copy-ceiling kernel reads (and writes) per launch
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
@@ -139,6 +143,19 @@ class Workload:
         return self.work_per_step()
 
 
+def n_sets(bytes_per_set: float) -> int:
+    """Buffer sets to cycle through: at least 3, spanning ROTATE_BYTES."""
+    return max(3, math.ceil(ROTATE_BYTES / bytes_per_set))
+
+
+def _clone(t):
+    """Another device copy of a ttnn tensor with the same layout (strides of
+    a transposed view, packed block-float tiles)."""
+    import ttnn
+    x = t._tensor.clone(memory_format=torch.preserve_format)
+    return ttnn.Tensor(x, block=t._block, logical_shape=t._logical_shape, layout=t._layout)
+
+
 class PlanWorkload(Workload):
     """A tt-lang kernel traced once by the drop-in `ttl`; each step executes
     its launch plan on one of the resident buffer sets."""
@@ -152,6 +169,8 @@ class PlanWorkload(Workload):
         self.sets = self.make_sets()
         self.plan = self.kernel.trace(*self.sets[0])
         assert len(self.plan.launches) == 1, self.plan.describe()
+        while len(self.sets) < n_sets(self.algorithmic_bytes()):
+            self.sets.append([_clone(t) for t in self.sets[0]])
         self.amaps = [dict(enumerate(s)) for s in self.sets]
         self._execute = P.execute
 
@@ -203,7 +222,7 @@ class EltwiseWorkload(PlanWorkload):
 
         self.kernel = self.make_kernel(ttl)
         base = [ttnn.from_torch(t) for t in self.cpu_inputs()]
-        nsets = max(3, math.ceil(300e6 / self.work_per_step()))
+        nsets = n_sets(self.work_per_step())
         sets = []
         for i in range(nsets):
             ins = base if i == 0 else [ttnn.Tensor(t._tensor.clone()) for t in base]
@@ -264,7 +283,7 @@ class ReduceWorkload(PlanWorkload):
         self.x = seeded((self.n, self.n), "uniform", self.seed, lo=-2, hi=2)
         x = ttnn.from_torch(self.x)
         sc = ttnn.from_torch(torch.ones(32, 32, dtype=torch.bfloat16))
-        nsets = max(3, math.ceil(300e6 / self.work_per_step()))
+        nsets = n_sets(self.work_per_step())
         sets = []
         for i in range(nsets):
             xi = x if i == 0 else ttnn.Tensor(x._tensor.clone())
@@ -297,7 +316,7 @@ class ReduceWorkload(PlanWorkload):
 class TilizeWorkload(Workload):
     """Row-major bf16 -> tilized element order (ttnn TILE_LAYOUT storage,
     16x16 faces) through ttlh_tilize; HBM-bound byte permutation, buffer sets
-    rotated over > 256 MB."""
+    rotated over > 1.2 GB."""
 
     def __init__(self, name, n, seed=5678):
         self.name, self.n, self.seed = name, n, seed
@@ -316,7 +335,7 @@ class TilizeWorkload(Workload):
         self.L = L
         self.x = seeded((self.n, self.n), "uniform", self.seed, lo=-1, hi=1)
         x = self.x.cuda()
-        nsets = max(3, math.ceil(300e6 / self.work_per_step()))
+        nsets = n_sets(self.work_per_step())
         self.sets = [(x if i == 0 else x.clone(),
                       torch.empty(self.n * self.n, dtype=torch.bfloat16, device="cuda"))
                      for i in range(nsets)]
@@ -574,12 +593,12 @@ class Bfp8LdsMatmulWorkload(Bfp8MatmulWorkload):
     def setup(self):
         super().setup()
         from ttlhip import kernels as Kn
-        a, wq, c = self.sets[0]
-        self._a, self._q, self._c = a._tensor, wq._tensor, c._tensor
+        self._ops = [tuple(t._tensor for t in s) for s in self.sets]
         self._mm = Kn.matmul_bfp8w
 
     def launch(self, i):
-        self._mm(self._a, self._q, self._c, two_pass=False)
+        a, q, c = self._ops[i % len(self._ops)]
+        self._mm(a, q, c, two_pass=False)
 
 
 class SdpaWorkload(PlanWorkload):
@@ -998,7 +1017,7 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded; resident in HBM; eltwise buffer sets rotated over > 256 MB)",
+        "data": "synthetic (seeded; resident in HBM; every workload's buffer sets rotated over > 1.2 GB)",
         "config": {"workload": h["config"], "kernel": "tt-lang kernel via drop-in ttl -> "
                    "ttlh_eltwise flat_kernel", "tiles": "32x32", "cb_block": "4x4 tiles",
                    "grid": "(8, 8) tt-lang cores -> one grid-wide launch"},
