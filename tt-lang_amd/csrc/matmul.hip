@@ -1041,13 +1041,20 @@ __device__ __forceinline__ void dma_gemm_main(const MmArgs& p, int bm, int bn, i
   if (s + 2 < nk) stage(I2(), std::false_type(), s + 2);
 }
 
-// One 32x32 accumulator tile, rounded to bf16, into the wave's 128-column
-// LDS quadrant at q (row stride 128 elements): lane pairs swap halves so each
-// lane writes one dword of two adjacent columns.
-__device__ __forceinline__ void epi_tile_to_lds(const f32x16& t, uint16_t* q, int lane) {
+// Column XOR of row r of a staged 64-row half quadrant (rows at a 256-byte
+// pitch): the four rows one dword store instruction writes (r, r + 1, r + 4,
+// r + 5) land in four different 64-byte bank groups, and a 16-byte chunk
+// stays contiguous.
+__device__ __forceinline__ int epi_swz(int r) { return ((r & 1) | ((r >> 1) & 2)) << 5; }
+
+// One 32x32 accumulator tile, rounded to bf16, into a staged half quadrant
+// (rows r0 + 0..31, columns c0 + 0..31): lane pairs swap halves so each lane
+// writes one dword of two adjacent columns.
+__device__ __forceinline__ void epi_tile_to_lds(const f32x16& t, uint16_t* half, int r0, int c0,
+                                                int lane) {
   const bool odd = lane & 1;
-  const int col = (lane & 31) & ~1;
-  const int rbase = 4 * (lane >> 5) + (odd ? 1 : 0);
+  const int col = c0 + ((lane & 31) & ~1);
+  const int rbase = r0 + 4 * (lane >> 5) + (odd ? 1 : 0);
   static_for<8>([&](auto mm) {
     constexpr int m = decltype(mm)::value;
     const float e0 = t[2 * m], e1 = t[2 * m + 1];
@@ -1056,8 +1063,15 @@ __device__ __forceinline__ void epi_tile_to_lds(const f32x16& t, uint16_t* q, in
     const float lo = odd ? n1 : e0;  // column 2c
     const float hi = odd ? e1 : n0;  // column 2c + 1
     const int row = rbase + 8 * (m >> 1) + 2 * (m & 1);
-    *reinterpret_cast<uint32_t*>(q + row * 128 + col) = cvt_pk_bf16x2(lo, hi);
+    *reinterpret_cast<uint32_t*>(half + row * 128 + (col ^ epi_swz(row))) = cvt_pk_bf16x2(lo, hi);
   });
+}
+
+// The 8 staged elements of the quadrant's row `row` (0-127) from column c8.
+__device__ __forceinline__ u32x4 epi_staged(const uint16_t* top, const uint16_t* bot, int row,
+                                            int c8) {
+  const int r = row & 63;
+  return *reinterpret_cast<const u32x4*>((row < 64 ? top : bot) + r * 128 + (c8 ^ epi_swz(r)));
 }
 
 // The wave's 128x128 quadrant, rounded to bf16, into LDS (rows 0-63 in A
@@ -1072,7 +1086,7 @@ __device__ __forceinline__ void quadrant_to_lds(const f32x16 (&acc)[4][4], int w
   uint16_t* const b = bot;
   static_for<16>([&](auto ij) {
     constexpr int i = decltype(ij)::value / 4, j = decltype(ij)::value % 4;
-    epi_tile_to_lds(acc[i][j], (i < 2 ? t : b) + (i & 1) * 32 * 128 + j * 32, lane);
+    epi_tile_to_lds(acc[i][j], i < 2 ? t : b, (i & 1) * 32, j * 32, lane);
   });
   __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the quadrant is in LDS
   asm volatile("" ::: "memory");       // (lanes read what other lanes wrote)
@@ -1287,7 +1301,7 @@ __device__ __forceinline__ void epi_finish(const EltArgs& e, const MmArgs& p, co
 #pragma unroll
   for (int u = 0; u < kEpiG; ++u) {
     const int qi = (g0 + u) * 64 + lane, row = qi >> 4, c8 = (qi & 15) * 8;
-    pr[u] = *reinterpret_cast<const u32x4*>((row < 64 ? top : bot) + (row & 63) * 128 + c8);
+    pr[u] = epi_staged(top, bot, row, c8);
   }
   epi_normalise<NG>(e, s);
   float acc[kEpiG][8];
@@ -1324,9 +1338,9 @@ __device__ __forceinline__ void epi_finish(const EltArgs& e, const MmArgs& p, co
 // the previous group's stores included).
 template <int NG>
 __device__ __forceinline__ void epi_groups(const EltArgs& e, const MmArgs& p, const uint16_t* top,
-                                           const uint16_t* bot, int r0, int c0, int lane) {
-  EpiGroup s0, s1;
-  epi_issue<NG>(e, p, r0, c0, lane, 0, s0);
+                                           const uint16_t* bot, int r0, int c0, int lane,
+                                           EpiGroup& s0) {
+  EpiGroup s1;
   for (int g0 = 0; g0 < 32; g0 += 2 * kEpiG) {
     epi_issue<NG>(e, p, r0, c0, lane, g0 + kEpiG, s1);
     epi_finish<NG>(e, p, top, bot, r0, c0, lane, g0, s0);
@@ -1346,10 +1360,12 @@ __global__ __launch_bounds__(kThreads, 1) void mm_dma_epi_kernel(const EpiArgs a
   const int wn = (wave & 1) * 128;
   f32x16 acc[4][4];
   dma_gemm_main(p, bm, bn, wm, wn, lane, acc);
+  const int r0 = bm * LM + wm, c0 = bn * LN + wn;
+  EpiGroup s0;  // the first group's operand loads overlap the staging
+  epi_issue<NG>(args.e, p, r0, c0, lane, 0, s0);
   uint16_t *top, *bot;
   quadrant_to_lds(acc, wave, lane, top, bot);
-  const int r0 = bm * LM + wm, c0 = bn * LN + wn;
-  epi_groups<NG>(args.e, p, top, bot, r0, c0, lane);
+  epi_groups<NG>(args.e, p, top, bot, r0, c0, lane, s0);
 }
 
 template <bool OUT_BF16, bool ACC>
