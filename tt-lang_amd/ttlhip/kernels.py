@@ -225,7 +225,8 @@ def matmul_eltwise_preferred(prog: StackProgram) -> bool:
     chip runs the epilogue at once and nothing hides its VALU work or its
     operand reads; the pair pays the product's round trip through HBM
     (write + read, 4 bytes per element) instead.  Measured at 4096^3
-    (fused / two launches): one op after the load 0.99-1.11x faster (bias
+    (fused / two launches; buffer sets rotated over 1.5 GB or not, the same
+    ratios within 1%): one op after the load 0.99-1.11x faster (bias
     add 1.03, row / column broadcast 1.00 / 1.01, scale 1.03, relu 1.02,
     max 1.11, div 1.09, sqrt 1.08, rsqrt 1.06, recip 1.00, exp 0.99); two or
     more ops 0.92-0.99x (relu(x + c) 0.99, x + c + d 0.98, exp(x s) c 0.94,
