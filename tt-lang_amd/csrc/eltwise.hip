@@ -124,7 +124,7 @@ __device__ __forceinline__ f32x8 chain_op(uint8_t code, f32x8 acc, f32x8 v) {
     case C_EXP: return vexp_uniform(acc);
     case C_NEG: return -acc;
     case C_ABS: return map8(acc, [](float t) { return fabsf(t); });
-    case C_RELU: return map8(acc, [](float t) { return t != t ? t : fmaxf(t, 0.0f); });
+    case C_RELU: return map8(acc, [](float t) { return relu1(t); });
     default: return 1.0f / acc;  // C_RECIP
   }
 }

@@ -283,6 +283,10 @@ __device__ __attribute__((noinline)) f32x8 unary_ext(int op, f32x8 a, float p, f
   return t;
 }
 
+// relu as torch computes it (clamp_min(x, 0): x unless x < 0), so -0 stays
+// -0 and a NaN passes through; a maximum with 0 would turn -0 into +0.
+__device__ __forceinline__ float relu1(float v) { return v < 0.0f ? 0.0f : v; }
+
 template <bool FULL>
 __device__ __forceinline__ f32x8 unary(int op, f32x8 a, float imm, float imm2 = 0.0f) {
   if constexpr (!FULL) {
@@ -290,7 +294,7 @@ __device__ __forceinline__ f32x8 unary(int op, f32x8 a, float imm, float imm2 = 
       case TTLH_OP_EXP: return vexp(a);
       case TTLH_OP_NEG: return -a;
       case TTLH_OP_ABS: return map8(a, [](float v) { return fabsf(v); });
-      case TTLH_OP_RELU: return map8(a, [](float v) { return v != v ? v : fmaxf(v, 0.0f); });
+      case TTLH_OP_RELU: return map8(a, [](float v) { return relu1(v); });
       default: return 1.0f / a;  // TTLH_OP_RECIP
     }
   }
@@ -302,7 +306,7 @@ __device__ __forceinline__ f32x8 unary(int op, f32x8 a, float imm, float imm2 = 
     case TTLH_OP_TANH: return map8(a, [](float v) { return tanhf(v); });
     case TTLH_OP_ABS: return map8(a, [](float v) { return fabsf(v); });
     case TTLH_OP_NEG: return -a;
-    case TTLH_OP_RELU: return map8(a, [](float v) { return v != v ? v : fmaxf(v, 0.0f); });
+    case TTLH_OP_RELU: return map8(a, [](float v) { return relu1(v); });
     case TTLH_OP_SIGMOID: return map8(a, [](float v) { return 1.0f / (1.0f + expf(-v)); });
     case TTLH_OP_RECIP: return 1.0f / a;
     case TTLH_OP_POWI: return map8(a, [imm](float v) { return powf(v, imm); });
@@ -342,7 +346,7 @@ __device__ __forceinline__ float unary1(float v) {
   else if constexpr (OP == TTLH_OP_RSQRT) return 1.0f / sqrtf(v);
   else if constexpr (OP == TTLH_OP_ABS) return fabsf(v);
   else if constexpr (OP == TTLH_OP_NEG) return -v;
-  else if constexpr (OP == TTLH_OP_RELU) return v != v ? v : fmaxf(v, 0.0f);
+  else if constexpr (OP == TTLH_OP_RELU) return relu1(v);
   else return 1.0f / v;  // TTLH_OP_RECIP
 }
 template <int OP>
