@@ -15,6 +15,8 @@ own roofline figures:
   C4, weights dequantised in LDS   ttlh_matmul_bfp8w (mm_dq_kernel)  TFLOP/s
   C5 SDPA [4,32,4096,128]     tt-lang attention program -> ttlh_sdpa_fwd   TFLOP/s
   row sums 4096^2 (spec reduce_sum)  tt-lang kernel (reduce_rows)  HBM GB/s
+  row softmax 4096^2 in one store   tt-lang kernel -> ttlh_reduce_rows_eltwise  HBM GB/s
+                              (and the same plan as three launches, for comparison)
   tilize 4096^2 bf16 (TILE_LAYOUT)   ttlh_tilize                  HBM GB/s
 
 A "step" is one pass of the hot path over one batch of synthetic input: one
@@ -311,6 +313,96 @@ class ReduceWorkload(PlanWorkload):
                 "kind": "port",
                 "sample": f"the full {self.n}x{self.n} workload through the eager tile-by-tile "
                           f"oracle executor (1 thread), {reps} runs of {dt:.2f} s"}
+
+
+class SoftmaxWorkload(PlanWorkload):
+    """Row softmax of a bf16 matrix written as one tt-lang store whose
+    expression holds the spec's reduce_max and reduce_sum
+    (tests/kernel_lib.py make_softmax_one_store: y = e * broadcast(recip(
+    reduce_sum(e))), e = exp(x - broadcast(reduce_max(x))), one block per
+    row band of 128 tiles, 8x8 grid).  Planned as two row reductions and the
+    elementwise program: one ttlh_reduce_rows_eltwise launch reading x once
+    (`separate`: the same plan run as its three launches, x read three
+    times, for comparison).  HBM-bound; algorithmic bytes = x read once, y
+    written once, the two reduction result tiles written once."""
+
+    def __init__(self, name, n, separate=False, seed=2468):
+        self.name, self.n, self.separate, self.seed = name, n, separate, seed
+        how = ("the plan's three launches (ttlh_reduce x2, ttlh_eltwise)" if separate else
+               "one ttlh_reduce_rows_eltwise launch")
+        self.config = (f"row softmax y = exp(x - max_r) / sum_r exp(x - max_r) in one store "
+                       f"(spec reduce_max / reduce_sum / broadcast), x bf16 {n}x{n} U[-4,4], "
+                       f"per-op bf16 rounding; {how}")
+
+    def kernel_name(self):
+        return "reduce_rows_bf16_kernel" if self.separate else "reduce_rows_eltwise_kernel"
+
+    def traffic_kernels(self):
+        if self.separate:
+            return [("reduce_rows_bf16_kernel", None), ("reduce_rows_wide_kernel", None),
+                    ("eltwise", None)]
+        return [("reduce_rows_eltwise_kernel<256, 1>", None)]
+
+    def work_per_step(self):
+        return 2 * self.n * self.n * 2 + 2 * self.n * 32 * 2
+
+    def make_sets(self):
+        import kernel_lib as KL
+        import ttl
+        import ttnn
+        from oracle.tile_ops import seeded
+        self.kernel = KL.make_softmax_one_store(ttl, gc=self.n // 32, grid=(8, 8))
+        self.x = seeded((self.n, self.n), "uniform", self.seed, lo=-4, hi=4)
+        x = ttnn.from_torch(self.x)
+        sc = ttnn.from_torch(torch.ones(32, 32, dtype=torch.bfloat16))
+        sets = []
+        for i in range(n_sets(self.work_per_step())):
+            xi = x if i == 0 else ttnn.Tensor(x._tensor.clone())
+            sets.append([xi, sc, ttnn.empty((self.n, self.n), dtype=torch.bfloat16)])
+        return sets
+
+    def setup(self):
+        from ttlhip import plan as P
+        super().setup()
+        (l,) = self.plan.launches
+        assert isinstance(l, P.ReduceEltwiseLaunch), self.plan.describe()
+        if self.separate:
+            self.plan = P.Plan(launches=list(l.reds) + [l.ew], created=self.plan.created,
+                               uses_created=self.plan.uses_created)
+
+    def check(self):
+        from oracle import tile_ops as O
+        from ttlhip import plan as P
+        self.launch(0)
+        torch.cuda.synchronize()
+        got = self.sets[0][-1].to_torch()
+        # the other execution of the same plan, bit for bit
+        other = P.Plan(launches=list(self.plan.launches[0].reds) + [self.plan.launches[0].ew]) \
+            if not self.separate else P.Plan(launches=[P.ReduceEltwiseLaunch(
+                self.plan.launches[:2], self.plan.launches[2])])
+        P.execute(other, self.amaps[0])
+        torch.cuda.synchronize()
+        again = self.sets[0][-1].to_torch()
+        ex = torch.softmax(self.x.double(), 1)
+        return {"bit_equal_fused_and_separate": bool(torch.equal(got.view(torch.int16),
+                                                                 again.view(torch.int16))),
+                "max_abs_err_vs_exact": float((got.double() - ex).abs().max()),
+                "max_exact": float(ex.max()),
+                "oracle": "float64 softmax (the per-op bf16 roundings bound the error by 2^-6 "
+                          "max); fused and separate launches compared bit for bit"}
+
+    def cpu_baseline(self):
+        import kernel_lib as KL
+        from oracle.tile_ops import seeded
+        rows = 128  # a bounded sample: 4 tile rows of the full width
+        x = seeded((rows, self.n), "uniform", self.seed, lo=-4, hi=4)
+        t = [x, torch.ones(32, 32, dtype=torch.bfloat16),
+             torch.zeros(rows, self.n, dtype=torch.bfloat16)]
+        dt, reps = _eager(lambda ns: KL.make_softmax_one_store(ns, gc=self.n // 32, grid=(1, 1)), t)
+        nbytes = 2 * rows * self.n * 2 + 2 * rows * 32 * 2
+        return {"value": round(nbytes / dt / 1e9, 5), "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": f"{rows} of the {self.n} rows through the eager tile-by-tile oracle "
+                          f"executor running the same kernel (1 thread), {reps} runs of {dt:.2f} s"}
 
 
 class TilizeWorkload(Workload):
@@ -687,6 +779,9 @@ WORKLOADS = {
                                                             4096),
     "sdpa_4x32x4096x128": lambda: SdpaWorkload("sdpa_4x32x4096x128", 4, 32, 4096, 128),
     "reduce_sum_rows_4096": lambda: ReduceWorkload("reduce_sum_rows_4096", 4096),
+    "softmax_rows_4096": lambda: SoftmaxWorkload("softmax_rows_4096", 4096),
+    "softmax_rows_4096_separate": lambda: SoftmaxWorkload("softmax_rows_4096_separate", 4096,
+                                                          separate=True),
     "tilize_4096": lambda: TilizeWorkload("tilize_4096", 4096),
 }
 HEADLINE = "exp_bcast_mul_4096"

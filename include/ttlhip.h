@@ -235,6 +235,53 @@ int ttlh_reduce_noalloc(const ttlh_instr* prog, const ttlh_operand* in,
                         int64_t x0, int64_t h, int64_t w, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Row reductions and the elementwise program that reads them, one launch
+ *
+ * One row reduction (the arguments of a ttlh_reduce call with dims =
+ * TTLH_REDUCE_DIM1 and the region of ttlh_reduce_rows_eltwise).            */
+typedef struct ttlh_row_reduce {
+  const ttlh_instr* prog;
+  const ttlh_operand* in;
+  int32_t n_instr;
+  int32_t kind;         /* TTLH_REDUCE_SUM / TTLH_REDUCE_MAX */
+  const void* scaler;   /* NULL: scale_imm alone              */
+  int32_t scaler_dtype;
+  float scale_imm;
+  void* out;            /* result of region row r at out[r * out_ld] */
+  int32_t out_dtype;
+  int32_t out_pad;
+  int64_t out_ld;
+} ttlh_row_reduce;
+
+/* The same as ttlh_reduce(red[0]), ..., ttlh_reduce(red[n_red - 1]) (each a
+ * row reduction over the region) followed by ttlh_eltwise(prog, in, n_instr,
+ * out, ...) over that region, in one launch and with the same results in
+ * every output, bit for bit: a row's operands are read from memory once and
+ * a later program's operand that reads an earlier reduction's result for the
+ * same row (its column 0) takes the value in registers.  For a store whose
+ * expression reduces rows and then uses the results on the same rows, e.g.
+ * softmax: exp(x - broadcast(reduce_max(x))) * broadcast(recip(reduce_sum(
+ * exp(x - broadcast(reduce_max(x)))))) (spec ops reduce_max / reduce_sum /
+ * broadcast, docs/sphinx/specs/TTLangSpecification.md:693-761; the
+ * simulator materialises every intermediate block, python/sim/
+ * block.py:870-920).  Returns TTLH_EUNSUPPORTED before launching, and the
+ * caller makes the separate calls, unless: 1 <= n_red <= 3; every program
+ * uses only + - * / max min exp sqrt rsqrt abs neg relu recip; w <= 8192 and
+ * every operand admits 16-byte chunks (w, x0, offsets 8-aligned), as does the
+ * output; for w >= 2048 every reduction program has at most four operands
+ * and only + - * exp neg abs relu recip (so that ttlh_reduce would sum in the
+ * order this launch uses); at most three distinct identity-mapped bf16
+ * operands and four other operands; no output overlaps another output, an
+ * operand or a scaler, except an elementwise output that is an operand read
+ * element for element in place, and a later read of a reduction's result
+ * maps every element of a row to that row's result.                        */
+int ttlh_reduce_rows_eltwise(const ttlh_row_reduce* red, int n_red,
+                             const ttlh_instr* prog, const ttlh_operand* in,
+                             int n_instr, void* out, int out_dtype,
+                             int64_t out_ld, int64_t y0, int64_t x0,
+                             int64_t h, int64_t w, void* stream);
+
+/* ------------------------------------------------------------------------
  * Tilized element order (the TILE_LAYOUT storage of ttnn tensors, which the
  * reference's compiled path requires: python/ttl/ttl_api.py:489-506; the
  * tilize itself lives in un-vendored tt-metal).  Tiles of 32x32 row-major

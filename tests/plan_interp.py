@@ -10,7 +10,8 @@ import torch
 
 from oracle import tile_ops as O
 from ttlhip import _lib as L
-from ttlhip.plan import EltwiseLaunch, FusedMatmulLaunch, MatmulLaunch, ReduceLaunch, SdpaLaunch
+from ttlhip.plan import (EltwiseLaunch, FusedMatmulLaunch, MatmulLaunch, ReduceEltwiseLaunch,
+                         ReduceLaunch, SdpaLaunch)
 
 _TORCH_BIN = {
     L.OP["add"]: torch.add, L.OP["sub"]: torch.sub, L.OP["mul"]: torch.mul,
@@ -175,6 +176,10 @@ def run(plan, args):
             run_sdpa(l, args)
         elif isinstance(l, FusedMatmulLaunch):  # the product materialised, then the program
             run_matmul(l.mm, args)
+            run_eltwise(l.ew, args)
+        elif isinstance(l, ReduceEltwiseLaunch):  # the reductions, then the program
+            for r in l.reds:
+                run_reduce(r, args)
             run_eltwise(l.ew, args)
         else:
             run_matmul(l, args)

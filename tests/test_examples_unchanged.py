@@ -118,7 +118,10 @@ def plan_signature(plan: P.Plan):
     """Everything a plan's launches do (not where in the source they came
     from): launch kinds, stack programs, operand maps, regions, bindings."""
     sig = []
+    flat = []
     for l in plan.launches:
+        flat += (l.reds + [l.ew]) if isinstance(l, P.ReduceEltwiseLaunch) else [l]
+    for l in flat:
         if isinstance(l, (P.EltwiseLaunch, P.ReduceLaunch)):
             steps = [(s.op, s.form, s.rnd, s.imm, s.imm2) for s in l.prog.steps]
             item = [type(l).__name__, tuple(l.region), steps,

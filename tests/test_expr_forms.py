@@ -45,7 +45,8 @@ def softmax_case(seed=5, rows=128, cols=128):
 def test_softmax_in_one_store_plans_reductions_first_and_matches_oracle():
     t = softmax_case()
     got, orc, plan = _both(KL.make_softmax_one_store, t, 2)
-    assert [type(l) for l in plan.launches] == [P.ReduceLaunch, P.ReduceLaunch, P.EltwiseLaunch]
+    (l,) = plan.launches  # the two reductions and the program: one fused launch
+    assert isinstance(l, P.ReduceEltwiseLaunch) and [r.kind for r in l.reds] == ["max", "sum"]
     assert torch.equal(got, orc)
     # the oracle against exact softmax: within a few bf16 roundings
     ex = torch.softmax(t[0].double(), 1)
@@ -57,7 +58,8 @@ def test_softmax_in_one_store_plans_reductions_first_and_matches_oracle():
 def test_row_centring_in_one_store_matches_oracle():
     t = softmax_case(seed=6)
     got, orc, plan = _both(KL.make_softmax_one_store, t, 2, form="center")
-    assert [type(l) for l in plan.launches] == [P.ReduceLaunch, P.EltwiseLaunch]
+    (l,) = plan.launches
+    assert isinstance(l, P.ReduceEltwiseLaunch) and [r.kind for r in l.reds] == ["sum"]
     assert torch.equal(got, orc)
     x = t[0].double()
     ex = x - x.mean(1, keepdim=True)

@@ -40,7 +40,7 @@ def test_reductions_inside_one_store_on_gpu(form):
     x = O.seeded((512, 512), "uniform", 7, lo=-4, hi=4)
     t = [x, torch.ones(32, 32, dtype=torch.bfloat16), torch.zeros(512, 512, dtype=torch.bfloat16)]
     got, orc, plan = _gpu_and_oracle(KL.make_softmax_one_store, t, 2, gc=16, form=form)
-    assert isinstance(plan.launches[0], P.ReduceLaunch)
+    assert isinstance(plan.launches[0], P.ReduceEltwiseLaunch)
     ulp = O.bf16_ulp_diff(got, orc)
     assert int(ulp.max()) <= 2, int(ulp.max())
     if form == "softmax":

@@ -208,6 +208,7 @@ def test_reduction_inside_a_larger_expression_plans_it_first():
     # reduce_sum(...) * 2: the reduction into a plan-owned tensor, then the
     # scale reading it (tests/test_expr_forms.py checks values end to end)
     plan = _one_block_kernel(lambda ob, xb, sb: ob.store(ttl.math.reduce_sum(xb, sb, dims=[1]) * 2.0))
+    # (the scale runs over the result tile, not the reduced rows: two launches)
     assert [type(l) for l in plan.launches] == [P.ReduceLaunch, P.EltwiseLaunch]
 
 

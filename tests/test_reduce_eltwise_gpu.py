@@ -1,0 +1,149 @@
+"""ttlh_reduce_rows_eltwise on the MI355X: row reductions and the elementwise
+program reading their results in one launch must leave every output (the
+program's and each reduction's result tiles) bit for bit as the separate
+ttlh_reduce and ttlh_eltwise calls leave them, which tests/test_reduce_gpu.py
+and tests/test_eltwise_gpu.py check against the oracle.  Forms: softmax
+(reduce_max, reduce_sum of exp(x - m), exp(x - m) / sum; python/sim-style
+per-op bf16 rounding), row centring with a scaled sum, and an RMS-style
+normalisation with a row-vector operand read from memory.  Widths cover both
+launch layouts (a wave per row below 2048 columns, a workgroup per row from
+2048) and ragged chunk counts; refusals must leave nothing launched.
+"""
+
+import pytest
+import torch
+
+from oracle import tile_ops as O
+from ttlhip import expr as X
+from ttlhip import kernels as Kn
+
+pytestmark = pytest.mark.gpu
+
+B16 = torch.bfloat16
+
+
+def _leaf(m):
+    return X.Leaf(m, m.tensor.dtype)
+
+
+def _ops(prog):
+    return [s.leaf.ref if s.leaf is not None else None for s in prog.steps]
+
+
+def _row_result(t):  # a reduction's result read as its row's value (column 0)
+    return Kn.OperandMap(t, col_mask=0)
+
+
+def _case(form, h, w, seed):
+    x = O.seeded((h, w), "uniform", seed, lo=-4, hi=4).cuda()
+    xm = Kn.OperandMap(x)
+    t1 = torch.full((h, 32), 5.0, dtype=B16, device="cuda")
+    t2 = torch.full((h, 32), 5.0, dtype=B16, device="cuda")
+    scaler = torch.full((1, 1), 1.0, dtype=B16, device="cuda")
+    if form == "softmax":
+        p1 = X.compile_expr(_leaf(xm))
+        e = X.Unary("exp", X.Binary("sub", _leaf(xm), _leaf(_row_result(t1)), B16), B16)
+        p2 = X.compile_expr(e)
+        e2 = X.Unary("exp", X.Binary("sub", _leaf(xm), _leaf(_row_result(t1)), B16), B16)
+        fin = X.compile_expr(X.Binary("mul", e2, X.Unary("recip", _leaf(_row_result(t2)), B16),
+                                      B16))
+        reds = [Kn.RowReduce(p1, _ops(p1), "max", t1, (0, 0), True, scaler),
+                Kn.RowReduce(p2, _ops(p2), "sum", t2, (0, 0), True, scaler)]
+    elif form == "center":
+        p1 = X.compile_expr(_leaf(xm))
+        fin = X.compile_expr(X.Binary("sub", _leaf(xm),
+                                      X.Binary("mul", _leaf(_row_result(t1)), X.Const(1.0 / w),
+                                               B16), B16))
+        reds = [Kn.RowReduce(p1, _ops(p1), "sum", t1, (0, 0), True, None, 0.5)]
+    else:  # rms: x * rsqrt(mean(x * x) + eps) * g, g a row vector read from memory
+        g = O.seeded((1, w), "uniform", seed + 1, lo=0.5, hi=1.5).cuda()
+        p1 = X.compile_expr(X.Binary("mul", _leaf(xm), _leaf(xm), B16))
+        ms = X.Binary("add", _leaf(_row_result(t1)), X.Const(1e-3), B16)
+        fin = X.compile_expr(X.Binary("mul", X.Binary("mul", _leaf(xm), X.Unary("rsqrt", ms, B16),
+                                                      B16), _leaf(Kn.OperandMap(g)), B16))
+        reds = [Kn.RowReduce(p1, _ops(p1), "sum", t1, (0, 0), True, None, 1.0 / w)]
+    out = torch.full((h, w), 7.0, dtype=B16, device="cuda")
+    return reds, fin, out, [r.out for r in reds]
+
+
+def _separate(reds, fin, out):
+    h, w = out.shape
+    for r in reds:
+        Kn.reduce(r.prog, r.operands, r.kind, [1], r.out, (0, 0, h, w), r.out_origin, r.out_pad,
+                  r.scaler, r.scale)
+    Kn.eltwise(fin, _ops(fin), out, region=(0, 0, h, w))
+
+
+def _bits(t):
+    return t.view(torch.int16).cpu()
+
+
+@pytest.mark.parametrize("form", ["softmax", "center", "rms"])
+@pytest.mark.parametrize("w", [128, 1056, 2048, 4096, 6144, 8192])
+def test_one_launch_equals_separate_calls(form, w):
+    print(f"reduce_rows_eltwise {form} w={w}", flush=True)
+    h = 96
+    reds, fin, out, temps = _case(form, h, w, seed=w + len(form))
+    assert Kn.reduce_rows_eltwise(reds, fin, _ops(fin), out, (0, 0, h, w))
+    torch.cuda.synchronize()
+    fused = [_bits(out)] + [_bits(t) for t in temps]
+    reds2, fin2, out2, temps2 = _case(form, h, w, seed=w + len(form))
+    _separate(reds2, fin2, out2)
+    torch.cuda.synchronize()
+    sep = [_bits(out2)] + [_bits(t) for t in temps2]
+    for a, b in zip(fused, sep):
+        assert torch.equal(a, b), int((a != b).sum())
+    if form == "softmax":  # and it is a softmax of x
+        x = O.seeded((h, w), "uniform", w + len(form), lo=-4, hi=4).double()
+        ex = torch.softmax(x, 1)
+        got = out.double().cpu()
+        assert float((got - ex).abs().max()) <= 2 ** -6 * float(ex.max())
+
+
+def test_region_offset_and_in_place_output():
+    print("reduce_rows_eltwise region offset, in place", flush=True)
+    big = O.seeded((160, 4096 + 64), "uniform", 3, lo=-3, hi=3).cuda()
+    ref = big.clone()
+    y0, x0, h, w = 32, 64, 96, 4096
+    xm = Kn.OperandMap(big)
+    t = torch.zeros(200, 64, dtype=B16, device="cuda")
+    p1 = X.compile_expr(_leaf(xm))
+    rm = Kn.OperandMap(t, col_mask=0, row_off=-y0 + 8, col_off=16)  # result rows from (8, 16)
+    fin = X.compile_expr(X.Binary("sub", _leaf(xm), _leaf(rm), B16))
+    red = Kn.RowReduce(p1, _ops(p1), "max", t, (8, 16), False, None, 1.0)
+    assert Kn.reduce_rows_eltwise([red], fin, _ops(fin), big, (y0, x0, h, w))  # in place
+    torch.cuda.synchronize()
+    t2 = torch.zeros(200, 64, dtype=B16, device="cuda")
+    rm2 = Kn.OperandMap(t2, col_mask=0, row_off=-y0 + 8, col_off=16)
+    xm2 = Kn.OperandMap(ref)
+    p1b = X.compile_expr(_leaf(xm2))
+    fin2 = X.compile_expr(X.Binary("sub", _leaf(xm2), _leaf(rm2), B16))
+    Kn.reduce(p1b, _ops(p1b), "max", [1], t2, (y0, x0, h, w), (8, 16), False, None, 1.0)
+    Kn.eltwise(fin2, _ops(fin2), ref, region=(y0, x0, h, w))
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(big), _bits(ref))
+    assert torch.equal(_bits(t), _bits(t2))
+
+
+def test_refusals_launch_nothing():
+    print("reduce_rows_eltwise refusals", flush=True)
+    h, w = 64, 4096
+    reds, fin, out, temps = _case("softmax", h, w, seed=9)
+    before = _bits(out)
+    # a row wider than the fused kernel holds
+    wide = torch.zeros(h, 16384, dtype=B16, device="cuda")
+    wm = Kn.OperandMap(wide)
+    p = X.compile_expr(_leaf(wm))
+    r = Kn.RowReduce(p, _ops(p), "sum", temps[0], (0, 0), True, None)
+    fw = X.compile_expr(X.Binary("add", _leaf(wm), _leaf(_row_result(temps[0])), B16))
+    assert not Kn.reduce_rows_eltwise([r], fw, _ops(fw), wide, (0, 0, h, 16384))
+    # a later stage reading a reduction's result other than as its row's value
+    xm = reds[0].operands[0]
+    bad = X.compile_expr(X.Binary("add", _leaf(xm), _leaf(Kn.OperandMap(temps[0], col_mask=31)),
+                                  B16))
+    assert not Kn.reduce_rows_eltwise(reds[:1], bad, _ops(bad), out, (0, 0, h, w))
+    # an op outside the fused set
+    lg = X.compile_expr(X.Unary("log", _leaf(xm), B16))
+    assert not Kn.reduce_rows_eltwise(reds[:1], lg, _ops(lg), out, (0, 0, h, w))
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(out), before)

@@ -142,9 +142,9 @@ def test_intermediate_stage_kept_when_read_by_matmul_or_reduced():
     s = torch.full((32, 32), 1.0, dtype=torch.bfloat16)
     _, plan = _plan_run(KL.make_softmax_rows, [x, s, torch.zeros(128, 128, dtype=torch.bfloat16)],
                         2)
-    kinds = [type(l).__name__ for l in plan.launches]
-    assert kinds == ["ReduceLaunch", "ReduceLaunch", "EltwiseLaunch"]
-    assert isinstance(plan.launches[0].out.obj, P._Scratch)
+    (l,) = plan.launches  # reduce_max, reduce_sum, the normalising program: one launch
+    assert isinstance(l, P.ReduceEltwiseLaunch) and [r.kind for r in l.reds] == ["max", "sum"]
+    assert isinstance(l.reds[0].out.obj, P._Scratch)
 
 
 def test_held_tile_split_into_parts():
@@ -199,8 +199,8 @@ def test_softmax_rows_through_intermediate_cbs():
     s = torch.full((32, 32), 1.0, dtype=torch.bfloat16)
     out = torch.zeros(256, 128, dtype=torch.bfloat16)
     got, plan = _plan_run(KL.make_softmax_rows, [x, s, out], 2)
-    assert [type(l).__name__ for l in plan.launches] == ["ReduceLaunch", "ReduceLaunch",
-                                                         "EltwiseLaunch"]
+    (l,) = plan.launches
+    assert isinstance(l, P.ReduceEltwiseLaunch) and [r.kind for r in l.reds] == ["max", "sum"]
     assert torch.equal(got, _oracle(KL.make_softmax_rows, [x, s, out], 2))
     # and it is a softmax: rows sum to 1, close to torch's
     assert float((got.float() - torch.softmax(x.float(), 1)).abs().max()) < 2e-3

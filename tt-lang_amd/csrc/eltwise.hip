@@ -582,6 +582,14 @@ __device__ __forceinline__ float red_combine(int kind, float a, float b) {
   return a + b;
 }
 
+// One value v, scaled by s, into a running reduction r: a sum adds v * s with
+// one rounding (a fused multiply-add, written out so that every kernel
+// rounds the same way whatever the compiler would contract), a maximum takes
+// the rounded product.
+__device__ __forceinline__ float red_acc(int kind, float r, float v, float s) {
+  return kind == TTLH_REDUCE_MAX ? red_combine(kind, r, v * s) : __builtin_fmaf(v, s, r);
+}
+
 // The scaler value through a 32-bit load of its (4-byte aligned, so in-bounds)
 // dword: a uniform 32-bit load compiles to s_load_dword, which the row loads
 // do not wait behind; a 16-bit load is a vector load whose vmcnt(0) wait
@@ -699,7 +707,7 @@ __global__ __launch_bounds__(256) void reduce_rows_kernel(const RedArgs a) {
       const f32x8 v =
           run_program<VEC, false, false, true, false, true>(a.e, q, q, q, q, y, a.e.x0 + xo);
 #pragma unroll
-      for (int k = 0; k < VEC; ++k) r = red_combine(a.kind, r, v[k] * s);
+      for (int k = 0; k < VEC; ++k) r = red_acc(a.kind, r, v[k], s);
     }
   } else {
     constexpr int D = red_depth<MODE>();
@@ -717,7 +725,7 @@ __global__ __launch_bounds__(256) void reduce_rows_kernel(const RedArgs a) {
           if (xo < a.w) {
             const f32x8 v = red_eval<MODE>(a.e, c[i], y, a.e.x0 + xo);
 #pragma unroll
-            for (int k = 0; k < 8; ++k) r = red_combine(a.kind, r, v[k] * s);
+            for (int k = 0; k < 8; ++k) r = red_acc(a.kind, r, v[k], s);
           }
           if (xo + D * S < a.w) c[i] = red_fetch<MODE>(a.e, y, a.e.x0 + xo + D * S);
         }, std::make_integer_sequence<int, D>());
@@ -755,7 +763,7 @@ __global__ __launch_bounds__(256) void reduce_rows_wide_kernel(const RedArgs a) 
       if (xo < a.w) {
         const f32x8 v = red_eval<MODE>(a.e, c[i], y, a.e.x0 + xo);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) r = red_combine(a.kind, r, v[k] * s);
+        for (int k = 0; k < 8; ++k) r = red_acc(a.kind, r, v[k], s);
       }
       if (xo + 2 * S < a.w) c[i] = red_fetch<MODE>(a.e, y, a.e.x0 + xo + 2 * S);
     }, std::make_integer_sequence<int, 2>());
@@ -786,6 +794,11 @@ __device__ __forceinline__ float red_combine_k(float a, float b) {
   if constexpr (KIND == TTLH_REDUCE_MAX) return (a != a || b != b) ? __builtin_nanf("") : fmaxf(a, b);
   else return a + b;
 }
+template <int KIND>
+__device__ __forceinline__ float red_acc_k(float r, float v, float s) {
+  if constexpr (KIND == TTLH_REDUCE_MAX) return red_combine_k<KIND>(r, v * s);
+  else return __builtin_fmaf(v, s, r);
+}
 
 template <bool NT>
 __device__ __forceinline__ u32x4 ld16(uintptr_t u) {
@@ -815,7 +828,7 @@ __global__ __launch_bounds__(256) void reduce_rows_bf16_kernel(const uint16_t* b
       if (xo < w) {
         const f32x8 v = unpack_bf16x8(c[i]);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) r = red_combine_k<KIND>(r, v[k] * s);
+        for (int k = 0; k < 8; ++k) r = red_acc_k<KIND>(r, v[k], s);
       }
       if (xo + 2 * S < w) c[i] = ld16<NT>(rowp + 2 * (xo + 2 * S));
     }
@@ -852,7 +865,7 @@ __global__ __launch_bounds__(256) void reduce_cols_kernel(const RedArgs a) {
         const f32x8 v = run_program<VEC, false, false, true, false, true>(
             a.e, q, q, q, q, a.e.y0 + row, a.e.x0 + xo);
 #pragma unroll
-        for (int k = 0; k < VEC; ++k) acc[k] = red_combine(a.kind, acc[k], v[k] * s);
+        for (int k = 0; k < VEC; ++k) acc[k] = red_acc(a.kind, acc[k], v[k], s);
       }
     } else {
       constexpr int D = red_depth<MODE>();
@@ -869,7 +882,7 @@ __global__ __launch_bounds__(256) void reduce_cols_kernel(const RedArgs a) {
             if (row < re) {
               const f32x8 v = red_eval<MODE>(a.e, c[i], a.e.y0 + row, x);
 #pragma unroll
-              for (int k = 0; k < VEC; ++k) acc[k] = red_combine(a.kind, acc[k], v[k] * s);
+              for (int k = 0; k < VEC; ++k) acc[k] = red_acc(a.kind, acc[k], v[k], s);
             }
             if (row + 4 * D < re) c[i] = red_fetch<MODE>(a.e, a.e.y0 + row + 4 * D, x);
           }, std::make_integer_sequence<int, D>());
@@ -945,16 +958,284 @@ __global__ __launch_bounds__(256) void reduce_all_finish_kernel(const RedArgs a)
   }
 }
 
+// ---------------------------------------------------------------------------
+// Row reductions and the elementwise program that reads their results, in one
+// launch (ttlh_reduce_rows_eltwise).  A workgroup (rows of w >= 2048) or a
+// wave (w < 2048) takes one row: it loads the row's chunks of the resident
+// operands (identity-mapped bf16 operands) into registers once, runs every
+// reduction stage over them in the summation order of the row-reduction
+// kernels above (lane l accumulates its chunks l, l + L, l + 2L, ... in
+// order, L = the lanes of the row; then the wave's butterfly; then, for a
+// workgroup, the wave partials as (p0 + p1) + (p2 + p3)), writes each result
+// where ttlh_reduce writes it, and hands it, rounded to its dtype, to the
+// later stages as the row's scalar; then runs the elementwise stage over the
+// same chunks.  Results are those of the separate ttlh_reduce and
+// ttlh_eltwise calls, bit for bit.
+
+constexpr int kRfRed = 3;     // reduction stages, at most
+constexpr int kRfRes = 3;     // resident operands, at most
+constexpr int kRfMem = 4;     // operands loaded at every use, at most
+constexpr int kRfChunks = 4;  // 8-element chunks of a row per lane, at most
+constexpr int kRfNodes = 8;   // row values a stage derives from earlier results, at most
+constexpr int kRfScal = kRfRed + kRfNodes;  // a row's scalars: results, then derived values
+
+// Each stage's program is compiled on the host into a chain over the row's
+// elements, acc = op(acc, operand) or op(acc) step by step, whose operands
+// are resident rows, other operands, immediates or row scalars: the
+// reductions' results and values derived from them alone (recip of a row sum,
+// a mean plus epsilon under rsqrt), which are computed once per row.
+enum : uint8_t {
+  RC_ADD, RC_SUB, RC_MUL, RC_DIV, RC_MAX, RC_MIN,                        // binary
+  RC_EXP, RC_SQRT, RC_RSQRT, RC_ABS, RC_NEG, RC_RELU, RC_RECIP, RC_COPY  // unary
+};
+// operand sources
+enum : uint8_t { RS_RES = 0x00, RS_MEM = 0x10, RS_SC = 0x20, RS_IMM = 0x30 };
+
+struct RfStep {    // one chain step; step 0 is RC_COPY of the chain's first value
+  uint8_t code;    // RC_*
+  uint8_t src;     // binary steps and step 0: the operand (RS_* + index)
+  uint8_t rnd;     // TTLH_BF16: the result is rounded to bf16
+  uint8_t rev;     // binary: op(operand, acc) instead of op(acc, operand)
+  uint8_t orn;     // TTLH_BF16: the operand is rounded to bf16 before use
+  uint8_t pad[3];
+  float imm;       // RS_IMM operand
+};
+
+struct RfNode {    // row scalar kRfRed + i = code(a, b) (unary: code(a)), rounded per rnd
+  uint8_t code, a, b, rnd;  // a, b: RS_SC + slot or RS_IMM
+  float imm_a, imm_b;
+};
+
+struct RfStage {
+  RfStep step[TTLH_MAX_INSTR];
+  RfNode node[kRfNodes];
+  int32_t n_steps, n_nodes;
+  int32_t kind, out_dtype, out_pad, scaler_dtype;  // reduction stages only from here
+  float scale_imm;
+  const void* scaler;
+  void* out;  // result of region row r at out[r * out_ld]
+  int64_t out_ld;
+};
+
+struct RfArgs {
+  RfStage st[kRfRed + 1];  // the reductions, then (at kRfRed) the elementwise stage
+  EltOperand mem[kRfMem];
+  EltOperand res[kRfRes];
+  void* out;
+  int64_t out_ld;
+  int64_t y0, x0, h, w;
+  int32_t out_dtype, n_red;
+};
+
+__device__ __forceinline__ f32x8 bf16x8_f32(const u32x4 q) {
+  return f32x8{__uint_as_float(q.x << 16), __uint_as_float(q.x & 0xffff0000u),
+               __uint_as_float(q.y << 16), __uint_as_float(q.y & 0xffff0000u),
+               __uint_as_float(q.z << 16), __uint_as_float(q.z & 0xffff0000u),
+               __uint_as_float(q.w << 16), __uint_as_float(q.w & 0xffff0000u)};
+}
+
+// the ops, with the definitions every other kernel uses (exp: exp1, with its
+// range handling hoisted where a chunk allows, giving the same values)
+__device__ __forceinline__ f32x8 rc_op8(uint8_t c, f32x8 a, f32x8 b) {
+  switch (c) {
+    case RC_ADD: return binary8<TTLH_OP_ADD>(a, b);
+    case RC_SUB: return binary8<TTLH_OP_SUB>(a, b);
+    case RC_MUL: return binary8<TTLH_OP_MUL>(a, b);
+    case RC_DIV: return binary8<TTLH_OP_DIV>(a, b);
+    case RC_MAX: return binary8<TTLH_OP_MAX>(a, b);
+    case RC_MIN: return binary8<TTLH_OP_MIN>(a, b);
+    case RC_EXP: return vexp_uniform(a);
+    case RC_SQRT: return unary8<TTLH_OP_SQRT>(a);
+    case RC_RSQRT: return unary8<TTLH_OP_RSQRT>(a);
+    case RC_ABS: return unary8<TTLH_OP_ABS>(a);
+    case RC_NEG: return unary8<TTLH_OP_NEG>(a);
+    case RC_RELU: return unary8<TTLH_OP_RELU>(a);
+    case RC_RECIP: return unary8<TTLH_OP_RECIP>(a);
+    default: return a;  // RC_COPY
+  }
+}
+__device__ __forceinline__ float rc_op1(uint8_t c, float a, float b) {
+  switch (c) {
+    case RC_ADD: return binary1<TTLH_OP_ADD>(a, b);
+    case RC_SUB: return binary1<TTLH_OP_SUB>(a, b);
+    case RC_MUL: return binary1<TTLH_OP_MUL>(a, b);
+    case RC_DIV: return binary1<TTLH_OP_DIV>(a, b);
+    case RC_MAX: return binary1<TTLH_OP_MAX>(a, b);
+    case RC_MIN: return binary1<TTLH_OP_MIN>(a, b);
+    case RC_EXP: return unary1<TTLH_OP_EXP>(a);
+    case RC_SQRT: return unary1<TTLH_OP_SQRT>(a);
+    case RC_RSQRT: return unary1<TTLH_OP_RSQRT>(a);
+    case RC_ABS: return unary1<TTLH_OP_ABS>(a);
+    case RC_NEG: return unary1<TTLH_OP_NEG>(a);
+    case RC_RELU: return unary1<TTLH_OP_RELU>(a);
+    case RC_RECIP: return unary1<TTLH_OP_RECIP>(a);
+    default: return a;  // RC_COPY
+  }
+}
+
+__device__ __forceinline__ float rf_round1(float x, uint8_t rnd) {
+  return rnd == TTLH_BF16 ? round_bf16(x) : x;
+}
+
+// The stage's row scalars derived from earlier results, once per row.  A
+// row's scalars live in LDS, one copy per wave (every wave of a row computes
+// the same values; a wave's LDS accesses take effect in program order), since
+// they are addressed by runtime indices.
+__device__ __forceinline__ void rf_nodes(const RfStage& st, float* sc) {
+#pragma unroll 1
+  for (int i = 0; i < st.n_nodes; ++i) {
+    const RfNode nd = st.node[i];
+    const float x = nd.a == RS_IMM ? nd.imm_a : sc[nd.a - RS_SC];
+    const float y = nd.b == RS_IMM ? nd.imm_b : sc[nd.b - RS_SC];
+    sc[kRfRed + i] = rf_round1(rc_op1(nd.code, x, y), nd.rnd);
+  }
+}
+
+// One stage's chain on one chunk (x: the chunk's first column).
+__device__ __forceinline__ f32x8 rf_chain(const RfArgs& a, const RfStage& st, const u32x4 q0,
+                                          const u32x4 q1, const u32x4 q2, const float* sc,
+                                          int64_t y, int64_t x) {
+  auto fetch = [&](const RfStep& p) -> f32x8 {
+    f32x8 v;
+    if (p.src == RS_RES + 0) v = bf16x8_f32(q0);
+    else if (p.src == RS_RES + 1) v = bf16x8_f32(q1);
+    else if (p.src == RS_RES + 2) v = bf16x8_f32(q2);
+    else if (p.src >= RS_IMM) v = splat(p.imm);
+    else if (p.src >= RS_SC) v = splat(sc[p.src - RS_SC]);
+    else {
+      const EltOperand& op = a.mem[p.src - RS_MEM];
+      v = to_f32<8, false>(op, load_raw<8, false>(op, operand_addr<false>(op, y, x)));
+    }
+    return p.orn == TTLH_BF16 ? round_bf16x8(v) : v;
+  };
+  const RfStep first = st.step[0];
+  f32x8 acc = fetch(first);
+  if (first.rnd == TTLH_BF16) acc = round_bf16x8(acc);
+#pragma unroll 1
+  for (int k = 1; k < st.n_steps; ++k) {
+    const RfStep p = st.step[k];
+    if (p.code <= RC_MIN) {
+      const f32x8 v = fetch(p);
+      acc = p.rev ? rc_op8(p.code, v, acc) : rc_op8(p.code, acc, v);
+    } else {
+      acc = rc_op8(p.code, acc, acc);
+    }
+    if (p.rnd == TTLH_BF16) acc = round_bf16x8(acc);
+  }
+  return acc;
+}
+
+// the reduction's scaler (red_scale's aligned 32-bit read)
+__device__ __forceinline__ float rf_scale(const RfStage& st) {
+  float s = st.scale_imm;
+  if (st.scaler) {
+    const uintptr_t u = reinterpret_cast<uintptr_t>(st.scaler);
+    const uint32_t w =
+        *reinterpret_cast<const __attribute__((address_space(1))) uint32_t*>(u & ~uintptr_t(3));
+    s *= st.scaler_dtype == TTLH_BF16 ? __uint_as_float((u & 2) ? (w & 0xffff0000u) : (w << 16))
+                                      : __uint_as_float(w);
+  }
+  return s;
+}
+
+// result of region row `row` where ttlh_reduce writes it: lane 0 the value,
+// lanes 1-31 the rest of the zero-padded result tile row
+__device__ __forceinline__ void rf_write(const RfStage& st, int64_t row, float v, int li) {
+  const int64_t off = row * st.out_ld + li;
+  if (li != 0 && !(st.out_pad && li < 32)) return;
+  const float x = li == 0 ? v : 0.0f;
+  if (st.out_dtype == TTLH_BF16) static_cast<uint16_t*>(st.out)[off] = f32_to_bf16(x);
+  else static_cast<float*>(st.out)[off] = x;
+}
+
+// chunk c (uniform) of the resident operands, selected through constant
+// indices (so the chunk arrays stay in registers)
+template <int NRES, int NCH>
+__device__ __forceinline__ void rf_chunk(const u32x4 (&rq)[NRES > 0 ? NRES : 1][NCH], int c,
+                                         u32x4& q0, u32x4& q1, u32x4& q2) {
+  q0 = q1 = q2 = u32x4{0u, 0u, 0u, 0u};
+  red_unroll([&](auto cc) {
+    constexpr int k = decltype(cc)::value;
+    if (c == k) {
+      if constexpr (NRES > 0) q0 = rq[0][k];
+      if constexpr (NRES > 1) q1 = rq[1][k];
+      if constexpr (NRES > 2) q2 = rq[2][k];
+    }
+  }, std::make_integer_sequence<int, NCH>());
+}
+
+// LANES: lanes per row (256: a workgroup per row; 64: a wave per row, four
+// rows per workgroup).  NRES: resident operands.  NCH: chunks per lane,
+// ceil(w / (8 LANES)); a lane whose chunk lies past the row's end loads the
+// row's last chunk instead (in bounds, never used), so every load is issued
+// unconditionally and all of them are in flight together.
+template <int LANES, int NRES, int NCH>
+__global__ __launch_bounds__(256) void reduce_rows_eltwise_kernel(const RfArgs a) {
+  constexpr int R = NRES > 0 ? NRES : 1;
+  __shared__ float part[kRfRed][4];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int64_t row = LANES == 256 ? int64_t(blockIdx.x) : int64_t(blockIdx.x) * 4 + wave;
+  if (LANES == 64 && row >= a.h) return;  // wave-uniform (no workgroup barrier in this layout)
+  const int64_t y = a.y0 + row;
+  const int li = LANES == 256 ? t : lane;  // the lane's index in its row
+  constexpr int64_t S = int64_t(LANES) * 8;  // elements from one of a lane's chunks to the next
+  const int64_t xl = int64_t(li) * 8;
+  u32x4 rq[R][NCH];
+  red_unroll([&](auto rr) {
+    constexpr int r = decltype(rr)::value;
+    const uintptr_t base = operand_addr<false>(a.res[r], y, a.x0);
+    red_unroll([&](auto cc) {
+      constexpr int c = decltype(cc)::value;
+      const int64_t xc = xl + c * S < a.w ? xl + c * S : a.w - 8;
+      rq[r][c] = ld16<true>(base + 2 * xc);
+    }, std::make_integer_sequence<int, NCH>());
+  }, std::make_integer_sequence<int, NRES>());
+  __shared__ float scl[4][kRfScal];
+  float* const sc = scl[wave];
+#pragma unroll 1
+  for (int j = 0; j < a.n_red; ++j) {
+    const RfStage& st = a.st[j];
+    rf_nodes(st, sc);
+    const float s = rf_scale(st);
+    float r = red_identity(st.kind);
+#pragma unroll 1
+    for (int c = 0; c < NCH; ++c) {
+      const int64_t xo = xl + c * S;
+      if (xo < a.w) {
+        u32x4 q0, q1, q2;
+        rf_chunk<NRES, NCH>(rq, c, q0, q1, q2);
+        const f32x8 v = rf_chain(a, st, q0, q1, q2, sc, y, a.x0 + xo);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) r = red_acc(st.kind, r, v[k], s);
+      }
+    }
+    r = red_wave(st.kind, r);
+    if constexpr (LANES == 256) {
+      if (lane == 0) part[j][wave] = r;
+      __syncthreads();
+      r = red_combine(st.kind, red_combine(st.kind, part[j][0], part[j][1]),
+                      red_combine(st.kind, part[j][2], part[j][3]));
+    }
+    rf_write(st, row, r, li);
+    sc[j] = st.out_dtype == TTLH_BF16 ? round_bf16(r) : r;
+  }
+  const RfStage& fe = a.st[kRfRed];
+  rf_nodes(fe, sc);
+#pragma unroll 1
+  for (int c = 0; c < NCH; ++c) {
+    const int64_t xo = xl + c * S;
+    if (xo < a.w) {
+      u32x4 q0, q1, q2;
+      rf_chunk<NRES, NCH>(rq, c, q0, q1, q2);
+      store_chunk<8>(a, y, a.x0 + xo, rf_chain(a, fe, q0, q1, q2, sc, y, a.x0 + xo));
+    }
+  }
+}
+
 }  // namespace
 }  // namespace ttlh
 
 using namespace ttlh;
-
-namespace ttlh {
-namespace {
-
-}  // namespace
-}  // namespace ttlh
 
 extern "C" int ttlh_eltwise(const ttlh_instr* prog, const ttlh_operand* in, int n_instr, void* out,
                             int out_dtype, int64_t out_ld, int64_t y0, int64_t x0, int64_t h,
@@ -1232,3 +1513,393 @@ int reduce_impl(const char* who, const ttlh_instr* prog, const ttlh_operand* in,
 
 }  // namespace
 }  // namespace ttlh
+
+namespace ttlh {
+namespace {
+
+// [lo, hi): the bytes operand o can touch over the region (a superset)
+void operand_span(const EltOperand& o, int64_t y0, int64_t x0, int64_t h, int64_t w,
+                  uintptr_t* lo, uintptr_t* hi) {
+  auto first = [](int64_t m, int64_t c) {
+    return m == -1 ? c : (m == ~int64_t(31) ? (c & ~int64_t(31)) : int64_t(0));
+  };
+  const int64_t esz = o.dtype == TTLH_BF16 ? 2 : 4;
+  const int64_t e0 = (first(o.rmask, y0) + o.roff) * o.rs + (first(o.cmask, x0) + o.coff) * o.cs;
+  const int64_t e1 = (mask_max(o.rmask, y0 + h - 1) + o.roff) * o.rs +
+                     (mask_max(o.cmask, x0 + w - 1) + o.coff) * o.cs;
+  const uintptr_t p = reinterpret_cast<uintptr_t>(o.ptr);
+  *lo = p + static_cast<uintptr_t>(e0 * esz);
+  *hi = p + static_cast<uintptr_t>((e1 + 1) * esz);
+}
+
+bool overlap(uintptr_t a0, uintptr_t a1, uintptr_t b0, uintptr_t b1) { return a0 < b1 && b0 < a1; }
+
+// bytes of a row reduction's results, the tile padding included
+void row_result_span(const ttlh_row_reduce& r, int64_t h, uintptr_t* lo, uintptr_t* hi) {
+  const int64_t esz = r.out_dtype == TTLH_BF16 ? 2 : 4;
+  *lo = reinterpret_cast<uintptr_t>(r.out);
+  *hi = *lo + static_cast<uintptr_t>(((h - 1) * r.out_ld + (r.out_pad ? 32 : 1)) * esz);
+}
+
+// whether o reads, at every element (y, x) of the region, reduction r's
+// result for row y (the element ttlh_reduce writes it to)
+bool reads_row_result(const EltOperand& o, const ttlh_row_reduce& r, int64_t y0, int64_t x0,
+                      int64_t h, int64_t w) {
+  if (o.dtype != r.out_dtype) return false;
+  const bool one_col = o.cs == 0 || o.cmask == 0 || w == 1;
+  const bool rows = h == 1 || (o.rmask == -1 && o.rs == r.out_ld);
+  if (!one_col || !rows) return false;
+  const int64_t esz = o.dtype == TTLH_BF16 ? 2 : 4;
+  const int64_t e = ((y0 & o.rmask) + o.roff) * o.rs + ((x0 & o.cmask) + o.coff) * o.cs;
+  return reinterpret_cast<uintptr_t>(o.ptr) + static_cast<uintptr_t>(e * esz) ==
+         reinterpret_cast<uintptr_t>(r.out);
+}
+
+bool same_map(const EltOperand& a, const EltOperand& b) {
+  return a.ptr == b.ptr && a.dtype == b.dtype && a.rs == b.rs && a.cs == b.cs &&
+         a.rmask == b.rmask && a.cmask == b.cmask && a.roff == b.roff && a.coff == b.coff;
+}
+
+uint8_t rc_code(int op) {
+  switch (op) {
+    case TTLH_OP_ADD: return RC_ADD;
+    case TTLH_OP_SUB: return RC_SUB;
+    case TTLH_OP_MUL: return RC_MUL;
+    case TTLH_OP_DIV: return RC_DIV;
+    case TTLH_OP_MAX: return RC_MAX;
+    case TTLH_OP_MIN: return RC_MIN;
+    case TTLH_OP_EXP: return RC_EXP;
+    case TTLH_OP_SQRT: return RC_SQRT;
+    case TTLH_OP_RSQRT: return RC_RSQRT;
+    case TTLH_OP_ABS: return RC_ABS;
+    case TTLH_OP_NEG: return RC_NEG;
+    case TTLH_OP_RELU: return RC_RELU;
+    default: return RC_RECIP;  // TTLH_OP_RECIP (is_inline_op admits no other)
+  }
+}
+
+// The decoded stage program `e` (nj steps; operand i's source src_of[i], an
+// RS_* code) as a chain over the row (RfStep) and the row scalars it needs
+// (RfNode): the expression tree the stack program evaluates, each node with
+// its step's rounding, walked from the root down the one child that depends
+// on the row's elements; the other child of every binary node must be a leaf,
+// an immediate or a subtree of row scalars and immediates only (a row
+// scalar).  Returns false when the program is no such chain.
+bool rf_compile(const EltArgs& e, int nj, const uint8_t* src_of, RfStage& st) {
+  struct Node {
+    uint8_t type;  // 0 operand leaf, 1 immediate, 2 unary, 3 binary
+    uint8_t op, rnd, src;
+    int a, b;
+    float imm;
+    bool uni;      // a row scalar: leaves of row results and immediates only
+  };
+  Node t[2 * TTLH_MAX_INSTR];
+  int nt = 0, stk[TTLH_MAX_STACK + 1], sp = 0;
+  for (int k = 0; k < nj; ++k) {
+    const Ins& ins = e.prog[k];
+    int v = -1;
+    if (ins.src == SRC_OPERAND) {
+      const uint8_t src = src_of[ins.arg];
+      t[nt] = Node{0, 0, TTLH_F32, src, -1, -1, 0.0f, src >= RS_SC && src < RS_IMM};
+      v = nt++;
+    } else if (ins.src == SRC_IMM) {
+      t[nt] = Node{1, 0, TTLH_F32, RS_IMM, -1, -1, ins.imm, true};
+      v = nt++;
+    } else if (ins.src == SRC_POP) {
+      v = stk[sp - 2];
+      stk[sp - 2] = stk[sp - 1];
+      --sp;
+    }
+    int r = v;
+    switch (ins.kind) {
+      case K_SET: stk[sp++] = v; break;  // LOAD / CONST: the stack was empty
+      case K_PUSH: stk[sp++] = v; break;
+      case K_UNARY:
+        t[nt] = Node{2, ins.op, TTLH_F32, 0, stk[sp - 1], -1, 0.0f, t[stk[sp - 1]].uni};
+        r = stk[sp - 1] = nt++;
+        break;
+      case K_BIN:
+        t[nt] = Node{3, ins.op, TTLH_F32, 0, stk[sp - 1], v, 0.0f, t[stk[sp - 1]].uni && t[v].uni};
+        r = stk[sp - 1] = nt++;
+        break;
+      default:  // K_BIN_REV (BIN_POP included: v is the value popped)
+        t[nt] = Node{3, ins.op, TTLH_F32, 0, v, stk[sp - 1], 0.0f, t[stk[sp - 1]].uni && t[v].uni};
+        r = stk[sp - 1] = nt++;
+        break;
+    }
+    t[r].rnd = ins.rnd;
+  }
+  if (sp != 1) return false;
+  auto imm_of = [&](const Node& x) {  // an immediate with its own rounding applied
+    return x.rnd == TTLH_BF16 ? bf16_to_f32(f32_to_bf16(x.imm)) : x.imm;
+  };
+  // a row-scalar subtree as an operand of a node: (RS_SC + slot or RS_IMM, imm)
+  int n_nodes = 0;
+  bool ok = true;
+  auto hoist = [&](auto&& self, int m, float& imm) -> uint8_t {
+    const Node& x = t[m];
+    imm = 0.0f;
+    if (x.type == 1) {
+      imm = imm_of(x);
+      return RS_IMM;
+    }
+    uint8_t a = RS_IMM, b = RS_IMM;
+    float ia = 0.0f, ib = 0.0f;
+    uint8_t code = RC_COPY;
+    if (x.type == 0) {
+      if (x.rnd != TTLH_BF16) return x.src;
+      a = x.src;
+    } else {
+      a = self(self, x.a, ia);
+      if (x.type == 3) b = self(self, x.b, ib);
+      code = rc_code(x.op);
+    }
+    if (n_nodes >= kRfNodes) {
+      ok = false;
+      return RS_IMM;
+    }
+    st.node[n_nodes] = RfNode{code, a, b, x.rnd, ia, ib};
+    return static_cast<uint8_t>(RS_SC + kRfRed + n_nodes++);
+  };
+  RfStep rev_steps[TTLH_MAX_INSTR + 1];
+  int ns = 0;
+  int n = stk[0];
+  for (;;) {
+    const Node& x = t[n];
+    RfStep p{};
+    p.rnd = x.rnd;
+    if (x.uni || x.type <= 1) {  // the chain's first value
+      p.code = RC_COPY;
+      if (x.type == 0) {
+        p.src = x.src;
+      } else {
+        p.src = hoist(hoist, n, p.imm);
+        p.rnd = TTLH_F32;  // a node or an immediate carries its rounding
+      }
+      rev_steps[ns++] = p;
+      break;
+    }
+    if (x.type == 2) {
+      p.code = rc_code(x.op);
+      rev_steps[ns++] = p;
+      n = x.a;
+      continue;
+    }
+    const Node &A = t[x.a], &B = t[x.b];
+    int spine, opnd;
+    if (!A.uni && !B.uni) {
+      if (B.type == 0) spine = x.a, opnd = x.b, p.rev = 0;
+      else if (A.type == 0) spine = x.b, opnd = x.a, p.rev = 1;
+      else return false;  // two operands computed from the row: no chain
+    } else if (B.uni) {
+      spine = x.a, opnd = x.b, p.rev = 0;
+    } else {
+      spine = x.b, opnd = x.a, p.rev = 1;
+    }
+    p.code = rc_code(x.op);
+    const Node& o = t[opnd];
+    if (o.type == 0) {
+      p.src = o.src;
+      p.orn = o.rnd;
+    } else {
+      p.src = hoist(hoist, opnd, p.imm);
+    }
+    rev_steps[ns++] = p;
+    n = spine;
+    if (ns > TTLH_MAX_INSTR) return false;
+  }
+  if (!ok) return false;
+  st.n_steps = ns;
+  st.n_nodes = n_nodes;
+  for (int k = 0; k < ns; ++k) st.step[k] = rev_steps[ns - 1 - k];
+  return true;
+}
+
+}  // namespace
+}  // namespace ttlh
+
+namespace ttlh {
+namespace {
+
+// one workgroup per row group (a row, or four rows of a wave each)
+template <int L, int R, int C>
+int rf_launch(const RfArgs& a, int64_t groups, hipStream_t s) {
+  TTLH_REQUIRE(groups < (int64_t(1) << 31), TTLH_EUNSUPPORTED,
+               "ttlh_reduce_rows_eltwise: region too large");
+  hipLaunchKernelGGL((reduce_rows_eltwise_kernel<L, R, C>), dim3(static_cast<uint32_t>(groups)),
+                     dim3(256), 0, s, a);
+  return check_launch("reduce_rows_eltwise_kernel");
+}
+
+}  // namespace
+}  // namespace ttlh
+
+extern "C" int ttlh_reduce_rows_eltwise(const ttlh_row_reduce* red, int n_red,
+                                        const ttlh_instr* prog, const ttlh_operand* in,
+                                        int n_instr, void* out, int out_dtype, int64_t out_ld,
+                                        int64_t y0, int64_t x0, int64_t h, int64_t w,
+                                        void* stream) {
+  clear_error();
+  const char* who = "ttlh_reduce_rows_eltwise";
+  TTLH_REQUIRE(red && n_red >= 1, TTLH_EINVAL, "%s: needs at least one reduction", who);
+  TTLH_REQUIRE(out && (out_dtype == TTLH_BF16 || out_dtype == TTLH_F32), TTLH_EINVAL,
+               "%s: bad output pointer or dtype", who);
+  TTLH_REQUIRE(h >= 1 && w >= 1 && y0 >= 0 && x0 >= 0 && out_ld >= x0 + w, TTLH_EINVAL,
+               "%s: bad region", who);
+  for (int j = 0; j < n_red; ++j) {
+    const ttlh_row_reduce& r = red[j];
+    TTLH_REQUIRE(r.kind == TTLH_REDUCE_SUM || r.kind == TTLH_REDUCE_MAX, TTLH_EINVAL,
+                 "%s: reduction %d: kind must be TTLH_REDUCE_SUM or TTLH_REDUCE_MAX", who, j);
+    TTLH_REQUIRE(r.out && (r.out_dtype == TTLH_BF16 || r.out_dtype == TTLH_F32), TTLH_EINVAL,
+                 "%s: reduction %d: bad output pointer or dtype", who, j);
+    TTLH_REQUIRE(!r.scaler || r.scaler_dtype == TTLH_BF16 || r.scaler_dtype == TTLH_F32,
+                 TTLH_EINVAL, "%s: reduction %d: bad scaler dtype", who, j);
+    TTLH_REQUIRE(r.out_pad == 0 || r.out_pad == 1, TTLH_EINVAL,
+                 "%s: reduction %d: out_pad must be 0 or 1", who, j);
+    TTLH_REQUIRE(r.out_ld >= (r.out_pad ? 32 : 1), TTLH_EINVAL, "%s: reduction %d: out_ld too small",
+                 who, j);
+  }
+  TTLH_REQUIRE(n_red <= kRfRed, TTLH_EUNSUPPORTED, "%s: at most %d reductions (got %d)", who,
+               kRfRed, n_red);
+  TTLH_REQUIRE(w <= int64_t(kRfChunks) * 2048, TTLH_EUNSUPPORTED,
+               "%s: rows of %lld elements (at most %d)", who, (long long)w, kRfChunks * 2048);
+  TTLH_REQUIRE(aligned16(out) && out_ld % 8 == 0, TTLH_EUNSUPPORTED,
+               "%s: the output does not admit 16-byte chunks", who);
+  const int64_t oesz = out_dtype == TTLH_BF16 ? 2 : 4;
+  const uintptr_t out_lo = reinterpret_cast<uintptr_t>(out) + static_cast<uintptr_t>((y0 * out_ld + x0) * oesz);
+  const uintptr_t out_hi =
+      reinterpret_cast<uintptr_t>(out) + static_cast<uintptr_t>(((y0 + h - 1) * out_ld + x0 + w) * oesz);
+  uintptr_t rlo[kRfRed], rhi[kRfRed];
+  for (int j = 0; j < n_red; ++j) {
+    row_result_span(red[j], h, &rlo[j], &rhi[j]);
+    TTLH_REQUIRE(!overlap(rlo[j], rhi[j], out_lo, out_hi), TTLH_EUNSUPPORTED,
+                 "%s: reduction %d's results overlap the output", who, j);
+    for (int i = 0; i < j; ++i)
+      TTLH_REQUIRE(!overlap(rlo[j], rhi[j], rlo[i], rhi[i]), TTLH_EUNSUPPORTED,
+                   "%s: the results of reductions %d and %d overlap", who, i, j);
+  }
+  for (int j = 0; j < n_red; ++j) {
+    if (!red[j].scaler) continue;
+    const uintptr_t s0 = reinterpret_cast<uintptr_t>(red[j].scaler);
+    const uintptr_t s1 = s0 + (red[j].scaler_dtype == TTLH_BF16 ? 2 : 4);
+    bool clash = overlap(s0, s1, out_lo, out_hi);
+    for (int i = 0; i < n_red; ++i) clash = clash || overlap(s0, s1, rlo[i], rhi[i]);
+    TTLH_REQUIRE(!clash, TTLH_EUNSUPPORTED, "%s: reduction %d's scaler overlaps an output", who, j);
+  }
+
+  RfArgs a = {};
+  a.out = out;
+  a.out_ld = out_ld;
+  a.out_dtype = out_dtype;
+  a.y0 = y0;
+  a.x0 = x0;
+  a.h = h;
+  a.w = w;
+  a.n_red = n_red;
+  int n_mem = 0, n_res = 0;
+  bool wide_order = true;  // every reduction sums as ttlh_reduce's workgroup-per-row kernels do
+  for (int j = 0; j <= n_red; ++j) {
+    const bool fin = j == n_red;
+    const ttlh_instr* pj = fin ? prog : red[j].prog;
+    const ttlh_operand* ij = fin ? in : red[j].in;
+    const int nj = fin ? n_instr : red[j].n_instr;
+    RfStage& st = a.st[fin ? kRfRed : j];
+    EltArgs e = {};
+    ProgInfo pi;
+    const int rc = decode_program(who, pj, ij, nj, y0, x0, h, w, e, pi);
+    if (rc != TTLH_OK) return rc;
+    for (int k = 0; k < nj; ++k)
+      TTLH_REQUIRE(is_inline_op(pj[k].form, pj[k].op), TTLH_EUNSUPPORTED,
+                   "%s: step %d uses op %d (the fused set is + - * / max min exp sqrt rsqrt abs "
+                   "neg relu recip)", who, k, pj[k].op);
+    TTLH_REQUIRE(pi.vec, TTLH_EUNSUPPORTED, "%s: an operand does not admit 16-byte chunks", who);
+    if (!fin) {
+      const bool plain = nj == 1 && pj[0].form == TTLH_FORM_LOAD;
+      const int mode = pi.n_ops < 1 || pi.n_ops > 4 ? 0 : (plain ? 1 : (pi.full ? 0 : 2));
+      wide_order = wide_order && mode != 0;
+      const ttlh_row_reduce& r = red[j];
+      st.kind = r.kind;
+      st.out_dtype = r.out_dtype;
+      st.out_pad = r.out_pad;
+      st.scaler_dtype = r.scaler_dtype;
+      st.scale_imm = r.scale_imm;
+      st.scaler = r.scaler;
+      st.out = r.out;
+      st.out_ld = r.out_ld;
+    }
+    uint8_t src_of[TTLH_MAX_INSTR] = {};
+    for (int i = 0; i < pi.n_ops; ++i) {
+      const EltOperand& o = e.ops[i];
+      int src = -1;
+      for (int p = 0; p < j && p < n_red && src < 0; ++p)
+        if (reads_row_result(o, red[p], y0, x0, h, w)) src = RS_SC + p;
+      uintptr_t lo, hi;
+      operand_span(o, y0, x0, h, w, &lo, &hi);
+      if (src < 0) {
+        for (int p = 0; p < n_red; ++p)
+          TTLH_REQUIRE(!overlap(lo, hi, rlo[p], rhi[p]), TTLH_EUNSUPPORTED,
+                       "%s: stage %d reads reduction %d's results other than as its rows' values",
+                       who, j, p);
+        // rows held in registers: identity-mapped bf16 operands read once (a
+        // row re-read by every row, stride 0, is left to the caches)
+        if (o.dtype == TTLH_BF16 && o.rmask == -1 && o.cmask == -1 && o.cs == 1 && o.vec &&
+            (o.rs != 0 || h == 1)) {
+          for (int q = 0; q < n_res && src < 0; ++q)
+            if (same_map(a.res[q], o)) src = RS_RES + q;
+          if (src < 0 && n_res < kRfRes) {
+            a.res[n_res] = o;
+            src = RS_RES + n_res++;
+          }
+        }
+      }
+      if (src < 0) {
+        TTLH_REQUIRE(n_mem < kRfMem, TTLH_EUNSUPPORTED, "%s: more than %d non-resident operands",
+                     who, kRfMem);
+        a.mem[n_mem] = o;
+        src = RS_MEM + n_mem++;
+      }
+      src_of[i] = static_cast<uint8_t>(src);
+      if (overlap(lo, hi, out_lo, out_hi)) {
+        // only an operand read element for element in place (loaded before the store)
+        const bool in_place = src < RS_MEM && out_dtype == TTLH_BF16 && o.rs == out_ld &&
+                              reinterpret_cast<uintptr_t>(o.ptr) +
+                                      static_cast<uintptr_t>((o.roff * o.rs + o.coff) * 2) ==
+                                  reinterpret_cast<uintptr_t>(out);
+        TTLH_REQUIRE(in_place, TTLH_EUNSUPPORTED,
+                     "%s: stage %d reads the output other than element for element", who, j);
+      }
+    }
+    TTLH_REQUIRE(rf_compile(e, nj, src_of, st), TTLH_EUNSUPPORTED,
+                 "%s: stage %d is not a chain over the row (a binary op of two values computed "
+                 "from the row's elements, or more than %d derived row values)", who, j, kRfNodes);
+  }
+  const bool wide = w >= 2048;
+  TTLH_REQUIRE(!wide || wide_order, TTLH_EUNSUPPORTED,
+               "%s: a reduction over rows of >= 2048 elements with a program outside + - * exp "
+               "neg abs relu recip or more than four operands sums in another order", who);
+  const int64_t groups = wide ? h : (h + 3) / 4;  // row groups: a workgroup's rows
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t lanes = wide ? 256 : 64;
+  const int nch = static_cast<int>((w + 8 * lanes - 1) / (8 * lanes));  // 1..kRfChunks
+  // one instantiation per (lanes, resident operands, chunks per lane)
+#define TTLH_RF3(L, R, C) return rf_launch<L, R, C>(a, groups, s)
+#define TTLH_RF2(L, R)                   \
+  switch (nch) {                         \
+    case 1: TTLH_RF3(L, R, 1);           \
+    case 2: TTLH_RF3(L, R, 2);           \
+    case 3: TTLH_RF3(L, R, 3);           \
+    default: TTLH_RF3(L, R, 4);          \
+  }
+#define TTLH_RF(L)                       \
+  switch (n_res) {                       \
+    case 0: TTLH_RF2(L, 0)               \
+    case 1: TTLH_RF2(L, 1)               \
+    case 2: TTLH_RF2(L, 2)               \
+    default: TTLH_RF2(L, 3)              \
+  }
+  if (wide) TTLH_RF(256)
+  TTLH_RF(64)
+#undef TTLH_RF
+#undef TTLH_RF2
+#undef TTLH_RF3
+}

@@ -72,6 +72,15 @@ class Operand(C.Structure):
     ]
 
 
+class RowReduce(C.Structure):
+    _fields_ = [
+        ("prog", C.POINTER(Instr)), ("in_", C.POINTER(Operand)), ("n_instr", C.c_int32),
+        ("kind", C.c_int32), ("scaler", C.c_void_p), ("scaler_dtype", C.c_int32),
+        ("scale_imm", C.c_float), ("out", C.c_void_p), ("out_dtype", C.c_int32),
+        ("out_pad", C.c_int32), ("out_ld", C.c_int64),
+    ]
+
+
 # every symbol include/ttlhip.h declares, with its ctypes signature
 _i64, _vp, _int = C.c_int64, C.c_void_p, C.c_int
 SIGNATURES = {
@@ -87,6 +96,9 @@ SIGNATURES = {
     "ttlh_reduce_noalloc": (_int, [C.POINTER(Instr), C.POINTER(Operand), _int, _int, _int, _vp,
                                    _int, C.c_float, _vp, _int, _i64, _int, _i64, _i64, _i64, _i64,
                                    _vp]),
+    "ttlh_reduce_rows_eltwise": (_int, [C.POINTER(RowReduce), _int, C.POINTER(Instr),
+                                        C.POINTER(Operand), _int, _vp, _int, _i64, _i64, _i64,
+                                        _i64, _i64, _vp]),
     "ttlh_matmul": (_int, [_vp, _int, _i64, _vp, _int, _i64, _vp, _int, _i64, _i64, _i64, _i64,
                            _int, _vp]),
     "ttlh_matmul_eltwise": (_int, [_vp, _i64, _vp, _i64, _i64, _i64, _i64, C.POINTER(Instr),

@@ -175,6 +175,90 @@ def reduce(prog: StackProgram, operands: Sequence[Optional[OperandMap]], kind: s
            L.stream_ptr(stream))
 
 
+def _program_structs(prog: StackProgram, operands: Sequence[Optional[OperandMap]], region):
+    y0, x0, h, w = region
+    n = len(prog.steps)
+    if len(operands) != n:
+        raise ValueError(f"{n} steps but {len(operands)} operand slots")
+    instrs = (L.Instr * n)()
+    ops = (L.Operand * n)()
+    for k, (s, m) in enumerate(zip(prog.steps, operands)):
+        instrs[k] = L.Instr(s.op, s.form, s.rnd, 0, s.imm, s.imm2)
+        if s.form in (L.FORM_LOAD, L.FORM_PUSH, L.FORM_BIN, L.FORM_BIN_REV):
+            if m is None:
+                raise ValueError(f"step {k} needs an operand")
+            ops[k] = _operand_struct(m, y0, x0, h, w)
+    return instrs, ops, n
+
+
+@dataclass
+class RowReduce:
+    """One row reduction of reduce_rows_eltwise(): the arguments of a
+    reduce(prog, operands, kind, [1], out, region, out_origin, out_pad,
+    scaler, scale) call over the common region."""
+
+    prog: StackProgram
+    operands: Sequence[Optional[OperandMap]]
+    kind: str
+    out: torch.Tensor
+    out_origin: tuple = (0, 0)
+    out_pad: bool = False
+    scaler: Optional[torch.Tensor] = None
+    scale: float = 1.0
+
+
+def reduce_rows_eltwise(reds: Sequence[RowReduce], prog: StackProgram,
+                        operands: Sequence[Optional[OperandMap]], out: torch.Tensor, region,
+                        stream=None) -> bool:
+    """The row reductions `reds` (each a reduce(..., dims=[1]) over
+    `region`), then eltwise(prog, operands, out, region), as one launch of
+    ttlh_reduce_rows_eltwise: the same values in every output, each row's
+    operands read once, a later program reading an earlier result for its
+    own row from registers.  Returns False, having launched nothing, where
+    the library refuses the combination (TTLH_EUNSUPPORTED); the caller then
+    makes the separate calls."""
+    y0, x0, h, w = region
+    if h <= 0 or w <= 0 or y0 < 0 or x0 < 0:
+        raise ValueError(f"bad region {tuple(region)}")
+    _check_device(out, "eltwise output")
+    if out.stride(1) != 1:
+        raise ValueError("eltwise output must have unit column stride")
+    if y0 + h > out.shape[0] or x0 + w > out.shape[1]:
+        raise ValueError(f"region {tuple(region)} outside output {tuple(out.shape)}")
+    keep = []  # ctypes arrays the structs point into, alive until the call returns
+    rr = (L.RowReduce * len(reds))()
+    for j, r in enumerate(reds):
+        _check_device(r.out, "reduce output")
+        if r.out.stride(1) != 1:
+            raise ValueError("reduce output must have unit column stride")
+        if r.kind not in ("sum", "max"):
+            raise ValueError(f"reduce kind must be 'sum' or 'max', got {r.kind!r}")
+        oy, ox = r.out_origin
+        cols = 32 if r.out_pad else 1
+        if oy < 0 or ox < 0 or oy + h > r.out.shape[0] or ox + cols > r.out.shape[1]:
+            raise ValueError(f"reduce result ({h}x{cols} at {(oy, ox)}) outside output "
+                             f"{tuple(r.out.shape)}")
+        instrs, ops, n = _program_structs(r.prog, r.operands, region)
+        keep += [instrs, ops]
+        sp, sdt = 0, 0
+        if r.scaler is not None:
+            if not r.scaler.is_cuda or r.scaler.numel() < 1:
+                raise ValueError("reduce scaler must be a non-empty device tensor")
+            sp, sdt = r.scaler.data_ptr(), L.dtype_code(r.scaler.dtype)
+        optr = r.out.data_ptr() + (oy * r.out.stride(0) + ox) * r.out.element_size()
+        rr[j] = L.RowReduce(instrs, ops, n, L.REDUCE_SUM if r.kind == "sum" else L.REDUCE_MAX,
+                            sp, sdt, float(r.scale), optr, L.dtype_code(r.out.dtype),
+                            int(bool(r.out_pad)), r.out.stride(0))
+    instrs, ops, n = _program_structs(prog, operands, region)
+    st = L.load().ttlh_reduce_rows_eltwise(rr, len(reds), instrs, ops, n, out.data_ptr(),
+                                           L.dtype_code(out.dtype), out.stride(0), y0, x0, h, w,
+                                           L.stream_ptr(stream))
+    if st == L.TTLH_EUNSUPPORTED:
+        return False
+    L.check("ttlh_reduce_rows_eltwise", st)
+    return True
+
+
 def matmul(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, accumulate: bool = False,
            stream=None) -> None:
     """c (=|+=) a @ b on the GPU, fp32 accumulation (bf16 or f32 MFMA)."""

@@ -163,6 +163,24 @@ class ReduceLaunch:
 
 
 @dataclass
+class ReduceEltwiseLaunch:
+    """Row reductions over one region followed by the elementwise launch
+    over the same region that reads their results, e.g. a softmax in one
+    store (reduce_max, reduce_sum, then the normalising program): one
+    ttlh_reduce_rows_eltwise launch reading each row once, with the results
+    of the separate launches in every output.  Where that entry point does
+    not take the combination, the launches run as planned."""
+
+    reds: List[ReduceLaunch]
+    ew: EltwiseLaunch
+    loc: Optional[Tuple[str, int]] = None
+
+    def describe(self) -> str:
+        kinds = ", ".join(f"reduce_{r.kind}" for r in self.reds)
+        return f"{kinds} and {self.ew.describe()} in one launch"
+
+
+@dataclass
 class SdpaLaunch:
     """Attention spelled out tile by tile with the spec's ops
     (docs/sphinx/specs/TTLangSpecification.md:693-761: @, reduce_max, exp,
@@ -1766,12 +1784,15 @@ def build_plan(groups: List[_Group], tensor_ref) -> Plan:
         inl.note_write(g.out_tensor)
     inl.finish(plan)
     _fuse_epilogues(plan)
+    _fuse_row_reductions(plan)
     return plan
 
 
 def _launch_refs(l) -> List[TensorRef]:
     if isinstance(l, FusedMatmulLaunch):
         return _launch_refs(l.mm) + _launch_refs(l.ew)
+    if isinstance(l, ReduceEltwiseLaunch):
+        return [r for x in l.reds for r in _launch_refs(x)] + _launch_refs(l.ew)
     if isinstance(l, (EltwiseLaunch, ReduceLaunch)):
         r = [l.out] + [s.ref for s in l.operands if s is not None]
         if isinstance(l, ReduceLaunch) and l.scaler is not None:
@@ -1811,6 +1832,33 @@ def _fuse_epilogues(plan: Plan) -> None:
                 i += 2
                 continue
         out.append(l)
+        i += 1
+    plan.launches = out
+
+
+_MAX_ROW_REDUCTIONS = 3  # ttlh_reduce_rows_eltwise's limit
+
+
+def _fuse_row_reductions(plan: Plan) -> None:
+    """One to three row reductions (dims [1]) over one region, immediately
+    followed by the elementwise launch over that region: the run becomes one
+    ReduceEltwiseLaunch.  Whether the library takes it (the later programs
+    reading each result as their rows' value, the op set, the row width) is
+    decided when it runs; otherwise the launches run as planned."""
+    L = plan.launches
+    out: List[Any] = []
+    i = 0
+    while i < len(L):
+        j = i
+        while (j < len(L) and j - i < _MAX_ROW_REDUCTIONS and isinstance(L[j], ReduceLaunch)
+               and L[j].dims == (1,) and tuple(L[j].region) == tuple(L[i].region)):
+            j += 1
+        if (j > i and j < len(L) and isinstance(L[j], EltwiseLaunch)
+                and tuple(L[j].region) == tuple(L[i].region)):
+            out.append(ReduceEltwiseLaunch(list(L[i:j]), L[j], L[j].loc or L[i].loc))
+            i = j + 1
+            continue
+        out.append(L[i])
         i += 1
     plan.launches = out
 
@@ -2157,6 +2205,11 @@ def _execute_one(l, args, stream, Kn) -> None:
         if not _execute_fused(l, args, stream, Kn):
             _execute_one(l.mm, args, stream, Kn)
             _execute_one(l.ew, args, stream, Kn)
+    elif isinstance(l, ReduceEltwiseLaunch):
+        if not _execute_row_fused(l, args, stream, Kn):
+            for r in l.reds:
+                _execute_one(r, args, stream, Kn)
+            _execute_one(l.ew, args, stream, Kn)
     elif isinstance(l, SdpaLaunch):
         q, kt, v, y = (r.resolve(args) for r in (l.q, l.kt, l.v, l.out))
         k = kt.t()
@@ -2225,3 +2278,24 @@ def _execute_fused(l: FusedMatmulLaunch, args, stream, Kn, force: bool = False) 
             raise
         return False  # refused before launching (operand alignment): two launches
     return True
+
+
+def _op_maps(operands, args, Kn):
+    return [None if spec is None else
+            Kn.OperandMap(spec.ref.resolve(args), spec.row_mask, spec.col_mask, spec.row_off,
+                          spec.col_off) for spec in operands]
+
+
+def _execute_row_fused(l: ReduceEltwiseLaunch, args, stream, Kn) -> bool:
+    """One ttlh_reduce_rows_eltwise launch; False (nothing launched) where
+    the library refuses the combination."""
+    reds = []
+    for r in l.reds:
+        sc = None
+        if r.scaler is not None:
+            y, x = r.scaler_at
+            sc = r.scaler.resolve(args)[y:y + 1, x:x + 1]
+        reds.append(Kn.RowReduce(r.prog, _op_maps(r.operands, args, Kn), r.kind,
+                                 r.out.resolve(args), r.out_origin, r.out_pad, sc, r.scale))
+    return Kn.reduce_rows_eltwise(reds, l.ew.prog, _op_maps(l.ew.operands, args, Kn),
+                                  l.ew.out.resolve(args), l.ew.region, stream=stream)

@@ -37,6 +37,25 @@ def launch_work(l, args: Dict[Any, Any]) -> Tuple[float, str, float]:
     matmul (MFMA-bound)."""
     if isinstance(l, P.FusedMatmulLaunch):
         return launch_work(l.mm, args)
+    if isinstance(l, P.ReduceEltwiseLaunch):  # each operand once, every output
+        total, seen = 0.0, set()
+        for x in l.reds + [l.ew]:
+            _, _, h, w = x.region
+            out = x.out.resolve(args)
+            total += (h if isinstance(x, P.ReduceLaunch) else h * w) * _elem_size(out.dtype)
+            for spec in x.operands:
+                if spec is None:
+                    continue
+                t = spec.ref.resolve(args)
+                key = (t.data_ptr(), spec.row_mask, spec.col_mask, spec.row_off, spec.col_off)
+                if key in seen or any(t.data_ptr() == r.out.resolve(args).data_ptr()
+                                      for r in l.reds):
+                    continue  # a reduction's result is read from registers
+                seen.add(key)
+                rows = 1 if t.shape[0] == 1 else (32 if spec.row_mask == 31 else h)
+                cols = 1 if t.shape[1] == 1 else (32 if spec.col_mask == 31 else w)
+                total += rows * cols * _elem_size(t.dtype)
+        return float(total), "GB/s", HBM_PEAK_GBS
     if isinstance(l, (P.EltwiseLaunch, P.ReduceLaunch)):
         _, _, h, w = l.region
         out = l.out.resolve(args)
@@ -70,6 +89,11 @@ def _launch_name(l, args) -> str:
     if isinstance(l, P.FusedMatmulLaunch):
         return (f"ttlh_matmul_eltwise {_launch_name(l.mm, args)[len('ttlh_matmul '):]} + "
                 f"{len(l.ew.prog.steps)}-step epilogue")
+    if isinstance(l, P.ReduceEltwiseLaunch):
+        _, _, h, w = l.ew.region
+        kinds = "+".join(r.kind for r in l.reds)
+        return (f"ttlh_reduce_rows_eltwise {h}x{w}: row {kinds}, then "
+                f"{len(l.ew.prog.steps)} steps")
     if isinstance(l, P.ReduceLaunch):
         _, _, h, w = l.region
         return f"ttlh_reduce {l.kind} dims {list(l.dims)} over {h}x{w}, {len(l.prog.steps)} steps"
