@@ -35,6 +35,7 @@
 //    separate "full" kernel variants so the common-op variants fit 8 waves
 //    per SIMD (<= 64 VGPRs) without spilling.
 
+#include <cstring>
 #include <mutex>
 #include <utility>
 
@@ -985,8 +986,9 @@ constexpr int kRfScal = kRfRed + kRfNodes;  // a row's scalars: results, then de
 // reductions' results and values derived from them alone (recip of a row sum,
 // a mean plus epsilon under rsqrt), which are computed once per row.
 enum : uint8_t {
-  RC_ADD, RC_SUB, RC_MUL, RC_DIV, RC_MAX, RC_MIN,                        // binary
-  RC_EXP, RC_SQRT, RC_RSQRT, RC_ABS, RC_NEG, RC_RELU, RC_RECIP, RC_COPY  // unary
+  RC_ADD, RC_SUB, RC_RSUB, RC_MUL, RC_DIV, RC_RDIV, RC_MAX, RC_RMAX, RC_MIN,  // binary: op(acc, v)
+  RC_RMIN,                                   // (R*: op(v, acc))
+  RC_EXP, RC_SQRT, RC_RSQRT, RC_ABS, RC_NEG, RC_RELU, RC_RECIP, RC_COPY       // unary
 };
 // operand sources
 enum : uint8_t { RS_RES = 0x00, RS_MEM = 0x10, RS_SC = 0x20, RS_IMM = 0x30 };
@@ -995,13 +997,11 @@ struct RfStep {    // one chain step; step 0 is RC_COPY of the chain's first val
   uint8_t code;    // RC_*
   uint8_t src;     // binary steps and step 0: the operand (RS_* + index)
   uint8_t rnd;     // TTLH_BF16: the result is rounded to bf16
-  uint8_t rev;     // binary: op(operand, acc) instead of op(acc, operand)
   uint8_t orn;     // TTLH_BF16: the operand is rounded to bf16 before use
-  uint8_t pad[3];
   float imm;       // RS_IMM operand
 };
 
-struct RfNode {    // row scalar kRfRed + i = code(a, b) (unary: code(a)), rounded per rnd
+struct RfNode {    // row scalar kRfRed + i = code(a, b) (unary: code(a); R*: op(b, a)), rounded
   uint8_t code, a, b, rnd;  // a, b: RS_SC + slot or RS_IMM
   float imm_a, imm_b;
 };
@@ -1010,6 +1010,7 @@ struct RfStage {
   RfStep step[TTLH_MAX_INSTR];
   RfNode node[kRfNodes];
   int32_t n_steps, n_nodes;
+  int32_t from_kept;  // > 0: the chain's first from_kept steps are the kept stage's chain
   int32_t kind, out_dtype, out_pad, scaler_dtype;  // reduction stages only from here
   float scale_imm;
   const void* scaler;
@@ -1025,6 +1026,7 @@ struct RfArgs {
   int64_t out_ld;
   int64_t y0, x0, h, w;
   int32_t out_dtype, n_red;
+  int32_t kept;  // reduction whose chain values later stages start from (-1: none)
 };
 
 __device__ __forceinline__ f32x8 bf16x8_f32(const u32x4 q) {
@@ -1036,32 +1038,18 @@ __device__ __forceinline__ f32x8 bf16x8_f32(const u32x4 q) {
 
 // the ops, with the definitions every other kernel uses (exp: exp1, with its
 // range handling hoisted where a chunk allows, giving the same values)
-__device__ __forceinline__ f32x8 rc_op8(uint8_t c, f32x8 a, f32x8 b) {
-  switch (c) {
-    case RC_ADD: return binary8<TTLH_OP_ADD>(a, b);
-    case RC_SUB: return binary8<TTLH_OP_SUB>(a, b);
-    case RC_MUL: return binary8<TTLH_OP_MUL>(a, b);
-    case RC_DIV: return binary8<TTLH_OP_DIV>(a, b);
-    case RC_MAX: return binary8<TTLH_OP_MAX>(a, b);
-    case RC_MIN: return binary8<TTLH_OP_MIN>(a, b);
-    case RC_EXP: return vexp_uniform(a);
-    case RC_SQRT: return unary8<TTLH_OP_SQRT>(a);
-    case RC_RSQRT: return unary8<TTLH_OP_RSQRT>(a);
-    case RC_ABS: return unary8<TTLH_OP_ABS>(a);
-    case RC_NEG: return unary8<TTLH_OP_NEG>(a);
-    case RC_RELU: return unary8<TTLH_OP_RELU>(a);
-    case RC_RECIP: return unary8<TTLH_OP_RECIP>(a);
-    default: return a;  // RC_COPY
-  }
-}
 __device__ __forceinline__ float rc_op1(uint8_t c, float a, float b) {
   switch (c) {
     case RC_ADD: return binary1<TTLH_OP_ADD>(a, b);
     case RC_SUB: return binary1<TTLH_OP_SUB>(a, b);
+    case RC_RSUB: return binary1<TTLH_OP_SUB>(b, a);
     case RC_MUL: return binary1<TTLH_OP_MUL>(a, b);
     case RC_DIV: return binary1<TTLH_OP_DIV>(a, b);
+    case RC_RDIV: return binary1<TTLH_OP_DIV>(b, a);
     case RC_MAX: return binary1<TTLH_OP_MAX>(a, b);
+    case RC_RMAX: return binary1<TTLH_OP_MAX>(b, a);
     case RC_MIN: return binary1<TTLH_OP_MIN>(a, b);
+    case RC_RMIN: return binary1<TTLH_OP_MIN>(b, a);
     case RC_EXP: return unary1<TTLH_OP_EXP>(a);
     case RC_SQRT: return unary1<TTLH_OP_SQRT>(a);
     case RC_RSQRT: return unary1<TTLH_OP_RSQRT>(a);
@@ -1091,10 +1079,40 @@ __device__ __forceinline__ void rf_nodes(const RfStage& st, float* sc) {
   }
 }
 
-// One stage's chain on one chunk (x: the chunk's first column).
+template <int N, typename F>
+__device__ __forceinline__ void rf_each(F&& f) {
+  red_unroll(f, std::make_integer_sequence<int, N>());
+}
+
+__device__ __forceinline__ f32x8 rc_op8(uint8_t c, f32x8 a, f32x8 v) {
+  switch (c) {  // uniform
+    case RC_ADD: return binary8<TTLH_OP_ADD>(a, v);
+    case RC_SUB: return binary8<TTLH_OP_SUB>(a, v);
+    case RC_RSUB: return binary8<TTLH_OP_SUB>(v, a);
+    case RC_MUL: return binary8<TTLH_OP_MUL>(a, v);
+    case RC_DIV: return binary8<TTLH_OP_DIV>(a, v);
+    case RC_RDIV: return binary8<TTLH_OP_DIV>(v, a);
+    case RC_MAX: return binary8<TTLH_OP_MAX>(a, v);
+    case RC_RMAX: return binary8<TTLH_OP_MAX>(v, a);
+    case RC_MIN: return binary8<TTLH_OP_MIN>(a, v);
+    case RC_RMIN: return binary8<TTLH_OP_MIN>(v, a);
+    case RC_EXP: return vexp_uniform(a);
+    case RC_SQRT: return unary8<TTLH_OP_SQRT>(a);
+    case RC_RSQRT: return unary8<TTLH_OP_RSQRT>(a);
+    case RC_ABS: return unary8<TTLH_OP_ABS>(a);
+    case RC_NEG: return unary8<TTLH_OP_NEG>(a);
+    case RC_RELU: return unary8<TTLH_OP_RELU>(a);
+    case RC_RECIP: return unary8<TTLH_OP_RECIP>(a);
+    default: return a;  // RC_COPY
+  }
+}
+
+// One stage's chain on one chunk (x: the chunk's first column, in bounds;
+// q0..q2: the chunk of the resident operands; kept: the kept stage's value
+// on the chunk, the start of a chain with from_kept > 0).
 __device__ __forceinline__ f32x8 rf_chain(const RfArgs& a, const RfStage& st, const u32x4 q0,
                                           const u32x4 q1, const u32x4 q2, const float* sc,
-                                          int64_t y, int64_t x) {
+                                          const f32x8 kept, int64_t y, int64_t x) {
   auto fetch = [&](const RfStep& p) -> f32x8 {
     f32x8 v;
     if (p.src == RS_RES + 0) v = bf16x8_f32(q0);
@@ -1108,18 +1126,18 @@ __device__ __forceinline__ f32x8 rf_chain(const RfArgs& a, const RfStage& st, co
     }
     return p.orn == TTLH_BF16 ? round_bf16x8(v) : v;
   };
-  const RfStep first = st.step[0];
-  f32x8 acc = fetch(first);
-  if (first.rnd == TTLH_BF16) acc = round_bf16x8(acc);
+  f32x8 acc = kept;
+  int k0 = st.from_kept;
+  if (k0 == 0) {
+    const RfStep first = st.step[0];
+    acc = fetch(first);
+    if (first.rnd == TTLH_BF16) acc = round_bf16x8(acc);
+    k0 = 1;
+  }
 #pragma unroll 1
-  for (int k = 1; k < st.n_steps; ++k) {
+  for (int k = k0; k < st.n_steps; ++k) {
     const RfStep p = st.step[k];
-    if (p.code <= RC_MIN) {
-      const f32x8 v = fetch(p);
-      acc = p.rev ? rc_op8(p.code, v, acc) : rc_op8(p.code, acc, v);
-    } else {
-      acc = rc_op8(p.code, acc, acc);
-    }
+    acc = rc_op8(p.code, acc, p.code <= RC_RMIN ? fetch(p) : acc);
     if (p.rnd == TTLH_BF16) acc = round_bf16x8(acc);
   }
   return acc;
@@ -1148,31 +1166,43 @@ __device__ __forceinline__ void rf_write(const RfStage& st, int64_t row, float v
   else static_cast<float*>(st.out)[off] = x;
 }
 
-// chunk c (uniform) of the resident operands, selected through constant
-// indices (so the chunk arrays stay in registers)
-template <int NRES, int NCH>
-__device__ __forceinline__ void rf_chunk(const u32x4 (&rq)[NRES > 0 ? NRES : 1][NCH], int c,
-                                         u32x4& q0, u32x4& q1, u32x4& q2) {
-  q0 = q1 = q2 = u32x4{0u, 0u, 0u, 0u};
-  red_unroll([&](auto cc) {
-    constexpr int k = decltype(cc)::value;
-    if (c == k) {
-      if constexpr (NRES > 0) q0 = rq[0][k];
-      if constexpr (NRES > 1) q1 = rq[1][k];
-      if constexpr (NRES > 2) q2 = rq[2][k];
+// One chunk's values into the lane's running reduction, as red_acc does it
+// element by element: a sum adds fma(v, s, r) (r + v when s = 1: the same
+// value); a maximum takes fmaxf(r, v * s) and records separately whether a
+// value was a NaN (red_combine's propagation: then the lane's result is NaN).
+__device__ __forceinline__ void rf_accumulate(int kind, float s, const f32x8 v, float& r,
+                                              bool& nan) {
+  if (kind == TTLH_REDUCE_SUM) {
+    if (s == 1.0f) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) r += v[k];
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) r = __builtin_fmaf(v[k], s, r);
     }
-  }, std::make_integer_sequence<int, NCH>());
+  } else {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float b = s == 1.0f ? v[k] : v[k] * s;
+      nan |= b != b;
+      r = fmaxf(r, b);
+    }
+  }
 }
 
 // LANES: lanes per row (256: a workgroup per row; 64: a wave per row, four
 // rows per workgroup).  NRES: resident operands.  NCH: chunks per lane,
-// ceil(w / (8 LANES)); a lane whose chunk lies past the row's end loads the
-// row's last chunk instead (in bounds, never used), so every load is issued
-// unconditionally and all of them are in flight together.
-template <int LANES, int NRES, int NCH>
+// ceil(w / (8 LANES)); a chunk past the row's end reads the row's last chunk
+// instead (in bounds, never used), so every load is issued unconditionally
+// and all of them are in flight together.  KEEP: a reduction's chain values
+// are kept for the later stages whose chains start with it.  The chunk loops
+// run at run time (one copy of each chain); a chunk's registers are selected
+// through constant indices.
+template <int LANES, int NRES, int NCH, bool KEEP>
 __global__ __launch_bounds__(256) void reduce_rows_eltwise_kernel(const RfArgs a) {
   constexpr int R = NRES > 0 ? NRES : 1;
   __shared__ float part[kRfRed][4];
+  __shared__ float scl[4][kRfScal];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int64_t row = LANES == 256 ? int64_t(blockIdx.x) : int64_t(blockIdx.x) * 4 + wave;
   if (LANES == 64 && row >= a.h) return;  // wave-uniform (no workgroup barrier in this layout)
@@ -1181,16 +1211,27 @@ __global__ __launch_bounds__(256) void reduce_rows_eltwise_kernel(const RfArgs a
   constexpr int64_t S = int64_t(LANES) * 8;  // elements from one of a lane's chunks to the next
   const int64_t xl = int64_t(li) * 8;
   u32x4 rq[R][NCH];
-  red_unroll([&](auto rr) {
-    constexpr int r = decltype(rr)::value;
+  rf_each<NRES>([&](auto r) {
     const uintptr_t base = operand_addr<false>(a.res[r], y, a.x0);
-    red_unroll([&](auto cc) {
-      constexpr int c = decltype(cc)::value;
-      const int64_t xc = xl + c * S < a.w ? xl + c * S : a.w - 8;
-      rq[r][c] = ld16<true>(base + 2 * xc);
-    }, std::make_integer_sequence<int, NCH>());
-  }, std::make_integer_sequence<int, NRES>());
-  __shared__ float scl[4][kRfScal];
+    rf_each<NCH>([&](auto c) {
+      const int64_t xo = xl + c * S;
+      rq[r][c] = ld16<true>(base + 2 * (xo < a.w ? xo : a.w - 8));
+    });
+  });
+  f32x8 kept[KEEP ? NCH : 1];
+  // chunk c's resident values and kept value (uniform c)
+  auto chunk = [&](int c, u32x4& q0, u32x4& q1, u32x4& q2, f32x8& kv) {
+    q0 = q1 = q2 = u32x4{0u, 0u, 0u, 0u};
+    kv = splat(0.0f);
+    rf_each<NCH>([&](auto cc) {
+      if (c == cc) {
+        if constexpr (NRES > 0) q0 = rq[0][cc];
+        if constexpr (NRES > 1) q1 = rq[1][cc];
+        if constexpr (NRES > 2) q2 = rq[2][cc];
+        if constexpr (KEEP) kv = kept[cc];
+      }
+    });
+  };
   float* const sc = scl[wave];
 #pragma unroll 1
   for (int j = 0; j < a.n_red; ++j) {
@@ -1198,17 +1239,23 @@ __global__ __launch_bounds__(256) void reduce_rows_eltwise_kernel(const RfArgs a
     rf_nodes(st, sc);
     const float s = rf_scale(st);
     float r = red_identity(st.kind);
+    bool nan = false;
 #pragma unroll 1
     for (int c = 0; c < NCH; ++c) {
       const int64_t xo = xl + c * S;
-      if (xo < a.w) {
-        u32x4 q0, q1, q2;
-        rf_chunk<NRES, NCH>(rq, c, q0, q1, q2);
-        const f32x8 v = rf_chain(a, st, q0, q1, q2, sc, y, a.x0 + xo);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) r = red_acc(st.kind, r, v[k], s);
+      u32x4 q0, q1, q2;
+      f32x8 kv;
+      chunk(c, q0, q1, q2, kv);
+      const f32x8 v = rf_chain(a, st, q0, q1, q2, sc, kv, y, a.x0 + (xo < a.w ? xo : a.w - 8));
+      if constexpr (KEEP) {
+        if (j == a.kept)
+          rf_each<NCH>([&](auto cc) {
+            if (c == cc) kept[cc] = v;
+          });
       }
+      if (xo < a.w) rf_accumulate(st.kind, s, v, r, nan);
     }
+    if (nan) r = __builtin_nanf("");
     r = red_wave(st.kind, r);
     if constexpr (LANES == 256) {
       if (lane == 0) part[j][wave] = r;
@@ -1226,8 +1273,9 @@ __global__ __launch_bounds__(256) void reduce_rows_eltwise_kernel(const RfArgs a
     const int64_t xo = xl + c * S;
     if (xo < a.w) {
       u32x4 q0, q1, q2;
-      rf_chunk<NRES, NCH>(rq, c, q0, q1, q2);
-      store_chunk<8>(a, y, a.x0 + xo, rf_chain(a, fe, q0, q1, q2, sc, y, a.x0 + xo));
+      f32x8 kv;
+      chunk(c, q0, q1, q2, kv);
+      store_chunk<8>(a, y, a.x0 + xo, rf_chain(a, fe, q0, q1, q2, sc, kv, y, a.x0 + xo));
     }
   }
 }
@@ -1560,14 +1608,15 @@ bool same_map(const EltOperand& a, const EltOperand& b) {
          a.rmask == b.rmask && a.cmask == b.cmask && a.roff == b.roff && a.coff == b.coff;
 }
 
-uint8_t rc_code(int op) {
+// rev: the op applied as op(operand, acc)
+uint8_t rc_code(int op, bool rev = false) {
   switch (op) {
     case TTLH_OP_ADD: return RC_ADD;
-    case TTLH_OP_SUB: return RC_SUB;
+    case TTLH_OP_SUB: return rev ? RC_RSUB : RC_SUB;
     case TTLH_OP_MUL: return RC_MUL;
-    case TTLH_OP_DIV: return RC_DIV;
-    case TTLH_OP_MAX: return RC_MAX;
-    case TTLH_OP_MIN: return RC_MIN;
+    case TTLH_OP_DIV: return rev ? RC_RDIV : RC_DIV;
+    case TTLH_OP_MAX: return rev ? RC_RMAX : RC_MAX;
+    case TTLH_OP_MIN: return rev ? RC_RMIN : RC_MIN;
     case TTLH_OP_EXP: return RC_EXP;
     case TTLH_OP_SQRT: return RC_SQRT;
     case TTLH_OP_RSQRT: return RC_RSQRT;
@@ -1687,16 +1736,17 @@ bool rf_compile(const EltArgs& e, int nj, const uint8_t* src_of, RfStage& st) {
     }
     const Node &A = t[x.a], &B = t[x.b];
     int spine, opnd;
+    bool rev;
     if (!A.uni && !B.uni) {
-      if (B.type == 0) spine = x.a, opnd = x.b, p.rev = 0;
-      else if (A.type == 0) spine = x.b, opnd = x.a, p.rev = 1;
+      if (B.type == 0) spine = x.a, opnd = x.b, rev = false;
+      else if (A.type == 0) spine = x.b, opnd = x.a, rev = true;
       else return false;  // two operands computed from the row: no chain
     } else if (B.uni) {
-      spine = x.a, opnd = x.b, p.rev = 0;
+      spine = x.a, opnd = x.b, rev = false;
     } else {
-      spine = x.b, opnd = x.a, p.rev = 1;
+      spine = x.b, opnd = x.a, rev = true;
     }
-    p.code = rc_code(x.op);
+    p.code = rc_code(x.op, rev);
     const Node& o = t[opnd];
     if (o.type == 0) {
       p.src = o.src;
@@ -1715,6 +1765,44 @@ bool rf_compile(const EltArgs& e, int nj, const uint8_t* src_of, RfStage& st) {
   return true;
 }
 
+// A reduction whose whole chain begins the chain of later stages (softmax:
+// exp(x - max) summed, then exp(x - max) scaled): its per-chunk values are
+// kept in registers and those stages start from them.  The shared steps may
+// read resident rows, other operands, immediates and reduction results, not
+// the stage-local derived scalars.  The reduction saving the most steps (of a
+// chain of at least two) is kept (a.kept = -1: none).
+void rf_choose_kept(RfArgs& a) {
+  a.kept = -1;
+  int best = 0;
+  for (int j = 0; j < a.n_red; ++j) {
+    const RfStage& sj = a.st[j];
+    if (sj.n_steps < 2) continue;  // a plain load: keeping it saves no arithmetic
+    bool local = false;
+    for (int k = 0; k < sj.n_steps; ++k)
+      local = local || (sj.step[k].src >= RS_SC + kRfRed && sj.step[k].src < RS_IMM &&
+                        (k == 0 || sj.step[k].code <= RC_RMIN));
+    if (local) continue;
+    int saved = 0;
+    for (int q = j + 1; q <= kRfRed; ++q) {
+      if (q >= a.n_red && q != kRfRed) continue;
+      const RfStage& sq = a.st[q];
+      if (sq.n_steps >= sj.n_steps &&
+          memcmp(sq.step, sj.step, sizeof(RfStep) * sj.n_steps) == 0)
+        saved += sj.n_steps;
+    }
+    if (saved > best) best = saved, a.kept = j;
+  }
+  for (int q = 0; q <= kRfRed; ++q) a.st[q].from_kept = 0;
+  if (a.kept < 0) return;
+  const RfStage& sj = a.st[a.kept];
+  for (int q = a.kept + 1; q <= kRfRed; ++q) {
+    if (q >= a.n_red && q != kRfRed) continue;
+    RfStage& sq = a.st[q];
+    if (sq.n_steps >= sj.n_steps && memcmp(sq.step, sj.step, sizeof(RfStep) * sj.n_steps) == 0)
+      sq.from_kept = sj.n_steps;
+  }
+}
+
 }  // namespace
 }  // namespace ttlh
 
@@ -1726,8 +1814,12 @@ template <int L, int R, int C>
 int rf_launch(const RfArgs& a, int64_t groups, hipStream_t s) {
   TTLH_REQUIRE(groups < (int64_t(1) << 31), TTLH_EUNSUPPORTED,
                "ttlh_reduce_rows_eltwise: region too large");
-  hipLaunchKernelGGL((reduce_rows_eltwise_kernel<L, R, C>), dim3(static_cast<uint32_t>(groups)),
-                     dim3(256), 0, s, a);
+  if (a.kept >= 0)
+    hipLaunchKernelGGL((reduce_rows_eltwise_kernel<L, R, C, true>),
+                       dim3(static_cast<uint32_t>(groups)), dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((reduce_rows_eltwise_kernel<L, R, C, false>),
+                       dim3(static_cast<uint32_t>(groups)), dim3(256), 0, s, a);
   return check_launch("reduce_rows_eltwise_kernel");
 }
 
@@ -1873,6 +1965,7 @@ extern "C" int ttlh_reduce_rows_eltwise(const ttlh_row_reduce* red, int n_red,
                  "%s: stage %d is not a chain over the row (a binary op of two values computed "
                  "from the row's elements, or more than %d derived row values)", who, j, kRfNodes);
   }
+  rf_choose_kept(a);
   const bool wide = w >= 2048;
   TTLH_REQUIRE(!wide || wide_order, TTLH_EUNSUPPORTED,
                "%s: a reduction over rows of >= 2048 elements with a program outside + - * exp "
