@@ -1267,6 +1267,7 @@ __global__ __launch_bounds__(256) void reduce_rows_eltwise_kernel(const RfArgs a
     sc[j] = st.out_dtype == TTLH_BF16 ? round_bf16(r) : r;
   }
   const RfStage& fe = a.st[kRfRed];
+  if (fe.n_steps == 0) return;  // reductions alone (ttlh_reduce)
   rf_nodes(fe, sc);
 #pragma unroll 1
   for (int c = 0; c < NCH; ++c) {
@@ -1409,6 +1410,11 @@ int reduce_impl(const char* who, const ttlh_instr* prog, const ttlh_operand* in,
                 void* out, int out_dtype, int64_t out_ld, int out_pad, int64_t y0, int64_t x0,
                 int64_t h, int64_t w, float* workspace, int64_t workspace_bytes, void* stream);
 
+int rows_fused_impl(const char* who, const ttlh_row_reduce* red, int n_red,
+                    const ttlh_instr* prog, const ttlh_operand* in, int n_instr, void* out,
+                    int out_dtype, int64_t out_ld, int64_t y0, int64_t x0, int64_t h, int64_t w,
+                    void* stream);
+
 }  // namespace
 }  // namespace ttlh
 
@@ -1493,6 +1499,17 @@ int reduce_impl(const char* who, const ttlh_instr* prog, const ttlh_operand* in,
   const bool plain = n_instr == 1 && prog[0].form == TTLH_FORM_LOAD;
   const int mode = !pi.vec || pi.n_ops < 1 || pi.n_ops > 4 ? 0 : (plain ? 1 : (pi.full ? 0 : 2));
   const int variant = mode == 0 ? (pi.vec ? 1 : 0) : mode + 1;
+  if (dims == TTLH_REDUCE_DIM1 && !plain) {
+    // a program: the fused row kernel's chain, which its row reductions
+    // share (so a row reduction gives the same values alone and fused);
+    // programs it does not take run on the kernels below
+    const ttlh_row_reduce r = {prog, in, n_instr, kind, scaler, scaler_dtype, scale_imm, out,
+                               out_dtype, out_pad, out_ld};
+    const int rc = rows_fused_impl(who, &r, 1, nullptr, nullptr, 0, nullptr, 0, 0, y0, x0, h, w,
+                                   stream);
+    if (rc != TTLH_EUNSUPPORTED) return rc;
+    clear_error();
+  }
   if (dims != TTLH_REDUCE_DIM0) {
     const bool wide = mode != 0 && w >= 2048;
     const dim3 grid(static_cast<uint32_t>(wide ? h : (h + 3) / 4));
@@ -1833,11 +1850,26 @@ extern "C" int ttlh_reduce_rows_eltwise(const ttlh_row_reduce* red, int n_red,
                                         void* stream) {
   clear_error();
   const char* who = "ttlh_reduce_rows_eltwise";
+  TTLH_REQUIRE(prog && in && n_instr > 0, TTLH_EINVAL, "%s: needs the elementwise program", who);
+  return rows_fused_impl(who, red, n_red, prog, in, n_instr, out, out_dtype, out_ld, y0, x0, h, w,
+                         stream);
+}
+
+namespace ttlh {
+namespace {
+
+// The fused row launch (n_instr == 0: the reductions alone, no elementwise
+// stage and no output).  TTLH_EUNSUPPORTED: nothing launched.
+int rows_fused_impl(const char* who, const ttlh_row_reduce* red, int n_red,
+                    const ttlh_instr* prog, const ttlh_operand* in, int n_instr, void* out,
+                    int out_dtype, int64_t out_ld, int64_t y0, int64_t x0, int64_t h, int64_t w,
+                    void* stream) {
+  const bool has_out = n_instr > 0;
   TTLH_REQUIRE(red && n_red >= 1, TTLH_EINVAL, "%s: needs at least one reduction", who);
-  TTLH_REQUIRE(out && (out_dtype == TTLH_BF16 || out_dtype == TTLH_F32), TTLH_EINVAL,
-               "%s: bad output pointer or dtype", who);
-  TTLH_REQUIRE(h >= 1 && w >= 1 && y0 >= 0 && x0 >= 0 && out_ld >= x0 + w, TTLH_EINVAL,
-               "%s: bad region", who);
+  TTLH_REQUIRE(!has_out || (out && (out_dtype == TTLH_BF16 || out_dtype == TTLH_F32)),
+               TTLH_EINVAL, "%s: bad output pointer or dtype", who);
+  TTLH_REQUIRE(h >= 1 && w >= 1 && y0 >= 0 && x0 >= 0 && (!has_out || out_ld >= x0 + w),
+               TTLH_EINVAL, "%s: bad region", who);
   for (int j = 0; j < n_red; ++j) {
     const ttlh_row_reduce& r = red[j];
     TTLH_REQUIRE(r.kind == TTLH_REDUCE_SUM || r.kind == TTLH_REDUCE_MAX, TTLH_EINVAL,
@@ -1855,12 +1887,16 @@ extern "C" int ttlh_reduce_rows_eltwise(const ttlh_row_reduce* red, int n_red,
                kRfRed, n_red);
   TTLH_REQUIRE(w <= int64_t(kRfChunks) * 2048, TTLH_EUNSUPPORTED,
                "%s: rows of %lld elements (at most %d)", who, (long long)w, kRfChunks * 2048);
-  TTLH_REQUIRE(aligned16(out) && out_ld % 8 == 0, TTLH_EUNSUPPORTED,
+  TTLH_REQUIRE(!has_out || (aligned16(out) && out_ld % 8 == 0), TTLH_EUNSUPPORTED,
                "%s: the output does not admit 16-byte chunks", who);
   const int64_t oesz = out_dtype == TTLH_BF16 ? 2 : 4;
-  const uintptr_t out_lo = reinterpret_cast<uintptr_t>(out) + static_cast<uintptr_t>((y0 * out_ld + x0) * oesz);
+  const uintptr_t out_lo =
+      has_out ? reinterpret_cast<uintptr_t>(out) + static_cast<uintptr_t>((y0 * out_ld + x0) * oesz)
+              : 0;
   const uintptr_t out_hi =
-      reinterpret_cast<uintptr_t>(out) + static_cast<uintptr_t>(((y0 + h - 1) * out_ld + x0 + w) * oesz);
+      has_out ? reinterpret_cast<uintptr_t>(out) +
+                    static_cast<uintptr_t>(((y0 + h - 1) * out_ld + x0 + w) * oesz)
+              : 0;
   uintptr_t rlo[kRfRed], rhi[kRfRed];
   for (int j = 0; j < n_red; ++j) {
     row_result_span(red[j], h, &rlo[j], &rhi[j]);
@@ -1889,9 +1925,12 @@ extern "C" int ttlh_reduce_rows_eltwise(const ttlh_row_reduce* red, int n_red,
   a.w = w;
   a.n_red = n_red;
   int n_mem = 0, n_res = 0;
-  bool wide_order = true;  // every reduction sums as ttlh_reduce's workgroup-per-row kernels do
   for (int j = 0; j <= n_red; ++j) {
     const bool fin = j == n_red;
+    if (fin && !has_out) {
+      a.st[kRfRed].n_steps = 0;
+      break;
+    }
     const ttlh_instr* pj = fin ? prog : red[j].prog;
     const ttlh_operand* ij = fin ? in : red[j].in;
     const int nj = fin ? n_instr : red[j].n_instr;
@@ -1906,9 +1945,6 @@ extern "C" int ttlh_reduce_rows_eltwise(const ttlh_row_reduce* red, int n_red,
                    "neg relu recip)", who, k, pj[k].op);
     TTLH_REQUIRE(pi.vec, TTLH_EUNSUPPORTED, "%s: an operand does not admit 16-byte chunks", who);
     if (!fin) {
-      const bool plain = nj == 1 && pj[0].form == TTLH_FORM_LOAD;
-      const int mode = pi.n_ops < 1 || pi.n_ops > 4 ? 0 : (plain ? 1 : (pi.full ? 0 : 2));
-      wide_order = wide_order && mode != 0;
       const ttlh_row_reduce& r = red[j];
       st.kind = r.kind;
       st.out_dtype = r.out_dtype;
@@ -1967,9 +2003,6 @@ extern "C" int ttlh_reduce_rows_eltwise(const ttlh_row_reduce* red, int n_red,
   }
   rf_choose_kept(a);
   const bool wide = w >= 2048;
-  TTLH_REQUIRE(!wide || wide_order, TTLH_EUNSUPPORTED,
-               "%s: a reduction over rows of >= 2048 elements with a program outside + - * exp "
-               "neg abs relu recip or more than four operands sums in another order", who);
   const int64_t groups = wide ? h : (h + 3) / 4;  // row groups: a workgroup's rows
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t lanes = wide ? 256 : 64;
@@ -1996,3 +2029,6 @@ extern "C" int ttlh_reduce_rows_eltwise(const ttlh_row_reduce* red, int n_red,
 #undef TTLH_RF2
 #undef TTLH_RF3
 }
+
+}  // namespace
+}  // namespace ttlh
