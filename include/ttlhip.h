@@ -266,15 +266,19 @@ typedef struct ttlh_row_reduce {
  * simulator materialises every intermediate block, python/sim/
  * block.py:870-920).  Returns TTLH_EUNSUPPORTED before launching, and the
  * caller makes the separate calls, unless: 1 <= n_red <= 3; every program
- * uses only + - * / max min exp sqrt rsqrt abs neg relu recip; w <= 8192 and
- * every operand admits 16-byte chunks (w, x0, offsets 8-aligned), as does the
- * output; for w >= 2048 every reduction program has at most four operands
- * and only + - * exp neg abs relu recip (so that ttlh_reduce would sum in the
- * order this launch uses); at most three distinct identity-mapped bf16
- * operands and four other operands; no output overlaps another output, an
- * operand or a scaler, except an elementwise output that is an operand read
- * element for element in place, and a later read of a reduction's result
- * maps every element of a row to that row's result.                        */
+ * uses only + - * / max min exp sqrt rsqrt abs neg relu recip and is a chain
+ * over the row (every binary op has at most one operand computed from the
+ * row's elements; the other is an operand, an immediate, or computed from
+ * earlier results and immediates alone, at most 8 such values per stage);
+ * w <= 8192 and every operand admits 16-byte chunks (w, x0, offsets
+ * 8-aligned), as does the output; at most three distinct identity-mapped
+ * bf16 operands and four other operands; no output overlaps another output,
+ * an operand or a scaler, except an elementwise output that is an operand
+ * read element for element in place, and a later read of a reduction's
+ * result maps every element of a row to that row's result.  ttlh_reduce
+ * runs its row reductions of a program (anything but a single LOAD) on this
+ * launch's kernel whenever it takes them, so a row reduction has the same
+ * summation order alone and fused.                                         */
 int ttlh_reduce_rows_eltwise(const ttlh_row_reduce* red, int n_red,
                              const ttlh_instr* prog, const ttlh_operand* in,
                              int n_instr, void* out, int out_dtype,
