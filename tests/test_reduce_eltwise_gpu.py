@@ -7,7 +7,8 @@ and tests/test_eltwise_gpu.py check against the oracle.  Forms: softmax
 per-op bf16 rounding), row centring with a scaled sum, and an RMS-style
 normalisation with a row-vector operand read from memory.  Widths cover both
 launch layouts (a wave per row below 2048 columns, a workgroup per row from
-2048) and ragged chunk counts; refusals must leave nothing launched.
+2048), ragged chunk and row counts and f32 operands and results (read from
+memory at each use); refusals must leave nothing launched.
 """
 
 import pytest
@@ -147,3 +148,41 @@ def test_refusals_launch_nothing():
     assert not Kn.reduce_rows_eltwise(reds[:1], lg, _ops(lg), out, (0, 0, h, w))
     torch.cuda.synchronize()
     assert torch.equal(_bits(out), before)
+
+
+@pytest.mark.parametrize("h,w", [(37, 512), (5, 2048), (33, 3000)])
+def test_ragged_rows_and_fp32_operands(h, w):
+    # f32 x (read from memory at each use, not held in registers), an f32
+    # result for the maximum, a bf16 one for the sum; h not a multiple of the
+    # four rows a workgroup takes below 2048 columns; 3000 columns leave the
+    # last chunk of some lanes past the row's end
+    print(f"reduce_rows_eltwise ragged h={h} w={w}", flush=True)
+    if w % 8:
+        pytest.skip("chunks of 8 columns")
+
+    def case():
+        x = O.seeded((h, w), "uniform", h + w, lo=-3, hi=3).float().cuda()
+        g = O.seeded((1, w), "uniform", h + w + 1, lo=0.5, hi=1.5).cuda()
+        xm, gm = Kn.OperandMap(x), Kn.OperandMap(g)
+        t1 = torch.full((h, 32), 5.0, dtype=torch.float32, device="cuda")
+        t2 = torch.full((h, 32), 5.0, dtype=B16, device="cuda")
+        p1 = X.compile_expr(X.Binary("mul", _leaf(xm), _leaf(gm), torch.float32))
+        p2 = X.compile_expr(X.Unary("exp", X.Binary("sub", _leaf(xm), _leaf(_row_result(t1)),
+                                                    torch.float32), B16))
+        fin = X.compile_expr(X.Binary("div", X.Binary("sub", _leaf(xm), _leaf(_row_result(t1)),
+                                                      B16), _leaf(_row_result(t2)), B16))
+        reds = [Kn.RowReduce(p1, _ops(p1), "max", t1, (0, 0), True, None, 0.5),
+                Kn.RowReduce(p2, _ops(p2), "sum", t2, (0, 0), True)]
+        return reds, fin, torch.full((h, w), 7.0, dtype=B16, device="cuda"), [t1, t2]
+
+    reds, fin, out, temps = case()
+    if w > 8192 or not Kn.reduce_rows_eltwise(reds, fin, _ops(fin), out, (0, 0, h, w)):
+        pytest.fail("the fused launch refused a chain program")
+    torch.cuda.synchronize()
+    reds2, fin2, out2, temps2 = case()
+    _separate(reds2, fin2, out2)
+    torch.cuda.synchronize()
+    for a, b in zip([out] + temps, [out2] + temps2):
+        ai = a.view(torch.int16 if a.dtype == B16 else torch.int32).cpu()
+        bi = b.view(torch.int16 if b.dtype == B16 else torch.int32).cpu()
+        assert torch.equal(ai, bi), int((ai != bi).sum())
