@@ -309,3 +309,30 @@ def test_flat_path_two_chunks_per_lane(h, out_dtype):
     got = run_gpu(e, env, {}, (h, w), out_dtype)
     ulp = O.bf16_ulp_diff(got.bfloat16(), O.eval_expr(e, env).bfloat16())
     assert int(ulp.max()) <= 1
+
+
+@pytest.mark.parametrize("h,w", [(64, 512), (96, 1536), (40, 4096), (17, 8192)])
+def test_row_kernel_stack_programs_with_row_constants(h, w):
+    # Programs that are not linear chains run on the row kernel when every
+    # binary op has at most one operand computed from the row (rows of 512+
+    # columns): a softmax-style exp(x - m) * recip(s) and a scale-and-shift
+    # (x - m) * rsqrt(v + eps) * g + b, with m, s, v column broadcasts
+    # (constant along a row) and g, b row vectors.  Against the oracle (exp
+    # within 1 bf16 ulp), and bit for bit against the generic interpreter,
+    # which runs the same program over the first 504 columns (narrower than
+    # the row kernel takes).
+    x = _u((h, w), 40, lo=-4, hi=4)
+    m, s = _u((h, 1), 41), _u((h, 1), 42, lo=0.5, hi=4.0)
+    var = _u((h, 1), 43, lo=0.1, hi=2.0)
+    g, b = _u((1, w), 44), _u((1, w), 45)
+    env = {"x": x, "m": m, "s": s, "v": var, "g": g, "b": b}
+    e1 = ("mul", ("exp", ("sub", ("leaf", "x"), ("leaf", "m"))), ("recip", ("leaf", "s")))
+    e2 = ("add", ("mul", ("mul", ("sub", ("leaf", "x"), ("leaf", "m")),
+                          ("rsqrt", ("add", ("leaf", "v"), ("const", 1e-3)))), ("leaf", "g")),
+          ("leaf", "b"))
+    got1 = run_gpu(e1, env, {}, (h, w), torch.bfloat16)
+    assert int(O.bf16_ulp_diff(got1, O.eval_expr(e1, env)).max()) <= 1
+    for e in (e1, e2):
+        full = run_gpu(e, env, {}, (h, w), torch.bfloat16)
+        part = run_gpu(e, env, {}, (h, w), torch.bfloat16, region=(0, 0, h, 504))
+        assert torch.equal(full[:, :504].view(torch.int16), part[:, :504].view(torch.int16))

@@ -977,14 +977,17 @@ constexpr int kRfRed = 3;     // reduction stages, at most
 constexpr int kRfRes = 3;     // resident operands, at most
 constexpr int kRfMem = 4;     // operands loaded at every use, at most
 constexpr int kRfChunks = 4;  // 8-element chunks of a row per lane, at most
+constexpr int kRfRow = 4;     // operands constant along a row (read once per row), at most
 constexpr int kRfNodes = 8;   // row values a stage derives from earlier results, at most
-constexpr int kRfScal = kRfRed + kRfNodes;  // a row's scalars: results, then derived values
+constexpr int kRfNode0 = kRfRed + kRfRow;   // a row's scalars: reduction results, row
+constexpr int kRfScal = kRfNode0 + kRfNodes;  // operands, then derived values
 
 // Each stage's program is compiled on the host into a chain over the row's
 // elements, acc = op(acc, operand) or op(acc) step by step, whose operands
 // are resident rows, other operands, immediates or row scalars: the
-// reductions' results and values derived from them alone (recip of a row sum,
-// a mean plus epsilon under rsqrt), which are computed once per row.
+// reductions' results, operands constant along the row (a column broadcast,
+// read once per row) and values derived from those alone (recip of a row
+// sum, a mean plus epsilon under rsqrt), which are computed once per row.
 enum : uint8_t {
   RC_ADD, RC_SUB, RC_RSUB, RC_MUL, RC_DIV, RC_RDIV, RC_MAX, RC_RMAX, RC_MIN,  // binary: op(acc, v)
   RC_RMIN,                                   // (R*: op(v, acc))
@@ -1001,7 +1004,7 @@ struct RfStep {    // one chain step; step 0 is RC_COPY of the chain's first val
   float imm;       // RS_IMM operand
 };
 
-struct RfNode {    // row scalar kRfRed + i = code(a, b) (unary: code(a); R*: op(b, a)), rounded
+struct RfNode {    // row scalar kRfNode0 + i = code(a, b) (unary: code(a); R*: op(b, a)), rounded
   uint8_t code, a, b, rnd;  // a, b: RS_SC + slot or RS_IMM
   float imm_a, imm_b;
 };
@@ -1022,6 +1025,8 @@ struct RfArgs {
   RfStage st[kRfRed + 1];  // the reductions, then (at kRfRed) the elementwise stage
   EltOperand mem[kRfMem];
   EltOperand res[kRfRes];
+  EltOperand row[kRfRow];  // row scalars kRfRed + i
+  int32_t n_row;
   void* out;
   int64_t out_ld;
   int64_t y0, x0, h, w;
@@ -1075,7 +1080,7 @@ __device__ __forceinline__ void rf_nodes(const RfStage& st, float* sc) {
     const RfNode nd = st.node[i];
     const float x = nd.a == RS_IMM ? nd.imm_a : sc[nd.a - RS_SC];
     const float y = nd.b == RS_IMM ? nd.imm_b : sc[nd.b - RS_SC];
-    sc[kRfRed + i] = rf_round1(rc_op1(nd.code, x, y), nd.rnd);
+    sc[kRfNode0 + i] = rf_round1(rc_op1(nd.code, x, y), nd.rnd);
   }
 }
 
@@ -1234,6 +1239,11 @@ __global__ __launch_bounds__(256) void reduce_rows_eltwise_kernel(const RfArgs a
   };
   float* const sc = scl[wave];
 #pragma unroll 1
+  for (int i = 0; i < a.n_row; ++i) {  // the row's values of the column-broadcast operands
+    const EltOperand& op = a.row[i];
+    sc[kRfRed + i] = to_f32<8, false>(op, load_raw<8, false>(op, operand_addr<false>(op, y, a.x0)))[0];
+  }
+#pragma unroll 1
   for (int j = 0; j < a.n_red; ++j) {
     const RfStage& st = a.st[j];
     rf_nodes(st, sc);
@@ -1286,6 +1296,15 @@ __global__ __launch_bounds__(256) void reduce_rows_eltwise_kernel(const RfArgs a
 
 using namespace ttlh;
 
+namespace ttlh {
+namespace {
+int rows_fused_impl(const char* who, const ttlh_row_reduce* red, int n_red,
+                    const ttlh_instr* prog, const ttlh_operand* in, int n_instr, void* out,
+                    int out_dtype, int64_t out_ld, int64_t y0, int64_t x0, int64_t h, int64_t w,
+                    void* stream);
+}  // namespace
+}  // namespace ttlh
+
 extern "C" int ttlh_eltwise(const ttlh_instr* prog, const ttlh_operand* in, int n_instr, void* out,
                             int out_dtype, int64_t out_ld, int64_t y0, int64_t x0, int64_t h,
                             int64_t w, void* stream) {
@@ -1327,6 +1346,16 @@ extern "C" int ttlh_eltwise(const ttlh_instr* prog, const ttlh_operand* in, int 
     if (pi.all_bf16 && try_stream(chain, n_instr, s, &status)) return status;
     return pi.all_bf16 ? dispatch_chain<true>(chain, n_instr, s)
                        : dispatch_chain<false>(chain, n_instr, s);
+  }
+  if (w >= 512) {
+    // not linear (a stack, an op of a broadcast value): the row kernel takes
+    // the programs it compiles into a chain over each row, operands constant
+    // along a row becoming row scalars (exp(x - m) * recip(s) with m, s column
+    // broadcasts); rows of 512+ elements keep its lanes busy
+    const int rc = rows_fused_impl("ttlh_eltwise", nullptr, 0, prog, in, n_instr, out, out_dtype,
+                                   out_ld, y0, x0, h, w, stream);
+    if (rc != TTLH_EUNSUPPORTED) return rc;
+    clear_error();
   }
   if (!preload) return launch<8, false, false, true, true, true>(a, s);
   if (pi.full) return launch<8, true, false, true, true, true>(a, s);
@@ -1725,7 +1754,7 @@ bool rf_compile(const EltArgs& e, int nj, const uint8_t* src_of, RfStage& st) {
       return RS_IMM;
     }
     st.node[n_nodes] = RfNode{code, a, b, x.rnd, ia, ib};
-    return static_cast<uint8_t>(RS_SC + kRfRed + n_nodes++);
+    return static_cast<uint8_t>(RS_SC + kRfNode0 + n_nodes++);
   };
   RfStep rev_steps[TTLH_MAX_INSTR + 1];
   int ns = 0;
@@ -1796,7 +1825,7 @@ void rf_choose_kept(RfArgs& a) {
     if (sj.n_steps < 2) continue;  // a plain load: keeping it saves no arithmetic
     bool local = false;
     for (int k = 0; k < sj.n_steps; ++k)
-      local = local || (sj.step[k].src >= RS_SC + kRfRed && sj.step[k].src < RS_IMM &&
+      local = local || (sj.step[k].src >= RS_SC + kRfNode0 && sj.step[k].src < RS_IMM &&
                         (k == 0 || sj.step[k].code <= RC_RMIN));
     if (local) continue;
     int saved = 0;
@@ -1851,6 +1880,7 @@ extern "C" int ttlh_reduce_rows_eltwise(const ttlh_row_reduce* red, int n_red,
   clear_error();
   const char* who = "ttlh_reduce_rows_eltwise";
   TTLH_REQUIRE(prog && in && n_instr > 0, TTLH_EINVAL, "%s: needs the elementwise program", who);
+  TTLH_REQUIRE(red && n_red >= 1, TTLH_EINVAL, "%s: needs at least one reduction", who);
   return rows_fused_impl(who, red, n_red, prog, in, n_instr, out, out_dtype, out_ld, y0, x0, h, w,
                          stream);
 }
@@ -1865,7 +1895,8 @@ int rows_fused_impl(const char* who, const ttlh_row_reduce* red, int n_red,
                     int out_dtype, int64_t out_ld, int64_t y0, int64_t x0, int64_t h, int64_t w,
                     void* stream) {
   const bool has_out = n_instr > 0;
-  TTLH_REQUIRE(red && n_red >= 1, TTLH_EINVAL, "%s: needs at least one reduction", who);
+  TTLH_REQUIRE(n_red >= 0 && (n_red == 0 || red) && (has_out || n_red >= 1), TTLH_EINVAL,
+               "%s: needs a reduction or an elementwise program", who);
   TTLH_REQUIRE(!has_out || (out && (out_dtype == TTLH_BF16 || out_dtype == TTLH_F32)),
                TTLH_EINVAL, "%s: bad output pointer or dtype", who);
   TTLH_REQUIRE(h >= 1 && w >= 1 && y0 >= 0 && x0 >= 0 && (!has_out || out_ld >= x0 + w),
@@ -1968,10 +1999,19 @@ int rows_fused_impl(const char* who, const ttlh_row_reduce* red, int n_red,
           TTLH_REQUIRE(!overlap(lo, hi, rlo[p], rhi[p]), TTLH_EUNSUPPORTED,
                        "%s: stage %d reads reduction %d's results other than as its rows' values",
                        who, j, p);
+        // constant along the row (a column broadcast): a row scalar
+        if (o.cs == 0 || o.cmask == 0 || w == 1) {
+          for (int q = 0; q < a.n_row && src < 0; ++q)
+            if (same_map(a.row[q], o)) src = RS_SC + kRfRed + q;
+          if (src < 0 && a.n_row < kRfRow) {
+            a.row[a.n_row] = o;
+            src = RS_SC + kRfRed + a.n_row++;
+          }
+        }
         // rows held in registers: identity-mapped bf16 operands read once (a
         // row re-read by every row, stride 0, is left to the caches)
-        if (o.dtype == TTLH_BF16 && o.rmask == -1 && o.cmask == -1 && o.cs == 1 && o.vec &&
-            (o.rs != 0 || h == 1)) {
+        if (src < 0 && o.dtype == TTLH_BF16 && o.rmask == -1 && o.cmask == -1 && o.cs == 1 &&
+            o.vec && (o.rs != 0 || h == 1)) {
           for (int q = 0; q < n_res && src < 0; ++q)
             if (same_map(a.res[q], o)) src = RS_RES + q;
           if (src < 0 && n_res < kRfRes) {
