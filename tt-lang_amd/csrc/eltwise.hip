@@ -822,18 +822,30 @@ __global__ __launch_bounds__(256) void reduce_rows_bf16_kernel(const uint16_t* b
     if (xf + i * S < w) c[i] = ld16<NT>(rowp + 2 * (xf + i * S));
   const float s = red_scale(a);  // after the first row loads are in flight
   float r = red_identity(KIND);
+  bool nan = false;  // maximum: whether a value was a NaN, kept apart from fmaxf
   for (int64_t xb = xf; xb < w; xb += 2 * S) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int64_t xo = xb + i * S;
       if (xo < w) {
         const f32x8 v = unpack_bf16x8(c[i]);
+        if constexpr (KIND == TTLH_REDUCE_MAX) {
+          // red_acc_k's value: fmaxf over the products, NaN once any is
 #pragma unroll
-        for (int k = 0; k < 8; ++k) r = red_acc_k<KIND>(r, v[k], s);
+          for (int k = 0; k < 8; ++k) {
+            const float b = v[k] * s;
+            nan |= b != b;
+            r = fmaxf(r, b);
+          }
+        } else {
+#pragma unroll
+          for (int k = 0; k < 8; ++k) r = red_acc_k<KIND>(r, v[k], s);
+        }
       }
       if (xo + 2 * S < w) c[i] = ld16<NT>(rowp + 2 * (xo + 2 * S));
     }
   }
+  if (nan) r = __builtin_nanf("");
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) r = red_combine_k<KIND>(r, __shfl_xor(r, off, 64));
   if (lane == 0) part[wave] = r;
