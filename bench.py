@@ -321,7 +321,8 @@ class SoftmaxWorkload(PlanWorkload):
     (tests/kernel_lib.py make_softmax_one_store: y = e * broadcast(recip(
     reduce_sum(e))), e = exp(x - broadcast(reduce_max(x))), one block per
     row band of 128 tiles, 8x8 grid).  Planned as two row reductions and the
-    elementwise program: one ttlh_reduce_rows_eltwise launch reading x once
+    elementwise program: one ttlh_reduce_rows_eltwise launch reading x once,
+    which runs the row softmax on its dedicated kernel
     (`separate`: the same plan run as its three launches, x read three
     times, for comparison).  HBM-bound; algorithmic bytes = x read once, y
     written once, the two reduction result tiles written once."""
@@ -335,7 +336,7 @@ class SoftmaxWorkload(PlanWorkload):
                        f"per-op bf16 rounding; {how}")
 
     def kernel_name(self):
-        return "reduce_rows_bf16_kernel" if self.separate else "reduce_rows_eltwise_kernel"
+        return "reduce_rows_bf16_kernel" if self.separate else "softmax_rows_kernel"
 
     def traffic_kernels(self):
         # separate: the row sum and the final program both run as
@@ -343,7 +344,7 @@ class SoftmaxWorkload(PlanWorkload):
         # which the per-kernel counter medians cannot tell apart: not listed
         if self.separate:
             return []
-        return [("reduce_rows_eltwise_kernel<256, 1, 2, true>", None)]
+        return [("softmax_rows_kernel<256, 2>", None)]
 
     def work_per_step(self):
         return 2 * self.n * self.n * 2 + 2 * self.n * 32 * 2

@@ -1303,6 +1303,101 @@ __global__ __launch_bounds__(256) void reduce_rows_eltwise_kernel(const RfArgs a
   }
 }
 
+// The row softmax, the commonest program of this launch, as compiled chains
+// recognised on the host (rf_softmax_form): reduction 0 = max over the row of
+// x (one resident bf16 operand) times s0; reduction 1 = sum of e = exp(x - m)
+// times s1 (m = reduction 0's result); out = e * recip(l) or e / l (l =
+// reduction 1's result), every step's rounding as the chains carry it.  The
+// same layout, order of summation and op definitions as the generic kernel,
+// written out without the interpreter: its results are the generic kernel's,
+// bit for bit.
+struct RfSoftmax {
+  uint8_t r_sub, r_exp, r_node, r_out;  // per-step rounding (TTLH_BF16 or not)
+  uint8_t r_m, r_g;                     // rounding of the operands m and g
+  uint8_t recip;                        // out = e * g, g = recip(l), else e / g, g = l
+};
+
+template <int LANES, int NCH>
+__global__ __launch_bounds__(256) void softmax_rows_kernel(const RfArgs a, const RfSoftmax f) {
+  __shared__ float part[2][4];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int64_t row = LANES == 256 ? int64_t(blockIdx.x) : int64_t(blockIdx.x) * 4 + wave;
+  if (LANES == 64 && row >= a.h) return;  // wave-uniform (no workgroup barrier in this layout)
+  const int64_t y = a.y0 + row;
+  const int li = LANES == 256 ? t : lane;
+  constexpr int64_t S = int64_t(LANES) * 8;
+  const int64_t xl = int64_t(li) * 8;
+  u32x4 q[NCH];
+  const uintptr_t base = operand_addr<false>(a.res[0], y, a.x0);
+  rf_each<NCH>([&](auto c) {
+    const int64_t xo = xl + c * S;
+    q[c] = ld16<true>(base + 2 * (xo < a.w ? xo : a.w - 8));
+  });
+  const float s0 = rf_scale(a.st[0]), s1 = rf_scale(a.st[1]);
+  auto row_value = [&](int j, float r) {  // the butterfly, the wave partials, the result's dtype
+    r = red_wave(a.st[j].kind, r);
+    if constexpr (LANES == 256) {
+      if (lane == 0) part[j][wave] = r;
+      __syncthreads();
+      r = red_combine(a.st[j].kind, red_combine(a.st[j].kind, part[j][0], part[j][1]),
+                      red_combine(a.st[j].kind, part[j][2], part[j][3]));
+    }
+    rf_write(a.st[j], row, r, li);
+    return a.st[j].out_dtype == TTLH_BF16 ? round_bf16(r) : r;
+  };
+  // reduction 0: the row maximum
+  float r = -__builtin_inff();
+  bool nan = false;
+  rf_each<NCH>([&](auto c) {
+    if (xl + c * S < a.w) {
+      const f32x8 x = bf16x8_f32(q[c]);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float b = s0 == 1.0f ? x[k] : x[k] * s0;
+        nan |= b != b;
+        r = fmaxf(r, b);
+      }
+    }
+  });
+  if (nan) r = __builtin_nanf("");
+  const float m = row_value(0, r);
+  // reduction 1: the sum of e = exp(x - m), e kept
+  f32x8 e[NCH];
+  r = 0.0f;
+  const float mm = f.r_m == TTLH_BF16 ? round_bf16(m) : m;
+  rf_each<NCH>([&](auto c) {
+    f32x8 d = bf16x8_f32(q[c]) - splat(mm);
+    if (f.r_sub == TTLH_BF16) d = round_bf16x8(d);
+    e[c] = vexp_uniform(d);
+    if (f.r_exp == TTLH_BF16) e[c] = round_bf16x8(e[c]);
+    if (xl + c * S < a.w) {
+      if (s1 == 1.0f) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) r += e[c][k];
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) r = __builtin_fmaf(e[c][k], s1, r);
+      }
+    }
+  });
+  const float l = row_value(1, r);
+  // the output
+  float g = l;
+  if (f.recip) {
+    g = unary1<TTLH_OP_RECIP>(l);
+    if (f.r_node == TTLH_BF16) g = round_bf16(g);
+  }
+  if (f.r_g == TTLH_BF16) g = round_bf16(g);
+  rf_each<NCH>([&](auto c) {
+    const int64_t xo = xl + c * S;
+    if (xo < a.w) {
+      f32x8 o = f.recip ? binary8<TTLH_OP_MUL>(e[c], splat(g)) : binary8<TTLH_OP_DIV>(e[c], splat(g));
+      if (f.r_out == TTLH_BF16) o = round_bf16x8(o);
+      store_chunk<8>(a, y, a.x0 + xo, o);
+    }
+  });
+}
+
 }  // namespace
 }  // namespace ttlh
 
@@ -1861,6 +1956,41 @@ void rf_choose_kept(RfArgs& a) {
   }
 }
 
+// Whether the compiled stages are the row softmax softmax_rows_kernel runs
+// (its comment has the form), and its rounding flags.
+bool rf_softmax_form(const RfArgs& a, RfSoftmax* f) {
+  if (a.n_red != 2 || a.kept != 1) return false;
+  const RfStage &s0 = a.st[0], &s1 = a.st[1], &fe = a.st[kRfRed];
+  // x, the one resident operand, is bf16: a bf16 rounding of it (a step's or
+  // an operand's) is the identity, so those flags do not matter
+  const uint8_t x = RS_RES + 0;
+  if (s0.kind != TTLH_REDUCE_MAX || s0.n_steps != 1 || s0.n_nodes != 0 ||
+      s0.step[0].code != RC_COPY || s0.step[0].src != x)
+    return false;
+  if (s1.kind != TTLH_REDUCE_SUM || s1.n_steps != 3 || s1.n_nodes != 0 || s1.from_kept != 0 ||
+      s1.step[0].code != RC_COPY || s1.step[0].src != x || s1.step[1].code != RC_SUB ||
+      s1.step[1].src != RS_SC + 0 || s1.step[2].code != RC_EXP)
+    return false;
+  if (fe.from_kept != 3 || fe.n_steps != 4) return false;
+  const RfStep& o = fe.step[3];
+  if (o.code == RC_MUL && o.src == RS_SC + kRfNode0 && fe.n_nodes == 1 &&
+      fe.node[0].code == RC_RECIP && fe.node[0].a == RS_SC + 1) {
+    f->recip = 1;
+    f->r_node = fe.node[0].rnd;
+  } else if (o.code == RC_DIV && o.src == RS_SC + 1 && fe.n_nodes == 0) {
+    f->recip = 0;
+    f->r_node = TTLH_F32;
+  } else {
+    return false;
+  }
+  f->r_sub = s1.step[1].rnd;
+  f->r_exp = s1.step[2].rnd;
+  f->r_out = o.rnd;
+  f->r_m = s1.step[1].orn;
+  f->r_g = o.orn;
+  return true;
+}
+
 }  // namespace
 }  // namespace ttlh
 
@@ -2059,6 +2189,25 @@ int rows_fused_impl(const char* who, const ttlh_row_reduce* red, int n_red,
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t lanes = wide ? 256 : 64;
   const int nch = static_cast<int>((w + 8 * lanes - 1) / (8 * lanes));  // 1..kRfChunks
+  RfSoftmax sm;
+  if (n_res == 1 && n_mem == 0 && a.n_row == 0 && rf_softmax_form(a, &sm)) {
+    TTLH_REQUIRE(groups < (int64_t(1) << 31), TTLH_EUNSUPPORTED, "%s: region too large", who);
+    const dim3 grid(static_cast<uint32_t>(groups)), block(256);
+#define TTLH_SM(L)                                                                            \
+  switch (nch) {                                                                              \
+    case 1: hipLaunchKernelGGL((softmax_rows_kernel<L, 1>), grid, block, 0, s, a, sm); break; \
+    case 2: hipLaunchKernelGGL((softmax_rows_kernel<L, 2>), grid, block, 0, s, a, sm); break; \
+    case 3: hipLaunchKernelGGL((softmax_rows_kernel<L, 3>), grid, block, 0, s, a, sm); break; \
+    default: hipLaunchKernelGGL((softmax_rows_kernel<L, 4>), grid, block, 0, s, a, sm); break; \
+  }
+    if (wide) {
+      TTLH_SM(256)
+    } else {
+      TTLH_SM(64)
+    }
+#undef TTLH_SM
+    return check_launch("softmax_rows_kernel");
+  }
   // one instantiation per (lanes, resident operands, chunks per lane)
 #define TTLH_RF3(L, R, C) return rf_launch<L, R, C>(a, groups, s)
 #define TTLH_RF2(L, R)                   \
