@@ -186,3 +186,48 @@ def test_ragged_rows_and_fp32_operands(h, w):
         ai = a.view(torch.int16 if a.dtype == B16 else torch.int32).cpu()
         bi = b.view(torch.int16 if b.dtype == B16 else torch.int32).cpu()
         assert torch.equal(ai, bi), int((ai != bi).sum())
+
+
+@pytest.mark.parametrize("form", ["recip", "div"])
+@pytest.mark.parametrize("w", [512, 4096])
+def test_softmax_flags_f32_results_scalers_and_specials(form, w):
+    # the row softmax's dedicated kernel with f32 reduction results, scalers
+    # other than 1, the e / l form as well as e * recip(l), and rows holding
+    # NaN, +inf and -inf: bit for bit as the separate calls
+    print(f"reduce_rows_eltwise softmax flags {form} w={w}", flush=True)
+    h = 64
+
+    def case():
+        x = O.seeded((h, w), "uniform", w + 3, lo=-4, hi=4)
+        x[3, 5] = float("nan")
+        x[7, 9] = float("inf")
+        x[11, :] = -float("inf")
+        x = x.cuda()
+        xm = Kn.OperandMap(x)
+        t1 = torch.full((h, 32), 5.0, dtype=torch.float32, device="cuda")
+        t2 = torch.full((h, 32), 5.0, dtype=torch.float32, device="cuda")
+        s0 = torch.full((1, 1), 0.5, dtype=B16, device="cuda")
+        p1 = X.compile_expr(_leaf(xm))
+        p2 = X.compile_expr(X.Unary("exp", X.Binary("sub", _leaf(xm), _leaf(_row_result(t1)),
+                                                    torch.float32), B16))
+        e2 = X.Unary("exp", X.Binary("sub", _leaf(xm), _leaf(_row_result(t1)), torch.float32),
+                     B16)
+        if form == "recip":
+            fin = X.compile_expr(X.Binary("mul", e2, X.Unary("recip", _leaf(_row_result(t2)),
+                                                             torch.float32), B16))
+        else:
+            fin = X.compile_expr(X.Binary("div", e2, _leaf(_row_result(t2)), B16))
+        reds = [Kn.RowReduce(p1, _ops(p1), "max", t1, (0, 0), True, s0, 2.0),
+                Kn.RowReduce(p2, _ops(p2), "sum", t2, (0, 0), True, None, 0.25)]
+        return reds, fin, torch.full((h, w), 7.0, dtype=B16, device="cuda"), [t1, t2]
+
+    reds, fin, out, temps = case()
+    assert Kn.reduce_rows_eltwise(reds, fin, _ops(fin), out, (0, 0, h, w))
+    torch.cuda.synchronize()
+    reds2, fin2, out2, temps2 = case()
+    _separate(reds2, fin2, out2)
+    torch.cuda.synchronize()
+    for a, b in zip([out] + temps, [out2] + temps2):
+        ai = a.view(torch.int16 if a.dtype == B16 else torch.int32).cpu()
+        bi = b.view(torch.int16 if b.dtype == B16 else torch.int32).cpu()
+        assert torch.equal(ai, bi), int((ai != bi).sum())
