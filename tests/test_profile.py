@@ -60,3 +60,20 @@ def test_auto_profile_report_on_device(monkeypatch, capsys):
     # the profiled call still computed the result
     ref = torch.exp(ts[0] + ts[1]) * ts[2]
     assert int(O.bf16_ulp_diff(ttnn.to_torch(args[3]), ref).max()) <= 1
+
+
+def test_fused_row_launch_work_reads_each_operand_once():
+    # a softmax in one store: one ReduceEltwiseLaunch whose work is x read
+    # once, y written once and one result per row of each reduction (the
+    # report's model for reductions), not x read three times
+    rows, cols = 64, 512
+    ts = [O.seeded((rows, cols), "uniform", 7, lo=-4, hi=4),
+          torch.ones(32, 32, dtype=torch.bfloat16), torch.zeros(rows, cols, dtype=torch.bfloat16)]
+    args = _args(ts)
+    plan = KL.make_softmax_one_store(ttl, gc=cols // 32, grid=(2, 1)).trace(*args.values())
+    (l,) = plan.launches
+    assert isinstance(l, P.ReduceEltwiseLaunch)
+    work, unit, _ = profile.launch_work(l, args)
+    assert unit == "GB/s" and work == 2 * rows * cols * 2 + 2 * rows * 2
+    text = profile.report("softmax", (2, 1), plan, args, [5.0])
+    assert "ttlh_reduce_rows_eltwise 64x512: row max+sum" in text
