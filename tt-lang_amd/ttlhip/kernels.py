@@ -41,6 +41,39 @@ def _check_device(t: torch.Tensor, what: str) -> None:
         raise ValueError(f"{what} must be 2-D, got shape {tuple(t.shape)}")
 
 
+# Device workspaces (column and full reductions, weight dequantisation), one
+# per (device, stream), grown to the largest size asked for and then kept.
+# Taking a fresh one from torch's caching allocator on every call costs tens
+# of microseconds of host time and now and then a millisecond-long stall,
+# far more than the kernels it serves.  Calls on one stream run in stream
+# order, so they share that stream's buffer safely; calls on different
+# streams get different buffers.  A HIP graph captured over such a call
+# keeps the buffer's address: replaying it while eager calls run on the
+# same buffer from another stream races, as with any shared buffer.
+_WORKSPACES: dict = {}
+
+
+def _workspace(device: torch.device, stream, nbytes: int) -> torch.Tensor:
+    sp = L.stream_ptr(stream)
+    key = (device.index, sp)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        if stream is not None:
+            # allocated on the current stream, used on `stream`: keep the
+            # block from being handed out again before that stream's work
+            # on it has finished once this buffer is replaced
+            ws.record_stream(stream)
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def release_workspaces() -> None:
+    """Drop the cached workspaces (their memory returns to torch's caching
+    allocator once the work queued on them has finished)."""
+    _WORKSPACES.clear()
+
+
 def _axis_range(lo: int, n: int, mask: int, off: int):
     """[min, max] of (c & mask) + off for c in [lo, lo + n)."""
     if n <= 0:
@@ -163,12 +196,7 @@ def reduce(prog: StackProgram, operands: Sequence[Optional[OperandMap]], kind: s
                L.stream_ptr(stream))
         return
     ws_bytes = int(L.load().ttlh_reduce_workspace_bytes(dbits, h, w))
-    ws = None
-    if ws_bytes:
-        # from torch's caching allocator; freed on return, reused in stream order
-        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=out.device)
-        if stream is not None:
-            ws.record_stream(stream)
+    ws = _workspace(out.device, stream, ws_bytes) if ws_bytes else None
     L.call("ttlh_reduce", instrs, ops, n, kcode,
            dbits, sp, sdt, float(scale), optr, L.dtype_code(out.dtype), out.stride(0),
            int(bool(out_pad)), y0, x0, h, w, ws.data_ptr() if ws is not None else 0, ws_bytes,
@@ -448,7 +476,7 @@ def matmul_bfp8w(a: torch.Tensor, bq: torch.Tensor, c: torch.Tensor, stream=None
                  two_pass: Optional[bool] = None) -> None:
     """c[M,N] = a[M,K] (bf16) @ dequant(bq)[K,N]; bf16 out.  `two_pass`
     forces the path (None: by M, see BFP8_TWO_PASS_MIN_M); the two-pass
-    workspace comes from torch's caching allocator on c's device."""
+    workspace is the cached one of c's device and the stream."""
     _check_device(a, "matmul_bfp8w A")
     _check_device(c, "matmul_bfp8w C")
     M, K = a.shape
@@ -466,11 +494,9 @@ def matmul_bfp8w(a: torch.Tensor, bq: torch.Tensor, c: torch.Tensor, stream=None
                c.stride(0), M, N, K, L.stream_ptr(stream))
         return
     nbytes = int(L.load().ttlh_matmul_bfp8w_workspace_bytes(M, N, K))
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=c.device)
+    ws = _workspace(c.device, stream, nbytes)
     L.call("ttlh_matmul_bfp8w_ws", a.data_ptr(), a.stride(0), bq.data_ptr(), c.data_ptr(),
            c.stride(0), M, N, K, ws.data_ptr(), nbytes, L.stream_ptr(stream))
-    if stream is not None:
-        ws.record_stream(stream)
 
 
 def bfp4_tiles_bytes(rows: int, cols: int) -> int:
@@ -509,7 +535,8 @@ def bfp4_unpack(q: torch.Tensor, rows: int, cols: int, stream=None) -> torch.Ten
 
 def matmul_bfp4w(a: torch.Tensor, bq: torch.Tensor, c: torch.Tensor, stream=None) -> None:
     """c[M,N] = a[M,K] (bf16) @ dequant(bq)[K,N] with bfloat4_b weights; the
-    dequantised weights go through a bf16 workspace from torch's allocator."""
+    dequantised weights go through a bf16 workspace (the cached one of c's
+    device and the stream)."""
     _check_device(a, "matmul_bfp4w A")
     _check_device(c, "matmul_bfp4w C")
     M, K = a.shape
@@ -520,11 +547,9 @@ def matmul_bfp4w(a: torch.Tensor, bq: torch.Tensor, c: torch.Tensor, stream=None
         raise ValueError("matmul_bfp4w: Bq must be device uint8 tiles of a K x N matrix")
     if a.stride(1) != 1 or c.stride(1) != 1:
         raise ValueError("matmul_bfp4w: A and C must be row-major")
-    ws = torch.empty(K * N * 2, dtype=torch.uint8, device=c.device)
+    ws = _workspace(c.device, stream, K * N * 2)
     L.call("ttlh_matmul_bfp4w_ws", a.data_ptr(), a.stride(0), bq.data_ptr(), c.data_ptr(),
            c.stride(0), M, N, K, ws.data_ptr(), K * N * 2, L.stream_ptr(stream))
-    if stream is not None:
-        ws.record_stream(stream)
 
 
 def sdpa_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, o: torch.Tensor, scale: float,
