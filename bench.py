@@ -181,23 +181,38 @@ class PlanWorkload(Workload):
 
 
 class EltwiseWorkload(PlanWorkload):
-    def __init__(self, name, n, kind, seed=1234):
+    """C1 / C2 through the drop-in.  `cols` (default n) other than a power of
+    two times 8 makes C2's row vector fall outside the flat kernel's 1-D
+    indexing (a row vector is read through a mask of its chunk count), so
+    the launch is the general 2-D `stream_kernel` (any region, masks and
+    offsets)."""
+
+    def __init__(self, name, n, kind, seed=1234, cols=None):
         self.name, self.n, self.kind, self.seed = name, n, kind, seed
-        self.config = ("eltwise add C = A + B, bf16 %dx%d, U[-1,1] (BASELINE configs[0])" % (n, n)
+        self.cols = n if cols is None else cols
+        shape = "%dx%d" % (n, self.cols)
+        self.config = ("eltwise add C = A + B, bf16 %s, U[-1,1] (BASELINE configs[0])" % shape
                        if kind == "add" else
-                       "fused eltwise pipe + broadcast Y = exp(A + b_row) * C, bf16 %dx%d, "
-                       "b_row 1x%d, U[-2,2] (BASELINE configs[1])" % (n, n, n))
+                       "fused eltwise pipe + broadcast Y = exp(A + b_row) * C, bf16 %s, "
+                       "b_row 1x%d, U[-2,2]%s" % (
+                           shape, self.cols, " (BASELINE configs[1])" if cols is None else
+                           " (C2's program at a row length that is not a power of two)"))
+
+    def flat(self):
+        cpr = self.cols // 8
+        return self.kind == "add" or (cpr & (cpr - 1)) == 0
 
     def kernel_name(self):
-        return "flat_kernel"
+        return "flat_kernel" if self.flat() else "stream_kernel"
 
-    def traffic_kernels(self):  # the flat kernel's instantiation for this program
-        return [("flat_kernel<2, 3u, true>" if self.kind == "add" else "flat_kernel<4, 11u, true>",
-                 None)]
+    def traffic_kernels(self):  # the kernel's instantiation for this program
+        if self.kind == "add":
+            return [("flat_kernel<2, 3u, true>", None)]
+        return [("flat_kernel<4, 11u, true>" if self.flat() else "stream_kernel<4, 11u>", None)]
 
     def work_per_step(self):
-        e = self.n * self.n * 2
-        return 3 * e if self.kind == "add" else 3 * e + self.n * 2
+        e = self.n * self.cols * 2
+        return 3 * e if self.kind == "add" else 3 * e + self.cols * 2
 
     def expr(self):
         if self.kind == "add":
@@ -206,13 +221,13 @@ class EltwiseWorkload(PlanWorkload):
 
     def cpu_inputs(self):
         from oracle.tile_ops import seeded
-        n, s = self.n, self.seed
+        n, m, s = self.n, self.cols, self.seed
         if self.kind == "add":
-            return [seeded((n, n), "uniform", s, lo=-1, hi=1),
-                    seeded((n, n), "uniform", s + 1, lo=-1, hi=1)]
-        return [seeded((n, n), "uniform", s, lo=-2, hi=2),
-                seeded((1, n), "uniform", s + 1, lo=-2, hi=2),
-                seeded((n, n), "uniform", s + 2, lo=-2, hi=2)]
+            return [seeded((n, m), "uniform", s, lo=-1, hi=1),
+                    seeded((n, m), "uniform", s + 1, lo=-1, hi=1)]
+        return [seeded((n, m), "uniform", s, lo=-2, hi=2),
+                seeded((1, m), "uniform", s + 1, lo=-2, hi=2),
+                seeded((n, m), "uniform", s + 2, lo=-2, hi=2)]
 
     def make_kernel(self, ttl_ns):
         import kernel_lib as KL
@@ -228,7 +243,7 @@ class EltwiseWorkload(PlanWorkload):
         sets = []
         for i in range(nsets):
             ins = base if i == 0 else [ttnn.Tensor(t._tensor.clone()) for t in base]
-            sets.append(ins + [ttnn.empty((self.n, self.n), dtype=torch.bfloat16)])
+            sets.append(ins + [ttnn.empty((self.n, self.cols), dtype=torch.bfloat16)])
         return sets
 
     def check(self):
@@ -246,13 +261,13 @@ class EltwiseWorkload(PlanWorkload):
         execution model) on the same tt-lang kernel and the full-size input."""
         from oracle import tile_ops as O
         ins = self.cpu_inputs()
-        out = torch.zeros(self.n, self.n, dtype=torch.bfloat16)
+        out = torch.zeros(self.n, self.cols, dtype=torch.bfloat16)
         dt, reps = _eager(self.make_kernel, ins + [out])
         env = dict(zip("abc", ins))
         dtv, _ = _repeat(lambda: O.eval_expr(self.expr(), env), min_s=1.0)
         return {"value": round(self.work_per_step() / dt / 1e9, 4), "unit": "GB/s", "cores": 1,
                 "kind": "port",
-                "sample": f"the full {self.n}x{self.n} workload through the eager tile-by-tile "
+                "sample": f"the full {self.n}x{self.cols} workload through the eager tile-by-tile "
                           f"oracle executor (simulator execution model, 1 thread), {reps} runs "
                           f"of {dt:.2f} s",
                 "host_cpu_count": os.cpu_count(),
@@ -773,6 +788,8 @@ class SdpaWorkload(PlanWorkload):
 WORKLOADS = {
     "exp_bcast_mul_4096": lambda: EltwiseWorkload("exp_bcast_mul_4096", 4096, "pipe"),
     "eltwise_add_2048": lambda: EltwiseWorkload("eltwise_add_2048", 2048, "add"),
+    "exp_bcast_mul_4096x3072": lambda: EltwiseWorkload("exp_bcast_mul_4096x3072", 4096, "pipe",
+                                                       cols=3072),
     "matmul_bf16_4096": lambda: MatmulWorkload("matmul_bf16_4096", 4096, 4096, 4096),
     "matmul_bfp8w_4096x11008": lambda: Bfp8MatmulWorkload("matmul_bfp8w_4096x11008", 4096,
                                                           11008, 4096),

@@ -227,6 +227,43 @@ def test_chain_fast_path_shapes(h, w):
     assert_bitexact(got, O.eval_expr(("add", ("leaf", "a"), ("leaf", "c")), env).float())
 
 
+@pytest.mark.parametrize("h,w,region", [
+    (257, 3072, None),                # 384 chunks per row: blocks of 128, not 256
+    (9, 1000, None),                  # 125 chunks per row, one block of 128
+    (70, 3072, (3, 256, 61, 2816)),   # 352 chunks per row at a column offset: blocks of 128
+    (70, 1536, (3, 256, 61, 1024)),   # 128 chunks per row, one block
+    (33, 2056, (1, 8, 31, 2000)),     # 250 chunks per row, one block of 256
+])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_stream_kernel_row_blocks(h, w, region, out_dtype):
+    # C2's program and two linear ones with a row vector take the 2-D stream
+    # kernel at row lengths that are not a power of two chunks (whole rows)
+    # and at column offsets; its row blocks narrow where the last block of a
+    # row would be mostly dead lanes; nothing outside the region is written
+    a, c = _u((h, w), 90), _u((h, w), 91)
+    b = _u((1, w), 92)
+    env = {"a": a, "b": b, "c": c}
+    for e in [("mul", ("exp", ("add", ("leaf", "a"), ("leaf", "b"))), ("leaf", "c")),
+              ("sub", ("mul", ("add", ("leaf", "a"), ("const", 3.0)), ("leaf", "c")),
+               ("leaf", "b")),
+              ("add", ("leaf", "a"), ("leaf", "b"))]:
+        got = run_gpu(e, env, {}, (h, w), out_dtype, region=region)
+        ref = O.eval_expr(e, env)
+        if out_dtype == torch.float32:
+            ref = ref.float()
+        if region is not None:
+            y0, x0, rh, rw = region
+            outside = torch.ones(h, w, dtype=torch.bool)
+            outside[y0:y0 + rh, x0:x0 + rw] = False
+            assert bool((got[outside] == 7.0).all()), "a write outside the region"
+            got = got[y0:y0 + rh, x0:x0 + rw]
+            ref = ref[y0:y0 + rh, x0:x0 + rw]
+        if e[0] == "mul":  # exp: within 1 bf16 ulp of the oracle (as the flat path)
+            assert int(O.bf16_ulp_diff(got.bfloat16(), ref.bfloat16()).max()) <= 1
+        else:
+            assert_bitexact(got, ref)
+
+
 def test_chain_exp_special_values():
     # a wave whose arguments include inf / NaN / overflow / subnormal results
     # leaves the straight-line exp path; every element still matches torch
