@@ -379,7 +379,9 @@ int ttlh_bfp8_pack_host(const float* src, void* dst, int64_t rows,
                         int64_t cols);
 int ttlh_bfp8_unpack_host(const void* src, uint16_t* dst_bf16, int64_t rows,
                           int64_t cols);
-/* device dequant: tiles -> row-major bf16 (device pointers) */
+/* device dequant: tiles -> row-major bf16 (device pointers, both 16-byte
+ * aligned; a tile's start is a multiple of 1088 = 68 x 16 bytes into the
+ * tile array, so any tile-aligned view of an aligned array qualifies) */
 int ttlh_bfp8_unpack(const void* src, void* dst_bf16, int64_t rows,
                      int64_t cols, void* stream);
 
@@ -392,8 +394,9 @@ int ttlh_matmul_bfp8w(const void* A, int64_t lda, const void* Bq, void* C,
 
 /* The same product in two passes, for large M: Bq is dequantised once into
  * `workspace` (row-major bf16 [K, N], at least ttlh_matmul_bfp8w_workspace_bytes
- * bytes, 16-byte aligned, caller-owned) by ttlh_bfp8_unpack, then multiplied
- * by the bf16 GEMM of ttlh_matmul.  The fused entry point above decodes each
+ * bytes, 16-byte aligned, caller-owned) by ttlh_bfp8_unpack (so Bq must be
+ * 16-byte aligned too), then multiplied by the bf16 GEMM of ttlh_matmul.
+ * The fused entry point above decodes each
  * weight tile once per 256-row block of A, so it is the better choice when M
  * is small (one or two blocks); this one decodes each tile once.  Results are
  * identical to the fused path's within fp32 summation order.  Reference
@@ -423,7 +426,9 @@ int ttlh_bfp4_pack_host(const float* src, void* dst, int64_t rows,
                         int64_t cols);
 int ttlh_bfp4_unpack_host(const void* src, uint16_t* dst_bf16, int64_t rows,
                           int64_t cols);
-/* device dequant: tiles -> row-major bf16 (device pointers) */
+/* device dequant: tiles -> row-major bf16 (device pointers, both 16-byte
+ * aligned; a tile's start is a multiple of 1088 = 68 x 16 bytes into the
+ * tile array, so any tile-aligned view of an aligned array qualifies) */
 int ttlh_bfp4_unpack(const void* src, void* dst_bf16, int64_t rows,
                      int64_t cols, void* stream);
 /* C[M,N] = A[M,K] (bf16, row-major) . dequant(Bq4)[K,N] in two passes: the

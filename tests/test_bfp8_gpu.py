@@ -123,6 +123,28 @@ def test_two_pass_matches_fused_path():
     assert int(O.bf16_ulp_diff(c1.cpu(), c2.cpu()).max()) <= 1
 
 
+def test_tile_array_at_an_8_byte_offset():
+    # the device decode reads tiles in 16-byte words: a tile array that is
+    # only 8-byte aligned is refused there, and the matmul wrapper sends it to
+    # the fused path, whose result it must equal
+    from ttlhip import kernels as Kn
+    M, K, N = 512, 256, 256
+    a = O.seeded((M, K), "normal", 13).cuda()
+    q = OB.pack_c(O.seeded((K, N), "normal", 14, torch.float32, std=0.02))
+    buf = torch.zeros(q.numel() + 8, dtype=torch.uint8, device="cuda")
+    qm = buf[8:]
+    qm.copy_(q.cuda())
+    assert qm.data_ptr() % 16 == 8
+    with pytest.raises(ValueError, match="16-byte aligned"):
+        Kn.bfp8_unpack(qm, K, N)
+    c1 = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    c2 = torch.empty_like(c1)
+    Kn.matmul_bfp8w(a, qm, c1)                            # M >= 512: fused for this Bq
+    Kn.matmul_bfp8w(a, q.cuda(), c2, two_pass=False)      # the fused path, aligned Bq
+    torch.cuda.synchronize()
+    assert torch.equal(c1.cpu().view(torch.int16), c2.cpu().view(torch.int16))
+
+
 def _bound_check(got, exact, K):
     err = (got.double() - exact).abs()
     bound = exact.abs() * 2.0 ** -8 + 1e-6 * math.sqrt(K) * float(exact.abs().max())

@@ -2030,8 +2030,9 @@ extern "C" int ttlh_matmul_bfp8w_ws(const void* A, int64_t lda, const void* Bq, 
   TTLH_REQUIRE(A && Bq && C, TTLH_EINVAL, "ttlh_matmul_bfp8w_ws: null pointer");
   TTLH_REQUIRE(M > 0 && M % 32 == 0 && N % 32 == 0 && K % 32 == 0, TTLH_EINVAL,
                "ttlh_matmul_bfp8w_ws: M, N, K must be positive multiples of 32");
-  TTLH_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15) == 0, TTLH_EINVAL,
-               "ttlh_matmul_bfp8w_ws: workspace must be 16-byte aligned");
+  TTLH_REQUIRE((reinterpret_cast<uintptr_t>(workspace) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(Bq) & 15) == 0,
+               TTLH_EINVAL, "ttlh_matmul_bfp8w_ws: Bq and the workspace must be 16-byte aligned");
   // pass 1: Bq tiles -> row-major bf16 [K, N] in the workspace (HBM bound);
   // pass 2: the bf16 GEMM.  The error text of a failing pass names it.
   int st = ttlh_bfp8_unpack(Bq, workspace, K, N, stream);

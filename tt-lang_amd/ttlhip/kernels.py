@@ -487,8 +487,8 @@ def matmul_bfp8w(a: torch.Tensor, bq: torch.Tensor, c: torch.Tensor, stream=None
         raise ValueError("matmul_bfp8w: Bq must be device uint8 tiles of a K x N matrix")
     if a.stride(1) != 1 or c.stride(1) != 1:
         raise ValueError("matmul_bfp8w: A and C must be row-major")
-    if two_pass is None:
-        two_pass = M >= BFP8_TWO_PASS_MIN_M
+    if two_pass is None:  # the two-pass decode reads Bq in 16-byte words
+        two_pass = M >= BFP8_TWO_PASS_MIN_M and bq.data_ptr() % 16 == 0
     if not two_pass:
         L.call("ttlh_matmul_bfp8w", a.data_ptr(), a.stride(0), bq.data_ptr(), c.data_ptr(),
                c.stride(0), M, N, K, L.stream_ptr(stream))
