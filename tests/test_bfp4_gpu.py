@@ -22,12 +22,26 @@ def test_device_dequant_all_pairs_bitexact():
     assert np.array_equal(got, _expected_all_pairs())
 
 
-@pytest.mark.parametrize("rows,cols", [(96, 1440), (32, 32)])
+@pytest.mark.parametrize("rows,cols", [(96, 1440), (32, 32), (64, 2080), (32, 2048)])
 def test_device_dequant_random(rows, cols):
     from ttlhip import kernels as K
     w = O.seeded((rows, cols), "normal", 71, torch.float32, std=0.3)
     q = OB.pack4_c(w)
     assert torch.equal(K.bfp4_unpack(q.cuda(), rows, cols).cpu().view(torch.int16),
+                       OB.unpack4_c(q, rows, cols).view(torch.int16))
+
+
+def test_device_dequant_tile_array_at_an_8_byte_offset():
+    # the decode stages tiles in 8-byte loads: an array that is 8- but not
+    # 16-byte aligned decodes to the same bits
+    from ttlhip import kernels as K
+    rows, cols = 64, 800
+    q = OB.pack4_c(O.seeded((rows, cols), "normal", 72, torch.float32, std=0.3))
+    buf = torch.zeros(q.numel() + 8, dtype=torch.uint8, device="cuda")
+    qm = buf[8:]
+    qm.copy_(q.cuda())
+    assert qm.data_ptr() % 16 == 8
+    assert torch.equal(K.bfp4_unpack(qm, rows, cols).cpu().view(torch.int16),
                        OB.unpack4_c(q, rows, cols).view(torch.int16))
 
 

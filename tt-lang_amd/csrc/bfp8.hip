@@ -211,26 +211,50 @@ uint16_t bfp4_decode_host(uint8_t e, uint32_t n) {
   return static_cast<uint16_t>((u >> 16) | ((n & 8u) << 12));
 }
 
-// One wave per tile, lane l = (face l / 16, face row l % 16): one exponent
-// byte and 8 element bytes per lane (contiguous across the wave), 32 bytes of
-// one bf16 output row written per lane.
+// The bfloat8_b unpack's layout (see bfp8_unpack_kernel): kUnpackTiles
+// consecutive tiles of a tile row per workgroup, staged in LDS (in 8-byte
+// loads: the tile array need only be 8-byte aligned, 576 = 72 x 8), then
+// 8-element chunks of whole output rows, each from 4 nibble bytes and the
+// face row's exponent.
 __global__ __launch_bounds__(256) void bfp4_unpack_kernel(const uint8_t* __restrict__ q,
                                                           uint16_t* __restrict__ out,
-                                                          int64_t cols, int64_t ntiles,
-                                                          int64_t nt_c) {
-  const int64_t tile = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) >> 6;
-  if (tile >= ntiles) return;
-  const int lane = threadIdx.x & 63;
-  const int f = lane >> 4, r = lane & 15;
-  const uint8_t* t = q + tile * TTLH_BFP4_TILE_BYTES;
-  const uint8_t e = t[lane];
-  const uint64_t nib = *reinterpret_cast<const uint64_t*>(t + 64 + 8 * lane);
-  u32x4 lo, hi;
-  bfp4_decode16(nib, e, lo, hi);
-  const int64_t tr = tile / nt_c, tc = tile - tr * nt_c;
-  uint16_t* o = out + (tr * 32 + (f >> 1) * 16 + r) * cols + tc * 32 + (f & 1) * 16;
-  *reinterpret_cast<u32x4*>(o) = lo;
-  *reinterpret_cast<u32x4*>(o + 8) = hi;
+                                                          int64_t cols, int64_t nt_c,
+                                                          int64_t groups_per_row) {
+  constexpr int kW = TTLH_BFP4_TILE_BYTES / 8;  // 8-byte words per tile
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kUnpackTiles * TTLH_BFP4_TILE_BYTES];
+  const int64_t g = blockIdx.x;
+  const int64_t tr = g / groups_per_row;
+  const int64_t tc0 = (g - tr * groups_per_row) * kUnpackTiles;
+  const int nt = static_cast<int>(min(static_cast<int64_t>(kUnpackTiles), nt_c - tc0));
+  const uint64_t* src =
+      reinterpret_cast<const uint64_t*>(q + (tr * nt_c + tc0) * TTLH_BFP4_TILE_BYTES);
+#pragma unroll
+  for (int i0 = 0; i0 < kUnpackTiles * kW; i0 += 256) {
+    const int i = i0 + static_cast<int>(threadIdx.x);
+    if (i < nt * kW) *reinterpret_cast<uint64_t*>(lds + 8 * i) = src[i];
+  }
+  __syncthreads();
+  // chunk i of the group: row i / 32, tile (i % 32) / 4, columns 8 (i % 4)
+  uint16_t* const orow = out + tr * 32 * cols + tc0 * 32;
+#pragma unroll
+  for (int i0 = 0; i0 < 32 * 4 * kUnpackTiles; i0 += 256) {
+    const int i = i0 + static_cast<int>(threadIdx.x);
+    const int r = i >> 5, c = i & 31;
+    const int t = c >> 2, col = (c & 3) * 8;
+    if (t >= nt) continue;  // a short last group of the tile row
+    const int f = ((r >> 4) << 1) | (col >> 4);
+    const uint8_t* tb = lds + t * TTLH_BFP4_TILE_BYTES;
+    const int sh = static_cast<int>(tb[16 * f + (r & 15)]) - 129;
+    const uint32_t nib =
+        *reinterpret_cast<const uint32_t*>(tb + 64 + 128 * f + 8 * (r & 15) + (col & 15) / 2);
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t b = (nib >> (8 * k)) & 0xffu;
+      w[k] = bfp4_decode1(b & 0xfu, sh) | (bfp4_decode1(b >> 4, sh) << 16);
+    }
+    *reinterpret_cast<u32x4*>(orow + r * cols + c * 8) = u32x4{w[0], w[1], w[2], w[3]};
+  }
 }
 
 }  // namespace
@@ -300,12 +324,12 @@ extern "C" int ttlh_bfp4_unpack(const void* src, void* dst_bf16, int64_t rows, i
                    (reinterpret_cast<uintptr_t>(dst_bf16) & 15) == 0,
                TTLH_EINVAL, "ttlh_bfp4_unpack: src must be 8-byte and dst 16-byte aligned");
   const int64_t nt_c = cols / 32;
-  const int64_t ntiles = (rows / 32) * nt_c;
-  const int64_t blocks = (ntiles + 3) / 4;
+  const int64_t groups_per_row = (nt_c + kUnpackTiles - 1) / kUnpackTiles;
+  const int64_t blocks = (rows / 32) * groups_per_row;
   TTLH_REQUIRE(blocks < (int64_t(1) << 31), TTLH_EUNSUPPORTED, "ttlh_bfp4_unpack: too large");
   hipLaunchKernelGGL(bfp4_unpack_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint8_t*>(src),
-                     static_cast<uint16_t*>(dst_bf16), cols, ntiles, nt_c);
+                     static_cast<uint16_t*>(dst_bf16), cols, nt_c, groups_per_row);
   return check_launch("bfp4_unpack_kernel");
 }
 

@@ -26,24 +26,12 @@ __device__ __forceinline__ u32x4 bfp8_decode8(uint64_t bytes, uint8_t e) {
   return r;
 }
 
-// 16 bfloat4_b nibbles (element c in bits 4c..4c+3) sharing exponent e ->
-// 16 bf16 in two u32x4.  value = (-1)^s * m * 2^(e - 129): converted and
-// scaled exactly as for bfloat8_b (at most 3 significant bits).
+// One bfloat4_b nibble (bit 3 sign, bits 2..0 magnitude m) with shift
+// sh = e - 129 -> bf16 bits of (-1)^s * m * 2^sh: converted and scaled
+// exactly as for bfloat8_b (at most 3 significant bits).
 __device__ __forceinline__ uint32_t bfp4_decode1(uint32_t n, int sh) {
   const float f = __builtin_amdgcn_ldexpf(static_cast<float>(n & 7u), sh);
   return (__float_as_uint(f) >> 16) | ((n & 8u) << 12);
-}
-
-__device__ __forceinline__ void bfp4_decode16(uint64_t nib, uint8_t e, u32x4& lo, u32x4& hi) {
-  const int sh = static_cast<int>(e) - 129;
-  uint32_t w[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const uint32_t b = static_cast<uint32_t>(nib >> (8 * i)) & 0xffu;
-    w[i] = bfp4_decode1(b & 0xfu, sh) | (bfp4_decode1(b >> 4, sh) << 16);
-  }
-  lo = u32x4{w[0], w[1], w[2], w[3]};
-  hi = u32x4{w[4], w[5], w[6], w[7]};
 }
 
 }  // namespace ttlh
