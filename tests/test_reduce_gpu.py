@@ -183,6 +183,39 @@ def test_abi_column_splits(h):
     assert bool(((got - xs.sum(0)).abs() <= _fp32_sum_bound(xs, 0)).all())
 
 
+def test_abi_cached_workspace_grows_and_follows_the_stream():
+    # column and full reductions keep one workspace per (device, stream),
+    # grown to the largest size asked for: a small call, a larger one (the
+    # buffer is replaced), calls on a side stream (its own buffer) and after a
+    # release all give the bits a first call on a fresh cache gives
+    K.release_workspaces()
+    small = O.seeded((48, 512), "normal", 41).cuda()
+    large = O.seeded((4096, 2048), "normal", 42).cuda()
+    want_small = _reduce(small, "sum", [0], (1, 512))
+    want_large = _reduce(large, "sum", [0], (1, 2048))
+    want_all = _reduce(large, "sum", [0, 1], (1, 1))
+    K.release_workspaces()
+    assert torch.equal(_reduce(small, "sum", [0], (1, 512)), want_small)
+    assert torch.equal(_reduce(large, "sum", [0], (1, 2048)), want_large)
+    assert torch.equal(_reduce(small, "sum", [0], (1, 512)), want_small)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    outs = []
+    with torch.cuda.stream(side):
+        for x, n in ((large, 2048), (small, 512), (large, 2048)):
+            o = torch.full((1, n), 7.0, dtype=torch.float32, device="cuda")
+            K.reduce(_load_prog(), [K.OperandMap(x)], "sum", [0], o, (0, 0) + tuple(x.shape),
+                     stream=side)
+            outs.append(o)
+        a = torch.full((1, 1), 7.0, dtype=torch.float32, device="cuda")
+        K.reduce(_load_prog(), [K.OperandMap(large)], "sum", [0, 1], a, (0, 0, 4096, 2048),
+                 stream=side)
+    side.synchronize()
+    assert torch.equal(outs[0].cpu(), want_large) and torch.equal(outs[2].cpu(), want_large)
+    assert torch.equal(outs[1].cpu(), want_small) and torch.equal(a.cpu(), want_all)
+    K.release_workspaces()
+
+
 def test_abi_repeatable_and_nan():
     x = O.seeded((2048, 2048), "normal", 39).cuda()
     a = _reduce(x, "sum", [0, 1], (1, 1))
