@@ -43,9 +43,9 @@ def _check_device(t: torch.Tensor, what: str) -> None:
 
 # Device workspaces (column and full reductions, weight dequantisation), one
 # per (device, stream), grown to the largest size asked for and then kept.
-# Taking a fresh one from torch's caching allocator on every call costs tens
-# of microseconds of host time and now and then a millisecond-long stall,
-# far more than the kernels it serves.  Calls on one stream run in stream
+# Taking a fresh one from torch's caching allocator on every call costs about
+# 10 us of host time (4096^2 column sums: 35 -> 25 us of host enqueue per
+# call, against 17 us of kernels).  Calls on one stream run in stream
 # order, so they share that stream's buffer safely; calls on different
 # streams get different buffers.  A HIP graph captured over such a call
 # keeps the buffer's address: replaying it while eager calls run on the
