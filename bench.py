@@ -288,6 +288,9 @@ class ReduceWorkload(PlanWorkload):
     def kernel_name(self):
         return "reduce_rows_bf16_kernel"
 
+    def traffic_kernels(self):  # the plain variant (the product one serves row_dot)
+        return [("reduce_rows_bf16_kernel<0, false, true, false>", self.n)]
+
     def work_per_step(self):
         return self.n * self.n * 2 + self.n * 2
 
@@ -328,6 +331,77 @@ class ReduceWorkload(PlanWorkload):
                 "kind": "port",
                 "sample": f"the full {self.n}x{self.n} workload through the eager tile-by-tile "
                           f"oracle executor (1 thread), {reps} runs of {dt:.2f} s"}
+
+
+class RowDotWorkload(PlanWorkload):
+    """Row dot products out[r] = sum_c a[r, c] * b[r, c] through a tt-lang
+    kernel (tests/kernel_lib.py make_row_dot: ttl.math.reduce_sum(a * b, 1,
+    dims=[1]) over whole rows, 8x8 grid): the reduction fused with the
+    elementwise stage that produces its operand, one launch (the bf16 row
+    kernel's product variant) reading both operands once; HBM-bound."""
+
+    def __init__(self, name, n, seed=4322):
+        self.name, self.n, self.seed = name, n, seed
+        self.config = (f"row dot products out[r] = sum_c a[r, c] * b[r, c], a, b bf16 {n}x{n} "
+                       f"U[-2,2], bf16 out {n}x32 (spec reduce_sum of a product, dims=[1])")
+
+    def kernel_name(self):
+        return "reduce_rows_bf16_kernel"
+
+    def traffic_kernels(self):
+        return [("reduce_rows_bf16_kernel<0, false, true, true>", self.n)]
+
+    def work_per_step(self):
+        return 2 * self.n * self.n * 2 + self.n * 32 * 2
+
+    def _make(self, ns, grid=(8, 8)):
+        import kernel_lib as KL
+        return KL.make_row_dot(ns, gr=2, gc=self.n // 32, grid=grid)
+
+    def _inputs(self):
+        from oracle.tile_ops import seeded
+        return (seeded((self.n, self.n), "uniform", self.seed, lo=-2, hi=2),
+                seeded((self.n, self.n), "uniform", self.seed + 1, lo=-2, hi=2))
+
+    def make_sets(self):
+        import ttl
+        import ttnn
+        self.kernel = self._make(ttl)
+        self.a, self.b = self._inputs()
+        a, b = ttnn.from_torch(self.a), ttnn.from_torch(self.b)
+        nsets = n_sets(self.work_per_step())
+        sets = []
+        for i in range(nsets):
+            ai = a if i == 0 else ttnn.Tensor(a._tensor.clone())
+            bi = b if i == 0 else ttnn.Tensor(b._tensor.clone())
+            sets.append([ai, bi, ttnn.empty((self.n, 32), dtype=torch.bfloat16)])
+        return sets
+
+    def check(self):
+        from oracle import tile_ops as O
+        self.launch(0)
+        torch.cuda.synchronize()
+        got = self.sets[0][-1].to_torch()
+        # the simulator rounds the product to bf16 before the sum
+        prod = (self.a.float() * self.b.float()).bfloat16().double()
+        exact = prod.sum(1).float().bfloat16()
+        ulp = O.bf16_ulp_diff(got[:, 0], exact)
+        return {"max_ulp": int(ulp.max()), "mismatch_frac": float((ulp > 0).float().mean()),
+                "padding_zero": bool((got[:, 1:] == 0).all()),
+                "oracle": "float64 row sums of the bf16-rounded products, rounded once to bf16"}
+
+    def cpu_baseline(self):
+        rows = 1024
+        a, b = self._inputs()
+        t = [a[:rows].contiguous(), b[:rows].contiguous(),
+             torch.zeros(rows, 32, dtype=torch.bfloat16)]
+        dt, reps = _eager(lambda ns: self._make(ns, grid=(1, 1)), t)
+        nbytes = 2 * rows * self.n * 2 + rows * 32 * 2
+        return {"value": round(nbytes / dt / 1e9, 4), "unit": "GB/s", "cores": 1,
+                "kind": "port",
+                "sample": f"{rows} of the {self.n} rows through the eager tile-by-tile oracle "
+                          f"executor running the same kernel (1 thread), {reps} runs of "
+                          f"{dt:.2f} s"}
 
 
 class SoftmaxWorkload(PlanWorkload):
@@ -799,6 +873,7 @@ WORKLOADS = {
                                                             4096),
     "sdpa_4x32x4096x128": lambda: SdpaWorkload("sdpa_4x32x4096x128", 4, 32, 4096, 128),
     "reduce_sum_rows_4096": lambda: ReduceWorkload("reduce_sum_rows_4096", 4096),
+    "row_dot_4096": lambda: RowDotWorkload("row_dot_4096", 4096),
     "softmax_rows_4096": lambda: SoftmaxWorkload("softmax_rows_4096", 4096),
     "softmax_rows_4096_separate": lambda: SoftmaxWorkload("softmax_rows_4096_separate", 4096,
                                                           separate=True),

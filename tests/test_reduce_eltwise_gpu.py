@@ -101,6 +101,56 @@ def test_one_launch_equals_separate_calls(form, w):
         assert float((got - ex).abs().max()) <= 2 ** -6 * float(ex.max())
 
 
+@pytest.mark.parametrize("kind", ["sum", "max"])
+@pytest.mark.parametrize("h,w", [(96, 2048), (33, 4096), (7, 6152), (64, 8192)])
+@pytest.mark.parametrize("out_dtype", [B16, torch.float32])
+def test_row_dot_alone_equals_fused(kind, h, w, out_dtype):
+    # a row reduction of a * b (two bf16 operands) alone takes the bf16 row
+    # kernel's product variant; inside one launch with a program it takes the
+    # fused row kernel: the results must be the same bits, with a scale, a
+    # scaler, NaN and infinite products included
+    print(f"row dot {kind} {h}x{w} {out_dtype}", flush=True)
+    a = O.seeded((h, w), "uniform", w + h, lo=-3, hi=3)
+    b = O.seeded((h, w), "uniform", w + h + 1, lo=-3, hi=3)
+    a[1, 5] = float("nan")
+    b[2, 9] = float("inf")
+    a, b = a.cuda(), b.cuda()
+    am, bm = Kn.OperandMap(a), Kn.OperandMap(b)
+    prog = X.compile_expr(X.Binary("mul", _leaf(am), _leaf(bm), B16))
+    assert len(prog.steps) == 2
+    scaler = torch.full((1, 1), 0.75, dtype=B16, device="cuda")
+
+    def red(out):
+        return Kn.RowReduce(prog, _ops(prog), kind, out, (0, 0), True, scaler, 0.5)
+
+    t_alone = torch.full((h, 32), 5.0, dtype=out_dtype, device="cuda")
+    r = red(t_alone)
+    Kn.reduce(r.prog, r.operands, r.kind, [1], r.out, (0, 0, h, w), r.out_origin, r.out_pad,
+              r.scaler, r.scale)
+    t_fused = torch.full((h, 32), 5.0, dtype=out_dtype, device="cuda")
+    fin = X.compile_expr(X.Binary("sub", _leaf(am), _leaf(_row_result(t_fused)), B16))
+    out = torch.full((h, w), 7.0, dtype=B16, device="cuda")
+    assert Kn.reduce_rows_eltwise([red(t_fused)], fin, _ops(fin), out, (0, 0, h, w))
+    torch.cuda.synchronize()
+    va, vf = t_alone.cpu(), t_fused.cpu()
+    assert torch.equal(va.view(torch.int32 if out_dtype == torch.float32 else torch.int16),
+                       vf.view(torch.int32 if out_dtype == torch.float32 else torch.int16))
+    # and the values are the reduction of the bf16-rounded products
+    prod = (a.cpu().float() * b.cpu().float()).bfloat16().double() * 0.375
+    ref = prod.sum(1) if kind == "sum" else prod.amax(1)
+    got = va[:, 0].double()
+    fin_rows = torch.isfinite(ref)
+    assert bool(torch.isnan(got[1])) and bool(torch.isnan(ref[1]))  # a NaN product
+    same = (got == ref) | (torch.isnan(got) & torch.isnan(ref))
+    assert bool(same[~fin_rows].all())  # infinite / NaN rows: the same value
+    prod = torch.nan_to_num(prod, nan=0.0, posinf=0.0, neginf=0.0)
+    tol = 2 ** -7 * prod.abs().sum(1) + 1e-6 if kind == "sum" else 2 ** -8 * ref.abs()
+    if out_dtype == torch.float32 and kind == "sum":
+        tol = w * 2.0 ** -24 * prod.abs().sum(1) + 1e-6
+    assert bool(((got - ref).abs()[fin_rows] <= tol[fin_rows]).all())
+    assert not bool(va[:, 1:].any())  # zero-padded result tiles
+
+
 def test_region_offset_and_in_place_output():
     print("reduce_rows_eltwise region offset, in place", flush=True)
     big = O.seeded((160, 4096 + 64), "uniform", 3, lo=-3, hi=3).cuda()
