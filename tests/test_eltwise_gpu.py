@@ -264,6 +264,22 @@ def test_stream_kernel_row_blocks(h, w, region, out_dtype):
             assert_bitexact(got, ref)
 
 
+@pytest.mark.parametrize("w", [1024, 4096])
+def test_row_path_f32_row_scalar_is_not_rounded(w):
+    # a program with a row-scalar subtree over rows of 512+ elements runs on
+    # the row kernel, which computes the subtree once per row: an f32 value
+    # (here rsqrt(c + 1e-5), c an f32 column) must reach the elementwise
+    # steps unrounded, as the oracle computes it
+    a = _u((64, w), 95)
+    c = _u((64, 1), 96, torch.float32, lo=0.5, hi=4.0)
+    env = {"a": a, "c": c}
+    e = ("mul", ("leaf", "a"), ("rsqrt", ("add", ("leaf", "c"), ("const", 1e-5))))
+    got = run_gpu(e, env, {}, (64, w), torch.float32)
+    ref = O.eval_expr(e, env)
+    assert ref.dtype == torch.float32
+    torch.testing.assert_close(got, ref, rtol=4e-6, atol=1e-7)
+
+
 def test_chain_exp_special_values():
     # a wave whose arguments include inf / NaN / overflow / subnormal results
     # leaves the straight-line exp path; every element still matches torch

@@ -56,13 +56,20 @@ def _case(form, h, w, seed):
                                       X.Binary("mul", _leaf(_row_result(t1)), X.Const(1.0 / w),
                                                B16), B16))
         reds = [Kn.RowReduce(p1, _ops(p1), "sum", t1, (0, 0), True, None, 0.5)]
-    else:  # rms: x * rsqrt(mean(x * x) + eps) * g, g a row vector read from memory
+    elif form == "rms":  # x * rsqrt(mean(x * x) + eps) * g, g a row vector read from memory
         g = O.seeded((1, w), "uniform", seed + 1, lo=0.5, hi=1.5).cuda()
         p1 = X.compile_expr(X.Binary("mul", _leaf(xm), _leaf(xm), B16))
         ms = X.Binary("add", _leaf(_row_result(t1)), X.Const(1e-3), B16)
         fin = X.compile_expr(X.Binary("mul", X.Binary("mul", _leaf(xm), X.Unary("rsqrt", ms, B16),
                                                       B16), _leaf(Kn.OperandMap(g)), B16))
         reds = [Kn.RowReduce(p1, _ops(p1), "sum", t1, (0, 0), True, None, 1.0 / w)]
+    else:  # rms_plain: x * rsqrt(mean(x * x) + eps), an f32 result tile
+        t1 = torch.full((h, 32), 5.0, dtype=torch.float32, device="cuda")
+        p1 = X.compile_expr(X.Binary("mul", _leaf(xm), _leaf(xm), B16))
+        ms = X.Binary("add", _leaf(_row_result(t1)), X.Const(1e-5), torch.float32)
+        fin = X.compile_expr(X.Binary("mul", _leaf(xm), X.Unary("rsqrt", ms, torch.float32),
+                                      torch.float32))
+        reds = [Kn.RowReduce(p1, _ops(p1), "sum", t1, (0, 0), True, scaler, 1.0 / w)]
     out = torch.full((h, w), 7.0, dtype=B16, device="cuda")
     return reds, fin, out, [r.out for r in reds]
 
@@ -79,7 +86,7 @@ def _bits(t):
     return t.view(torch.int16).cpu()
 
 
-@pytest.mark.parametrize("form", ["softmax", "center", "rms"])
+@pytest.mark.parametrize("form", ["softmax", "center", "rms", "rms_plain"])
 @pytest.mark.parametrize("w", [128, 1056, 2048, 4096, 6144, 8192])
 def test_one_launch_equals_separate_calls(form, w):
     print(f"reduce_rows_eltwise {form} w={w}", flush=True)

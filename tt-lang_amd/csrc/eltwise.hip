@@ -1424,6 +1424,88 @@ __global__ __launch_bounds__(256) void softmax_rows_kernel(const RfArgs a, const
   });
 }
 
+// A row normalisation by the sum of squares, e.g. RMS norm x * rsqrt(mean(x
+// x) + eps) * g, as compiled chains recognised on the host (rf_norm_form):
+// one reduction, the sum of x * x (x the one resident bf16 operand) times
+// its scale; the program x * c (* g), c a row scalar (a reduction result or
+// a node computed from it, such as rsqrt(r + eps)), g an operand read from
+// memory.  The generic kernel's layout, summation order, node evaluation and
+// per-step / per-operand roundings (read from the stages), without the
+// interpreter: the same bits.
+template <int LANES, int NCH>
+__global__ __launch_bounds__(256) void norm_rows_kernel(const RfArgs a) {
+  __shared__ float part[4];
+  __shared__ float scl[4][kRfScal];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int64_t row = LANES == 256 ? int64_t(blockIdx.x) : int64_t(blockIdx.x) * 4 + wave;
+  if (LANES == 64 && row >= a.h) return;  // wave-uniform (no workgroup barrier in this layout)
+  const int64_t y = a.y0 + row;
+  const int li = LANES == 256 ? t : lane;
+  constexpr int64_t S = int64_t(LANES) * 8;
+  const int64_t xl = int64_t(li) * 8;
+  u32x4 q[NCH];
+  const uintptr_t base = operand_addr<false>(a.res[0], y, a.x0);
+  rf_each<NCH>([&](auto c) {
+    const int64_t xo = xl + c * S;
+    q[c] = ld16<true>(base + 2 * (xo < a.w ? xo : a.w - 8));
+  });
+  auto rnd8 = [](f32x8 v, uint8_t r) { return r == TTLH_BF16 ? round_bf16x8(v) : v; };
+  float* const sc = scl[wave];
+#pragma unroll 1
+  for (int i = 0; i < a.n_row; ++i) {  // the row's values of the column-broadcast operands
+    const EltOperand& op = a.row[i];
+    sc[kRfRed + i] = to_f32<8, false>(op, load_raw<8, false>(op, operand_addr<false>(op, y, a.x0)))[0];
+  }
+  // the reduction: the sum of x * x, times its scale
+  const RfStage& st = a.st[0];
+  const RfStep p0 = st.step[0], p1 = st.step[1];
+  const float s = rf_scale(st);
+  float r = 0.0f;
+  rf_each<NCH>([&](auto c) {
+    if (xl + c * S < a.w) {
+      const f32x8 x = bf16x8_f32(q[c]);
+      const f32x8 v = rnd8(binary8<TTLH_OP_MUL>(rnd8(rnd8(x, p0.orn), p0.rnd), rnd8(x, p1.orn)),
+                           p1.rnd);
+      if (s == 1.0f) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) r += v[k];
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) r = __builtin_fmaf(v[k], s, r);
+      }
+    }
+  });
+  r = red_wave(TTLH_REDUCE_SUM, r);
+  if constexpr (LANES == 256) {
+    if (lane == 0) part[wave] = r;
+    __syncthreads();
+    r = (part[0] + part[1]) + (part[2] + part[3]);
+  }
+  rf_write(st, row, r, li);
+  sc[0] = st.out_dtype == TTLH_BF16 ? round_bf16(r) : r;
+  // the program: x * c (* g)
+  const RfStage& fe = a.st[kRfRed];
+  rf_nodes(fe, sc);
+  const RfStep f0 = fe.step[0], f1 = fe.step[1], f2 = fe.step[2];
+  const f32x8 cv = rnd8(splat(sc[f1.src - RS_SC]), f1.orn);
+  const bool has_g = fe.n_steps == 3;
+  const EltOperand& g = a.mem[has_g ? f2.src - RS_MEM : 0];
+  rf_each<NCH>([&](auto c) {
+    const int64_t xo = xl + c * S;
+    if (xo < a.w) {
+      f32x8 o = rnd8(rnd8(bf16x8_f32(q[c]), f0.orn), f0.rnd);
+      o = rnd8(binary8<TTLH_OP_MUL>(o, cv), f1.rnd);
+      if (has_g) {
+        const f32x8 gv = rnd8(
+            to_f32<8, false>(g, load_raw<8, false>(g, operand_addr<false>(g, y, a.x0 + xo))),
+            f2.orn);
+        o = rnd8(binary8<TTLH_OP_MUL>(o, gv), f2.rnd);
+      }
+      store_chunk<8>(a, y, a.x0 + xo, o);
+    }
+  });
+}
+
 }  // namespace
 }  // namespace ttlh
 
@@ -1929,9 +2011,11 @@ bool rf_compile(const EltArgs& e, int nj, const uint8_t* src_of, RfStage& st) {
       p.code = RC_COPY;
       if (x.type == 0) {
         p.src = x.src;
+        p.orn = x.rnd;
       } else {
         p.src = hoist(hoist, n, p.imm);
         p.rnd = TTLH_F32;  // a node or an immediate carries its rounding
+        p.orn = TTLH_F32;
       }
       rev_steps[ns++] = p;
       break;
@@ -1960,7 +2044,11 @@ bool rf_compile(const EltArgs& e, int nj, const uint8_t* src_of, RfStage& st) {
       p.src = o.src;
       p.orn = o.rnd;
     } else {
+      // a node or an immediate carries its own rounding: the fetch adds none
+      // (left at the zero default, TTLH_BF16, it would round an f32 node or
+      // an immediate such as 0.1 to bf16, where ttlh_eltwise does not)
       p.src = hoist(hoist, opnd, p.imm);
+      p.orn = TTLH_F32;
     }
     rev_steps[ns++] = p;
     n = spine;
@@ -2043,6 +2131,27 @@ bool rf_softmax_form(const RfArgs& a, RfSoftmax* f) {
   f->r_out = o.rnd;
   f->r_m = s1.step[1].orn;
   f->r_g = o.orn;
+  return true;
+}
+
+// Whether the compiled stages are the row normalisation norm_rows_kernel
+// runs: one reduction, the sum of x * x; the program x * c or x * c * g with
+// c a row scalar and g an operand read from memory (x the resident operand).
+bool rf_norm_form(const RfArgs& a) {
+  if (a.n_red != 1 || a.kept != -1) return false;
+  const uint8_t x = RS_RES + 0;
+  const RfStage &st = a.st[0], &fe = a.st[kRfRed];
+  if (st.kind != TTLH_REDUCE_SUM || st.n_steps != 2 || st.n_nodes != 0 || st.from_kept != 0 ||
+      st.step[0].code != RC_COPY || st.step[0].src != x || st.step[1].code != RC_MUL ||
+      st.step[1].src != x)
+    return false;
+  if ((fe.n_steps != 2 && fe.n_steps != 3) || fe.from_kept != 0 || fe.step[0].code != RC_COPY ||
+      fe.step[0].src != x || fe.step[1].code != RC_MUL || fe.step[1].src < RS_SC ||
+      fe.step[1].src >= RS_IMM)
+    return false;
+  if (fe.n_steps == 3 && (fe.step[2].code != RC_MUL || fe.step[2].src < RS_MEM ||
+                          fe.step[2].src >= RS_SC))
+    return false;
   return true;
 }
 
@@ -2262,6 +2371,24 @@ int rows_fused_impl(const char* who, const ttlh_row_reduce* red, int n_red,
     }
 #undef TTLH_SM
     return check_launch("softmax_rows_kernel");
+  }
+  if (n_res == 1 && rf_norm_form(a)) {
+    TTLH_REQUIRE(groups < (int64_t(1) << 31), TTLH_EUNSUPPORTED, "%s: region too large", who);
+    const dim3 grid(static_cast<uint32_t>(groups)), block(256);
+#define TTLH_NORM(L)                                                                         \
+  switch (nch) {                                                                             \
+    case 1: hipLaunchKernelGGL((norm_rows_kernel<L, 1>), grid, block, 0, s, a); break;      \
+    case 2: hipLaunchKernelGGL((norm_rows_kernel<L, 2>), grid, block, 0, s, a); break;      \
+    case 3: hipLaunchKernelGGL((norm_rows_kernel<L, 3>), grid, block, 0, s, a); break;      \
+    default: hipLaunchKernelGGL((norm_rows_kernel<L, 4>), grid, block, 0, s, a); break;     \
+  }
+    if (wide) {
+      TTLH_NORM(256)
+    } else {
+      TTLH_NORM(64)
+    }
+#undef TTLH_NORM
+    return check_launch("norm_rows_kernel");
   }
   // one instantiation per (lanes, resident operands, chunks per lane)
 #define TTLH_RF3(L, R, C) return rf_launch<L, R, C>(a, groups, s)
