@@ -413,6 +413,8 @@ class SoftmaxWorkload(PlanWorkload):
     times, for comparison).  HBM-bound; algorithmic bytes = x read once, y
     written once, the two reduction result tiles written once."""
 
+    form = "softmax"
+
     def __init__(self, name, n, separate=False, seed=2468):
         self.name, self.n, self.separate, self.seed = name, n, separate, seed
         how = ("the plan's three launches (ttlh_reduce x2, ttlh_eltwise)" if separate else
@@ -440,7 +442,7 @@ class SoftmaxWorkload(PlanWorkload):
         import ttl
         import ttnn
         from oracle.tile_ops import seeded
-        self.kernel = KL.make_softmax_one_store(ttl, gc=self.n // 32, grid=(8, 8))
+        self.kernel = KL.make_softmax_one_store(ttl, gc=self.n // 32, grid=(8, 8), form=self.form)
         self.x = seeded((self.n, self.n), "uniform", self.seed, lo=-4, hi=4)
         x = ttnn.from_torch(self.x)
         sc = ttnn.from_torch(torch.ones(32, 32, dtype=torch.bfloat16))
@@ -468,17 +470,20 @@ class SoftmaxWorkload(PlanWorkload):
         # the other execution of the same plan, bit for bit
         other = P.Plan(launches=list(self.plan.launches[0].reds) + [self.plan.launches[0].ew]) \
             if not self.separate else P.Plan(launches=[P.ReduceEltwiseLaunch(
-                self.plan.launches[:2], self.plan.launches[2])])
+                self.plan.launches[:-1], self.plan.launches[-1])])
         P.execute(other, self.amaps[0])
         torch.cuda.synchronize()
         again = self.sets[0][-1].to_torch()
-        ex = torch.softmax(self.x.double(), 1)
+        ex = self.exact()
         return {"bit_equal_fused_and_separate": bool(torch.equal(got.view(torch.int16),
                                                                  again.view(torch.int16))),
                 "max_abs_err_vs_exact": float((got.double() - ex).abs().max()),
-                "max_exact": float(ex.max()),
-                "oracle": "float64 softmax (the per-op bf16 roundings bound the error by 2^-6 "
-                          "max); fused and separate launches compared bit for bit"}
+                "max_exact": float(ex.abs().max()),
+                "oracle": f"float64 {self.form} (the per-op bf16 roundings bound the error by "
+                          "2^-6 max); fused and separate launches compared bit for bit"}
+
+    def exact(self):
+        return torch.softmax(self.x.double(), 1)
 
     def cpu_baseline(self):
         import kernel_lib as KL
@@ -487,11 +492,42 @@ class SoftmaxWorkload(PlanWorkload):
         x = seeded((rows, self.n), "uniform", self.seed, lo=-4, hi=4)
         t = [x, torch.ones(32, 32, dtype=torch.bfloat16),
              torch.zeros(rows, self.n, dtype=torch.bfloat16)]
-        dt, reps = _eager(lambda ns: KL.make_softmax_one_store(ns, gc=self.n // 32, grid=(1, 1)), t)
-        nbytes = 2 * rows * self.n * 2 + 2 * rows * 32 * 2
+        dt, reps = _eager(lambda ns: KL.make_softmax_one_store(ns, gc=self.n // 32, grid=(1, 1),
+                                                               form=self.form), t)
+        nbytes = self.work_per_step() * rows / self.n  # the step's bytes for `rows` rows
         return {"value": round(nbytes / dt / 1e9, 5), "unit": "GB/s", "cores": 1, "kind": "port",
                 "sample": f"{rows} of the {self.n} rows through the eager tile-by-tile oracle "
                           f"executor running the same kernel (1 thread), {reps} runs of {dt:.2f} s"}
+
+
+class RmsNormWorkload(SoftmaxWorkload):
+    """RMS normalisation of a bf16 matrix written as one tt-lang store
+    (tests/kernel_lib.py make_softmax_one_store, form "rms": y = x *
+    rsqrt(broadcast(reduce_sum(x * x)) / W + 1e-5), one block per row band
+    of 128 tiles, 8x8 grid): one row reduction and the program in one
+    ttlh_reduce_rows_eltwise launch, on its dedicated kernel; HBM-bound;
+    algorithmic bytes = x read once, y written once, the result tiles."""
+
+    form = "rms"
+
+    def __init__(self, name, n, separate=False, seed=1357):
+        self.name, self.n, self.separate, self.seed = name, n, separate, seed
+        self.config = (f"row RMS normalisation y = x * rsqrt(sum_r x^2 / W + 1e-5) in one store "
+                       f"(spec reduce_sum / broadcast / rsqrt), x bf16 {n}x{n} U[-4,4], per-op "
+                       f"bf16 rounding; one ttlh_reduce_rows_eltwise launch")
+
+    def kernel_name(self):
+        return "norm_rows_kernel"
+
+    def traffic_kernels(self):
+        return [("norm_rows_kernel<256, 2>", None)]
+
+    def work_per_step(self):
+        return 2 * self.n * self.n * 2 + self.n * 32 * 2
+
+    def exact(self):
+        x = self.x.double()
+        return x * torch.rsqrt((x * x).mean(1, keepdim=True) + 1e-5)
 
 
 class TilizeWorkload(Workload):
@@ -872,6 +908,7 @@ WORKLOADS = {
     "reduce_sum_rows_4096": lambda: ReduceWorkload("reduce_sum_rows_4096", 4096),
     "row_dot_4096": lambda: RowDotWorkload("row_dot_4096", 4096),
     "softmax_rows_4096": lambda: SoftmaxWorkload("softmax_rows_4096", 4096),
+    "rms_norm_rows_4096": lambda: RmsNormWorkload("rms_norm_rows_4096", 4096),
     "softmax_rows_4096_separate": lambda: SoftmaxWorkload("softmax_rows_4096_separate", 4096,
                                                           separate=True),
     "tilize_4096": lambda: TilizeWorkload("tilize_4096", 4096),

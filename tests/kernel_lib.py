@@ -1403,7 +1403,8 @@ def make_softmax_one_store(ttl, gc=4, grid=(2, 2), form="softmax"):
       e = exp(x - m)
       y = e * broadcast(recip(reduce_sum(e, s, dims=[1])), out, dims=[1])
     form "center": y = x - broadcast(reduce_sum(x, s, dims=[1]), out, dims=[1]) * (1 / W)
-    (a row mean subtracted)."""
+    (a row mean subtracted); form "rms": y = x * rsqrt(broadcast(reduce_sum(x * x, s,
+    dims=[1]), out, dims=[1]) * (1 / W) + 1e-5) (RMS normalisation)."""
 
     @ttl.kernel(grid=grid)
     def softmax_one_store(x, s, y):
@@ -1425,6 +1426,10 @@ def make_softmax_one_store(ttl, gc=4, grid=(2, 2), form="softmax"):
                             e = ttl.math.exp(xb - m)
                             r = ttl.math.recip(ttl.math.reduce_sum(e, sb, dims=[1]))
                             yb.store(e * ttl.math.broadcast(r, yb, dims=[1]))
+                        elif form == "rms":
+                            ss = ttl.math.broadcast(ttl.math.reduce_sum(xb * xb, sb, dims=[1]),
+                                                    yb, dims=[1])
+                            yb.store(xb * ttl.math.rsqrt(ss * (1.0 / width) + 1e-5))
                         else:
                             tot = ttl.math.broadcast(ttl.math.reduce_sum(xb, sb, dims=[1]), yb,
                                                      dims=[1])

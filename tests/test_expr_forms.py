@@ -66,6 +66,17 @@ def test_row_centring_in_one_store_matches_oracle():
     assert float((orc.double() - ex).abs().max()) <= 2 ** -6 * float(x.abs().max())
 
 
+def test_rms_normalisation_in_one_store_matches_oracle():
+    t = softmax_case(seed=8)
+    got, orc, plan = _both(KL.make_softmax_one_store, t, 2, form="rms")
+    (l,) = plan.launches
+    assert isinstance(l, P.ReduceEltwiseLaunch) and [r.kind for r in l.reds] == ["sum"]
+    assert torch.equal(got, orc)
+    x = t[0].double()
+    ex = x * torch.rsqrt((x * x).mean(1, keepdim=True) + 1e-5)
+    assert float((orc.double() - ex).abs().max()) <= 2 ** -6 * float(ex.abs().max())
+
+
 def _mm_exact(a, b, c, form):
     r = lambda v: v.to(torch.bfloat16).double()  # one bf16 rounding
     A, B = a.double(), b.double()

@@ -34,7 +34,7 @@ def _gpu_and_oracle(make, tensors, out_index, **kw):
     return got, oargs[out_index].t, k.last_plan
 
 
-@pytest.mark.parametrize("form", ["softmax", "center"])
+@pytest.mark.parametrize("form", ["softmax", "center", "rms"])
 def test_reductions_inside_one_store_on_gpu(form):
     print(f"expr forms gpu: {form}", flush=True)
     x = O.seeded((512, 512), "uniform", 7, lo=-4, hi=4)
